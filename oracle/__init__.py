@@ -1,0 +1,254 @@
+"""CPU oracle for the moebius-cpu conv/norm path (test infrastructure only).
+
+ctypes bindings over ``liboracle.so`` (built from this directory by
+``make``), a C++ restatement of moebius-cpu ``src/engine`` and of the
+``src/unet`` / ``src/vae`` block chains. Only ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg import
+this module; the product library never does.
+
+Arrays are numpy float32 NHWC, C-contiguous. Each wrapper names the
+reference function it restates.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i64 = ctypes.c_int64
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle library missing: {LIB_PATH} (run `make -C oracle`)")
+        _lib = ctypes.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+def _declare(L):
+    vp = ctypes.c_void_p
+    L.orc_exp.restype = ctypes.c_float
+    L.orc_exp.argtypes = [ctypes.c_float]
+    L.orc_silu.restype = ctypes.c_float
+    L.orc_silu.argtypes = [ctypes.c_float]
+    L.orc_matmul.argtypes = [vp, vp, _i64, _i64, vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_int]
+    L.orc_init_output.restype = ctypes.c_int
+    L.orc_init_output.argtypes = [vp, _i64, _i64, vp, vp]
+    L.orc_conv1x1.argtypes = [vp, _i64, _i64, vp, _i64, vp, vp, vp]
+    L.orc_conv3x3_forward.argtypes = [vp, _i64, _i64, _i64, _i64, vp, _i64, vp, ctypes.c_int, vp, ctypes.c_int,
+                                      vp, vp, ctypes.c_int, vp]
+    L.orc_conv3x3_im2col.argtypes = [vp, _i64, _i64, _i64, _i64, vp, _i64, vp, ctypes.c_int, vp, ctypes.c_int, vp]
+    L.orc_im2col_gather_row.argtypes = [vp, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int, _i64, vp]
+    L.orc_depthwise3x3.argtypes = [vp, _i64, _i64, _i64, _i64, vp, vp, ctypes.c_int, vp]
+    L.orc_group_norm_affine.argtypes = [vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, vp, vp, vp, vp, vp]
+    L.orc_group_norm_forward.argtypes = [vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, vp, vp, vp,
+                                         ctypes.c_int, vp]
+    L.orc_layer_norm.argtypes = [vp, _i64, _i64, vp, vp, ctypes.c_float, vp]
+    L.orc_silu_inplace.argtypes = [vp, _i64]
+    L.orc_add_inplace.argtypes = [vp, vp, _i64]
+    L.orc_concat_channels.argtypes = [vp, _i64, vp, _i64, _i64, vp]
+    L.orc_to_u8.argtypes = [vp, _i64, vp]
+    L.orc_set_threads.argtypes = [ctypes.c_int]
+    L.orc_get_threads.restype = ctypes.c_int
+
+
+def _p(a):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data
+
+
+def _f32(a):
+    if a is None:
+        return None
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(int(n))
+
+
+def threads() -> int:
+    return int(lib().orc_get_threads())
+
+
+def exp(x: float) -> float:
+    """src/engine/math.rs:17-30"""
+    return float(lib().orc_exp(float(x)))
+
+
+def silu_scalar(x: float) -> float:
+    """src/engine/math.rs:33-36"""
+    return float(lib().orc_silu(float(x)))
+
+
+def matmul(a, b, c=None, accumulate=False):
+    """src/engine/gemm.rs:63-132 with numpy views: a [m, k], b [k, n] of any strides."""
+    a = np.asarray(a, dtype=np.float32)
+    b = np.asarray(b, dtype=np.float32)
+    m, k = a.shape
+    k2, n = b.shape
+    assert k == k2, "inner dimensions differ"
+    if c is None:
+        c = np.zeros((m, n), np.float32)
+    es = 4
+    lib().orc_matmul(_p(c), a.ctypes.data, a.strides[0] // es, a.strides[1] // es, b.ctypes.data,
+                     b.strides[0] // es, b.strides[1] // es, m, k, n, int(bool(accumulate)))
+    return c
+
+
+def conv1x1(x, weight, bias=None, residual=None):
+    """src/engine/conv.rs:38-55: x [n,h,w,ci], weight [co, ci]."""
+    x, weight, bias, residual = _f32(x), _f32(weight), _f32(bias), _f32(residual)
+    n, h, w, ci = x.shape
+    co = weight.shape[0]
+    assert weight.shape == (co, ci), "Conv1x1 weight size"
+    out = np.empty((n, h, w, co), np.float32)
+    if residual is not None:
+        assert residual.shape == out.shape, "Conv1x1 residual shape"
+    lib().orc_conv1x1(_p(x), n * h * w, ci, _p(weight), co, _p(bias), _p(residual), _p(out))
+    return out
+
+
+def conv3x3_output_hw(h, w, stride=1, pad=(1, 1, 1, 1), upsample2x=False):
+    """src/engine/conv.rs:77-81"""
+    up = 2 if upsample2x else 1
+    return ((h * up + pad[0] + pad[2] - 3) // stride + 1, (w * up + pad[1] + pad[3] - 3) // stride + 1)
+
+
+def conv3x3(x, weight, bias=None, stride=1, pad=(1, 1, 1, 1), upsample2x=False, prologue=None, im2col=False):
+    """src/engine/conv.rs:83-102 (forward / forward_prologue) or 106-130 (im2col).
+
+    weight [co, 3, 3, ci]; prologue = (scale [n*ci], shift [n*ci], silu) or None."""
+    x, weight, bias = _f32(x), _f32(weight), _f32(bias)
+    n, h, w, ci = x.shape
+    co = weight.shape[0]
+    assert weight.size == 9 * ci * co, "Conv3x3 weight size"
+    ho, wo = conv3x3_output_hw(h, w, stride, pad, upsample2x)
+    out = np.empty((n, ho, wo, co), np.float32)
+    padv = (ctypes.c_int * 4)(*pad)
+    if im2col:
+        assert prologue is None
+        lib().orc_conv3x3_im2col(_p(x), n, h, w, ci, _p(weight), co, _p(bias), stride, padv, int(upsample2x),
+                                 _p(out))
+    else:
+        sc = sh = None
+        silu = 0
+        if prologue is not None:
+            assert stride == 1 and tuple(pad) == (1, 1, 1, 1), \
+                "Conv3x3 prologue needs the stride-1 / pad-1 Winograd path"
+            sc, sh, silu = _f32(prologue[0]), _f32(prologue[1]), int(prologue[2])
+        lib().orc_conv3x3_forward(_p(x), n, h, w, ci, _p(weight), co, _p(bias), stride, padv, int(upsample2x),
+                                  _p(sc), _p(sh), silu, _p(out))
+    return out
+
+
+def im2col_row(x, p, stride=1, pad=(1, 1, 1, 1), upsample2x=False):
+    """src/engine/conv.rs:145-165: patch row of output pixel p."""
+    x = _f32(x)
+    n, h, w, c = x.shape
+    ho, wo = conv3x3_output_hw(h, w, stride, pad, upsample2x)
+    row = np.empty(9 * c, np.float32)
+    lib().orc_im2col_gather_row(_p(x), n, h, w, c, ho, wo, stride, pad[0], pad[1], int(upsample2x), int(p), _p(row))
+    return row
+
+
+EPILOGUE = {"none": 0, "relu": 1, "glu_silu": 2}
+
+
+def depthwise3x3(x, weight, bias, epilogue="none"):
+    """src/engine/depthwise.rs:31-59; weight [3,3,c], bias [c]."""
+    x, weight, bias = _f32(x), _f32(weight), _f32(bias)
+    n, h, w, c = x.shape
+    assert weight.size == 9 * c, "depthwise weight size"
+    assert bias.size == c, "depthwise bias size"
+    ep = EPILOGUE[epilogue]
+    co = c // 2 if ep == 2 else c
+    out = np.empty((n, h, w, co), np.float32)
+    lib().orc_depthwise3x3(_p(x), n, h, w, c, _p(weight), _p(bias), ep, _p(out))
+    return out
+
+
+def group_norm_affine(x, groups, eps, gamma, beta, add=None):
+    """src/engine/norm.rs:57-105: returns (scale [n*c], shift [n*c])."""
+    x, gamma, beta, add = _f32(x), _f32(gamma), _f32(beta), _f32(add)
+    n, h, w, c = x.shape
+    assert c % groups == 0, "channels not divisible by groups"
+    scale = np.empty(n * c, np.float32)
+    shift = np.empty(n * c, np.float32)
+    lib().orc_group_norm_affine(_p(x), n, h, w, c, groups, float(eps), _p(gamma), _p(beta), _p(add), _p(scale),
+                                _p(shift))
+    return scale, shift
+
+
+def group_norm(x, groups, eps, gamma, beta, add=None, silu=False):
+    """src/engine/norm.rs:41-53"""
+    x, gamma, beta, add = _f32(x), _f32(gamma), _f32(beta), _f32(add)
+    n, h, w, c = x.shape
+    out = np.empty_like(x)
+    lib().orc_group_norm_forward(_p(x), n, h, w, c, groups, float(eps), _p(gamma), _p(beta), _p(add), int(silu),
+                                 _p(out))
+    return out
+
+
+def layer_norm(x, gamma, beta, eps):
+    """src/engine/norm.rs:151-173, over the last axis."""
+    x, gamma, beta = _f32(x), _f32(gamma), _f32(beta)
+    c = x.shape[-1]
+    out = np.empty_like(x)
+    lib().orc_layer_norm(_p(x), x.size // c, c, _p(gamma), _p(beta), float(eps), _p(out))
+    return out
+
+
+def silu(x):
+    """src/engine/ops.rs:11-13 (out of place)."""
+    y = _f32(x).copy()
+    lib().orc_silu_inplace(_p(y), y.size)
+    return y
+
+
+def add(a, b):
+    """src/engine/ops.rs:16-19 (out of place)."""
+    y = _f32(a).copy()
+    b = _f32(b)
+    assert y.size == b.size, "add length mismatch"
+    lib().orc_add_inplace(_p(y), _p(b), y.size)
+    return y
+
+
+def init_output(rows, cols, bias=None, residual=None):
+    """src/engine/conv.rs:170-191: returns (prefilled [rows, cols], accumulate)."""
+    bias, residual = _f32(bias), _f32(residual)
+    out = np.zeros((rows, cols), np.float32)
+    acc = lib().orc_init_output(_p(out), rows, cols, _p(bias), _p(residual))
+    return out, bool(acc)
+
+
+def concat_channels(a, b):
+    """src/engine/tensor.rs:59-73"""
+    a, b = _f32(a), _f32(b)
+    assert a.shape[:3] == b.shape[:3], "concat_channels: spatial shapes differ"
+    n, h, w, ca = a.shape
+    cb = b.shape[3]
+    out = np.empty((n, h, w, ca + cb), np.float32)
+    lib().orc_concat_channels(_p(a), ca, _p(b), cb, n * h * w, _p(out))
+    return out
+
+
+def to_u8(x):
+    """src/imaging/blend.rs:21-24"""
+    x = _f32(x)
+    out = np.empty(x.shape, np.uint8)
+    lib().orc_to_u8(_p(x), x.size, _p(out))
+    return out

@@ -1,0 +1,182 @@
+/*
+ * moebius-hip C API: the MI355X (gfx950) conv/norm hot path of moebius-cpu.
+ *
+ * Conventions follow the reference's C API (include/moebius_cpu.h:11-19,
+ * 48-51): status codes, a thread-local last-error string, no exceptions or
+ * panics across the boundary. Below it, one entry point per `src/engine`
+ * kernel a Rust `extern "C"` shim would bind in place of the CPU kernel
+ * (each cites the reference function it replaces), plus the device plumbing
+ * (context, memory, events) such a shim needs.
+ *
+ * Memory and ordering:
+ *  - Tensors are device pointers to dense NHWC f32 (row-major over n, h, w, c),
+ *    exactly the reference's `Tensor` layout (src/engine/tensor.rs:11-34).
+ *  - Weights use the converter layouts (tools/convert_weights.py:25-28):
+ *    1x1 [c_out, c_in], dense 3x3 [c_out, 3, 3, c_in], depthwise [3, 3, c].
+ *    GEMM weights may be f32 or f16 (`Param`, src/engine/param.rs:14-17);
+ *    f16 is widened to f32 exactly before the arithmetic.
+ *  - Outputs must not alias inputs (src/engine/tensor.rs:58) unless the entry
+ *    point says "in place".
+ *  - Every kernel entry point is asynchronous on the context's stream (no
+ *    host synchronisation); mh_synchronize / mh_memcpy_d2h order the host.
+ *  - Shape checks that the reference asserts (a panic) return
+ *    MH_ERR_INVALID_ARGUMENT with the reference's assertion text.
+ */
+#ifndef MOEBIUS_HIP_H
+#define MOEBIUS_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MH_ABI_VERSION 1u
+
+/* Same values as MOEBIUS_OK .. MOEBIUS_ERR_INTERNAL (include/moebius_cpu.h:13-19). */
+#define MH_OK 0
+#define MH_ERR_INVALID_ARGUMENT 1
+#define MH_ERR_WEIGHTS 2
+#define MH_ERR_UNSUPPORTED_DEVICE 3 /* moebius_cpu.h: MOEBIUS_ERR_UNSUPPORTED_CPU */
+#define MH_ERR_CANCELLED 4
+#define MH_ERR_IO 5
+#define MH_ERR_INTERNAL 6
+#define MH_ERR_OUT_OF_MEMORY 7 /* new: device memory exhausted */
+
+/* Param storage (src/engine/param.rs:14-17). */
+#define MH_DTYPE_F32 0u
+#define MH_DTYPE_F16 1u
+
+/* Depthwise epilogues (src/engine/depthwise.rs:22-28). */
+#define MH_EPILOGUE_NONE 0u
+#define MH_EPILOGUE_RELU 1u
+#define MH_EPILOGUE_GLU_SILU 2u
+
+/* Arithmetic of the GEMM-shaped kernels. EXACT: f32 MFMA, f32 accumulate (the
+ * reference's arithmetic). FAST: activations and weights rounded to f16, f16
+ * MFMA with f32 accumulate. */
+#define MH_PRECISION_EXACT 0u
+#define MH_PRECISION_FAST 1u
+
+typedef struct MhContext MhContext;
+typedef struct MhEvent MhEvent;
+
+/* ---- library / context (moebius_cpu.h:48-56 conventions) ---- */
+uint32_t mh_abi_version(void);
+/* Message of the last failed call on the calling thread. Never NULL. */
+const char *mh_last_error(void);
+/* device: HIP ordinal. Creates one stream (default priority) and a workspace. */
+int32_t mh_context_create(int32_t device, MhContext **out);
+void mh_context_destroy(MhContext *ctx);
+int32_t mh_context_set_precision(MhContext *ctx, uint32_t precision);
+/* The context's hipStream_t, for callers that order their own work with it. */
+void *mh_context_stream(MhContext *ctx);
+int32_t mh_synchronize(MhContext *ctx);
+/* Name of the device's ISA (e.g. "gfx950") into buf; fails on other ISAs' kernels. */
+int32_t mh_device_arch(MhContext *ctx, char *buf, uint32_t len);
+
+/* ---- device memory (the reference's Vec<f32> buffers, now in HBM) ---- */
+int32_t mh_malloc(MhContext *ctx, uint64_t bytes, void **out);
+int32_t mh_free(MhContext *ctx, void *ptr);
+/* Synchronous copies on the context's stream. */
+int32_t mh_memcpy_h2d(MhContext *ctx, void *dst, const void *src, uint64_t bytes);
+int32_t mh_memcpy_d2h(MhContext *ctx, void *dst, const void *src, uint64_t bytes);
+int32_t mh_memcpy_d2d(MhContext *ctx, void *dst, const void *src, uint64_t bytes);
+
+/* ---- timing on the context's stream ---- */
+int32_t mh_event_create(MhContext *ctx, MhEvent **out);
+int32_t mh_event_record(MhContext *ctx, MhEvent *ev);
+/* Waits for `end`; milliseconds between the two records. */
+int32_t mh_event_elapsed_ms(MhEvent *start, MhEvent *end, float *ms);
+void mh_event_destroy(MhEvent *ev);
+
+/* ---- engine kernels (src/engine) ---- */
+
+/* src/engine/conv.rs:170-191 `init_output`, fused with the accumulate it
+ * prepares: out[r, :] = (residual[r, :] + bias) + x[r, :]. bias and residual
+ * may each be NULL (then that term is absent). rows x cols, row-major. */
+int32_t mh_bias_residual_add(MhContext *ctx, const float *x, uint64_t rows, uint32_t cols, const float *bias,
+                             const float *residual, float *out);
+
+/* src/engine/conv.rs:38-55 `Conv1x1::forward`: out = x . W^T + bias (+ residual).
+ * x [n,h,w,c_in]; weight [c_out, c_in] (dtype MH_DTYPE_*); bias [c_out] or NULL;
+ * residual [n,h,w,c_out] or NULL; out [n,h,w,c_out]. */
+int32_t mh_conv1x1_forward(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c_in,
+                           const void *weight, uint32_t weight_dtype, uint32_t c_out, const float *bias,
+                           const float *residual, float *out);
+
+/* src/engine/conv.rs:77-81 `Conv3x3::output_hw`. pad = [top, left, bottom, right]. */
+int32_t mh_conv3x3_output_hw(uint32_t h, uint32_t w, uint32_t stride, const uint32_t pad[4], uint32_t upsample2x,
+                             uint32_t *ho, uint32_t *wo);
+
+/* src/engine/conv.rs:83-102 `Conv3x3::forward` / `forward_prologue`:
+ * out = conv3x3(f(x)) + bias, any stride / padding, optional nearest-2x
+ * upsample of the input; f is the GroupNorm affine (+SiLU) of
+ * src/engine/norm.rs:33-37 when prologue_scale/shift ([n * c_in] each) are
+ * given, applied to in-image values only (padding stays zero). As in the
+ * reference, a prologue needs stride 1 and pad [1,1,1,1].
+ * weight [c_out, 3, 3, c_in]; out [n, ho, wo, c_out]. */
+int32_t mh_conv3x3_forward(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c_in,
+                           const void *weight, uint32_t weight_dtype, uint32_t c_out, const float *bias,
+                           uint32_t stride, const uint32_t pad[4], uint32_t upsample2x, const float *prologue_scale,
+                           const float *prologue_shift, uint32_t prologue_silu, float *out);
+
+/* src/engine/conv.rs:145-165 `Geometry::gather`: patch rows [3,3,c] of output
+ * pixels first..first+count (the implicit-GEMM conv's A operand, materialised
+ * for a bit-exact check). rows [count, 9*c]. */
+int32_t mh_im2col_gather(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
+                         uint32_t stride, const uint32_t pad[4], uint32_t upsample2x, uint64_t first, uint64_t count,
+                         float *rows);
+
+/* src/engine/depthwise.rs:31-59 `depthwise3x3`: stride 1, zero pad 1.
+ * weight [3,3,c], bias [c]; out [n,h,w,c] (c/2 channels for GLU_SILU). */
+int32_t mh_depthwise3x3(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
+                        const float *weight, const float *bias, uint32_t epilogue, float *out);
+
+/* src/engine/norm.rs:57-105 `GroupNorm::affine`: per item and channel
+ * scale/shift ([n * c] each, device) with GN(x + add) = x.scale + shift.
+ * add [n * c] or NULL. Statistics: f32 per-channel partials over 256-pixel
+ * chunks, folded per group in f64. */
+int32_t mh_group_norm_affine(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
+                             uint32_t groups, float eps, const float *gamma, const float *beta, const float *add,
+                             float *scale, float *shift);
+
+/* src/engine/norm.rs:41-53 `GroupNorm::forward`: out = [SiLU](GN(x + add)). */
+int32_t mh_group_norm_forward(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
+                              uint32_t groups, float eps, const float *gamma, const float *beta, const float *add,
+                              uint32_t silu, float *out);
+
+/* src/engine/norm.rs:132-148 `apply_affine` over n items: out = [SiLU](x.scale + shift). */
+int32_t mh_apply_affine(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
+                        const float *scale, const float *shift, uint32_t silu, float *out);
+
+/* src/engine/norm.rs:151-173 `layer_norm` over the channel axis of rows tokens. */
+int32_t mh_layer_norm(MhContext *ctx, const float *x, uint64_t rows, uint32_t c, const float *gamma,
+                      const float *beta, float eps, float *out);
+
+/* src/engine/ops.rs:11-13 `silu_inplace` (in place). */
+int32_t mh_silu_inplace(MhContext *ctx, float *x, uint64_t len);
+/* src/engine/ops.rs:16-19 `add_inplace`: a += b (in place on a). */
+int32_t mh_add_inplace(MhContext *ctx, float *a, const float *b, uint64_t len);
+
+/* src/engine/tensor.rs:59-73 `concat_channels_into`: out[p] = [a[p] || b[p]]. */
+int32_t mh_concat_channels(MhContext *ctx, const float *a, uint32_t ca, const float *b, uint32_t cb,
+                           uint64_t pixels, float *out);
+
+/* src/imaging/blend.rs:21-24 `to_u8`: (clamp(v,0,1)*255) truncated, NaN -> 0. */
+int32_t mh_to_u8(MhContext *ctx, const float *x, uint64_t len, uint8_t *out);
+
+/* src/engine/math.rs:17-36 on device: y = exp(x) (which=0) or SiLU(x) (which=1),
+ * the reference's Cephes polynomial, for bit-exact checks of the device math. */
+int32_t mh_math_eval(MhContext *ctx, uint32_t which, const float *x, uint64_t len, float *y);
+
+/* Lane-layout probe of the f32 matrix instruction the convs use (no
+ * counterpart in the reference): d[32][32] = a[32][2] . b[2][32] through one
+ * v_mfma_f32_32x32x2f32, all operands host memory. */
+int32_t mh_selftest_mfma_f32(MhContext *ctx, const float *a, const float *b, float *d);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MOEBIUS_HIP_H */

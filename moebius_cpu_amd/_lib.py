@@ -1,0 +1,111 @@
+"""ctypes declarations of include/moebius_hip.h over libmoebius_hip.so.
+
+Loading fails loudly when the library is missing: there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmoebius_hip.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "moebius_hip.h")
+
+OK = 0
+ERR_INVALID_ARGUMENT = 1
+ERR_WEIGHTS = 2
+ERR_UNSUPPORTED_DEVICE = 3
+ERR_CANCELLED = 4
+ERR_IO = 5
+ERR_INTERNAL = 6
+ERR_OUT_OF_MEMORY = 7
+
+DTYPE_F32 = 0
+DTYPE_F16 = 1
+EPILOGUE = {"none": 0, "relu": 1, "glu_silu": 2}
+PRECISION_EXACT = 0
+PRECISION_FAST = 1
+
+
+class MoebiusError(RuntimeError):
+    """A non-zero status from the C API, with mh_last_error's message."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+        self.msg = msg
+
+
+_vp = ctypes.c_void_p
+_u32 = ctypes.c_uint32
+_u64 = ctypes.c_uint64
+_i32 = ctypes.c_int32
+_f32 = ctypes.c_float
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+
+# name -> (restype, argtypes); every function include/moebius_hip.h declares.
+SIGNATURES = {
+    "mh_abi_version": (_u32, []),
+    "mh_last_error": (ctypes.c_char_p, []),
+    "mh_context_create": (_i32, [_i32, ctypes.POINTER(_vp)]),
+    "mh_context_destroy": (None, [_vp]),
+    "mh_context_set_precision": (_i32, [_vp, _u32]),
+    "mh_context_stream": (_vp, [_vp]),
+    "mh_synchronize": (_i32, [_vp]),
+    "mh_device_arch": (_i32, [_vp, ctypes.c_char_p, _u32]),
+    "mh_malloc": (_i32, [_vp, _u64, ctypes.POINTER(_vp)]),
+    "mh_free": (_i32, [_vp, _vp]),
+    "mh_memcpy_h2d": (_i32, [_vp, _vp, _vp, _u64]),
+    "mh_memcpy_d2h": (_i32, [_vp, _vp, _vp, _u64]),
+    "mh_memcpy_d2d": (_i32, [_vp, _vp, _vp, _u64]),
+    "mh_event_create": (_i32, [_vp, ctypes.POINTER(_vp)]),
+    "mh_event_record": (_i32, [_vp, _vp]),
+    "mh_event_elapsed_ms": (_i32, [_vp, _vp, ctypes.POINTER(_f32)]),
+    "mh_event_destroy": (None, [_vp]),
+    "mh_bias_residual_add": (_i32, [_vp, _vp, _u64, _u32, _vp, _vp, _vp]),
+    "mh_conv1x1_forward": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _u32, _u32, _vp, _vp, _vp]),
+    "mh_conv3x3_output_hw": (_i32, [_u32, _u32, _u32, _u32p, _u32, _u32p, _u32p]),
+    "mh_conv3x3_forward": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _u32, _u32, _vp, _u32, _u32p, _u32,
+                                  _vp, _vp, _u32, _vp]),
+    "mh_im2col_gather": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32p, _u32, _u64, _u64, _vp]),
+    "mh_depthwise3x3": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _vp]),
+    "mh_group_norm_affine": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _f32, _vp, _vp, _vp, _vp, _vp]),
+    "mh_group_norm_forward": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _f32, _vp, _vp, _vp, _u32, _vp]),
+    "mh_apply_affine": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _vp]),
+    "mh_layer_norm": (_i32, [_vp, _vp, _u64, _u32, _vp, _vp, _f32, _vp]),
+    "mh_silu_inplace": (_i32, [_vp, _vp, _u64]),
+    "mh_add_inplace": (_i32, [_vp, _vp, _vp, _u64]),
+    "mh_concat_channels": (_i32, [_vp, _vp, _u32, _vp, _u32, _u64, _vp]),
+    "mh_to_u8": (_i32, [_vp, _vp, _u64, _vp]),
+    "mh_math_eval": (_i32, [_vp, _u32, _vp, _u64, _vp]),
+    "mh_selftest_mfma_f32": (_i32, [_vp, _vp, _vp, _vp]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"HIP library not built: {LIB_PATH} is missing (run __graft_entry__.build() or "
+                "`python -m moebius_cpu_amd.build`); there is no CPU fallback")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != OK:
+        msg = lib().mh_last_error().decode("utf-8", "replace")
+        raise MoebiusError(int(status), msg)
+
+
+def u32x4(vals):
+    return (ctypes.c_uint32 * 4)(*[int(v) for v in vals])

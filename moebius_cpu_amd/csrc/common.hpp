@@ -1,0 +1,92 @@
+// Shared host-side plumbing of the HIP library: errors, the per-device
+// context (stream + workspace arena), device helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace mh {
+
+// Status codes of include/moebius_hip.h (the reference's moebius_cpu.h:13-19 values).
+enum Status : int32_t {
+    kOk = 0,
+    kInvalidArgument = 1,
+    kWeights = 2,
+    kUnsupportedDevice = 3,
+    kCancelled = 4,
+    kIo = 5,
+    kInternal = 6,
+    kOutOfMemory = 7,
+};
+
+struct Error : std::runtime_error {
+    int32_t code;
+    Error(int32_t c, const std::string &m) : std::runtime_error(m), code(c) {}
+};
+
+[[noreturn]] void fail(int32_t code, const std::string &msg);
+[[noreturn]] void hip_fail(hipError_t e, const char *expr, const char *file, int line);
+
+#define MH_REQUIRE(cond, msg)                                         \
+    do {                                                              \
+        if (!(cond)) ::mh::fail(::mh::kInvalidArgument, (msg));      \
+    } while (0)
+
+#define HIP_CHECK(expr)                                                          \
+    do {                                                                         \
+        hipError_t e_ = (expr);                                                  \
+        if (e_ != hipSuccess) ::mh::hip_fail(e_, #expr, __FILE__, __LINE__);     \
+    } while (0)
+
+#define MH_LAUNCH_CHECK() HIP_CHECK(hipGetLastError())
+
+enum class Precision : uint32_t { Exact = 0, Fast = 1 };
+
+// Device arena for kernel scratch (split-K partials, norm partials): grown on
+// demand, kept for the context's life, like the reference's `Scratch` panels
+// (src/engine/mod.rs:25-34). Growth synchronises the stream first, since
+// queued kernels may still read the old block.
+class Workspace {
+  public:
+    Workspace() = default;
+    Workspace(const Workspace &) = delete;
+    Workspace &operator=(const Workspace &) = delete;
+    ~Workspace();
+    void *get(size_t bytes, hipStream_t stream);
+    size_t capacity() const { return cap_; }
+
+  private:
+    void *ptr_ = nullptr;
+    size_t cap_ = 0;
+};
+
+struct Context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    Precision precision = Precision::Exact;
+    int cu_count = 0;
+    std::string arch;
+    Workspace ws;
+    // Self-resetting completion counters for "last block finalises" kernels.
+    // Zeroed once at creation; every kernel that increments one returns it
+    // to zero, so no memset is ever queued (graph-capture safe).
+    unsigned int *counters = nullptr;
+    static constexpr int kCounters = 4096;
+    int next_counter = 0;
+    unsigned int *counter_block(int n);
+
+    explicit Context(int dev);
+    ~Context();
+    Context(const Context &) = delete;
+    Context &operator=(const Context &) = delete;
+};
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// NULL counts as aligned (an absent optional operand).
+inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace mh

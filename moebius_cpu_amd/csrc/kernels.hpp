@@ -1,0 +1,61 @@
+// Host-side C++ engine API over the gfx950 kernels: one function per
+// moebius-cpu `src/engine` entry point (same argument meaning), used by the C
+// ABI (capi.cpp) and by the UNet / VAE block chains. All calls are
+// asynchronous on ctx.stream; shapes are validated here with the reference's
+// assertion texts and raise mh::Error.
+#pragma once
+
+#include <cstdint>
+
+#include "common.hpp"
+
+namespace mh {
+
+enum WeightType : uint32_t { kF32 = 0, kF16 = 1 };
+
+// Epilogues the GEMM-shaped kernels can fuse after `acc + bias (+ residual)`.
+enum class GemmEpilogue : int { None = 0, Silu = 1 };
+
+// GroupNorm affine handed to a consumer (src/engine/norm.rs:33-37): per item
+// and channel scale/shift, device arrays [n * c].
+struct Affine {
+    const float *scale = nullptr;
+    const float *shift = nullptr;
+    bool silu = false;
+};
+
+// ---- elementwise (elementwise.hip) ----
+void bias_residual_add(Context &ctx, const float *x, int64_t rows, int cols, const float *bias,
+                       const float *residual, float *out);
+void silu_inplace(Context &ctx, float *x, int64_t len);
+void add_inplace(Context &ctx, float *a, const float *b, int64_t len);
+void concat_channels(Context &ctx, const float *a, int ca, const float *b, int cb, int64_t pixels, float *out);
+void to_u8(Context &ctx, const float *x, int64_t len, uint8_t *out);
+void math_eval(Context &ctx, int which, const float *x, int64_t len, float *y);
+
+// ---- normalisation (norm.hip) ----
+void group_norm_affine(Context &ctx, const float *x, int n, int h, int w, int c, int groups, float eps,
+                       const float *gamma, const float *beta, const float *add, float *scale, float *shift);
+void apply_affine(Context &ctx, const float *x, int n, int h, int w, int c, const float *scale, const float *shift,
+                  bool silu, float *out);
+void group_norm_forward(Context &ctx, const float *x, int n, int h, int w, int c, int groups, float eps,
+                        const float *gamma, const float *beta, const float *add, bool silu, float *out);
+void layer_norm(Context &ctx, const float *x, int64_t rows, int c, const float *gamma, const float *beta, float eps,
+                float *out);
+
+// ---- depthwise (depthwise.hip) ----
+void depthwise3x3(Context &ctx, const float *x, int n, int h, int w, int c, const float *weight, const float *bias,
+                  int epilogue, float *out);
+
+// ---- GEMM-shaped convs (gemm.hip) ----
+void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void *weight, WeightType wt, int c_out,
+             const float *bias, const float *residual, float *out, GemmEpilogue epi = GemmEpilogue::None);
+void conv3x3(Context &ctx, const float *x, int n, int h, int w, int c_in, const void *weight, WeightType wt,
+             int c_out, const float *bias, int stride, const int pad[4], bool upsample2x, const Affine *prologue,
+             float *out);
+void conv3x3_output_hw(int h, int w, int stride, const int pad[4], bool upsample2x, int *ho, int *wo);
+void im2col_gather(Context &ctx, const float *x, int n, int h, int w, int c, int stride, const int pad[4],
+                   bool upsample2x, int64_t first, int64_t count, float *rows);
+void selftest_mfma_f32(Context &ctx, const float *a_host, const float *b_host, float *d_host);
+
+}  // namespace mh

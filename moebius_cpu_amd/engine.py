@@ -1,0 +1,384 @@
+"""Host-side mirror of moebius-cpu's `src/engine` API over the HIP C ABI.
+
+Same type and function names as the reference (`Tensor`, `Param`, `Conv1x1`,
+`Conv3x3`, `GroupNorm`, `Affine`, `depthwise3x3`, `layer_norm`,
+`silu_inplace`, `add_inplace`, `concat_channels_into`), same argument meaning,
+and the reference's assertion texts as `MoebiusError` messages, so the parity
+tests read like the reference's own tests/kernels.rs. Tensors live in HBM;
+`.numpy()` copies back. Every call goes through libmoebius_hip.so.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from ._lib import MoebiusError, check, lib, u32x4
+
+
+class Context:
+    """One device, one stream (include/moebius_hip.h `MhContext`)."""
+
+    def __init__(self, device: int = 0):
+        h = ctypes.c_void_p()
+        check(lib().mh_context_create(int(device), ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().mh_context_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def synchronize(self):
+        check(lib().mh_synchronize(self.h))
+
+    def set_precision(self, fast: bool):
+        check(lib().mh_context_set_precision(self.h, _lib.PRECISION_FAST if fast else _lib.PRECISION_EXACT))
+
+    @property
+    def arch(self) -> str:
+        buf = ctypes.create_string_buffer(64)
+        check(lib().mh_device_arch(self.h, buf, 64))
+        return buf.value.decode()
+
+    # ---- timing
+    def event(self):
+        return Event(self)
+
+
+class Event:
+    def __init__(self, ctx: Context):
+        self.ctx = ctx
+        h = ctypes.c_void_p()
+        check(lib().mh_event_create(ctx.h, ctypes.byref(h)))
+        self.h = h
+
+    def record(self):
+        check(lib().mh_event_record(self.ctx.h, self.h))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = ctypes.c_float()
+        check(lib().mh_event_elapsed_ms(self.h, end.h, ctypes.byref(ms)))
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            lib().mh_event_destroy(self.h)
+        except Exception:
+            pass
+
+
+class DeviceArray:
+    """A flat device buffer with a numpy dtype and shape."""
+
+    def __init__(self, ctx: Context, shape, dtype=np.float32):
+        self.ctx = ctx
+        self.dtype = np.dtype(dtype)
+        self.shape = tuple(int(s) for s in shape)
+        self.nbytes = int(np.prod(self.shape, dtype=np.int64)) * self.dtype.itemsize
+        self._cap = self.nbytes
+        p = ctypes.c_void_p()
+        check(lib().mh_malloc(ctx.h, max(self.nbytes, 1), ctypes.byref(p)))
+        self.ptr = p.value
+
+    @classmethod
+    def from_numpy(cls, ctx: Context, arr) -> "DeviceArray":
+        arr = np.ascontiguousarray(arr)
+        d = cls(ctx, arr.shape, arr.dtype)
+        if arr.nbytes:
+            check(lib().mh_memcpy_h2d(ctx.h, d.ptr, arr.ctypes.data, arr.nbytes))
+        return d
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr, dtype=self.dtype)
+        assert arr.nbytes == self.nbytes, "upload size mismatch"
+        check(lib().mh_memcpy_h2d(self.ctx.h, self.ptr, arr.ctypes.data, arr.nbytes))
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        if self.nbytes:
+            check(lib().mh_memcpy_d2h(self.ctx.h, out.ctypes.data, self.ptr, self.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr:
+            lib().mh_free(self.ctx.h, self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if self.ctx.h:
+                self.free()
+        except Exception:
+            pass
+
+
+def _ptr(t):
+    return None if t is None else t.ptr
+
+
+class Tensor(DeviceArray):
+    """Dense NHWC f32 activation tensor in HBM (src/engine/tensor.rs:11-34)."""
+
+    def __init__(self, ctx: Context, n=0, h=0, w=0, c=0):
+        super().__init__(ctx, (n, h, w, c), np.float32)
+
+    @classmethod
+    def from_numpy(cls, ctx: Context, arr) -> "Tensor":
+        arr = np.ascontiguousarray(arr, dtype=np.float32)
+        assert arr.ndim == 4, "Tensor is [n, h, w, c]"
+        t = cls(ctx, *arr.shape)
+        if arr.nbytes:
+            check(lib().mh_memcpy_h2d(ctx.h, t.ptr, arr.ctypes.data, arr.nbytes))
+        return t
+
+    @property
+    def n(self):
+        return self.shape[0]
+
+    @property
+    def h(self):
+        return self.shape[1]
+
+    @property
+    def w(self):
+        return self.shape[2]
+
+    @property
+    def c(self):
+        return self.shape[3]
+
+    def pixels(self) -> int:
+        return self.n * self.h * self.w
+
+    def set_shape(self, n, h, w, c):
+        """Reshape for use as an output; reallocates only when growing (tensor.rs:31-34)."""
+        need = n * h * w * c * 4
+        if need > self._cap:
+            self.free()
+            p = ctypes.c_void_p()
+            check(lib().mh_malloc(self.ctx.h, max(need, 1), ctypes.byref(p)))
+            self.ptr = p.value
+            self._cap = need
+        self.shape = (n, h, w, c)
+        self.nbytes = need
+
+
+class Param:
+    """GEMM weight in its stored precision (src/engine/param.rs:14-17)."""
+
+    def __init__(self, ctx: Context, values, f16: bool = False):
+        arr = np.ascontiguousarray(values, dtype=np.float16 if f16 else np.float32)
+        self.dtype = _lib.DTYPE_F16 if f16 else _lib.DTYPE_F32
+        self.buf = DeviceArray.from_numpy(ctx, arr)
+        self.size = arr.size
+
+    @classmethod
+    def f16_from(cls, ctx: Context, values) -> "Param":
+        """Round an f32 tensor to f16 storage (param.rs:29-31)."""
+        return cls(ctx, np.asarray(values, np.float32).astype(np.float16), f16=True)
+
+    def __len__(self):
+        return self.size
+
+    @property
+    def ptr(self):
+        return self.buf.ptr
+
+
+def _vec(ctx, v):
+    if v is None:
+        return None
+    if isinstance(v, DeviceArray):
+        return v
+    return DeviceArray.from_numpy(ctx, np.ascontiguousarray(v, dtype=np.float32))
+
+
+class Conv1x1:
+    """src/engine/conv.rs:28-56"""
+
+    def __init__(self, ctx, c_in, c_out, weight: Param, bias=None):
+        self.ctx, self.c_in, self.c_out, self.weight = ctx, c_in, c_out, weight
+        self.bias = _vec(ctx, bias)
+
+    def forward(self, x: Tensor, out: Tensor, residual: Tensor | None = None):
+        if x.c != self.c_in:
+            raise MoebiusError(1, "Conv1x1 input channels")
+        if len(self.weight) != self.c_in * self.c_out:
+            raise MoebiusError(1, "Conv1x1 weight size")
+        out.set_shape(x.n, x.h, x.w, self.c_out)
+        if residual is not None and residual.shape != out.shape:
+            raise MoebiusError(1, "Conv1x1 residual shape")
+        check(lib().mh_conv1x1_forward(self.ctx.h, x.ptr, x.n, x.h, x.w, x.c, self.weight.ptr, self.weight.dtype,
+                                       self.c_out, _ptr(self.bias), _ptr(residual), out.ptr))
+
+
+class Affine:
+    """Per-item, per-channel GroupNorm affine (src/engine/norm.rs:33-37)."""
+
+    def __init__(self, scale: DeviceArray, shift: DeviceArray, silu: bool):
+        self.scale, self.shift, self.silu = scale, shift, silu
+
+
+class Conv3x3:
+    """src/engine/conv.rs:58-131"""
+
+    def __init__(self, ctx, c_in, c_out, weight: Param, bias=None, stride=1, pad=(1, 1, 1, 1), upsample2x=False):
+        self.ctx, self.c_in, self.c_out, self.weight = ctx, c_in, c_out, weight
+        self.bias = _vec(ctx, bias)
+        self.stride, self.pad, self.upsample2x = stride, tuple(pad), upsample2x
+
+    @classmethod
+    def same(cls, ctx, c_in, c_out, weight, bias=None):
+        return cls(ctx, c_in, c_out, weight, bias)
+
+    def output_hw(self, h, w):
+        ho, wo = ctypes.c_uint32(), ctypes.c_uint32()
+        check(lib().mh_conv3x3_output_hw(h, w, self.stride, u32x4(self.pad), int(self.upsample2x),
+                                         ctypes.byref(ho), ctypes.byref(wo)))
+        return ho.value, wo.value
+
+    def forward(self, x: Tensor, out: Tensor):
+        self.forward_prologue(x, None, out)
+
+    def forward_prologue(self, x: Tensor, prologue: Affine | None, out: Tensor):
+        if x.c != self.c_in:
+            raise MoebiusError(1, "Conv3x3 input channels")
+        if len(self.weight) != 9 * self.c_in * self.c_out:
+            raise MoebiusError(1, "Conv3x3 weight size")
+        ho, wo = self.output_hw(x.h, x.w)
+        out.set_shape(x.n, ho, wo, self.c_out)
+        sc = sh = None
+        silu = 0
+        if prologue is not None:
+            sc, sh, silu = prologue.scale.ptr, prologue.shift.ptr, int(prologue.silu)
+        check(lib().mh_conv3x3_forward(self.ctx.h, x.ptr, x.n, x.h, x.w, x.c, self.weight.ptr, self.weight.dtype,
+                                       self.c_out, _ptr(self.bias), self.stride, u32x4(self.pad),
+                                       int(self.upsample2x), sc, sh, silu, out.ptr))
+
+
+def im2col_gather(x: Tensor, stride=1, pad=(1, 1, 1, 1), upsample2x=False, first=0, count=None) -> np.ndarray:
+    """src/engine/conv.rs:145-165 patch rows, gathered on the device."""
+    ho, wo = ctypes.c_uint32(), ctypes.c_uint32()
+    check(lib().mh_conv3x3_output_hw(x.h, x.w, stride, u32x4(pad), int(upsample2x), ctypes.byref(ho),
+                                     ctypes.byref(wo)))
+    total = x.n * ho.value * wo.value
+    count = total - first if count is None else count
+    rows = DeviceArray(x.ctx, (count, 9 * x.c))
+    check(lib().mh_im2col_gather(x.ctx.h, x.ptr, x.n, x.h, x.w, x.c, stride, u32x4(pad), int(upsample2x), first,
+                                 count, rows.ptr))
+    return rows.numpy()
+
+
+class GroupNorm:
+    """src/engine/norm.rs:22-105"""
+
+    def __init__(self, ctx, groups, eps, gamma, beta):
+        self.ctx, self.groups, self.eps = ctx, groups, float(eps)
+        self.gamma, self.beta = _vec(ctx, gamma), _vec(ctx, beta)
+        self.c = self.gamma.shape[0]
+
+    def _check(self, x, add):
+        if x.c % self.groups != 0:
+            raise MoebiusError(1, "channels not divisible by groups")
+        if self.c != x.c:
+            raise MoebiusError(1, "GroupNorm gamma size")
+        if add is not None and add.nbytes // 4 != x.n * x.c:
+            raise MoebiusError(1, "GroupNorm add size")
+
+    def affine(self, x: Tensor, add: DeviceArray | None, silu_out: bool) -> Affine:
+        self._check(x, add)
+        scale = DeviceArray(self.ctx, (x.n * x.c,))
+        shift = DeviceArray(self.ctx, (x.n * x.c,))
+        check(lib().mh_group_norm_affine(self.ctx.h, x.ptr, x.n, x.h, x.w, x.c, self.groups, self.eps,
+                                         self.gamma.ptr, self.beta.ptr, _ptr(add), scale.ptr, shift.ptr))
+        return Affine(scale, shift, silu_out)
+
+    def forward(self, x: Tensor, add: DeviceArray | None, silu_out: bool, out: Tensor):
+        self._check(x, add)
+        out.set_shape(x.n, x.h, x.w, x.c)
+        check(lib().mh_group_norm_forward(self.ctx.h, x.ptr, x.n, x.h, x.w, x.c, self.groups, self.eps,
+                                          self.gamma.ptr, self.beta.ptr, _ptr(add), int(silu_out), out.ptr))
+
+
+def apply_affine(x: Tensor, aff: Affine, out: Tensor):
+    """src/engine/norm.rs:132-148 over every item."""
+    out.set_shape(x.n, x.h, x.w, x.c)
+    check(lib().mh_apply_affine(x.ctx.h, x.ptr, x.n, x.h, x.w, x.c, aff.scale.ptr, aff.shift.ptr, int(aff.silu),
+                                out.ptr))
+
+
+def depthwise3x3(x: Tensor, weight, bias, epilogue: str, out: Tensor):
+    """src/engine/depthwise.rs:31-59; epilogue 'none' | 'relu' | 'glu_silu'."""
+    ctx = x.ctx
+    weight, bias = _vec(ctx, weight), _vec(ctx, bias)
+    if weight.nbytes // 4 != 9 * x.c:
+        raise MoebiusError(1, "depthwise weight size")
+    if bias.nbytes // 4 != x.c:
+        raise MoebiusError(1, "depthwise bias size")
+    ep = _lib.EPILOGUE[epilogue]
+    if ep == 2 and x.c % 2:
+        raise MoebiusError(1, "GLU needs an even channel count")
+    out.set_shape(x.n, x.h, x.w, x.c // 2 if ep == 2 else x.c)
+    check(lib().mh_depthwise3x3(ctx.h, x.ptr, x.n, x.h, x.w, x.c, weight.ptr, bias.ptr, ep, out.ptr))
+
+
+def layer_norm(x: Tensor, gamma, beta, eps: float, out: Tensor):
+    """src/engine/norm.rs:151-163"""
+    ctx = x.ctx
+    gamma, beta = _vec(ctx, gamma), _vec(ctx, beta)
+    if gamma.shape[0] != x.c:
+        raise MoebiusError(1, "LayerNorm gamma size")
+    out.set_shape(x.n, x.h, x.w, x.c)
+    check(lib().mh_layer_norm(ctx.h, x.ptr, x.pixels(), x.c, gamma.ptr, beta.ptr, float(eps), out.ptr))
+
+
+def silu_inplace(x: DeviceArray):
+    """src/engine/ops.rs:11-13"""
+    check(lib().mh_silu_inplace(x.ctx.h, x.ptr, x.nbytes // 4))
+
+
+def add_inplace(a: DeviceArray, b: DeviceArray):
+    """src/engine/ops.rs:16-19"""
+    if a.nbytes != b.nbytes:
+        raise MoebiusError(1, "add length mismatch")
+    check(lib().mh_add_inplace(a.ctx.h, a.ptr, b.ptr, a.nbytes // 4))
+
+
+def concat_channels_into(a: Tensor, b: Tensor, out: Tensor):
+    """src/engine/tensor.rs:59-73"""
+    if (a.n, a.h, a.w) != (b.n, b.h, b.w):
+        raise MoebiusError(1, "concat_channels: spatial shapes differ")
+    out.set_shape(a.n, a.h, a.w, a.c + b.c)
+    check(lib().mh_concat_channels(a.ctx.h, a.ptr, a.c, b.ptr, b.c, a.pixels(), out.ptr))
+
+
+def bias_residual_add(x: Tensor, bias, residual: Tensor | None, out: Tensor):
+    """src/engine/conv.rs:170-191 prefill plus the accumulate: out = (residual + bias) + x."""
+    ctx = x.ctx
+    bias = _vec(ctx, bias)
+    out.set_shape(*x.shape)
+    check(lib().mh_bias_residual_add(ctx.h, x.ptr, x.pixels(), x.c, _ptr(bias), _ptr(residual), out.ptr))
+
+
+def to_u8(x: DeviceArray) -> np.ndarray:
+    """src/imaging/blend.rs:21-24 on the device."""
+    n = x.nbytes // 4
+    out = DeviceArray(x.ctx, (n,), np.uint8)
+    check(lib().mh_to_u8(x.ctx.h, x.ptr, n, out.ptr))
+    return out.numpy().reshape(x.shape)
+
+
+def math_eval(ctx: Context, which: str, x) -> np.ndarray:
+    """Device exp/SiLU of src/engine/math.rs on a host array."""
+    d = DeviceArray.from_numpy(ctx, np.ascontiguousarray(x, np.float32))
+    y = DeviceArray(ctx, d.shape)
+    check(lib().mh_math_eval(ctx.h, {"exp": 0, "silu": 1}[which], d.ptr, d.nbytes // 4, y.ptr))
+    return y.numpy()

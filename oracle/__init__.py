@@ -53,6 +53,7 @@ def _declare(L):
     L.orc_group_norm_affine.argtypes = [vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, vp, vp, vp, vp, vp]
     L.orc_group_norm_forward.argtypes = [vp, _i64, _i64, _i64, _i64, _i64, ctypes.c_float, vp, vp, vp,
                                          ctypes.c_int, vp]
+    L.orc_apply_affine.argtypes = [vp, _i64, _i64, vp, vp, ctypes.c_int, vp]
     L.orc_layer_norm.argtypes = [vp, _i64, _i64, vp, vp, ctypes.c_float, vp]
     L.orc_silu_inplace.argtypes = [vp, _i64]
     L.orc_add_inplace.argtypes = [vp, vp, _i64]
@@ -199,6 +200,15 @@ def group_norm(x, groups, eps, gamma, beta, add=None, silu=False):
     out = np.empty_like(x)
     lib().orc_group_norm_forward(_p(x), n, h, w, c, groups, float(eps), _p(gamma), _p(beta), _p(add), int(silu),
                                  _p(out))
+    return out
+
+
+def apply_affine(x, scale, shift, silu):
+    """src/engine/norm.rs:132-148 for one item: x [pixels, c] (any leading shape), scale/shift [c]."""
+    x, scale, shift = _f32(x), _f32(scale), _f32(shift)
+    c = x.shape[-1]
+    out = np.empty_like(x)
+    lib().orc_apply_affine(_p(x), x.size // c, c, _p(scale), _p(shift), int(silu), _p(out))
     return out
 
 

@@ -1,0 +1,293 @@
+"""GPU parity of the engine kernels, through the C ABI (libmoebius_hip.so).
+
+Each test names the reference test or function it mirrors. Bars: the
+reference's scaled error 1e-5 against its fixtures (tests/kernels.rs:28-38);
+max-abs <= 1e-4 * max|ref| against the oracle for f32 convs; bit-exact for
+gathers, layout moves, quantisation and the device exp/SiLU; and for kernels
+that restate the reference's arithmetic order (depthwise, GroupNorm apply)
+bit-exact to the oracle as well."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from moebius_cpu_amd import engine as E
+from moebius_cpu_amd import synthetic as S
+from tests.util import Lcg, assert_close, fixtures, hashed, max_abs_rel, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-4  # max-abs <= 1e-4 * max|ref| for f32 paths
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = E.Context(0)
+    yield c
+    c.synchronize()
+    c.close()
+
+
+@pytest.fixture(scope="module")
+def fx():
+    return fixtures()
+
+
+def T(ctx, a):
+    return E.Tensor.from_numpy(ctx, a)
+
+
+def conv3(ctx, x, w, b=None, stride=1, pad=(1, 1, 1, 1), up=False, prologue=None, f16=False):
+    co, ci = w.shape[0], w.shape[3]
+    conv = E.Conv3x3(ctx, ci, co, E.Param(ctx, w, f16=f16), b, stride, pad, up)
+    out = E.Tensor(ctx)
+    conv.forward_prologue(T(ctx, x), prologue, out)
+    return out.numpy()
+
+
+def conv1(ctx, x, w, b=None, r=None, f16=False):
+    co, ci = w.shape
+    conv = E.Conv1x1(ctx, ci, co, E.Param(ctx, w, f16=f16), b)
+    out = E.Tensor(ctx)
+    conv.forward(T(ctx, x), out, None if r is None else T(ctx, r))
+    return out.numpy()
+
+
+# ---- lane layout of the matrix instruction the convs are built on
+def test_mfma_f32_32x32x2_lane_layout(ctx):
+    import ctypes
+
+    rng = np.random.default_rng(0)
+    a = rng.integers(-8, 8, (32, 2)).astype(np.float32)
+    b = rng.integers(-8, 8, (2, 32)).astype(np.float32)
+    d = np.empty((32, 32), np.float32)
+    E.check(E.lib().mh_selftest_mfma_f32(ctx.h, a.ctypes.data, b.ctypes.data, d.ctypes.data))
+    assert np.array_equal(d, a @ b)
+
+
+def test_device_arch(ctx):
+    assert ctx.arch.startswith("gfx950")
+
+
+# ---- tests/kernels.rs:40-63
+def test_conv1x1_bias_and_residual(ctx, fx):
+    x, w, b, r = fx["c1.x"], fx["c1.w"], fx["c1.b"], fx["c1.r"]
+    assert_close(conv1(ctx, x, w, b), fx["c1.y"], 1e-5)
+    assert_close(conv1(ctx, x, w, b, r), fx["c1.yr"], 1e-5)
+
+
+def test_conv1x1_f16_weights_match_rounded_f32(ctx, fx):
+    x, w = fx["c1.x"], fx["c1.w"]
+    rounded = w.astype(np.float16).astype(np.float32)
+    assert_close(conv1(ctx, x, w, f16=True), conv1(ctx, x, rounded), 1e-6)
+
+
+# ---- tests/kernels.rs:65-84
+@pytest.mark.parametrize("name,stride,pad,up", [
+    ("c3.same", 1, (1, 1, 1, 1), False),
+    ("c3.s2p1", 2, (1, 1, 1, 1), False),
+    ("c3.s2vae", 2, (0, 0, 1, 1), False),
+    ("c3.up", 1, (1, 1, 1, 1), True),
+])
+def test_conv3x3_variants(ctx, fx, name, stride, pad, up):
+    out = conv3(ctx, fx["c3.x"], fx["c3.w"], fx["c3.b"], stride, pad, up)
+    assert_close(out, fx[name], 1e-5)
+    assert max_abs_rel(out, oracle.conv3x3(fx["c3.x"], fx["c3.w"], fx["c3.b"], stride, pad, up)) <= F32_TOL
+
+
+# ---- tests/kernels.rs:86-116
+def test_conv3x3_band_boundaries(ctx):
+    n, h, w, c = 1, 40, 30, 1024
+    x = hashed(n * h * w * c, 7919, 211, 211.0, 0.5).reshape(n, h, w, c)
+    wt = (((np.arange(2 * 9 * c, dtype=np.int64) * 104_729) % 97).astype(np.float32) / np.float32(970.0)
+          - np.float32(0.05)).astype(np.float32).reshape(2, 3, 3, c)
+    xp = np.zeros((h + 2, w + 2, c), np.float64)
+    xp[1:-1, 1:-1] = x[0]
+    want = np.zeros((1, h, w, 2), np.float64)
+    for ky in range(3):
+        for kx in range(3):
+            want[0] += xp[ky:ky + h, kx:kx + w] @ wt[:, ky, kx, :].astype(np.float64).T
+    assert_close(conv3(ctx, x, wt), want.astype(np.float32), 2e-5)
+
+
+# ---- tests/kernels.rs:118-128
+def test_depthwise_epilogues(ctx, fx):
+    x, w, b = fx["dw.x"], fx["dw.w"], fx["dw.b"]
+    for ep, name in (("relu", "dw.relu"), ("glu_silu", "dw.glu")):
+        out = E.Tensor(ctx)
+        E.depthwise3x3(T(ctx, x), w, b, ep, out)
+        got = out.numpy()
+        assert_close(got, fx[name], 1e-5)
+        assert np.array_equal(got, oracle.depthwise3x3(x, w, b, ep))
+
+
+# ---- tests/kernels.rs:130-141
+def test_group_norm_plain_and_fused(ctx, fx):
+    x, g, b, add = fx["gn.x"], fx["gn.gamma"], fx["gn.beta"], fx["gn.add"]
+    out = E.Tensor(ctx)
+    E.GroupNorm(ctx, 32, 1e-6, g, b).forward(T(ctx, x), None, False, out)
+    assert_close(out.numpy(), fx["gn.y"], 1e-5)
+    addd = E.DeviceArray.from_numpy(ctx, add)
+    E.GroupNorm(ctx, 32, 1e-5, g, b).forward(T(ctx, x), addd, True, out)
+    assert_close(out.numpy(), fx["gn.y_add_silu"], 1e-5)
+
+
+# ---- tests/kernels.rs:143-151
+def test_layer_norm_tokens(ctx, fx):
+    out = E.Tensor(ctx)
+    E.layer_norm(T(ctx, fx["ln.x"].reshape(3, 17, 1, 44)), fx["ln.gamma"], fx["ln.beta"], 1e-5, out)
+    assert_close(out.numpy().reshape(3, 17, 44), fx["ln.y"], 1e-5)
+
+
+# ---- tests/kernels.rs:153-170: the device conv against both CPU paths
+@pytest.mark.parametrize("n,h,w,ci,co,up", [(2, 37, 23, 24, 40, False), (1, 9, 13, 16, 8, True),
+                                            (1, 6, 5, 768, 720, False)])
+def test_conv3x3_odd_sizes_f16_weights(ctx, n, h, w, ci, co, up):
+    x = hashed(n * h * w * ci, 7919, 401, 401.0, 0.5).reshape(n, h, w, ci)
+    wt = (((np.arange(co * 9 * ci, dtype=np.int64) * 104_729) % 113).astype(np.float32) / np.float32(1130.0)
+          - np.float32(0.05)).astype(np.float32).reshape(co, 3, 3, ci)
+    b = (np.arange(co, dtype=np.float32) * np.float32(0.01)).astype(np.float32)
+    wr = wt.astype(np.float16).astype(np.float32)
+    got = conv3(ctx, x, wt, b, up=up, f16=True)
+    assert_close(got, oracle.conv3x3(x, wr, b, upsample2x=up, im2col=True), 2e-5)
+    assert_close(got, oracle.conv3x3(x, wr, b, upsample2x=up), 2e-5)
+
+
+# ---- tests/kernels.rs:172-213
+@pytest.mark.parametrize("h,w,c,ep", [(5, 7, 64, "relu"), (4, 9, 70, "none"), (3, 5, 140, "glu_silu"),
+                                      (2, 4, 64, "glu_silu"), (7, 5, 9, "relu")])
+def test_depthwise_register_blocks_and_tails(ctx, h, w, c, ep):
+    x = hashed(h * w * c, 7919, 211, 211.0, 0.5).reshape(1, h, w, c)
+    wt = hashed(9 * c, 31, 17, 17.0, 0.5).reshape(3, 3, c)
+    b = (np.arange(c, dtype=np.float32) * np.float32(0.01) - np.float32(0.2)).astype(np.float32)
+    out = E.Tensor(ctx)
+    E.depthwise3x3(T(ctx, x), wt, b, ep, out)
+    assert np.array_equal(out.numpy(), oracle.depthwise3x3(x, wt, b, ep))
+
+
+# ---- tests/kernels.rs:233-265: the fused GN prologue, padding stays zero
+@pytest.mark.parametrize("n,h,w,ci,groups,co", [(2, 7, 9, 40, 8, 24), (2, 37, 23, 768, 32, 16)])
+@pytest.mark.parametrize("up", [False, True])
+def test_conv3x3_prologue_matches_group_norm_then_conv(ctx, n, h, w, ci, groups, co, up):
+    rnd = Lcg(7 + ci)
+    x = (rnd.take(n * h * w * ci) * np.float32(3.0) + np.float32(0.7)).reshape(n, h, w, ci)
+    gamma = np.float32(1.0) + np.float32(0.5) * rnd.take(ci)
+    beta = rnd.take(ci)
+    wt = (rnd.take(co * 9 * ci) * np.float32(0.05)).reshape(co, 3, 3, ci)
+    bias = (np.arange(co, dtype=np.float32) * np.float32(0.01)).astype(np.float32)
+    gn = E.GroupNorm(ctx, groups, 1e-6, gamma, beta)
+    aff = gn.affine(T(ctx, x), None, True)
+    got = conv3(ctx, x, wt, bias, up=up, prologue=aff)
+    wr = wt.astype(np.float16).astype(np.float32)
+    got16 = conv3(ctx, x, wt, bias, up=up, prologue=aff, f16=True)
+    sc, sh = oracle.group_norm_affine(x, groups, 1e-6, gamma, beta)
+    assert np.array_equal(aff.scale.numpy(), sc) or max_abs_rel(aff.scale.numpy(), sc) < 1e-6
+    want = oracle.conv3x3(x, wt, bias, upsample2x=up, prologue=(sc, sh, True))
+    want16 = oracle.conv3x3(x, wr, bias, upsample2x=up, prologue=(sc, sh, True))
+    assert rel_l2(got, want) <= 1e-6
+    assert rel_l2(got16, want16) <= 1e-6
+
+
+# ---- src/engine/conv.rs:145-165: the implicit GEMM's gather, bit for bit
+@pytest.mark.parametrize("stride,pad,up", [(1, (1, 1, 1, 1), False), (2, (1, 1, 1, 1), False),
+                                           (2, (0, 0, 1, 1), False), (1, (1, 1, 1, 1), True)])
+def test_im2col_gather_bit_exact(ctx, fx, stride, pad, up):
+    x = fx["c3.x"]
+    got = E.im2col_gather(T(ctx, x), stride, pad, up)
+    want = np.stack([oracle.im2col_row(x, p, stride, pad, up) for p in range(got.shape[0])])
+    assert np.array_equal(got, want)
+
+
+# ---- data movement and math, bit for bit
+def test_concat_channels_bit_exact(ctx):
+    rng = np.random.default_rng(1)
+    for ca, cb in ((1280, 1280), (640, 320), (3, 5)):
+        a = rng.standard_normal((2, 5, 7, ca)).astype(np.float32)
+        b = rng.standard_normal((2, 5, 7, cb)).astype(np.float32)
+        out = E.Tensor(ctx)
+        E.concat_channels_into(T(ctx, a), T(ctx, b), out)
+        assert np.array_equal(out.numpy(), oracle.concat_channels(a, b))
+
+
+def test_to_u8_bit_exact(ctx):
+    v = np.array([0.99999, 1.2, -0.1, 0.5, 1.0, 0.0, np.nan, np.inf, -np.inf, 0.00392], np.float32)
+    rng = np.random.default_rng(2)
+    v = np.concatenate([v, rng.uniform(-0.2, 1.2, 100000).astype(np.float32)])
+    d = E.DeviceArray.from_numpy(ctx, v)
+    assert np.array_equal(E.to_u8(d), oracle.to_u8(v))
+
+
+def test_device_exp_and_silu_bit_exact(ctx):
+    xs = np.concatenate([np.arange(-100.0, 100.0, 0.0137, dtype=np.float64).astype(np.float32),
+                         np.array([0.0, -0.0, 88.0, -87.33655, 1000.0, -1000.0], np.float32)])
+    assert np.array_equal(E.math_eval(ctx, "exp", xs), np.array([oracle.exp(v) for v in xs], np.float32))
+    assert np.array_equal(E.math_eval(ctx, "silu", xs), oracle.silu(xs))
+
+
+def test_silu_and_add_inplace(ctx):
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal(100003).astype(np.float32)
+    b = rng.standard_normal(100003).astype(np.float32)
+    da, db = E.DeviceArray.from_numpy(ctx, a), E.DeviceArray.from_numpy(ctx, b)
+    E.silu_inplace(da)
+    assert np.array_equal(da.numpy(), oracle.silu(a))
+    E.add_inplace(da, db)
+    assert np.array_equal(da.numpy(), oracle.add(oracle.silu(a), b))
+
+
+# ---- closed forms on the device
+def test_group_norm_closed_form_moments(ctx):
+    rng = np.random.default_rng(4)
+    n, h, w, c, g, eps = 2, 33, 17, 320, 32, 1e-5
+    x = (rng.standard_normal((n, h, w, c)) * 2.5 + 0.3).astype(np.float32)
+    out = E.Tensor(ctx)
+    E.GroupNorm(ctx, g, eps, np.ones(c, np.float32), np.zeros(c, np.float32)).forward(T(ctx, x), None, False, out)
+    y = out.numpy().astype(np.float64).reshape(n, h * w, g, c // g)
+    xs = x.astype(np.float64).reshape(n, h * w, g, c // g)
+    var = xs.var(axis=(1, 3))
+    assert np.max(np.abs(y.mean(axis=(1, 3)))) < 1e-6
+    assert np.max(np.abs(y.var(axis=(1, 3)) - var / (var + np.float64(np.float32(eps))))) < 1e-5
+
+
+def test_group_norm_apply_bit_exact_given_affine(ctx):
+    """The apply pass restates apply_affine exactly: same scale/shift -> same bits."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((2, 16, 16, 640)).astype(np.float32)
+    sc = rng.standard_normal(2 * 640).astype(np.float32)
+    sh = rng.standard_normal(2 * 640).astype(np.float32)
+    out = E.Tensor(ctx)
+    aff = E.Affine(E.DeviceArray.from_numpy(ctx, sc), E.DeviceArray.from_numpy(ctx, sh), True)
+    E.apply_affine(T(ctx, x), aff, out)
+    want = np.stack([oracle.apply_affine(x[b], sc[b * 640:(b + 1) * 640], sh[b * 640:(b + 1) * 640], True)
+                     for b in range(2)])
+    assert np.array_equal(out.numpy(), want)
+
+
+# ---- determinism: the split-K reduction and the GN fold have fixed orders
+def test_runs_are_bitwise_deterministic(ctx):
+    x = S.normal(11, (2, 16, 16, 1280))
+    w = S.kaiming(12, (1280, 1280), 1280)
+    a = conv1(ctx, x, w)
+    b = conv1(ctx, x, w)
+    assert np.array_equal(a, b)
+    w3 = S.kaiming(13, (640, 3, 3, 640), 9 * 640)
+    x3 = S.normal(14, (1, 16, 16, 640))
+    assert np.array_equal(conv3(ctx, x3, w3), conv3(ctx, x3, w3))
+    out1, out2 = E.Tensor(ctx), E.Tensor(ctx)
+    gn = E.GroupNorm(ctx, 32, 1e-6, np.ones(128, np.float32), np.zeros(128, np.float32))
+    xg = S.normal(15, (1, 256, 256, 128))
+    gn.forward(T(ctx, xg), None, True, out1)
+    gn.forward(T(ctx, xg), None, True, out2)
+    assert np.array_equal(out1.numpy(), out2.numpy())
+
+
+# ---- shape errors carry the reference's assertion text
+def test_shape_errors(ctx):
+    conv = E.Conv1x1(ctx, 20, 36, E.Param(ctx, np.zeros((36, 20), np.float32)))
+    with pytest.raises(E.MoebiusError, match="Conv1x1 input channels"):
+        conv.forward(E.Tensor.from_numpy(ctx, np.zeros((1, 2, 2, 8), np.float32)), E.Tensor(ctx))
+    c3 = E.Conv3x3(ctx, 8, 8, E.Param(ctx, np.zeros((8, 3, 3, 8), np.float32)), stride=2)
+    aff = E.Affine(E.DeviceArray(ctx, (8,)), E.DeviceArray(ctx, (8,)), True)
+    with pytest.raises(E.MoebiusError, match="prologue needs the stride-1"):
+        c3.forward_prologue(E.Tensor.from_numpy(ctx, np.zeros((1, 4, 4, 8), np.float32)), aff, E.Tensor(ctx))

@@ -48,6 +48,27 @@ def cpu_threads():
     return int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
 
 
+def cpu_baseline(workload, extra=(), note=""):
+    """Times the CPU oracle on the same workload in a child process that never
+    touches the GPU (oracle/baseline.py); a failure there is reported, not fatal."""
+    import subprocess
+
+    cmd = [sys.executable, "-X", "faulthandler", "-m", "oracle.baseline", "--workload", workload,
+           "--threads", str(cpu_threads()), *extra]
+    log("CPU baseline: " + " ".join(cmd[1:]))
+    try:
+        r = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=600)
+    except subprocess.TimeoutExpired:
+        return {"value": None, "unit": "ms", "cores": cpu_threads(), "kind": "port", "error": "timed out"}
+    if r.returncode != 0:
+        log(r.stderr[-2000:])
+        return {"value": None, "unit": "ms", "cores": cpu_threads(), "kind": "port",
+                "error": f"baseline process exited with {r.returncode}"}
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    return {"value": res["value"], "unit": "ms", "cores": res["cores"], "kind": "port",
+            "sample": res["sample"] + note}
+
+
 def bench_conv_gn(args):
     """conv3x3 64x64x320 -> 320 + GroupNorm(32, eps 1e-5) + SiLU, f32."""
     from moebius_cpu_amd import engine as E
@@ -85,34 +106,101 @@ def bench_conv_gn(args):
         "components": {"conv_ms": round(conv_ms, 5), "conv_mfma_util": round(conv_tflops / PEAK_F32_MFMA_TFLOPS, 4),
                        "groupnorm_silu_ms": round(gn_ms, 5), "groupnorm_gbps_8B_per_elem": round(gn_gbps, 1)},
     }
-    if not args.no_cpu:
-        import oracle
-
-        oracle.set_threads(cpu_threads())
-        oracle.group_norm(oracle.conv3x3(wl.x, wl.w, wl.b), 32, wl.eps, wl.gamma, wl.beta, silu=True)
-        times = []
-        t_end = time.perf_counter() + 15.0
-        while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 50):
-            t0 = time.perf_counter()
-            oracle.group_norm(oracle.conv3x3(wl.x, wl.w, wl.b), 32, wl.eps, wl.gamma, wl.beta, silu=True)
-            times.append(time.perf_counter() - t0)
-        out["cpu_baseline"] = {"value": round(float(np.median(times)) * 1e3, 3), "unit": "ms",
-                               "cores": oracle.threads(), "kind": "port",
-                               "sample": f"full workload, median of {len(times)} runs after one warm-up "
-                                         "(C++ restatement of the CPU engine: Winograd F(2x2,3x3) + GN)"}
     ctx.close()
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline("conv3x3_gn_silu", note=" (C++ restatement of the CPU engine: "
+                                           "Winograd F(2x2,3x3) conv + GroupNorm, OpenMP)")
     return out
 
 
-WORKLOADS = {"conv3x3_gn_silu": bench_conv_gn}
+def _components(ctx, steps):
+    """Standalone per-kernel figures of the metric: the 3x3 conv's f32 MFMA
+    utilisation (64x64x320 -> 320) and GroupNorm+SiLU HBM GB/s at the VAE's
+    512x512x128 map (8 B/element: one read, one write)."""
+    from moebius_cpu_amd import engine as E
+    from moebius_cpu_amd import synthetic as S
+    from moebius_cpu_amd import workloads as W
+
+    wl = W.conv3x3_gn_silu()
+    x = E.Tensor.from_numpy(ctx, wl.x)
+    conv = E.Conv3x3.same(ctx, 320, 320, E.Param(ctx, wl.w), wl.b)
+    y = E.Tensor(ctx, 1, 64, 64, 320)
+    conv.forward(x, y)
+    conv_ms = time_region(ctx, lambda: conv.forward(x, y), steps)
+    xg = E.Tensor.from_numpy(ctx, S.normal(77, (1, 512, 512, 128)))
+    gn = E.GroupNorm(ctx, 32, 1e-6, S.normal(78, (128,), 0.1, 1.0), S.normal(79, (128,), 0.1))
+    z = E.Tensor(ctx, 1, 512, 512, 128)
+    gn.forward(xg, None, True, z)
+    gn_ms = time_region(ctx, lambda: gn.forward(xg, None, True, z), steps)
+    conv_tf = wl.flops / (conv_ms * 1e-3) / 1e12
+    gn_gbps = 8.0 * 512 * 512 * 128 / (gn_ms * 1e-3) / 1e9
+    return {"conv3x3_64x64x320_ms": round(conv_ms, 5),
+            "conv3x3_mfma_util": round(conv_tf / PEAK_F32_MFMA_TFLOPS, 4),
+            "groupnorm_silu_512x512x128_ms": round(gn_ms, 5),
+            "groupnorm_silu_gbps_8B_per_elem": round(gn_gbps, 1),
+            "groupnorm_hbm_frac": round(gn_gbps / PEAK_HBM_GBPS, 4)}
+
+
+def bench_unet(args):
+    """One full 512^2 denoise step: 64x64x9 latent stack, CFG batch 2, f32 Exact."""
+    from moebius_cpu_amd import engine as E
+    from moebius_cpu_amd import unet_params as U
+    from moebius_cpu_amd.unet import UNet
+
+    cfg = not args.cond_only
+    b = 2 if cfg else 1
+    log("generating random-init weights")
+    params = U.random_unet(seed=4000)
+    inp = U.unet_input(seed=5000)
+    ctx = E.Context(0)
+    net = UNet(ctx, params, f16_gemm=args.f16_weights)
+    x = E.DeviceArray.from_numpy(ctx, inp.x)
+    eps = E.DeviceArray(ctx, (b, 64, 64, 4))
+    step = lambda: net.forward(x, inp.timestep, cfg, eps)  # noqa: E731
+    log("warm-up")
+    for _ in range(max(args.warmup, 1)):
+        step()
+    ctx.synchronize()
+    log("timed steps")
+    ms = time_region(ctx, step, args.steps)
+    flops = U.step_flops(b)
+    achieved = flops["total"] / (ms * 1e-3) / 1e12
+    wbytes, pbytes = net.memory()
+    out = {
+        "metric": METRIC, "value": round(ms, 4), "unit": "ms", "higher_is_better": False,
+        "ms_per_step": round(ms, 4), "dtype": "f32",
+        "config": {"workload": "Moebius UNet denoise step, 512x512 image (64x64x9 latent stack), "
+                               f"{'CFG batch 2' if cfg else 'cond-only batch 1'}, "
+                               f"{'f16-stored GEMM weights, ' if args.f16_weights else ''}f32 arithmetic",
+                   "latent": [1, 64, 64, 9], "batch": b, "timestep": inp.timestep,
+                   "params_M": round(U.param_count() / 1e6, 1), "weight_bytes": wbytes, "pool_bytes": pbytes},
+        "roofline": {"bound": "mfma", "kernel": "whole step (all kernels, one stream)",
+                     "achieved": round(achieved, 2), "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_F32_MFMA_TFLOPS, 4), "traffic": None,
+                     "work_per_launch": f"{flops['total'] / 1e9:.1f} GFLOP per step",
+                     "avg_launch_ms": round(ms, 4)},
+    }
+    log("component kernels")
+    out["components"] = _components(ctx, 20)
+    del net, x, eps
+    ctx.close()
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline("unet_step", () if cfg else ("--cond-only",),
+                                           note=" (C++ restatement of the CPU engine's UNet, OpenMP)")
+    return out
+
+
+WORKLOADS = {"unet_step": bench_unet, "conv3x3_gn_silu": bench_conv_gn}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="conv3x3_gn_silu", choices=sorted(WORKLOADS))
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="unet_step", choices=sorted(WORKLOADS))
+    ap.add_argument("--cond-only", action="store_true", help="UNet: batch 1 (no CFG)")
+    ap.add_argument("--f16-weights", action="store_true", help="UNet: f16-stored GEMM weights")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:

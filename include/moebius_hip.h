@@ -58,8 +58,28 @@ extern "C" {
 #define MH_PRECISION_EXACT 0u
 #define MH_PRECISION_FAST 1u
 
+/* Conditioning rows of a UNet step (src/unet/mod.rs:46-60). */
+#define MH_GUIDANCE_CFG 0u       /* batch 2: items 0 = uncond, 1 = cond */
+#define MH_GUIDANCE_COND_ONLY 1u /* batch 1: cond */
+
 typedef struct MhContext MhContext;
 typedef struct MhEvent MhEvent;
+typedef struct MhUNet MhUNet;
+
+/* One converter tensor (tools/convert_weights.py:13-33 names and layouts) in
+ * host memory: GEMM weights F32 or F16, everything else F32. */
+typedef struct MhNamedTensor {
+    const char *name;
+    const void *data;
+    uint32_t dtype; /* MH_DTYPE_* */
+    uint32_t reserved;
+    uint64_t numel;
+} MhNamedTensor;
+
+/* Per-block trace callback (src/unet/mod.rs:148-157): `dev` is a device
+ * pointer valid during the call; the stream is idle when it is made. */
+typedef void (*MhTraceFn)(void *user, const char *name, const float *dev, uint32_t n, uint32_t h, uint32_t w,
+                          uint32_t c);
 
 /* ---- library / context (moebius_cpu.h:48-56 conventions) ---- */
 uint32_t mh_abi_version(void);
@@ -169,6 +189,60 @@ int32_t mh_to_u8(MhContext *ctx, const float *x, uint64_t len, uint8_t *out);
 /* src/engine/math.rs:17-36 on device: y = exp(x) (which=0) or SiLU(x) (which=1),
  * the reference's Cephes polynomial, for bit-exact checks of the device math. */
 int32_t mh_math_eval(MhContext *ctx, uint32_t which, const float *x, uint64_t len, float *y);
+
+/* src/unet/lambda.rs:452-489 `softmax_lambda` per item: keys [nb][rows][k]
+ * (read only), v [nb][rows][vd] -> lambda_t [nb][vd][k], the TRANSPOSE of the
+ * reference's lambda_c [k][vd]. k, vd <= 160. */
+int32_t mh_softmax_lambda(MhContext *ctx, const float *keys, const float *v, uint32_t nb, uint32_t rows, uint32_t k,
+                          uint32_t vd, float *lambda_t);
+
+/* src/unet/lambda.rs:288-314 `tap_filter` over nb items of hh x ww pixels:
+ * o [nb*hh*ww][8*vd] += A[., 225] + 15x15 taps of v [nb*hh*ww][vd]; a [nb*hh*ww][8][226]. */
+int32_t mh_tap_filter(MhContext *ctx, const float *a, const float *v, float *o, uint32_t nb, uint32_t hh,
+                      uint32_t ww, uint32_t vd);
+
+/* src/unet/lambda.rs:406-425 `position_term`: o [nb*hw][8*k] += (q . E) . V[branch]
+ * with e [hw][10][k], v_branches [2][10][k], item i using branch br0 + i. */
+int32_t mh_position_term(MhContext *ctx, const float *q, const float *e, const float *v_branches, uint32_t br0,
+                         uint32_t nb, uint32_t hw, uint32_t k, float *o);
+
+/* src/engine/gemm.rs:63-132 `matmul` for K-contiguous operands, on the device:
+ * c [m][ldc] = a [m][lda] . b[n][ldb]^T (+ bias[n]) (+ residual [m][ldc]); b F32/F16. */
+int32_t mh_gemm_nt(MhContext *ctx, const float *a, uint64_t lda, const void *b, uint32_t b_dtype, uint64_t ldb,
+                   uint32_t m, uint32_t n, uint32_t k, const float *bias, const float *residual, float *c,
+                   uint64_t ldc);
+
+/* ---- UNet (src/unet) ---- */
+
+/* src/unet/mod.rs:86-140 `UNet::load` from the converter tensors (copied to
+ * HBM; the table may be freed afterwards). Precomputes the cross-lambda
+ * constants and the folded self-lambda filter. MH_ERR_WEIGHTS names the first
+ * missing or mis-sized tensor. */
+int32_t mh_unet_create(MhContext *ctx, const MhNamedTensor *tensors, uint32_t count, MhUNet **out);
+void mh_unet_destroy(MhUNet *unet);
+
+/* src/unet/mod.rs:144-146 `UNet::forward`: x [1,64,64,9] (noisy latent | mask |
+ * masked latent) -> eps [b,64,64,4], b = 2 for MH_GUIDANCE_CFG, 1 for
+ * COND_ONLY. Device pointers; asynchronous on the context stream. */
+int32_t mh_unet_forward(MhUNet *unet, const float *x_dev, uint32_t timestep, uint32_t guidance, float *eps_dev);
+
+/* The same with host buffers (synchronous), as the reference's Tensor API. */
+int32_t mh_unet_forward_host(MhUNet *unet, const float *x_host, uint32_t timestep, uint32_t guidance,
+                             float *eps_host);
+
+/* src/unet/mod.rs:150-157 `forward_traced`: trace(name, tensor) after every block. */
+int32_t mh_unet_forward_traced(MhUNet *unet, const float *x_dev, uint32_t timestep, uint32_t guidance,
+                               float *eps_dev, MhTraceFn trace, void *user);
+
+/* HBM held by the weights and by the activation pool. */
+int32_t mh_unet_memory(MhUNet *unet, uint64_t *weight_bytes, uint64_t *pool_bytes);
+
+/* src/unet/embed.rs:21-30 `timestep_sinusoid` (host arithmetic, f32 libm). */
+void mh_timestep_sinusoid(uint32_t t, float *out /* [320] */);
+
+/* src/engine/mod.rs:104-117 `best_fit`: the pool's buffer choice among (len, cap)
+ * pairs for a request of `len` elements; -1 when count is 0. Host only. */
+int64_t mh_scratch_best_fit(const uint64_t *lens, const uint64_t *caps, uint64_t count, uint64_t len);
 
 /* Lane-layout probe of the f32 matrix instruction the convs use (no
  * counterpart in the reference): d[32][32] = a[32][2] . b[2][32] through one

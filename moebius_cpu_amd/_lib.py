@@ -79,7 +79,31 @@ SIGNATURES = {
     "mh_to_u8": (_i32, [_vp, _vp, _u64, _vp]),
     "mh_math_eval": (_i32, [_vp, _u32, _vp, _u64, _vp]),
     "mh_selftest_mfma_f32": (_i32, [_vp, _vp, _vp, _vp]),
+    "mh_softmax_lambda": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
+    "mh_tap_filter": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32]),
+    "mh_position_term": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
+    "mh_gemm_nt": (_i32, [_vp, _vp, _u64, _vp, _u32, _u64, _u32, _u32, _u32, _vp, _vp, _vp, _u64]),
+    "mh_unet_create": (_i32, [_vp, _vp, _u32, ctypes.POINTER(_vp)]),
+    "mh_unet_destroy": (None, [_vp]),
+    "mh_unet_forward": (_i32, [_vp, _vp, _u32, _u32, _vp]),
+    "mh_unet_forward_host": (_i32, [_vp, _vp, _u32, _u32, _vp]),
+    "mh_unet_forward_traced": (_i32, [_vp, _vp, _u32, _u32, _vp, _vp, _vp]),
+    "mh_unet_memory": (_i32, [_vp, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
+    "mh_timestep_sinusoid": (None, [_u32, _vp]),
+    "mh_scratch_best_fit": (ctypes.c_int64, [_vp, _vp, _u64, _u64]),
 }
+
+GUIDANCE_CFG = 0
+GUIDANCE_COND_ONLY = 1
+
+
+class NamedTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("data", ctypes.c_void_p), ("dtype", ctypes.c_uint32),
+                ("reserved", ctypes.c_uint32), ("numel", ctypes.c_uint64)]
+
+
+TRACE_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p, ctypes.c_uint32,
+                            ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32)
 
 _lib = None
 

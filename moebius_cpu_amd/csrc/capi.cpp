@@ -5,16 +5,29 @@
 // (include/moebius_cpu.h:50-51). Nothing throws across the boundary.
 #include <cstring>
 #include <exception>
+#include <memory>
 #include <new>
 #include <string>
 
 #include "../../include/moebius_hip.h"
 #include "common.hpp"
 #include "kernels.hpp"
+#include "pool.hpp"
+#include "unet.hpp"
 
 struct MhContext {
     mh::Context ctx;
     explicit MhContext(int dev) : ctx(dev) {}
+};
+
+struct MhUNet {
+    MhContext *owner;
+    std::unique_ptr<mh::UNet> net;
+    float *x_dev = nullptr, *eps_dev = nullptr;
+    ~MhUNet() {
+        if (x_dev) (void)hipFree(x_dev);
+        if (eps_dev) (void)hipFree(eps_dev);
+    }
 };
 
 struct MhEvent {
@@ -395,6 +408,159 @@ int32_t mh_math_eval(MhContext *ctx, uint32_t which, const float *x, uint64_t le
         need(y, "y");
         mh::math_eval(cc, int(which), x, int64_t(len), y);
     });
+}
+
+int32_t mh_softmax_lambda(MhContext *ctx, const float *keys, const float *v, uint32_t nb, uint32_t rows, uint32_t k,
+                          uint32_t vd, float *lambda_t) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(keys, "keys");
+        need(v, "v");
+        need(lambda_t, "lambda_t");
+        mh::softmax_lambda(c, keys, v, dim(nb, "nb"), dim(rows, "rows"), dim(k, "k"), dim(vd, "vd"), lambda_t);
+    });
+}
+
+int32_t mh_tap_filter(MhContext *ctx, const float *a, const float *v, float *o, uint32_t nb, uint32_t hh,
+                      uint32_t ww, uint32_t vd) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(a, "a");
+        need(v, "v");
+        need(o, "o");
+        mh::tap_filter(c, a, v, o, dim(nb, "nb"), dim(hh, "hh"), dim(ww, "ww"), dim(vd, "vd"));
+    });
+}
+
+int32_t mh_position_term(MhContext *ctx, const float *q, const float *e, const float *v_branches, uint32_t br0,
+                         uint32_t nb, uint32_t hw, uint32_t k, float *o) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(q, "q");
+        need(e, "e");
+        need(v_branches, "v_branches");
+        need(o, "o");
+        mh::position_term(c, q, e, v_branches, dim(br0, "br0"), dim(nb, "nb"), dim(hw, "hw"), dim(k, "k"), o);
+    });
+}
+
+int32_t mh_gemm_nt(MhContext *ctx, const float *a, uint64_t lda, const void *b, uint32_t b_dtype, uint64_t ldb,
+                   uint32_t m, uint32_t n, uint32_t k, const float *bias, const float *residual, float *c,
+                   uint64_t ldc) {
+    return guard([&] {
+        mh::Context &cc = C(ctx);
+        need(a, "a");
+        need(b, "b");
+        need(c, "c");
+        if (lda < k || ldb < k || ldc < n) mh::fail(mh::kInvalidArgument, "gemm: leading dimension too small");
+        mh::gemm_nt(cc, a, int64_t(lda), 0, b, wtype(b_dtype), int64_t(ldb), 0, dim(m, "m"), dim(n, "n"),
+                    dim(k, "k"), 1, bias, residual, c, int64_t(ldc), 0);
+    });
+}
+
+int32_t mh_unet_create(MhContext *ctx, const MhNamedTensor *tensors, uint32_t count, MhUNet **out) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(out, "out");
+        *out = nullptr;
+        need(tensors, "tensors");
+        std::vector<mh::NamedTensor> t(count);
+        for (uint32_t i = 0; i < count; ++i) {
+            t[i].name = tensors[i].name;
+            t[i].data = tensors[i].data;
+            t[i].dtype = tensors[i].dtype;
+            t[i].numel = tensors[i].numel;
+        }
+        auto u = std::make_unique<MhUNet>();
+        u->owner = ctx;
+        u->net = std::make_unique<mh::UNet>(c, t.data(), int(count));
+        *out = u.release();
+    });
+}
+
+void mh_unet_destroy(MhUNet *unet) {
+    if (!unet) return;
+    (void)hipSetDevice(unet->owner->ctx.device);
+    delete unet;
+}
+
+static mh::Context &unet_ctx(MhUNet *u) {
+    if (!u) mh::fail(mh::kInvalidArgument, "unet is NULL");
+    return C(u->owner);
+}
+
+static bool guidance_cfg(uint32_t g) {
+    if (g == MH_GUIDANCE_CFG) return true;
+    if (g == MH_GUIDANCE_COND_ONLY) return false;
+    mh::fail(mh::kInvalidArgument, "unknown guidance");
+}
+
+int32_t mh_unet_forward(MhUNet *unet, const float *x_dev, uint32_t timestep, uint32_t guidance, float *eps_dev) {
+    return guard([&] {
+        unet_ctx(unet);
+        need(x_dev, "x");
+        need(eps_dev, "eps");
+        unet->net->forward(x_dev, int(timestep), guidance_cfg(guidance), eps_dev);
+    });
+}
+
+int32_t mh_unet_forward_host(MhUNet *unet, const float *x_host, uint32_t timestep, uint32_t guidance,
+                             float *eps_host) {
+    return guard([&] {
+        mh::Context &c = unet_ctx(unet);
+        need(x_host, "x");
+        need(eps_host, "eps");
+        const bool cfg = guidance_cfg(guidance);
+        if (!unet->x_dev) HIP_CHECK(hipMalloc(&unet->x_dev, 64 * 64 * 9 * sizeof(float)));
+        if (!unet->eps_dev) HIP_CHECK(hipMalloc(&unet->eps_dev, 2 * 64 * 64 * 4 * sizeof(float)));
+        HIP_CHECK(hipMemcpyAsync(unet->x_dev, x_host, 64 * 64 * 9 * sizeof(float), hipMemcpyHostToDevice, c.stream));
+        unet->net->forward(unet->x_dev, int(timestep), cfg, unet->eps_dev);
+        HIP_CHECK(hipMemcpyAsync(eps_host, unet->eps_dev, size_t(cfg ? 2 : 1) * 64 * 64 * 4 * sizeof(float),
+                                 hipMemcpyDeviceToHost, c.stream));
+        HIP_CHECK(hipStreamSynchronize(c.stream));
+    });
+}
+
+namespace {
+struct TraceCtx {
+    MhTraceFn fn;
+    void *user;
+    hipStream_t stream;
+};
+void trace_bridge(void *user, const char *name, const float *dev, int n, int h, int w, int c) {
+    auto *t = static_cast<TraceCtx *>(user);
+    HIP_CHECK(hipStreamSynchronize(t->stream));
+    t->fn(t->user, name, dev, uint32_t(n), uint32_t(h), uint32_t(w), uint32_t(c));
+}
+}  // namespace
+
+int32_t mh_unet_forward_traced(MhUNet *unet, const float *x_dev, uint32_t timestep, uint32_t guidance,
+                               float *eps_dev, MhTraceFn trace, void *user) {
+    return guard([&] {
+        mh::Context &c = unet_ctx(unet);
+        need(x_dev, "x");
+        need(eps_dev, "eps");
+        TraceCtx tc{trace, user, c.stream};
+        unet->net->forward(x_dev, int(timestep), guidance_cfg(guidance), eps_dev, trace ? trace_bridge : nullptr,
+                           &tc);
+    });
+}
+
+int32_t mh_unet_memory(MhUNet *unet, uint64_t *weight_bytes, uint64_t *pool_bytes) {
+    return guard([&] {
+        unet_ctx(unet);
+        if (weight_bytes) *weight_bytes = unet->net->weight_bytes();
+        if (pool_bytes) *pool_bytes = unet->net->pool_bytes();
+    });
+}
+
+void mh_timestep_sinusoid(uint32_t t, float *out) {
+    if (out) mh::timestep_sinusoid(int(t), out);
+}
+
+int64_t mh_scratch_best_fit(const uint64_t *lens, const uint64_t *caps, uint64_t count, uint64_t len) {
+    if (count == 0 || !lens || !caps) return -1;
+    return mh::best_fit(lens, caps, int64_t(count), len);
 }
 
 int32_t mh_selftest_mfma_f32(MhContext *ctx, const float *a, const float *b, float *d) {

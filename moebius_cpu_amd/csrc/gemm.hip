@@ -68,6 +68,8 @@ struct GemmArgs {
     // split K
     int k_split;      // K per split (multiple of BK)
     float *partial;   // [splits][M][N] when splitting
+    // batch (grid y): element offsets of item z's A, B and output/residual
+    int64_t a_bs, b_bs, c_bs;
 };
 
 __device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
@@ -189,6 +191,13 @@ __device__ __forceinline__ floatx4 load_b(const GemmArgs &p, int n, int k) {
 template <int BM, int BN, int MODE, bool PRO, bool F16, bool BVEC, int EPI, bool SPLIT>
 __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
     constexpr int FM = BM / 64, FN = BN / 64;        // 32x32 blocks per wave
+    if (blockIdx.y) {
+        const int64_t bz = blockIdx.y;
+        p.a += bz * p.a_bs;
+        p.b = static_cast<const char *>(p.b) + bz * p.b_bs * (F16 ? 2 : 4);
+        p.out += bz * p.c_bs;
+        if (p.res) p.res += bz * p.c_bs;
+    }
     constexpr int A_LD = BM * K4 / 256, B_LD = BN * K4 / 256;
     __shared__ float As[BM * LDS_S];
     __shared__ float Bs[BN * LDS_S];
@@ -376,7 +385,7 @@ Plan plan_for(int M, int N, int K, int cus) {
 }
 
 template <int BM, int BN, int MODE, bool PRO, bool F16, bool BVEC>
-void launch_cfg(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi) {
+void launch_cfg(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int batch) {
     const unsigned tiles = unsigned(ceil_div(p.M, BM) * ceil_div(p.N, BN));
     if (pl.splits > 1) {
         const size_t bytes = size_t(pl.splits) * p.M * p.N * sizeof(float);
@@ -395,35 +404,38 @@ void launch_cfg(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi) {
                                                                 p.out);
     } else {
         p.k_split = p.K;
+        const dim3 grid(tiles, unsigned(batch));
         if (epi == GemmEpilogue::Silu)
-            gemm_f32_kernel<BM, BN, MODE, PRO, F16, BVEC, 1, false><<<tiles, 256, 0, ctx.stream>>>(p);
+            gemm_f32_kernel<BM, BN, MODE, PRO, F16, BVEC, 1, false><<<grid, 256, 0, ctx.stream>>>(p);
         else
-            gemm_f32_kernel<BM, BN, MODE, PRO, F16, BVEC, 0, false><<<tiles, 256, 0, ctx.stream>>>(p);
+            gemm_f32_kernel<BM, BN, MODE, PRO, F16, BVEC, 0, false><<<grid, 256, 0, ctx.stream>>>(p);
     }
     MH_LAUNCH_CHECK();
 }
 
 template <int MODE, bool PRO, bool F16, bool BVEC>
-void launch_tiles(Context &ctx, GemmArgs &p, GemmEpilogue epi) {
-    const Plan pl = plan_for(p.M, p.N, p.K, ctx.cu_count);
+void launch_tiles(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
+    Plan pl = plan_for(p.M, p.N, p.K, int(ceil_div(ctx.cu_count, batch)));
+    if (batch > 1) pl.splits = 1;
     if (pl.bm == 128 && pl.bn == 128)
-        launch_cfg<128, 128, MODE, PRO, F16, BVEC>(ctx, p, pl, epi);
+        launch_cfg<128, 128, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
     else if (pl.bm == 128)
-        launch_cfg<128, 64, MODE, PRO, F16, BVEC>(ctx, p, pl, epi);
+        launch_cfg<128, 64, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
     else
-        launch_cfg<64, 64, MODE, PRO, F16, BVEC>(ctx, p, pl, epi);
+        launch_cfg<64, 64, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
 }
 
 template <int MODE, bool PRO>
-void launch_b(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi) {
-    const bool bvec = p.K % 4 == 0 && p.ldb % 4 == 0 &&
-                      (reinterpret_cast<uintptr_t>(p.b) % (wt == kF16 ? 8 : 16)) == 0;
+void launch_b(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi, int batch = 1) {
+    const int esz = wt == kF16 ? 2 : 4;
+    const bool bvec = p.K % 4 == 0 && p.ldb % 4 == 0 && (reinterpret_cast<uintptr_t>(p.b) % (4 * esz)) == 0 &&
+                      (batch == 1 || p.b_bs % 4 == 0);
     if (wt == kF16) {
-        if (bvec) launch_tiles<MODE, PRO, true, true>(ctx, p, epi);
-        else launch_tiles<MODE, PRO, true, false>(ctx, p, epi);
+        if (bvec) launch_tiles<MODE, PRO, true, true>(ctx, p, epi, batch);
+        else launch_tiles<MODE, PRO, true, false>(ctx, p, epi, batch);
     } else {
-        if (bvec) launch_tiles<MODE, PRO, false, true>(ctx, p, epi);
-        else launch_tiles<MODE, PRO, false, false>(ctx, p, epi);
+        if (bvec) launch_tiles<MODE, PRO, false, true>(ctx, p, epi, batch);
+        else launch_tiles<MODE, PRO, false, false>(ctx, p, epi, batch);
     }
 }
 
@@ -478,6 +490,33 @@ void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void 
         launch_b<kDense, false>(ctx, p, wt, epi);
     else
         launch_b<kDenseScalar, false>(ctx, p, wt, epi);
+}
+
+void gemm_nt(Context &ctx, const float *a, int64_t lda, int64_t a_bs, const void *b, WeightType wt, int64_t ldb,
+             int64_t b_bs, int m, int n, int k, int batch, const float *bias, const float *residual, float *out,
+             int64_t ldc, int64_t c_bs, GemmEpilogue epi) {
+    MH_REQUIRE(m >= 0 && n > 0 && k > 0 && batch > 0, "gemm: bad shape");
+    if (m == 0) return;
+    GemmArgs p{};
+    p.a = a;
+    p.lda = lda;
+    p.M = m;
+    p.N = n;
+    p.K = k;
+    p.b = b;
+    p.ldb = ldb;
+    p.bias = bias;
+    p.res = residual;
+    p.out = out;
+    p.ldc = ldc;
+    p.a_bs = a_bs;
+    p.b_bs = b_bs;
+    p.c_bs = c_bs;
+    const bool vec = k % 4 == 0 && lda % 4 == 0 && aligned16(a) && (batch == 1 || a_bs % 4 == 0);
+    if (vec)
+        launch_b<kDense, false>(ctx, p, wt, epi, batch);
+    else
+        launch_b<kDenseScalar, false>(ctx, p, wt, epi, batch);
 }
 
 void conv3x3_output_hw(int h, int w, int stride, const int pad[4], bool upsample2x, int *ho, int *wo) {

@@ -54,8 +54,23 @@ void conv3x3(Context &ctx, const float *x, int n, int h, int w, int c_in, const 
              int c_out, const float *bias, int stride, const int pad[4], bool upsample2x, const Affine *prologue,
              float *out);
 void conv3x3_output_hw(int h, int w, int stride, const int pad[4], bool upsample2x, int *ho, int *wo);
+// C[z] = A[z] . B[z]^T (+ bias) (+ residual[z]) [SiLU] for z < batch, all K-contiguous:
+// A [m][lda], B [n][ldb], C [m][ldc]; *_bs are per-item element offsets.
+void gemm_nt(Context &ctx, const float *a, int64_t lda, int64_t a_bs, const void *b, WeightType wt, int64_t ldb,
+             int64_t b_bs, int m, int n, int k, int batch, const float *bias, const float *residual, float *out,
+             int64_t ldc, int64_t c_bs, GemmEpilogue epi = GemmEpilogue::None);
 void im2col_gather(Context &ctx, const float *x, int n, int h, int w, int c, int stride, const int pad[4],
                    bool upsample2x, int64_t first, int64_t count, float *rows);
 void selftest_mfma_f32(Context &ctx, const float *a_host, const float *b_host, float *d_host);
+
+// ---- lambda layers (lambda.hip), src/unet/lambda.rs
+// keys [nb][rows][k], v [nb][rows][vd] -> lambda_t [nb][vd][k] (transposed lambda_c).
+void softmax_lambda(Context &ctx, const float *keys, const float *v, int nb, int rows, int k, int vd,
+                    float *lambda_t);
+// o [nb*hh*ww][8*vd] += bias column + 15x15 taps of v; a [nb*hh*ww][8][226].
+void tap_filter(Context &ctx, const float *a, const float *v, float *o, int nb, int hh, int ww, int vd);
+// o [nb*hw][8*k] += (q . E) . V[branch]; e [hw][10][k]; v_branches [2][10][k].
+void position_term(Context &ctx, const float *q, const float *e, const float *v_branches, int br0, int nb, int hw,
+                   int k, float *o);
 
 }  // namespace mh

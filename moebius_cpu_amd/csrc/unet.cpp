@@ -1,0 +1,604 @@
+// Device UNet: src/unet/{mod,blocks,transformer,lambda,embed,load}.rs over the
+// gfx950 kernels. The whole denoise step stays in HBM: inputs tiled to the CFG
+// batch on the device, the skip stack held in pooled buffers, and only eps
+// leaves the device.
+#include "unet.hpp"
+
+#include <cmath>
+#include <cstring>
+
+namespace mh {
+
+namespace {
+
+constexpr int CH[3] = {320, 640, 1280};
+constexpr int LAYERS = 2;
+constexpr int HEADS = 8;
+constexpr int GROUPS = 32;
+constexpr int TIME_PROJ = 320;
+constexpr int TIME_EMBED = 1280;
+constexpr int TOKENS = 10;
+constexpr int EHS = 3072;
+constexpr int XDIM = 768;
+constexpr int TAPS = 225, TAPS_B = 226;
+constexpr float RESNET_EPS = 1e-5f;
+constexpr float TGN_EPS = 1e-6f;
+constexpr float LN_EPS = 1e-5f;
+
+uint16_t f32_to_f16_bits(float f) {
+    _Float16 h = static_cast<_Float16>(f);
+    uint16_t b;
+    std::memcpy(&b, &h, 2);
+    return b;
+}
+
+float f16_bits_to_f32(uint16_t b) {
+    _Float16 h;
+    std::memcpy(&h, &b, 2);
+    return static_cast<float>(h);
+}
+
+}  // namespace
+
+void timestep_sinusoid(int t, float *out) {
+    const int half = TIME_PROJ / 2;
+    const float log_period = -float(std::log(10000.0));
+    for (int i = 0; i < half; ++i) {
+        const float freq = std::exp(log_period * float(i) / float(half));
+        const float arg = float(t) * freq;
+        out[i] = std::cos(arg);
+        out[half + i] = std::sin(arg);
+    }
+}
+
+// ---------------------------------------------------------------- weights
+WeightStore::WeightStore(Context &ctx, const NamedTensor *t, int count) {
+    std::vector<size_t> off(static_cast<size_t>(count));
+    size_t total = 0;
+    for (int i = 0; i < count; ++i) {
+        if (!t[i].name || !t[i].data) fail(kInvalidArgument, "weight table entry with NULL name or data");
+        if (t[i].dtype != kF32 && t[i].dtype != kF16) fail(kInvalidArgument, std::string("bad dtype for ") + t[i].name);
+        off[size_t(i)] = total;
+        total += (t[i].numel * (t[i].dtype == kF16 ? 2 : 4) + 255) & ~size_t(255);
+    }
+    HIP_CHECK(hipMalloc(&block_, total ? total : 256));
+    bytes_ = total;
+    for (int i = 0; i < count; ++i) {
+        char *dst = static_cast<char *>(block_) + off[size_t(i)];
+        const size_t nb = t[i].numel * (t[i].dtype == kF16 ? 2 : 4);
+        HIP_CHECK(hipMemcpyAsync(dst, t[i].data, nb, hipMemcpyHostToDevice, ctx.stream));
+        Entry e;
+        e.d.p = dst;
+        e.d.wt = t[i].dtype == kF16 ? kF16 : kF32;
+        e.d.numel = int64_t(t[i].numel);
+        e.host = t[i].data;
+        e.host_dtype = t[i].dtype;
+        if (!m_.emplace(t[i].name, e).second) fail(kInvalidArgument, std::string("duplicate tensor ") + t[i].name);
+    }
+    HIP_CHECK(hipStreamSynchronize(ctx.stream));
+}
+
+WeightStore::~WeightStore() {
+    if (block_) (void)hipFree(block_);
+}
+
+DParam WeightStore::get(const std::string &name, int64_t numel, bool gemm) const {
+    auto it = m_.find(name);
+    if (it == m_.end()) fail(kWeights, "missing tensor " + name);
+    const DParam &d = it->second.d;
+    if (d.numel != numel)
+        fail(kWeights, "tensor " + name + " has " + std::to_string(d.numel) + " values, expected " +
+                           std::to_string(numel));
+    if (!gemm && d.wt != kF32) fail(kWeights, "tensor " + name + " must be stored f32");
+    return d;
+}
+
+const float *WeightStore::host_f32(const std::string &name, int64_t numel, std::vector<float> &scratch) const {
+    auto it = m_.find(name);
+    if (it == m_.end()) fail(kWeights, "missing tensor " + name);
+    if (it->second.d.numel != numel) fail(kWeights, "tensor " + name + " has the wrong size");
+    if (it->second.host_dtype == kF32) return static_cast<const float *>(it->second.host);
+    scratch.resize(size_t(numel));
+    const uint16_t *h = static_cast<const uint16_t *>(it->second.host);
+    for (int64_t i = 0; i < numel; ++i) scratch[size_t(i)] = f16_bits_to_f32(h[i]);
+    return scratch.data();
+}
+
+// ---------------------------------------------------------------- layers
+namespace {
+
+struct Env {
+    Context &ctx;
+    Pool &pool;
+};
+
+struct Lin {  // Conv1x1 (src/engine/conv.rs:28-55)
+    int ci = 0, co = 0;
+    DParam w;
+    const float *b = nullptr;
+    void load(const WeightStore &W, const std::string &p, int ci_, int co_, bool bias) {
+        ci = ci_, co = co_;
+        w = W.get(p + ".weight", int64_t(ci) * co, true);
+        b = bias ? W.get(p + ".bias", co, false).f() : nullptr;
+    }
+    void fwd(Env &e, const float *x, int64_t px, float *out, const float *res = nullptr,
+             GemmEpilogue epi = GemmEpilogue::None) const {
+        conv1x1(e.ctx, x, px, ci, w.p, w.wt, co, b, res, out, epi);
+    }
+    DT fwd(Env &e, const DT &x, const DT *res = nullptr, GemmEpilogue epi = GemmEpilogue::None) const {
+        DT out = e.pool.tensor(x.n, x.h, x.w, co);
+        fwd(e, x.p, x.px(), out.p, res ? res->p : nullptr, epi);
+        return out;
+    }
+};
+
+struct GN {
+    int c = 0;
+    float eps = 0;
+    const float *g = nullptr, *b = nullptr;
+    void load(const WeightStore &W, const std::string &p, int c_, float eps_) {
+        c = c_, eps = eps_;
+        g = W.get(p + ".weight", c, false).f();
+        b = W.get(p + ".bias", c, false).f();
+    }
+    DT fwd(Env &e, const DT &x, const float *add, bool silu) const {
+        DT out = e.pool.tensor(x.n, x.h, x.w, x.c);
+        group_norm_forward(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, eps, g, b, add, silu, out.p);
+        return out;
+    }
+};
+
+struct LNp {
+    int c = 0;
+    const float *g = nullptr, *b = nullptr;
+    void load(const WeightStore &W, const std::string &p, int c_) {
+        c = c_;
+        g = W.get(p + ".weight", c, false).f();
+        b = W.get(p + ".bias", c, false).f();
+    }
+    DT fwd(Env &e, const DT &x) const {
+        DT out = e.pool.tensor(x.n, x.h, x.w, x.c);
+        layer_norm(e.ctx, x.p, x.px(), c, g, b, LN_EPS, out.p);
+        return out;
+    }
+};
+
+// src/unet/blocks.rs:31-54: pw1x1(relu(dw3x3(x) + b1)) + b2 (+ x when c_in == c_out)
+struct DwConv2d {
+    int ci = 0, co = 0;
+    const float *dw = nullptr, *dwb = nullptr;
+    Lin pw;
+    void load(const WeightStore &W, const std::string &p, int ci_, int co_) {
+        ci = ci_, co = co_;
+        dw = W.get(p + ".conv_dw.weight", int64_t(9) * ci, false).f();
+        dwb = W.get(p + ".conv_dw.bias", ci, false).f();
+        pw.load(W, p + ".conv_pw", ci, co, true);
+    }
+    DT fwd(Env &e, const DT &x) const {
+        DT mid = e.pool.tensor(x.n, x.h, x.w, x.c);
+        depthwise3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, dw, dwb, 1, mid.p);
+        DT out = pw.fwd(e, mid, ci == co ? &x : nullptr);
+        e.pool.recycle(mid);
+        return out;
+    }
+};
+
+// src/unet/blocks.rs:56-113
+struct DwResnet {
+    int ci = 0, co = 0;
+    GN norm1, norm2;
+    DwConv2d conv1, conv2;
+    Lin temb_proj, shortcut;
+    bool has_shortcut = false;
+    void load(const WeightStore &W, const std::string &p, int ci_, int co_) {
+        ci = ci_, co = co_;
+        norm1.load(W, p + ".norm1", ci, RESNET_EPS);
+        conv1.load(W, p + ".conv1", ci, co);
+        temb_proj.load(W, p + ".time_emb_proj", TIME_EMBED, co, true);
+        norm2.load(W, p + ".norm2", co, RESNET_EPS);
+        conv2.load(W, p + ".conv2", co, co);
+        has_shortcut = ci != co;
+        if (has_shortcut) shortcut.load(W, p + ".conv_shortcut", ci, co, true);
+    }
+    // temb_silu: [n, 1280] = SiLU(temb), shared by every resnet of the step.
+    DT fwd(Env &e, const DT &x, const float *temb_silu) const {
+        DT a = norm1.fwd(e, x, nullptr, true);
+        DT b = conv1.fwd(e, a);
+        e.pool.recycle(a);
+        float *tp = e.pool.floats(int64_t(x.n) * co);
+        temb_proj.fwd(e, temb_silu, x.n, tp);
+        a = norm2.fwd(e, b, tp, true);
+        e.pool.recycle(tp);
+        e.pool.recycle(b);
+        DT out = conv2.fwd(e, a);
+        e.pool.recycle(a);
+        if (has_shortcut) {
+            DT s = shortcut.fwd(e, x);
+            add_inplace(e.ctx, out.p, s.p, out.numel());
+            e.pool.recycle(s);
+        } else {
+            add_inplace(e.ctx, out.p, x.p, out.numel());
+        }
+        return out;
+    }
+};
+
+// src/unet/lambda.rs:203-282
+struct SelfLambda {
+    int c = 0, k = 0;
+    Lin to_q, to_k, to_v;
+    float *w_aug_t = nullptr;  // [226][k]: column d of the folded filter per row
+    void load(Env &e, const WeightStore &W, const std::string &p, int c_) {
+        c = c_, k = c / HEADS;
+        std::vector<float> s1, s2;
+        const float *w = W.host_f32(p + ".pos_conv.weight", int64_t(k) * TAPS, s1);
+        const float *b = W.host_f32(p + ".pos_conv.bias", k, s2);
+        std::vector<float> t(size_t(TAPS_B) * k);
+        for (int kk = 0; kk < k; ++kk) {
+            for (int d = 0; d < TAPS; ++d) t[size_t(d) * k + kk] = w[kk * TAPS + d];
+            t[size_t(TAPS) * k + kk] = b[kk];
+        }
+        HIP_CHECK(hipMalloc(&w_aug_t, t.size() * sizeof(float)));
+        HIP_CHECK(hipMemcpy(w_aug_t, t.data(), t.size() * sizeof(float), hipMemcpyHostToDevice));
+        to_q.load(W, p + ".to_q", c, c, true);
+        to_k.load(W, p + ".to_k", c, k, false);
+        to_v.load(W, p + ".to_v", c, k, true);
+        (void)e;
+    }
+    void release() {
+        if (w_aug_t) (void)hipFree(w_aug_t);
+        w_aug_t = nullptr;
+    }
+    DT fwd(Env &e, const DT &x) const {
+        const int hw = x.h * x.w;
+        DT q = to_q.fwd(e, x);
+        DT kt = to_k.fwd(e, x);
+        DT vt = to_v.fwd(e, x);
+        float *lam_t = e.pool.floats(int64_t(x.n) * k * k);
+        softmax_lambda(e.ctx, kt.p, vt.p, x.n, hw, k, k, lam_t);
+        e.pool.recycle(kt);
+        DT out = e.pool.tensor(x.n, x.h, x.w, c);
+        // Yc = Q . lambda_c per item, Q viewed as [(hw*8) x k].
+        gemm_nt(e.ctx, q.p, k, int64_t(hw) * c, lam_t, kF32, k, int64_t(k) * k, hw * HEADS, k, k, x.n, nullptr,
+                nullptr, out.p, k, int64_t(hw) * c);
+        e.pool.recycle(lam_t);
+        // A = Q . W_aug over every pixel and head of the batch, then the tap filter.
+        float *a = e.pool.floats(x.px() * HEADS * TAPS_B);
+        gemm_nt(e.ctx, q.p, k, 0, w_aug_t, kF32, k, 0, int(x.px() * HEADS), TAPS_B, k, 1, nullptr, nullptr, a,
+                TAPS_B, 0);
+        tap_filter(e.ctx, a, vt.p, out.p, x.n, x.h, x.w, k);
+        e.pool.recycle(a);
+        e.pool.recycle(q);
+        e.pool.recycle(vt);
+        return out;
+    }
+};
+
+// src/unet/lambda.rs:317-425
+struct CrossLambda {
+    int c = 0, k = 0, n = 0;
+    Lin to_q;
+    const float *e = nullptr;       // rel_pos_emb [n][10][k]
+    float *lambda_t = nullptr;      // [2][k][k] transposed lambda_c per branch
+    float *v = nullptr;             // [2][10][k]
+    void load(Env &env, const WeightStore &W, const std::string &p, int c_, const float *ehs_dev /*[2][10][768]*/) {
+        c = c_, k = c / HEADS;
+        const int side = 64 * 320 / c;
+        n = side * side;
+        const DParam wk = W.get(p + ".to_k.weight", int64_t(k) * XDIM, true);
+        const DParam wv = W.get(p + ".to_v.weight", int64_t(k) * XDIM, true);
+        const float *bv = W.get(p + ".to_v.bias", k, false).f();
+        HIP_CHECK(hipMalloc(&lambda_t, size_t(2) * k * k * sizeof(float)));
+        HIP_CHECK(hipMalloc(&v, size_t(2) * TOKENS * k * sizeof(float)));
+        float *keys = env.pool.floats(int64_t(2) * TOKENS * k);
+        for (int br = 0; br < 2; ++br) {
+            const float *x = ehs_dev + int64_t(br) * TOKENS * XDIM;
+            gemm_nt(env.ctx, x, XDIM, 0, wk.p, wk.wt, XDIM, 0, TOKENS, k, XDIM, 1, nullptr, nullptr,
+                    keys + int64_t(br) * TOKENS * k, k, 0);
+            // v = ehs . Wv^T, then + bias (src/unet/lambda.rs:362-365)
+            gemm_nt(env.ctx, x, XDIM, 0, wv.p, wv.wt, XDIM, 0, TOKENS, k, XDIM, 1, nullptr, nullptr,
+                    v + int64_t(br) * TOKENS * k, k, 0);
+            bias_residual_add(env.ctx, v + int64_t(br) * TOKENS * k, TOKENS, k, bv, nullptr,
+                              v + int64_t(br) * TOKENS * k);
+        }
+        softmax_lambda(env.ctx, keys, v, 2, TOKENS, k, k, lambda_t);
+        env.pool.recycle(keys);
+        to_q.load(W, p + ".to_q", c, c, true);
+        e = W.get(p + ".rel_pos_emb", int64_t(n) * TOKENS * k, false).f();
+    }
+    void release() {
+        if (lambda_t) (void)hipFree(lambda_t);
+        if (v) (void)hipFree(v);
+        lambda_t = v = nullptr;
+    }
+    DT fwd(Env &env, const DT &x, int br0) const {
+        const int hw = x.h * x.w;
+        if (hw != n) fail(kInvalidArgument, "CrossLambda input size does not match the position table");
+        DT q = to_q.fwd(env, x);
+        DT out = env.pool.tensor(x.n, x.h, x.w, c);
+        gemm_nt(env.ctx, q.p, k, int64_t(hw) * c, lambda_t + int64_t(br0) * k * k, kF32, k, int64_t(k) * k,
+                hw * HEADS, k, k, x.n, nullptr, nullptr, out.p, k, int64_t(hw) * c);
+        position_term(env.ctx, q.p, e, v, br0, x.n, hw, k, out.p);
+        env.pool.recycle(q);
+        return out;
+    }
+};
+
+// src/unet/transformer.rs:49-130
+struct MixTransformer {
+    int c = 0, hidden = 0;
+    GN norm;
+    Lin proj_in, proj_out, inverted, point;
+    LNp ln1, ln2, ln3;
+    SelfLambda attn1;
+    CrossLambda attn2;
+    const float *dw = nullptr, *dwb = nullptr;
+    void load(Env &env, const WeightStore &W, const std::string &p, int c_, const float *ehs_dev) {
+        c = c_;
+        hidden = int(float(c) * 2.5f);
+        const std::string b = p + ".transformer_blocks.0";
+        const std::string ff = b + ".ff";
+        dw = W.get(ff + ".depth_conv.conv.weight", int64_t(9) * 2 * hidden, false).f();
+        dwb = W.get(ff + ".depth_conv.conv.bias", 2 * hidden, false).f();
+        norm.load(W, p + ".norm", c, TGN_EPS);
+        proj_in.load(W, p + ".proj_in", c, c, true);
+        ln1.load(W, b + ".norm1", c);
+        attn1.load(env, W, b + ".attn1", c);
+        ln2.load(W, b + ".norm2", c);
+        attn2.load(env, W, b + ".attn2", c, ehs_dev);
+        ln3.load(W, b + ".norm3", c);
+        inverted.load(W, ff + ".inverted_conv.conv", c, 2 * hidden, true);
+        point.load(W, ff + ".point_conv.conv", hidden, c, false);
+        proj_out.load(W, p + ".proj_out", c, c, true);
+    }
+    void release() {
+        attn1.release();
+        attn2.release();
+    }
+    DT fwd(Env &e, const DT &x, int br0) const {
+        DT t = norm.fwd(e, x, nullptr, false);
+        DT h = proj_in.fwd(e, t);
+        e.pool.recycle(t);
+        t = ln1.fwd(e, h);
+        DT u = attn1.fwd(e, t);
+        e.pool.recycle(t);
+        add_inplace(e.ctx, h.p, u.p, h.numel());
+        e.pool.recycle(u);
+        t = ln2.fwd(e, h);
+        u = attn2.fwd(e, t, br0);
+        e.pool.recycle(t);
+        add_inplace(e.ctx, h.p, u.p, h.numel());
+        e.pool.recycle(u);
+        t = ln3.fwd(e, h);
+        // MixFFN (transformer.rs:121-129): SiLU(inverted(t)) -> GLU depthwise -> point + h
+        DT a = inverted.fwd(e, t, nullptr, GemmEpilogue::Silu);
+        e.pool.recycle(t);
+        DT g = e.pool.tensor(a.n, a.h, a.w, hidden);
+        depthwise3x3(e.ctx, a.p, a.n, a.h, a.w, a.c, dw, dwb, 2, g.p);
+        e.pool.recycle(a);
+        u = point.fwd(e, g, &h);
+        e.pool.recycle(g);
+        e.pool.recycle(h);
+        DT out = proj_out.fwd(e, u, &x);
+        e.pool.recycle(u);
+        return out;
+    }
+};
+
+struct Conv3 {  // Downsample / Upsample (src/unet/blocks.rs:116-145)
+    int c = 0, stride = 1;
+    bool up = false;
+    DParam w;
+    const float *b = nullptr;
+    void load(const WeightStore &W, const std::string &p, int c_, int stride_, bool up_) {
+        c = c_, stride = stride_, up = up_;
+        w = W.get(p + ".conv.weight", int64_t(9) * c * c, true);
+        b = W.get(p + ".conv.bias", c, false).f();
+    }
+    DT fwd(Env &e, const DT &x) const {
+        const int pad[4] = {1, 1, 1, 1};
+        int ho, wo;
+        conv3x3_output_hw(x.h, x.w, stride, pad, up, &ho, &wo);
+        DT out = e.pool.tensor(x.n, ho, wo, c);
+        conv3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, w.p, w.wt, c, b, stride, pad, up, nullptr, out.p);
+        return out;
+    }
+};
+
+}  // namespace
+
+// ---------------------------------------------------------------- model
+class UNetDevice {
+  public:
+    UNetDevice(Context &ctx, const NamedTensor *t, int count) : ctx_(ctx), pool_(ctx), W_(ctx, t, count) {
+        Env env{ctx_, pool_};
+        // embed::conditioning (src/unet/embed.rs:72-83): [uncond = rows 10..20, cond = rows 0..10]
+        const DParam table = W_.get("embedding_layer.weight", int64_t(20) * EHS, false);
+        Lin proj;
+        proj.load(W_, "diff_model.encoder_hid_proj", EHS, XDIM, true);
+        float *ehs = pool_.floats(int64_t(2) * TOKENS * XDIM);
+        proj.fwd(env, table.f() + int64_t(TOKENS) * EHS, TOKENS, ehs);
+        proj.fwd(env, table.f(), TOKENS, ehs + TOKENS * XDIM);
+
+        const std::string d = "diff_model";
+        int c_prev = CH[0];
+        for (int i = 0; i < 3; ++i) {
+            Block blk;
+            const std::string l = d + ".down_blocks." + std::to_string(i);
+            for (int j = 0; j < LAYERS; ++j) {
+                blk.res.emplace_back();
+                blk.res.back().load(W_, l + ".resnets." + std::to_string(j), j == 0 ? c_prev : CH[i], CH[i]);
+                blk.attn.emplace_back();
+                blk.attn.back().load(env, W_, l + ".attentions." + std::to_string(j), CH[i], ehs);
+            }
+            if (i + 1 < 3) {
+                blk.has_sample = true;
+                blk.sample.load(W_, l + ".downsamplers.0", CH[i], 2, false);
+            }
+            down_.push_back(std::move(blk));
+            c_prev = CH[i];
+        }
+        std::vector<int> skips = {CH[0]};
+        for (int i = 0; i < 3; ++i) {
+            skips.push_back(CH[i]);
+            skips.push_back(CH[i]);
+            if (i + 1 < 3) skips.push_back(CH[i]);
+        }
+        int h_c = CH[2];
+        for (int i = 0; i < 3; ++i) {
+            const int c = CH[2 - i];
+            Block blk;
+            const std::string l = d + ".up_blocks." + std::to_string(i);
+            for (int j = 0; j <= LAYERS; ++j) {
+                const int skip_c = skips.back();
+                skips.pop_back();
+                blk.res.emplace_back();
+                blk.res.back().load(W_, l + ".resnets." + std::to_string(j), h_c + skip_c, c);
+                blk.attn.emplace_back();
+                blk.attn.back().load(env, W_, l + ".attentions." + std::to_string(j), c, ehs);
+                h_c = c;
+            }
+            if (i + 1 < 3) {
+                blk.has_sample = true;
+                blk.sample.load(W_, l + ".upsamplers.0", c, 1, true);
+            }
+            up_.push_back(std::move(blk));
+        }
+        lin1_.load(W_, d + ".time_embedding.linear_1", TIME_PROJ, TIME_EMBED, true);
+        lin2_.load(W_, d + ".time_embedding.linear_2", TIME_EMBED, TIME_EMBED, true);
+        conv_in_.load(W_, d + ".conv_in", 9, CH[0]);
+        norm_out_.load(W_, d + ".conv_norm_out", CH[0], RESNET_EPS);
+        conv_out_.load(W_, d + ".conv_out", CH[0], 4);
+        HIP_CHECK(hipStreamSynchronize(ctx_.stream));
+        pool_.recycle(ehs);
+        HIP_CHECK(hipMalloc(&sinus_dev_, TIME_PROJ * sizeof(float)));
+    }
+
+    ~UNetDevice() {
+        (void)hipStreamSynchronize(ctx_.stream);
+        for (auto *v : {&down_, &up_})
+            for (auto &b : *v)
+                for (auto &a : b.attn) a.release();
+        if (sinus_dev_) (void)hipFree(sinus_dev_);
+    }
+
+    // src/unet/mod.rs:150-243
+    void forward(const float *x_dev, int timestep, bool cfg, float *eps_dev, TraceFn trace, void *user) {
+        Env e{ctx_, pool_};
+        const int b = cfg ? 2 : 1;
+        const int br0 = cfg ? 0 : 1;  // branch of item 0: uncond with CFG, cond otherwise
+        auto tr = [&](const std::string &name, const DT &t) {
+            if (trace) trace(user, name.c_str(), t.p, t.n, t.h, t.w, t.c);
+        };
+        // time embedding (src/unet/embed.rs:48-66), computed once and tiled to the batch
+        float sinus[TIME_PROJ];
+        timestep_sinusoid(timestep, sinus);
+        HIP_CHECK(hipMemcpyAsync(sinus_dev_, sinus, sizeof(sinus), hipMemcpyHostToDevice, ctx_.stream));
+        HIP_CHECK(hipStreamSynchronize(ctx_.stream));  // the host array goes out of scope
+        float *a1 = pool_.floats(TIME_EMBED);
+        lin1_.fwd(e, sinus_dev_, 1, a1);
+        silu_inplace(ctx_, a1, TIME_EMBED);
+        DT temb = pool_.tensor(b, 1, 1, TIME_EMBED);
+        lin2_.fwd(e, a1, 1, temb.p);
+        pool_.recycle(a1);
+        for (int i = 1; i < b; ++i)
+            HIP_CHECK(hipMemcpyAsync(temb.p + int64_t(i) * TIME_EMBED, temb.p, TIME_EMBED * sizeof(float),
+                                     hipMemcpyDeviceToDevice, ctx_.stream));
+        tr("unet.temb", temb);
+        float *temb_silu = pool_.floats(int64_t(b) * TIME_EMBED);
+        HIP_CHECK(hipMemcpyAsync(temb_silu, temb.p, size_t(b) * TIME_EMBED * sizeof(float), hipMemcpyDeviceToDevice,
+                                 ctx_.stream));
+        silu_inplace(ctx_, temb_silu, int64_t(b) * TIME_EMBED);
+
+        DT input = pool_.tensor(b, 64, 64, 9);
+        for (int i = 0; i < b; ++i)
+            HIP_CHECK(hipMemcpyAsync(input.p + int64_t(i) * 64 * 64 * 9, x_dev, 64 * 64 * 9 * sizeof(float),
+                                     hipMemcpyDeviceToDevice, ctx_.stream));
+        std::vector<DT> skips;
+        skips.push_back(conv_in_.fwd(e, input));
+        pool_.recycle(input);
+        tr("unet.conv_in", skips.back());
+        for (size_t i = 0; i < down_.size(); ++i) {
+            for (size_t j = 0; j < down_[i].res.size(); ++j) {
+                DT a = down_[i].res[j].fwd(e, skips.back(), temb_silu);
+                tr("unet.down." + std::to_string(i) + ".res." + std::to_string(j), a);
+                DT h = down_[i].attn[j].fwd(e, a, br0);
+                pool_.recycle(a);
+                tr("unet.down." + std::to_string(i) + ".attn." + std::to_string(j), h);
+                skips.push_back(h);
+            }
+            if (down_[i].has_sample) skips.push_back(down_[i].sample.fwd(e, skips.back()));
+            tr("unet.down." + std::to_string(i) + ".out", skips.back());
+        }
+        // The last down output is both the hidden state and the first skip.
+        DT h = pool_.tensor(skips.back().n, skips.back().h, skips.back().w, skips.back().c);
+        HIP_CHECK(hipMemcpyAsync(h.p, skips.back().p, size_t(h.numel()) * sizeof(float), hipMemcpyDeviceToDevice,
+                                 ctx_.stream));
+        for (size_t i = 0; i < up_.size(); ++i) {
+            for (size_t j = 0; j < up_[i].res.size(); ++j) {
+                DT skip = skips.back();
+                skips.pop_back();
+                DT cat = pool_.tensor(h.n, h.h, h.w, h.c + skip.c);
+                concat_channels(ctx_, h.p, h.c, skip.p, skip.c, h.px(), cat.p);
+                pool_.recycle(skip);
+                pool_.recycle(h);
+                DT a = up_[i].res[j].fwd(e, cat, temb_silu);
+                pool_.recycle(cat);
+                tr("unet.up." + std::to_string(i) + ".res." + std::to_string(j), a);
+                h = up_[i].attn[j].fwd(e, a, br0);
+                pool_.recycle(a);
+                tr("unet.up." + std::to_string(i) + ".attn." + std::to_string(j), h);
+            }
+            if (up_[i].has_sample) {
+                DT a = up_[i].sample.fwd(e, h);
+                pool_.recycle(h);
+                h = a;
+            }
+            tr("unet.up." + std::to_string(i) + ".out", h);
+        }
+        if (!skips.empty()) fail(kInternal, "skip stack not consumed");
+        DT a = norm_out_.fwd(e, h, nullptr, true);
+        pool_.recycle(h);
+        // conv_out writes eps straight into the caller's buffer.
+        DT mid = pool_.tensor(a.n, a.h, a.w, a.c);
+        depthwise3x3(ctx_, a.p, a.n, a.h, a.w, a.c, conv_out_.dw, conv_out_.dwb, 1, mid.p);
+        conv_out_.pw.fwd(e, mid.p, mid.px(), eps_dev);
+        pool_.recycle(mid);
+        pool_.recycle(a);
+        pool_.recycle(temb);
+        pool_.recycle(temb_silu);
+        if (trace) {
+            DT o{eps_dev, b, 64, 64, 4};
+            tr("unet.out", o);
+        }
+    }
+
+    size_t weight_bytes() const { return W_.bytes(); }
+    size_t pool_bytes() const { return pool_.bytes_held(); }
+
+  private:
+    struct Block {
+        std::vector<DwResnet> res;
+        std::vector<MixTransformer> attn;
+        bool has_sample = false;
+        Conv3 sample;
+    };
+    Context &ctx_;
+    Pool pool_;
+    WeightStore W_;
+    std::vector<Block> down_, up_;
+    Lin lin1_, lin2_;
+    DwConv2d conv_in_, conv_out_;
+    GN norm_out_;
+    float *sinus_dev_ = nullptr;
+};
+
+UNet::UNet(Context &ctx, const NamedTensor *t, int count) : d_(new UNetDevice(ctx, t, count)) {}
+UNet::~UNet() = default;
+void UNet::forward(const float *x_dev, int timestep, bool cfg, float *eps_dev, TraceFn trace, void *user) {
+    d_->forward(x_dev, timestep, cfg, eps_dev, trace, user);
+}
+size_t UNet::weight_bytes() const { return d_->weight_bytes(); }
+size_t UNet::pool_bytes() const { return d_->pool_bytes(); }
+
+}  // namespace mh

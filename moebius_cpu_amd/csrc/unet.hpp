@@ -1,0 +1,78 @@
+// The Moebius UNet on the device (src/unet): weights resident in HBM, every
+// activation of a denoise step in the pool, kernels queued on the context
+// stream. Host C++ mirror of src/unet/{mod,blocks,transformer,lambda,embed}.rs.
+#pragma once
+
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+#include "kernels.hpp"
+#include "pool.hpp"
+
+namespace mh {
+
+// One converter tensor handed in by the host (tools/convert_weights.py layouts).
+struct NamedTensor {
+    const char *name;
+    const void *data;  // host memory
+    uint32_t dtype;    // kF32 / kF16
+    uint64_t numel;
+};
+
+// Device copy of a tensor in its stored precision (src/engine/param.rs:14-17).
+struct DParam {
+    const void *p = nullptr;
+    WeightType wt = kF32;
+    int64_t numel = 0;
+    const float *f() const { return static_cast<const float *>(p); }
+};
+
+// Uploads tensors into one HBM block; GEMM weights keep their dtype, every
+// other tensor is stored f32.
+class WeightStore {
+  public:
+    WeightStore(Context &ctx, const NamedTensor *t, int count);
+    ~WeightStore();
+    WeightStore(const WeightStore &) = delete;
+    WeightStore &operator=(const WeightStore &) = delete;
+    // Shape-checked lookup (by element count); gemm: may be f16.
+    DParam get(const std::string &name, int64_t numel, bool gemm) const;
+    const float *host_f32(const std::string &name, int64_t numel, std::vector<float> &scratch) const;
+    size_t bytes() const { return bytes_; }
+
+  private:
+    struct Entry {
+        DParam d;
+        const void *host;
+        uint32_t host_dtype;
+    };
+    std::map<std::string, Entry> m_;
+    void *block_ = nullptr;
+    size_t bytes_ = 0;
+};
+
+using TraceFn = void (*)(void *user, const char *name, const float *dev, int n, int h, int w, int c);
+
+class UNetDevice;
+
+class UNet {
+  public:
+    UNet(Context &ctx, const NamedTensor *t, int count);
+    ~UNet();
+    // x_dev [1,64,64,9] -> eps_dev [b,64,64,4]; b = 2 with CFG (branches uncond, cond), else 1.
+    void forward(const float *x_dev, int timestep, bool cfg, float *eps_dev, TraceFn trace = nullptr,
+                 void *user = nullptr);
+    size_t weight_bytes() const;
+    size_t pool_bytes() const;
+
+  private:
+    std::unique_ptr<UNetDevice> d_;
+};
+
+// src/unet/embed.rs:21-30 (host, libm), shared with the C ABI tests.
+void timestep_sinusoid(int t, float *out /* [320] */);
+
+}  // namespace mh

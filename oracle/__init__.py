@@ -262,3 +262,147 @@ def to_u8(x):
     out = np.empty(x.shape, np.uint8)
     lib().orc_to_u8(_p(x), x.size, _p(out))
     return out
+
+
+# ---- UNet chain (oracle/unet.cpp)
+class _Named(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("data", ctypes.c_void_p), ("numel", ctypes.c_int64)]
+
+
+_TRACE_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float), ctypes.c_int64,
+                             ctypes.c_int64, ctypes.c_int64, ctypes.c_int64)
+
+
+def _declare_unet(L):
+    vp = ctypes.c_void_p
+    L.orc_timestep_sinusoid.argtypes = [ctypes.c_int, vp]
+    L.orc_unet_create.restype = vp
+    L.orc_unet_create.argtypes = [ctypes.POINTER(_Named), ctypes.c_int, ctypes.c_char_p, ctypes.c_int]
+    L.orc_unet_destroy.argtypes = [vp]
+    L.orc_unet_forward.restype = ctypes.c_int
+    L.orc_unet_forward.argtypes = [vp, vp, ctypes.c_int, ctypes.c_int, vp, _TRACE_FN, vp]
+    L.orc_softmax_lambda.argtypes = [vp, vp, _i64, _i64, _i64, vp]
+    L.orc_tap_filter.argtypes = [vp, vp, vp, _i64, _i64, _i64, _i64, _i64]
+    L.orc_dot8.restype = ctypes.c_float
+    L.orc_dot8.argtypes = [vp, vp, _i64]
+    L.orc_position_term.argtypes = [vp, vp, vp, vp, _i64, _i64]
+    L.orc_block_forward.restype = ctypes.c_int
+    L.orc_block_forward.argtypes = [ctypes.c_int, ctypes.POINTER(_Named), ctypes.c_int, ctypes.c_char_p, vp, _i64,
+                                    _i64, _i64, _i64, _i64, vp, vp, vp, ctypes.c_char_p, ctypes.c_int]
+
+
+def timestep_sinusoid(t: int) -> np.ndarray:
+    """src/unet/embed.rs:21-30"""
+    L = lib()
+    _declare_unet(L)
+    out = np.empty(320, np.float32)
+    L.orc_timestep_sinusoid(int(t), _p(out))
+    return out
+
+
+def softmax_lambda(keys, v):
+    """src/unet/lambda.rs:452-489: keys [rows, k], v [rows, vd] -> lambda [k, vd]."""
+    L = lib()
+    _declare_unet(L)
+    keys = _f32(keys).copy()
+    v = _f32(v)
+    rows, k = keys.shape
+    vd = v.shape[1]
+    out = np.empty((k, vd), np.float32)
+    L.orc_softmax_lambda(_p(keys), _p(v), rows, k, vd, _p(out))
+    return out
+
+
+def tap_filter(a, v, o, hh, ww):
+    """src/unet/lambda.rs:288-314 over a whole item: a [hw, 8, 226], v [hw, k], o [hw, 8*k] (updated)."""
+    L = lib()
+    _declare_unet(L)
+    a, v = _f32(a), _f32(v)
+    o = _f32(o).copy()
+    L.orc_tap_filter(_p(a), _p(v), _p(o), 0, hh * ww, hh, ww, v.shape[1])
+    return o
+
+
+def position_term(q, e, v, o):
+    """src/unet/lambda.rs:409-425: q, o [px, 8k]; e [px, 10, k]; v [10, k]; returns the updated o."""
+    L = lib()
+    _declare_unet(L)
+    q, e, v = _f32(q), _f32(e), _f32(v)
+    o = _f32(o).copy()
+    L.orc_position_term(_p(q), _p(e), _p(v), _p(o), q.shape[0], v.shape[1])
+    return o
+
+
+def dot8(a, b):
+    """src/unet/lambda.rs:429-439"""
+    L = lib()
+    _declare_unet(L)
+    a, b = _f32(a), _f32(b)
+    return float(L.orc_dot8(_p(a), _p(b), a.size))
+
+
+class UNet:
+    """src/unet/mod.rs UNet over a dict of converter tensors (f32 arrays)."""
+
+    def __init__(self, params: dict):
+        L = lib()
+        _declare_unet(L)
+        self._keep = {k: np.ascontiguousarray(v, dtype=np.float32) for k, v in params.items()}
+        arr = (_Named * len(self._keep))()
+        for i, (k, v) in enumerate(self._keep.items()):
+            arr[i].name = k.encode()
+            arr[i].data = v.ctypes.data
+            arr[i].numel = v.size
+        err = ctypes.create_string_buffer(512)
+        self.h = L.orc_unet_create(arr, len(self._keep), err, 512)
+        if not self.h:
+            raise RuntimeError("oracle UNet load failed: " + err.value.decode())
+
+    def forward(self, x, timestep: int, cfg: bool = True, trace: bool = False):
+        """x [1,64,64,9] -> eps [b,64,64,4] (b = 2 with CFG); with trace, also {name: tensor}."""
+        x = _f32(x)
+        b = 2 if cfg else 1
+        eps = np.empty((b, 64, 64, 4), np.float32)
+        traced = {}
+
+        def cb(_user, name, data, n, h, w, c):
+            traced[name.decode()] = np.ctypeslib.as_array(data, shape=(n * h * w * c,)).reshape(n, h, w, c).copy()
+
+        fn = _TRACE_FN(cb) if trace else _TRACE_FN()
+        st = lib().orc_unet_forward(self.h, _p(x), int(timestep), 0 if cfg else 1, _p(eps), fn, None)
+        if st != 0:
+            raise RuntimeError("oracle UNet forward failed")
+        return (eps, traced) if trace else eps
+
+    def __del__(self):
+        try:
+            lib().orc_unet_destroy(self.h)
+        except Exception:
+            pass
+
+
+BLOCK_KINDS = {"dwconv": 0, "resnet": 1, "self_lambda": 2, "cross_lambda": 3, "transformer": 4}
+
+
+def block_forward(kind: str, params: dict, prefix: str, x, c_out=None, temb=None, branches=None):
+    """One UNet block alone (oracle/unet.cpp orc_block_forward)."""
+    L = lib()
+    _declare_unet(L)
+    keep = {k: np.ascontiguousarray(v, dtype=np.float32) for k, v in params.items()}
+    arr = (_Named * len(keep))()
+    for i, (k, v) in enumerate(keep.items()):
+        arr[i].name = k.encode()
+        arr[i].data = v.ctypes.data
+        arr[i].numel = v.size
+    x = _f32(x)
+    n, h, w, ci = x.shape
+    co = ci if c_out is None else c_out
+    out = np.empty((n, h, w, co), np.float32)
+    temb = _f32(temb)
+    br = None if branches is None else np.ascontiguousarray(branches, dtype=np.int32)
+    err = ctypes.create_string_buffer(512)
+    st = L.orc_block_forward(BLOCK_KINDS[kind], arr, len(keep), prefix.encode(), _p(x), n, h, w, ci, co, _p(temb),
+                             None if br is None else br.ctypes.data, _p(out), err, 512)
+    if st != 0:
+        raise RuntimeError(err.value.decode())
+    return out

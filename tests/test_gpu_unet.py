@@ -1,0 +1,178 @@
+"""GPU parity of the UNet path, through the C ABI: the lambda-layer kernels
+against the oracle (bit for bit where the kernel restates the CPU operation
+order), then one full 512^2 denoise step (64x64 latent, random-init weights)
+against the oracle, block by block with the reference's trace names."""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from moebius_cpu_amd import engine as E
+from moebius_cpu_amd import unet_params as U
+from moebius_cpu_amd.unet import UNet
+from tests.util import max_abs_rel
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = E.Context(0)
+    yield c
+    c.synchronize()
+    c.close()
+
+
+def D(ctx, a):
+    return E.DeviceArray.from_numpy(ctx, np.ascontiguousarray(a, dtype=np.float32))
+
+
+@pytest.mark.parametrize("nb,rows,k", [(2, 4096, 40), (2, 1024, 80), (2, 256, 160), (2, 10, 40)])
+def test_softmax_lambda_kernel(ctx, nb, rows, k):
+    rng = np.random.default_rng(rows + k)
+    keys = (rng.standard_normal((nb, rows, k)) * 2).astype(np.float32)
+    v = rng.standard_normal((nb, rows, k)).astype(np.float32)
+    out = E.DeviceArray(ctx, (nb, k, k))
+    kd, vd_ = D(ctx, keys), D(ctx, v)  # held until the call returns
+    E.check(E.lib().mh_softmax_lambda(ctx.h, kd.ptr, vd_.ptr, nb, rows, k, k, out.ptr))
+    got = out.numpy()
+    for b in range(nb):
+        want = oracle.softmax_lambda(keys[b], v[b])
+        assert max_abs_rel(got[b].T, want) < 1e-5
+
+
+@pytest.mark.parametrize("nb,hh,ww,vd", [(2, 16, 12, 40), (1, 7, 5, 8), (2, 16, 16, 160)])
+def test_tap_filter_kernel_bit_exact(ctx, nb, hh, ww, vd):
+    rng = np.random.default_rng(hh * ww + vd)
+    a = rng.standard_normal((nb, hh * ww, 8, 226)).astype(np.float32)
+    v = rng.standard_normal((nb, hh * ww, vd)).astype(np.float32)
+    o = rng.standard_normal((nb, hh * ww, 8 * vd)).astype(np.float32)
+    od = D(ctx, o)
+    ad, vdev = D(ctx, a), D(ctx, v)
+    E.check(E.lib().mh_tap_filter(ctx.h, ad.ptr, vdev.ptr, od.ptr, nb, hh, ww, vd))
+    got = od.numpy()
+    for b in range(nb):
+        assert np.array_equal(got[b], oracle.tap_filter(a[b], v[b], o[b], hh, ww))
+
+
+@pytest.mark.parametrize("br0,nb,k", [(0, 2, 40), (1, 1, 80), (0, 2, 160)])
+def test_position_term_kernel_bit_exact(ctx, br0, nb, k):
+    hw = 37
+    rng = np.random.default_rng(k + nb)
+    q = rng.standard_normal((nb, hw, 8 * k)).astype(np.float32)
+    e = rng.standard_normal((hw, 10, k)).astype(np.float32)
+    vb = rng.standard_normal((2, 10, k)).astype(np.float32)
+    o = rng.standard_normal((nb, hw, 8 * k)).astype(np.float32)
+    od = D(ctx, o)
+    qd, ed, vbd = D(ctx, q), D(ctx, e), D(ctx, vb)
+    E.check(E.lib().mh_position_term(ctx.h, qd.ptr, ed.ptr, vbd.ptr, br0, nb, hw, k, od.ptr))
+    got = od.numpy()
+    for b in range(nb):
+        assert np.array_equal(got[b], oracle.position_term(q[b], e, vb[br0 + b], o[b]))
+
+
+def test_gemm_nt_kernel(ctx):
+    rng = np.random.default_rng(9)
+    m, n, k = 300, 226, 40
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    b = rng.standard_normal((n, k)).astype(np.float32)
+    c = E.DeviceArray(ctx, (m, n))
+    ad, bd = D(ctx, a), D(ctx, b)
+    E.check(E.lib().mh_gemm_nt(ctx.h, ad.ptr, k, bd.ptr, 0, k, m, n, k, None, None, c.ptr, n))
+    assert max_abs_rel(c.numpy(), a.astype(np.float64) @ b.astype(np.float64).T) < 1e-5
+
+
+def test_best_fit_matches_reference_policy():
+    """src/engine/mod.rs:104-117 and its tests (mod.rs:124-181)."""
+    L = E.lib()
+
+    def bf(pairs, want):
+        lens = (ctypes.c_uint64 * len(pairs))(*[p[0] for p in pairs])
+        caps = (ctypes.c_uint64 * len(pairs))(*[p[1] for p in pairs])
+        return L.mh_scratch_best_fit(lens, caps, len(pairs), want)
+
+    assert bf([(100, 100), (1000, 1000), (10, 10)], 1000) == 1
+    assert bf([(100, 100), (1000, 1000), (10, 10)], 10) == 2
+    assert bf([(100, 100), (1000, 1000), (10, 10)], 100) == 0
+    assert bf([(100, 100), (1000, 1000), (10, 10)], 5000) == 1  # largest grows
+    assert bf([(10, 200), (50, 60)], 55) == 1                    # least growth within capacity
+    assert bf([(64, 64), (64, 64)], 64) == 1                     # later entries win ties
+    assert bf([], 1) == -1
+
+
+@pytest.fixture(scope="module")
+def params():
+    return U.random_unet(seed=4000)
+
+
+@pytest.fixture(scope="module")
+def onet(params):
+    return oracle.UNet(params)
+
+
+@pytest.fixture(scope="module")
+def gnet(ctx, params):
+    return UNet(ctx, params)
+
+
+def _compare_traces(got, want):
+    assert list(got) == list(want), "trace names or order differ"
+    worst = 0.0
+    for name in want:
+        err = max_abs_rel(got[name], want[name])
+        worst = max(worst, err)
+        assert err <= TOL, f"{name}: max-abs/max|ref| {err:.3e}"
+    return worst
+
+
+def test_unet_step_cfg_matches_oracle(ctx, gnet, onet):
+    inp = U.unet_input(seed=5000)
+    eps_o, tr_o = onet.forward(inp.x, inp.timestep, cfg=True, trace=True)
+    eps_g, tr_g = gnet.forward_traced(inp.x, inp.timestep, cfg=True)
+    worst = _compare_traces(tr_g, tr_o)
+    print(f"worst block max-abs/max|ref| = {worst:.3e}")
+    assert max_abs_rel(eps_g, eps_o) <= TOL
+
+
+def test_unet_step_cond_only_matches_oracle(ctx, gnet, onet):
+    inp = U.unet_input(seed=5003)
+    eps_o = onet.forward(inp.x, inp.timestep, cfg=False)
+    eps_g = gnet.forward_host(inp.x, inp.timestep, cfg=False)
+    assert eps_g.shape == (1, 64, 64, 4)
+    assert max_abs_rel(eps_g, eps_o) <= TOL
+
+
+def test_unet_step_is_deterministic_and_batch_consistent(ctx, gnet):
+    inp = U.unet_input(seed=5004)
+    a = gnet.forward_host(inp.x, inp.timestep, cfg=True)
+    b = gnet.forward_host(inp.x, inp.timestep, cfg=True)
+    assert np.array_equal(a, b)
+    c = gnet.forward_host(inp.x, inp.timestep, cfg=False)
+    assert max_abs_rel(c[0], a[1]) <= TOL  # the cond item of a CFG step is the cond-only step
+
+
+def test_unet_f16_stored_weights(ctx, params, onet):
+    """f16-stored GEMM weights, f32 arithmetic: equals the f32 path on the rounded weights."""
+    p16 = {k: v for k, v in params.items()}
+    gemm = {s.name for s in U.unet_specs() if s.gemm}
+    rounded = {k: (v.astype(np.float16).astype(np.float32) if k in gemm else v) for k, v in p16.items()}
+    net16 = UNet(ctx, params, f16_gemm=True)
+    inp = U.unet_input(seed=5005)
+    got = net16.forward_host(inp.x, inp.timestep, cfg=False)
+    want = oracle.UNet(rounded).forward(inp.x, inp.timestep, cfg=False)
+    assert max_abs_rel(got, want) <= TOL
+    w, _ = net16.memory()
+    w32, _ = UNet(ctx, params).memory()
+    assert w < 0.6 * w32  # GEMM weights really stored at half width
+
+
+def test_missing_weight_is_a_weights_error(ctx, params):
+    broken = dict(params)
+    broken.pop("diff_model.down_blocks.1.attentions.0.proj_in.weight")
+    with pytest.raises(E.MoebiusError) as ei:
+        UNet(ctx, broken)
+    assert ei.value.code == 2 and "proj_in.weight" in ei.value.msg

@@ -125,6 +125,18 @@ int32_t mh_conv1x1_forward(MhContext *ctx, const float *x, uint32_t n, uint32_t 
                            const void *weight, uint32_t weight_dtype, uint32_t c_out, const float *bias,
                            const float *residual, float *out);
 
+/* Conv1x1::forward fused with what the reference does around it in a resnet
+ * block (src/unet/blocks.rs:47-52, 98-109): the residual is transformed per item
+ * and channel as GroupNorm's apply would, [SiLU](residual . scale + shift) with
+ * scale/shift [n * c_out] from mh_group_norm_affine (the normalised block input
+ * is never stored), and a second residual is added last, as the block's
+ * add_inplace: out = ((residual' + bias) + x . W^T) + residual2. residual_scale
+ * and residual_shift NULL: residual used as is; residual2 may be NULL. */
+int32_t mh_conv1x1_fused(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c_in,
+                         const void *weight, uint32_t weight_dtype, uint32_t c_out, const float *bias,
+                         const float *residual, const float *residual_scale, const float *residual_shift,
+                         uint32_t residual_silu, const float *residual2, float *out);
+
 /* src/engine/conv.rs:77-81 `Conv3x3::output_hw`. pad = [top, left, bottom, right]. */
 int32_t mh_conv3x3_output_hw(uint32_t h, uint32_t w, uint32_t stride, const uint32_t pad[4], uint32_t upsample2x,
                              uint32_t *ho, uint32_t *wo);
@@ -152,6 +164,14 @@ int32_t mh_im2col_gather(MhContext *ctx, const float *x, uint32_t n, uint32_t h,
  * weight [3,3,c], bias [c]; out [n,h,w,c] (c/2 channels for GLU_SILU). */
 int32_t mh_depthwise3x3(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
                         const float *weight, const float *bias, uint32_t epilogue, float *out);
+
+/* depthwise3x3 reading GroupNorm's output without storing it
+ * (src/unet/blocks.rs:89-90, 98-101: norm then DwConv2d): each in-image input
+ * value becomes [SiLU](x . scale + shift) (scale/shift [n * c] from
+ * mh_group_norm_affine) as it is loaded; the zero padding is not transformed. */
+int32_t mh_depthwise3x3_fused(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
+                              const float *weight, const float *bias, uint32_t epilogue, const float *prologue_scale,
+                              const float *prologue_shift, uint32_t prologue_silu, float *out);
 
 /* src/engine/norm.rs:57-105 `GroupNorm::affine`: per item and channel
  * scale/shift ([n * c] each, device) with GN(x + add) = x.scale + shift.
@@ -196,21 +216,30 @@ int32_t mh_math_eval(MhContext *ctx, uint32_t which, const float *x, uint64_t le
 int32_t mh_softmax_lambda(MhContext *ctx, const float *keys, const float *v, uint32_t nb, uint32_t rows, uint32_t k,
                           uint32_t vd, float *lambda_t);
 
-/* src/unet/lambda.rs:288-314 `tap_filter` over nb items of hh x ww pixels:
- * o [nb*hh*ww][8*vd] += A[., 225] + 15x15 taps of v [nb*hh*ww][vd]; a [nb*hh*ww][8][226]. */
-int32_t mh_tap_filter(MhContext *ctx, const float *a, const float *v, float *o, uint32_t nb, uint32_t hh,
-                      uint32_t ww, uint32_t vd);
+/* src/unet/lambda.rs:288-314 `tap_filter` over nb items of hh x ww pixels, per
+ * pixel, head and value channel: u = (yc + A[225]) then + A[dy*15+dx] * v[pixel +
+ * (dy-7, dx-7)] over the in-image taps in (dy, dx) order; out = u, or residual + u
+ * when residual is given (the block's following `add_inplace`). a_t is the
+ * reference's A [pixel][head][226] stored tap-major, [nb*hh*ww][226][8];
+ * v [nb*hh*ww][vd]; yc, residual, out [nb*hh*ww][8*vd]; out may alias yc or residual. */
+int32_t mh_tap_filter(MhContext *ctx, const float *a_t, const float *v, const float *yc, const float *residual,
+                      float *out, uint32_t nb, uint32_t hh, uint32_t ww, uint32_t vd);
 
-/* src/unet/lambda.rs:406-425 `position_term`: o [nb*hw][8*k] += (q . E) . V[branch]
- * with e [hw][10][k], v_branches [2][10][k], item i using branch br0 + i. */
+/* src/unet/lambda.rs:406-425 `position_term`: u = yc + (q . E) . V[branch], per
+ * element in the reference's order; out = u, or residual + u when residual is
+ * given. e [hw][10][k], v_branches [2][10][k], item i using branch br0 + i;
+ * q, yc, residual, out [nb*hw][8*k]; out may alias yc or residual. */
 int32_t mh_position_term(MhContext *ctx, const float *q, const float *e, const float *v_branches, uint32_t br0,
-                         uint32_t nb, uint32_t hw, uint32_t k, float *o);
+                         uint32_t nb, uint32_t hw, uint32_t k, const float *yc, const float *residual, float *out);
 
 /* src/engine/gemm.rs:63-132 `matmul` for K-contiguous operands, on the device:
- * c [m][ldc] = a [m][lda] . b[n][ldb]^T (+ bias[n]) (+ residual [m][ldc]); b F32/F16. */
+ * c [m][ldc] = a [m][lda] . b[n][ldb]^T (+ bias[n]) (+ residual [m][ldc]); b F32/F16.
+ * row_group g > 1 (m a multiple of g, g <= 64) stores row i, column j at
+ * c[(i / g) * ldc + j * g + i % g] (residual read the same way), e.g. the
+ * lambda layer's per-(pixel, head) rows as [pixel][tap][head]; 0 or 1: plain. */
 int32_t mh_gemm_nt(MhContext *ctx, const float *a, uint64_t lda, const void *b, uint32_t b_dtype, uint64_t ldb,
                    uint32_t m, uint32_t n, uint32_t k, const float *bias, const float *residual, float *c,
-                   uint64_t ldc);
+                   uint64_t ldc, uint32_t row_group);
 
 /* ---- UNet (src/unet) ---- */
 

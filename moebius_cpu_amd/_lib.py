@@ -64,11 +64,14 @@ SIGNATURES = {
     "mh_event_destroy": (None, [_vp]),
     "mh_bias_residual_add": (_i32, [_vp, _vp, _u64, _u32, _vp, _vp, _vp]),
     "mh_conv1x1_forward": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _u32, _u32, _vp, _vp, _vp]),
+    "mh_conv1x1_fused": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _u32, _u32, _vp, _vp, _vp, _vp, _u32, _vp,
+                                 _vp]),
     "mh_conv3x3_output_hw": (_i32, [_u32, _u32, _u32, _u32p, _u32, _u32p, _u32p]),
     "mh_conv3x3_forward": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _u32, _u32, _vp, _u32, _u32p, _u32,
                                   _vp, _vp, _u32, _vp]),
     "mh_im2col_gather": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32p, _u32, _u64, _u64, _vp]),
     "mh_depthwise3x3": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _vp]),
+    "mh_depthwise3x3_fused": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _vp, _vp, _u32, _vp]),
     "mh_group_norm_affine": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _f32, _vp, _vp, _vp, _vp, _vp]),
     "mh_group_norm_forward": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _f32, _vp, _vp, _vp, _u32, _vp]),
     "mh_apply_affine": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _vp]),
@@ -80,9 +83,9 @@ SIGNATURES = {
     "mh_math_eval": (_i32, [_vp, _u32, _vp, _u64, _vp]),
     "mh_selftest_mfma_f32": (_i32, [_vp, _vp, _vp, _vp]),
     "mh_softmax_lambda": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
-    "mh_tap_filter": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32]),
-    "mh_position_term": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
-    "mh_gemm_nt": (_i32, [_vp, _vp, _u64, _vp, _u32, _u64, _u32, _u32, _u32, _vp, _vp, _vp, _u64]),
+    "mh_tap_filter": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32]),
+    "mh_position_term": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
+    "mh_gemm_nt": (_i32, [_vp, _vp, _u64, _vp, _u32, _u64, _u32, _u32, _u32, _vp, _vp, _vp, _u64, _u32]),
     "mh_unet_create": (_i32, [_vp, _vp, _u32, ctypes.POINTER(_vp)]),
     "mh_unet_destroy": (None, [_vp]),
     "mh_unet_forward": (_i32, [_vp, _vp, _u32, _u32, _vp]),

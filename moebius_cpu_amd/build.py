@@ -29,8 +29,12 @@ FLAGS = [
 ]
 
 
-def _compile(src: str) -> str:
+def _compile(src: str, incremental: bool = False) -> str:
     obj = os.path.join(OBJ, os.path.basename(src) + ".o")
+    if incremental and os.path.exists(obj):
+        deps = [src, *glob.glob(os.path.join(CSRC, "*.hpp")), os.path.join(HERE, "..", "include", "moebius_hip.h")]
+        if os.path.getmtime(obj) >= max(os.path.getmtime(d) for d in deps if os.path.exists(d)):
+            return obj
     cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -42,15 +46,16 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(jobs: int | None = None, verbose: bool = True) -> str:
-    """Compiles every source and links the library; returns its path."""
+def build(jobs: int | None = None, verbose: bool = True, incremental: bool = False) -> str:
+    """Compiles every source and links the library; returns its path.
+    incremental: reuse objects newer than their source and every header."""
     if not os.path.exists(HIPCC) and shutil.which("hipcc") is None:
         raise RuntimeError("hipcc not found")
     os.makedirs(OBJ, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
     jobs = jobs or min(len(srcs), os.cpu_count() or 4, 16)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, srcs))
+        objs = list(ex.map(lambda s: _compile(s, incremental), srcs))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -63,4 +68,4 @@ def build(jobs: int | None = None, verbose: bool = True) -> str:
 
 
 if __name__ == "__main__":
-    build()
+    build(incremental="-i" in sys.argv[1:])

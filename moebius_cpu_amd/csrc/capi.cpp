@@ -247,6 +247,28 @@ int32_t mh_conv1x1_forward(MhContext *ctx, const float *x, uint32_t n, uint32_t 
     });
 }
 
+int32_t mh_conv1x1_fused(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c_in,
+                         const void *weight, uint32_t weight_dtype, uint32_t c_out, const float *bias,
+                         const float *residual, const float *residual_scale, const float *residual_shift,
+                         uint32_t residual_silu, const float *residual2, float *out) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(x, "x");
+        need(weight, "weight");
+        need(out, "out");
+        if ((residual_scale == nullptr) != (residual_shift == nullptr))
+            mh::fail(mh::kInvalidArgument, "residual_scale and residual_shift go together");
+        const int64_t pixels = int64_t(n) * h * w;
+        mh::ResidualAffine ra;
+        ra.scale = residual_scale;
+        ra.shift = residual_shift;
+        ra.silu = residual_silu != 0;
+        ra.rows_per_item = int(int64_t(h) * w);
+        mh::conv1x1(c, x, pixels, dim(c_in, "c_in"), weight, wtype(weight_dtype), dim(c_out, "c_out"), bias,
+                    residual, out, mh::GemmEpilogue::None, residual_scale ? &ra : nullptr, residual2);
+    });
+}
+
 int32_t mh_conv3x3_output_hw(uint32_t h, uint32_t w, uint32_t stride, const uint32_t pad[4], uint32_t upsample2x,
                              uint32_t *ho, uint32_t *wo) {
     return guard([&] {
@@ -308,6 +330,27 @@ int32_t mh_depthwise3x3(MhContext *ctx, const float *x, uint32_t n, uint32_t h, 
         need(out, "out");
         if (epilogue > MH_EPILOGUE_GLU_SILU) mh::fail(mh::kInvalidArgument, "unknown depthwise epilogue");
         mh::depthwise3x3(cc, x, dim(n, "n"), dim(h, "h"), dim(w, "w"), dim(c, "c"), weight, bias, int(epilogue), out);
+    });
+}
+
+int32_t mh_depthwise3x3_fused(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
+                              const float *weight, const float *bias, uint32_t epilogue, const float *prologue_scale,
+                              const float *prologue_shift, uint32_t prologue_silu, float *out) {
+    return guard([&] {
+        mh::Context &cc = C(ctx);
+        need(x, "x");
+        need(weight, "weight");
+        need(bias, "bias");
+        need(out, "out");
+        need(prologue_scale, "prologue_scale");
+        need(prologue_shift, "prologue_shift");
+        if (epilogue > MH_EPILOGUE_GLU_SILU) mh::fail(mh::kInvalidArgument, "unknown depthwise epilogue");
+        mh::Affine aff;
+        aff.scale = prologue_scale;
+        aff.shift = prologue_shift;
+        aff.silu = prologue_silu != 0;
+        mh::depthwise3x3(cc, x, dim(n, "n"), dim(h, "h"), dim(w, "w"), dim(c, "c"), weight, bias, int(epilogue), out,
+                         &aff);
     });
 }
 
@@ -421,40 +464,45 @@ int32_t mh_softmax_lambda(MhContext *ctx, const float *keys, const float *v, uin
     });
 }
 
-int32_t mh_tap_filter(MhContext *ctx, const float *a, const float *v, float *o, uint32_t nb, uint32_t hh,
-                      uint32_t ww, uint32_t vd) {
+int32_t mh_tap_filter(MhContext *ctx, const float *a_t, const float *v, const float *yc, const float *residual,
+                      float *out, uint32_t nb, uint32_t hh, uint32_t ww, uint32_t vd) {
     return guard([&] {
         mh::Context &c = C(ctx);
-        need(a, "a");
+        need(a_t, "a_t");
         need(v, "v");
-        need(o, "o");
-        mh::tap_filter(c, a, v, o, dim(nb, "nb"), dim(hh, "hh"), dim(ww, "ww"), dim(vd, "vd"));
+        need(yc, "yc");
+        need(out, "out");
+        mh::tap_filter(c, a_t, v, yc, residual, out, dim(nb, "nb"), dim(hh, "hh"), dim(ww, "ww"), dim(vd, "vd"));
     });
 }
 
 int32_t mh_position_term(MhContext *ctx, const float *q, const float *e, const float *v_branches, uint32_t br0,
-                         uint32_t nb, uint32_t hw, uint32_t k, float *o) {
+                         uint32_t nb, uint32_t hw, uint32_t k, const float *yc, const float *residual, float *out) {
     return guard([&] {
         mh::Context &c = C(ctx);
         need(q, "q");
         need(e, "e");
         need(v_branches, "v_branches");
-        need(o, "o");
-        mh::position_term(c, q, e, v_branches, dim(br0, "br0"), dim(nb, "nb"), dim(hw, "hw"), dim(k, "k"), o);
+        need(yc, "yc");
+        need(out, "out");
+        mh::position_term(c, q, e, v_branches, dim(br0, "br0"), dim(nb, "nb"), dim(hw, "hw"), dim(k, "k"), yc,
+                          residual, out);
     });
 }
 
 int32_t mh_gemm_nt(MhContext *ctx, const float *a, uint64_t lda, const void *b, uint32_t b_dtype, uint64_t ldb,
                    uint32_t m, uint32_t n, uint32_t k, const float *bias, const float *residual, float *c,
-                   uint64_t ldc) {
+                   uint64_t ldc, uint32_t row_group) {
     return guard([&] {
         mh::Context &cc = C(ctx);
         need(a, "a");
         need(b, "b");
         need(c, "c");
-        if (lda < k || ldb < k || ldc < n) mh::fail(mh::kInvalidArgument, "gemm: leading dimension too small");
+        const uint64_t row_len = uint64_t(n) * (row_group > 1 ? row_group : 1);
+        if (lda < k || ldb < k || ldc < row_len) mh::fail(mh::kInvalidArgument, "gemm: leading dimension too small");
+        if (row_group > 64) mh::fail(mh::kInvalidArgument, "gemm: row group above 64");
         mh::gemm_nt(cc, a, int64_t(lda), 0, b, wtype(b_dtype), int64_t(ldb), 0, dim(m, "m"), dim(n, "n"),
-                    dim(k, "k"), 1, bias, residual, c, int64_t(ldc), 0);
+                    dim(k, "k"), 1, bias, residual, c, int64_t(ldc), 0, mh::GemmEpilogue::None, int(row_group));
     });
 }
 

@@ -1,0 +1,605 @@
+// Implicit-GEMM kernel template shared by the GEMM translation units (one
+// file per family of A-operand modes, so they compile in parallel). Everything
+// here has internal linkage: each file launches only its own instantiations.
+#pragma once
+#include <hip/hip_fp16.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <type_traits>
+
+#include "common.hpp"
+#include "dmath.hpp"
+#include "kernels.hpp"
+
+namespace mh {
+namespace gemm {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
+
+constexpr int BK = 32;          // K per LDS stage
+constexpr int LDS_S = BK + 4;   // padded LDS row stride (floats): conflict-free b128 reads
+constexpr int K4 = BK / 4;      // float4 per tile row
+
+// Matrix instruction: v_mfma_f32_16x16x4f32 (MF = 16) or v_mfma_f32_32x32x2f32
+// (MF = 32). Output lane layouts: 16x16: register v of lane l is row
+// 4 * (l / 16) + v, column l % 16; 32x32: row 8 * (v / 4) + 4 * (l / 32) + v % 4,
+// column l % 32.
+constexpr int MF = 32;
+constexpr int kAccRegs = MF * MF / 64;
+constexpr int kKStep = MF == 32 ? 8 : 16;  // K covered by one float4 read per lane
+typedef std::conditional_t<MF == 32, floatx16, floatx4> Acc;
+
+template <int M = MF>
+__device__ __forceinline__ std::conditional_t<M == 32, floatx16, floatx4> mfma(
+    float a, float b, const std::conditional_t<M == 32, floatx16, floatx4> &c) {
+    if constexpr (M == 32) return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+    else return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int acc_row(int v, int lane) {
+    if constexpr (MF == 32) return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+    else return 4 * (lane >> 4) + v;
+}
+
+enum AMode : int {
+    kDense = 0,      // A[m][k] row-major with leading dimension lda, K % 4 == 0
+    kDenseScalar,    // same, any K
+    kConvAligned,    // conv gather, Ci % BK == 0: one tap per K tile
+    kConvVec,        // conv gather, Ci % 4 == 0: one tap per float4
+    kConvScalar,     // conv gather, any Ci
+};
+
+struct GemmArgs {
+    const float *a;
+    int64_t lda;
+    int M, N, K;
+    // conv geometry
+    int cn, ch, cw, ci, ho, wo, stride, pad_t, pad_l, up;
+    const float *psc, *psh;
+    int psilu;
+    // B operand: [N][ldb]
+    const void *b;
+    int64_t ldb;
+    // epilogue
+    const float *bias, *res;
+    float *out;
+    int64_t ldc;
+    // split K
+    int k_split;      // K per split (multiple of BK)
+    float *partial;   // [splits][M][N] when splitting
+    // batch (grid y): element offsets of item z's A, B and output/residual
+    int64_t a_bs, b_bs, c_bs;
+    // row grouping of the output (0 or 1: plain): row m, column n is stored at
+    // (m / rg) * ldc + n * rg + m % rg, e.g. [pixel][tap][head] from (pixel, head) rows
+    int rg;
+    // residual transform: res' = [SiLU](res . rsc + rsh), per item (rows / r_rows) and column
+    const float *rsc, *rsh;
+    int rsilu, r_rows;
+    // second residual, added last: y = y + res2
+    const float *res2;
+    // byte extents of one item's A (or conv input) and of B, for the buffer
+    // loads' range check (< 2^31): an access at or past the extent reads zero
+    uint32_t a_bytes, b_bytes;
+};
+
+// (residual [transformed] + bias) + acc [SiLU] (+ res2): the reference's
+// Conv1x1 epilogue (src/engine/conv.rs:38-55) followed by the block's add_inplace.
+template <int EPI>
+__device__ __forceinline__ float epilogue_value(const GemmArgs &p, int row, int col, int64_t o, float acc, float bcol) {
+    float y;
+    if (p.res) {
+        float rv = p.res[o];
+        if (p.rsc) {
+            const int64_t i = int64_t(row / p.r_rows) * p.N + col;
+            rv = __builtin_fmaf(rv, p.rsc[i], p.rsh[i]);
+            if (p.rsilu) rv = ref_silu(rv);
+        }
+        const float t = p.bias ? rv + bcol : rv;
+        y = t + acc;
+    } else {
+        y = p.bias ? bcol + acc : acc;
+    }
+    if (EPI == 1) y = ref_silu(y);
+    if (p.res2) y = y + p.res2[o];
+    return y;
+}
+
+// Launchers, one per A-operand family (gemm_dense.hip, gemm_conv.hip).
+void launch_dense(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi, int batch, bool vec);
+void launch_conv(Context &ctx, GemmArgs &p, WeightType wt, int mode, bool pro);
+
+namespace {
+
+
+__device__ __forceinline__ int64_t out_index(const GemmArgs &p, int row, int col) {
+    if (p.rg > 1) return int64_t(row / p.rg) * p.ldc + int64_t(col) * p.rg + row % p.rg;
+    return int64_t(row) * p.ldc + col;
+}
+
+__device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
+
+// Per-row conv geometry, fixed over the K loop.
+struct ConvRow {
+    int b, iy0, ix0;
+    bool valid;
+};
+
+__device__ __forceinline__ ConvRow conv_row(const GemmArgs &p, int m) {
+    ConvRow r;
+    r.valid = m < p.M;
+    const int mm = r.valid ? m : 0;
+    const int hw = p.ho * p.wo;
+    r.b = mm / hw;
+    const int rem = mm - r.b * hw;
+    const int oy = rem / p.wo, ox = rem - (rem / p.wo) * p.wo;
+    r.iy0 = oy * p.stride - p.pad_t;
+    r.ix0 = ox * p.stride - p.pad_l;
+    return r;
+}
+
+// Source element offset of (row, tap) or -1 outside the (upsampled) image.
+__device__ __forceinline__ int64_t conv_src(const GemmArgs &p, const ConvRow &r, int ky, int kx) {
+    const int iy = r.iy0 + ky, ix = r.ix0 + kx;
+    const int hi = p.ch << p.up, wi = p.cw << p.up;
+    if (!r.valid || iy < 0 || ix < 0 || iy >= hi || ix >= wi) return -1;
+    return ((int64_t(r.b) * p.ch + (iy >> p.up)) * p.cw + (ix >> p.up)) * p.ci;
+}
+
+__device__ __forceinline__ float prologue1(const GemmArgs &p, int b, int c, float v) {
+    const float y = __builtin_fmaf(v, p.psc[int64_t(b) * p.ci + c], p.psh[int64_t(b) * p.ci + c]);
+    return p.psilu ? ref_silu(y) : y;
+}
+
+template <int MODE, bool PRO>
+__device__ __forceinline__ floatx4 load_a(const GemmArgs &p, const ConvRow &r, int m, int k, int tap_ky,
+                                          int tap_kx, int tap_ci0) {
+    if (MODE == kDense) {
+        if (m >= p.M || k >= p.K) return zero4();
+        return *reinterpret_cast<const floatx4 *>(p.a + int64_t(m) * p.lda + k);
+    } else if (MODE == kDenseScalar) {
+        floatx4 v = zero4();
+        if (m < p.M) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (k + e < p.K) v[e] = p.a[int64_t(m) * p.lda + k + e];
+        }
+        return v;
+    } else if (MODE == kConvAligned || MODE == kConvVec) {
+        if (k >= p.K) return zero4();
+        int ky, kx, c;
+        if (MODE == kConvAligned) {
+            ky = tap_ky;
+            kx = tap_kx;
+            c = tap_ci0 + (k & (BK - 1));
+        } else {
+            const int tap = k / p.ci;
+            c = k - tap * p.ci;
+            ky = tap / 3;
+            kx = tap - ky * 3;
+        }
+        const int64_t off = conv_src(p, r, ky, kx);
+        if (off < 0) return zero4();
+        floatx4 v = *reinterpret_cast<const floatx4 *>(p.a + off + c);
+        if (PRO) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = prologue1(p, r.b, c + e, v[e]);
+        }
+        return v;
+    } else {  // kConvScalar
+        floatx4 v = zero4();
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int kk = k + e;
+            if (kk >= p.K) break;
+            const int tap = kk / p.ci;
+            const int c = kk - tap * p.ci;
+            const int ky = tap / 3, kx = tap - ky * 3;
+            const int64_t off = conv_src(p, r, ky, kx);
+            if (off >= 0) {
+                float x = p.a[off + c];
+                if (PRO) x = prologue1(p, r.b, c, x);
+                v[e] = x;
+            }
+        }
+        return v;
+    }
+}
+
+// Buffer loads: a lane whose element is outside the operand (rows past M or
+// N, K past the split's end, conv padding) gets an offset past the resource's
+// extent, which the hardware answers with zeros. The loads are therefore
+// unconditional (no branch per load), and the compiler can wait for one K
+// tile's loads while the next tile's are still in flight.
+constexpr int kOob = int(0x80000000u);
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), short(0), int(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ floatx4 buf_load4(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+template <int MODE, bool PRO>
+__device__ __forceinline__ floatx4 load_a_buf(const GemmArgs &p, __amdgpu_buffer_rsrc_t ar, const ConvRow &r, int m,
+                                              int k, int k_end, int tap_ky, int tap_kx, int tap_ci0) {
+    if constexpr (MODE == kDense) {
+        const bool ok = m < p.M && k < k_end;
+        return buf_load4(ar, ok ? int((int64_t(m) * p.lda + k) * 4) : kOob);
+    } else {
+        int ky, kx, c;
+        if constexpr (MODE == kConvAligned) {
+            ky = tap_ky;
+            kx = tap_kx;
+            c = tap_ci0 + (k & (BK - 1));
+        } else {
+            const int tap = k / p.ci;
+            c = k - tap * p.ci;
+            ky = tap / 3;
+            kx = tap - ky * 3;
+        }
+        const int64_t src = conv_src(p, r, ky, kx);
+        const bool ok = k < k_end && src >= 0;
+        floatx4 v = buf_load4(ar, ok ? int((src + c) * 4) : kOob);
+        if constexpr (PRO) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = ok ? prologue1(p, r.b, c + e, v[e]) : 0.0f;
+        }
+        return v;
+    }
+}
+
+template <bool F16>
+__device__ __forceinline__ floatx4 load_b_buf(const GemmArgs &p, __amdgpu_buffer_rsrc_t br, int n, int k, int k_end) {
+    const bool ok = n < p.N && k < k_end;
+    const int64_t e = int64_t(n) * p.ldb + k;
+    if constexpr (F16) {
+        const auto raw = __builtin_amdgcn_raw_buffer_load_b64(br, ok ? int(e * 2) : kOob, 0, 0);
+        const halfx4 h = __builtin_bit_cast(halfx4, raw);
+        floatx4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = float(h[i]);
+        return v;
+    } else {
+        return buf_load4(br, ok ? int(e * 4) : kOob);
+    }
+}
+
+template <bool F16, bool BVEC>
+__device__ __forceinline__ floatx4 load_b(const GemmArgs &p, int n, int k) {
+    floatx4 v = zero4();
+    if (n >= p.N) return v;
+    if (BVEC) {
+        if (k >= p.K) return v;
+        if (F16) {
+            const halfx4 h = *reinterpret_cast<const halfx4 *>(static_cast<const _Float16 *>(p.b) + int64_t(n) * p.ldb + k);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = float(h[e]);
+        } else {
+            v = *reinterpret_cast<const floatx4 *>(static_cast<const float *>(p.b) + int64_t(n) * p.ldb + k);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (k + e < p.K) {
+                if (F16)
+                    v[e] = float(static_cast<const _Float16 *>(p.b)[int64_t(n) * p.ldb + k + e]);
+                else
+                    v[e] = static_cast<const float *>(p.b)[int64_t(n) * p.ldb + k + e];
+            }
+        }
+    }
+    return v;
+}
+
+template <int BM, int BN, int MODE, bool PRO, bool F16, bool BVEC, int EPI, bool SPLIT>
+__global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
+    constexpr int FM = BM / 2 / MF, FN = BN / 2 / MF;  // MF x MF blocks per wave
+    if (blockIdx.y) {
+        const int64_t bz = blockIdx.y;
+        p.a += bz * p.a_bs;
+        p.b = static_cast<const char *>(p.b) + bz * p.b_bs * (F16 ? 2 : 4);
+        p.out += bz * p.c_bs;
+        if (p.res) p.res += bz * p.c_bs;
+    }
+    constexpr int A_LD = BM * K4 / 256, B_LD = BN * K4 / 256;
+    // Two LDS stages: tile kt+1 is written while tile kt is read, one barrier per K tile.
+    __shared__ float As[2][BM * LDS_S];
+    __shared__ float Bs[2][BN * LDS_S];
+
+    const int tiles_m = (p.M + BM - 1) / BM;
+    const int tiles_n = (p.N + BN - 1) / BN;
+    // Grouped tile order: 8 tile-rows share their B panels while they run.
+    int tm, tn;
+    {
+        constexpr int GROUP = 8;
+        const int pid = blockIdx.x;
+        const int in_group = GROUP * tiles_n;
+        const int gid = pid / in_group;
+        const int first = gid * GROUP;
+        const int gsize = min(tiles_m - first, GROUP);
+        const int r = pid - gid * in_group;
+        tm = first + r % gsize;
+        tn = r / gsize;
+    }
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int k_begin = SPLIT ? blockIdx.z * p.k_split : 0;
+    const int k_end = SPLIT ? min(p.K, k_begin + p.k_split) : p.K;
+    const int ktiles = (k_end - k_begin + BK - 1) / BK;
+
+    const int tid = threadIdx.x;
+    const int lrow = tid >> 3, lc4 = tid & 7;  // load slot: row within 32-row pass, float4 column
+
+    ConvRow crow[A_LD];
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+        if (MODE >= kConvAligned) crow[i] = conv_row(p, m0 + lrow + 32 * i);
+        else crow[i] = ConvRow{0, 0, 0, true};
+    }
+
+    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(p.a, p.a_bytes);
+    const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(p.b, p.b_bytes);
+    // Two register stages (tiles kt+1 and kt+2 in flight while LDS stage kt&1
+    // is consumed), two LDS stages: a load has two compute phases to land.
+    floatx4 ra0[A_LD], rb0[B_LD], ra1[A_LD], rb1[B_LD];
+    auto fetch = [&](int kt, floatx4 (&ra)[A_LD], floatx4 (&rb)[B_LD]) {
+        const int k0 = k_begin + kt * BK;
+        int tky = 0, tkx = 0, tci = 0;
+        if (MODE == kConvAligned) {
+            const int tap = k0 / p.ci;
+            tci = k0 - tap * p.ci;
+            tky = tap / 3;
+            tkx = tap - tky * 3;
+        }
+        const int k = k0 + lc4 * 4;
+#pragma unroll
+        for (int i = 0; i < A_LD; ++i) {
+            if constexpr (MODE == kDense || MODE == kConvAligned || MODE == kConvVec)
+                ra[i] = load_a_buf<MODE, PRO>(p, a_rsrc, crow[i], m0 + lrow + 32 * i, k, k_end, tky, tkx, tci);
+            else
+                ra[i] = (k < k_end) ? load_a<MODE, PRO>(p, crow[i], m0 + lrow + 32 * i, k, tky, tkx, tci) : zero4();
+        }
+#pragma unroll
+        for (int i = 0; i < B_LD; ++i) {
+            if constexpr (BVEC)
+                rb[i] = load_b_buf<F16>(p, b_rsrc, n0 + lrow + 32 * i, k, k_end);
+            else
+                rb[i] = (k < k_end) ? load_b<F16, BVEC>(p, n0 + lrow + 32 * i, k) : zero4();
+        }
+    };
+    auto stash = [&](int buf, const floatx4 (&ra)[A_LD], const floatx4 (&rb)[B_LD]) {
+#pragma unroll
+        for (int i = 0; i < A_LD; ++i)
+            *reinterpret_cast<floatx4 *>(As[buf] + (lrow + 32 * i) * LDS_S + lc4 * 4) = ra[i];
+#pragma unroll
+        for (int i = 0; i < B_LD; ++i)
+            *reinterpret_cast<floatx4 *>(Bs[buf] + (lrow + 32 * i) * LDS_S + lc4 * 4) = rb[i];
+    };
+
+    Acc acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int v = 0; v < kAccRegs; ++v) acc[i][j][v] = 0.f;
+
+    // Lane l reads a float4 along K at row l % MF, K offset 4 * (l / MF): the
+    // four lane groups (two for 32x32) each cover 4 consecutive K.
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int a_off = (wm * (BM / 2) + (lane % MF)) * LDS_S + (lane / MF) * 4;
+    const int b_off = (wn * (BN / 2) + (lane % MF)) * LDS_S + (lane / MF) * 4;
+    auto compute = [&](int buf) {
+        const float *as_w = As[buf] + a_off;
+        const float *bs_w = Bs[buf] + b_off;
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += kKStep) {
+            floatx4 a[FM], b[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const floatx4 *>(as_w + i * MF * LDS_S + kk);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) b[j] = *reinterpret_cast<const floatx4 *>(bs_w + j * MF * LDS_S + kk);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+#pragma unroll
+                    for (int j = 0; j < FN; ++j) acc[i][j] = mfma(a[i][t], b[j][t], acc[i][j]);
+        }
+    };
+
+    // Even half: LDS 0 holds tile kt, registers 1 hold kt+1, registers 0 kt+2.
+    // Odd half: LDS 1 holds kt+1, registers 0 hold kt+2, registers 1 kt+3.
+    // Tiles past the end are fetched as zeros (out-of-range offsets) and never
+    // computed; the loop body has no per-tile conditions, so the compiler waits
+    // only for the older register stage before each LDS store.
+    fetch(0, ra0, rb0);
+    fetch(1, ra1, rb1);
+    stash(0, ra0, rb0);
+    fetch(2, ra0, rb0);
+    __syncthreads();
+    int kt = 0;
+    for (; kt + 3 < ktiles; kt += 2) {  // four or more tiles left: one pair, no exits inside
+        compute(0);
+        stash(1, ra1, rb1);
+        fetch(kt + 3, ra1, rb1);
+        __syncthreads();
+        compute(1);
+        stash(0, ra0, rb0);
+        fetch(kt + 4, ra0, rb0);
+        __syncthreads();
+    }
+    // one to three tiles left: kt in LDS 0, kt+1 in registers 1, kt+2 in registers 0
+    compute(0);
+    if (kt + 1 < ktiles) {
+        stash(1, ra1, rb1);
+        __syncthreads();
+        compute(1);
+        if (kt + 2 < ktiles) {
+            stash(0, ra0, rb0);
+            __syncthreads();
+            compute(0);
+        }
+    }
+
+    // Epilogue: block (i, j), register v, lane l holds row acc_row(v, l), column l % MF.
+    const int row_base = m0 + wm * (BM / 2);
+    const int col_base = n0 + wn * (BN / 2) + (lane % MF);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int col = col_base + j * MF;
+        if (col >= p.N) continue;
+        const float bcol = (!SPLIT && p.bias) ? p.bias[col] : 0.f;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+#pragma unroll
+            for (int v = 0; v < kAccRegs; ++v) {
+                const int row = row_base + i * MF + acc_row(v, lane);
+                if (row >= p.M) continue;
+                const float r = acc[i][j][v];
+                if (SPLIT) {
+                    p.partial[(int64_t(blockIdx.z) * p.M + row) * p.N + col] = r;
+                } else {
+                    const int64_t o = out_index(p, row, col);
+                    p.out[o] = epilogue_value<EPI>(p, row, col, o, r, bcol);
+                }
+            }
+        }
+    }
+}
+
+// Sums split-K partials in split order, then (residual + bias) + sum [SiLU].
+template <int EPI>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int splits) {
+    const int64_t total = int64_t(p.M) * p.N;
+    for (int64_t e = blockIdx.x * int64_t(256) + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
+        float s = p.partial[e];
+        for (int z = 1; z < splits; ++z) s += p.partial[int64_t(z) * total + e];
+        const int row = int(e / p.N);
+        const int col = int(e - int64_t(row) * p.N);
+        const int64_t o = out_index(p, row, col);
+        p.out[o] = epilogue_value<EPI>(p, row, col, o, s, p.bias ? p.bias[col] : 0.0f);
+    }
+}
+
+struct Plan {
+    int bm, bn, splits, k_split;
+};
+
+// Tile shape and K split, from a sweep of every (tile, split) on MI355X over
+// the UNet's GEMM shapes (M 2..65536, N 4..6400, K 9..11520):
+//  - Long K (>= 4096, the upsample / downsample convs): 128x128 tiles, K split
+//    in 3; 75-77% of f32 MFMA peak, against 67% unsplit.
+//  - Otherwise 64x64 tiles, several co-resident workgroups per CU hiding load
+//    latency: K is split only while the grid is under twice the CU count and
+//    each split keeps at least 8 K tiles.
+inline Plan plan_for(int M, int N, int K, int cus) {
+    const int ktiles = int(ceil_div(K, BK));
+    auto split = [&](int64_t tiles, int64_t target, int max_splits) {
+        int want = 1;
+        if (tiles < target) want = int(std::min<int64_t>(ceil_div(target, tiles), std::max(1, ktiles / 8)));
+        want = std::max(1, std::min(want, max_splits));
+        const int per = int(ceil_div(ktiles, want));
+        return std::make_pair(int(ceil_div(ktiles, per)), per * BK);
+    };
+    if (K >= 4096 && M >= 1024) {
+        const auto s = split(ceil_div(M, 128) * ceil_div(N, 128), 3 * int64_t(cus), 3);
+        return Plan{128, 128, s.first, s.second};
+    }
+    const auto s = split(ceil_div(M, 64) * ceil_div(N, 64), 2 * int64_t(cus), 6);
+    return Plan{64, 64, s.first, s.first > 1 ? s.second : K};
+}
+
+template <int BM, int BN, int MODE, bool PRO, bool F16, bool BVEC>
+void launch_cfg(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int batch) {
+    const unsigned tiles = unsigned(ceil_div(p.M, BM) * ceil_div(p.N, BN));
+    if (pl.splits > 1) {
+        const size_t bytes = size_t(pl.splits) * p.M * p.N * sizeof(float);
+        p.partial = static_cast<float *>(ctx.ws.get(bytes, ctx.stream));
+        p.k_split = pl.k_split;
+        dim3 grid(tiles, 1, pl.splits);
+        gemm_f32_kernel<BM, BN, MODE, PRO, F16, BVEC, 0, true><<<grid, 256, 0, ctx.stream>>>(p);
+        MH_LAUNCH_CHECK();
+        const int64_t total = int64_t(p.M) * p.N;
+        const unsigned rb = unsigned(std::min<int64_t>(ceil_div(total, 256), 8192));
+        if (epi == GemmEpilogue::Silu)
+            splitk_reduce_kernel<1><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
+        else
+            splitk_reduce_kernel<0><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
+    } else {
+        p.k_split = p.K;
+        const dim3 grid(tiles, unsigned(batch));
+        // The SiLU epilogue is only instantiated for dense operands (the convs never use it).
+        if constexpr (MODE <= kDenseScalar) {
+            if (epi == GemmEpilogue::Silu) {
+                gemm_f32_kernel<BM, BN, MODE, PRO, F16, BVEC, 1, false><<<grid, 256, 0, ctx.stream>>>(p);
+                MH_LAUNCH_CHECK();
+                return;
+            }
+        } else {
+            MH_REQUIRE(epi == GemmEpilogue::None, "conv GEMM: SiLU epilogue not available");
+        }
+        gemm_f32_kernel<BM, BN, MODE, PRO, F16, BVEC, 0, false><<<grid, 256, 0, ctx.stream>>>(p);
+    }
+    MH_LAUNCH_CHECK();
+}
+
+template <int MODE, bool PRO, bool F16, bool BVEC>
+void launch_tiles(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
+    Plan pl = plan_for(p.M, p.N, p.K, int(ceil_div(ctx.cu_count, batch)));
+    // MOEBIUS_HIP_GEMM_PLAN="bm,bn,splits" forces the tiling (tuning and A/B runs),
+    // as MOEBIUS_GEMM selects the CPU engine's GEMM backend (src/engine/gemm.rs:57-60).
+    if (const char *force = std::getenv("MOEBIUS_HIP_GEMM_PLAN")) {
+        int bm = 0, bn = 0, sp = 0;
+        if (std::sscanf(force, "%d,%d,%d", &bm, &bn, &sp) == 3 && (bm == 64 || bm == 128) && (bn == 64 || bn == 128) &&
+            sp >= 1) {
+            const int ktiles = int(ceil_div(p.K, BK));
+            const int per = int(ceil_div(ktiles, sp));
+            pl = Plan{bm, bn, int(ceil_div(ktiles, per)), per * BK};
+        }
+    }
+    if (batch > 1) pl.splits = 1;
+    if (pl.bm == 128 && pl.bn == 128)
+        launch_cfg<128, 128, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
+    else if (pl.bm == 128)
+        launch_cfg<128, 64, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
+    else if (pl.bn == 128)
+        launch_cfg<64, 128, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
+    else
+        launch_cfg<64, 64, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
+}
+
+template <int MODE, bool PRO>
+void launch_b(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi, int batch = 1) {
+    const int esz = wt == kF16 ? 2 : 4;
+    const bool bvec = p.K % 4 == 0 && p.ldb % 4 == 0 && (reinterpret_cast<uintptr_t>(p.b) % (4 * esz)) == 0 &&
+                      (batch == 1 || p.b_bs % 4 == 0);
+    // Vector conv gathers come with vector weight rows (9 * c_in, c_in % 4 == 0);
+    // the scalar gather takes any weight layout. Only those pairs are built.
+    if constexpr (MODE == kConvAligned || MODE == kConvVec) {
+        MH_REQUIRE(bvec, "conv GEMM: weight rows must be 4-element aligned for the vector gather");
+        if (wt == kF16) launch_tiles<MODE, PRO, true, true>(ctx, p, epi, batch);
+        else launch_tiles<MODE, PRO, false, true>(ctx, p, epi, batch);
+    } else if constexpr (MODE == kConvScalar) {
+        if (wt == kF16) launch_tiles<MODE, PRO, true, false>(ctx, p, epi, batch);
+        else launch_tiles<MODE, PRO, false, false>(ctx, p, epi, batch);
+    } else {
+        if (wt == kF16) {
+            if (bvec) launch_tiles<MODE, PRO, true, true>(ctx, p, epi, batch);
+            else launch_tiles<MODE, PRO, true, false>(ctx, p, epi, batch);
+        } else {
+            if (bvec) launch_tiles<MODE, PRO, false, true>(ctx, p, epi, batch);
+            else launch_tiles<MODE, PRO, false, false>(ctx, p, epi, batch);
+        }
+    }
+}
+
+}  // namespace
+}  // namespace gemm
+}  // namespace mh

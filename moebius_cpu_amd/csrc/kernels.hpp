@@ -42,23 +42,36 @@ void group_norm_forward(Context &ctx, const float *x, int n, int h, int w, int c
                         const float *gamma, const float *beta, const float *add, bool silu, float *out);
 void layer_norm(Context &ctx, const float *x, int64_t rows, int c, const float *gamma, const float *beta, float eps,
                 float *out);
+// Per-row (mean, rstd) of LayerNorm for consumers that apply it themselves: stats [rows][2].
+void layer_norm_stats(Context &ctx, const float *x, int64_t rows, int c, float eps, float *stats);
 
 // ---- depthwise (depthwise.hip) ----
+// prologue (optional): GroupNorm affine [+SiLU] applied to in-image inputs as they load.
 void depthwise3x3(Context &ctx, const float *x, int n, int h, int w, int c, const float *weight, const float *bias,
-                  int epilogue, float *out);
+                  int epilogue, float *out, const Affine *prologue = nullptr);
 
 // ---- GEMM-shaped convs (gemm.hip) ----
+// Per item and channel transform of a GEMM residual: res' = [SiLU](res . scale + shift),
+// item = row / rows_per_item (a GroupNorm affine applied to the block input on the fly).
+struct ResidualAffine {
+    const float *scale = nullptr, *shift = nullptr;
+    bool silu = false;
+    int rows_per_item = 0;
+};
+// out = ([res'] + bias) + x . W^T [SiLU] (+ residual2)
 void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void *weight, WeightType wt, int c_out,
-             const float *bias, const float *residual, float *out, GemmEpilogue epi = GemmEpilogue::None);
+             const float *bias, const float *residual, float *out, GemmEpilogue epi = GemmEpilogue::None,
+             const ResidualAffine *raff = nullptr, const float *residual2 = nullptr);
 void conv3x3(Context &ctx, const float *x, int n, int h, int w, int c_in, const void *weight, WeightType wt,
              int c_out, const float *bias, int stride, const int pad[4], bool upsample2x, const Affine *prologue,
              float *out);
 void conv3x3_output_hw(int h, int w, int stride, const int pad[4], bool upsample2x, int *ho, int *wo);
 // C[z] = A[z] . B[z]^T (+ bias) (+ residual[z]) [SiLU] for z < batch, all K-contiguous:
 // A [m][lda], B [n][ldb], C [m][ldc]; *_bs are per-item element offsets.
+// row_group g > 1 stores row m, column n at (m / g) * ldc + n * g + m % g.
 void gemm_nt(Context &ctx, const float *a, int64_t lda, int64_t a_bs, const void *b, WeightType wt, int64_t ldb,
              int64_t b_bs, int m, int n, int k, int batch, const float *bias, const float *residual, float *out,
-             int64_t ldc, int64_t c_bs, GemmEpilogue epi = GemmEpilogue::None);
+             int64_t ldc, int64_t c_bs, GemmEpilogue epi = GemmEpilogue::None, int row_group = 0);
 void im2col_gather(Context &ctx, const float *x, int n, int h, int w, int c, int stride, const int pad[4],
                    bool upsample2x, int64_t first, int64_t count, float *rows);
 void selftest_mfma_f32(Context &ctx, const float *a_host, const float *b_host, float *d_host);
@@ -67,10 +80,13 @@ void selftest_mfma_f32(Context &ctx, const float *a_host, const float *b_host, f
 // keys [nb][rows][k], v [nb][rows][vd] -> lambda_t [nb][vd][k] (transposed lambda_c).
 void softmax_lambda(Context &ctx, const float *keys, const float *v, int nb, int rows, int k, int vd,
                     float *lambda_t);
-// o [nb*hh*ww][8*vd] += bias column + 15x15 taps of v; a [nb*hh*ww][8][226].
-void tap_filter(Context &ctx, const float *a, const float *v, float *o, int nb, int hh, int ww, int vd);
-// o [nb*hw][8*k] += (q . E) . V[branch]; e [hw][10][k]; v_branches [2][10][k].
+// out [nb*hh*ww][8*vd] = (residual +) (yc + bias tap + 15x15 taps of v); a_t [nb*hh*ww][226][8]
+// (heads innermost). out may alias yc or residual.
+void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc, const float *residual, float *out,
+                int nb, int hh, int ww, int vd);
+// out [nb*hw][8*k] = (residual +) (yc + (q . E) . V[branch]); e [hw][10][k]; v_branches [2][10][k].
+// out may alias yc or residual.
 void position_term(Context &ctx, const float *q, const float *e, const float *v_branches, int br0, int nb, int hw,
-                   int k, float *o);
+                   int k, const float *yc, const float *residual, float *out);
 
 }  // namespace mh

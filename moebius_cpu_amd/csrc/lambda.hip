@@ -1,7 +1,7 @@
 // Lambda-layer kernels of the UNet's MixTransformer (src/unet/lambda.rs).
 //
-// softmax_lambda (lambda.rs:452-489): lambda_c[kk][j] = sum_r softmax_r(K)[r][kk] * V[r][j]
-//   1. column maxima of K over rows, per 32-row chunk;
+// softmax_lambda (lambda.rs:322-359): lambda_c[kk][j] = sum_r softmax_r(K)[r][kk] * V[r][j]
+//   1. column maxima of K over rows, per row chunk;
 //   2. per chunk: e = exp(K - colmax) (the reference's Cephes exp), f32 column
 //      sums over the chunk, and the chunk's partial e^T V in f32;
 //   3. finalise: partials summed over chunks in order (f32 for lambda, f64 for
@@ -11,9 +11,14 @@
 // tap_filter (lambda.rs:288-314): per pixel, head and value channel,
 //   o = Yc + A[., 225] then + A[., dy*15+dx] * V[pixel + (dy-7, dx-7)] over the
 //   in-image taps in (dy, dx) order with fused multiply-adds: the reference's
-//   per-element operation order.
+//   per-element operation order. A arrives tap-major ([pixel][226][8], written
+//   that way by the GEMM that makes it) so one thread's heads share each value
+//   load; the block's residual add can be folded into the store.
 // position_term (lambda.rs:406-425): per pixel, B[h][m] = q_h . E[n][m] with
-//   the reference's 8-lane dot, then o_h += B[h][m] * V[m] for m = 0..9.
+//   the reference's 8-lane dot, then o_h += B[h][m] * V[m] for m = 0..9; the
+//   block's residual add can be folded into the store.
+#include <cstdlib>
+
 #include "common.hpp"
 #include "dmath.hpp"
 #include "kernels.hpp"
@@ -21,127 +26,215 @@
 namespace mh {
 namespace {
 
-constexpr int kLamChunk = 32;   // rows per softmax_lambda chunk
 constexpr int kWin = 15, kTaps = 225, kPad = 7, kTapsB = 226;
 constexpr int kHeads = 8, kTokens = 10;
 
-// keys [b][rows][k]; partial max [b][chunks][k]
-__global__ void lambda_colmax_kernel(const float *__restrict__ keys, int rows, int k, int chunks,
-                                     float *__restrict__ pmax) {
+// Rows per softmax_lambda chunk: at most ~400K multiply-adds of e^T V per
+// block and 64 KB of LDS (128 rows at k = vd = 40, 64 at 80, 16 at 160), so the
+// UNet's levels get 16-32 chunks per item and the partials are few to fold.
+int lambda_chunk_rows(int k, int vd) {
+    int ch = 256;
+    while (ch > 8 && (int64_t(ch) * k * vd > 409600 || int64_t(ch) * (k + vd) + k > 16384)) ch >>= 1;
+    return ch;
+}
+
+// Column maxima of keys [b][rows][k] per chunk -> pmax [b][chunks][k].
+// 64 lanes over column quads (k <= 160 -> at most 40), 4 waves over rows.
+__global__ __launch_bounds__(256) void lambda_colmax_kernel(const float *__restrict__ keys, int rows, int k, int ch,
+                                                            int chunks, float *__restrict__ pmax) {
     const int chunk = blockIdx.x, b = blockIdx.y;
-    const float *kb = keys + (size_t(b) * rows + size_t(chunk) * kLamChunk) * k;
-    const int r1 = min(kLamChunk, rows - chunk * kLamChunk);
-    for (int j = threadIdx.x; j < k; j += blockDim.x) {
-        float m = -INFINITY;
-        for (int r = 0; r < r1; ++r) m = fmaxf(m, kb[size_t(r) * k + j]);
-        pmax[(size_t(b) * chunks + chunk) * k + j] = m;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int k4 = k >> 2;
+    const int r0 = chunk * ch, r1 = min(rows, r0 + ch);
+    float4 m = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    if (lane < k4) {
+        const float4 *kb = reinterpret_cast<const float4 *>(keys + size_t(b) * rows * k) + lane;
+        for (int r = r0 + wave; r < r1; r += 4) {
+            const float4 x = kb[size_t(r) * k4];
+            m = make_float4(fmaxf(m.x, x.x), fmaxf(m.y, x.y), fmaxf(m.z, x.z), fmaxf(m.w, x.w));
+        }
+    }
+    __shared__ float4 red[4][64];
+    red[wave][lane] = m;
+    __syncthreads();
+    if (wave == 0 && lane < k4) {
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+            const float4 x = red[w][lane];
+            m = make_float4(fmaxf(m.x, x.x), fmaxf(m.y, x.y), fmaxf(m.z, x.z), fmaxf(m.w, x.w));
+        }
+        reinterpret_cast<float4 *>(pmax + (size_t(b) * chunks + chunk) * k)[lane] = m;
     }
 }
 
-// One block per (chunk, item): e = exp(K - max) into LDS, column sums, partial e^T V.
-// LDS: e [32][k], v [32][vd] with k, vd <= 160.
+// One block per (chunk, item): e = exp(K - max) into LDS, f32 column sums,
+// and the chunk's partial e^T V [k][vd] (rows summed in order with fmaf).
+// Dynamic LDS: e [ch][k], v [ch][vd], max [k].
 __global__ __launch_bounds__(256) void lambda_partial_kernel(const float *__restrict__ keys,
                                                              const float *__restrict__ v, int rows, int k, int vd,
-                                                             int chunks, const float *__restrict__ pmax,
+                                                             int ch, int chunks, const float *__restrict__ pmax,
                                                              float *__restrict__ psum, float *__restrict__ plam) {
-    __shared__ float es[kLamChunk * 160];
-    __shared__ float vs[kLamChunk * 160];
-    __shared__ float mx[160];
+    extern __shared__ float lds[];
+    float *es = lds, *vs = lds + ch * k, *mx = vs + ch * vd;
     const int chunk = blockIdx.x, b = blockIdx.y;
-    const int r0 = chunk * kLamChunk;
-    const int r1 = min(kLamChunk, rows - r0);
-    for (int j = threadIdx.x; j < k; j += blockDim.x) {
+    const int r0 = chunk * ch;
+    const int nr = min(ch, rows - r0);
+    for (int j = threadIdx.x; j < k; j += 256) {
+        const float *pm = pmax + size_t(b) * chunks * k + j;
         float m = -INFINITY;
-        for (int c = 0; c < chunks; ++c) m = fmaxf(m, pmax[(size_t(b) * chunks + c) * k + j]);
+        for (int c = 0; c < chunks; ++c) m = fmaxf(m, pm[size_t(c) * k]);
         mx[j] = m;
     }
     __syncthreads();
     const float *kb = keys + (size_t(b) * rows + r0) * k;
     const float *vb = v + (size_t(b) * rows + r0) * vd;
-    for (int i = threadIdx.x; i < kLamChunk * k; i += blockDim.x) {
-        const int r = i / k, j = i - r * k;
-        es[i] = r < r1 ? ref_exp(kb[size_t(r) * k + j] - mx[j]) : 0.0f;
+    for (int i = threadIdx.x; i < nr * k; i += 256) {
+        const int j = i % k;
+        es[i] = ref_exp(kb[i] - mx[j]);
     }
-    for (int i = threadIdx.x; i < kLamChunk * vd; i += blockDim.x) {
-        const int r = i / vd;
-        vs[i] = r < r1 ? vb[i] : 0.0f;
-    }
+    for (int i = threadIdx.x; i < nr * vd; i += 256) vs[i] = vb[i];
     __syncthreads();
     float *ps = psum + (size_t(b) * chunks + chunk) * k;
-    for (int j = threadIdx.x; j < k; j += blockDim.x) {
+    for (int j = threadIdx.x; j < k; j += 256) {
         float s = 0.0f;
-        for (int r = 0; r < r1; ++r) s += es[r * k + j];
+        for (int r = 0; r < nr; ++r) s += es[r * k + j];
         ps[j] = s;
     }
-    float *pl = plam + (size_t(b) * chunks + chunk) * size_t(k) * vd;
-    for (int i = threadIdx.x; i < k * vd; i += blockDim.x) {
-        const int kk = i / vd, j = i - kk * vd;
-        float acc = 0.0f;
-        for (int r = 0; r < r1; ++r) acc = __builtin_fmaf(es[r * k + kk], vs[r * vd + j], acc);
-        pl[i] = acc;
-    }
-}
-
-// out_t [b][vd][k] = (sum_c plam[b][c][kk][j]) * (f32)(1 / sum_c psum[b][c][kk]).
-__global__ void lambda_finalize_kernel(const float *__restrict__ psum, const float *__restrict__ plam, int k, int vd,
-                                       int chunks, int nb, float *__restrict__ out_t) {
-    const int64_t total = int64_t(nb) * k * vd;
-    for (int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; e < total; e += int64_t(gridDim.x) * blockDim.x) {
-        const int b = int(e / (int64_t(k) * vd));
-        const int i = int(e - int64_t(b) * k * vd);
-        const int kk = i / vd, j = i - kk * vd;
-        float acc = 0.0f;
-        double s = 0.0;
-        for (int c = 0; c < chunks; ++c) {
-            acc += plam[(size_t(b) * chunks + c) * size_t(k) * vd + i];
-            s += double(psum[(size_t(b) * chunks + c) * k + kk]);
+    // e^T V: task (kk, j quad); vd % 4 == 0.
+    const int vq = vd >> 2;
+    float4 *pl = reinterpret_cast<float4 *>(plam + (size_t(b) * chunks + chunk) * size_t(k) * vd);
+    for (int t = threadIdx.x; t < k * vq; t += 256) {
+        const int kk = t / vq, jq = t - kk * vq;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 *vr = reinterpret_cast<const float4 *>(vs) + jq;
+        for (int r = 0; r < nr; ++r) {
+            const float e = es[r * k + kk];
+            const float4 x = vr[r * vq];
+            acc.x = __builtin_fmaf(e, x.x, acc.x);
+            acc.y = __builtin_fmaf(e, x.y, acc.y);
+            acc.z = __builtin_fmaf(e, x.z, acc.z);
+            acc.w = __builtin_fmaf(e, x.w, acc.w);
         }
-        const float inv = float(1.0 / s);
-        out_t[(size_t(b) * vd + j) * k + kk] = acc * inv;
+        pl[t] = acc;
     }
 }
 
-// One thread per (pixel, head, 4 value channels). a: [b*hw][8][226]; v: [b*hw][vd];
-// o: [b*hw][8*vd], holding Yc on entry.
-__global__ __launch_bounds__(256) void tap_filter_kernel(const float *__restrict__ a, const float *__restrict__ v,
-                                                         float *__restrict__ o, int nb, int hh, int ww, int vd) {
+// out_t [b][vd][k] = (sum over chunks of plam[b][c][kk][j]) * (f32)(1 / sum over
+// chunks of psum[b][c][kk]); chunk partials folded in chunk order, the sums in f64.
+__global__ __launch_bounds__(256) void lambda_finalize_kernel(const float *__restrict__ psum,
+                                                              const float *__restrict__ plam, int k, int vd,
+                                                              int chunks, int nb, float *__restrict__ out_t) {
+    const int64_t total = int64_t(nb) * k * vd;
+    const int64_t e = blockIdx.x * int64_t(256) + threadIdx.x;
+    if (e >= total) return;
+    const int b = int(e / (int64_t(k) * vd));
+    const int i = int(e - int64_t(b) * k * vd);
+    const int kk = i / vd, j = i - kk * vd;
+    const float *pl = plam + size_t(b) * chunks * size_t(k) * vd + i;
+    const float *ps = psum + size_t(b) * chunks * k + kk;
+    float acc = 0.0f;
+    double s = 0.0;
+#pragma unroll 4
+    for (int c = 0; c < chunks; ++c) {
+        acc += pl[size_t(c) * k * vd];
+        s += double(ps[size_t(c) * k]);
+    }
+    const float inv = float(1.0 / s);
+    out_t[(size_t(b) * vd + j) * k + kk] = acc * inv;
+}
+
+// HG heads' coefficients of one tap: a_t row [226][8] (heads innermost).
+template <int HG>
+__device__ __forceinline__ void load_heads(const float *__restrict__ p, float (&c)[HG]) {
+    if constexpr (HG >= 4) {
+#pragma unroll
+        for (int i = 0; i < HG; i += 4) {
+            const float4 t = *reinterpret_cast<const float4 *>(p + i);
+            c[i] = t.x;
+            c[i + 1] = t.y;
+            c[i + 2] = t.z;
+            c[i + 3] = t.w;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < HG; ++i) c[i] = p[i];
+    }
+}
+
+// One thread per (pixel, head group of HG, 4 value channels): the value taps
+// are loaded once and used for HG heads; the HG coefficients of a tap are one
+// or two 16-byte loads from the tap-major a_t. Per output element the
+// operations are the reference's: (yc + bias) then one fused multiply-add per
+// in-image tap in (dy, dx) order; then residual + u when a residual is given.
+template <int HG>
+__global__ __launch_bounds__(256) void tap_filter_kernel(const float *__restrict__ a_t, const float *__restrict__ v,
+                                                         const float *yc, const float *res, float *out, int nb,
+                                                         int hh, int ww, int vd) {
+    constexpr int NG = kHeads / HG;
     const int v4 = vd >> 2;
-    const int64_t total = int64_t(nb) * hh * ww * kHeads * v4;
+    const int64_t total = int64_t(nb) * hh * ww * NG * v4;
     const int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x;
     if (t >= total) return;
     const int jq = int(t % v4);
-    const int64_t nh = t / v4;
-    const int h = int(nh % kHeads);
-    const int64_t pix = nh / kHeads;  // b*hw + y*ww + x
+    const int64_t r = t / v4;
+    const int hg = int(r % NG);
+    const int64_t pix = r / NG;  // b*hw + y*ww + x
     const int hw = hh * ww;
     const int b = int(pix / hw);
     const int rem = int(pix - int64_t(b) * hw);
     const int y = rem / ww, x = rem - (rem / ww) * ww;
-    const float *ap = a + (pix * kHeads + h) * kTapsB;
-    float4 *op = reinterpret_cast<float4 *>(o + pix * (kHeads * vd) + h * vd) + jq;
-    float4 acc = *op;
-    const float bias = ap[kTaps];
-    acc.x += bias;
-    acc.y += bias;
-    acc.z += bias;
-    acc.w += bias;
-    const float4 *vb = reinterpret_cast<const float4 *>(v + int64_t(b) * hw * vd);
-    const int kx0 = max(kPad - x, 0), kx1 = min(kWin, ww + kPad - x);
-    for (int ky = 0; ky < kWin; ++ky) {
-        const int iy = y + ky - kPad;
-        if (iy < 0 || iy >= hh) continue;
-        const float4 *vr = vb + (int64_t(iy) * ww + x - kPad) * v4 + jq;
-        const float *ar = ap + ky * kWin;
-        for (int kx = kx0; kx < kx1; ++kx) {
-            const float c = ar[kx];
-            const float4 s = vr[int64_t(kx) * v4];
-            acc.x = __builtin_fmaf(c, s.x, acc.x);
-            acc.y = __builtin_fmaf(c, s.y, acc.y);
-            acc.z = __builtin_fmaf(c, s.z, acc.z);
-            acc.w = __builtin_fmaf(c, s.w, acc.w);
+    const float *ap = a_t + pix * (kTapsB * kHeads) + hg * HG;
+    const int64_t obase = pix * (kHeads * v4) + int64_t(hg) * HG * v4 + jq;  // in float4 units
+    float4 acc[HG];
+    {
+        float bias[HG];
+        load_heads<HG>(ap + kTaps * kHeads, bias);
+#pragma unroll
+        for (int i = 0; i < HG; ++i) {
+            const float4 c = reinterpret_cast<const float4 *>(yc)[obase + i * v4];
+            acc[i] = make_float4(c.x + bias[i], c.y + bias[i], c.z + bias[i], c.w + bias[i]);
         }
     }
-    *op = acc;
+    const float4 *vb = reinterpret_cast<const float4 *>(v + int64_t(b) * hw * vd) + jq;
+    const int kx0 = max(kPad - x, 0), kx1 = min(kWin, ww + kPad - x);
+    const int ky0 = max(kPad - y, 0), ky1 = min(kWin, hh + kPad - y);
+    // A whole 15-tap row is loaded before any of it is used (the loads of a
+    // thread overlap instead of queueing one tap at a time); columns outside the
+    // image are loaded from a clamped, valid address and skipped in the sum.
+    for (int ky = ky0; ky < ky1; ++ky) {
+        const float4 *vr = vb + int64_t(y + ky - kPad) * ww * v4;
+        const float *ar = ap + (ky * kWin) * kHeads;
+        float c[kWin][HG];
+        float4 s[kWin];
+#pragma unroll
+        for (int kx = 0; kx < kWin; ++kx) {
+            const int ix = min(max(x + kx - kPad, 0), ww - 1);
+            s[kx] = vr[int64_t(ix) * v4];
+            load_heads<HG>(ar + kx * kHeads, c[kx]);
+        }
+#pragma unroll
+        for (int kx = 0; kx < kWin; ++kx) {
+            if (kx >= kx0 && kx < kx1) {
+#pragma unroll
+                for (int i = 0; i < HG; ++i) {
+                    acc[i].x = __builtin_fmaf(c[kx][i], s[kx].x, acc[i].x);
+                    acc[i].y = __builtin_fmaf(c[kx][i], s[kx].y, acc[i].y);
+                    acc[i].z = __builtin_fmaf(c[kx][i], s[kx].z, acc[i].z);
+                    acc[i].w = __builtin_fmaf(c[kx][i], s[kx].w, acc[i].w);
+                }
+            }
+        }
+    }
+    float4 *o4 = reinterpret_cast<float4 *>(out);
+#pragma unroll
+    for (int i = 0; i < HG; ++i) {
+        float4 u = acc[i];
+        if (res) {
+            const float4 h = reinterpret_cast<const float4 *>(res)[obase + i * v4];
+            u = make_float4(h.x + u.x, h.y + u.y, h.z + u.z, h.w + u.w);
+        }
+        o4[obase + i * v4] = u;
+    }
 }
 
 // 8-lane dot of src/unet/lambda.rs:429-439 (k a multiple of 8).
@@ -165,11 +258,11 @@ __device__ __forceinline__ float dot8_ref(const float *__restrict__ a, const flo
     return s + 0.0f;
 }
 
-// Block of 256 threads handles 8 pixels. q, o: [b*hw][8*k]; e: [hw][10][k];
-// vb: [2][10][k] (per branch); branch of item b = br0 + b.
+// Block of 256 threads handles 8 pixels. q, yc, res, out: [b*hw][8*k]; e: [hw][10][k];
+// vb: [2][10][k] (per branch); branch of item b = br0 + b. out may alias yc or res.
 __global__ __launch_bounds__(256) void position_term_kernel(const float *__restrict__ q, const float *__restrict__ e,
                                                             const float *__restrict__ vbr, int br0, int nb, int hw,
-                                                            int k, float *__restrict__ o) {
+                                                            int k, const float *yc, const float *res, float *out) {
     constexpr int P = 8;
     __shared__ float bm[P][kHeads][kTokens];
     const int64_t pix0 = int64_t(blockIdx.x) * P;
@@ -187,17 +280,35 @@ __global__ __launch_bounds__(256) void position_term_kernel(const float *__restr
         bm[p][h][m] = val;
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < P * c; i += 256) {
-        const int p = i / c, hj = i - p * c;
-        const int h = hj / k, j = hj - h * k;
+    // (pixel, head, 4 channels) per step: float4 loads and stores, each
+    // component summed in the reference's order.
+    const int k4 = k >> 2;
+    const float4 *yc4 = reinterpret_cast<const float4 *>(yc);
+    const float4 *res4 = reinterpret_cast<const float4 *>(res);
+    float4 *out4 = reinterpret_cast<float4 *>(out);
+    for (int i = threadIdx.x; i < P * kHeads * k4; i += 256) {
+        const int p = i / (kHeads * k4), hq = i - p * (kHeads * k4);
+        const int h = hq / k4, jq = hq - h * k4;
         const int64_t pix = pix0 + p;
         if (pix >= npix) continue;
         const int b = int(pix / hw);
-        const float *vm = vbr + int64_t(br0 + b) * kTokens * k;
-        float acc = o[pix * c + hj];
+        const float4 *vm = reinterpret_cast<const float4 *>(vbr + int64_t(br0 + b) * kTokens * k) + jq;
+        const int64_t o = pix * (kHeads * k4) + hq;
+        float4 acc = yc4[o];
 #pragma unroll
-        for (int m = 0; m < kTokens; ++m) acc = __builtin_fmaf(bm[p][h][m], vm[m * k + j], acc);
-        o[pix * c + hj] = acc;
+        for (int m = 0; m < kTokens; ++m) {
+            const float w = bm[p][h][m];
+            const float4 x = vm[m * k4];
+            acc.x = __builtin_fmaf(w, x.x, acc.x);
+            acc.y = __builtin_fmaf(w, x.y, acc.y);
+            acc.z = __builtin_fmaf(w, x.z, acc.z);
+            acc.w = __builtin_fmaf(w, x.w, acc.w);
+        }
+        if (res) {
+            const float4 r = res4[o];
+            acc = make_float4(r.x + acc.x, r.y + acc.y, r.z + acc.z, r.w + acc.w);
+        }
+        out4[o] = acc;
     }
 }
 
@@ -206,15 +317,20 @@ __global__ __launch_bounds__(256) void position_term_kernel(const float *__restr
 void softmax_lambda(Context &ctx, const float *keys, const float *v, int nb, int rows, int k, int vd,
                     float *lambda_t) {
     MH_REQUIRE(k > 0 && k <= 160 && vd > 0 && vd <= 160, "softmax_lambda: widths above 160 are not supported");
+    MH_REQUIRE(k % 4 == 0 && vd % 4 == 0, "softmax_lambda: widths must be multiples of 4");
+    MH_REQUIRE(aligned16(keys) && aligned16(v), "softmax_lambda: keys and v must be 16-byte aligned");
     MH_REQUIRE(rows > 0 && nb > 0, "softmax_lambda: empty input");
-    const int chunks = int(ceil_div(rows, kLamChunk));
+    const int ch = lambda_chunk_rows(k, vd);
+    const int chunks = int(ceil_div(rows, ch));
     const size_t pm = size_t(nb) * chunks * k;
     const size_t pl = size_t(nb) * chunks * size_t(k) * vd;
     float *ws = static_cast<float *>(ctx.ws.get((2 * pm + pl) * sizeof(float), ctx.stream));
     float *pmax = ws, *psum = ws + pm, *plam = ws + 2 * pm;
-    lambda_colmax_kernel<<<dim3(chunks, nb), 64, 0, ctx.stream>>>(keys, rows, k, chunks, pmax);
+    lambda_colmax_kernel<<<dim3(chunks, nb), 256, 0, ctx.stream>>>(keys, rows, k, ch, chunks, pmax);
     MH_LAUNCH_CHECK();
-    lambda_partial_kernel<<<dim3(chunks, nb), 256, 0, ctx.stream>>>(keys, v, rows, k, vd, chunks, pmax, psum, plam);
+    const size_t lds = (size_t(ch) * (k + vd) + k) * sizeof(float);
+    lambda_partial_kernel<<<dim3(chunks, nb), 256, lds, ctx.stream>>>(keys, v, rows, k, vd, ch, chunks, pmax, psum,
+                                                                      plam);
     MH_LAUNCH_CHECK();
     const int64_t total = int64_t(nb) * k * vd;
     lambda_finalize_kernel<<<unsigned(ceil_div(total, 256)), 256, 0, ctx.stream>>>(psum, plam, k, vd, chunks, nb,
@@ -222,23 +338,45 @@ void softmax_lambda(Context &ctx, const float *keys, const float *v, int nb, int
     MH_LAUNCH_CHECK();
 }
 
-void tap_filter(Context &ctx, const float *a, const float *v, float *o, int nb, int hh, int ww, int vd) {
+void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc, const float *residual, float *out,
+                int nb, int hh, int ww, int vd) {
     MH_REQUIRE(vd % 4 == 0, "tap_filter: value width must be a multiple of 4");
-    MH_REQUIRE(aligned16(v) && aligned16(o), "tap_filter: v and o must be 16-byte aligned");
-    const int64_t total = int64_t(nb) * hh * ww * kHeads * (vd / 4);
-    if (total == 0) return;
-    tap_filter_kernel<<<unsigned(ceil_div(total, 256)), 256, 0, ctx.stream>>>(a, v, o, nb, hh, ww, vd);
+    MH_REQUIRE(aligned16(a_t) && aligned16(v) && aligned16(yc) && aligned16(residual) && aligned16(out),
+               "tap_filter: buffers must be 16-byte aligned");
+    const int64_t pix = int64_t(nb) * hh * ww;
+    if (pix == 0) return;
+    // Heads per thread: the most (value loads shared by more heads) that still
+    // gives the chip about 2048 waves: 4 at 64x64 x 40 channels, 2 at 32x32 x 80,
+    // 1 at 16x16 x 160 (batch 2).
+    const int v4 = vd / 4;
+    int hg = 4;
+    while (hg > 1 && pix * v4 * (kHeads / hg) < 2048 * 64) hg >>= 1;
+    if (const char *f = std::getenv("MOEBIUS_HIP_TAP_HEADS")) {
+        const int want = std::atoi(f);
+        if (want == 1 || want == 2 || want == 4 || want == 8) hg = want;
+    }
+    const int64_t total = pix * (kHeads / hg) * v4;
+    const unsigned blocks = unsigned(ceil_div(total, 256));
+    switch (hg) {
+        case 8: tap_filter_kernel<8><<<blocks, 256, 0, ctx.stream>>>(a_t, v, yc, residual, out, nb, hh, ww, vd); break;
+        case 4: tap_filter_kernel<4><<<blocks, 256, 0, ctx.stream>>>(a_t, v, yc, residual, out, nb, hh, ww, vd); break;
+        case 2: tap_filter_kernel<2><<<blocks, 256, 0, ctx.stream>>>(a_t, v, yc, residual, out, nb, hh, ww, vd); break;
+        default: tap_filter_kernel<1><<<blocks, 256, 0, ctx.stream>>>(a_t, v, yc, residual, out, nb, hh, ww, vd);
+    }
     MH_LAUNCH_CHECK();
 }
 
 void position_term(Context &ctx, const float *q, const float *e, const float *v_branches, int br0, int nb, int hw,
-                   int k, float *o) {
+                   int k, const float *yc, const float *residual, float *out) {
     MH_REQUIRE(k % 8 == 0, "position_term: head width must be a multiple of 8");
-    MH_REQUIRE(aligned16(q) && aligned16(e), "position_term: q and e must be 16-byte aligned");
+    MH_REQUIRE(aligned16(q) && aligned16(e) && aligned16(v_branches) && aligned16(yc) && aligned16(residual) &&
+                   aligned16(out),
+               "position_term: buffers must be 16-byte aligned");
     MH_REQUIRE(br0 >= 0 && br0 + nb <= 2, "position_term: branch out of range");
     const int64_t npix = int64_t(nb) * hw;
     if (npix == 0) return;
-    position_term_kernel<<<unsigned(ceil_div(npix, 8)), 256, 0, ctx.stream>>>(q, e, v_branches, br0, nb, hw, k, o);
+    position_term_kernel<<<unsigned(ceil_div(npix, 8)), 256, 0, ctx.stream>>>(q, e, v_branches, br0, nb, hw, k, yc,
+                                                                             residual, out);
     MH_LAUNCH_CHECK();
 }
 

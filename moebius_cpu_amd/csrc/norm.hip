@@ -2,13 +2,15 @@
 // LayerNorm. Bandwidth-bound; NHWC keeps every access a coalesced run of
 // channels.
 //
-// GroupNorm (src/engine/norm.rs:57-148). Statistics follow the reference's
-// structure: per-channel f32 partial sums of y and y*y (fused) over 256-pixel
-// chunks (norm.rs:20, 73-82), then an f64 fold per group over channels and
-// chunks (norm.rs:83-90), then mean/var/rstd and the per-channel scale/shift in
-// f64 (norm.rs:93-101). One launch does it all: each block reduces a
-// [256 px x 64 ch] tile of one item into per-channel partials, and the last
-// block of the item to finish (device-scope fence + counter) folds them.
+// GroupNorm (src/engine/norm.rs:57-148). Statistics keep the reference's
+// structure: per-channel f32 partial sums of y and y*y (fused) over pixel
+// chunks (norm.rs:73-82), folded per group in f64 over channels and chunks
+// (norm.rs:83-90), then mean/var/rstd and the per-channel scale/shift in f64
+// (norm.rs:93-101). Two launches: gn_partial_kernel reduces [64 px x 64 ch]
+// tiles (thousands of blocks at the UNet/VAE sizes), gn_finalize_kernel folds
+// one (item, group) per block with a fixed-order tree, so results are
+// deterministic. The apply pass is a separate kernel, or is fused into the
+// consumer (the depthwise and GEMM prologues) with the scale/shift produced here.
 #include "common.hpp"
 #include "dmath.hpp"
 #include "kernels.hpp"
@@ -16,22 +18,22 @@
 namespace mh {
 namespace {
 
-constexpr int kGnChunk = 256;  // pixels per statistics chunk (norm.rs:20)
 constexpr int kGnTileC = 64;   // channels per block: 16 lanes x float4
 constexpr int kGnRows = 16;    // pixel rows per block pass
 
-__device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+// Pixels per statistics chunk: 64, doubled until the partials grid is at most
+// ~4096 blocks, so small maps get many blocks and 512x512 maps moderate ones.
+int gn_chunk_px(int n, int hw, int c) {
+    const int64_t ctiles = ceil_div(c, kGnTileC);
+    int chunk = 64;
+    while (chunk < hw && ceil_div(hw, chunk) * ctiles * n > 4096) chunk *= 2;
+    return chunk;
 }
 
-__global__ __launch_bounds__(256) void gn_stats_kernel(const float *__restrict__ x, const float *__restrict__ add,
-                                                       int hw, int c, int nchunks, int nctiles, int groups,
-                                                       float eps, const float *__restrict__ gamma,
-                                                       const float *__restrict__ beta, float *__restrict__ part,
-                                                       unsigned int *counters, float *__restrict__ scale,
-                                                       float *__restrict__ shift) {
+// part [n][chunks][c][2] = per-channel (sum y, sum y*y) over the chunk, y = x (+ add).
+__global__ __launch_bounds__(256) void gn_partial_kernel(const float *__restrict__ x, const float *__restrict__ add,
+                                                         int hw, int c, int chunk_px, int nchunks,
+                                                         float *__restrict__ part) {
     const int chunk = blockIdx.x, ct = blockIdx.y, b = blockIdx.z;
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
     const int c0 = ct * kGnTileC + tx * 4;
@@ -40,8 +42,9 @@ __global__ __launch_bounds__(256) void gn_stats_kernel(const float *__restrict__
         float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
         if (add) a = *reinterpret_cast<const float4 *>(add + size_t(b) * c + c0);
         const float *xb = x + size_t(b) * hw * c + c0;
-        const int p1 = min(hw, (chunk + 1) * kGnChunk);
-        for (int p = chunk * kGnChunk + ty; p < p1; p += kGnRows) {
+        const int p1 = min(hw, (chunk + 1) * chunk_px);
+#pragma unroll 4
+        for (int p = chunk * chunk_px + ty; p < p1; p += kGnRows) {
             float4 v = *reinterpret_cast<const float4 *>(xb + size_t(p) * c);
             if (add) {
                 v.x = v.x + a.x;
@@ -79,48 +82,87 @@ __global__ __launch_bounds__(256) void gn_stats_kernel(const float *__restrict__
         *reinterpret_cast<float4 *>(dst) = make_float4(s.x, q.x, s.y, q.y);
         *reinterpret_cast<float4 *>(dst + 4) = make_float4(s.z, q.z, s.w, q.w);
     }
-    // Completion: the last block of item b folds all partials of the item.
-    __threadfence();
-    __syncthreads();
-    __shared__ bool last;
-    if (threadIdx.x == 0) {
-        const unsigned int prev = atomicAdd(&counters[b], 1u);
-        last = prev == unsigned(nchunks * nctiles - 1);
-    }
-    __syncthreads();
-    if (!last) return;
-    __threadfence();
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int cg = c / groups;
-    const int total = nchunks * cg;
-    const double count = double(hw) * double(cg);
-    const float *pb = part + size_t(b) * nchunks * c * 2;
-    for (int g = wave; g < groups; g += 4) {
-        double ds = 0.0, dq = 0.0;
-        for (int i = lane; i < total; i += 64) {
-            const int ch = i / cg, j = i - ch * cg;
-            const float *e = pb + (size_t(ch) * c + g * cg + j) * 2;
-            ds += double(e[0]);
-            dq += double(e[1]);
-        }
-        ds = wave_sum(ds);
-        dq = wave_sum(dq);
-        const double mean = ds / count;
-        const double var = fmax(dq / count - mean * mean, 0.0);
-        const double rstd = 1.0 / sqrt(var + double(eps));
-        for (int j = lane; j < cg; j += 64) {
-            const int ch = g * cg + j;
-            const double sc = rstd * double(gamma[ch]);
-            const double pre = add ? double(add[size_t(b) * c + ch]) : 0.0;
-            scale[size_t(b) * c + ch] = float(sc);
-            shift[size_t(b) * c + ch] = float(double(beta[ch]) + (pre - mean) * sc);
-        }
-    }
-    if (threadIdx.x == 0) counters[b] = 0u;
 }
 
-// out = [SiLU](x . scale + shift), per item b = blockIdx.y; each block handles a
-// contiguous run of float4s of its item. c4 = c/4 quads per pixel.
+// One block per (group, item): f64 fold of the group's partials, then scale/shift.
+__global__ __launch_bounds__(256) void gn_finalize_kernel(const float *__restrict__ part, const float *__restrict__ add,
+                                                          int hw, int c, int nchunks, int groups, float eps,
+                                                          const float *__restrict__ gamma,
+                                                          const float *__restrict__ beta, float *__restrict__ scale,
+                                                          float *__restrict__ shift) {
+    const int g = blockIdx.x, b = blockIdx.y;
+    const int cg = c / groups;
+    const int total = nchunks * cg;
+    const float *pb = part + size_t(b) * nchunks * c * 2 + size_t(g) * cg * 2;
+    double ds = 0.0, dq = 0.0;
+    for (int i = threadIdx.x; i < total; i += 256) {
+        const int ch = i / cg, j = i - ch * cg;
+        const float2 e = *reinterpret_cast<const float2 *>(pb + (size_t(ch) * c + j) * 2);
+        ds += double(e.x);
+        dq += double(e.y);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        ds += __shfl_xor(ds, off, 64);
+        dq += __shfl_xor(dq, off, 64);
+    }
+    __shared__ double red[2][4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        red[0][wave] = ds;
+        red[1][wave] = dq;
+    }
+    __syncthreads();
+    const double sum = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+    const double sumsq = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+    const double count = double(hw) * double(cg);
+    const double mean = sum / count;
+    const double var = fmax(sumsq / count - mean * mean, 0.0);
+    const double rstd = 1.0 / sqrt(var + double(eps));
+    for (int j = threadIdx.x; j < cg; j += 256) {
+        const int ch = g * cg + j;
+        const double sc = rstd * double(gamma[ch]);
+        const double pre = add ? double(add[size_t(b) * c + ch]) : 0.0;
+        scale[size_t(b) * c + ch] = float(sc);
+        shift[size_t(b) * c + ch] = float(double(beta[ch]) + (pre - mean) * sc);
+    }
+}
+
+// LayerNorm row statistics (src/engine/norm.rs:151-173) for a consumer that
+// applies ((v - mean) * rstd) * gamma + beta itself: stats [rows][2] = (mean, rstd).
+template <int MAXV>
+__global__ __launch_bounds__(256) void ln_stats_kernel(const float *__restrict__ x, int64_t rows, int c, float eps,
+                                                       float2 *__restrict__ stats) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int c4 = c >> 2;
+    const float4 *src = reinterpret_cast<const float4 *>(x + row * c);
+    float4 v[MAXV];
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) {
+        const int q = lane + 64 * i;
+        v[i] = q < c4 ? src[q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        s += (v[i].x + v[i].y) + (v[i].z + v[i].w);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    const float mean = s / float(c);
+    float vs = 0.f;
+#pragma unroll
+    for (int i = 0; i < MAXV; ++i) {
+        const int q = lane + 64 * i;
+        if (q < c4) {
+            const float a = v[i].x - mean, b = v[i].y - mean, cc = v[i].z - mean, d = v[i].w - mean;
+            vs += (a * a + b * b) + (cc * cc + d * d);
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) vs += __shfl_xor(vs, off, 64);
+    if (lane == 0) stats[row] = make_float2(mean, 1.0f / sqrtf(vs / float(c) + eps));
+}
+
 template <int ITER>
 __global__ __launch_bounds__(256) void affine_apply_kernel(const float4 *__restrict__ x,
                                                            const float4 *__restrict__ scale,
@@ -257,13 +299,29 @@ void group_norm_affine(Context &ctx, const float *x, int n, int h, int w, int c,
     MH_REQUIRE(n > 0 && h > 0 && w > 0, "GroupNorm: empty tensor");
     MH_REQUIRE(aligned16(x) && aligned16(add), "GroupNorm: x and add must be 16-byte aligned");
     const int hw = h * w;
-    const int nchunks = int(ceil_div(hw, kGnChunk));
+    const int chunk_px = gn_chunk_px(n, hw, c);
+    const int nchunks = int(ceil_div(hw, chunk_px));
     const int nctiles = int(ceil_div(c, kGnTileC));
     float *part = static_cast<float *>(ctx.ws.get(size_t(n) * nchunks * c * 2 * sizeof(float), ctx.stream));
-    unsigned int *ctr = ctx.counter_block(n);
-    dim3 grid(nchunks, nctiles, n);
-    gn_stats_kernel<<<grid, 256, 0, ctx.stream>>>(x, add, hw, c, nchunks, nctiles, groups, eps, gamma, beta, part,
-                                                  ctr, scale, shift);
+    gn_partial_kernel<<<dim3(nchunks, nctiles, n), 256, 0, ctx.stream>>>(x, add, hw, c, chunk_px, nchunks, part);
+    MH_LAUNCH_CHECK();
+    gn_finalize_kernel<<<dim3(groups, n), 256, 0, ctx.stream>>>(part, add, hw, c, nchunks, groups, eps, gamma, beta,
+                                                                scale, shift);
+    MH_LAUNCH_CHECK();
+}
+
+void layer_norm_stats(Context &ctx, const float *x, int64_t rows, int c, float eps, float *stats) {
+    MH_REQUIRE(c % 4 == 0 && c <= 1280 && aligned16(x), "LayerNorm stats: channels must be a multiple of 4, <= 1280");
+    if (rows == 0) return;
+    const unsigned blocks = unsigned(ceil_div(rows, 4));
+    float2 *st = reinterpret_cast<float2 *>(stats);
+    const int c4 = c / 4;
+    if (c4 <= 64)
+        ln_stats_kernel<1><<<blocks, 256, 0, ctx.stream>>>(x, rows, c, eps, st);
+    else if (c4 <= 128)
+        ln_stats_kernel<2><<<blocks, 256, 0, ctx.stream>>>(x, rows, c, eps, st);
+    else
+        ln_stats_kernel<5><<<blocks, 256, 0, ctx.stream>>>(x, rows, c, eps, st);
     MH_LAUNCH_CHECK();
 }
 
@@ -290,7 +348,7 @@ void group_norm_forward(Context &ctx, const float *x, int n, int h, int w, int c
                         const float *gamma, const float *beta, const float *add, bool silu, float *out) {
     // scale/shift live in the tail of the workspace's partial block.
     const size_t part_bytes =
-        size_t(n) * ceil_div(int64_t(h) * w, kGnChunk) * c * 2 * sizeof(float);
+        size_t(n) * ceil_div(int64_t(h) * w, gn_chunk_px(n, h * w, c)) * c * 2 * sizeof(float);
     const size_t aff_off = (part_bytes + 255) & ~size_t(255);
     char *ws = static_cast<char *>(ctx.ws.get(aff_off + size_t(n) * c * 2 * sizeof(float), ctx.stream));
     float *scale = reinterpret_cast<float *>(ws + aff_off);

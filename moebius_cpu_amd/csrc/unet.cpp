@@ -146,6 +146,12 @@ struct GN {
         group_norm_forward(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, eps, g, b, add, silu, out.p);
         return out;
     }
+    // Statistics only: [scale | shift], each [n * c], for a consumer that applies them.
+    float *affine(Env &e, const DT &x, const float *add) const {
+        float *ss = e.pool.floats(int64_t(2) * x.n * x.c);
+        group_norm_affine(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, eps, g, b, add, ss, ss + int64_t(x.n) * x.c);
+        return ss;
+    }
 };
 
 struct LNp {
@@ -174,10 +180,27 @@ struct DwConv2d {
         dwb = W.get(p + ".conv_dw.bias", ci, false).f();
         pw.load(W, p + ".conv_pw", ci, co, true);
     }
-    DT fwd(Env &e, const DT &x) const {
+    // gn: [scale | shift] of a GroupNorm + SiLU whose output is this conv's input;
+    // it is applied as the depthwise loads x and to the skip, never stored.
+    // res2: added last (the resnet's shortcut). out: caller's buffer or a new tensor.
+    DT fwd(Env &e, const DT &x, const float *gn = nullptr, const float *res2 = nullptr, float *out_p = nullptr) const {
         DT mid = e.pool.tensor(x.n, x.h, x.w, x.c);
-        depthwise3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, dw, dwb, 1, mid.p);
-        DT out = pw.fwd(e, mid, ci == co ? &x : nullptr);
+        Affine pro;
+        if (gn) {
+            pro.scale = gn;
+            pro.shift = gn + int64_t(x.n) * x.c;
+            pro.silu = true;
+        }
+        depthwise3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, dw, dwb, 1, mid.p, gn ? &pro : nullptr);
+        DT out = out_p ? DT{out_p, x.n, x.h, x.w, co} : e.pool.tensor(x.n, x.h, x.w, co);
+        ResidualAffine ra;
+        ra.scale = pro.scale;
+        ra.shift = pro.shift;
+        ra.silu = true;
+        ra.rows_per_item = x.h * x.w;
+        const bool skip = ci == co;
+        conv1x1(e.ctx, mid.p, mid.px(), ci, pw.w.p, pw.w.wt, co, pw.b, skip ? x.p : nullptr, out.p,
+                GemmEpilogue::None, skip && gn ? &ra : nullptr, res2);
         e.pool.recycle(mid);
         return out;
     }
@@ -201,24 +224,23 @@ struct DwResnet {
         if (has_shortcut) shortcut.load(W, p + ".conv_shortcut", ci, co, true);
     }
     // temb_silu: [n, 1280] = SiLU(temb), shared by every resnet of the step.
+    // The GroupNorm outputs are never stored: each norm's scale/shift is applied
+    // inside the depthwise conv that reads it and to the DwConv2d skip, and the
+    // shortcut (or x) is added in conv2's pointwise epilogue.
     DT fwd(Env &e, const DT &x, const float *temb_silu) const {
-        DT a = norm1.fwd(e, x, nullptr, true);
-        DT b = conv1.fwd(e, a);
-        e.pool.recycle(a);
+        float *gn1 = norm1.affine(e, x, nullptr);
+        DT b = conv1.fwd(e, x, gn1);
+        e.pool.recycle(gn1);
         float *tp = e.pool.floats(int64_t(x.n) * co);
         temb_proj.fwd(e, temb_silu, x.n, tp);
-        a = norm2.fwd(e, b, tp, true);
+        float *gn2 = norm2.affine(e, b, tp);
         e.pool.recycle(tp);
+        DT s;
+        if (has_shortcut) s = shortcut.fwd(e, x);
+        DT out = conv2.fwd(e, b, gn2, has_shortcut ? s.p : x.p);
+        if (has_shortcut) e.pool.recycle(s);
+        e.pool.recycle(gn2);
         e.pool.recycle(b);
-        DT out = conv2.fwd(e, a);
-        e.pool.recycle(a);
-        if (has_shortcut) {
-            DT s = shortcut.fwd(e, x);
-            add_inplace(e.ctx, out.p, s.p, out.numel());
-            e.pool.recycle(s);
-        } else {
-            add_inplace(e.ctx, out.p, x.p, out.numel());
-        }
         return out;
     }
 };
@@ -249,7 +271,8 @@ struct SelfLambda {
         if (w_aug_t) (void)hipFree(w_aug_t);
         w_aug_t = nullptr;
     }
-    DT fwd(Env &e, const DT &x) const {
+    // h [x.px()][c] += SelfLambda(x): the block's residual add is folded into the tap filter.
+    void fwd_add(Env &e, const DT &x, float *h) const {
         const int hw = x.h * x.w;
         DT q = to_q.fwd(e, x);
         DT kt = to_k.fwd(e, x);
@@ -257,20 +280,20 @@ struct SelfLambda {
         float *lam_t = e.pool.floats(int64_t(x.n) * k * k);
         softmax_lambda(e.ctx, kt.p, vt.p, x.n, hw, k, k, lam_t);
         e.pool.recycle(kt);
-        DT out = e.pool.tensor(x.n, x.h, x.w, c);
+        DT yc = e.pool.tensor(x.n, x.h, x.w, c);
         // Yc = Q . lambda_c per item, Q viewed as [(hw*8) x k].
         gemm_nt(e.ctx, q.p, k, int64_t(hw) * c, lam_t, kF32, k, int64_t(k) * k, hw * HEADS, k, k, x.n, nullptr,
-                nullptr, out.p, k, int64_t(hw) * c);
+                nullptr, yc.p, k, int64_t(hw) * c);
         e.pool.recycle(lam_t);
-        // A = Q . W_aug over every pixel and head of the batch, then the tap filter.
+        // A = Q . W_aug over every pixel and head of the batch, stored [pixel][tap][head].
         float *a = e.pool.floats(x.px() * HEADS * TAPS_B);
         gemm_nt(e.ctx, q.p, k, 0, w_aug_t, kF32, k, 0, int(x.px() * HEADS), TAPS_B, k, 1, nullptr, nullptr, a,
-                TAPS_B, 0);
-        tap_filter(e.ctx, a, vt.p, out.p, x.n, x.h, x.w, k);
+                int64_t(TAPS_B) * HEADS, 0, GemmEpilogue::None, HEADS);
+        tap_filter(e.ctx, a, vt.p, yc.p, h, h, x.n, x.h, x.w, k);
         e.pool.recycle(a);
+        e.pool.recycle(yc);
         e.pool.recycle(q);
         e.pool.recycle(vt);
-        return out;
     }
 };
 
@@ -311,16 +334,17 @@ struct CrossLambda {
         if (v) (void)hipFree(v);
         lambda_t = v = nullptr;
     }
-    DT fwd(Env &env, const DT &x, int br0) const {
+    // h [x.px()][c] += CrossLambda(x): the residual add is folded into the position term.
+    void fwd_add(Env &env, const DT &x, int br0, float *h) const {
         const int hw = x.h * x.w;
         if (hw != n) fail(kInvalidArgument, "CrossLambda input size does not match the position table");
         DT q = to_q.fwd(env, x);
-        DT out = env.pool.tensor(x.n, x.h, x.w, c);
+        DT yc = env.pool.tensor(x.n, x.h, x.w, c);
         gemm_nt(env.ctx, q.p, k, int64_t(hw) * c, lambda_t + int64_t(br0) * k * k, kF32, k, int64_t(k) * k,
-                hw * HEADS, k, k, x.n, nullptr, nullptr, out.p, k, int64_t(hw) * c);
-        position_term(env.ctx, q.p, e, v, br0, x.n, hw, k, out.p);
+                hw * HEADS, k, k, x.n, nullptr, nullptr, yc.p, k, int64_t(hw) * c);
+        position_term(env.ctx, q.p, e, v, br0, x.n, hw, k, yc.p, h, h);
+        env.pool.recycle(yc);
         env.pool.recycle(q);
-        return out;
     }
 };
 
@@ -360,15 +384,11 @@ struct MixTransformer {
         DT h = proj_in.fwd(e, t);
         e.pool.recycle(t);
         t = ln1.fwd(e, h);
-        DT u = attn1.fwd(e, t);
+        attn1.fwd_add(e, t, h.p);
         e.pool.recycle(t);
-        add_inplace(e.ctx, h.p, u.p, h.numel());
-        e.pool.recycle(u);
         t = ln2.fwd(e, h);
-        u = attn2.fwd(e, t, br0);
+        attn2.fwd_add(e, t, br0, h.p);
         e.pool.recycle(t);
-        add_inplace(e.ctx, h.p, u.p, h.numel());
-        e.pool.recycle(u);
         t = ln3.fwd(e, h);
         // MixFFN (transformer.rs:121-129): SiLU(inverted(t)) -> GLU depthwise -> point + h
         DT a = inverted.fwd(e, t, nullptr, GemmEpilogue::Silu);
@@ -376,7 +396,7 @@ struct MixTransformer {
         DT g = e.pool.tensor(a.n, a.h, a.w, hidden);
         depthwise3x3(e.ctx, a.p, a.n, a.h, a.w, a.c, dw, dwb, 2, g.p);
         e.pool.recycle(a);
-        u = point.fwd(e, g, &h);
+        DT u = point.fwd(e, g, &h);
         e.pool.recycle(g);
         e.pool.recycle(h);
         DT out = proj_out.fwd(e, u, &x);
@@ -557,14 +577,11 @@ class UNetDevice {
             tr("unet.up." + std::to_string(i) + ".out", h);
         }
         if (!skips.empty()) fail(kInternal, "skip stack not consumed");
-        DT a = norm_out_.fwd(e, h, nullptr, true);
+        // norm_out + SiLU applied inside conv_out's depthwise; eps goes straight to the caller's buffer.
+        float *gn = norm_out_.affine(e, h, nullptr);
+        conv_out_.fwd(e, h, gn, nullptr, eps_dev);
+        pool_.recycle(gn);
         pool_.recycle(h);
-        // conv_out writes eps straight into the caller's buffer.
-        DT mid = pool_.tensor(a.n, a.h, a.w, a.c);
-        depthwise3x3(ctx_, a.p, a.n, a.h, a.w, a.c, conv_out_.dw, conv_out_.dwb, 1, mid.p);
-        conv_out_.pw.fwd(e, mid.p, mid.px(), eps_dev);
-        pool_.recycle(mid);
-        pool_.recycle(a);
         pool_.recycle(temb);
         pool_.recycle(temb_silu);
         if (trace) {

@@ -45,18 +45,28 @@ def test_softmax_lambda_kernel(ctx, nb, rows, k):
         assert max_abs_rel(got[b].T, want) < 1e-5
 
 
-@pytest.mark.parametrize("nb,hh,ww,vd", [(2, 16, 12, 40), (1, 7, 5, 8), (2, 16, 16, 160)])
-def test_tap_filter_kernel_bit_exact(ctx, nb, hh, ww, vd):
+@pytest.mark.parametrize("nb,hh,ww,vd", [(2, 16, 12, 40), (1, 7, 5, 8), (2, 16, 16, 160), (1, 20, 9, 80)])
+@pytest.mark.parametrize("heads_per_thread", ["8", "4", "2"])
+def test_tap_filter_kernel_bit_exact(ctx, nb, hh, ww, vd, heads_per_thread, monkeypatch):
+    monkeypatch.setenv("MOEBIUS_HIP_TAP_HEADS", heads_per_thread)
     rng = np.random.default_rng(hh * ww + vd)
     a = rng.standard_normal((nb, hh * ww, 8, 226)).astype(np.float32)
     v = rng.standard_normal((nb, hh * ww, vd)).astype(np.float32)
     o = rng.standard_normal((nb, hh * ww, 8 * vd)).astype(np.float32)
-    od = D(ctx, o)
-    ad, vdev = D(ctx, a), D(ctx, v)
-    E.check(E.lib().mh_tap_filter(ctx.h, ad.ptr, vdev.ptr, od.ptr, nb, hh, ww, vd))
-    got = od.numpy()
+    h = rng.standard_normal((nb, hh * ww, 8 * vd)).astype(np.float32)
+    # the device takes A tap-major: [pixel][226][head]
+    ad, vdev, yd = D(ctx, a.transpose(0, 1, 3, 2)), D(ctx, v), D(ctx, o)
+    out = E.DeviceArray(ctx, o.shape)
+    E.check(E.lib().mh_tap_filter(ctx.h, ad.ptr, vdev.ptr, yd.ptr, None, out.ptr, nb, hh, ww, vd))
+    got = out.numpy()
+    # residual form, in place on the residual: h + u
+    hd = D(ctx, h)
+    E.check(E.lib().mh_tap_filter(ctx.h, ad.ptr, vdev.ptr, yd.ptr, hd.ptr, hd.ptr, nb, hh, ww, vd))
+    got_res = hd.numpy()
     for b in range(nb):
-        assert np.array_equal(got[b], oracle.tap_filter(a[b], v[b], o[b], hh, ww))
+        want = oracle.tap_filter(a[b], v[b], o[b], hh, ww)
+        assert np.array_equal(got[b], want)
+        assert np.array_equal(got_res[b], h[b] + want)
 
 
 @pytest.mark.parametrize("br0,nb,k", [(0, 2, 40), (1, 1, 80), (0, 2, 160)])
@@ -67,23 +77,37 @@ def test_position_term_kernel_bit_exact(ctx, br0, nb, k):
     e = rng.standard_normal((hw, 10, k)).astype(np.float32)
     vb = rng.standard_normal((2, 10, k)).astype(np.float32)
     o = rng.standard_normal((nb, hw, 8 * k)).astype(np.float32)
+    h = rng.standard_normal((nb, hw, 8 * k)).astype(np.float32)
     od = D(ctx, o)
-    qd, ed, vbd = D(ctx, q), D(ctx, e), D(ctx, vb)
-    E.check(E.lib().mh_position_term(ctx.h, qd.ptr, ed.ptr, vbd.ptr, br0, nb, hw, k, od.ptr))
-    got = od.numpy()
+    qd, ed, vbd, hd = D(ctx, q), D(ctx, e), D(ctx, vb), D(ctx, h)
+    out = E.DeviceArray(ctx, o.shape)
+    E.check(E.lib().mh_position_term(ctx.h, qd.ptr, ed.ptr, vbd.ptr, br0, nb, hw, k, od.ptr, None, out.ptr))
+    E.check(E.lib().mh_position_term(ctx.h, qd.ptr, ed.ptr, vbd.ptr, br0, nb, hw, k, od.ptr, hd.ptr, hd.ptr))
+    got, got_res = out.numpy(), hd.numpy()
     for b in range(nb):
-        assert np.array_equal(got[b], oracle.position_term(q[b], e, vb[br0 + b], o[b]))
+        want = oracle.position_term(q[b], e, vb[br0 + b], o[b])
+        assert np.array_equal(got[b], want)
+        assert np.array_equal(got_res[b], h[b] + want)
 
 
-def test_gemm_nt_kernel(ctx):
+@pytest.mark.parametrize("row_group", [0, 8])
+def test_gemm_nt_kernel(ctx, row_group):
     rng = np.random.default_rng(9)
-    m, n, k = 300, 226, 40
+    m, n, k = 304, 226, 40
     a = rng.standard_normal((m, k)).astype(np.float32)
     b = rng.standard_normal((n, k)).astype(np.float32)
-    c = E.DeviceArray(ctx, (m, n))
+    want = a.astype(np.float64) @ b.astype(np.float64).T
     ad, bd = D(ctx, a), D(ctx, b)
-    E.check(E.lib().mh_gemm_nt(ctx.h, ad.ptr, k, bd.ptr, 0, k, m, n, k, None, None, c.ptr, n))
-    assert max_abs_rel(c.numpy(), a.astype(np.float64) @ b.astype(np.float64).T) < 1e-5
+    if row_group:
+        g = row_group
+        c = E.DeviceArray(ctx, (m // g, n, g))
+        E.check(E.lib().mh_gemm_nt(ctx.h, ad.ptr, k, bd.ptr, 0, k, m, n, k, None, None, c.ptr, n * g, g))
+        got = c.numpy().transpose(0, 2, 1).reshape(m, n)
+    else:
+        c = E.DeviceArray(ctx, (m, n))
+        E.check(E.lib().mh_gemm_nt(ctx.h, ad.ptr, k, bd.ptr, 0, k, m, n, k, None, None, c.ptr, n, 0))
+        got = c.numpy()
+    assert max_abs_rel(got, want) < 1e-5
 
 
 def test_best_fit_matches_reference_policy():

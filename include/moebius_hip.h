@@ -65,6 +65,7 @@ extern "C" {
 typedef struct MhContext MhContext;
 typedef struct MhEvent MhEvent;
 typedef struct MhUNet MhUNet;
+typedef struct MhVae MhVae;
 
 /* One converter tensor (tools/convert_weights.py:13-33 names and layouts) in
  * host memory: GEMM weights F32 or F16, everything else F32. */
@@ -265,6 +266,45 @@ int32_t mh_unet_forward_traced(MhUNet *unet, const float *x_dev, uint32_t timest
 
 /* HBM held by the weights and by the activation pool. */
 int32_t mh_unet_memory(MhUNet *unet, uint64_t *weight_bytes, uint64_t *pool_bytes);
+
+/* ---- VAE (src/vae) ---- */
+
+/* src/vae/mod.rs:88-103 `Vae::load` from the converter tensors of vae.safetensors
+ * (diffusers AutoencoderKL names at the file root; 3x3 [o,3,3,i], 1x1 and linear
+ * [o,i]), copied to HBM once. The scaling_factor metadata check stays with the host. */
+int32_t mh_vae_create(MhContext *ctx, const MhNamedTensor *tensors, uint32_t count, MhVae **out);
+/* Destroy every MhVae / MhUNet before the context they were created on. */
+void mh_vae_destroy(MhVae *vae);
+
+/* src/vae/mod.rs:105-109 `Vae::encode` (encoder.rs:77-118), device buffers:
+ * images [b,h,w,3] in [-1,1] (h, w multiples of 8), noise [b,h/8,w/8,4] ~N(0,1)
+ * -> z [b,h/8,w/8,4] = (mean + exp(0.5 clamp(logvar, -30, 20)) noise) 0.13025.
+ * trace (may be NULL) gets vae.encoder.item<b>.{conv_in, down.<i>, mid, moments}. */
+int32_t mh_vae_encode(MhVae *vae, const float *images_dev, uint32_t b, uint32_t h, uint32_t w,
+                      const float *noise_dev, float *z_dev, MhTraceFn trace, void *user);
+
+/* src/vae/mod.rs:111-115 `Vae::decode` (decoder.rs:74-99), device buffers:
+ * latents [1,h,w,4] (scaled) -> out [1,8h,8w,3] = (dec(latents / 0.13025) + 1) / 2,
+ * unclamped. trace (may be NULL) gets vae.decoder.{conv_in, mid, up.<i>}. */
+int32_t mh_vae_decode(MhVae *vae, const float *latents_dev, uint32_t h, uint32_t w, float *out_dev,
+                      MhTraceFn trace, void *user);
+
+/* The same on host buffers (synchronous), as the pipeline calls them
+ * (src/pipeline.rs:259,266,286,358-366). */
+int32_t mh_vae_encode_host(MhVae *vae, const float *images, uint32_t b, uint32_t h, uint32_t w, const float *noise,
+                           float *z);
+int32_t mh_vae_decode_host(MhVae *vae, const float *latents, uint32_t h, uint32_t w, float *out);
+
+int32_t mh_vae_memory(MhVae *vae, uint64_t *weight_bytes, uint64_t *pool_bytes);
+
+/* src/vae/mod.rs:275-294 `softmax_rows`, in place on device rows [nrows][n]
+ * (n <= 15360, scale > 0): per row max, exp((v - max) scale) with values below
+ * exp(-40) flushed to 0, summed in row order, times (f32)(1 / sum). */
+int32_t mh_softmax_rows(MhContext *ctx, float *rows, uint64_t nrows, uint32_t n, float scale);
+
+/* src/vae/encoder.rs:121-133 `sample`: moments [pixels][8] = mean(4) | logvar(4),
+ * noise [pixels][4] -> z [pixels][4]. */
+int32_t mh_vae_sample(MhContext *ctx, const float *moments, const float *noise, uint64_t pixels, float *z);
 
 /* src/unet/embed.rs:21-30 `timestep_sinusoid` (host arithmetic, f32 libm). */
 void mh_timestep_sinusoid(uint32_t t, float *out /* [320] */);

@@ -92,6 +92,15 @@ SIGNATURES = {
     "mh_unet_forward_host": (_i32, [_vp, _vp, _u32, _u32, _vp]),
     "mh_unet_forward_traced": (_i32, [_vp, _vp, _u32, _u32, _vp, _vp, _vp]),
     "mh_unet_memory": (_i32, [_vp, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
+    "mh_vae_create": (_i32, [_vp, _vp, _u32, _vp]),
+    "mh_vae_destroy": (None, [_vp]),
+    "mh_vae_encode": (_i32, [_vp, _vp, _u32, _u32, _u32, _vp, _vp, _vp, _vp]),
+    "mh_vae_decode": (_i32, [_vp, _vp, _u32, _u32, _vp, _vp, _vp]),
+    "mh_vae_encode_host": (_i32, [_vp, _vp, _u32, _u32, _u32, _vp, _vp]),
+    "mh_vae_decode_host": (_i32, [_vp, _vp, _u32, _u32, _vp]),
+    "mh_vae_memory": (_i32, [_vp, _vp, _vp]),
+    "mh_softmax_rows": (_i32, [_vp, _vp, _u64, _u32, _f32]),
+    "mh_vae_sample": (_i32, [_vp, _vp, _vp, _u64, _vp]),
     "mh_timestep_sinusoid": (None, [_u32, _vp]),
     "mh_scratch_best_fit": (ctypes.c_int64, [_vp, _vp, _u64, _u64]),
 }

@@ -14,6 +14,7 @@
 #include "kernels.hpp"
 #include "pool.hpp"
 #include "unet.hpp"
+#include "vae.hpp"
 
 struct MhContext {
     mh::Context ctx;
@@ -28,6 +29,11 @@ struct MhUNet {
         if (x_dev) (void)hipFree(x_dev);
         if (eps_dev) (void)hipFree(eps_dev);
     }
+};
+
+struct MhVae {
+    MhContext *owner;
+    std::unique_ptr<mh::Vae> vae;
 };
 
 struct MhEvent {
@@ -599,6 +605,133 @@ int32_t mh_unet_memory(MhUNet *unet, uint64_t *weight_bytes, uint64_t *pool_byte
         unet_ctx(unet);
         if (weight_bytes) *weight_bytes = unet->net->weight_bytes();
         if (pool_bytes) *pool_bytes = unet->net->pool_bytes();
+    });
+}
+
+int32_t mh_vae_create(MhContext *ctx, const MhNamedTensor *tensors, uint32_t count, MhVae **out) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(out, "out");
+        *out = nullptr;
+        need(tensors, "tensors");
+        std::vector<mh::NamedTensor> t(count);
+        for (uint32_t i = 0; i < count; ++i) {
+            t[i].name = tensors[i].name;
+            t[i].data = tensors[i].data;
+            t[i].dtype = tensors[i].dtype;
+            t[i].numel = tensors[i].numel;
+        }
+        auto v = std::make_unique<MhVae>();
+        v->owner = ctx;
+        v->vae = std::make_unique<mh::Vae>(c, t.data(), int(count));
+        *out = v.release();
+    });
+}
+
+void mh_vae_destroy(MhVae *vae) {
+    if (!vae) return;
+    (void)hipSetDevice(vae->owner->ctx.device);
+    delete vae;
+}
+
+static mh::Context &vae_ctx(MhVae *v) {
+    if (!v) mh::fail(mh::kInvalidArgument, "vae is NULL");
+    return C(v->owner);
+}
+
+int32_t mh_vae_encode(MhVae *vae, const float *images_dev, uint32_t b, uint32_t h, uint32_t w,
+                      const float *noise_dev, float *z_dev, MhTraceFn trace, void *user) {
+    return guard([&] {
+        mh::Context &c = vae_ctx(vae);
+        need(images_dev, "images");
+        need(noise_dev, "noise");
+        need(z_dev, "z");
+        TraceCtx tc{trace, user, c.stream};
+        vae->vae->encode(images_dev, dim(b, "b"), dim(h, "h"), dim(w, "w"), noise_dev, z_dev,
+                         trace ? trace_bridge : nullptr, &tc);
+    });
+}
+
+int32_t mh_vae_decode(MhVae *vae, const float *latents_dev, uint32_t h, uint32_t w, float *out_dev,
+                      MhTraceFn trace, void *user) {
+    return guard([&] {
+        mh::Context &c = vae_ctx(vae);
+        need(latents_dev, "latents");
+        need(out_dev, "out");
+        TraceCtx tc{trace, user, c.stream};
+        vae->vae->decode(latents_dev, dim(h, "h"), dim(w, "w"), out_dev, trace ? trace_bridge : nullptr, &tc);
+    });
+}
+
+int32_t mh_vae_encode_host(MhVae *vae, const float *images, uint32_t b, uint32_t h, uint32_t w, const float *noise,
+                           float *z) {
+    return guard([&] {
+        mh::Context &c = vae_ctx(vae);
+        need(images, "images");
+        need(noise, "noise");
+        need(z, "z");
+        const size_t ib = size_t(b) * h * w * 3 * sizeof(float);
+        const size_t zb = size_t(b) * (h / 8) * (w / 8) * 4 * sizeof(float);
+        float *d = nullptr;
+        HIP_CHECK(hipMalloc(&d, ib + 2 * zb));
+        struct Free {
+            float *p;
+            ~Free() { (void)hipFree(p); }
+        } f{d};
+        float *dn = d + ib / sizeof(float), *dz = dn + zb / sizeof(float);
+        HIP_CHECK(hipMemcpyAsync(d, images, ib, hipMemcpyHostToDevice, c.stream));
+        HIP_CHECK(hipMemcpyAsync(dn, noise, zb, hipMemcpyHostToDevice, c.stream));
+        vae->vae->encode(d, dim(b, "b"), dim(h, "h"), dim(w, "w"), dn, dz);
+        HIP_CHECK(hipMemcpyAsync(z, dz, zb, hipMemcpyDeviceToHost, c.stream));
+        HIP_CHECK(hipStreamSynchronize(c.stream));
+    });
+}
+
+int32_t mh_vae_decode_host(MhVae *vae, const float *latents, uint32_t h, uint32_t w, float *out) {
+    return guard([&] {
+        mh::Context &c = vae_ctx(vae);
+        need(latents, "latents");
+        need(out, "out");
+        const size_t lb = size_t(h) * w * 4 * sizeof(float);
+        const size_t ob = size_t(h) * w * 64 * 3 * sizeof(float);
+        float *d = nullptr;
+        HIP_CHECK(hipMalloc(&d, lb + ob));
+        struct Free {
+            float *p;
+            ~Free() { (void)hipFree(p); }
+        } f{d};
+        float *dout = d + lb / sizeof(float);
+        HIP_CHECK(hipMemcpyAsync(d, latents, lb, hipMemcpyHostToDevice, c.stream));
+        vae->vae->decode(d, dim(h, "h"), dim(w, "w"), dout);
+        HIP_CHECK(hipMemcpyAsync(out, dout, ob, hipMemcpyDeviceToHost, c.stream));
+        HIP_CHECK(hipStreamSynchronize(c.stream));
+    });
+}
+
+int32_t mh_vae_memory(MhVae *vae, uint64_t *weight_bytes, uint64_t *pool_bytes) {
+    return guard([&] {
+        vae_ctx(vae);
+        if (weight_bytes) *weight_bytes = vae->vae->weight_bytes();
+        if (pool_bytes) *pool_bytes = vae->vae->pool_bytes();
+    });
+}
+
+int32_t mh_softmax_rows(MhContext *ctx, float *rows, uint64_t nrows, uint32_t n, float scale) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(rows, "rows");
+        if (!(scale > 0.0f)) mh::fail(mh::kInvalidArgument, "softmax_rows: scale must be positive");
+        mh::softmax_rows(c, rows, int64_t(nrows), dim(n, "n"), scale);
+    });
+}
+
+int32_t mh_vae_sample(MhContext *ctx, const float *moments, const float *noise, uint64_t pixels, float *z) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(moments, "moments");
+        need(noise, "noise");
+        need(z, "z");
+        mh::vae_sample(c, moments, noise, int64_t(pixels), z);
     });
 }
 

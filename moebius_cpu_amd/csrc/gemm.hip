@@ -143,7 +143,7 @@ void conv3x3_output_hw(int h, int w, int stride, const int pad[4], bool upsample
 
 void conv3x3(Context &ctx, const float *x, int n, int h, int w, int c_in, const void *weight, WeightType wt,
              int c_out, const float *bias, int stride, const int pad[4], bool upsample2x, const Affine *prologue,
-             float *out) {
+             float *out, const float *residual2) {
     MH_REQUIRE(c_in > 0 && c_out > 0, "Conv3x3 input channels");
     if (prologue) {
         MH_REQUIRE(stride == 1 && pad[0] == 1 && pad[1] == 1 && pad[2] == 1 && pad[3] == 1,
@@ -176,6 +176,7 @@ void conv3x3(Context &ctx, const float *x, int n, int h, int w, int c_in, const 
     p.bias = bias;
     p.out = out;
     p.ldc = c_out;
+    p.res2 = residual2;
     const bool pro = prologue != nullptr;
     if (pro) {
         p.psc = prologue->scale;

@@ -62,9 +62,10 @@ struct ResidualAffine {
 void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void *weight, WeightType wt, int c_out,
              const float *bias, const float *residual, float *out, GemmEpilogue epi = GemmEpilogue::None,
              const ResidualAffine *raff = nullptr, const float *residual2 = nullptr);
+// residual2 (optional, [n, ho, wo, c_out]) is added last: out = (bias + conv) + residual2.
 void conv3x3(Context &ctx, const float *x, int n, int h, int w, int c_in, const void *weight, WeightType wt,
              int c_out, const float *bias, int stride, const int pad[4], bool upsample2x, const Affine *prologue,
-             float *out);
+             float *out, const float *residual2 = nullptr);
 void conv3x3_output_hw(int h, int w, int stride, const int pad[4], bool upsample2x, int *ho, int *wo);
 // C[z] = A[z] . B[z]^T (+ bias) (+ residual[z]) [SiLU] for z < batch, all K-contiguous:
 // A [m][lda], B [n][ldb], C [m][ldc]; *_bs are per-item element offsets.
@@ -88,5 +89,16 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
 // out may alias yc or residual.
 void position_term(Context &ctx, const float *q, const float *e, const float *v_branches, int br0, int nb, int hw,
                    int k, const float *yc, const float *residual, float *out);
+
+// ---- VAE (vae_kernels.hip), src/vae
+// In place over rows [nrows][n] (n <= 15360): softmax(scale * row) with
+// probabilities below e^-40 flushed to zero (src/vae/mod.rs:275-294).
+void softmax_rows(Context &ctx, float *rows, int64_t nrows, int n, float scale);
+// out [cols][rows] = in [rows][cols] with row stride ld_in.
+void transpose(Context &ctx, const float *in, int64_t ld_in, int rows, int cols, float *out);
+// z [pixels][4] = posterior sample from moments [pixels][8] and noise [pixels][4].
+void vae_sample(Context &ctx, const float *moments, const float *noise, int64_t pixels, float *z);
+// which 0: y = x / 0.13025; 1: y = (x + 1) * 0.5.
+void vae_rescale(Context &ctx, const float *x, int64_t len, int which, float *y);
 
 }  // namespace mh

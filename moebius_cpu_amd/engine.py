@@ -10,6 +10,7 @@ tests read like the reference's own tests/kernels.rs. Tensors live in HBM;
 from __future__ import annotations
 
 import ctypes
+import weakref
 
 import numpy as np
 
@@ -24,9 +25,16 @@ class Context:
         h = ctypes.c_void_p()
         check(lib().mh_context_create(int(device), ctypes.byref(h)))
         self.h = h
+        self._models = weakref.WeakSet()  # UNet / Vae objects, destroyed before the context
+
+    def adopt(self, model):
+        """Registers a model (anything with close()) to be closed before this context."""
+        self._models.add(model)
 
     def close(self):
         if self.h:
+            for m in list(self._models):
+                m.close()
             lib().mh_context_destroy(self.h)
             self.h = None
 

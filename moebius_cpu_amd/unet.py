@@ -38,6 +38,7 @@ class UNet:
         h = ctypes.c_void_p()
         check(lib().mh_unet_create(ctx.h, arr, len(params), ctypes.byref(h)))
         self.h = h
+        ctx.adopt(self)
 
     def close(self):
         if getattr(self, "h", None):

@@ -406,3 +406,127 @@ def block_forward(kind: str, params: dict, prefix: str, x, c_out=None, temb=None
     if st != 0:
         raise RuntimeError(err.value.decode())
     return out
+
+
+# ---- VAE chain (oracle/vae.cpp)
+def _declare_vae(L):
+    vp, i64, cp, ci = ctypes.c_void_p, _i64, ctypes.c_char_p, ctypes.c_int
+    _declare_unet(L)
+    L.orc_vae_create.restype = vp
+    L.orc_vae_create.argtypes = [ctypes.POINTER(_Named), ci, cp, ci]
+    L.orc_vae_destroy.argtypes = [vp]
+    L.orc_vae_encode.restype = ci
+    L.orc_vae_encode.argtypes = [vp, vp, i64, i64, i64, vp, vp, _TRACE_FN, vp, cp, ci]
+    L.orc_vae_decode.restype = ci
+    L.orc_vae_decode.argtypes = [vp, vp, i64, i64, vp, _TRACE_FN, vp, cp, ci]
+    L.orc_softmax_rows.argtypes = [vp, i64, i64, ctypes.c_float]
+    L.orc_vae_sample.argtypes = [vp, vp, i64, vp]
+    L.orc_vae_attention.restype = ci
+    L.orc_vae_attention.argtypes = [ctypes.POINTER(_Named), ci, cp, vp, i64, i64, i64, i64, vp, cp, ci]
+    L.orc_vae_resnet.restype = ci
+    L.orc_vae_resnet.argtypes = [ctypes.POINTER(_Named), ci, cp, vp, i64, i64, i64, i64, i64, vp, cp, ci]
+
+
+def _named_table(params: dict):
+    keep = {k: np.ascontiguousarray(v, dtype=np.float32) for k, v in params.items()}
+    arr = (_Named * len(keep))()
+    for i, (k, v) in enumerate(keep.items()):
+        arr[i].name = k.encode()
+        arr[i].data = v.ctypes.data
+        arr[i].numel = v.size
+    return keep, arr
+
+
+def softmax_rows(rows, scale: float):
+    """src/vae/mod.rs:275-294 over rows [nrows, n] (returns a new array)."""
+    L = lib()
+    _declare_vae(L)
+    r = _f32(rows).copy()
+    L.orc_softmax_rows(_p(r), r.shape[0], r.shape[1], float(scale))
+    return r
+
+
+def vae_sample(moments, noise):
+    """src/vae/encoder.rs:121-133: moments [..., 8], noise [..., 4] -> z [..., 4]."""
+    L = lib()
+    _declare_vae(L)
+    m, nz = _f32(moments), _f32(noise)
+    z = np.empty(nz.shape, np.float32)
+    L.orc_vae_sample(_p(m), _p(nz), nz.size // 4, _p(z))
+    return z
+
+
+def vae_attention(params: dict, prefix: str, x):
+    """src/vae/mod.rs:240-270 with the weights under prefix (attentions.0)."""
+    L = lib()
+    _declare_vae(L)
+    keep, arr = _named_table(params)
+    x = _f32(x)
+    out = np.empty_like(x)
+    err = ctypes.create_string_buffer(512)
+    if L.orc_vae_attention(arr, len(keep), prefix.encode(), _p(x), *x.shape, _p(out), err, 512) != 0:
+        raise RuntimeError(err.value.decode())
+    return out
+
+
+def vae_resnet(params: dict, prefix: str, x, c_out: int):
+    """src/vae/mod.rs:174-211 with the weights under prefix (resnets.j)."""
+    L = lib()
+    _declare_vae(L)
+    keep, arr = _named_table(params)
+    x = _f32(x)
+    n, h, w, c = x.shape
+    out = np.empty((n, h, w, c_out), np.float32)
+    err = ctypes.create_string_buffer(512)
+    if L.orc_vae_resnet(arr, len(keep), prefix.encode(), _p(x), n, h, w, c, c_out, _p(out), err, 512) != 0:
+        raise RuntimeError(err.value.decode())
+    return out
+
+
+class Vae:
+    """src/vae/mod.rs Vae over a dict of converter tensors (f32 arrays)."""
+
+    def __init__(self, params: dict):
+        L = lib()
+        _declare_vae(L)
+        self._keep, arr = _named_table(params)
+        err = ctypes.create_string_buffer(512)
+        self.h = L.orc_vae_create(arr, len(self._keep), err, 512)
+        if not self.h:
+            raise RuntimeError("oracle VAE load failed: " + err.value.decode())
+
+    @staticmethod
+    def _tracer(traced):
+        def cb(_user, name, data, n, h, w, c):
+            traced[name.decode()] = np.ctypeslib.as_array(data, shape=(n * h * w * c,)).reshape(n, h, w, c).copy()
+        return _TRACE_FN(cb)
+
+    def encode(self, images, noise, trace: bool = False):
+        """images [b,h,w,3] in [-1,1], noise [b,h/8,w/8,4] -> z [b,h/8,w/8,4]."""
+        images, noise = _f32(images), _f32(noise)
+        b, h, w, _ = images.shape
+        z = np.empty((b, h // 8, w // 8, 4), np.float32)
+        traced = {}
+        fn = self._tracer(traced) if trace else _TRACE_FN()
+        err = ctypes.create_string_buffer(512)
+        if lib().orc_vae_encode(self.h, _p(images), b, h, w, _p(noise), _p(z), fn, None, err, 512) != 0:
+            raise RuntimeError("oracle VAE encode failed: " + err.value.decode())
+        return (z, traced) if trace else z
+
+    def decode(self, latents, trace: bool = False):
+        """latents [1,h,w,4] (scaled) -> [1,8h,8w,3] = (dec + 1) / 2."""
+        latents = _f32(latents)
+        _, h, w, _ = latents.shape
+        out = np.empty((1, 8 * h, 8 * w, 3), np.float32)
+        traced = {}
+        fn = self._tracer(traced) if trace else _TRACE_FN()
+        err = ctypes.create_string_buffer(512)
+        if lib().orc_vae_decode(self.h, _p(latents), h, w, _p(out), fn, None, err, 512) != 0:
+            raise RuntimeError("oracle VAE decode failed: " + err.value.decode())
+        return (out, traced) if trace else out
+
+    def __del__(self):
+        try:
+            lib().orc_vae_destroy(self.h)
+        except Exception:
+            pass

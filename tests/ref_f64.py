@@ -142,3 +142,96 @@ def timestep_embedding_sinusoid(t):
     freq = np.exp(-np.log(10000.0) * np.arange(half) / half)
     arg = t * freq
     return np.concatenate([np.cos(arg), np.sin(arg)])
+
+
+# ---- VAE (diffusers AutoencoderKL definitions, upstream of src/vae)
+VAE_CH = (128, 256, 512, 512)
+
+
+def conv3x3(x, w, b, stride=1, pad=(1, 1, 1, 1), up=False):
+    """Direct 3x3 conv in f64: x [n,h,w,ci], w [co,3,3,ci]; pad = top, left, bottom, right."""
+    if up:
+        x = x.repeat(2, axis=1).repeat(2, axis=2)
+    n, h, w_, ci = x.shape
+    xp = np.zeros((n, h + pad[0] + pad[2], w_ + pad[1] + pad[3], ci))
+    xp[:, pad[0]:pad[0] + h, pad[1]:pad[1] + w_] = x
+    ho = (h + pad[0] + pad[2] - 3) // stride + 1
+    wo = (w_ + pad[1] + pad[3] - 3) // stride + 1
+    out = np.zeros((n, ho, wo, w.shape[0])) + b
+    for ky in range(3):
+        for kx in range(3):
+            patch = xp[:, ky:ky + stride * (ho - 1) + 1:stride, kx:kx + stride * (wo - 1) + 1:stride]
+            out += patch @ w[:, ky, kx, :].T
+    return out
+
+
+def vae_resnet(params, p, x, ci, co):
+    g = lambda n: P(params, n)  # noqa: E731
+    h = silu(group_norm(x, 32, 1e-6, g(p + ".norm1.weight"), g(p + ".norm1.bias")))
+    h = conv3x3(h, g(p + ".conv1.weight"), g(p + ".conv1.bias"))
+    h = silu(group_norm(h, 32, 1e-6, g(p + ".norm2.weight"), g(p + ".norm2.bias")))
+    h = conv3x3(h, g(p + ".conv2.weight"), g(p + ".conv2.bias"))
+    sc = linear(x, g(p + ".conv_shortcut.weight"), g(p + ".conv_shortcut.bias")) if ci != co else x
+    return sc + h
+
+
+def vae_attention(params, p, x):
+    g = lambda n: P(params, n)  # noqa: E731
+    n, h, w, c = x.shape
+    t = group_norm(x, 32, 1e-6, g(p + ".group_norm.weight"), g(p + ".group_norm.bias")).reshape(n, h * w, c)
+    q = linear(t, g(p + ".to_q.weight"), g(p + ".to_q.bias"))
+    k = linear(t, g(p + ".to_k.weight"), g(p + ".to_k.bias"))
+    v = linear(t, g(p + ".to_v.weight"), g(p + ".to_v.bias"))
+    s = q @ k.transpose(0, 2, 1) / np.sqrt(c)
+    s = np.exp(s - s.max(axis=-1, keepdims=True))
+    a = (s / s.sum(axis=-1, keepdims=True)) @ v
+    return linear(a, g(p + ".to_out.0.weight"), g(p + ".to_out.0.bias")).reshape(n, h, w, c) + x
+
+
+def vae_mid(params, p, x):
+    c = x.shape[-1]
+    x = vae_resnet(params, p + ".resnets.0", x, c, c)
+    x = vae_attention(params, p + ".attentions.0", x)
+    return vae_resnet(params, p + ".resnets.1", x, c, c)
+
+
+def vae_encode(params, images, noise):
+    """AutoencoderKL.encode(x).latent_dist.sample() * 0.13025 with the given noise."""
+    g = lambda n: P(params, n)  # noqa: E731
+    e = "encoder"
+    x = conv3x3(images.astype(np.float64), g(e + ".conv_in.weight"), g(e + ".conv_in.bias"))
+    c_prev = VAE_CH[0]
+    for i, c in enumerate(VAE_CH):
+        for j in range(2):
+            x = vae_resnet(params, f"{e}.down_blocks.{i}.resnets.{j}", x, c_prev if j == 0 else c, c)
+        if i + 1 < len(VAE_CH):
+            x = conv3x3(x, g(f"{e}.down_blocks.{i}.downsamplers.0.conv.weight"),
+                        g(f"{e}.down_blocks.{i}.downsamplers.0.conv.bias"), stride=2, pad=(0, 0, 1, 1))
+        c_prev = c
+    x = vae_mid(params, e + ".mid_block", x)
+    x = silu(group_norm(x, 32, 1e-6, g(e + ".conv_norm_out.weight"), g(e + ".conv_norm_out.bias")))
+    x = conv3x3(x, g(e + ".conv_out.weight"), g(e + ".conv_out.bias"))
+    m = linear(x, g("quant_conv.weight"), g("quant_conv.bias"))
+    mean, logvar = m[..., :4], np.clip(m[..., 4:], -30.0, 20.0)
+    return (mean + np.exp(0.5 * logvar) * noise) * 0.13025
+
+
+def vae_decode(params, latents):
+    """(AutoencoderKL.decode(z / 0.13025) + 1) / 2."""
+    g = lambda n: P(params, n)  # noqa: E731
+    d = "decoder"
+    z = linear(latents.astype(np.float64) / np.float64(np.float32(0.13025)), g("post_quant_conv.weight"),
+               g("post_quant_conv.bias"))
+    x = conv3x3(z, g(d + ".conv_in.weight"), g(d + ".conv_in.bias"))
+    x = vae_mid(params, d + ".mid_block", x)
+    c_prev = VAE_CH[-1]
+    for i, c in enumerate(reversed(VAE_CH)):
+        for j in range(3):
+            x = vae_resnet(params, f"{d}.up_blocks.{i}.resnets.{j}", x, c_prev if j == 0 else c, c)
+        if i + 1 < len(VAE_CH):
+            x = conv3x3(x, g(f"{d}.up_blocks.{i}.upsamplers.0.conv.weight"),
+                        g(f"{d}.up_blocks.{i}.upsamplers.0.conv.bias"), up=True)
+        c_prev = c
+    x = silu(group_norm(x, 32, 1e-6, g(d + ".conv_norm_out.weight"), g(d + ".conv_norm_out.bias")))
+    x = conv3x3(x, g(d + ".conv_out.weight"), g(d + ".conv_out.bias"))
+    return (x + 1.0) / 2.0

@@ -1,0 +1,143 @@
+"""GPU parity of the VAE path, through the C ABI: the mid attention's row
+softmax and the posterior sample bit for bit against the oracle, then encode
+and decode (random-init SDXL-VAE weights) against the oracle block by block,
+at small sizes and at the pipeline's 512x512 / 64x64 shapes."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from moebius_cpu_amd import engine as E
+from moebius_cpu_amd import synthetic as S
+from moebius_cpu_amd import vae_params as V
+from moebius_cpu_amd.vae import Vae
+from tests.util import max_abs_rel, rel_l2
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4  # max-abs <= 1e-4 * max|ref| for f32 paths
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = E.Context(0)
+    yield c
+    c.synchronize()
+    c.close()
+
+
+def D(ctx, a):
+    return E.DeviceArray.from_numpy(ctx, np.ascontiguousarray(a, dtype=np.float32))
+
+
+@pytest.mark.parametrize("rows,n,scale", [(64, 4096, 1.0 / np.sqrt(512.0)), (37, 300, 0.7), (5, 1, 1.0)])
+def test_softmax_rows_bit_exact(ctx, rows, n, scale):
+    rng = np.random.default_rng(n + rows)
+    x = (rng.standard_normal((rows, n)) * (20.0 / scale)).astype(np.float32)  # peaky rows: many flushed entries
+    x[0, :] = 2.5  # equal entries
+    d = D(ctx, x)
+    E.check(E.lib().mh_softmax_rows(ctx.h, d.ptr, rows, n, np.float32(scale)))
+    got = d.numpy()
+    want = oracle.softmax_rows(x, np.float32(scale))
+    assert np.array_equal(got, want)
+    if n > 1:
+        assert (got == 0).any()  # the flush threshold was exercised
+
+
+def test_sample_bit_exact(ctx):
+    rng = np.random.default_rng(7)
+    m = (rng.standard_normal((1000, 8)) * 20).astype(np.float32)  # logvar beyond the clamp both ways
+    m[3, 5] = np.nan
+    nz = rng.standard_normal((1000, 4)).astype(np.float32)
+    md, nd = D(ctx, m), D(ctx, nz)
+    z = E.DeviceArray(ctx, (1000, 4))
+    E.check(E.lib().mh_vae_sample(ctx.h, md.ptr, nd.ptr, 1000, z.ptr))
+    assert np.array_equal(z.numpy(), oracle.vae_sample(m, nz), equal_nan=True)
+
+
+@pytest.fixture(scope="module")
+def params():
+    return V.random_vae()
+
+
+@pytest.fixture(scope="module")
+def ovae(params):
+    return oracle.Vae(params)
+
+
+@pytest.fixture(scope="module")
+def gvae(ctx, params):
+    return Vae(ctx, params)
+
+
+def _compare_traces(got, want):
+    # the device encodes the batch together, the oracle item by item: same names, other order
+    assert sorted(got) == sorted(want), "trace names differ"
+    for name in want:
+        err = max_abs_rel(got[name], want[name])
+        assert err <= TOL, f"{name}: max-abs/max|ref| {err:.3e}"
+
+
+def test_decode_small_matches_oracle(gvae, ovae):
+    lat = S.normal(21, (1, 8, 6, 4))
+    want, tr_o = ovae.decode(lat, trace=True)
+    got, tr_g = gvae.decode_traced(lat)
+    _compare_traces(tr_g, tr_o)
+    assert got.shape == (1, 64, 48, 3)
+    assert max_abs_rel(got, want) <= TOL
+
+
+def test_encode_small_matches_oracle(gvae, ovae):
+    images = V.vae_images(seed=22, b=2, h=64, w=48)
+    noise = S.normal(23, (2, 8, 6, 4))
+    want, tr_o = ovae.encode(images, noise, trace=True)
+    got, tr_g = gvae.encode_traced(images, noise)
+    _compare_traces(tr_g, tr_o)
+    assert max_abs_rel(got, want) <= TOL
+
+
+def test_decode_512_matches_oracle(gvae, ovae):
+    """The pipeline's decode: a [1,64,64,4] latent to a [1,512,512,3] image."""
+    lat = S.normal(24, (1, 64, 64, 4))
+    want = ovae.decode(lat)
+    got = gvae.decode_host(lat)
+    assert max_abs_rel(got, want) <= TOL and rel_l2(got, want) <= 1e-5
+    # quantised as the pipeline does (src/imaging/blend.rs:21-24): the images differ
+    # only where an f32-rounding difference crosses a level, by one level
+    u8g, u8o = oracle.to_u8(got), oracle.to_u8(want)
+    assert np.mean(u8g != u8o) < 1e-3
+    assert np.abs(u8g.astype(np.int32) - u8o.astype(np.int32)).max() <= 1
+
+
+def test_encode_512_matches_oracle(gvae, ovae):
+    """The pipeline's encode: image and masked image as a batch of 2 at 512x512."""
+    images = V.vae_images(seed=25, b=2, h=512, w=512)
+    noise = S.normal(26, (2, 64, 64, 4))
+    want = ovae.encode(images, noise)
+    got = gvae.encode_host(images, noise)
+    assert max_abs_rel(got, want) <= TOL and rel_l2(got, want) <= 1e-5
+
+
+def test_decode_is_deterministic(gvae):
+    lat = S.normal(27, (1, 16, 16, 4))
+    assert np.array_equal(gvae.decode_host(lat), gvae.decode_host(lat))
+
+
+def test_vae_f16_stored_weights(ctx, params):
+    """f16-stored conv / linear weights, f32 arithmetic: equals the oracle on the rounded weights."""
+    gemm = {s.name for s in V.vae_specs() if s.gemm}
+    rounded = {k: (v.astype(np.float16).astype(np.float32) if k in gemm else v) for k, v in params.items()}
+    v16 = Vae(ctx, params, f16_gemm=True)
+    lat = S.normal(28, (1, 8, 8, 4))
+    got = v16.decode_host(lat)
+    want = oracle.Vae(rounded).decode(lat)
+    assert max_abs_rel(got, want) <= TOL
+    w, _ = v16.memory()
+    w32, _ = Vae(ctx, params).memory()
+    assert w < 0.6 * w32
+
+
+def test_bad_image_size_is_an_argument_error(gvae):
+    with pytest.raises(E.MoebiusError) as ei:
+        gvae.encode_host(np.zeros((1, 60, 64, 3), np.float32), np.zeros((1, 7, 8, 4), np.float32))
+    assert ei.value.code == 1 and "multiple of 8" in str(ei.value)

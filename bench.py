@@ -190,7 +190,55 @@ def bench_unet(args):
     return out
 
 
-WORKLOADS = {"unet_step": bench_unet, "conv3x3_gn_silu": bench_conv_gn}
+def _vae_run(args, which):
+    """VAE decode ([1,64,64,4] latent -> [1,512,512,3]) or encode (2 x 512x512 images), f32."""
+    from moebius_cpu_amd import engine as E
+    from moebius_cpu_amd import synthetic as S
+    from moebius_cpu_amd import vae_params as V
+    from moebius_cpu_amd.vae import Vae
+
+    log("generating random-init VAE weights")
+    params = V.random_vae()
+    ctx = E.Context(0)
+    vae = Vae(ctx, params, f16_gemm=args.f16_weights)
+    if which == "decode":
+        lat = E.DeviceArray.from_numpy(ctx, S.normal(24, (1, 64, 64, 4)))
+        out = E.DeviceArray(ctx, (1, 512, 512, 3))
+        step = lambda: vae.decode(lat, out)  # noqa: E731
+        flops = V.decode_flops(64, 64)
+        wl = "Moebius VAE decode, [1,64,64,4] latent -> [1,512,512,3] image"
+    else:
+        img = E.DeviceArray.from_numpy(ctx, V.vae_images(seed=25, b=2, h=512, w=512))
+        noise = E.DeviceArray.from_numpy(ctx, S.normal(26, (2, 64, 64, 4)))
+        z = E.DeviceArray(ctx, (2, 64, 64, 4))
+        step = lambda: vae.encode(img, noise, z)  # noqa: E731
+        flops = V.encode_flops(2, 512, 512)
+        wl = "Moebius VAE encode, 2 x [512,512,3] images (image + masked image) -> [2,64,64,4]"
+    for _ in range(max(args.warmup, 1)):
+        step()
+    ctx.synchronize()
+    ms = time_region(ctx, step, args.steps)
+    achieved = flops / (ms * 1e-3) / 1e12
+    wbytes, pbytes = vae.memory()
+    res = {
+        "metric": METRIC, "value": round(ms, 4), "unit": "ms", "higher_is_better": False,
+        "ms_per_step": round(ms, 4), "dtype": "f32",
+        "config": {"workload": wl + (", f16-stored weights" if args.f16_weights else "") + ", f32 arithmetic",
+                   "params_M": round(V.param_count() / 1e6, 1), "weight_bytes": wbytes, "pool_bytes": pbytes},
+        "roofline": {"bound": "mfma", "kernel": "whole pass (all kernels, one stream)",
+                     "achieved": round(achieved, 2), "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_F32_MFMA_TFLOPS, 4), "traffic": None,
+                     "work_per_launch": f"{flops / 1e9:.1f} GFLOP per pass", "avg_launch_ms": round(ms, 4)},
+    }
+    vae.close()
+    ctx.close()
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(f"vae_{which}", note=" (C++ restatement of the CPU engine's VAE, OpenMP)")
+    return res
+
+
+WORKLOADS = {"unet_step": bench_unet, "conv3x3_gn_silu": bench_conv_gn,
+             "vae_decode": lambda a: _vae_run(a, "decode"), "vae_encode": lambda a: _vae_run(a, "encode")}
 
 
 def main():
@@ -200,7 +248,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="unet_step", choices=sorted(WORKLOADS))
     ap.add_argument("--cond-only", action="store_true", help="UNet: batch 1 (no CFG)")
-    ap.add_argument("--f16-weights", action="store_true", help="UNet: f16-stored GEMM weights")
+    ap.add_argument("--f16-weights", action="store_true", help="UNet / VAE: f16-stored GEMM weights")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     if args.gpus != 1:

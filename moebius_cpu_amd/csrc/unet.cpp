@@ -180,27 +180,13 @@ struct DwConv2d {
         dwb = W.get(p + ".conv_dw.bias", ci, false).f();
         pw.load(W, p + ".conv_pw", ci, co, true);
     }
-    // gn: [scale | shift] of a GroupNorm + SiLU whose output is this conv's input;
-    // it is applied as the depthwise loads x and to the skip, never stored.
     // res2: added last (the resnet's shortcut). out: caller's buffer or a new tensor.
-    DT fwd(Env &e, const DT &x, const float *gn = nullptr, const float *res2 = nullptr, float *out_p = nullptr) const {
+    DT fwd(Env &e, const DT &x, const float *res2 = nullptr, float *out_p = nullptr) const {
         DT mid = e.pool.tensor(x.n, x.h, x.w, x.c);
-        Affine pro;
-        if (gn) {
-            pro.scale = gn;
-            pro.shift = gn + int64_t(x.n) * x.c;
-            pro.silu = true;
-        }
-        depthwise3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, dw, dwb, 1, mid.p, gn ? &pro : nullptr);
+        depthwise3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, dw, dwb, 1, mid.p);
         DT out = out_p ? DT{out_p, x.n, x.h, x.w, co} : e.pool.tensor(x.n, x.h, x.w, co);
-        ResidualAffine ra;
-        ra.scale = pro.scale;
-        ra.shift = pro.shift;
-        ra.silu = true;
-        ra.rows_per_item = x.h * x.w;
-        const bool skip = ci == co;
-        conv1x1(e.ctx, mid.p, mid.px(), ci, pw.w.p, pw.w.wt, co, pw.b, skip ? x.p : nullptr, out.p,
-                GemmEpilogue::None, skip && gn ? &ra : nullptr, res2);
+        conv1x1(e.ctx, mid.p, mid.px(), ci, pw.w.p, pw.w.wt, co, pw.b, ci == co ? x.p : nullptr, out.p,
+                GemmEpilogue::None, nullptr, res2);
         e.pool.recycle(mid);
         return out;
     }
@@ -224,23 +210,23 @@ struct DwResnet {
         if (has_shortcut) shortcut.load(W, p + ".conv_shortcut", ci, co, true);
     }
     // temb_silu: [n, 1280] = SiLU(temb), shared by every resnet of the step.
-    // The GroupNorm outputs are never stored: each norm's scale/shift is applied
-    // inside the depthwise conv that reads it and to the DwConv2d skip, and the
-    // shortcut (or x) is added in conv2's pointwise epilogue.
+    // The shortcut (or x) is added in conv2's pointwise epilogue. (The GroupNorm
+    // outputs are written out: applying GN + SiLU inside the depthwise conv's
+    // loads re-evaluates SiLU for every tap, which costs more than the pass.)
     DT fwd(Env &e, const DT &x, const float *temb_silu) const {
-        float *gn1 = norm1.affine(e, x, nullptr);
-        DT b = conv1.fwd(e, x, gn1);
-        e.pool.recycle(gn1);
+        DT a = norm1.fwd(e, x, nullptr, true);
+        DT b = conv1.fwd(e, a);
+        e.pool.recycle(a);
         float *tp = e.pool.floats(int64_t(x.n) * co);
         temb_proj.fwd(e, temb_silu, x.n, tp);
-        float *gn2 = norm2.affine(e, b, tp);
+        a = norm2.fwd(e, b, tp, true);
         e.pool.recycle(tp);
+        e.pool.recycle(b);
         DT s;
         if (has_shortcut) s = shortcut.fwd(e, x);
-        DT out = conv2.fwd(e, b, gn2, has_shortcut ? s.p : x.p);
+        DT out = conv2.fwd(e, a, has_shortcut ? s.p : x.p);
         if (has_shortcut) e.pool.recycle(s);
-        e.pool.recycle(gn2);
-        e.pool.recycle(b);
+        e.pool.recycle(a);
         return out;
     }
 };
@@ -577,11 +563,11 @@ class UNetDevice {
             tr("unet.up." + std::to_string(i) + ".out", h);
         }
         if (!skips.empty()) fail(kInternal, "skip stack not consumed");
-        // norm_out + SiLU applied inside conv_out's depthwise; eps goes straight to the caller's buffer.
-        float *gn = norm_out_.affine(e, h, nullptr);
-        conv_out_.fwd(e, h, gn, nullptr, eps_dev);
-        pool_.recycle(gn);
+        // norm_out + SiLU, then conv_out straight into the caller's eps buffer.
+        DT a = norm_out_.fwd(e, h, nullptr, true);
         pool_.recycle(h);
+        conv_out_.fwd(e, a, nullptr, eps_dev);
+        pool_.recycle(a);
         pool_.recycle(temb);
         pool_.recycle(temb_silu);
         if (trace) {

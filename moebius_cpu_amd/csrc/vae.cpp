@@ -1,12 +1,13 @@
 // Device VAE: src/vae/{mod,encoder,decoder}.rs over the gfx950 kernels.
 //
-// Every GroupNorm + SiLU in front of a 3x3 conv is applied inside the conv's
-// input gather (scale/shift from the statistics pass), as the reference's
-// forward_prologue does; the resnet's identity add is the conv epilogue's
-// second residual. The mid attention keeps its whole 4096 x 4096 score matrix
-// per item in HBM: q.k^T on the matrix cores, the row softmax with the
-// reference's flush threshold, then P.v. The encoder runs its batch together
-// (the reference runs items one after the other; every statistic is per item).
+// Every GroupNorm + SiLU in front of a 3x3 conv is written out once (the
+// reference fuses it into the conv's gather to save CPU memory traffic; here
+// the gather would re-evaluate SiLU per tap and tile); the resnet's identity
+// add is the conv epilogue's second residual. The mid attention keeps its
+// whole 4096 x 4096 score matrix per item in HBM: q.k^T on the matrix cores,
+// the row softmax with the reference's flush threshold, then P.v. The encoder
+// runs its batch together (the reference runs items one after the other;
+// every statistic is per item).
 #include "vae.hpp"
 
 #include <cmath>
@@ -38,16 +39,9 @@ struct GNv {  // GroupNorm, eps 1e-6 (src/engine/norm.rs:22-105)
         g = W.get(p + ".weight", c, false).f();
         b = W.get(p + ".bias", c, false).f();
     }
-    // [scale | shift], each [n * c]
-    float *affine(Env &e, const DT &x) const {
-        float *ss = e.pool.floats(int64_t(2) * x.n * x.c);
-        group_norm_affine(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, VAE_EPS, g, b, nullptr, ss,
-                          ss + int64_t(x.n) * x.c);
-        return ss;
-    }
-    DT fwd(Env &e, const DT &x) const {
+    DT fwd(Env &e, const DT &x, bool silu = false) const {
         DT out = e.pool.tensor(x.n, x.h, x.w, x.c);
-        group_norm_forward(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, VAE_EPS, g, b, nullptr, false, out.p);
+        group_norm_forward(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, VAE_EPS, g, b, nullptr, silu, out.p);
         return out;
     }
 };
@@ -66,19 +60,22 @@ struct Conv3v {  // Conv3x3 (src/engine/conv.rs:60-102)
         w = W.get(p + ".weight", int64_t(co) * 9 * ci, true);
         b = W.get(p + ".bias", co, false).f();
     }
-    // gn: [scale | shift] of a GroupNorm + SiLU applied to x on the fly; res2 added last.
-    DT fwd(Env &e, const DT &x, const float *gn = nullptr, const float *res2 = nullptr,
-           float *out_p = nullptr) const {
+    // res2 (optional) added last: out = (bias + conv) + res2.
+    DT fwd(Env &e, const DT &x, const float *res2 = nullptr, float *out_p = nullptr) const {
         int ho, wo;
         conv3x3_output_hw(x.h, x.w, stride, pad, up, &ho, &wo);
         DT out = out_p ? DT{out_p, x.n, ho, wo, co} : e.pool.tensor(x.n, ho, wo, co);
-        Affine pro;
-        if (gn) {
-            pro.scale = gn;
-            pro.shift = gn + int64_t(x.n) * x.c;
-            pro.silu = true;
-        }
-        conv3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, w.p, w.wt, co, b, stride, pad, up, gn ? &pro : nullptr, out.p, res2);
+        conv3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, w.p, w.wt, co, b, stride, pad, up, nullptr, out.p, res2);
+        return out;
+    }
+    // conv(SiLU(GN(x))): the normalised map is written once and read by the conv.
+    // (Applying GN + SiLU inside the conv's gather, as the reference's
+    // forward_prologue does, re-evaluates SiLU for every tap and column tile:
+    // on the matrix cores that costs more than one extra pass over the map.)
+    DT fwd_gn(Env &e, const GNv &gn, const DT &x, const float *res2 = nullptr, float *out_p = nullptr) const {
+        DT a = gn.fwd(e, x, true);
+        DT out = fwd(e, a, res2, out_p);
+        e.pool.recycle(a);
         return out;
     }
 };
@@ -116,20 +113,16 @@ struct Resnet {
         if (has_sc) sc.load(W, p + ".conv_shortcut", ci, co);
     }
     DT fwd(Env &e, const DT &x) const {
-        float *gn1 = n1.affine(e, x);
-        DT h = c1.fwd(e, x, gn1);
-        e.pool.recycle(gn1);
-        float *gn2 = n2.affine(e, h);
+        DT h = c1.fwd_gn(e, n1, x);
         DT out;
         if (has_sc) {
             // h2 = conv2(...), then shortcut(x) with residual h2 (mod.rs:205-207)
-            DT h2 = c2.fwd(e, h, gn2);
+            DT h2 = c2.fwd_gn(e, n2, h);
             out = sc.fwd(e, x, h2.p);
             e.pool.recycle(h2);
         } else {
-            out = c2.fwd(e, h, gn2, x.p);  // conv2 + x (mod.rs:209)
+            out = c2.fwd_gn(e, n2, h, x.p);  // conv2 + x (mod.rs:209)
         }
-        e.pool.recycle(gn2);
         e.pool.recycle(h);
         return out;
     }
@@ -309,9 +302,7 @@ class VaeDevice {
         DT m = e_mid_.fwd(e, cur);
         pool_.recycle(cur);
         tr(".mid", m);
-        float *gn = e_norm_.affine(e, m);
-        DT o = e_out_.fwd(e, m, gn);
-        pool_.recycle(gn);
+        DT o = e_out_.fwd_gn(e, e_norm_, m);
         pool_.recycle(m);
         DT moments = quant_.fwd(e, o);
         pool_.recycle(o);
@@ -351,9 +342,7 @@ class VaeDevice {
             }
             tr(("vae.decoder.up." + std::to_string(i)).c_str(), cur);
         }
-        float *gn = d_norm_.affine(e, cur);
-        DT o = d_out_.fwd(e, cur, gn, nullptr, out);
-        pool_.recycle(gn);
+        DT o = d_out_.fwd_gn(e, d_norm_, cur, nullptr, out);
         pool_.recycle(cur);
         vae_rescale(ctx_, o.p, o.numel(), 1, out);
     }

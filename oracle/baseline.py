@@ -56,9 +56,31 @@ def conv3x3_gn_silu(budget_s: float):
     return ms, runs, f"full workload, median of {runs} runs after one warm-up"
 
 
+def vae_decode(budget_s: float):
+    from moebius_cpu_amd import synthetic as S
+    from moebius_cpu_amd import vae_params as V
+
+    vae = oracle.Vae(V.random_vae())
+    lat = S.normal(24, (1, 64, 64, 4))
+    ms, runs = _time(lambda: vae.decode(lat), budget_s, 1, 3)
+    return ms, runs, f"the same decode ([1,64,64,4] -> [1,512,512,3]), median of {runs} runs after one warm-up"
+
+
+def vae_encode(budget_s: float):
+    from moebius_cpu_amd import synthetic as S
+    from moebius_cpu_amd import vae_params as V
+
+    vae = oracle.Vae(V.random_vae())
+    images = V.vae_images(seed=25, b=2, h=512, w=512)
+    noise = S.normal(26, (2, 64, 64, 4))
+    ms, runs = _time(lambda: vae.encode(images, noise), budget_s, 1, 3)
+    return ms, runs, f"the same encode (2 x [512,512,3]), median of {runs} runs after one warm-up"
+
+
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--workload", default="unet_step", choices=["unet_step", "conv3x3_gn_silu"])
+    ap.add_argument("--workload", default="unet_step",
+                    choices=["unet_step", "conv3x3_gn_silu", "vae_decode", "vae_encode"])
     ap.add_argument("--threads", type=int, default=0)
     ap.add_argument("--cond-only", action="store_true")
     ap.add_argument("--budget-s", type=float, default=20.0)
@@ -67,6 +89,10 @@ def main():
         oracle.set_threads(args.threads)
     if args.workload == "unet_step":
         ms, runs, sample = unet_step(not args.cond_only, args.budget_s)
+    elif args.workload == "vae_decode":
+        ms, runs, sample = vae_decode(args.budget_s)
+    elif args.workload == "vae_encode":
+        ms, runs, sample = vae_encode(args.budget_s)
     else:
         ms, runs, sample = conv3x3_gn_silu(args.budget_s)
     print(json.dumps({"value": round(ms, 3), "unit": "ms", "cores": oracle.threads(), "runs": runs,

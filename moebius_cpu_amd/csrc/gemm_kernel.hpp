@@ -492,13 +492,17 @@ struct Plan {
     int bm, bn, splits, k_split;
 };
 
-// Tile shape and K split, from a sweep of every (tile, split) on MI355X over
-// the UNet's GEMM shapes (M 2..65536, N 4..6400, K 9..11520):
+// Tile shape and K split, from sweeps of every (tile, split) on MI355X over
+// the UNet's GEMM shapes (M 2..65536, N 4..6400, K 9..11520) and the VAE's
+// convs (M up to 262144, K 1152..4608):
+//  - Many 128x128 tiles (two per CU or more) and K >= 1024: 128x128, no split
+//    (71-80% of f32 MFMA peak on the VAE's 3x3 convs, against 60-77% at 64x64).
 //  - Long K (>= 4096, the upsample / downsample convs): 128x128 tiles, K split
 //    in 3; 75-77% of f32 MFMA peak, against 67% unsplit.
 //  - Otherwise 64x64 tiles, several co-resident workgroups per CU hiding load
-//    latency: K is split only while the grid is under twice the CU count and
-//    each split keeps at least 8 K tiles.
+//    latency: K is split only while the grid is under three times the CU count and
+//    each split keeps at least 8 K tiles (measured: the UNet's 160-320-tile
+//    GEMMs lose 15-25% unsplit, more than the reduction launch costs).
 inline Plan plan_for(int M, int N, int K, int cus) {
     const int ktiles = int(ceil_div(K, BK));
     auto split = [&](int64_t tiles, int64_t target, int max_splits) {
@@ -508,11 +512,13 @@ inline Plan plan_for(int M, int N, int K, int cus) {
         const int per = int(ceil_div(ktiles, want));
         return std::make_pair(int(ceil_div(ktiles, per)), per * BK);
     };
+    const int64_t t128 = ceil_div(M, 128) * ceil_div(N, 128);
+    if (K >= 1024 && t128 >= 2 * int64_t(cus)) return Plan{128, 128, 1, K};  // VAE-sized convs: 71-80%
     if (K >= 4096 && M >= 1024) {
-        const auto s = split(ceil_div(M, 128) * ceil_div(N, 128), 3 * int64_t(cus), 3);
+        const auto s = split(t128, 3 * int64_t(cus), 3);
         return Plan{128, 128, s.first, s.second};
     }
-    const auto s = split(ceil_div(M, 64) * ceil_div(N, 64), 2 * int64_t(cus), 6);
+    const auto s = split(ceil_div(M, 64) * ceil_div(N, 64), 3 * int64_t(cus), 6);
     return Plan{64, 64, s.first, s.first > 1 ? s.second : K};
 }
 

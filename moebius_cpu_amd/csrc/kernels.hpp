@@ -34,12 +34,15 @@ void to_u8(Context &ctx, const float *x, int64_t len, uint8_t *out);
 void math_eval(Context &ctx, int which, const float *x, int64_t len, float *y);
 
 // ---- normalisation (norm.hip) ----
+// add (optional): per item and channel, item b's row at add + b * add_ld (add_ld 0: c).
 void group_norm_affine(Context &ctx, const float *x, int n, int h, int w, int c, int groups, float eps,
-                       const float *gamma, const float *beta, const float *add, float *scale, float *shift);
+                       const float *gamma, const float *beta, const float *add, float *scale, float *shift,
+                       int64_t add_ld = 0);
 void apply_affine(Context &ctx, const float *x, int n, int h, int w, int c, const float *scale, const float *shift,
                   bool silu, float *out);
 void group_norm_forward(Context &ctx, const float *x, int n, int h, int w, int c, int groups, float eps,
-                        const float *gamma, const float *beta, const float *add, bool silu, float *out);
+                        const float *gamma, const float *beta, const float *add, bool silu, float *out,
+                        int64_t add_ld = 0);
 void layer_norm(Context &ctx, const float *x, int64_t rows, int c, const float *gamma, const float *beta, float eps,
                 float *out);
 // Per-row (mean, rstd) of LayerNorm for consumers that apply it themselves: stats [rows][2].

@@ -81,9 +81,14 @@ __global__ __launch_bounds__(256) void lambda_partial_kernel(const float *__rest
     const int nr = min(ch, rows - r0);
     for (int j = threadIdx.x; j < k; j += 256) {
         const float *pm = pmax + size_t(b) * chunks * k + j;
-        float m = -INFINITY;
-        for (int c = 0; c < chunks; ++c) m = fmaxf(m, pm[size_t(c) * k]);
-        mx[j] = m;
+        // eight chunk maxima in flight per step (the maximum is order-free)
+        float m[8] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY, -INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        for (int c0 = 0; c0 < chunks; c0 += 8) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                m[u] = fmaxf(m[u], pm[size_t(min(c0 + u, chunks - 1)) * k]);  // a repeat is harmless
+        }
+        mx[j] = fmaxf(fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3])), fmaxf(fmaxf(m[4], m[5]), fmaxf(m[6], m[7])));
     }
     __syncthreads();
     const float *kb = keys + (size_t(b) * rows + r0) * k;

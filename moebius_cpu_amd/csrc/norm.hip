@@ -11,6 +11,8 @@
 // one (item, group) per block with a fixed-order tree, so results are
 // deterministic. The apply pass is a separate kernel, or is fused into the
 // consumer (the depthwise and GEMM prologues) with the scale/shift produced here.
+#include <cstdlib>
+
 #include "common.hpp"
 #include "dmath.hpp"
 #include "kernels.hpp"
@@ -22,17 +24,27 @@ constexpr int kGnTileC = 64;   // channels per block: 16 lanes x float4
 constexpr int kGnRows = 16;    // pixel rows per block pass
 
 // Pixels per statistics chunk: 64, doubled until the partials grid is at most
-// ~4096 blocks, so small maps get many blocks and 512x512 maps moderate ones.
+// kGnMaxBlocks blocks, so small maps get many blocks and large maps few
+// enough partials for the fold to stay short.
+int gn_max_blocks() {
+    static const int v = [] {
+        const char *e = std::getenv("MOEBIUS_HIP_GN_BLOCKS");  // tuning override
+        const int b = e ? std::atoi(e) : 0;
+        return b >= 64 ? b : 512;  // 512x512x128: 4096 blocks 78 us, 512 blocks 66 us (stats + SiLU apply)
+    }();
+    return v;
+}
+
 int gn_chunk_px(int n, int hw, int c) {
     const int64_t ctiles = ceil_div(c, kGnTileC);
     int chunk = 64;
-    while (chunk < hw && ceil_div(hw, chunk) * ctiles * n > 4096) chunk *= 2;
+    while (chunk < hw && ceil_div(hw, chunk) * ctiles * n > gn_max_blocks()) chunk *= 2;
     return chunk;
 }
 
 // part [n][chunks][c][2] = per-channel (sum y, sum y*y) over the chunk, y = x (+ add).
 __global__ __launch_bounds__(256) void gn_partial_kernel(const float *__restrict__ x, const float *__restrict__ add,
-                                                         int hw, int c, int chunk_px, int nchunks,
+                                                         int64_t add_ld, int hw, int c, int chunk_px, int nchunks,
                                                          float *__restrict__ part) {
     const int chunk = blockIdx.x, ct = blockIdx.y, b = blockIdx.z;
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
@@ -40,7 +52,7 @@ __global__ __launch_bounds__(256) void gn_partial_kernel(const float *__restrict
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f), q = s;
     if (c0 < c) {
         float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (add) a = *reinterpret_cast<const float4 *>(add + size_t(b) * c + c0);
+        if (add) a = *reinterpret_cast<const float4 *>(add + size_t(b) * add_ld + c0);
         const float *xb = x + size_t(b) * hw * c + c0;
         const int p1 = min(hw, (chunk + 1) * chunk_px);
 #pragma unroll 4
@@ -86,7 +98,8 @@ __global__ __launch_bounds__(256) void gn_partial_kernel(const float *__restrict
 
 // One block per (group, item): f64 fold of the group's partials, then scale/shift.
 __global__ __launch_bounds__(256) void gn_finalize_kernel(const float *__restrict__ part, const float *__restrict__ add,
-                                                          int hw, int c, int nchunks, int groups, float eps,
+                                                          int64_t add_ld, int hw, int c, int nchunks, int groups,
+                                                          float eps,
                                                           const float *__restrict__ gamma,
                                                           const float *__restrict__ beta, float *__restrict__ scale,
                                                           float *__restrict__ shift) {
@@ -122,7 +135,7 @@ __global__ __launch_bounds__(256) void gn_finalize_kernel(const float *__restric
     for (int j = threadIdx.x; j < cg; j += 256) {
         const int ch = g * cg + j;
         const double sc = rstd * double(gamma[ch]);
-        const double pre = add ? double(add[size_t(b) * c + ch]) : 0.0;
+        const double pre = add ? double(add[size_t(b) * add_ld + ch]) : 0.0;
         scale[size_t(b) * c + ch] = float(sc);
         shift[size_t(b) * c + ch] = float(double(beta[ch]) + (pre - mean) * sc);
     }
@@ -167,9 +180,11 @@ template <int ITER>
 __global__ __launch_bounds__(256) void affine_apply_kernel(const float4 *__restrict__ x,
                                                            const float4 *__restrict__ scale,
                                                            const float4 *__restrict__ shift, int item4, int c4,
-                                                           int silu, float4 *__restrict__ out) {
+                                                           int silu, int reverse, float4 *__restrict__ out) {
     const int b = blockIdx.y;
-    const int e0 = blockIdx.x * (256 * ITER) + threadIdx.x;
+    // reverse: blocks walk the map from its end, where the statistics pass read last.
+    const int bx = reverse ? int(gridDim.x) - 1 - int(blockIdx.x) : int(blockIdx.x);
+    const int e0 = bx * (256 * ITER) + threadIdx.x;
     if (e0 >= item4) return;
     const size_t base = size_t(b) * item4;
     int q = e0 % c4;
@@ -293,7 +308,10 @@ __global__ __launch_bounds__(256) void layer_norm_generic_kernel(const float *__
 }  // namespace
 
 void group_norm_affine(Context &ctx, const float *x, int n, int h, int w, int c, int groups, float eps,
-                       const float *gamma, const float *beta, const float *add, float *scale, float *shift) {
+                       const float *gamma, const float *beta, const float *add, float *scale, float *shift,
+                       int64_t add_ld) {
+    if (add_ld <= 0) add_ld = c;
+    MH_REQUIRE(add_ld % 4 == 0, "GroupNorm: add row stride must be a multiple of 4");
     MH_REQUIRE(groups > 0 && c % groups == 0, "channels not divisible by groups");
     MH_REQUIRE(c % 4 == 0, "GroupNorm: channel count must be a multiple of 4 on the GPU path");
     MH_REQUIRE(n > 0 && h > 0 && w > 0, "GroupNorm: empty tensor");
@@ -303,10 +321,11 @@ void group_norm_affine(Context &ctx, const float *x, int n, int h, int w, int c,
     const int nchunks = int(ceil_div(hw, chunk_px));
     const int nctiles = int(ceil_div(c, kGnTileC));
     float *part = static_cast<float *>(ctx.ws.get(size_t(n) * nchunks * c * 2 * sizeof(float), ctx.stream));
-    gn_partial_kernel<<<dim3(nchunks, nctiles, n), 256, 0, ctx.stream>>>(x, add, hw, c, chunk_px, nchunks, part);
+    gn_partial_kernel<<<dim3(nchunks, nctiles, n), 256, 0, ctx.stream>>>(x, add, add_ld, hw, c, chunk_px, nchunks,
+                                                                        part);
     MH_LAUNCH_CHECK();
-    gn_finalize_kernel<<<dim3(groups, n), 256, 0, ctx.stream>>>(part, add, hw, c, nchunks, groups, eps, gamma, beta,
-                                                                scale, shift);
+    gn_finalize_kernel<<<dim3(groups, n), 256, 0, ctx.stream>>>(part, add, add_ld, hw, c, nchunks, groups, eps, gamma,
+                                                                beta, scale, shift);
     MH_LAUNCH_CHECK();
 }
 
@@ -333,9 +352,14 @@ void apply_affine(Context &ctx, const float *x, int n, int h, int w, int c, cons
         constexpr int ITER = 8;
         const int item4 = int(item / 4);
         dim3 grid(unsigned(ceil_div(item4, 256 * ITER)), n);
+        static const int reverse = [] {
+            const char *e = std::getenv("MOEBIUS_HIP_GN_REVERSE");  // tuning override
+            return e ? std::atoi(e) : 0;
+        }();
         affine_apply_kernel<ITER><<<grid, 256, 0, ctx.stream>>>(
             reinterpret_cast<const float4 *>(x), reinterpret_cast<const float4 *>(scale),
-            reinterpret_cast<const float4 *>(shift), item4, c / 4, silu ? 1 : 0, reinterpret_cast<float4 *>(out));
+            reinterpret_cast<const float4 *>(shift), item4, c / 4, silu ? 1 : 0, reverse,
+            reinterpret_cast<float4 *>(out));
     } else {
         const int64_t total = item * n;
         const int blocks = int(std::min<int64_t>(ceil_div(total, 256), 65536));
@@ -345,7 +369,10 @@ void apply_affine(Context &ctx, const float *x, int n, int h, int w, int c, cons
 }
 
 void group_norm_forward(Context &ctx, const float *x, int n, int h, int w, int c, int groups, float eps,
-                        const float *gamma, const float *beta, const float *add, bool silu, float *out) {
+                        const float *gamma, const float *beta, const float *add, bool silu, float *out,
+                        int64_t add_ld) {
+    if (add_ld <= 0) add_ld = c;
+    MH_REQUIRE(groups > 0 && c % groups == 0, "channels not divisible by groups");
     // scale/shift live in the tail of the workspace's partial block.
     const size_t part_bytes =
         size_t(n) * ceil_div(int64_t(h) * w, gn_chunk_px(n, h * w, c)) * c * 2 * sizeof(float);
@@ -353,7 +380,7 @@ void group_norm_forward(Context &ctx, const float *x, int n, int h, int w, int c
     char *ws = static_cast<char *>(ctx.ws.get(aff_off + size_t(n) * c * 2 * sizeof(float), ctx.stream));
     float *scale = reinterpret_cast<float *>(ws + aff_off);
     float *shift = scale + size_t(n) * c;
-    group_norm_affine(ctx, x, n, h, w, c, groups, eps, gamma, beta, add, scale, shift);
+    group_norm_affine(ctx, x, n, h, w, c, groups, eps, gamma, beta, add, scale, shift, add_ld);
     apply_affine(ctx, x, n, h, w, c, scale, shift, silu, out);
 }
 

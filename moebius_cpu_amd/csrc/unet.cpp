@@ -141,9 +141,9 @@ struct GN {
         g = W.get(p + ".weight", c, false).f();
         b = W.get(p + ".bias", c, false).f();
     }
-    DT fwd(Env &e, const DT &x, const float *add, bool silu) const {
+    DT fwd(Env &e, const DT &x, const float *add, bool silu, int64_t add_ld = 0) const {
         DT out = e.pool.tensor(x.n, x.h, x.w, x.c);
-        group_norm_forward(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, eps, g, b, add, silu, out.p);
+        group_norm_forward(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, eps, g, b, add, silu, out.p, add_ld);
         return out;
     }
     // Statistics only: [scale | shift], each [n * c], for a consumer that applies them.
@@ -199,6 +199,7 @@ struct DwResnet {
     DwConv2d conv1, conv2;
     Lin temb_proj, shortcut;
     bool has_shortcut = false;
+    int temb_off = 0;  // this block's columns in the step's batched time projection
     void load(const WeightStore &W, const std::string &p, int ci_, int co_) {
         ci = ci_, co = co_;
         norm1.load(W, p + ".norm1", ci, RESNET_EPS);
@@ -210,17 +211,16 @@ struct DwResnet {
         if (has_shortcut) shortcut.load(W, p + ".conv_shortcut", ci, co, true);
     }
     // temb_silu: [n, 1280] = SiLU(temb), shared by every resnet of the step.
-    // The shortcut (or x) is added in conv2's pointwise epilogue. (The GroupNorm
+    // tp: this block's time projection, item i's row at tp + i * tp_ld (all the
+    // step's projections come out of one GEMM, UNetDevice::forward). The
+    // shortcut (or x) is added in conv2's pointwise epilogue. (The GroupNorm
     // outputs are written out: applying GN + SiLU inside the depthwise conv's
     // loads re-evaluates SiLU for every tap, which costs more than the pass.)
-    DT fwd(Env &e, const DT &x, const float *temb_silu) const {
+    DT fwd(Env &e, const DT &x, const float *tp, int64_t tp_ld) const {
         DT a = norm1.fwd(e, x, nullptr, true);
         DT b = conv1.fwd(e, a);
         e.pool.recycle(a);
-        float *tp = e.pool.floats(int64_t(x.n) * co);
-        temb_proj.fwd(e, temb_silu, x.n, tp);
-        a = norm2.fwd(e, b, tp, true);
-        e.pool.recycle(tp);
+        a = norm2.fwd(e, b, tp, true, tp_ld);
         e.pool.recycle(b);
         DT s;
         if (has_shortcut) s = shortcut.fwd(e, x);
@@ -470,6 +470,31 @@ class UNetDevice {
             }
             up_.push_back(std::move(blk));
         }
+        // Every resnet's time_emb_proj in one [sum c_out][1280] matrix (and bias),
+        // so a step projects the time embedding for all of them in one GEMM.
+        {
+            std::vector<DwResnet *> rs;
+            for (auto *v : {&down_, &up_})
+                for (auto &blk : *v)
+                    for (auto &r : blk.res) rs.push_back(&r);
+            temb_wt_ = rs.front()->temb_proj.w.wt;
+            temb_total_ = 0;
+            for (DwResnet *r : rs) {
+                if (r->temb_proj.w.wt != temb_wt_) fail(kWeights, "time_emb_proj weights must share one dtype");
+                r->temb_off = temb_total_;
+                temb_total_ += r->co;
+            }
+            const size_t esz = temb_wt_ == kF16 ? 2 : 4;
+            HIP_CHECK(hipMalloc(&temb_w_, size_t(temb_total_) * TIME_EMBED * esz));
+            HIP_CHECK(hipMalloc(&temb_b_, size_t(temb_total_) * sizeof(float)));
+            for (DwResnet *r : rs) {
+                HIP_CHECK(hipMemcpyAsync(static_cast<char *>(temb_w_) + size_t(r->temb_off) * TIME_EMBED * esz,
+                                         r->temb_proj.w.p, size_t(r->co) * TIME_EMBED * esz, hipMemcpyDeviceToDevice,
+                                         ctx_.stream));
+                HIP_CHECK(hipMemcpyAsync(temb_b_ + r->temb_off, r->temb_proj.b, size_t(r->co) * sizeof(float),
+                                         hipMemcpyDeviceToDevice, ctx_.stream));
+            }
+        }
         lin1_.load(W_, d + ".time_embedding.linear_1", TIME_PROJ, TIME_EMBED, true);
         lin2_.load(W_, d + ".time_embedding.linear_2", TIME_EMBED, TIME_EMBED, true);
         conv_in_.load(W_, d + ".conv_in", 9, CH[0]);
@@ -486,6 +511,8 @@ class UNetDevice {
             for (auto &b : *v)
                 for (auto &a : b.attn) a.release();
         if (sinus_dev_) (void)hipFree(sinus_dev_);
+        if (temb_w_) (void)hipFree(temb_w_);
+        if (temb_b_) (void)hipFree(temb_b_);
     }
 
     // src/unet/mod.rs:150-243
@@ -515,6 +542,9 @@ class UNetDevice {
         HIP_CHECK(hipMemcpyAsync(temb_silu, temb.p, size_t(b) * TIME_EMBED * sizeof(float), hipMemcpyDeviceToDevice,
                                  ctx_.stream));
         silu_inplace(ctx_, temb_silu, int64_t(b) * TIME_EMBED);
+        // all resnets' time projections: tp [b][temb_total_]
+        float *tp = pool_.floats(int64_t(b) * temb_total_);
+        conv1x1(ctx_, temb_silu, b, TIME_EMBED, temb_w_, temb_wt_, temb_total_, temb_b_, nullptr, tp);
 
         DT input = pool_.tensor(b, 64, 64, 9);
         for (int i = 0; i < b; ++i)
@@ -526,7 +556,8 @@ class UNetDevice {
         tr("unet.conv_in", skips.back());
         for (size_t i = 0; i < down_.size(); ++i) {
             for (size_t j = 0; j < down_[i].res.size(); ++j) {
-                DT a = down_[i].res[j].fwd(e, skips.back(), temb_silu);
+                const DwResnet &r = down_[i].res[j];
+                DT a = r.fwd(e, skips.back(), tp + r.temb_off, temb_total_);
                 tr("unet.down." + std::to_string(i) + ".res." + std::to_string(j), a);
                 DT h = down_[i].attn[j].fwd(e, a, br0);
                 pool_.recycle(a);
@@ -548,7 +579,8 @@ class UNetDevice {
                 concat_channels(ctx_, h.p, h.c, skip.p, skip.c, h.px(), cat.p);
                 pool_.recycle(skip);
                 pool_.recycle(h);
-                DT a = up_[i].res[j].fwd(e, cat, temb_silu);
+                const DwResnet &r = up_[i].res[j];
+                DT a = r.fwd(e, cat, tp + r.temb_off, temb_total_);
                 pool_.recycle(cat);
                 tr("unet.up." + std::to_string(i) + ".res." + std::to_string(j), a);
                 h = up_[i].attn[j].fwd(e, a, br0);
@@ -570,6 +602,7 @@ class UNetDevice {
         pool_.recycle(a);
         pool_.recycle(temb);
         pool_.recycle(temb_silu);
+        pool_.recycle(tp);
         if (trace) {
             DT o{eps_dev, b, 64, 64, 4};
             tr("unet.out", o);
@@ -594,6 +627,10 @@ class UNetDevice {
     DwConv2d conv_in_, conv_out_;
     GN norm_out_;
     float *sinus_dev_ = nullptr;
+    void *temb_w_ = nullptr;  // [temb_total_][1280]: every resnet's time_emb_proj.weight
+    float *temb_b_ = nullptr;
+    WeightType temb_wt_ = kF32;
+    int temb_total_ = 0;
 };
 
 UNet::UNet(Context &ctx, const NamedTensor *t, int count) : d_(new UNetDevice(ctx, t, count)) {}

@@ -141,6 +141,35 @@ def _components(ctx, steps):
             "groupnorm_hbm_frac": round(gn_gbps / PEAK_HBM_GBPS, 4)}
 
 
+# HBM bytes per launch of the dominant kernel (below), from rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE over one UNet step, each scaled by the counter's reading for a plain
+# 256 MiB device copy (FETCH_SIZE reads half the copied bytes, WRITE_SIZE all of them):
+# 19.70 MiB fetched + 10.00 MiB written per launch.
+DOMINANT_TRAFFIC_BYTES = int((19.70 + 10.00) * 1048576)
+
+
+def _dominant_gemm(ctx, steps):
+    """The step's most frequent GEMM, timed on its own with events: the 1x1 conv of
+    a [2,64,64,320] map to 320 channels with bias (gemm_f32_kernel, 64x64 tiles,
+    640 workgroups), i.e. M = 8192, N = 320, K = 320."""
+    from moebius_cpu_amd import engine as E
+    from moebius_cpu_amd import synthetic as S
+
+    x = E.Tensor.from_numpy(ctx, S.normal(81, (2, 64, 64, 320)))
+    conv = E.Conv1x1(ctx, 320, 320, E.Param(ctx, S.normal(82, (320, 320), 0.05)), S.normal(83, (320,), 0.02))
+    y = E.Tensor(ctx)
+    conv.forward(x, y)
+    us = time_region(ctx, lambda: conv.forward(x, y), steps) * 1e3
+    flops = 2.0 * 8192 * 320 * 320
+    tf = flops / (us * 1e-6) / 1e12
+    return {"bound": "mfma", "kernel": "gemm_f32_kernel<64,64,dense> (1x1 conv [2,64,64,320] -> 320, "
+                                       "M=8192 N=320 K=320: the step's most frequent GEMM)",
+            "achieved": round(tf, 2), "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(tf / PEAK_F32_MFMA_TFLOPS, 4), "traffic": DOMINANT_TRAFFIC_BYTES,
+            "work_per_launch": f"{flops / 1e9:.3f} GFLOP; algorithmic bytes {(8192 * 320 * 2 + 320 * 320) * 4}",
+            "avg_launch_us": round(us, 2)}
+
+
 def bench_unet(args):
     """One full 512^2 denoise step: 64x64x9 latent stack, CFG batch 2, f32 Exact."""
     from moebius_cpu_amd import engine as E
@@ -174,13 +203,13 @@ def bench_unet(args):
                                f"{'f16-stored GEMM weights, ' if args.f16_weights else ''}f32 arithmetic",
                    "latent": [1, 64, 64, 9], "batch": b, "timestep": inp.timestep,
                    "params_M": round(U.param_count() / 1e6, 1), "weight_bytes": wbytes, "pool_bytes": pbytes},
-        "roofline": {"bound": "mfma", "kernel": "whole step (all kernels, one stream)",
-                     "achieved": round(achieved, 2), "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_F32_MFMA_TFLOPS, 4), "traffic": None,
-                     "work_per_launch": f"{flops['total'] / 1e9:.1f} GFLOP per step",
-                     "avg_launch_ms": round(ms, 4)},
+        "step_roofline": {"bound": "mfma", "kernel": "whole step (all kernels, one stream)",
+                          "achieved": round(achieved, 2), "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                          "frac": round(achieved / PEAK_F32_MFMA_TFLOPS, 4),
+                          "work": f"{flops['total'] / 1e9:.1f} GFLOP per step"},
     }
-    log("component kernels")
+    log("dominant kernel and component kernels")
+    out["roofline"] = _dominant_gemm(ctx, 50)
     out["components"] = _components(ctx, 20)
     del net, x, eps
     ctx.close()

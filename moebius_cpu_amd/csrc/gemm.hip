@@ -102,6 +102,35 @@ void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void 
         launch_dense(ctx, p, wt, epi, 1, false);
 }
 
+void conv1x1_segments(Context &ctx, const float *x, int64_t pixels, int c_in, const void *weight, WeightType wt,
+                      const float *bias, int nseg, const int *widths, float *const *outs) {
+    MH_REQUIRE(nseg >= 1 && nseg <= kMaxSeg, "Conv1x1 segments: 1 to 3 outputs");
+    MH_REQUIRE(pixels < (int64_t(1) << 31), "Conv1x1: too many pixels");
+    if (pixels == 0) return;
+    GemmArgs p{};
+    p.a = x;
+    p.lda = c_in;
+    p.M = int(pixels);
+    int n = 0;
+    p.nseg = nseg;
+    for (int i = 0; i < nseg; ++i) {
+        MH_REQUIRE(widths[i] > 0 && outs[i], "Conv1x1 segments: empty segment");
+        p.seg_col[i] = n;
+        p.seg_out[i] = outs[i];
+        n += widths[i];
+    }
+    p.seg_col[nseg] = n;
+    p.N = n;
+    p.K = c_in;
+    p.b = weight;
+    p.ldb = c_in;
+    p.a_bytes = extent(pixels, c_in, c_in, 4);
+    p.b_bytes = extent(n, c_in, c_in, wt == kF16 ? 2 : 4);
+    p.bias = bias;
+    p.ldc = n;
+    launch_dense(ctx, p, wt, GemmEpilogue::None, 1, c_in % 4 == 0 && aligned16(x));
+}
+
 void gemm_nt(Context &ctx, const float *a, int64_t lda, int64_t a_bs, const void *b, WeightType wt, int64_t ldb,
              int64_t b_bs, int m, int n, int k, int batch, const float *bias, const float *residual, float *out,
              int64_t ldc, int64_t c_bs, GemmEpilogue epi, int row_group) {

@@ -24,6 +24,7 @@ typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
 constexpr int BK = 32;          // K per LDS stage
 constexpr int LDS_S = BK + 4;   // padded LDS row stride (floats): conflict-free b128 reads
 constexpr int K4 = BK / 4;      // float4 per tile row
+constexpr int kMaxSeg = 3;      // column segments of a segmented output
 
 // Matrix instruction: v_mfma_f32_16x16x4f32 (MF = 16) or v_mfma_f32_32x32x2f32
 // (MF = 32). Output lane layouts: 16x16: register v of lane l is row
@@ -82,6 +83,10 @@ struct GemmArgs {
     int rsilu, r_rows;
     // second residual, added last: y = y + res2
     const float *res2;
+    // column segments (0: one output): see out_ptr
+    int nseg;
+    int seg_col[kMaxSeg + 1];
+    float *seg_out[kMaxSeg];
     // byte extents of one item's A (or conv input) and of B, for the buffer
     // loads' range check (< 2^31): an access at or past the extent reads zero
     uint32_t a_bytes, b_bytes;
@@ -119,6 +124,32 @@ namespace {
 __device__ __forceinline__ int64_t out_index(const GemmArgs &p, int row, int col) {
     if (p.rg > 1) return int64_t(row / p.rg) * p.ldc + int64_t(col) * p.rg + row % p.rg;
     return int64_t(row) * p.ldc + col;
+}
+
+// Column-segmented output: columns [seg_col[s], seg_col[s+1]) go to their own
+// row-major buffer seg_out[s] (leading dimension = segment width), so one GEMM
+// over concatenated weights fills several separate tensors.
+__device__ __forceinline__ float *out_ptr(const GemmArgs &p, int row, int col, int64_t &o) {
+    if (p.nseg == 0) {
+        o = out_index(p, row, col);
+        return p.out;
+    }
+    // constant indices only: a runtime index into the by-value arguments would
+    // move them to scratch memory
+    float *dst = p.seg_out[0];
+    int c0 = 0, c1 = p.seg_col[1];
+    if (p.nseg > 1 && col >= p.seg_col[1]) {
+        dst = p.seg_out[1];
+        c0 = p.seg_col[1];
+        c1 = p.seg_col[2];
+    }
+    if (p.nseg > 2 && col >= p.seg_col[2]) {
+        dst = p.seg_out[2];
+        c0 = p.seg_col[2];
+        c1 = p.seg_col[3];
+    }
+    o = int64_t(row) * (c1 - c0) + (col - c0);
+    return dst;
 }
 
 __device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
@@ -466,8 +497,9 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
                 if (SPLIT) {
                     p.partial[(int64_t(blockIdx.z) * p.M + row) * p.N + col] = r;
                 } else {
-                    const int64_t o = out_index(p, row, col);
-                    p.out[o] = epilogue_value<EPI>(p, row, col, o, r, bcol);
+                    int64_t o;
+                    float *dst = out_ptr(p, row, col, o);
+                    dst[o] = epilogue_value<EPI>(p, row, col, o, r, bcol);
                 }
             }
         }
@@ -483,8 +515,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int spli
         for (int z = 1; z < splits; ++z) s += p.partial[int64_t(z) * total + e];
         const int row = int(e / p.N);
         const int col = int(e - int64_t(row) * p.N);
-        const int64_t o = out_index(p, row, col);
-        p.out[o] = epilogue_value<EPI>(p, row, col, o, s, p.bias ? p.bias[col] : 0.0f);
+        int64_t o;
+        float *dst = out_ptr(p, row, col, o);
+        dst[o] = epilogue_value<EPI>(p, row, col, o, s, p.bias ? p.bias[col] : 0.0f);
     }
 }
 

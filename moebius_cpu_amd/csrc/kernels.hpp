@@ -70,6 +70,10 @@ void conv3x3(Context &ctx, const float *x, int n, int h, int w, int c_in, const 
              int c_out, const float *bias, int stride, const int pad[4], bool upsample2x, const Affine *prologue,
              float *out, const float *residual2 = nullptr);
 void conv3x3_output_hw(int h, int w, int stride, const int pad[4], bool upsample2x, int *ho, int *wo);
+// One 1x1 conv over concatenated weights [sum widths][c_in] (bias [sum widths] or NULL)
+// whose output columns land in nseg (<= 3) separate [pixels][widths[i]] buffers.
+void conv1x1_segments(Context &ctx, const float *x, int64_t pixels, int c_in, const void *weight, WeightType wt,
+                      const float *bias, int nseg, const int *widths, float *const *outs);
 // C[z] = A[z] . B[z]^T (+ bias) (+ residual[z]) [SiLU] for z < batch, all K-contiguous:
 // A [m][lda], B [n][ldb], C [m][ldc]; *_bs are per-item element offsets.
 // row_group g > 1 stores row m, column n at (m / g) * ldc + n * g + m % g.

@@ -236,6 +236,9 @@ struct SelfLambda {
     int c = 0, k = 0;
     Lin to_q, to_k, to_v;
     float *w_aug_t = nullptr;  // [226][k]: column d of the folded filter per row
+    void *wqkv = nullptr;      // [c + 2k][c]: to_q | to_k | to_v
+    float *bqkv = nullptr;
+    WeightType wt = kF32;
     void load(Env &e, const WeightStore &W, const std::string &p, int c_) {
         c = c_, k = c / HEADS;
         std::vector<float> s1, s2;
@@ -251,18 +254,44 @@ struct SelfLambda {
         to_q.load(W, p + ".to_q", c, c, true);
         to_k.load(W, p + ".to_k", c, k, false);
         to_v.load(W, p + ".to_v", c, k, true);
-        (void)e;
+        // q | k | v weights [c + 2k][c] and bias (k has none: zeros), for one GEMM.
+        wt = to_q.w.wt;
+        if (to_k.w.wt != wt || to_v.w.wt != wt) fail(kWeights, "lambda q/k/v weights must share one dtype");
+        const size_t esz = wt == kF16 ? 2 : 4;
+        HIP_CHECK(hipMalloc(&wqkv, size_t(c + 2 * k) * c * esz));
+        HIP_CHECK(hipMalloc(&bqkv, size_t(c + 2 * k) * sizeof(float)));
+        char *dst = static_cast<char *>(wqkv);
+        HIP_CHECK(hipMemcpyAsync(dst, to_q.w.p, size_t(c) * c * esz, hipMemcpyDeviceToDevice, e.ctx.stream));
+        HIP_CHECK(hipMemcpyAsync(dst + size_t(c) * c * esz, to_k.w.p, size_t(k) * c * esz, hipMemcpyDeviceToDevice,
+                                 e.ctx.stream));
+        HIP_CHECK(hipMemcpyAsync(dst + size_t(c + k) * c * esz, to_v.w.p, size_t(k) * c * esz,
+                                 hipMemcpyDeviceToDevice, e.ctx.stream));
+        std::vector<float> zeros(size_t(k), 0.0f);
+        HIP_CHECK(hipMemcpyAsync(bqkv, to_q.b, size_t(c) * sizeof(float), hipMemcpyDeviceToDevice, e.ctx.stream));
+        HIP_CHECK(hipMemcpy(bqkv + c, zeros.data(), size_t(k) * sizeof(float), hipMemcpyHostToDevice));
+        HIP_CHECK(hipMemcpyAsync(bqkv + c + k, to_v.b, size_t(k) * sizeof(float), hipMemcpyDeviceToDevice,
+                                 e.ctx.stream));
+        HIP_CHECK(hipStreamSynchronize(e.ctx.stream));
     }
     void release() {
         if (w_aug_t) (void)hipFree(w_aug_t);
+        if (wqkv) (void)hipFree(wqkv);
+        if (bqkv) (void)hipFree(bqkv);
         w_aug_t = nullptr;
+        wqkv = nullptr;
+        bqkv = nullptr;
     }
     // h [x.px()][c] += SelfLambda(x): the block's residual add is folded into the tap filter.
     void fwd_add(Env &e, const DT &x, float *h) const {
         const int hw = x.h * x.w;
-        DT q = to_q.fwd(e, x);
-        DT kt = to_k.fwd(e, x);
-        DT vt = to_v.fwd(e, x);
+        DT q = e.pool.tensor(x.n, x.h, x.w, c);
+        DT kt = e.pool.tensor(x.n, x.h, x.w, k);
+        DT vt = e.pool.tensor(x.n, x.h, x.w, k);
+        {
+            const int widths[3] = {c, k, k};
+            float *const outs[3] = {q.p, kt.p, vt.p};
+            conv1x1_segments(e.ctx, x.p, x.px(), c, wqkv, wt, bqkv, 3, widths, outs);
+        }
         float *lam_t = e.pool.floats(int64_t(x.n) * k * k);
         softmax_lambda(e.ctx, kt.p, vt.p, x.n, hw, k, k, lam_t);
         e.pool.recycle(kt);

@@ -142,10 +142,11 @@ def _components(ctx, steps):
 
 
 # HBM bytes per launch of the dominant kernel (below), from rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE over one UNet step, each scaled by the counter's reading for a plain
-# 256 MiB device copy (FETCH_SIZE reads half the copied bytes, WRITE_SIZE all of them):
-# 19.70 MiB fetched + 10.00 MiB written per launch.
-DOMINANT_TRAFFIC_BYTES = int((19.70 + 10.00) * 1048576)
+# WRITE_SIZE over this script's own default run (two UNet steps plus the standalone
+# timing loop), each scaled by the counter's reading for a plain 256 MiB device copy
+# (FETCH_SIZE reads half the copied bytes, WRITE_SIZE all of them): 17.01 MiB fetched +
+# 10.00 MiB written per launch, mean of 95 launches.
+DOMINANT_TRAFFIC_BYTES = int((17.01 + 10.00) * 1048576)
 
 
 def _dominant_gemm(ctx, steps):
@@ -279,12 +280,25 @@ def main():
     ap.add_argument("--cond-only", action="store_true", help="UNet: batch 1 (no CFG)")
     ap.add_argument("--f16-weights", action="store_true", help="UNet / VAE: f16-stored GEMM weights")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--calibration-copy", action="store_true",
+                    help="end with one 256 MiB device-to-device copy (the known-size reference that "
+                         "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the multi-GPU design is described in "
               "DESIGN.md and no multi-GPU figure is produced.", file=sys.stderr)
         sys.exit(2)
     res = WORKLOADS[args.workload](args)
+    if args.calibration_copy:
+        from moebius_cpu_amd import engine as E
+
+        ctx = E.Context(0)
+        n = 64 << 20  # floats: 256 MiB
+        src, dst = E.DeviceArray(ctx, (n,)), E.DeviceArray(ctx, (n,))
+        E.check(E.lib().mh_memcpy_d2d(ctx.h, dst.ptr, src.ptr, 4 * n))
+        ctx.synchronize()
+        del src, dst
+        ctx.close()
     line = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"), "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": res.pop("ms_per_step"),
             "higher_is_better": res.pop("higher_is_better"), "scaling": "weak", "vs_baseline": None,

@@ -90,6 +90,9 @@ struct GemmArgs {
     // byte extents of one item's A (or conv input) and of B, for the buffer
     // loads' range check (< 2^31): an access at or past the extent reads zero
     uint32_t a_bytes, b_bytes;
+    // set by the launcher: the output (or split partials) may be written four
+    // adjacent columns at a time with 16-byte accesses (see out_vec_ok)
+    int vec_out;
 };
 
 // (residual [transformed] + bias) + acc [SiLU] (+ res2): the reference's
@@ -150,6 +153,59 @@ __device__ __forceinline__ float *out_ptr(const GemmArgs &p, int row, int col, i
     }
     o = int64_t(row) * (c1 - c0) + (col - c0);
     return dst;
+}
+
+// epilogue_value for four adjacent columns col..col+3 of one row, with 16-byte
+// loads and one 16-byte store (the caller has checked out_vec_ok).
+template <int EPI>
+__device__ __forceinline__ void store4(const GemmArgs &p, int row, int col, float4 s) {
+    int64_t o;
+    float *dst = out_ptr(p, row, col, o);
+    float y[4] = {s.x, s.y, s.z, s.w};
+    const float4 bv = p.bias ? *reinterpret_cast<const float4 *>(p.bias + col) : float4{0.f, 0.f, 0.f, 0.f};
+    const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
+    if (p.res) {
+        const float4 r4 = *reinterpret_cast<const float4 *>(p.res + o);
+        float rv[4] = {r4.x, r4.y, r4.z, r4.w};
+        if (p.rsc) {
+            const int64_t i = int64_t(row / p.r_rows) * p.N + col;
+            const float4 sc = *reinterpret_cast<const float4 *>(p.rsc + i);
+            const float4 sh = *reinterpret_cast<const float4 *>(p.rsh + i);
+            rv[0] = __builtin_fmaf(rv[0], sc.x, sh.x);
+            rv[1] = __builtin_fmaf(rv[1], sc.y, sh.y);
+            rv[2] = __builtin_fmaf(rv[2], sc.z, sh.z);
+            rv[3] = __builtin_fmaf(rv[3], sc.w, sh.w);
+            if (p.rsilu)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) rv[j] = ref_silu(rv[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) y[j] = (p.bias ? rv[j] + bb[j] : rv[j]) + y[j];
+    } else if (p.bias) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) y[j] = bb[j] + y[j];
+    }
+    if (EPI == 1)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) y[j] = ref_silu(y[j]);
+    if (p.res2) {
+        const float4 r2 = *reinterpret_cast<const float4 *>(p.res2 + o);
+        y[0] = y[0] + r2.x, y[1] = y[1] + r2.y, y[2] = y[2] + r2.z, y[3] = y[3] + r2.w;
+    }
+    *reinterpret_cast<float4 *>(dst + o) = float4{y[0], y[1], y[2], y[3]};
+}
+
+// Whether the output can be written four adjacent columns at a time: N, the
+// leading dimensions, batch strides and segment bounds multiples of 4, no row
+// grouping, 16-byte aligned buffers.
+inline bool out_vec_ok(const GemmArgs &p) {
+    auto al = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    if (p.rg > 1 || (p.N & 3) || (p.c_bs & 3)) return false;
+    if (!al(p.bias) || !al(p.res) || !al(p.res2) || !al(p.rsc) || !al(p.rsh)) return false;
+    if (p.nseg == 0) return (p.ldc & 3) == 0 && al(p.out);
+    for (int s = 0; s < p.nseg; ++s)
+        if ((p.seg_col[s] & 3) || (p.seg_col[s + 1] & 3) || !al(p.seg_out[s])) return false;
+    return true;
 }
 
 __device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
@@ -339,9 +395,15 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
         if (p.res) p.res += bz * p.c_bs;
     }
     constexpr int A_LD = BM * K4 / 256, B_LD = BN * K4 / 256;
-    // Two LDS stages: tile kt+1 is written while tile kt is read, one barrier per K tile.
-    __shared__ float As[2][BM * LDS_S];
-    __shared__ float Bs[2][BN * LDS_S];
+    // Two LDS stages: tile kt+1 is written while tile kt is read, one barrier
+    // per K tile. The epilogue reuses the space for the C tile (row stride CS:
+    // the two row halves of a 32x32 block's store fall on different banks).
+    constexpr int CS = BN + 8;
+    constexpr int SMEM = 2 * (BM + BN) * LDS_S;
+    static_assert(BM * CS <= SMEM, "C tile must fit in the staging space");
+    __shared__ float smem[SMEM];
+    float(*As)[BM * LDS_S] = reinterpret_cast<float(*)[BM * LDS_S]>(smem);
+    float(*Bs)[BN * LDS_S] = reinterpret_cast<float(*)[BN * LDS_S]>(smem + 2 * BM * LDS_S);
 
     const int tiles_m = (p.M + BM - 1) / BM;
     const int tiles_n = (p.N + BN - 1) / BN;
@@ -479,46 +541,93 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
         }
     }
 
-    // Epilogue: block (i, j), register v, lane l holds row acc_row(v, l), column l % MF.
-    const int row_base = m0 + wm * (BM / 2);
-    const int col_base = n0 + wn * (BN / 2) + (lane % MF);
+    // Epilogue through LDS: block (i, j), register v, lane l holds row
+    // acc_row(v, l), column l % MF; the tile is written to LDS, then each thread
+    // finishes four adjacent columns of a row at a time (16-byte loads and stores).
+    __syncthreads();
+    {
+        const int r0 = wm * (BM / 2), c0 = wn * (BN / 2) + (lane % MF);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-        const int col = col_base + j * MF;
-        if (col >= p.N) continue;
-        const float bcol = (!SPLIT && p.bias) ? p.bias[col] : 0.f;
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
+            for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int v = 0; v < kAccRegs; ++v) {
-                const int row = row_base + i * MF + acc_row(v, lane);
-                if (row >= p.M) continue;
-                const float r = acc[i][j][v];
-                if (SPLIT) {
-                    p.partial[(int64_t(blockIdx.z) * p.M + row) * p.N + col] = r;
-                } else {
-                    int64_t o;
-                    float *dst = out_ptr(p, row, col, o);
-                    dst[o] = epilogue_value<EPI>(p, row, col, o, r, bcol);
-                }
+                for (int v = 0; v < kAccRegs; ++v)
+                    smem[(r0 + i * MF + acc_row(v, lane)) * CS + c0 + j * MF] = acc[i][j][v];
+    }
+    __syncthreads();
+    if (p.vec_out) {
+        constexpr int C4 = BN / 4, RPP = 256 / C4;  // float4 per tile row, rows per pass
+        const int cc = (tid % C4) * 4, col = n0 + cc;
+        if (col < p.N) {  // N % 4 == 0: the whole float4 is inside
+#pragma unroll
+            for (int it = 0; it < BM / RPP; ++it) {
+                const int rr = tid / C4 + it * RPP, row = m0 + rr;
+                if (row >= p.M) break;
+                const float4 v = *reinterpret_cast<const float4 *>(smem + rr * CS + cc);
+                if (SPLIT)
+                    *reinterpret_cast<float4 *>(p.partial + (int64_t(blockIdx.z) * p.M + row) * p.N + col) = v;
+                else
+                    store4<EPI>(p, row, col, v);
+            }
+        }
+    } else {
+        // One element per thread and pass; consecutive threads take consecutive
+        // rows when rows are grouped (their outputs are adjacent), else columns.
+        const bool by_row = p.rg > 1;
+        for (int e = tid; e < BM * BN; e += 256) {
+            const int rr = by_row ? e % BM : e / BN, cc = by_row ? e / BM : e % BN;
+            const int row = m0 + rr, col = n0 + cc;
+            if (row >= p.M || col >= p.N) continue;
+            const float r = smem[rr * CS + cc];
+            if (SPLIT) {
+                p.partial[(int64_t(blockIdx.z) * p.M + row) * p.N + col] = r;
+            } else {
+                int64_t o;
+                float *dst = out_ptr(p, row, col, o);
+                dst[o] = epilogue_value<EPI>(p, row, col, o, r, p.bias ? p.bias[col] : 0.f);
             }
         }
     }
 }
 
 // Sums split-K partials in split order, then (residual + bias) + sum [SiLU].
-template <int EPI>
+// VEC: four adjacent columns per thread (N, the output's leading dimensions and
+// segment bounds multiples of 4, M * N < 2^31, 16-byte aligned buffers; checked
+// by the launcher), so every load and store is 16 bytes wide.
+template <int EPI, bool VEC>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int splits) {
     const int64_t total = int64_t(p.M) * p.N;
-    for (int64_t e = blockIdx.x * int64_t(256) + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
-        float s = p.partial[e];
-        for (int z = 1; z < splits; ++z) s += p.partial[int64_t(z) * total + e];
-        const int row = int(e / p.N);
-        const int col = int(e - int64_t(row) * p.N);
-        int64_t o;
-        float *dst = out_ptr(p, row, col, o);
-        dst[o] = epilogue_value<EPI>(p, row, col, o, s, p.bias ? p.bias[col] : 0.0f);
+    if constexpr (VEC) {
+        const uint32_t n4 = uint32_t(p.N) >> 2;
+        const uint32_t total4 = uint32_t(total >> 2);
+        const float4 *pp = reinterpret_cast<const float4 *>(p.partial);
+        for (uint32_t e = blockIdx.x * 256u + threadIdx.x; e < total4; e += gridDim.x * 256u) {
+            float4 s = pp[e];
+            for (int z = 1; z < splits; ++z) {
+                const float4 t = pp[uint64_t(z) * total4 + e];
+                s.x += t.x, s.y += t.y, s.z += t.z, s.w += t.w;
+            }
+            const int row = int(e / n4);
+            store4<EPI>(p, row, int(e - uint32_t(row) * n4) << 2, s);
+        }
+    } else {
+        for (int64_t e = blockIdx.x * int64_t(256) + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
+            float s = p.partial[e];
+            for (int z = 1; z < splits; ++z) s += p.partial[int64_t(z) * total + e];
+            const int row = int(e / p.N);
+            const int col = int(e - int64_t(row) * p.N);
+            int64_t o;
+            float *dst = out_ptr(p, row, col, o);
+            dst[o] = epilogue_value<EPI>(p, row, col, o, s, p.bias ? p.bias[col] : 0.0f);
+        }
     }
+}
+
+// Whether the split-K reduction may use 16-byte accesses (see splitk_reduce_kernel).
+inline bool reduce_vec_ok(const GemmArgs &p) {
+    return out_vec_ok(p) && (reinterpret_cast<uintptr_t>(p.partial) & 15) == 0 &&
+           int64_t(p.M) * p.N < (int64_t(1) << 31);
 }
 
 struct Plan {
@@ -562,17 +671,27 @@ void launch_cfg(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int
         const size_t bytes = size_t(pl.splits) * p.M * p.N * sizeof(float);
         p.partial = static_cast<float *>(ctx.ws.get(bytes, ctx.stream));
         p.k_split = pl.k_split;
+        p.vec_out = (p.N & 3) == 0 && (reinterpret_cast<uintptr_t>(p.partial) & 15) == 0;
         dim3 grid(tiles, 1, pl.splits);
         gemm_f32_kernel<BM, BN, MODE, PRO, F16, BVEC, 0, true><<<grid, 256, 0, ctx.stream>>>(p);
         MH_LAUNCH_CHECK();
         const int64_t total = int64_t(p.M) * p.N;
-        const unsigned rb = unsigned(std::min<int64_t>(ceil_div(total, 256), 8192));
-        if (epi == GemmEpilogue::Silu)
-            splitk_reduce_kernel<1><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
-        else
-            splitk_reduce_kernel<0><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
+        if (reduce_vec_ok(p)) {
+            const unsigned rb = unsigned(std::min<int64_t>(ceil_div(total / 4, 256), 8192));
+            if (epi == GemmEpilogue::Silu)
+                splitk_reduce_kernel<1, true><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
+            else
+                splitk_reduce_kernel<0, true><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
+        } else {
+            const unsigned rb = unsigned(std::min<int64_t>(ceil_div(total, 256), 8192));
+            if (epi == GemmEpilogue::Silu)
+                splitk_reduce_kernel<1, false><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
+            else
+                splitk_reduce_kernel<0, false><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
+        }
     } else {
         p.k_split = p.K;
+        p.vec_out = out_vec_ok(p);
         const dim3 grid(tiles, unsigned(batch));
         // The SiLU epilogue is only instantiated for dense operands (the convs never use it).
         if constexpr (MODE <= kDenseScalar) {

@@ -151,8 +151,8 @@ DOMINANT_TRAFFIC_BYTES = int((17.01 + 10.00) * 1048576)
 
 def _dominant_gemm(ctx, steps):
     """The step's most frequent GEMM, timed on its own with events: the 1x1 conv of
-    a [2,64,64,320] map to 320 channels with bias (gemm_f32_kernel, 64x64 tiles,
-    640 workgroups), i.e. M = 8192, N = 320, K = 320."""
+    a [2,64,64,320] map to 320 channels with bias (gemm_f32_kernel, 32x32 tiles on
+    v_mfma_f32_16x16x4f32, 2560 workgroups), i.e. M = 8192, N = 320, K = 320."""
     from moebius_cpu_amd import engine as E
     from moebius_cpu_amd import synthetic as S
 
@@ -163,7 +163,7 @@ def _dominant_gemm(ctx, steps):
     us = time_region(ctx, lambda: conv.forward(x, y), steps) * 1e3
     flops = 2.0 * 8192 * 320 * 320
     tf = flops / (us * 1e-6) / 1e12
-    return {"bound": "mfma", "kernel": "gemm_f32_kernel<64,64,dense> (1x1 conv [2,64,64,320] -> 320, "
+    return {"bound": "mfma", "kernel": "gemm_f32_kernel<32,32,dense> (1x1 conv [2,64,64,320] -> 320, "
                                        "M=8192 N=320 K=320: the step's most frequent GEMM)",
             "achieved": round(tf, 2), "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
             "frac": round(tf / PEAK_F32_MFMA_TFLOPS, 4), "traffic": DOMINANT_TRAFFIC_BYTES,

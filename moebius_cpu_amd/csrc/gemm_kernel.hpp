@@ -26,26 +26,28 @@ constexpr int LDS_S = BK + 4;   // padded LDS row stride (floats): conflict-free
 constexpr int K4 = BK / 4;      // float4 per tile row
 constexpr int kMaxSeg = 3;      // column segments of a segmented output
 
-// Matrix instruction: v_mfma_f32_16x16x4f32 (MF = 16) or v_mfma_f32_32x32x2f32
-// (MF = 32). Output lane layouts: 16x16: register v of lane l is row
+// Matrix instruction: v_mfma_f32_32x32x2f32 (MF = 32) for tiles of 64 or more
+// in both dimensions, v_mfma_f32_16x16x4f32 (MF = 16) for the 32-wide tiles of
+// small GEMMs. Output lane layouts: 16x16: register v of lane l is row
 // 4 * (l / 16) + v, column l % 16; 32x32: row 8 * (v / 4) + 4 * (l / 32) + v % 4,
 // column l % 32.
-constexpr int MF = 32;
-constexpr int kAccRegs = MF * MF / 64;
-constexpr int kKStep = MF == 32 ? 8 : 16;  // K covered by one float4 read per lane
-typedef std::conditional_t<MF == 32, floatx16, floatx4> Acc;
+template <int BM, int BN>
+constexpr int mf_for() { return (BM >= 64 && BN >= 64) ? 32 : 16; }
 
-template <int M = MF>
-__device__ __forceinline__ std::conditional_t<M == 32, floatx16, floatx4> mfma(
-    float a, float b, const std::conditional_t<M == 32, floatx16, floatx4> &c) {
-    if constexpr (M == 32) return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
-    else return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ int acc_row(int v, int lane) {
-    if constexpr (MF == 32) return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-    else return 4 * (lane >> 4) + v;
-}
+template <int M>
+struct Mf {
+    static constexpr int kAccRegs = M * M / 64;
+    static constexpr int kKStep = M == 32 ? 8 : 16;  // K covered by one float4 read per lane
+    typedef std::conditional_t<M == 32, floatx16, floatx4> Acc;
+    static __device__ __forceinline__ Acc mfma(float a, float b, const Acc &c) {
+        if constexpr (M == 32) return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+        else return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ int acc_row(int v, int lane) {
+        if constexpr (M == 32) return 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+        else return 4 * (lane >> 4) + v;
+    }
+};
 
 enum AMode : int {
     kDense = 0,      // A[m][k] row-major with leading dimension lda, K % 4 == 0
@@ -386,6 +388,8 @@ __device__ __forceinline__ floatx4 load_b(const GemmArgs &p, int n, int k) {
 
 template <int BM, int BN, int MODE, bool PRO, bool F16, bool BVEC, int EPI, bool SPLIT>
 __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
+    constexpr int MF = mf_for<BM, BN>();
+    using MI = Mf<MF>;
     constexpr int FM = BM / 2 / MF, FN = BN / 2 / MF;  // MF x MF blocks per wave
     if (blockIdx.y) {
         const int64_t bz = blockIdx.y;
@@ -474,13 +478,13 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
             *reinterpret_cast<floatx4 *>(Bs[buf] + (lrow + 32 * i) * LDS_S + lc4 * 4) = rb[i];
     };
 
-    Acc acc[FM][FN];
+    typename MI::Acc acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int v = 0; v < kAccRegs; ++v) acc[i][j][v] = 0.f;
+            for (int v = 0; v < MI::kAccRegs; ++v) acc[i][j][v] = 0.f;
 
     // Lane l reads a float4 along K at row l % MF, K offset 4 * (l / MF): the
     // four lane groups (two for 32x32) each cover 4 consecutive K.
@@ -492,7 +496,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
         const float *as_w = As[buf] + a_off;
         const float *bs_w = Bs[buf] + b_off;
 #pragma unroll
-        for (int kk = 0; kk < BK; kk += kKStep) {
+        for (int kk = 0; kk < BK; kk += MI::kKStep) {
             floatx4 a[FM], b[FN];
 #pragma unroll
             for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const floatx4 *>(as_w + i * MF * LDS_S + kk);
@@ -503,7 +507,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
 #pragma unroll
                 for (int i = 0; i < FM; ++i)
 #pragma unroll
-                    for (int j = 0; j < FN; ++j) acc[i][j] = mfma(a[i][t], b[j][t], acc[i][j]);
+                    for (int j = 0; j < FN; ++j) acc[i][j] = MI::mfma(a[i][t], b[j][t], acc[i][j]);
         }
     };
 
@@ -552,8 +556,8 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
 #pragma unroll
             for (int j = 0; j < FN; ++j)
 #pragma unroll
-                for (int v = 0; v < kAccRegs; ++v)
-                    smem[(r0 + i * MF + acc_row(v, lane)) * CS + c0 + j * MF] = acc[i][j][v];
+                for (int v = 0; v < MI::kAccRegs; ++v)
+                    smem[(r0 + i * MF + MI::acc_row(v, lane)) * CS + c0 + j * MF] = acc[i][j][v];
     }
     __syncthreads();
     if (p.vec_out) {
@@ -641,11 +645,15 @@ struct Plan {
 //    (71-80% of f32 MFMA peak on the VAE's 3x3 convs, against 60-77% at 64x64).
 //  - Long K (>= 4096, the upsample / downsample convs): 128x128 tiles, K split
 //    in 3; 75-77% of f32 MFMA peak, against 67% unsplit.
-//  - Otherwise 64x64 tiles, several co-resident workgroups per CU hiding load
-//    latency: K is split only while the grid is under three times the CU count and
-//    each split keeps at least 8 K tiles (measured: the UNet's 160-320-tile
-//    GEMMs lose 15-25% unsplit, more than the reduction launch costs).
-inline Plan plan_for(int M, int N, int K, int cus) {
+//  - Dense operands (1x1 convs, linears): 64x64 tiles when there are four per
+//    CU or more; 64x64 with K split in 3 for long K (>= 1536) on grids of
+//    fewer than four 32x32 tiles per CU; otherwise 32x32 tiles (16x16 MFMA),
+//    K split in up to 3 only under two tiles per CU with K >= 1024. Against
+//    64x64 tiles with up to 6 splits this takes 10-30% off the UNet's
+//    16x16- and 32x32-latent GEMMs (2048x640x640: 28.4 -> 19.7 us).
+//  - Implicit-GEMM convs otherwise: 64x64 tiles, K split while the grid is under
+//    three times the CU count and each split keeps at least 8 K tiles.
+inline Plan plan_for(int M, int N, int K, int cus, bool dense) {
     const int ktiles = int(ceil_div(K, BK));
     auto split = [&](int64_t tiles, int64_t target, int max_splits) {
         int want = 1;
@@ -660,7 +668,21 @@ inline Plan plan_for(int M, int N, int K, int cus) {
         const auto s = split(t128, 3 * int64_t(cus), 3);
         return Plan{128, 128, s.first, s.second};
     }
-    const auto s = split(ceil_div(M, 64) * ceil_div(N, 64), 3 * int64_t(cus), 6);
+    const int64_t t64 = ceil_div(M, 64) * ceil_div(N, 64);
+    if (dense) {
+        const int64_t t32 = ceil_div(M, 32) * ceil_div(N, 32);
+        if (t64 >= 4 * int64_t(cus)) return Plan{64, 64, 1, K};
+        if (K >= 1536 && t32 < 4 * int64_t(cus)) {
+            const auto s = split(t64, 3 * t64, 3);
+            return Plan{64, 64, s.first, s.first > 1 ? s.second : K};
+        }
+        if (K >= 1024 && t32 < 2 * int64_t(cus)) {
+            const auto s = split(t32, 2 * int64_t(cus), 3);
+            return Plan{32, 32, s.first, s.first > 1 ? s.second : K};
+        }
+        return Plan{32, 32, 1, K};
+    }
+    const auto s = split(t64, 3 * int64_t(cus), 6);
     return Plan{64, 64, s.first, s.first > 1 ? s.second : K};
 }
 
@@ -710,19 +732,25 @@ void launch_cfg(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int
 
 template <int MODE, bool PRO, bool F16, bool BVEC>
 void launch_tiles(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
-    Plan pl = plan_for(p.M, p.N, p.K, int(ceil_div(ctx.cu_count, batch)));
+    Plan pl = plan_for(p.M, p.N, p.K, int(ceil_div(ctx.cu_count, batch)), MODE <= kDenseScalar);
     // MOEBIUS_HIP_GEMM_PLAN="bm,bn,splits" forces the tiling (tuning and A/B runs),
     // as MOEBIUS_GEMM selects the CPU engine's GEMM backend (src/engine/gemm.rs:57-60).
     if (const char *force = std::getenv("MOEBIUS_HIP_GEMM_PLAN")) {
         int bm = 0, bn = 0, sp = 0;
-        if (std::sscanf(force, "%d,%d,%d", &bm, &bn, &sp) == 3 && (bm == 64 || bm == 128) && (bn == 64 || bn == 128) &&
-            sp >= 1) {
+        if (std::sscanf(force, "%d,%d,%d", &bm, &bn, &sp) == 3 && (bm == 32 || bm == 64 || bm == 128) &&
+            (bn == 32 || bn == 64 || bn == 128) && (bm == 32) == (bn == 32) && sp >= 1) {
             const int ktiles = int(ceil_div(p.K, BK));
             const int per = int(ceil_div(ktiles, sp));
             pl = Plan{bm, bn, int(ceil_div(ktiles, per)), per * BK};
         }
     }
     if (batch > 1) pl.splits = 1;
+    if constexpr (MODE <= kDenseScalar) {  // small tiles for the small dense GEMMs only
+        if (pl.bm == 32) {
+            launch_cfg<32, 32, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
+            return;
+        }
+    }
     if (pl.bm == 128 && pl.bn == 128)
         launch_cfg<128, 128, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
     else if (pl.bm == 128)

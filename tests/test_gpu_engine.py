@@ -219,6 +219,35 @@ def test_conv1x1_residual_transform_and_second_residual(ctx, n, h, w, c, f16):
     assert max_abs_rel(got, want) <= F32_TOL
 
 
+# ---- every tiling the planner can pick (32x32 tiles on 16x16 MFMA, 64/128
+# tiles on 32x32 MFMA, split K with the separate reduction), with edge tiles
+# in M and N and both epilogue store paths (N % 4 == 0: 16-byte, else scalar):
+# each within the f32 bar of the oracle
+@pytest.mark.parametrize("plan", ["32,32,1", "32,32,3", "64,64,1", "64,64,2", "128,64,1", "64,128,3", "128,128,2"])
+@pytest.mark.parametrize("c_out", [72, 70])
+def test_conv1x1_every_tiling(ctx, plan, c_out, monkeypatch):
+    rng = np.random.default_rng(c_out)
+    n, h, w, c = 2, 9, 11, 200
+    x = rng.standard_normal((n, h, w, c)).astype(np.float32)
+    r = rng.standard_normal((n, h, w, c_out)).astype(np.float32)
+    r2 = rng.standard_normal((n, h, w, c_out)).astype(np.float32)
+    wt = (rng.standard_normal((c_out, c)) / np.sqrt(c)).astype(np.float32)
+    b = (rng.standard_normal(c_out) * 0.1).astype(np.float32)
+    sc = (1 + 0.1 * rng.standard_normal(n * c_out)).astype(np.float32)
+    sh = (0.1 * rng.standard_normal(n * c_out)).astype(np.float32)
+    a = np.stack([oracle.apply_affine(r[i], sc[i * c_out:(i + 1) * c_out], sh[i * c_out:(i + 1) * c_out], True)
+                  for i in range(n)])
+    param = E.Param(ctx, wt)
+    dev = {k: E.DeviceArray.from_numpy(ctx, v) for k, v in dict(x=x, r=r, r2=r2, b=b, sc=sc, sh=sh).items()}
+    out = E.DeviceArray(ctx, (n, h, w, c_out))
+    monkeypatch.setenv("MOEBIUS_HIP_GEMM_PLAN", plan)
+    E.check(E.lib().mh_conv1x1_fused(ctx.h, dev["x"].ptr, n, h, w, c, param.ptr, param.dtype, c_out, dev["b"].ptr,
+                                     dev["r"].ptr, dev["sc"].ptr, dev["sh"].ptr, 1, dev["r2"].ptr, out.ptr))
+    got = out.numpy()
+    want = oracle.conv1x1(x, wt, b, a) + r2
+    assert max_abs_rel(got, want) <= F32_TOL
+
+
 # ---- tests/kernels.rs:233-265: the fused GN prologue, padding stays zero
 @pytest.mark.parametrize("n,h,w,ci,groups,co", [(2, 7, 9, 40, 8, 24), (2, 37, 23, 768, 32, 16)])
 @pytest.mark.parametrize("up", [False, True])

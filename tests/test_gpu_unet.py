@@ -91,7 +91,10 @@ def test_position_term_kernel_bit_exact(ctx, br0, nb, k):
 
 
 @pytest.mark.parametrize("row_group", [0, 8])
-def test_gemm_nt_kernel(ctx, row_group):
+@pytest.mark.parametrize("plan", [None, "32,32,1", "64,64,1", "64,64,2"])
+def test_gemm_nt_kernel(ctx, row_group, plan, monkeypatch):
+    if plan:
+        monkeypatch.setenv("MOEBIUS_HIP_GEMM_PLAN", plan)
     rng = np.random.default_rng(9)
     m, n, k = 304, 226, 40
     a = rng.standard_normal((m, k)).astype(np.float32)

@@ -233,6 +233,14 @@ int32_t mh_tap_filter(MhContext *ctx, const float *a_t, const float *v, const fl
 int32_t mh_position_term(MhContext *ctx, const float *q, const float *e, const float *v_branches, uint32_t br0,
                          uint32_t nb, uint32_t hw, uint32_t k, const float *yc, const float *residual, float *out);
 
+/* src/unet/lambda.rs:258-271, the body of `CrossLambda::forward` after to_q, in
+ * one pass: u = q . lambda_c[branch] (src/unet/lambda.rs:266) + (q . E) . V[branch]
+ * (the position term as mh_position_term computes it); out = u, or residual + u.
+ * lambda_c [2][k][k] row-major; e, v_branches, q, residual, out as for
+ * mh_position_term. out may alias residual, not q. k a multiple of 8, <= 256. */
+int32_t mh_cross_lambda(MhContext *ctx, const float *q, const float *e, const float *lambda_c, const float *v_branches,
+                        uint32_t br0, uint32_t nb, uint32_t hw, uint32_t k, const float *residual, float *out);
+
 /* src/engine/gemm.rs:63-132 `matmul` for K-contiguous operands, on the device:
  * c [m][ldc] = a [m][lda] . b[n][ldb]^T (+ bias[n]) (+ residual [m][ldc]); b F32/F16.
  * row_group g > 1 (m a multiple of g, g <= 64) stores row i, column j at

@@ -496,6 +496,20 @@ int32_t mh_position_term(MhContext *ctx, const float *q, const float *e, const f
     });
 }
 
+int32_t mh_cross_lambda(MhContext *ctx, const float *q, const float *e, const float *lambda_c, const float *v_branches,
+                        uint32_t br0, uint32_t nb, uint32_t hw, uint32_t k, const float *residual, float *out) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(q, "q");
+        need(e, "e");
+        need(lambda_c, "lambda_c");
+        need(v_branches, "v_branches");
+        need(out, "out");
+        mh::cross_lambda(c, q, e, lambda_c, v_branches, dim(br0, "br0"), dim(nb, "nb"), dim(hw, "hw"), dim(k, "k"),
+                         residual, out);
+    });
+}
+
 int32_t mh_gemm_nt(MhContext *ctx, const float *a, uint64_t lda, const void *b, uint32_t b_dtype, uint64_t ldb,
                    uint32_t m, uint32_t n, uint32_t k, const float *bias, const float *residual, float *c,
                    uint64_t ldc, uint32_t row_group) {

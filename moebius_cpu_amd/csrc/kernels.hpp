@@ -96,6 +96,10 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
 // out may alias yc or residual.
 void position_term(Context &ctx, const float *q, const float *e, const float *v_branches, int br0, int nb, int hw,
                    int k, const float *yc, const float *residual, float *out);
+// out [nb*hw][8*k] = (residual +) (q . lambda_c[branch] + (q . E) . V[branch]) in one pass;
+// lambda_c [2][k][k] row-major. out may alias residual, not q.
+void cross_lambda(Context &ctx, const float *q, const float *e, const float *lambda_c, const float *v_branches, int br0,
+                  int nb, int hw, int k, const float *residual, float *out);
 
 // ---- VAE (vae_kernels.hip), src/vae
 // In place over rows [nrows][n] (n <= 15360): softmax(scale * row) with

@@ -317,6 +317,137 @@ __global__ __launch_bounds__(256) void position_term_kernel(const float *__restr
     }
 }
 
+// Cross-lambda output (src/unet/lambda.rs:258-271) in one pass per pixel: Yc =
+// Q . lambda_c[branch] (a fused multiply-add chain over kk), then the position
+// term as position_term_kernel computes it (8-lane dots q_h . E[n][m], then
+// o_h += B[h][m] * V[m] for m = 0..9 in order), then the block's residual. The
+// block's pixels' q is staged in LDS transposed ([p][kk][h]) so a thread reads
+// its HG heads of one kk in one or two 16-byte loads; lambda_c rows are shared
+// by every thread with the same channel quad. Thread: (pixel, head group,
+// channel quad); P pixels per block. lam: [2][k][k] row-major (lambda_c[kk][j]).
+template <int HG>
+__global__ __launch_bounds__(256) void cross_lambda_kernel(const float *__restrict__ q, const float *__restrict__ e,
+                                                           const float *__restrict__ lam,
+                                                           const float *__restrict__ vbr, int br0, int nb, int hw,
+                                                           int k, int P, const float *res, float *out) {
+    extern __shared__ float sm[];
+    const int c = kHeads * k;
+    float *qs = sm;                  // [P][k][8]
+    float *bm = sm + size_t(P) * c;  // [P][8][10]
+    const int64_t pix0 = int64_t(blockIdx.x) * P;
+    const int np = int(min<int64_t>(P, int64_t(nb) * hw - pix0));
+    const float4 *q4 = reinterpret_cast<const float4 *>(q + pix0 * c);
+    for (int t = threadIdx.x; t < np * (c >> 2); t += blockDim.x) {
+        const int r = t * 4, p = r / c, hk = r - p * c, h = hk / k, kk = hk - h * k;  // k % 4 == 0
+        const float4 v = q4[t];
+        float *d = qs + (size_t(p) * k + kk) * kHeads + h;
+        d[0] = v.x, d[kHeads] = v.y, d[2 * kHeads] = v.z, d[3 * kHeads] = v.w;
+    }
+    __syncthreads();
+    // B[p][h][m] = q_h . E[n][m]: one (pixel, token, group of HG heads) per
+    // thread and pass; per head the reference's 8-lane dot (acc[l] takes
+    // kk = l, l + 8, ...; the lanes summed in order).
+    constexpr int NG = kHeads / HG;
+    for (int t = threadIdx.x; t < np * kTokens * NG; t += blockDim.x) {
+        const int p = t / (kTokens * NG), mg = t - p * (kTokens * NG), m = mg / NG, g = mg - m * NG;
+        const int n = int((pix0 + p) % hw);
+        const float4 *e4 = reinterpret_cast<const float4 *>(e + (int64_t(n) * kTokens + m) * k);
+        const float *qp = qs + size_t(p) * k * kHeads + g * HG;
+        float acc[HG][8];
+#pragma unroll
+        for (int h = 0; h < HG; ++h)
+#pragma unroll
+            for (int l = 0; l < 8; ++l) acc[h][l] = 0.f;
+        for (int i = 0; i < k; i += 8) {
+            const float4 ea = e4[i >> 2], eb = e4[(i >> 2) + 1];
+            const float ev[8] = {ea.x, ea.y, ea.z, ea.w, eb.x, eb.y, eb.z, eb.w};
+#pragma unroll
+            for (int l = 0; l < 8; ++l) {
+                float qv[HG];
+                if constexpr (HG >= 4) {
+#pragma unroll
+                    for (int h = 0; h < HG; h += 4) {
+                        const float4 t4 = *reinterpret_cast<const float4 *>(qp + (i + l) * kHeads + h);
+                        qv[h] = t4.x, qv[h + 1] = t4.y, qv[h + 2] = t4.z, qv[h + 3] = t4.w;
+                    }
+                } else {
+                    const float2 t2 = *reinterpret_cast<const float2 *>(qp + (i + l) * kHeads);
+                    qv[0] = t2.x, qv[1] = t2.y;
+                }
+#pragma unroll
+                for (int h = 0; h < HG; ++h) acc[h][l] = __builtin_fmaf(qv[h], ev[l], acc[h][l]);
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < HG; ++h) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int l = 0; l < 8; ++l) sum += acc[h][l];
+            bm[(p * kHeads + g * HG + h) * kTokens + m] = sum + 0.0f;
+        }
+    }
+    __syncthreads();
+    const int k4 = k >> 2, per_px = NG * k4;
+    const int p = threadIdx.x / per_px;
+    if (p >= np) return;  // no barrier follows
+    const int r = threadIdx.x - p * per_px, hg = r / k4, jq = r - hg * k4;
+    const int64_t pix = pix0 + p;
+    const int br = br0 + int(pix / hw);
+    const float4 *l4 = reinterpret_cast<const float4 *>(lam + int64_t(br) * k * k) + jq;
+    const float *qp = qs + size_t(p) * k * kHeads + hg * HG;
+    float4 acc[HG];
+#pragma unroll
+    for (int i = 0; i < HG; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+    for (int kk = 0; kk < k; ++kk) {
+        const float4 l = l4[kk * k4];
+        float qv[HG];
+        if constexpr (HG >= 4) {
+#pragma unroll
+            for (int i = 0; i < HG; i += 4) {
+                const float4 t4 = *reinterpret_cast<const float4 *>(qp + kk * kHeads + i);
+                qv[i] = t4.x, qv[i + 1] = t4.y, qv[i + 2] = t4.z, qv[i + 3] = t4.w;
+            }
+        } else {
+            const float2 t2 = *reinterpret_cast<const float2 *>(qp + kk * kHeads);
+            qv[0] = t2.x, qv[1] = t2.y;
+        }
+#pragma unroll
+        for (int i = 0; i < HG; ++i) {
+            acc[i].x = __builtin_fmaf(qv[i], l.x, acc[i].x);
+            acc[i].y = __builtin_fmaf(qv[i], l.y, acc[i].y);
+            acc[i].z = __builtin_fmaf(qv[i], l.z, acc[i].z);
+            acc[i].w = __builtin_fmaf(qv[i], l.w, acc[i].w);
+        }
+    }
+    const float4 *v4 = reinterpret_cast<const float4 *>(vbr + int64_t(br) * kTokens * k) + jq;
+    const float *bp = bm + (size_t(p) * kHeads + hg * HG) * kTokens;
+#pragma unroll
+    for (int m = 0; m < kTokens; ++m) {
+        const float4 x = v4[m * k4];
+#pragma unroll
+        for (int i = 0; i < HG; ++i) {
+            const float w = bp[i * kTokens + m];
+            acc[i].x = __builtin_fmaf(w, x.x, acc[i].x);
+            acc[i].y = __builtin_fmaf(w, x.y, acc[i].y);
+            acc[i].z = __builtin_fmaf(w, x.z, acc[i].z);
+            acc[i].w = __builtin_fmaf(w, x.w, acc[i].w);
+        }
+    }
+    const float4 *res4 = reinterpret_cast<const float4 *>(res);
+    float4 *out4 = reinterpret_cast<float4 *>(out);
+#pragma unroll
+    for (int i = 0; i < HG; ++i) {
+        const int64_t o = pix * (kHeads * k4) + int64_t(hg * HG + i) * k4 + jq;
+        float4 u = acc[i];
+        if (res) {
+            const float4 rr = res4[o];
+            u = make_float4(rr.x + u.x, rr.y + u.y, rr.z + u.z, rr.w + u.w);
+        }
+        out4[o] = u;
+    }
+}
+
 }  // namespace
 
 void softmax_lambda(Context &ctx, const float *keys, const float *v, int nb, int rows, int k, int vd,
@@ -382,6 +513,46 @@ void position_term(Context &ctx, const float *q, const float *e, const float *v_
     if (npix == 0) return;
     position_term_kernel<<<unsigned(ceil_div(npix, 8)), 256, 0, ctx.stream>>>(q, e, v_branches, br0, nb, hw, k, yc,
                                                                              residual, out);
+    MH_LAUNCH_CHECK();
+}
+
+void cross_lambda(Context &ctx, const float *q, const float *e, const float *lambda_c, const float *v_branches, int br0,
+                  int nb, int hw, int k, const float *residual, float *out) {
+    MH_REQUIRE(k % 8 == 0 && k <= 256, "cross_lambda: head width must be a multiple of 8, at most 256");
+    MH_REQUIRE(aligned16(q) && aligned16(e) && aligned16(lambda_c) && aligned16(v_branches) && aligned16(residual) &&
+                   aligned16(out),
+               "cross_lambda: buffers must be 16-byte aligned");
+    MH_REQUIRE(br0 >= 0 && br0 + nb <= 2, "cross_lambda: branch out of range");
+    MH_REQUIRE(out != q, "cross_lambda: out must not alias q");
+    const int64_t npix = int64_t(nb) * hw;
+    if (npix == 0) return;
+    // Heads per thread: the most that still gives every CU a block (8, 4 or 2).
+    const int k4 = k / 4;
+    int hg = 2;
+    for (int cand : {8, 4}) {
+        const int P = 256 / ((kHeads / cand) * k4);
+        if (P >= 1 && ceil_div(npix, P) >= ctx.cu_count) {
+            hg = cand;
+            break;
+        }
+    }
+    const int P = std::max(1, 256 / ((kHeads / hg) * k4));
+    const unsigned threads = unsigned(P * (kHeads / hg) * k4);
+    const size_t lds = (size_t(P) * kHeads * k + size_t(P) * kHeads * kTokens) * sizeof(float);
+    const unsigned blocks = unsigned(ceil_div(npix, P));
+    switch (hg) {
+        case 8:
+            cross_lambda_kernel<8><<<blocks, threads, lds, ctx.stream>>>(q, e, lambda_c, v_branches, br0, nb, hw, k,
+                                                                          P, residual, out);
+            break;
+        case 4:
+            cross_lambda_kernel<4><<<blocks, threads, lds, ctx.stream>>>(q, e, lambda_c, v_branches, br0, nb, hw, k,
+                                                                          P, residual, out);
+            break;
+        default:
+            cross_lambda_kernel<2><<<blocks, threads, lds, ctx.stream>>>(q, e, lambda_c, v_branches, br0, nb, hw, k,
+                                                                          P, residual, out);
+    }
     MH_LAUNCH_CHECK();
 }
 

@@ -317,7 +317,7 @@ struct CrossLambda {
     int c = 0, k = 0, n = 0;
     Lin to_q;
     const float *e = nullptr;       // rel_pos_emb [n][10][k]
-    float *lambda_t = nullptr;      // [2][k][k] transposed lambda_c per branch
+    float *lambda_c = nullptr;      // [2][k][k] lambda_c per branch (row-major)
     float *v = nullptr;             // [2][10][k]
     void load(Env &env, const WeightStore &W, const std::string &p, int c_, const float *ehs_dev /*[2][10][768]*/) {
         c = c_, k = c / HEADS;
@@ -326,7 +326,7 @@ struct CrossLambda {
         const DParam wk = W.get(p + ".to_k.weight", int64_t(k) * XDIM, true);
         const DParam wv = W.get(p + ".to_v.weight", int64_t(k) * XDIM, true);
         const float *bv = W.get(p + ".to_v.bias", k, false).f();
-        HIP_CHECK(hipMalloc(&lambda_t, size_t(2) * k * k * sizeof(float)));
+        HIP_CHECK(hipMalloc(&lambda_c, size_t(2) * k * k * sizeof(float)));
         HIP_CHECK(hipMalloc(&v, size_t(2) * TOKENS * k * sizeof(float)));
         float *keys = env.pool.floats(int64_t(2) * TOKENS * k);
         for (int br = 0; br < 2; ++br) {
@@ -339,26 +339,27 @@ struct CrossLambda {
             bias_residual_add(env.ctx, v + int64_t(br) * TOKENS * k, TOKENS, k, bv, nullptr,
                               v + int64_t(br) * TOKENS * k);
         }
+        float *lambda_t = env.pool.floats(int64_t(2) * k * k);
         softmax_lambda(env.ctx, keys, v, 2, TOKENS, k, k, lambda_t);
+        for (int br = 0; br < 2; ++br)
+            transpose(env.ctx, lambda_t + int64_t(br) * k * k, k, k, k, lambda_c + int64_t(br) * k * k);
+        env.pool.recycle(lambda_t);
         env.pool.recycle(keys);
         to_q.load(W, p + ".to_q", c, c, true);
         e = W.get(p + ".rel_pos_emb", int64_t(n) * TOKENS * k, false).f();
     }
     void release() {
-        if (lambda_t) (void)hipFree(lambda_t);
+        if (lambda_c) (void)hipFree(lambda_c);
         if (v) (void)hipFree(v);
-        lambda_t = v = nullptr;
+        lambda_c = v = nullptr;
     }
-    // h [x.px()][c] += CrossLambda(x): the residual add is folded into the position term.
+    // h [x.px()][c] += CrossLambda(x): Yc = Q . lambda_c, the position term and
+    // the residual add in one kernel after the q projection.
     void fwd_add(Env &env, const DT &x, int br0, float *h) const {
         const int hw = x.h * x.w;
         if (hw != n) fail(kInvalidArgument, "CrossLambda input size does not match the position table");
         DT q = to_q.fwd(env, x);
-        DT yc = env.pool.tensor(x.n, x.h, x.w, c);
-        gemm_nt(env.ctx, q.p, k, int64_t(hw) * c, lambda_t + int64_t(br0) * k * k, kF32, k, int64_t(k) * k,
-                hw * HEADS, k, k, x.n, nullptr, nullptr, yc.p, k, int64_t(hw) * c);
-        position_term(env.ctx, q.p, e, v, br0, x.n, hw, k, yc.p, h, h);
-        env.pool.recycle(yc);
+        cross_lambda(env.ctx, q.p, e, lambda_c, v, br0, x.n, hw, k, h, h);
         env.pool.recycle(q);
     }
 };

@@ -90,6 +90,38 @@ def test_position_term_kernel_bit_exact(ctx, br0, nb, k):
         assert np.array_equal(got_res[b], h[b] + want)
 
 
+# CrossLambda::forward after to_q (src/unet/lambda.rs:258-271) in one kernel:
+# with lambda_c = 0 the Yc part is exactly +0 and the rest must be the
+# position term bit for bit; with a real lambda_c, Yc = Q . lambda_c (f64
+# reference) within the f32 bar. Sizes select each heads-per-thread variant
+# (8 at 64x64 / k 40, 4 at 32x32 / k 80, 2 at 16x16 / k 160) plus a ragged block.
+@pytest.mark.parametrize("br0,nb,hw,k", [(0, 2, 4096, 40), (0, 2, 1024, 80), (0, 2, 256, 160), (1, 1, 37, 40)])
+def test_cross_lambda_kernel(ctx, br0, nb, hw, k):
+    rng = np.random.default_rng(k + hw)
+    q = rng.standard_normal((nb, hw, 8 * k)).astype(np.float32)
+    e = rng.standard_normal((hw, 10, k)).astype(np.float32)
+    vb = rng.standard_normal((2, 10, k)).astype(np.float32)
+    lam = (rng.standard_normal((2, k, k)) / np.sqrt(k)).astype(np.float32)
+    h = rng.standard_normal((nb, hw, 8 * k)).astype(np.float32)
+    qd, ed, vbd, hd = D(ctx, q), D(ctx, e), D(ctx, vb), D(ctx, h)
+    out = E.DeviceArray(ctx, q.shape)
+    zero = D(ctx, np.zeros_like(lam))
+    E.check(E.lib().mh_cross_lambda(ctx.h, qd.ptr, ed.ptr, zero.ptr, vbd.ptr, br0, nb, hw, k, None, out.ptr))
+    got0 = out.numpy()
+    lamd = D(ctx, lam)
+    E.check(E.lib().mh_cross_lambda(ctx.h, qd.ptr, ed.ptr, lamd.ptr, vbd.ptr, br0, nb, hw, k, None, out.ptr))
+    got = out.numpy()
+    E.check(E.lib().mh_cross_lambda(ctx.h, qd.ptr, ed.ptr, lamd.ptr, vbd.ptr, br0, nb, hw, k, hd.ptr, hd.ptr))
+    got_res = hd.numpy()
+    for b in range(nb):
+        zeros = np.zeros((hw, 8 * k), np.float32)
+        assert np.array_equal(got0[b], oracle.position_term(q[b], e, vb[br0 + b], zeros))
+        yc = (q[b].reshape(hw * 8, k).astype(np.float64) @ lam[br0 + b].astype(np.float64)).reshape(hw, 8 * k)
+        want = oracle.position_term(q[b], e, vb[br0 + b], yc.astype(np.float32))
+        assert max_abs_rel(got[b], want) < 1e-5
+        assert max_abs_rel(got_res[b], h[b] + want) < 1e-5
+
+
 @pytest.mark.parametrize("row_group", [0, 8])
 @pytest.mark.parametrize("plan", [None, "32,32,1", "64,64,1", "64,64,2"])
 def test_gemm_nt_kernel(ctx, row_group, plan, monkeypatch):

@@ -532,7 +532,13 @@ class UNetDevice {
         conv_out_.load(W_, d + ".conv_out", CH[0], 4);
         HIP_CHECK(hipStreamSynchronize(ctx_.stream));
         pool_.recycle(ehs);
-        HIP_CHECK(hipMalloc(&sinus_dev_, TIME_PROJ * sizeof(float)));
+        // Sinusoids of every timestep the schedulers use (0..999), computed on the
+        // host once, so a step reads its row from HBM with no host copy or sync.
+        std::vector<float> sinus(size_t(kSinusSteps + 1) * TIME_PROJ);
+        for (int t = 0; t < kSinusSteps; ++t) timestep_sinusoid(t, sinus.data() + size_t(t) * TIME_PROJ);
+        HIP_CHECK(hipMalloc(&sinus_dev_, sinus.size() * sizeof(float)));
+        HIP_CHECK(hipMemcpy(sinus_dev_, sinus.data(), size_t(kSinusSteps) * TIME_PROJ * sizeof(float),
+                            hipMemcpyHostToDevice));
     }
 
     ~UNetDevice() {
@@ -554,12 +560,17 @@ class UNetDevice {
             if (trace) trace(user, name.c_str(), t.p, t.n, t.h, t.w, t.c);
         };
         // time embedding (src/unet/embed.rs:48-66), computed once and tiled to the batch
-        float sinus[TIME_PROJ];
-        timestep_sinusoid(timestep, sinus);
-        HIP_CHECK(hipMemcpyAsync(sinus_dev_, sinus, sizeof(sinus), hipMemcpyHostToDevice, ctx_.stream));
-        HIP_CHECK(hipStreamSynchronize(ctx_.stream));  // the host array goes out of scope
+        const bool in_table = timestep >= 0 && timestep < kSinusSteps;
+        const float *sinus = sinus_dev_ + int64_t(in_table ? timestep : kSinusSteps) * TIME_PROJ;
+        if (!in_table) {  // outside the table: the spare last row
+            float host[TIME_PROJ];
+            timestep_sinusoid(timestep, host);
+            HIP_CHECK(hipMemcpyAsync(sinus_dev_ + int64_t(kSinusSteps) * TIME_PROJ, host, sizeof(host),
+                                     hipMemcpyHostToDevice, ctx_.stream));
+            HIP_CHECK(hipStreamSynchronize(ctx_.stream));  // the host array goes out of scope
+        }
         float *a1 = pool_.floats(TIME_EMBED);
-        lin1_.fwd(e, sinus_dev_, 1, a1);
+        lin1_.fwd(e, sinus, 1, a1);
         silu_inplace(ctx_, a1, TIME_EMBED);
         DT temb = pool_.tensor(b, 1, 1, TIME_EMBED);
         lin2_.fwd(e, a1, 1, temb.p);
@@ -656,7 +667,8 @@ class UNetDevice {
     Lin lin1_, lin2_;
     DwConv2d conv_in_, conv_out_;
     GN norm_out_;
-    float *sinus_dev_ = nullptr;
+    static constexpr int kSinusSteps = 1000;
+    float *sinus_dev_ = nullptr;  // [kSinusSteps + 1][TIME_PROJ]
     void *temb_w_ = nullptr;  // [temb_total_][1280]: every resnet's time_emb_proj.weight
     float *temb_b_ = nullptr;
     WeightType temb_wt_ = kF32;

@@ -242,6 +242,111 @@ __global__ __launch_bounds__(256) void tap_filter_kernel(const float *__restrict
     }
 }
 
+// Tap filter with LDS staging: a block takes tx consecutive pixels of one
+// image row; its threads are (pixel, group of HG heads, channel quad). For each
+// tap row (dy) the value row segment [x0 - 7, x0 + tx + 7) and the block's
+// pixels' 15 x 8 coefficients of that row are staged into LDS with coalesced
+// loads (double-buffered, one barrier per row), so the inner loop reads LDS
+// only and every value and coefficient leaves HBM/L2 once per block. Per output
+// element the operations are tap_filter_kernel's (the reference's order).
+template <int HG>
+__global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__restrict__ a_t,
+                                                              const float *__restrict__ v, const float *yc,
+                                                              const float *res, float *out, int hh, int ww, int vd,
+                                                              int tx) {
+    extern __shared__ float4 sh4[];
+    constexpr int kRowC4 = kWin * kHeads / 4;  // float4 of coefficients per pixel and tap row: 30
+    constexpr int NG = kHeads / HG;
+    const int v4 = vd >> 2, tpp = NG * v4, span = tx + kWin - 1;
+    float4 *vls = sh4;                  // [2][span][v4]
+    float4 *cls = sh4 + 2 * span * v4;  // [2][tx][30]
+    const int tiles_x = (ww + tx - 1) / tx;
+    const int bx = int(blockIdx.x % unsigned(tiles_x));
+    const int row = int(blockIdx.x / unsigned(tiles_x));  // b * hh + y
+    const int b = row / hh, y = row - b * hh;
+    const int x0 = bx * tx, ntx = min(tx, ww - x0);
+    const int xl = int(threadIdx.x) / tpp, r = int(threadIdx.x) - xl * tpp;
+    const int hg = r / v4, jq = r - hg * v4;
+    const int x = x0 + xl;
+    const bool active = xl < ntx;
+    const int64_t pix0 = int64_t(row) * ww + x0, pix = pix0 + xl;
+    const float4 *a4 = reinterpret_cast<const float4 *>(a_t);
+    const int64_t o4 = pix * (kHeads * v4) + int64_t(hg) * HG * v4 + jq;  // output float4 of head hg*HG
+    float4 acc[HG];
+    if (active) {
+        const float4 *yc4 = reinterpret_cast<const float4 *>(yc);
+#pragma unroll
+        for (int g = 0; g < HG / 4; ++g) {
+            const float4 bias = a4[pix * (kTapsB * kHeads / 4) + (kTaps * kHeads) / 4 + hg * (HG / 4) + g];
+            const float bb[4] = {bias.x, bias.y, bias.z, bias.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 c = yc4[o4 + (g * 4 + i) * v4];
+                acc[g * 4 + i] = make_float4(c.x + bb[i], c.y + bb[i], c.z + bb[i], c.w + bb[i]);
+            }
+        }
+    }
+    const int ky0 = max(kPad - y, 0), ky1 = min(kWin, hh + kPad - y);
+    const int kx0 = max(kPad - x, 0), kx1 = min(kWin, ww + kPad - x);
+    const float4 *vb = reinterpret_cast<const float4 *>(v) + int64_t(b) * hh * ww * v4;
+    auto stage = [&](int ky, int buf) {
+        const int iy = y + ky - kPad;
+        float4 *vd4 = vls + buf * span * v4;
+        for (int t = threadIdx.x; t < span * v4; t += blockDim.x) {
+            const int c = t / v4, q = t - c * v4, ix = x0 - kPad + c;
+            vd4[t] = (ix >= 0 && ix < ww) ? vb[(int64_t(iy) * ww + ix) * v4 + q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        float4 *cd4 = cls + buf * tx * kRowC4;
+        for (int t = threadIdx.x; t < ntx * kRowC4; t += blockDim.x) {
+            const int p = t / kRowC4, w = t - p * kRowC4;
+            cd4[t] = a4[(pix0 + p) * (kTapsB * kHeads / 4) + ky * kRowC4 + w];
+        }
+    };
+    stage(ky0, 0);
+    __syncthreads();
+    for (int ky = ky0; ky < ky1; ++ky) {
+        const int buf = (ky - ky0) & 1;
+        if (ky + 1 < ky1) stage(ky + 1, buf ^ 1);
+        if (active) {
+            const float4 *vr = vls + buf * span * v4 + xl * v4 + jq;
+            const float4 *cr = cls + buf * tx * kRowC4 + xl * kRowC4 + hg * (HG / 4);
+#pragma unroll
+            for (int kx = 0; kx < kWin; ++kx) {
+                if (kx >= kx0 && kx < kx1) {
+                    float cf[HG];
+#pragma unroll
+                    for (int g = 0; g < HG / 4; ++g) {
+                        const float4 c4 = cr[kx * 2 + g];
+                        cf[4 * g] = c4.x, cf[4 * g + 1] = c4.y, cf[4 * g + 2] = c4.z, cf[4 * g + 3] = c4.w;
+                    }
+                    const float4 s = vr[kx * v4];
+#pragma unroll
+                    for (int i = 0; i < HG; ++i) {
+                        acc[i].x = __builtin_fmaf(cf[i], s.x, acc[i].x);
+                        acc[i].y = __builtin_fmaf(cf[i], s.y, acc[i].y);
+                        acc[i].z = __builtin_fmaf(cf[i], s.z, acc[i].z);
+                        acc[i].w = __builtin_fmaf(cf[i], s.w, acc[i].w);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (active) {
+        float4 *out4 = reinterpret_cast<float4 *>(out);
+        const float4 *res4 = reinterpret_cast<const float4 *>(res);
+#pragma unroll
+        for (int i = 0; i < HG; ++i) {
+            float4 u = acc[i];
+            if (res) {
+                const float4 h = res4[o4 + i * v4];
+                u = make_float4(h.x + u.x, h.y + u.y, h.z + u.z, h.w + u.w);
+            }
+            out4[o4 + i * v4] = u;
+        }
+    }
+}
+
 // 8-lane dot of src/unet/lambda.rs:429-439 (k a multiple of 8).
 __device__ __forceinline__ float dot8_ref(const float *__restrict__ a, const float *__restrict__ b, int k) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -485,10 +590,32 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
     // gives the chip about 2048 waves: 4 at 64x64 x 40 channels, 2 at 32x32 x 80,
     // 1 at 16x16 x 160 (batch 2).
     const int v4 = vd / 4;
+    // Default (measured on MI355X at the UNet's three sizes): the LDS-staged
+    // row-tile kernel with 4 heads per thread while a block spans 10 or more
+    // pixels (its value rows are then staged at most 2.4 times over: 64x64 x 40
+    // 59.6 -> 47.2 us), else the per-thread kernel with 4 heads per thread
+    // (32x32 x 80: 28.4 us, 16x16 x 160: 18.7 us; the tile kernel 34.7 / 35.0).
+    // MOEBIUS_HIP_TAP_HEADS forces a variant for A/B runs: "t8" / "t4" the tile
+    // kernel with 8 / 4 heads per thread; 1, 2, 4 or 8 the per-thread kernel.
+    const char *force = std::getenv("MOEBIUS_HIP_TAP_HEADS");
+    int tile_hg = (!force && std::min(256 / (2 * v4), ww) >= 10) ? 4 : 0;
+    if (force && force[0] == 't') tile_hg = std::atoi(force + 1) == 4 ? 4 : 8;
+    if (tile_hg && (kHeads / tile_hg) * v4 <= 256) {
+        const int tpp = (kHeads / tile_hg) * v4, tx = std::max(1, std::min(256 / tpp, ww));
+        const size_t lds = (size_t(2) * (tx + kWin - 1) * v4 + size_t(2) * tx * (kWin * kHeads / 4)) * 16;
+        const int64_t blocks = int64_t(nb) * hh * ceil_div(ww, tx);
+        if (tile_hg == 8)
+            tap_filter_tile_kernel<8><<<unsigned(blocks), unsigned(tx * tpp), lds, ctx.stream>>>(
+                a_t, v, yc, residual, out, hh, ww, vd, tx);
+        else
+            tap_filter_tile_kernel<4><<<unsigned(blocks), unsigned(tx * tpp), lds, ctx.stream>>>(
+                a_t, v, yc, residual, out, hh, ww, vd, tx);
+        MH_LAUNCH_CHECK();
+        return;
+    }
     int hg = 4;
-    while (hg > 1 && pix * v4 * (kHeads / hg) < 2048 * 64) hg >>= 1;
-    if (const char *f = std::getenv("MOEBIUS_HIP_TAP_HEADS")) {
-        const int want = std::atoi(f);
+    if (force) {
+        const int want = std::atoi(force);
         if (want == 1 || want == 2 || want == 4 || want == 8) hg = want;
     }
     const int64_t total = pix * (kHeads / hg) * v4;

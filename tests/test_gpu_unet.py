@@ -45,10 +45,17 @@ def test_softmax_lambda_kernel(ctx, nb, rows, k):
         assert max_abs_rel(got[b].T, want) < 1e-5
 
 
-@pytest.mark.parametrize("nb,hh,ww,vd", [(2, 16, 12, 40), (1, 7, 5, 8), (2, 16, 16, 160), (1, 20, 9, 80)])
-@pytest.mark.parametrize("heads_per_thread", ["8", "4", "2"])
+# "default": the planner's choice; "t8"/"t4": the LDS-staged row-tile kernel
+# with 8 / 4 heads per thread (partial tiles at 9 x 70, 16 x 16 x 160 and
+# 20 x 9); "8"/"4"/"2": the per-thread kernel's variants.
+@pytest.mark.parametrize("nb,hh,ww,vd", [(2, 16, 12, 40), (1, 7, 5, 8), (2, 16, 16, 160), (1, 20, 9, 80),
+                                         (1, 9, 70, 40)])
+@pytest.mark.parametrize("heads_per_thread", ["default", "t8", "t4", "8", "4", "2"])
 def test_tap_filter_kernel_bit_exact(ctx, nb, hh, ww, vd, heads_per_thread, monkeypatch):
-    monkeypatch.setenv("MOEBIUS_HIP_TAP_HEADS", heads_per_thread)
+    if heads_per_thread == "default":
+        monkeypatch.delenv("MOEBIUS_HIP_TAP_HEADS", raising=False)
+    else:
+        monkeypatch.setenv("MOEBIUS_HIP_TAP_HEADS", heads_per_thread)
     rng = np.random.default_rng(hh * ww + vd)
     a = rng.standard_normal((nb, hh * ww, 8, 226)).astype(np.float32)
     v = rng.standard_normal((nb, hh * ww, vd)).astype(np.float32)

@@ -29,91 +29,92 @@ namespace {
 constexpr int kWin = 15, kTaps = 225, kPad = 7, kTapsB = 226;
 constexpr int kHeads = 8, kTokens = 10;
 
-// Rows per softmax_lambda chunk: at most ~400K multiply-adds of e^T V per
-// block and 64 KB of LDS (128 rows at k = vd = 40, 64 at 80, 16 at 160), so the
-// UNet's levels get 16-32 chunks per item and the partials are few to fold.
-int lambda_chunk_rows(int k, int vd) {
-    int ch = 256;
-    while (ch > 8 && (int64_t(ch) * k * vd > 409600 || int64_t(ch) * (k + vd) + k > 16384)) ch >>= 1;
-    return ch;
+// softmax_lambda work split: chunks of rows per item (about 16-32, so the
+// finalising fold stays short) and tiles of tk key columns per block, so the
+// UNet's three sizes get 300+ blocks: 64x64 x 40 -> 128 rows x 8 columns,
+// 32x32 x 80 -> 64 x 16, 16x16 x 160 -> 16 x 16.
+struct LambdaSplit {
+    int ch, chunks, tk, ktiles;
+};
+
+LambdaSplit lambda_split(int rows, int k, int vd) {
+    LambdaSplit s;
+    s.ch = 128;
+    while (s.ch > 8 && ceil_div(rows, s.ch) < 16) s.ch >>= 1;
+    while (s.ch > 8 && int64_t(s.ch) * (16 + vd) > 12288) s.ch >>= 1;  // LDS: keys tile + values
+    s.chunks = int(ceil_div(rows, s.ch));
+    s.tk = k % 16 == 0 && k >= 80 ? 16 : (k % 8 == 0 ? 8 : 4);
+    s.ktiles = int(ceil_div(k, s.tk));
+    return s;
 }
 
-// Column maxima of keys [b][rows][k] per chunk -> pmax [b][chunks][k].
-// 64 lanes over column quads (k <= 160 -> at most 40), 4 waves over rows.
-__global__ __launch_bounds__(256) void lambda_colmax_kernel(const float *__restrict__ keys, int rows, int k, int ch,
-                                                            int chunks, float *__restrict__ pmax) {
-    const int chunk = blockIdx.x, b = blockIdx.y;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int k4 = k >> 2;
-    const int r0 = chunk * ch, r1 = min(rows, r0 + ch);
-    float4 m = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-    if (lane < k4) {
-        const float4 *kb = reinterpret_cast<const float4 *>(keys + size_t(b) * rows * k) + lane;
-        for (int r = r0 + wave; r < r1; r += 4) {
-            const float4 x = kb[size_t(r) * k4];
-            m = make_float4(fmaxf(m.x, x.x), fmaxf(m.y, x.y), fmaxf(m.z, x.z), fmaxf(m.w, x.w));
-        }
-    }
-    __shared__ float4 red[4][64];
-    red[wave][lane] = m;
-    __syncthreads();
-    if (wave == 0 && lane < k4) {
-#pragma unroll
-        for (int w = 1; w < 4; ++w) {
-            const float4 x = red[w][lane];
-            m = make_float4(fmaxf(m.x, x.x), fmaxf(m.y, x.y), fmaxf(m.z, x.z), fmaxf(m.w, x.w));
-        }
-        reinterpret_cast<float4 *>(pmax + (size_t(b) * chunks + chunk) * k)[lane] = m;
-    }
-}
-
-// One block per (chunk, item): e = exp(K - max) into LDS, f32 column sums,
-// and the chunk's partial e^T V [k][vd] (rows summed in order with fmaf).
-// Dynamic LDS: e [ch][k], v [ch][vd], max [k].
+// One block per (chunk, item, key tile): chunk-local column maxima m of its tk
+// key columns, e = exp(K - m) (the reference's Cephes exp), f32 column sums of
+// e and the partial e^T V [tk][vd] over the chunk's rows. The chunk results
+// are rescaled to the global maximum when they are folded (finalize), so no
+// separate maximum pass is needed. Dynamic LDS: e [ch][tk], v [ch][vd],
+// reduction scratch [256].
 __global__ __launch_bounds__(256) void lambda_partial_kernel(const float *__restrict__ keys,
                                                              const float *__restrict__ v, int rows, int k, int vd,
-                                                             int ch, int chunks, const float *__restrict__ pmax,
+                                                             int ch, int chunks, int tk, float *__restrict__ pmax,
                                                              float *__restrict__ psum, float *__restrict__ plam) {
     extern __shared__ float lds[];
-    float *es = lds, *vs = lds + ch * k, *mx = vs + ch * vd;
-    const int chunk = blockIdx.x, b = blockIdx.y;
-    const int r0 = chunk * ch;
-    const int nr = min(ch, rows - r0);
-    for (int j = threadIdx.x; j < k; j += 256) {
-        const float *pm = pmax + size_t(b) * chunks * k + j;
-        // eight chunk maxima in flight per step (the maximum is order-free)
-        float m[8] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY, -INFINITY, -INFINITY, -INFINITY, -INFINITY};
-        for (int c0 = 0; c0 < chunks; c0 += 8) {
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                m[u] = fmaxf(m[u], pm[size_t(min(c0 + u, chunks - 1)) * k]);  // a repeat is harmless
-        }
-        mx[j] = fmaxf(fmaxf(fmaxf(m[0], m[1]), fmaxf(m[2], m[3])), fmaxf(fmaxf(m[4], m[5]), fmaxf(m[6], m[7])));
+    float *es = lds, *vs = lds + ch * tk, *red = vs + ch * vd;
+    const int chunk = blockIdx.x, b = blockIdx.y, k0 = blockIdx.z * tk;
+    const int r0 = chunk * ch, nr = min(ch, rows - r0);
+    const int nk = min(tk, k - k0);
+    const float *kb = keys + (size_t(b) * rows + r0) * k + k0;
+    for (int i = threadIdx.x; i < nr * tk; i += 256) {
+        const int r = i / tk, j = i - r * tk;
+        es[i] = j < nk ? kb[size_t(r) * k + j] : 0.0f;
+    }
+    const float4 *vb4 = reinterpret_cast<const float4 *>(v + (size_t(b) * rows + r0) * vd);
+    float4 *vs4 = reinterpret_cast<float4 *>(vs);
+    for (int i = threadIdx.x; i < nr * (vd >> 2); i += 256) vs4[i] = vb4[i];
+    __syncthreads();
+    // column maxima and (after exp) column sums: column j = t % tk, rows
+    // r = g, g + G, ... for row group g = t / tk; groups folded in order
+    const int G = 256 / tk;
+    const int j = threadIdx.x % tk, g = threadIdx.x / tk;
+    float m = -INFINITY;
+    if (g < G)
+        for (int r = g; r < nr; r += G) m = fmaxf(m, es[r * tk + j]);
+    red[threadIdx.x] = m;
+    __syncthreads();
+    if (threadIdx.x < tk) {
+        float mm = red[threadIdx.x];
+        for (int q = 1; q < G; ++q) mm = fmaxf(mm, red[q * tk + threadIdx.x]);
+        red[threadIdx.x] = mm;  // read back below as the column maximum
     }
     __syncthreads();
-    const float *kb = keys + (size_t(b) * rows + r0) * k;
-    const float *vb = v + (size_t(b) * rows + r0) * vd;
-    for (int i = threadIdx.x; i < nr * k; i += 256) {
-        const int j = i % k;
-        es[i] = ref_exp(kb[i] - mx[j]);
-    }
-    for (int i = threadIdx.x; i < nr * vd; i += 256) vs[i] = vb[i];
+    const float colmax = red[j];
     __syncthreads();
-    float *ps = psum + (size_t(b) * chunks + chunk) * k;
-    for (int j = threadIdx.x; j < k; j += 256) {
-        float s = 0.0f;
-        for (int r = 0; r < nr; ++r) s += es[r * k + j];
-        ps[j] = s;
+    for (int i = threadIdx.x; i < nr * tk; i += 256) es[i] = ref_exp(es[i] - red[i % tk]);
+    // (red[0..tk) still holds the maxima: the loop above only reads it)
+    float sum = 0.0f;
+    __syncthreads();
+    if (g < G)
+        for (int r = g; r < nr; r += G) sum += es[r * tk + j];
+    __syncthreads();
+    red[threadIdx.x] = sum;
+    __syncthreads();
+    if (threadIdx.x < nk) {
+        float t = red[threadIdx.x];
+        for (int q = 1; q < G; ++q) t += red[q * tk + threadIdx.x];
+        const size_t o = (size_t(b) * chunks + chunk) * k + k0 + threadIdx.x;
+        psum[o] = t;
+        pmax[o] = colmax;
     }
-    // e^T V: task (kk, j quad); vd % 4 == 0.
+    // e^T V: task (kk, j quad) per thread and pass
     const int vq = vd >> 2;
-    float4 *pl = reinterpret_cast<float4 *>(plam + (size_t(b) * chunks + chunk) * size_t(k) * vd);
-    for (int t = threadIdx.x; t < k * vq; t += 256) {
+    float4 *pl = reinterpret_cast<float4 *>(plam + ((size_t(b) * chunks + chunk) * k + k0) * vd);
+    for (int t = threadIdx.x; t < nk * vq; t += 256) {
         const int kk = t / vq, jq = t - kk * vq;
         float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4 *vr = reinterpret_cast<const float4 *>(vs) + jq;
+        const float4 *vr = vs4 + jq;
+#pragma unroll 4
         for (int r = 0; r < nr; ++r) {
-            const float e = es[r * k + kk];
+            const float e = es[r * tk + kk];
             const float4 x = vr[r * vq];
             acc.x = __builtin_fmaf(e, x.x, acc.x);
             acc.y = __builtin_fmaf(e, x.y, acc.y);
@@ -124,28 +125,44 @@ __global__ __launch_bounds__(256) void lambda_partial_kernel(const float *__rest
     }
 }
 
-// out_t [b][vd][k] = (sum over chunks of plam[b][c][kk][j]) * (f32)(1 / sum over
-// chunks of psum[b][c][kk]); chunk partials folded in chunk order, the sums in f64.
-__global__ __launch_bounds__(256) void lambda_finalize_kernel(const float *__restrict__ psum,
+// out_t [b][vd][k] = (sum over chunks of plam[b][c][kk][j] * f_c) * (f32)(1 /
+// sum over chunks of psum[b][c][kk] * f_c), f_c = exp(m_c - max over chunks of
+// m_c): the chunk partials rescaled to the global column maximum. Block: kt
+// key rows kk of one item. Per row one wave takes the chunks on its lanes
+// (chunks <= 64): maximum and f_c, then the f64 sum of psum * f_c over a fixed
+// shuffle tree; then every thread folds lambda over the chunks in order (f32).
+__global__ __launch_bounds__(256) void lambda_finalize_kernel(const float *__restrict__ pmax,
+                                                              const float *__restrict__ psum,
                                                               const float *__restrict__ plam, int k, int vd,
-                                                              int chunks, int nb, float *__restrict__ out_t) {
-    const int64_t total = int64_t(nb) * k * vd;
-    const int64_t e = blockIdx.x * int64_t(256) + threadIdx.x;
-    if (e >= total) return;
-    const int b = int(e / (int64_t(k) * vd));
-    const int i = int(e - int64_t(b) * k * vd);
-    const int kk = i / vd, j = i - kk * vd;
-    const float *pl = plam + size_t(b) * chunks * size_t(k) * vd + i;
-    const float *ps = psum + size_t(b) * chunks * k + kk;
-    float acc = 0.0f;
-    double s = 0.0;
-#pragma unroll 4
-    for (int c = 0; c < chunks; ++c) {
-        acc += pl[size_t(c) * k * vd];
-        s += double(ps[size_t(c) * k]);
+                                                              int chunks, int kt, float *__restrict__ out_t) {
+    __shared__ float fs[64][64];  // [row in tile][chunk]
+    __shared__ float sinv[64];
+    const int b = blockIdx.y, kk0 = blockIdx.x * kt;
+    const int nk = min(kt, k - kk0);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = int(blockDim.x) >> 6;
+    for (int r = wave; r < nk; r += waves) {
+        const int kk = kk0 + r;
+        const size_t o = (size_t(b) * chunks + lane) * k + kk;
+        const float m = lane < chunks ? pmax[o] : -INFINITY;
+        float mx = m;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        const float f = lane < chunks ? ref_exp(m - mx) : 0.0f;
+        fs[r][lane] = f;
+        double t = lane < chunks ? double(psum[o]) * double(f) : 0.0;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off, 64);
+        if (lane == 0) sinv[r] = float(1.0 / t);
     }
-    const float inv = float(1.0 / s);
-    out_t[(size_t(b) * vd + j) * k + kk] = acc * inv;
+    __syncthreads();
+    for (int t = threadIdx.x; t < nk * vd; t += blockDim.x) {
+        const int r = t / vd, j = t - r * vd, kk = kk0 + r;
+        const float *pl = plam + size_t(b) * chunks * size_t(k) * vd + size_t(kk) * vd + j;
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int c = 0; c < chunks; ++c) acc = __builtin_fmaf(pl[size_t(c) * k * vd], fs[r][c], acc);
+        out_t[(size_t(b) * vd + j) * k + kk] = acc * sinv[r];
+    }
 }
 
 // HG heads' coefficients of one tap: a_t row [226][8] (heads innermost).
@@ -557,25 +574,24 @@ __global__ __launch_bounds__(256) void cross_lambda_kernel(const float *__restri
 
 void softmax_lambda(Context &ctx, const float *keys, const float *v, int nb, int rows, int k, int vd,
                     float *lambda_t) {
-    MH_REQUIRE(k > 0 && k <= 160 && vd > 0 && vd <= 160, "softmax_lambda: widths above 160 are not supported");
+    MH_REQUIRE(k > 0 && k <= 256 && vd > 0 && vd <= 256, "softmax_lambda: widths above 256 are not supported");
     MH_REQUIRE(k % 4 == 0 && vd % 4 == 0, "softmax_lambda: widths must be multiples of 4");
     MH_REQUIRE(aligned16(keys) && aligned16(v), "softmax_lambda: keys and v must be 16-byte aligned");
     MH_REQUIRE(rows > 0 && nb > 0, "softmax_lambda: empty input");
-    const int ch = lambda_chunk_rows(k, vd);
-    const int chunks = int(ceil_div(rows, ch));
-    const size_t pm = size_t(nb) * chunks * k;
-    const size_t pl = size_t(nb) * chunks * size_t(k) * vd;
+    const LambdaSplit sp = lambda_split(rows, k, vd);
+    MH_REQUIRE(sp.chunks <= 64, "softmax_lambda: at most 64 x 128 rows per item");
+    const size_t pm = size_t(nb) * sp.chunks * k;
+    const size_t pl = size_t(nb) * sp.chunks * size_t(k) * vd;
     float *ws = static_cast<float *>(ctx.ws.get((2 * pm + pl) * sizeof(float), ctx.stream));
     float *pmax = ws, *psum = ws + pm, *plam = ws + 2 * pm;
-    lambda_colmax_kernel<<<dim3(chunks, nb), 256, 0, ctx.stream>>>(keys, rows, k, ch, chunks, pmax);
+    const size_t lds = (size_t(sp.ch) * (sp.tk + vd) + 256) * sizeof(float);
+    lambda_partial_kernel<<<dim3(sp.chunks, nb, sp.ktiles), 256, lds, ctx.stream>>>(
+        keys, v, rows, k, vd, sp.ch, sp.chunks, sp.tk, pmax, psum, plam);
     MH_LAUNCH_CHECK();
-    const size_t lds = (size_t(ch) * (k + vd) + k) * sizeof(float);
-    lambda_partial_kernel<<<dim3(chunks, nb), 256, lds, ctx.stream>>>(keys, v, rows, k, vd, ch, chunks, pmax, psum,
-                                                                      plam);
-    MH_LAUNCH_CHECK();
-    const int64_t total = int64_t(nb) * k * vd;
-    lambda_finalize_kernel<<<unsigned(ceil_div(total, 256)), 256, 0, ctx.stream>>>(psum, plam, k, vd, chunks, nb,
-                                                                                   lambda_t);
+    const int kt = std::max(1, std::min(64, 256 / vd));
+    const unsigned threads = unsigned(std::max(64, std::min(256, int(ceil_div(kt * vd, 64)) * 64)));
+    lambda_finalize_kernel<<<dim3(unsigned(ceil_div(k, kt)), unsigned(nb)), threads, 0, ctx.stream>>>(
+        pmax, psum, plam, k, vd, sp.chunks, kt, lambda_t);
     MH_LAUNCH_CHECK();
 }
 

@@ -24,6 +24,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "ms per 512² UNet denoise step; conv MFMA util %; GroupNorm HBM GB/s"
 PEAK_F32_MFMA_TFLOPS = 157.3
+PEAK_F16_MFMA_TFLOPS = 2500.0
 PEAK_HBM_GBPS = 8000.0
 
 
@@ -149,7 +150,7 @@ def _components(ctx, steps):
 DOMINANT_TRAFFIC_BYTES = int((17.01 + 10.00) * 1048576)
 
 
-def _dominant_gemm(ctx, steps):
+def _dominant_gemm(ctx, steps, fast=False):
     """The step's most frequent GEMM, timed on its own with events: the 1x1 conv of
     a [2,64,64,320] map to 320 channels with bias (gemm_f32_kernel, 32x32 tiles on
     v_mfma_f32_16x16x4f32, 2560 workgroups), i.e. M = 8192, N = 320, K = 320."""
@@ -157,12 +158,24 @@ def _dominant_gemm(ctx, steps):
     from moebius_cpu_amd import synthetic as S
 
     x = E.Tensor.from_numpy(ctx, S.normal(81, (2, 64, 64, 320)))
-    conv = E.Conv1x1(ctx, 320, 320, E.Param(ctx, S.normal(82, (320, 320), 0.05)), S.normal(83, (320,), 0.02))
+    conv = E.Conv1x1(ctx, 320, 320, E.Param(ctx, S.normal(82, (320, 320), 0.05), f16=fast), S.normal(83, (320,), 0.02))
     y = E.Tensor(ctx)
     conv.forward(x, y)
     us = time_region(ctx, lambda: conv.forward(x, y), steps) * 1e3
     flops = 2.0 * 8192 * 320 * 320
     tf = flops / (us * 1e-6) / 1e12
+    if fast:
+        # f16 products at 16x the f32 rate leave this shape bound by its operand
+        # traffic: x read and y written in f32, the weight read in f16.
+        nbytes = 8192 * 320 * 4 * 2 + 320 * 320 * 2 + 320 * 4
+        gbps = nbytes / (us * 1e-6) / 1e9
+        return {"bound": "hbm", "kernel": "gemm_h16_kernel (f16 MFMA, f32 accumulate; 1x1 conv [2,64,64,320] -> "
+                                          "320, M=8192 N=320 K=320: the step's most frequent GEMM)",
+                "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None,
+                "work_per_launch": f"algorithmic bytes {nbytes}; {flops / 1e9:.3f} GFLOP "
+                                   f"({tf:.1f} TFLOP/s = {tf / PEAK_F16_MFMA_TFLOPS:.3f} of f16 MFMA peak)",
+                "avg_launch_us": round(us, 2)}
     return {"bound": "mfma", "kernel": "gemm_f32_kernel<32,32,dense> (1x1 conv [2,64,64,320] -> 320, "
                                        "M=8192 N=320 K=320: the step's most frequent GEMM)",
             "achieved": round(tf, 2), "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
@@ -183,7 +196,9 @@ def bench_unet(args):
     params = U.random_unet(seed=4000)
     inp = U.unet_input(seed=5000)
     ctx = E.Context(0)
-    net = UNet(ctx, params, f16_gemm=args.f16_weights)
+    if args.fast:
+        ctx.set_precision(True)
+    net = UNet(ctx, params, f16_gemm=args.f16_weights or args.fast)
     x = E.DeviceArray.from_numpy(ctx, inp.x)
     eps = E.DeviceArray(ctx, (b, 64, 64, 4))
     step = lambda: net.forward(x, inp.timestep, cfg, eps)  # noqa: E731
@@ -196,21 +211,26 @@ def bench_unet(args):
     flops = U.step_flops(b)
     achieved = flops["total"] / (ms * 1e-3) / 1e12
     wbytes, pbytes = net.memory()
+    peak = PEAK_F16_MFMA_TFLOPS if args.fast else PEAK_F32_MFMA_TFLOPS
+    if args.fast:
+        arith = "FAST: f16-stored GEMM weights, GEMM operands rounded to f16 on f16 MFMA with f32 accumulate"
+    else:
+        arith = f"{'f16-stored GEMM weights, ' if args.f16_weights else ''}f32 arithmetic"
     out = {
         "metric": METRIC, "value": round(ms, 4), "unit": "ms", "higher_is_better": False,
-        "ms_per_step": round(ms, 4), "dtype": "f32",
+        "ms_per_step": round(ms, 4), "dtype": "f16 (f32 accumulate)" if args.fast else "f32",
         "config": {"workload": "Moebius UNet denoise step, 512x512 image (64x64x9 latent stack), "
-                               f"{'CFG batch 2' if cfg else 'cond-only batch 1'}, "
-                               f"{'f16-stored GEMM weights, ' if args.f16_weights else ''}f32 arithmetic",
+                               f"{'CFG batch 2' if cfg else 'cond-only batch 1'}, {arith}",
                    "latent": [1, 64, 64, 9], "batch": b, "timestep": inp.timestep,
                    "params_M": round(U.param_count() / 1e6, 1), "weight_bytes": wbytes, "pool_bytes": pbytes},
         "step_roofline": {"bound": "mfma", "kernel": "whole step (all kernels, one stream)",
-                          "achieved": round(achieved, 2), "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                          "frac": round(achieved / PEAK_F32_MFMA_TFLOPS, 4),
+                          "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
+                          "frac": round(achieved / peak, 4),
                           "work": f"{flops['total'] / 1e9:.1f} GFLOP per step"},
     }
     log("dominant kernel and component kernels")
-    out["roofline"] = _dominant_gemm(ctx, 50)
+    out["roofline"] = _dominant_gemm(ctx, 50, fast=args.fast)
+    ctx.set_precision(False)
     out["components"] = _components(ctx, 20)
     del net, x, eps
     ctx.close()
@@ -279,6 +299,8 @@ def main():
     ap.add_argument("--workload", default="unet_step", choices=sorted(WORKLOADS))
     ap.add_argument("--cond-only", action="store_true", help="UNet: batch 1 (no CFG)")
     ap.add_argument("--f16-weights", action="store_true", help="UNet / VAE: f16-stored GEMM weights")
+    ap.add_argument("--fast", action="store_true",
+                    help="UNet: FAST precision (f16-stored weights, f16 MFMA with f32 accumulate)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="end with one 256 MiB device-to-device copy (the known-size reference that "

@@ -84,6 +84,16 @@ struct Context {
     Context &operator=(const Context &) = delete;
 };
 
+// Sets the context's GEMM precision for a scope, then restores it.
+struct PrecisionScope {
+    Context &ctx;
+    Precision saved;
+    PrecisionScope(Context &c, Precision p) : ctx(c), saved(c.precision) { c.precision = p; }
+    ~PrecisionScope() { ctx.precision = saved; }
+    PrecisionScope(const PrecisionScope &) = delete;
+    PrecisionScope &operator=(const PrecisionScope &) = delete;
+};
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // NULL counts as aligned (an absent optional operand).

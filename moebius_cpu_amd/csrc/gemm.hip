@@ -22,7 +22,7 @@
 // Small grids (MI355X has 256 CUs) split K across workgroups; the partial
 // tiles are summed in a fixed order by a reduction kernel that also applies
 // bias / residual / SiLU, so results are deterministic run to run.
-#include "gemm_kernel.hpp"
+#include "gemm_h16.hpp"
 
 namespace mh {
 using namespace gemm;
@@ -33,6 +33,18 @@ uint32_t extent(int64_t rows, int64_t ld, int64_t cols, int esz) {
     const int64_t bytes = rows > 0 ? ((rows - 1) * ld + cols) * esz : 0;
     MH_REQUIRE(bytes < (int64_t(1) << 31), "GEMM operand above 2 GiB");
     return uint32_t(bytes);
+}
+
+// Context precision selects the kernel family: EXACT runs f32 matrix
+// instructions, FAST the f16 ones (activations rounded to f16 as they load).
+void run_dense(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi, int batch, bool vec) {
+    if (ctx.precision == Precision::Fast) launch_dense_h16(ctx, p, wt, epi, batch, vec);
+    else launch_dense(ctx, p, wt, epi, batch, vec);
+}
+
+void run_conv(Context &ctx, GemmArgs &p, WeightType wt, int mode, bool pro) {
+    if (ctx.precision == Precision::Fast) launch_conv_h16(ctx, p, wt, mode, pro);
+    else launch_conv(ctx, p, wt, mode, pro);
 }
 
 __global__ void im2col_gather_kernel(GemmArgs p, int64_t first, int64_t count, float *__restrict__ rows) {
@@ -97,9 +109,9 @@ void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void 
     }
     p.res2 = residual2;
     if (c_in % 4 == 0 && aligned16(x))
-        launch_dense(ctx, p, wt, epi, 1, true);
+        run_dense(ctx, p, wt, epi, 1, true);
     else
-        launch_dense(ctx, p, wt, epi, 1, false);
+        run_dense(ctx, p, wt, epi, 1, false);
 }
 
 void conv1x1_segments(Context &ctx, const float *x, int64_t pixels, int c_in, const void *weight, WeightType wt,
@@ -128,7 +140,7 @@ void conv1x1_segments(Context &ctx, const float *x, int64_t pixels, int c_in, co
     p.b_bytes = extent(n, c_in, c_in, wt == kF16 ? 2 : 4);
     p.bias = bias;
     p.ldc = n;
-    launch_dense(ctx, p, wt, GemmEpilogue::None, 1, c_in % 4 == 0 && aligned16(x));
+    run_dense(ctx, p, wt, GemmEpilogue::None, 1, c_in % 4 == 0 && aligned16(x));
 }
 
 void gemm_nt(Context &ctx, const float *a, int64_t lda, int64_t a_bs, const void *b, WeightType wt, int64_t ldb,
@@ -157,9 +169,9 @@ void gemm_nt(Context &ctx, const float *a, int64_t lda, int64_t a_bs, const void
     p.rg = row_group;
     const bool vec = k % 4 == 0 && lda % 4 == 0 && aligned16(a) && (batch == 1 || a_bs % 4 == 0);
     if (vec)
-        launch_dense(ctx, p, wt, epi, batch, true);
+        run_dense(ctx, p, wt, epi, batch, true);
     else
-        launch_dense(ctx, p, wt, epi, batch, false);
+        run_dense(ctx, p, wt, epi, batch, false);
 }
 
 void conv3x3_output_hw(int h, int w, int stride, const int pad[4], bool upsample2x, int *ho, int *wo) {
@@ -217,7 +229,7 @@ void conv3x3(Context &ctx, const float *x, int n, int h, int w, int c_in, const 
     const int esz = wt == kF16 ? 2 : 4;
     const bool wvec = (reinterpret_cast<uintptr_t>(weight) % (4 * esz)) == 0;
     const int mode = vec && wvec ? (c_in % BK == 0 ? kConvAligned : kConvVec) : kConvScalar;
-    launch_conv(ctx, p, wt, mode, pro);
+    run_conv(ctx, p, wt, mode, pro);
 }
 
 void im2col_gather(Context &ctx, const float *x, int n, int h, int w, int c, int stride, const int pad[4],

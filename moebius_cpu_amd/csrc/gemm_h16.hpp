@@ -1,0 +1,376 @@
+// Fast-precision GEMM kernel (f16 matrix cores, f32 accumulate) shared by
+// gemm_fast_dense.hip and gemm_fast_conv.hip. Same operands, conv gathers,
+// epilogues and split-K reduction as the f32 kernel of gemm_kernel.hpp; what
+// changes is the arithmetic:
+//   - the A operand (f32 activations, or the gathered conv input after the
+//     optional GroupNorm prologue) is rounded to f16 (round to nearest even,
+//     saturated at +-65504 so an outlier does not become inf) as it is staged
+//     in LDS;
+//   - f16 weights enter as stored; f32 weights are rounded like A;
+//   - products run on v_mfma_f32_32x32x16_f16 (tiles of 64 or more in both
+//     dimensions) or v_mfma_f32_16x16x32_f16 (32-wide tiles), summed in f32.
+// Each lane reads eight consecutive K of one A row and of one B column from
+// LDS with one 16-byte read per instruction; A and B use the same lane-to-K
+// assignment, so the sum covers every K exactly once whatever order the
+// matrix unit takes the eight values in.
+#pragma once
+
+#include "gemm_kernel.hpp"
+
+namespace mh {
+namespace gemm {
+
+typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
+
+// Launchers of the fast kernels (gemm_fast_dense.hip, gemm_fast_conv.hip).
+void launch_dense_h16(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi, int batch, bool vec);
+void launch_conv_h16(Context &ctx, GemmArgs &p, WeightType wt, int mode, bool pro);
+
+namespace {
+
+constexpr int BKH = 64;          // K per LDS stage
+constexpr int LDS_H = BKH + 8;   // padded LDS row stride (halves): 144 bytes, conflict-free b128 reads
+constexpr int KCH = BKH / 4;     // 4-element chunks per tile row
+
+template <int M>
+struct MfH {
+    static constexpr int kAccRegs = M * M / 64;
+    static constexpr int kKStep = M == 32 ? 16 : 32;  // K per instruction
+    typedef std::conditional_t<M == 32, floatx16, floatx4> Acc;
+    static __device__ __forceinline__ Acc mfma(halfx8 a, halfx8 b, const Acc &c) {
+        if constexpr (M == 32) return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+        else return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+// f32 -> f16, round to nearest even; finite values beyond f16's range saturate
+// to +-65504, NaN stays NaN.
+__device__ __forceinline__ halfx4 to_h4(floatx4 v) {
+    halfx4 h;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float x = __builtin_fabsf(v[e]) > 65504.0f ? __builtin_copysignf(65504.0f, v[e]) : v[e];
+        h[e] = static_cast<_Float16>(x);
+    }
+    return h;
+}
+
+// Four consecutive K of A row m, starting at k (k0: first K of the tile, whose
+// tap the aligned conv gather shares across the tile).
+template <int MODE, bool PRO>
+__device__ __forceinline__ floatx4 load_a_h(const GemmArgs &p, __amdgpu_buffer_rsrc_t ar, const ConvRow &r, int m,
+                                            int k, int k_end, int tky, int tkx, int tci, int k0) {
+    if constexpr (MODE == kDense) {
+        const bool ok = m < p.M && k < k_end;
+        return buf_load4(ar, ok ? int((int64_t(m) * p.lda + k) * 4) : kOob);
+    } else if constexpr (MODE == kConvAligned || MODE == kConvVec) {
+        int ky, kx, c;
+        if constexpr (MODE == kConvAligned) {
+            ky = tky;
+            kx = tkx;
+            c = tci + (k - k0);
+        } else {
+            const int tap = k / p.ci;
+            c = k - tap * p.ci;
+            ky = tap / 3;
+            kx = tap - ky * 3;
+        }
+        const int64_t src = conv_src(p, r, ky, kx);
+        const bool ok = k < k_end && src >= 0;
+        floatx4 v = buf_load4(ar, ok ? int((src + c) * 4) : kOob);
+        if constexpr (PRO) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = ok ? prologue1(p, r.b, c + e, v[e]) : 0.0f;
+        }
+        return v;
+    } else {  // scalar modes
+        return k < k_end ? load_a<MODE, PRO>(p, r, m, k, tky, tkx, tci) : zero4();
+    }
+}
+
+// B chunk as stored: f16 weights with vector rows come as raw halves.
+template <bool F16, bool BVEC>
+struct BChunk {
+    typedef std::conditional_t<F16 && BVEC, halfx4, floatx4> T;
+};
+
+template <bool F16, bool BVEC>
+__device__ __forceinline__ typename BChunk<F16, BVEC>::T load_b_h(const GemmArgs &p, __amdgpu_buffer_rsrc_t br,
+                                                                   int n, int k, int k_end) {
+    if constexpr (F16 && BVEC) {
+        const bool ok = n < p.N && k < k_end;
+        const auto raw =
+            __builtin_amdgcn_raw_buffer_load_b64(br, ok ? int((int64_t(n) * p.ldb + k) * 2) : kOob, 0, 0);
+        return __builtin_bit_cast(halfx4, raw);
+    } else if constexpr (BVEC) {
+        return load_b_buf<false>(p, br, n, k, k_end);
+    } else {
+        return k < k_end ? load_b<F16, false>(p, n, k) : zero4();
+    }
+}
+
+__device__ __forceinline__ halfx4 as_h4(halfx4 v) { return v; }
+__device__ __forceinline__ halfx4 as_h4(floatx4 v) { return to_h4(v); }
+
+template <int BM, int BN, int MODE, bool PRO, bool F16, bool BVEC, int EPI, bool SPLIT>
+__global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
+    constexpr int MF = mf_for<BM, BN>();
+    using MI = MfH<MF>;
+    constexpr int FM = BM / 2 / MF, FN = BN / 2 / MF;
+    if (blockIdx.y) {
+        const int64_t bz = blockIdx.y;
+        p.a += bz * p.a_bs;
+        p.b = static_cast<const char *>(p.b) + bz * p.b_bs * (F16 ? 2 : 4);
+        p.out += bz * p.c_bs;
+        if (p.res) p.res += bz * p.c_bs;
+    }
+    constexpr int A_LD = BM * KCH / 256, B_LD = BN * KCH / 256;
+    constexpr int SMEM_H = 2 * (BM + BN) * LDS_H;  // halves
+    static_assert(BM * (BN + 8) * 2 <= SMEM_H, "C tile must fit in the staging space");
+    __shared__ __align__(16) _Float16 smem[SMEM_H];
+    _Float16(*As)[BM * LDS_H] = reinterpret_cast<_Float16(*)[BM * LDS_H]>(smem);
+    _Float16(*Bs)[BN * LDS_H] = reinterpret_cast<_Float16(*)[BN * LDS_H]>(smem + 2 * BM * LDS_H);
+
+    const int tiles_m = (p.M + BM - 1) / BM;
+    const int tiles_n = (p.N + BN - 1) / BN;
+    int tm, tn;
+    {
+        constexpr int GROUP = 8;
+        const int pid = blockIdx.x;
+        const int in_group = GROUP * tiles_n;
+        const int gid = pid / in_group;
+        const int first = gid * GROUP;
+        const int gsize = min(tiles_m - first, GROUP);
+        const int r = pid - gid * in_group;
+        tm = first + r % gsize;
+        tn = r / gsize;
+    }
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int k_begin = SPLIT ? blockIdx.z * p.k_split : 0;
+    const int k_end = SPLIT ? min(p.K, k_begin + p.k_split) : p.K;
+    const int ktiles = (k_end - k_begin + BKH - 1) / BKH;
+
+    const int tid = threadIdx.x;
+    const int lrow = tid >> 4, lc = tid & 15;  // load slot: row within a 16-row pass, 4-element chunk
+
+    ConvRow crow[A_LD];
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+        if (MODE >= kConvAligned) crow[i] = conv_row(p, m0 + lrow + 16 * i);
+        else crow[i] = ConvRow{0, 0, 0, true};
+    }
+
+    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(p.a, p.a_bytes);
+    const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(p.b, p.b_bytes);
+    using BT = typename BChunk<F16, BVEC>::T;
+    floatx4 ra0[A_LD], ra1[A_LD];
+    BT rb0[B_LD], rb1[B_LD];
+    auto fetch = [&](int kt, floatx4 (&ra)[A_LD], BT (&rb)[B_LD]) {
+        const int k0 = k_begin + kt * BKH;
+        int tky = 0, tkx = 0, tci = 0;
+        if (MODE == kConvAligned) {
+            const int tap = k0 / p.ci;
+            tci = k0 - tap * p.ci;
+            tky = tap / 3;
+            tkx = tap - tky * 3;
+        }
+        const int k = k0 + lc * 4;
+#pragma unroll
+        for (int i = 0; i < A_LD; ++i)
+            ra[i] = load_a_h<MODE, PRO>(p, a_rsrc, crow[i], m0 + lrow + 16 * i, k, k_end, tky, tkx, tci, k0);
+#pragma unroll
+        for (int i = 0; i < B_LD; ++i) rb[i] = load_b_h<F16, BVEC>(p, b_rsrc, n0 + lrow + 16 * i, k, k_end);
+    };
+    auto stash = [&](int buf, const floatx4 (&ra)[A_LD], const BT (&rb)[B_LD]) {
+#pragma unroll
+        for (int i = 0; i < A_LD; ++i)
+            *reinterpret_cast<halfx4 *>(As[buf] + (lrow + 16 * i) * LDS_H + lc * 4) = to_h4(ra[i]);
+#pragma unroll
+        for (int i = 0; i < B_LD; ++i)
+            *reinterpret_cast<halfx4 *>(Bs[buf] + (lrow + 16 * i) * LDS_H + lc * 4) = as_h4(rb[i]);
+    };
+
+    typename MI::Acc acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int v = 0; v < MI::kAccRegs; ++v) acc[i][j][v] = 0.f;
+
+    // Lane l reads eight consecutive K at row l % MF, K offset 8 * (l / MF).
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int a_off = (wm * (BM / 2) + (lane % MF)) * LDS_H + (lane / MF) * 8;
+    const int b_off = (wn * (BN / 2) + (lane % MF)) * LDS_H + (lane / MF) * 8;
+    auto compute = [&](int buf) {
+        const _Float16 *as_w = As[buf] + a_off;
+        const _Float16 *bs_w = Bs[buf] + b_off;
+#pragma unroll
+        for (int kk = 0; kk < BKH; kk += MI::kKStep) {
+            halfx8 a[FM], b[FN];
+#pragma unroll
+            for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const halfx8 *>(as_w + i * MF * LDS_H + kk);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) b[j] = *reinterpret_cast<const halfx8 *>(bs_w + j * MF * LDS_H + kk);
+#pragma unroll
+            for (int i = 0; i < FM; ++i)
+#pragma unroll
+                for (int j = 0; j < FN; ++j) acc[i][j] = MI::mfma(a[i], b[j], acc[i][j]);
+        }
+    };
+
+    // The same two-register-stage / two-LDS-stage pipeline as gemm_f32_kernel.
+    fetch(0, ra0, rb0);
+    fetch(1, ra1, rb1);
+    stash(0, ra0, rb0);
+    fetch(2, ra0, rb0);
+    __syncthreads();
+    int kt = 0;
+    for (; kt + 3 < ktiles; kt += 2) {
+        compute(0);
+        stash(1, ra1, rb1);
+        fetch(kt + 3, ra1, rb1);
+        __syncthreads();
+        compute(1);
+        stash(0, ra0, rb0);
+        fetch(kt + 4, ra0, rb0);
+        __syncthreads();
+    }
+    compute(0);
+    if (kt + 1 < ktiles) {
+        stash(1, ra1, rb1);
+        __syncthreads();
+        compute(1);
+        if (kt + 2 < ktiles) {
+            stash(0, ra0, rb0);
+            __syncthreads();
+            compute(0);
+        }
+    }
+    __syncthreads();
+    write_tile<BM, BN, MF, EPI, SPLIT>(p, reinterpret_cast<float *>(smem), acc, m0, n0);
+}
+
+// Tile shape and K split of the fast kernel. Its products run at 16x the f32
+// rate, so these GEMMs are bound by operand traffic and latency: the largest
+// tiles that still give every CU work, and a K split only where even 32x32
+// tiles leave CUs idle.
+inline Plan plan_h16(int M, int N, int K, int cus, bool dense) {
+    const int ktiles = int(ceil_div(K, BKH));
+    const int64_t t128 = ceil_div(M, 128) * ceil_div(N, 128);
+    const int64_t t64 = ceil_div(M, 64) * ceil_div(N, 64);
+    const int64_t t32 = ceil_div(M, 32) * ceil_div(N, 32);
+    if (t128 >= 2 * int64_t(cus)) return Plan{128, 128, 1, K};
+    if (t64 >= int64_t(cus) || !dense) {
+        int want = 1;
+        if (t64 < int64_t(cus)) want = int(std::min<int64_t>(ceil_div(cus, t64), std::max(1, ktiles / 4)));
+        want = std::max(1, std::min(want, 8));
+        const int per = int(ceil_div(ktiles, want));
+        const int splits = int(ceil_div(ktiles, per));
+        return Plan{64, 64, splits, splits > 1 ? per * BKH : K};
+    }
+    int want = 1;
+    if (t32 < int64_t(cus)) want = int(std::min<int64_t>(ceil_div(cus, t32), std::max(1, ktiles / 4)));
+    want = std::max(1, std::min(want, 8));
+    const int per = int(ceil_div(ktiles, want));
+    const int splits = int(ceil_div(ktiles, per));
+    return Plan{32, 32, splits, splits > 1 ? per * BKH : K};
+}
+
+template <int BM, int BN, int MODE, bool PRO, bool F16, bool BVEC>
+void launch_cfg_h16(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int batch) {
+    const unsigned tiles = unsigned(ceil_div(p.M, BM) * ceil_div(p.N, BN));
+    if (pl.splits > 1) {
+        const size_t bytes = size_t(pl.splits) * p.M * p.N * sizeof(float);
+        p.partial = static_cast<float *>(ctx.ws.get(bytes, ctx.stream));
+        p.k_split = pl.k_split;
+        p.vec_out = (p.N & 3) == 0 && (reinterpret_cast<uintptr_t>(p.partial) & 15) == 0;
+        dim3 grid(tiles, 1, pl.splits);
+        gemm_h16_kernel<BM, BN, MODE, PRO, F16, BVEC, 0, true><<<grid, 256, 0, ctx.stream>>>(p);
+        MH_LAUNCH_CHECK();
+        const int64_t total = int64_t(p.M) * p.N;
+        if (reduce_vec_ok(p)) {
+            const unsigned rb = unsigned(std::min<int64_t>(ceil_div(total / 4, 256), 8192));
+            if (epi == GemmEpilogue::Silu)
+                splitk_reduce_kernel<1, true><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
+            else
+                splitk_reduce_kernel<0, true><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
+        } else {
+            const unsigned rb = unsigned(std::min<int64_t>(ceil_div(total, 256), 8192));
+            if (epi == GemmEpilogue::Silu)
+                splitk_reduce_kernel<1, false><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
+            else
+                splitk_reduce_kernel<0, false><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
+        }
+    } else {
+        p.k_split = p.K;
+        p.vec_out = out_vec_ok(p);
+        const dim3 grid(tiles, unsigned(batch));
+        if constexpr (MODE <= kDenseScalar) {
+            if (epi == GemmEpilogue::Silu) {
+                gemm_h16_kernel<BM, BN, MODE, PRO, F16, BVEC, 1, false><<<grid, 256, 0, ctx.stream>>>(p);
+                MH_LAUNCH_CHECK();
+                return;
+            }
+        } else {
+            MH_REQUIRE(epi == GemmEpilogue::None, "conv GEMM: SiLU epilogue not available");
+        }
+        gemm_h16_kernel<BM, BN, MODE, PRO, F16, BVEC, 0, false><<<grid, 256, 0, ctx.stream>>>(p);
+    }
+    MH_LAUNCH_CHECK();
+}
+
+template <int MODE, bool PRO, bool F16, bool BVEC>
+void launch_tiles_h16(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
+    Plan pl = plan_h16(p.M, p.N, p.K, int(ceil_div(ctx.cu_count, batch)), MODE <= kDenseScalar);
+    // MOEBIUS_HIP_GEMM_PLAN="bm,bn,splits" forces the tiling, as for the f32 kernel.
+    if (const char *force = std::getenv("MOEBIUS_HIP_GEMM_PLAN")) {
+        int bm = 0, bn = 0, sp = 0;
+        if (std::sscanf(force, "%d,%d,%d", &bm, &bn, &sp) == 3 && bm == bn && (bm == 32 || bm == 64 || bm == 128) &&
+            sp >= 1) {
+            const int ktiles = int(ceil_div(p.K, BKH));
+            const int per = int(ceil_div(ktiles, sp));
+            pl = Plan{bm, bn, int(ceil_div(ktiles, per)), per * BKH};
+        }
+    }
+    if (batch > 1) pl.splits = 1;
+    if (pl.splits == 1) pl.k_split = p.K;
+    if constexpr (MODE <= kDenseScalar) {
+        if (pl.bm == 32) {
+            launch_cfg_h16<32, 32, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
+            return;
+        }
+    }
+    if (pl.bm == 128)
+        launch_cfg_h16<128, 128, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
+    else
+        launch_cfg_h16<64, 64, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
+}
+
+template <int MODE, bool PRO>
+void launch_b_h16(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi, int batch = 1) {
+    const int esz = wt == kF16 ? 2 : 4;
+    const bool bvec = p.K % 4 == 0 && p.ldb % 4 == 0 && (reinterpret_cast<uintptr_t>(p.b) % (4 * esz)) == 0 &&
+                      (batch == 1 || p.b_bs % 4 == 0);
+    if constexpr (MODE == kConvAligned || MODE == kConvVec) {
+        MH_REQUIRE(bvec, "conv GEMM: weight rows must be 4-element aligned for the vector gather");
+        if (wt == kF16) launch_tiles_h16<MODE, PRO, true, true>(ctx, p, epi, batch);
+        else launch_tiles_h16<MODE, PRO, false, true>(ctx, p, epi, batch);
+    } else if constexpr (MODE == kConvScalar) {
+        if (wt == kF16) launch_tiles_h16<MODE, PRO, true, false>(ctx, p, epi, batch);
+        else launch_tiles_h16<MODE, PRO, false, false>(ctx, p, epi, batch);
+    } else {
+        if (wt == kF16) {
+            if (bvec) launch_tiles_h16<MODE, PRO, true, true>(ctx, p, epi, batch);
+            else launch_tiles_h16<MODE, PRO, true, false>(ctx, p, epi, batch);
+        } else {
+            if (bvec) launch_tiles_h16<MODE, PRO, false, true>(ctx, p, epi, batch);
+            else launch_tiles_h16<MODE, PRO, false, false>(ctx, p, epi, batch);
+        }
+    }
+}
+
+}  // namespace
+}  // namespace gemm
+}  // namespace mh

@@ -386,6 +386,63 @@ __device__ __forceinline__ floatx4 load_b(const GemmArgs &p, int n, int k) {
     return v;
 }
 
+// Epilogue through LDS, shared by the f32 and f16 kernels (smem holds at least
+// BM * (BN + 8) floats and is free): block (i, j), register v, lane l of wave
+// (wm, wn) holds row acc_row(v, l), column l % MF; the tile is written to LDS,
+// then each thread finishes four adjacent columns of a row at a time (16-byte
+// loads and stores), or one element at a time where that is not possible.
+template <int BM, int BN, int MF, int EPI, bool SPLIT, typename Acc, int FM, int FN>
+__device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const Acc (&acc)[FM][FN], int m0, int n0) {
+    using MI = Mf<MF>;
+    constexpr int CS = BN + 8;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    {
+        const int r0 = wm * (BM / 2), c0 = wn * (BN / 2) + (lane % MF);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int v = 0; v < MI::kAccRegs; ++v)
+                    smem[(r0 + i * MF + MI::acc_row(v, lane)) * CS + c0 + j * MF] = acc[i][j][v];
+    }
+    __syncthreads();
+    if (p.vec_out) {
+        constexpr int C4 = BN / 4, RPP = 256 / C4;  // float4 per tile row, rows per pass
+        const int cc = (tid % C4) * 4, col = n0 + cc;
+        if (col < p.N) {  // N % 4 == 0: the whole float4 is inside
+#pragma unroll
+            for (int it = 0; it < BM / RPP; ++it) {
+                const int rr = tid / C4 + it * RPP, row = m0 + rr;
+                if (row >= p.M) break;
+                const float4 v = *reinterpret_cast<const float4 *>(smem + rr * CS + cc);
+                if (SPLIT)
+                    *reinterpret_cast<float4 *>(p.partial + (int64_t(blockIdx.z) * p.M + row) * p.N + col) = v;
+                else
+                    store4<EPI>(p, row, col, v);
+            }
+        }
+    } else {
+        // One element per thread and pass; consecutive threads take consecutive
+        // rows when rows are grouped (their outputs are adjacent), else columns.
+        const bool by_row = p.rg > 1;
+        for (int e = tid; e < BM * BN; e += 256) {
+            const int rr = by_row ? e % BM : e / BN, cc = by_row ? e / BM : e % BN;
+            const int row = m0 + rr, col = n0 + cc;
+            if (row >= p.M || col >= p.N) continue;
+            const float r = smem[rr * CS + cc];
+            if (SPLIT) {
+                p.partial[(int64_t(blockIdx.z) * p.M + row) * p.N + col] = r;
+            } else {
+                int64_t o;
+                float *dst = out_ptr(p, row, col, o);
+                dst[o] = epilogue_value<EPI>(p, row, col, o, r, p.bias ? p.bias[col] : 0.f);
+            }
+        }
+    }
+}
+
 template <int BM, int BN, int MODE, bool PRO, bool F16, bool BVEC, int EPI, bool SPLIT>
 __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
     constexpr int MF = mf_for<BM, BN>();
@@ -545,54 +602,8 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
         }
     }
 
-    // Epilogue through LDS: block (i, j), register v, lane l holds row
-    // acc_row(v, l), column l % MF; the tile is written to LDS, then each thread
-    // finishes four adjacent columns of a row at a time (16-byte loads and stores).
     __syncthreads();
-    {
-        const int r0 = wm * (BM / 2), c0 = wn * (BN / 2) + (lane % MF);
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j)
-#pragma unroll
-                for (int v = 0; v < MI::kAccRegs; ++v)
-                    smem[(r0 + i * MF + MI::acc_row(v, lane)) * CS + c0 + j * MF] = acc[i][j][v];
-    }
-    __syncthreads();
-    if (p.vec_out) {
-        constexpr int C4 = BN / 4, RPP = 256 / C4;  // float4 per tile row, rows per pass
-        const int cc = (tid % C4) * 4, col = n0 + cc;
-        if (col < p.N) {  // N % 4 == 0: the whole float4 is inside
-#pragma unroll
-            for (int it = 0; it < BM / RPP; ++it) {
-                const int rr = tid / C4 + it * RPP, row = m0 + rr;
-                if (row >= p.M) break;
-                const float4 v = *reinterpret_cast<const float4 *>(smem + rr * CS + cc);
-                if (SPLIT)
-                    *reinterpret_cast<float4 *>(p.partial + (int64_t(blockIdx.z) * p.M + row) * p.N + col) = v;
-                else
-                    store4<EPI>(p, row, col, v);
-            }
-        }
-    } else {
-        // One element per thread and pass; consecutive threads take consecutive
-        // rows when rows are grouped (their outputs are adjacent), else columns.
-        const bool by_row = p.rg > 1;
-        for (int e = tid; e < BM * BN; e += 256) {
-            const int rr = by_row ? e % BM : e / BN, cc = by_row ? e / BM : e % BN;
-            const int row = m0 + rr, col = n0 + cc;
-            if (row >= p.M || col >= p.N) continue;
-            const float r = smem[rr * CS + cc];
-            if (SPLIT) {
-                p.partial[(int64_t(blockIdx.z) * p.M + row) * p.N + col] = r;
-            } else {
-                int64_t o;
-                float *dst = out_ptr(p, row, col, o);
-                dst[o] = epilogue_value<EPI>(p, row, col, o, r, p.bias ? p.bias[col] : 0.f);
-            }
-        }
-    }
+    write_tile<BM, BN, MF, EPI, SPLIT>(p, smem, acc, m0, n0);
 }
 
 // Sums split-K partials in split order, then (residual + bias) + sum [SiLU].

@@ -274,6 +274,9 @@ class VaeDevice {
 
     // src/vae/encoder.rs:77-118
     void encode(const float *images, int nb, int h, int w, const float *noise, float *z, TraceFn trace, void *user) {
+        // f32 arithmetic whatever the context's precision: the SDXL VAE's
+        // activations overflow f16 (src/vae/mod.rs:2-3).
+        PrecisionScope exact(ctx_, Precision::Exact);
         if (nb <= 0 || h <= 0 || w <= 0 || h % 8 || w % 8) fail(kInvalidArgument, "image size must be a multiple of 8");
         Env e{ctx_, pool_};
         auto tr = [&](const std::string &name, const DT &t) {
@@ -313,6 +316,9 @@ class VaeDevice {
 
     // src/vae/decoder.rs:74-99
     void decode(const float *latents, int h, int w, float *out, TraceFn trace, void *user) {
+        // f32 arithmetic whatever the context's precision: the SDXL VAE's
+        // activations overflow f16 (src/vae/mod.rs:2-3).
+        PrecisionScope exact(ctx_, Precision::Exact);
         if (h <= 0 || w <= 0) fail(kInvalidArgument, "empty latent");
         Env e{ctx_, pool_};
         auto tr = [&](const char *name, const DT &t) {

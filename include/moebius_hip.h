@@ -154,6 +154,44 @@ int32_t mh_conv3x3_forward(MhContext *ctx, const float *x, uint32_t n, uint32_t 
                            uint32_t stride, const uint32_t pad[4], uint32_t upsample2x, const float *prologue_scale,
                            const float *prologue_shift, uint32_t prologue_silu, float *out);
 
+/* src/engine/winograd.rs:254-297 `transform_kernel` / `kernel_transform`:
+ * U = G g G^T for every (output, input) channel pair, G = [[1,0,0],
+ * [1/2,1/2,1/2],[1/2,-1/2,1/2],[0,0,1]], in the reference's operation order;
+ * f16 weights are widened (exactly) first, as winograd.rs:260-263 does.
+ * weight [c_out, 3, 3, c_in]; u [16, c_out, c_in] f32. */
+int32_t mh_winograd_weight_transform(MhContext *ctx, const void *weight, uint32_t weight_dtype, uint32_t c_out,
+                                     uint32_t c_in, float *u);
+
+/* src/engine/winograd.rs:144-160, 210-251, 299-327 (`Geo::input_tile`,
+ * `fill_strip`, `input_transform`): V = B^T d B for every 2x2 output tile
+ * (tiles = n * ceil(H/2) * ceil(W/2), H x W the output = the (upsampled)
+ * input size, ordered item, tile row, tile column), d the tile's 4x4 input
+ * patch: zero outside the image, nearest-2x upsample when upsample2x, the
+ * GroupNorm affine (+SiLU) prologue on in-image values when prologue_scale /
+ * prologue_shift ([n * c] each) are given. x [n, h, w, c]; v [16, tiles, c];
+ * c a multiple of 4. */
+int32_t mh_winograd_input_transform(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
+                                    uint32_t upsample2x, const float *prologue_scale, const float *prologue_shift,
+                                    uint32_t prologue_silu, float *v);
+
+/* src/engine/winograd.rs:164-202, 329-352 (`Geo::output_band`,
+ * `output_transform`): out = A^T m A + bias per tile, A^T = [[1,1,1,0],
+ * [0,1,-1,-1]]; the pixels of partial tiles (odd H or W) are not written.
+ * m [16, tiles, c_out]; bias [c_out] or NULL; out [n, H, W, c_out]. */
+int32_t mh_winograd_output_transform(MhContext *ctx, const float *m, uint32_t n, uint32_t h, uint32_t w,
+                                     uint32_t c_out, uint32_t upsample2x, const float *bias, float *out);
+
+/* src/engine/winograd.rs:48-120 `conv3x3_same` (the stride-1 / pad-1 path of
+ * `Conv3x3::forward` / `forward_prologue`, src/engine/conv.rs:92-102):
+ * the input transform, 16 matrix-core GEMMs [tiles x c_in] . [c_in x c_out]
+ * in one batched launch, and the output transform. u from
+ * mh_winograd_weight_transform (the transformed kernel, built once per
+ * weight as the reference does per call); c_in, c_out multiples of 4. */
+int32_t mh_conv3x3_winograd(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c_in,
+                            const float *u, uint32_t c_out, const float *bias, uint32_t upsample2x,
+                            const float *prologue_scale, const float *prologue_shift, uint32_t prologue_silu,
+                            float *out);
+
 /* src/engine/conv.rs:145-165 `Geometry::gather`: patch rows [3,3,c] of output
  * pixels first..first+count (the implicit-GEMM conv's A operand, materialised
  * for a bit-exact check). rows [count, 9*c]. */

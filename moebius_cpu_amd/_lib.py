@@ -69,6 +69,10 @@ SIGNATURES = {
     "mh_conv3x3_output_hw": (_i32, [_u32, _u32, _u32, _u32p, _u32, _u32p, _u32p]),
     "mh_conv3x3_forward": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _u32, _u32, _vp, _u32, _u32p, _u32,
                                   _vp, _vp, _u32, _vp]),
+    "mh_winograd_weight_transform": (_i32, [_vp, _vp, _u32, _u32, _u32, _vp]),
+    "mh_winograd_input_transform": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _vp]),
+    "mh_winograd_output_transform": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp, _vp]),
+    "mh_conv3x3_winograd": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _u32, _vp, _u32, _vp, _vp, _u32, _vp]),
     "mh_im2col_gather": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32p, _u32, _u64, _u64, _vp]),
     "mh_depthwise3x3": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _vp]),
     "mh_depthwise3x3_fused": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _vp, _vp, _u32, _vp]),

@@ -312,6 +312,65 @@ int32_t mh_conv3x3_forward(MhContext *ctx, const float *x, uint32_t n, uint32_t 
     });
 }
 
+int32_t mh_winograd_weight_transform(MhContext *ctx, const void *weight, uint32_t weight_dtype, uint32_t c_out,
+                                     uint32_t c_in, float *u) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(weight, "weight");
+        need(u, "u");
+        mh::winograd_weight_transform(c, weight, wtype(weight_dtype), dim(c_out, "c_out"), dim(c_in, "c_in"), u);
+    });
+}
+
+int32_t mh_winograd_input_transform(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
+                                    uint32_t upsample2x, const float *prologue_scale, const float *prologue_shift,
+                                    uint32_t prologue_silu, float *v) {
+    return guard([&] {
+        mh::Context &cc = C(ctx);
+        need(x, "x");
+        need(v, "v");
+        if ((prologue_scale == nullptr) != (prologue_shift == nullptr))
+            mh::fail(mh::kInvalidArgument, "prologue needs both scale and shift");
+        mh::Affine aff;
+        aff.scale = prologue_scale;
+        aff.shift = prologue_shift;
+        aff.silu = prologue_silu != 0;
+        mh::winograd_input_transform(cc, x, dim(n, "n"), dim(h, "h"), dim(w, "w"), dim(c, "c"), upsample2x != 0,
+                                     prologue_scale ? &aff : nullptr, v);
+    });
+}
+
+int32_t mh_winograd_output_transform(MhContext *ctx, const float *m, uint32_t n, uint32_t h, uint32_t w,
+                                     uint32_t c_out, uint32_t upsample2x, const float *bias, float *out) {
+    return guard([&] {
+        mh::Context &cc = C(ctx);
+        need(m, "m");
+        need(out, "out");
+        mh::winograd_output_transform(cc, m, dim(n, "n"), dim(h, "h"), dim(w, "w"), dim(c_out, "c_out"),
+                                      upsample2x != 0, bias, nullptr, out);
+    });
+}
+
+int32_t mh_conv3x3_winograd(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c_in,
+                            const float *u, uint32_t c_out, const float *bias, uint32_t upsample2x,
+                            const float *prologue_scale, const float *prologue_shift, uint32_t prologue_silu,
+                            float *out) {
+    return guard([&] {
+        mh::Context &cc = C(ctx);
+        need(x, "x");
+        need(u, "u");
+        need(out, "out");
+        if ((prologue_scale == nullptr) != (prologue_shift == nullptr))
+            mh::fail(mh::kInvalidArgument, "prologue needs both scale and shift");
+        mh::Affine aff;
+        aff.scale = prologue_scale;
+        aff.shift = prologue_shift;
+        aff.silu = prologue_silu != 0;
+        mh::conv3x3_winograd(cc, x, dim(n, "n"), dim(h, "h"), dim(w, "w"), dim(c_in, "c_in"), u, mh::kF32,
+                             dim(c_out, "c_out"), bias, upsample2x != 0, prologue_scale ? &aff : nullptr, out);
+    });
+}
+
 int32_t mh_im2col_gather(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
                          uint32_t stride, const uint32_t pad[4], uint32_t upsample2x, uint64_t first, uint64_t count,
                          float *rows) {

@@ -252,30 +252,34 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
     write_tile<BM, BN, MF, EPI, SPLIT>(p, reinterpret_cast<float *>(smem), acc, m0, n0);
 }
 
-// Tile shape and K split of the fast kernel. Its products run at 16x the f32
-// rate, so these GEMMs are bound by operand traffic and latency: the largest
-// tiles that still give every CU work, and a K split only where even 32x32
-// tiles leave CUs idle.
+// Tile shape and K split of the fast kernel, from sweeps of every (tile,
+// split) on MI355X over the UNet's GEMM shapes. Its products run at 16x the
+// f32 rate, so these GEMMs are bound by operand traffic and per-workgroup
+// latency:
+//  - implicit-GEMM convs: 64x64 tiles, K split up to 4 ways while each split
+//    keeps 10 or more K tiles (every UNet 3x3 conv: 15-30% faster than unsplit);
+//  - a few rows (the time-embedding linears): 32x32;
+//  - wide outputs (N >= 2048) with 10+ K tiles: 128x128, split in 2 when the
+//    grid is under one tile per CU (the MixFFN inverted 1x1 at 32^2 and 16^2);
+//  - long K (25+ tiles) on small grids: 64x64 with K split up to 4 ways;
+//  - otherwise 64x64, or 32x32 when 64x64 leaves a quarter of the CUs idle.
 inline Plan plan_h16(int M, int N, int K, int cus, bool dense) {
     const int ktiles = int(ceil_div(K, BKH));
     const int64_t t128 = ceil_div(M, 128) * ceil_div(N, 128);
     const int64_t t64 = ceil_div(M, 64) * ceil_div(N, 64);
-    const int64_t t32 = ceil_div(M, 32) * ceil_div(N, 32);
-    if (t128 >= 2 * int64_t(cus)) return Plan{128, 128, 1, K};
-    if (t64 >= int64_t(cus) || !dense) {
-        int want = 1;
-        if (t64 < int64_t(cus)) want = int(std::min<int64_t>(ceil_div(cus, t64), std::max(1, ktiles / 4)));
-        want = std::max(1, std::min(want, 8));
+    auto plan = [&](int bm, int want) {
+        want = std::max(1, std::min(want, ktiles));
         const int per = int(ceil_div(ktiles, want));
         const int splits = int(ceil_div(ktiles, per));
-        return Plan{64, 64, splits, splits > 1 ? per * BKH : K};
-    }
-    int want = 1;
-    if (t32 < int64_t(cus)) want = int(std::min<int64_t>(ceil_div(cus, t32), std::max(1, ktiles / 4)));
-    want = std::max(1, std::min(want, 8));
-    const int per = int(ceil_div(ktiles, want));
-    const int splits = int(ceil_div(ktiles, per));
-    return Plan{32, 32, splits, splits > 1 ? per * BKH : K};
+        return Plan{bm, bm, splits, splits > 1 ? per * BKH : K};
+    };
+    if (!dense) return plan(64, t64 >= 2 * int64_t(cus) ? 1 : std::min(4, ktiles / 10));
+    if (M <= 32) return plan(32, 1);
+    if (ktiles >= 10 && N >= 2048 && 2 * t128 >= int64_t(cus))
+        return plan(128, t128 >= int64_t(cus) || ktiles < 20 ? 1 : 2);
+    if (ktiles >= 25 && t64 < 2 * int64_t(cus)) return plan(64, int(std::min<int64_t>(4, ceil_div(2 * cus, t64))));
+    if (4 * t64 < 3 * int64_t(cus)) return plan(32, 1);
+    return plan(64, 1);
 }
 
 template <int BM, int BN, int MODE, bool PRO, bool F16, bool BVEC>

@@ -394,7 +394,10 @@ __device__ __forceinline__ floatx4 load_b(const GemmArgs &p, int n, int k) {
 template <int BM, int BN, int MF, int EPI, bool SPLIT, typename Acc, int FM, int FN>
 __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const Acc (&acc)[FM][FN], int m0, int n0) {
     using MI = Mf<MF>;
-    constexpr int CS = BN + 8;
+    // C tile row stride: the lane groups of one register's store sit 4 rows
+    // apart (16x16 blocks: 16 columns per group) or 4 rows apart in two halves
+    // (32x32: 32 columns); BN + 4 (resp. + 8) puts those groups on disjoint banks.
+    constexpr int CS = BN + (MF == 16 ? 4 : 8);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     {

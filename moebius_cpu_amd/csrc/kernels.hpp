@@ -82,6 +82,22 @@ void gemm_nt(Context &ctx, const float *a, int64_t lda, int64_t a_bs, const void
              int64_t ldc, int64_t c_bs, GemmEpilogue epi = GemmEpilogue::None, int row_group = 0);
 void im2col_gather(Context &ctx, const float *x, int n, int h, int w, int c, int stride, const int pad[4],
                    bool upsample2x, int64_t first, int64_t count, float *rows);
+
+// ---- Winograd F(2x2,3x3) stride-1 / pad-1 conv (winograd.hip), src/engine/winograd.rs
+// Tiles of a (upsampled) n x h x w map: n * ceil(H/2) * ceil(W/2), ordered (item, row, column).
+int64_t winograd_tiles(int n, int h, int w, bool upsample2x);
+// weight [c_out][3][3][c_in] (f32 or f16) -> u [16][c_out][c_in] f32 (G g G^T).
+void winograd_weight_transform(Context &ctx, const void *weight, WeightType wt, int c_out, int c_in, float *u);
+// x [n,h,w,c] -> v [16][tiles][c] (B^T d B), prologue applied to in-image values.
+void winograd_input_transform(Context &ctx, const float *x, int n, int h, int w, int c, bool upsample2x,
+                              const Affine *prologue, float *v);
+// m [16][tiles][c_out] -> out [n, H, W, c_out] = A^T m A + bias (+ residual2).
+void winograd_output_transform(Context &ctx, const float *m, int n, int h, int w, int c_out, bool upsample2x,
+                               const float *bias, const float *residual2, float *out);
+// The whole conv: u from winograd_weight_transform (ut kF32) or an f16 copy of it.
+void conv3x3_winograd(Context &ctx, const float *x, int n, int h, int w, int c_in, const void *u, WeightType ut,
+                      int c_out, const float *bias, bool upsample2x, const Affine *prologue, float *out,
+                      const float *residual2 = nullptr);
 void selftest_mfma_f32(Context &ctx, const float *a_host, const float *b_host, float *d_host);
 
 // ---- lambda layers (lambda.hip), src/unet/lambda.rs

@@ -41,7 +41,10 @@ class WeightStore {
     // Shape-checked lookup (by element count); gemm: may be f16.
     DParam get(const std::string &name, int64_t numel, bool gemm) const;
     const float *host_f32(const std::string &name, int64_t numel, std::vector<float> &scratch) const;
-    size_t bytes() const { return bytes_; }
+    // Winograd kernel U = G g G^T [16][co][ci] (f32) of a 3x3 conv weight
+    // [co][3][3][ci], built on the device once and owned by the store.
+    const float *winograd_kernel(const DParam &w, int co, int ci) const;
+    size_t bytes() const { return bytes_ + derived_bytes_; }
 
   private:
     struct Entry {
@@ -49,9 +52,12 @@ class WeightStore {
         const void *host;
         uint32_t host_dtype;
     };
+    Context &ctx_;
     std::map<std::string, Entry> m_;
     void *block_ = nullptr;
     size_t bytes_ = 0;
+    mutable std::vector<void *> derived_;
+    mutable size_t derived_bytes_ = 0;
 };
 
 using TraceFn = void (*)(void *user, const char *name, const float *dev, int n, int h, int w, int c);

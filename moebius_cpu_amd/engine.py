@@ -238,14 +238,26 @@ class Affine:
 class Conv3x3:
     """src/engine/conv.rs:58-131"""
 
-    def __init__(self, ctx, c_in, c_out, weight: Param, bias=None, stride=1, pad=(1, 1, 1, 1), upsample2x=False):
+    def __init__(self, ctx, c_in, c_out, weight: Param, bias=None, stride=1, pad=(1, 1, 1, 1), upsample2x=False,
+                 winograd=False):
+        """winograd: run the stride-1 / pad-1 conv as Winograd F(2x2,3x3)
+        (src/engine/winograd.rs:48-120), with the kernel transformed once here;
+        otherwise as an implicit GEMM."""
         self.ctx, self.c_in, self.c_out, self.weight = ctx, c_in, c_out, weight
         self.bias = _vec(ctx, bias)
         self.stride, self.pad, self.upsample2x = stride, tuple(pad), upsample2x
+        self.u = None
+        if winograd:
+            if stride != 1 or tuple(pad) != (1, 1, 1, 1):
+                raise MoebiusError(1, "Winograd needs stride 1 and pad [1,1,1,1]")
+            if len(weight) != 9 * c_in * c_out:
+                raise MoebiusError(1, "Conv3x3 weight size")
+            self.u = DeviceArray(ctx, (16, c_out, c_in))
+            check(lib().mh_winograd_weight_transform(ctx.h, weight.ptr, weight.dtype, c_out, c_in, self.u.ptr))
 
     @classmethod
-    def same(cls, ctx, c_in, c_out, weight, bias=None):
-        return cls(ctx, c_in, c_out, weight, bias)
+    def same(cls, ctx, c_in, c_out, weight, bias=None, winograd=False):
+        return cls(ctx, c_in, c_out, weight, bias, winograd=winograd)
 
     def output_hw(self, h, w):
         ho, wo = ctypes.c_uint32(), ctypes.c_uint32()
@@ -267,6 +279,10 @@ class Conv3x3:
         silu = 0
         if prologue is not None:
             sc, sh, silu = prologue.scale.ptr, prologue.shift.ptr, int(prologue.silu)
+        if self.u is not None:
+            check(lib().mh_conv3x3_winograd(self.ctx.h, x.ptr, x.n, x.h, x.w, x.c, self.u.ptr, self.c_out,
+                                            _ptr(self.bias), int(self.upsample2x), sc, sh, silu, out.ptr))
+            return
         check(lib().mh_conv3x3_forward(self.ctx.h, x.ptr, x.n, x.h, x.w, x.c, self.weight.ptr, self.weight.dtype,
                                        self.c_out, _ptr(self.bias), self.stride, u32x4(self.pad),
                                        int(self.upsample2x), sc, sh, silu, out.ptr))

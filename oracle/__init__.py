@@ -47,6 +47,9 @@ def _declare(L):
     L.orc_conv3x3_forward.argtypes = [vp, _i64, _i64, _i64, _i64, vp, _i64, vp, ctypes.c_int, vp, ctypes.c_int,
                                       vp, vp, ctypes.c_int, vp]
     L.orc_conv3x3_im2col.argtypes = [vp, _i64, _i64, _i64, _i64, vp, _i64, vp, ctypes.c_int, vp, ctypes.c_int, vp]
+    L.orc_wino_kernel_transform_all.argtypes = [vp, _i64, _i64, vp]
+    L.orc_wino_input_transform_all.argtypes = [vp, _i64, _i64, _i64, _i64, ctypes.c_int, vp, vp, ctypes.c_int, vp]
+    L.orc_wino_output_transform_all.argtypes = [vp, _i64, _i64, _i64, _i64, ctypes.c_int, vp, vp]
     L.orc_im2col_gather_row.argtypes = [vp, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_int, ctypes.c_int,
                                         ctypes.c_int, ctypes.c_int, _i64, vp]
     L.orc_depthwise3x3.argtypes = [vp, _i64, _i64, _i64, _i64, vp, vp, ctypes.c_int, vp]
@@ -152,6 +155,44 @@ def conv3x3(x, weight, bias=None, stride=1, pad=(1, 1, 1, 1), upsample2x=False, 
             sc, sh, silu = _f32(prologue[0]), _f32(prologue[1]), int(prologue[2])
         lib().orc_conv3x3_forward(_p(x), n, h, w, ci, _p(weight), co, _p(bias), stride, padv, int(upsample2x),
                                   _p(sc), _p(sh), silu, _p(out))
+    return out
+
+
+def wino_tiles(n, h, w, upsample2x=False):
+    """Tiles of the Winograd F(2x2,3x3) conv (src/engine/winograd.rs:64-69)."""
+    up = 2 if upsample2x else 1
+    return n * ((h * up + 1) // 2) * ((w * up + 1) // 2)
+
+
+def wino_kernel_transform(weight):
+    """src/engine/winograd.rs:254-297: U = G g G^T; weight [co,3,3,ci] -> u [16,co,ci]."""
+    weight = _f32(weight)
+    co, ci = weight.shape[0], weight.shape[3]
+    u = np.empty((16, co, ci), np.float32)
+    lib().orc_wino_kernel_transform_all(_p(weight), co, ci, _p(u))
+    return u
+
+
+def wino_input_transform(x, upsample2x=False, prologue=None):
+    """src/engine/winograd.rs:144-160, 210-251, 299-327: V = B^T d B per tile -> v [16, tiles, ci]."""
+    x = _f32(x)
+    n, h, w, ci = x.shape
+    v = np.empty((16, wino_tiles(n, h, w, upsample2x), ci), np.float32)
+    sc = sh = None
+    silu = 0
+    if prologue is not None:
+        sc, sh, silu = _f32(prologue[0]), _f32(prologue[1]), int(prologue[2])
+    lib().orc_wino_input_transform_all(_p(x), n, h, w, ci, int(upsample2x), _p(sc), _p(sh), silu, _p(v))
+    return v
+
+
+def wino_output_transform(m, n, h, w, upsample2x=False, bias=None):
+    """src/engine/winograd.rs:164-202, 329-352: out = A^T m A + bias; m [16, tiles, co]."""
+    m, bias = _f32(m), _f32(bias)
+    co = m.shape[2]
+    up = 2 if upsample2x else 1
+    out = np.zeros((n, h * up, w * up, co), np.float32)
+    lib().orc_wino_output_transform_all(_p(m), n, h, w, co, int(upsample2x), _p(bias), _p(out))
     return out
 
 

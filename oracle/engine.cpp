@@ -303,6 +303,79 @@ extern "C" void orc_winograd_conv3x3_same(const float *x, int64_t n, int64_t h, 
     }
 }
 
+// Whole-map forms of the Winograd transforms above, in the device library's
+// plane-major layout (test infrastructure: they pin mh_winograd_*_transform bit
+// for bit). Tiles and their 4x4 patches follow orc_winograd_conv3x3_same.
+// u [16][c_out][ci] from weight [c_out][3][3][ci].
+extern "C" void orc_wino_kernel_transform_all(const float *weight, int64_t c_out, int64_t ci, float *u) {
+    std::vector<float> one(size_t(16 * ci));
+    for (int64_t o = 0; o < c_out; ++o) {
+        orc_wino_kernel_transform(weight + o * 9 * ci, ci, one.data());
+        for (int xi = 0; xi < 16; ++xi)
+            std::memcpy(u + (xi * c_out + o) * ci, one.data() + xi * ci, size_t(ci) * sizeof(float));
+    }
+}
+
+// v [16][tiles][ci] from x [n][h][w][ci] (GroupNorm prologue on in-image values).
+extern "C" void orc_wino_input_transform_all(const float *x, int64_t n, int64_t h, int64_t w, int64_t ci,
+                                             int upsample2x, const float *psc, const float *psh, int psilu,
+                                             float *v) {
+    const int shift = upsample2x ? 1 : 0;
+    const int64_t hi = h << shift, wi = w << shift;
+    const int64_t th = (hi + 1) / 2, tw = (wi + 1) / 2;
+    const int64_t tiles = n * th * tw;
+    std::vector<float> zeros(size_t(ci), 0.0f), norm(size_t(16 * ci)), one(size_t(16 * ci));
+    for (int64_t t = 0; t < tiles; ++t) {
+        const int64_t b = t / (th * tw), rem = t % (th * tw);
+        const int64_t ty = rem / tw, tx = rem % tw;
+        const float *rows[16];
+        for (int kk = 0; kk < 16; ++kk) {
+            const int64_t iy = 2 * ty + kk / 4 - 1, ix = 2 * tx + kk % 4 - 1;
+            if (iy >= 0 && iy < hi && ix >= 0 && ix < wi) {
+                const float *src = x + ((b * h + (iy >> shift)) * w + (ix >> shift)) * ci;
+                if (psc) {
+                    float *dst = norm.data() + kk * ci;
+                    for (int64_t j = 0; j < ci; ++j) {
+                        const float y = std::fma(src[j], psc[b * ci + j], psh[b * ci + j]);
+                        dst[j] = psilu ? orc_silu(y) : y;
+                    }
+                    rows[kk] = dst;
+                } else {
+                    rows[kk] = src;
+                }
+            } else {
+                rows[kk] = zeros.data();
+            }
+        }
+        orc_wino_input_transform(rows, ci, one.data());
+        for (int xi = 0; xi < 16; ++xi)
+            std::memcpy(v + (xi * tiles + t) * ci, one.data() + xi * ci, size_t(ci) * sizeof(float));
+    }
+}
+
+// out [n][H][W][c_out] from m [16][tiles][c_out]; partial-tile pixels skipped.
+extern "C" void orc_wino_output_transform_all(const float *m, int64_t n, int64_t h, int64_t w, int64_t c_out,
+                                              int upsample2x, const float *bias, float *out) {
+    const int shift = upsample2x ? 1 : 0;
+    const int64_t hi = h << shift, wi = w << shift;
+    const int64_t th = (hi + 1) / 2, tw = (wi + 1) / 2;
+    const int64_t tiles = n * th * tw;
+    std::vector<float> y(size_t(4 * c_out)), zero(size_t(c_out), 0.0f);
+    if (!bias) bias = zero.data();
+    for (int64_t t = 0; t < tiles; ++t) {
+        const int64_t b = t / (th * tw), rem = t % (th * tw);
+        const int64_t ty = rem / tw, tx = rem % tw;
+        const float *planes[16];
+        for (int xi = 0; xi < 16; ++xi) planes[xi] = m + (xi * tiles + t) * c_out;
+        orc_wino_output_transform(planes, bias, c_out, y.data());
+        for (int kk = 0; kk < 4; ++kk) {
+            const int64_t oy = 2 * ty + kk / 2, ox = 2 * tx + kk % 2;
+            if (oy >= hi || ox >= wi) continue;
+            std::memcpy(out + ((b * hi + oy) * wi + ox) * c_out, y.data() + kk * c_out, c_out * sizeof(float));
+        }
+    }
+}
+
 // src/engine/conv.rs:92-102
 extern "C" void orc_conv3x3_forward(const float *x, int64_t n, int64_t h, int64_t w, int64_t c_in,
                                     const float *weight, int64_t c_out, const float *bias, int stride,

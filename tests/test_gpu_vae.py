@@ -132,9 +132,13 @@ def test_vae_f16_stored_weights(ctx, params):
     got = v16.decode_host(lat)
     want = oracle.Vae(rounded).decode(lat)
     assert max_abs_rel(got, want) <= TOL
+    # The GEMM weights really are stored at half width: f16 storage saves 2 bytes
+    # per GEMM weight value (the Winograd kernels built at load from the widened
+    # weights are f32 in both stores, as the reference transforms in f32).
     w, _ = v16.memory()
     w32, _ = Vae(ctx, params).memory()
-    assert w < 0.6 * w32
+    half = 2 * sum(params[k].size for k in gemm)
+    assert 0.98 * half <= w32 - w <= 1.02 * half + 256 * len(gemm)
 
 
 def test_bad_image_size_is_an_argument_error(gvae):

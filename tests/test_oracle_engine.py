@@ -298,3 +298,32 @@ def test_torch_fp32_cross_check():
     assert_close(oracle.group_norm(x, 32, 1e-5, gm, be, silu=True), nhwc(F.silu(gn)), 1e-5)
     ln = F.layer_norm(torch.from_numpy(x), (64,), torch.from_numpy(gm), torch.from_numpy(be), eps=1e-5)
     assert_close(oracle.layer_norm(x, gm, be, 1e-5), ln.numpy(), 1e-5)
+
+
+@pytest.mark.parametrize("n,h,w,ci,co,up", [(2, 5, 7, 8, 12, False), (1, 4, 3, 6, 5, True), (1, 1, 1, 4, 3, False)])
+def test_winograd_transforms_compose_to_the_direct_conv(n, h, w, ci, co, up):
+    """The whole-map kernel, input and output transforms (src/engine/winograd.rs:
+    254-352) composed through an f64 product equal the f64 direct conv, odd
+    sizes (partial tiles) and the nearest-2x upsample included; and they are the
+    same values the oracle's own Winograd conv uses."""
+    from tests import ref_f64 as R
+
+    rng = np.random.default_rng(n * 100 + h * 10 + w)
+    x = rng.standard_normal((n, h, w, ci)).astype(np.float32)
+    wt = rng.standard_normal((co, 3, 3, ci)).astype(np.float32)
+    b = rng.standard_normal(co).astype(np.float32)
+    u = oracle.wino_kernel_transform(wt)
+    v = oracle.wino_input_transform(x, up)
+    assert u.shape == (16, co, ci) and v.shape == (16, oracle.wino_tiles(n, h, w, up), ci)
+    m = np.einsum("xtc,xoc->xto", v.astype(np.float64), u.astype(np.float64)).astype(np.float32)
+    y = oracle.wino_output_transform(m, n, h, w, up, b)
+    direct = R.conv3x3(x.astype(np.float64), wt.astype(np.float64), b.astype(np.float64), up=up)
+    assert np.max(np.abs(y - direct)) <= 1e-5 * max(1.0, np.max(np.abs(direct)))
+    assert np.max(np.abs(y - oracle.conv3x3(x, wt, b, upsample2x=up))) <= 1e-5 * max(1.0, np.max(np.abs(direct)))
+    # integer inputs with even-integer weights: every transform and sum is exact
+    xi = rng.integers(-4, 5, x.shape).astype(np.float32)
+    wi = (2 * rng.integers(-3, 4, wt.shape)).astype(np.float32)
+    mi = np.einsum("xtc,xoc->xto", oracle.wino_input_transform(xi, up).astype(np.float64),
+                   oracle.wino_kernel_transform(wi).astype(np.float64)).astype(np.float32)
+    yi = oracle.wino_output_transform(mi, n, h, w, up, None)
+    assert np.array_equal(yi, R.conv3x3(xi.astype(np.float64), wi.astype(np.float64), 0.0, up=up).astype(np.float32))

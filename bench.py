@@ -71,14 +71,17 @@ def cpu_baseline(workload, extra=(), note=""):
 
 
 def bench_conv_gn(args):
-    """conv3x3 64x64x320 -> 320 + GroupNorm(32, eps 1e-5) + SiLU, f32."""
+    """conv3x3 64x64x320 -> 320 + GroupNorm(32, eps 1e-5) + SiLU, f32. The conv
+    runs as Winograd F(2x2,3x3) (the CPU engine's algorithm for stride-1 convs);
+    the implicit-GEMM conv is timed beside it."""
     from moebius_cpu_amd import engine as E
     from moebius_cpu_amd import workloads as W
 
     ctx = E.Context(0)
     wl = W.conv3x3_gn_silu()
     x = E.Tensor.from_numpy(ctx, wl.x)
-    conv = E.Conv3x3.same(ctx, 320, 320, E.Param(ctx, wl.w), wl.b)
+    conv = E.Conv3x3.same(ctx, 320, 320, E.Param(ctx, wl.w), wl.b, winograd=True)
+    conv_g = E.Conv3x3.same(ctx, 320, 320, E.Param(ctx, wl.w), wl.b)
     gn = E.GroupNorm(ctx, wl.groups, wl.eps, wl.gamma, wl.beta)
     y, z = E.Tensor(ctx, *wl.x.shape[:3], 320), E.Tensor(ctx, *wl.x.shape[:3], 320)
 
@@ -90,21 +93,29 @@ def bench_conv_gn(args):
         step()
     ms = time_region(ctx, step, args.steps)
     conv_ms = time_region(ctx, lambda: conv.forward(x, y), args.steps)
+    conv_g.forward(x, y)
+    gemm_ms = time_region(ctx, lambda: conv_g.forward(x, y), args.steps)
     gn_ms = time_region(ctx, lambda: gn.forward(y, None, True, z), args.steps)
     elems = y.pixels() * 320
-    conv_tflops = wl.flops / (conv_ms * 1e-3) / 1e12
+    wino_flops = 16 * 2.0 * (64 // 2) * (64 // 2) * 320 * 320  # 16 plane GEMMs over 32x32 tiles
+    conv_tflops = wino_flops / (conv_ms * 1e-3) / 1e12
+    gemm_tflops = wl.flops / (gemm_ms * 1e-3) / 1e12
     gn_gbps = 8.0 * elems / (gn_ms * 1e-3) / 1e9
 
     out = {
         "metric": METRIC, "value": round(ms, 5), "unit": "ms", "higher_is_better": False,
         "ms_per_step": round(ms, 5), "dtype": "f32",
-        "config": {"workload": "conv3x3 64x64x320->320 + GroupNorm(32)+SiLU (f32, batch 1)",
+        "config": {"workload": "conv3x3 64x64x320->320 (Winograd F(2x2,3x3)) + GroupNorm(32)+SiLU (f32, batch 1)",
                    "input": [1, 64, 64, 320], "weight": [320, 3, 3, 320], "groups": 32, "eps": 1e-5},
-        "roofline": {"bound": "mfma", "kernel": "gemm_f32_kernel (implicit-GEMM conv3x3)",
+        "roofline": {"bound": "mfma", "kernel": "Winograd conv3x3 (input transform, 16 batched gemm_f32_kernel "
+                                                "plane GEMMs, output transform)",
                      "achieved": round(conv_tflops, 3), "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(conv_tflops / PEAK_F32_MFMA_TFLOPS, 4), "traffic": None,
-                     "work_per_launch": f"{wl.flops / 1e9:.3f} GFLOP", "avg_launch_ms": round(conv_ms, 5)},
-        "components": {"conv_ms": round(conv_ms, 5), "conv_mfma_util": round(conv_tflops / PEAK_F32_MFMA_TFLOPS, 4),
+                     "work_per_launch": f"{wino_flops / 1e9:.3f} GFLOP of plane GEMMs per conv (direct conv: "
+                                        f"{wl.flops / 1e9:.3f} GFLOP, {wl.flops / (conv_ms * 1e-3) / 1e12:.1f} "
+                                        "TFLOP/s equivalent)", "avg_launch_ms": round(conv_ms, 5)},
+        "components": {"conv_winograd_ms": round(conv_ms, 5), "conv_implicit_gemm_ms": round(gemm_ms, 5),
+                       "conv_implicit_gemm_mfma_util": round(gemm_tflops / PEAK_F32_MFMA_TFLOPS, 4),
                        "groupnorm_silu_ms": round(gn_ms, 5), "groupnorm_gbps_8B_per_elem": round(gn_gbps, 1)},
     }
     ctx.close()
@@ -116,8 +127,9 @@ def bench_conv_gn(args):
 
 def _components(ctx, steps):
     """Standalone per-kernel figures of the metric: the 3x3 conv's f32 MFMA
-    utilisation (64x64x320 -> 320) and GroupNorm+SiLU HBM GB/s at the VAE's
-    512x512x128 map (8 B/element: one read, one write)."""
+    utilisation (64x64x320 -> 320, implicit GEMM), the same conv as Winograd
+    F(2x2,3x3), and GroupNorm+SiLU HBM GB/s at the VAE's 512x512x128 map
+    (8 B/element: one read, one write)."""
     from moebius_cpu_amd import engine as E
     from moebius_cpu_amd import synthetic as S
     from moebius_cpu_amd import workloads as W
@@ -128,6 +140,9 @@ def _components(ctx, steps):
     y = E.Tensor(ctx, 1, 64, 64, 320)
     conv.forward(x, y)
     conv_ms = time_region(ctx, lambda: conv.forward(x, y), steps)
+    wconv = E.Conv3x3.same(ctx, 320, 320, E.Param(ctx, wl.w), wl.b, winograd=True)
+    wconv.forward(x, y)
+    wino_ms = time_region(ctx, lambda: wconv.forward(x, y), steps)
     xg = E.Tensor.from_numpy(ctx, S.normal(77, (1, 512, 512, 128)))
     gn = E.GroupNorm(ctx, 32, 1e-6, S.normal(78, (128,), 0.1, 1.0), S.normal(79, (128,), 0.1))
     z = E.Tensor(ctx, 1, 512, 512, 128)
@@ -137,6 +152,8 @@ def _components(ctx, steps):
     gn_gbps = 8.0 * 512 * 512 * 128 / (gn_ms * 1e-3) / 1e9
     return {"conv3x3_64x64x320_ms": round(conv_ms, 5),
             "conv3x3_mfma_util": round(conv_tf / PEAK_F32_MFMA_TFLOPS, 4),
+            "conv3x3_64x64x320_winograd_ms": round(wino_ms, 5),
+            "conv3x3_winograd_direct_equivalent_tflops": round(wl.flops / (wino_ms * 1e-3) / 1e12, 1),
             "groupnorm_silu_512x512x128_ms": round(gn_ms, 5),
             "groupnorm_silu_gbps_8B_per_elem": round(gn_gbps, 1),
             "groupnorm_hbm_frac": round(gn_gbps / PEAK_HBM_GBPS, 4)}
@@ -208,7 +225,8 @@ def bench_unet(args):
     ctx.synchronize()
     log("timed steps")
     ms = time_region(ctx, step, args.steps)
-    flops = U.step_flops(b)
+    flops = U.step_flops(b, winograd=True)  # the upsample convs run as Winograd F(2x2,3x3)
+    direct = U.step_flops(b)["total"]
     achieved = flops["total"] / (ms * 1e-3) / 1e12
     wbytes, pbytes = net.memory()
     peak = PEAK_F16_MFMA_TFLOPS if args.fast else PEAK_F32_MFMA_TFLOPS
@@ -226,7 +244,9 @@ def bench_unet(args):
         "step_roofline": {"bound": "mfma", "kernel": "whole step (all kernels, one stream)",
                           "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
                           "frac": round(achieved / peak, 4),
-                          "work": f"{flops['total'] / 1e9:.1f} GFLOP per step"},
+                          "work": f"{flops['total'] / 1e9:.1f} GFLOP per step (matrix-core work as executed: "
+                                  f"the upsample convs as Winograd GEMMs; {direct / 1e9:.1f} GFLOP with direct convs)",
+                          "direct_equivalent_tflops": round(direct / (ms * 1e-3) / 1e12, 2)},
     }
     log("dominant kernel and component kernels")
     out["roofline"] = _dominant_gemm(ctx, 50, fast=args.fast)
@@ -255,14 +275,14 @@ def _vae_run(args, which):
         lat = E.DeviceArray.from_numpy(ctx, S.normal(24, (1, 64, 64, 4)))
         out = E.DeviceArray(ctx, (1, 512, 512, 3))
         step = lambda: vae.decode(lat, out)  # noqa: E731
-        flops = V.decode_flops(64, 64)
+        flops, direct = V.decode_flops(64, 64, winograd=True), V.decode_flops(64, 64)
         wl = "Moebius VAE decode, [1,64,64,4] latent -> [1,512,512,3] image"
     else:
         img = E.DeviceArray.from_numpy(ctx, V.vae_images(seed=25, b=2, h=512, w=512))
         noise = E.DeviceArray.from_numpy(ctx, S.normal(26, (2, 64, 64, 4)))
         z = E.DeviceArray(ctx, (2, 64, 64, 4))
         step = lambda: vae.encode(img, noise, z)  # noqa: E731
-        flops = V.encode_flops(2, 512, 512)
+        flops, direct = V.encode_flops(2, 512, 512, winograd=True), V.encode_flops(2, 512, 512)
         wl = "Moebius VAE encode, 2 x [512,512,3] images (image + masked image) -> [2,64,64,4]"
     for _ in range(max(args.warmup, 1)):
         step()
@@ -278,7 +298,9 @@ def _vae_run(args, which):
         "roofline": {"bound": "mfma", "kernel": "whole pass (all kernels, one stream)",
                      "achieved": round(achieved, 2), "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_F32_MFMA_TFLOPS, 4), "traffic": None,
-                     "work_per_launch": f"{flops / 1e9:.1f} GFLOP per pass", "avg_launch_ms": round(ms, 4)},
+                     "work_per_launch": f"{flops / 1e9:.1f} GFLOP per pass (stride-1 3x3 convs as Winograd GEMMs; "
+                                        f"{direct / 1e9:.1f} GFLOP with direct convs)", "avg_launch_ms": round(ms, 4),
+                     "direct_equivalent_tflops": round(direct / (ms * 1e-3) / 1e12, 2)},
     }
     vae.close()
     ctx.close()

@@ -11,6 +11,8 @@
 // Arithmetic matches the reference tap for tap: acc = bias, then for ky, for kx,
 // acc = fma(w, x, acc) (depthwise.rs:118-141); rows outside the image are
 // skipped and columns outside contribute fma(w, 0, acc) == acc.
+#include <cstdlib>
+
 #include "common.hpp"
 #include "dmath.hpp"
 #include "kernels.hpp"
@@ -138,6 +140,129 @@ __global__ __launch_bounds__(256) void depthwise_kernel(const typename Vec<VW>::
     }
 }
 
+// LDS-tiled variant for channel counts that are multiples of 4: a workgroup
+// stages the (8+2) x (8+2) input pixels of an 8x8 output tile for 16 channel
+// quads (and the matching gate quads for GLU) in LDS once, then each thread
+// computes four adjacent output pixels of one quad from LDS. Every input value
+// is read from L2/HBM about (10*10)/(8*8) = 1.6 times instead of 4.5, and the
+// optional GroupNorm prologue is applied once per staged value. The tap order
+// and the skipped out-of-image rows are those of depthwise_kernel.
+constexpr int kDwTH = 8, kDwTW = 8, kDwCQ = 16;
+constexpr int kDwNP = (kDwTH + 2) * (kDwTW + 2);
+
+template <int EPI, bool PRO>
+__global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__restrict__ x, int n, int h, int w,
+                                                             int cv, const float4 *__restrict__ wt,
+                                                             const float4 *__restrict__ bias, DwPrologue pro,
+                                                             float4 *__restrict__ out) {
+    using V = Vec<4>;
+    constexpr int PARTS = EPI == 2 ? 2 : 1;
+    __shared__ float4 tile[PARTS][kDwNP][kDwCQ];
+    const int co_v = EPI == 2 ? cv / 2 : cv;
+    const int tiles_x = (w + kDwTW - 1) / kDwTW, tiles_y = (h + kDwTH - 1) / kDwTH;
+    int bid = blockIdx.x;
+    const int tx = bid % tiles_x;
+    bid /= tiles_x;
+    const int ty = bid % tiles_y;
+    const int b = bid / tiles_y;
+    const int q0 = blockIdx.y * kDwCQ;
+    const int oy0 = ty * kDwTH, ox0 = tx * kDwTW;
+    // Staging: every load of the thread is issued before the first LDS store,
+    // so a thread has all of its (up to 13) 16-byte loads in flight at once.
+    constexpr int TOTAL = PARTS * kDwNP * kDwCQ;
+    constexpr int PER = (TOTAL + 255) / 256;
+    float4 v[PER];
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int idx = threadIdx.x + 256 * i;
+        const int part = idx / (kDwNP * kDwCQ);
+        const int r = idx - part * (kDwNP * kDwCQ);
+        const int pix = r / kDwCQ, qq = r - pix * kDwCQ;
+        const int iy = oy0 - 1 + pix / (kDwTW + 2), ix = ox0 - 1 + pix % (kDwTW + 2);
+        v[i] = V::zero();
+        if (idx < TOTAL && q0 + qq < co_v && iy >= 0 && iy < h && ix >= 0 && ix < w)
+            v[i] = x[(size_t(b) * h + iy) * size_t(w) * cv + size_t(ix) * cv + q0 + qq + part * co_v];
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+        const int idx = threadIdx.x + 256 * i;
+        if (idx >= TOTAL) break;
+        const int part = idx / (kDwNP * kDwCQ);
+        const int r = idx - part * (kDwNP * kDwCQ);
+        const int pix = r / kDwCQ, qq = r - pix * kDwCQ;
+        if (PRO) {
+            const int iy = oy0 - 1 + pix / (kDwTW + 2), ix = ox0 - 1 + pix % (kDwTW + 2);
+            if (q0 + qq < co_v && iy >= 0 && iy < h && ix >= 0 && ix < w) {
+                const int qin = q0 + qq + part * co_v;
+                v[i] = V::fma(v[i], reinterpret_cast<const float4 *>(pro.scale)[size_t(b) * cv + qin],
+                              reinterpret_cast<const float4 *>(pro.shift)[size_t(b) * cv + qin]);
+                if (pro.silu) v[i] = V::silu(v[i]);
+            }
+        }
+        tile[part][pix][qq] = v[i];
+    }
+    __syncthreads();
+    const int qq = threadIdx.x % kDwCQ, g = threadIdx.x / kDwCQ;
+    const int r = g / (kDwTW / 4), c0 = (g % (kDwTW / 4)) * 4;
+    const int q = q0 + qq, oy = oy0 + r;
+    if (q >= co_v || oy >= h) return;  // no barrier follows
+    float4 acc[PARTS][4];
+#pragma unroll
+    for (int part = 0; part < PARTS; ++part) {
+        const int qw = q + part * co_v;
+        const float4 bv = bias[qw];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[part][j] = bv;
+#pragma unroll
+        for (int ky = 0; ky < 3; ++ky) {
+            const int iy = oy + ky - 1;
+            if (iy < 0 || iy >= h) continue;
+            float4 win[6];
+#pragma unroll
+            for (int j = 0; j < 6; ++j) win[j] = tile[part][(r + ky) * (kDwTW + 2) + c0 + j][qq];
+            const float4 w0 = wt[(ky * 3 + 0) * cv + qw], w1 = wt[(ky * 3 + 1) * cv + qw],
+                         w2 = wt[(ky * 3 + 2) * cv + qw];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[part][j] = V::fma(w0, win[j], acc[part][j]);
+                acc[part][j] = V::fma(w1, win[j + 1], acc[part][j]);
+                acc[part][j] = V::fma(w2, win[j + 2], acc[part][j]);
+            }
+        }
+    }
+    float4 *dst = out + (size_t(b) * h + oy) * size_t(w) * co_v + q;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int ox = ox0 + c0 + j;
+        if (ox >= w) break;
+        float4 y;
+        if (EPI == 2) y = V::glu(acc[0][j], acc[PARTS - 1][j]);
+        else if (EPI == 1) y = V::relu(acc[0][j]);
+        else y = acc[0][j];
+        dst[size_t(ox) * co_v] = y;
+    }
+}
+
+template <bool PRO>
+void launch_dw_tile(Context &ctx, const float *x, int n, int h, int w, int c, const float *wt, const float *bias,
+                    int epilogue, const DwPrologue &pro, float *out) {
+    const int cv = c / 4;
+    const int co_v = epilogue == 2 ? cv / 2 : cv;
+    const int64_t tiles = int64_t(n) * ceil_div(h, kDwTH) * ceil_div(w, kDwTW);
+    MH_REQUIRE(tiles < (int64_t(1) << 31), "depthwise: map too large");
+    const dim3 grid(unsigned(tiles), unsigned(ceil_div(co_v, kDwCQ)));
+    const float4 *xv = reinterpret_cast<const float4 *>(x);
+    const float4 *wv = reinterpret_cast<const float4 *>(wt);
+    const float4 *bv = reinterpret_cast<const float4 *>(bias);
+    float4 *ov = reinterpret_cast<float4 *>(out);
+    switch (epilogue) {
+        case 0: depthwise_tile_kernel<0, PRO><<<grid, 256, 0, ctx.stream>>>(xv, n, h, w, cv, wv, bv, pro, ov); break;
+        case 1: depthwise_tile_kernel<1, PRO><<<grid, 256, 0, ctx.stream>>>(xv, n, h, w, cv, wv, bv, pro, ov); break;
+        default: depthwise_tile_kernel<2, PRO><<<grid, 256, 0, ctx.stream>>>(xv, n, h, w, cv, wv, bv, pro, ov); break;
+    }
+    MH_LAUNCH_CHECK();
+}
+
 template <int VW, int TX, bool PRO>
 void launch_dw(Context &ctx, const float *x, int n, int h, int w, int c, const float *wt, const float *bias,
                int epilogue, const DwPrologue &pro, float *out) {
@@ -176,7 +301,12 @@ void depthwise3x3(Context &ctx, const float *x, int n, int h, int w, int c, cons
     }
     const bool vec4 = co % 4 == 0 && aligned16(x) && aligned16(weight) && aligned16(bias) && aligned16(out) &&
                       aligned16(pro.scale) && aligned16(pro.shift);
-    if (vec4) {
+    const char *tiled_env = std::getenv("MOEBIUS_HIP_DW_TILED");  // A/B override: 0 = register-window kernel
+    const int tiled = tiled_env ? std::atoi(tiled_env) : 1;
+    if (vec4 && tiled) {
+        if (prologue) launch_dw_tile<true>(ctx, x, n, h, w, c, weight, bias, epilogue, pro, out);
+        else launch_dw_tile<false>(ctx, x, n, h, w, c, weight, bias, epilogue, pro, out);
+    } else if (vec4) {
         if (prologue) launch_dw<4, 4, true>(ctx, x, n, h, w, c, weight, bias, epilogue, pro, out);
         else launch_dw<4, 4, false>(ctx, x, n, h, w, c, weight, bias, epilogue, pro, out);
     } else {

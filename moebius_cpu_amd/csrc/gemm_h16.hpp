@@ -117,8 +117,11 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
     constexpr int MF = mf_for<BM, BN>();
     using MI = MfH<MF>;
     constexpr int FM = BM / 2 / MF, FN = BN / 2 / MF;
-    if (blockIdx.y) {
-        const int64_t bz = blockIdx.y;
+    const int tiles_m = (p.M + BM - 1) / BM;
+    const int tiles_n = (p.N + BN - 1) / BN;
+    const TileIdx ti = tile_index(tiles_m, tiles_n);
+    if (ti.y) {
+        const int64_t bz = ti.y;
         p.a += bz * p.a_bs;
         p.b = static_cast<const char *>(p.b) + bz * p.b_bs * (F16 ? 2 : 4);
         p.out += bz * p.c_bs;
@@ -131,22 +134,8 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
     _Float16(*As)[BM * LDS_H] = reinterpret_cast<_Float16(*)[BM * LDS_H]>(smem);
     _Float16(*Bs)[BN * LDS_H] = reinterpret_cast<_Float16(*)[BN * LDS_H]>(smem + 2 * BM * LDS_H);
 
-    const int tiles_m = (p.M + BM - 1) / BM;
-    const int tiles_n = (p.N + BN - 1) / BN;
-    int tm, tn;
-    {
-        constexpr int GROUP = 8;
-        const int pid = blockIdx.x;
-        const int in_group = GROUP * tiles_n;
-        const int gid = pid / in_group;
-        const int first = gid * GROUP;
-        const int gsize = min(tiles_m - first, GROUP);
-        const int r = pid - gid * in_group;
-        tm = first + r % gsize;
-        tn = r / gsize;
-    }
-    const int m0 = tm * BM, n0 = tn * BN;
-    const int k_begin = SPLIT ? blockIdx.z * p.k_split : 0;
+    const int m0 = ti.tm * BM, n0 = ti.tn * BN;
+    const int k_begin = SPLIT ? ti.z * p.k_split : 0;
     const int k_end = SPLIT ? min(p.K, k_begin + p.k_split) : p.K;
     const int ktiles = (k_end - k_begin + BKH - 1) / BKH;
 
@@ -249,7 +238,7 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
         }
     }
     __syncthreads();
-    write_tile<BM, BN, MF, EPI, SPLIT>(p, reinterpret_cast<float *>(smem), acc, m0, n0);
+    write_tile<BM, BN, MF, EPI, SPLIT>(p, reinterpret_cast<float *>(smem), acc, m0, n0, ti.z);
 }
 
 // Tile shape and K split of the fast kernel, from sweeps of every (tile,

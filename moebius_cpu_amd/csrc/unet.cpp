@@ -2,6 +2,7 @@
 // gfx950 kernels. The whole denoise step stays in HBM: inputs tiled to the CFG
 // batch on the device, the skip stack held in pooled buffers, and only eps
 // leaves the device.
+#include <cstdlib>
 #include "unet.hpp"
 
 #include <cmath>
@@ -159,9 +160,10 @@ struct GN {
         return out;
     }
     // Statistics only: [scale | shift], each [n * c], for a consumer that applies them.
-    float *affine(Env &e, const DT &x, const float *add) const {
+    float *affine(Env &e, const DT &x, const float *add, int64_t add_ld = 0) const {
         float *ss = e.pool.floats(int64_t(2) * x.n * x.c);
-        group_norm_affine(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, eps, g, b, add, ss, ss + int64_t(x.n) * x.c);
+        group_norm_affine(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, eps, g, b, add, ss, ss + int64_t(x.n) * x.c,
+                          add_ld);
         return ss;
     }
 };
@@ -202,6 +204,30 @@ struct DwConv2d {
         e.pool.recycle(mid);
         return out;
     }
+    // The same of a = SiLU(x . scale + shift) (a GroupNorm affine, ss = [scale |
+    // shift] per item and channel) without writing a: the depthwise conv applies
+    // the affine as it stages its input, and the identity residual (c_in ==
+    // c_out) is a transformed in the pointwise conv's epilogue. Every value is
+    // computed as the separate apply pass would (fma, then SiLU), so the result
+    // is bit-identical to fwd(apply(x)).
+    DT fwd_gn(Env &e, const DT &x, const float *ss, const float *res2 = nullptr, float *out_p = nullptr) const {
+        Affine aff;
+        aff.scale = ss;
+        aff.shift = ss + int64_t(x.n) * x.c;
+        aff.silu = true;
+        DT mid = e.pool.tensor(x.n, x.h, x.w, x.c);
+        depthwise3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, dw, dwb, 1, mid.p, &aff);
+        DT out = out_p ? DT{out_p, x.n, x.h, x.w, co} : e.pool.tensor(x.n, x.h, x.w, co);
+        ResidualAffine ra;
+        ra.scale = aff.scale;
+        ra.shift = aff.shift;
+        ra.silu = true;
+        ra.rows_per_item = x.h * x.w;
+        conv1x1(e.ctx, mid.p, mid.px(), ci, pw.w.p, pw.w.wt, co, pw.b, ci == co ? x.p : nullptr, out.p,
+                GemmEpilogue::None, ci == co ? &ra : nullptr, res2);
+        e.pool.recycle(mid);
+        return out;
+    }
 };
 
 // src/unet/blocks.rs:56-113
@@ -224,21 +250,22 @@ struct DwResnet {
     }
     // temb_silu: [n, 1280] = SiLU(temb), shared by every resnet of the step.
     // tp: this block's time projection, item i's row at tp + i * tp_ld (all the
-    // step's projections come out of one GEMM, UNetDevice::forward). The
-    // shortcut (or x) is added in conv2's pointwise epilogue. (The GroupNorm
-    // outputs are written out: applying GN + SiLU inside the depthwise conv's
-    // loads re-evaluates SiLU for every tap, which costs more than the pass.)
+    // step's projections come out of one GEMM, UNetDevice::forward), folded into
+    // norm2's shift. Neither GroupNorm output is written: each DwConv2d applies
+    // GN + SiLU as its depthwise conv stages the input in LDS (about 1.6
+    // evaluations per value), and its identity residual in the pointwise
+    // epilogue. The shortcut (or x) is added in conv2's pointwise epilogue.
     DT fwd(Env &e, const DT &x, const float *tp, int64_t tp_ld) const {
-        DT a = norm1.fwd(e, x, nullptr, true);
-        DT b = conv1.fwd(e, a);
-        e.pool.recycle(a);
-        a = norm2.fwd(e, b, tp, true, tp_ld);
-        e.pool.recycle(b);
+        float *ss1 = norm1.affine(e, x, nullptr);
+        DT b = conv1.fwd_gn(e, x, ss1);
+        e.pool.recycle(ss1);
+        float *ss2 = norm2.affine(e, b, tp, tp_ld);
         DT s;
         if (has_shortcut) s = shortcut.fwd(e, x);
-        DT out = conv2.fwd(e, a, has_shortcut ? s.p : x.p);
+        DT out = conv2.fwd_gn(e, b, ss2, has_shortcut ? s.p : x.p);
         if (has_shortcut) e.pool.recycle(s);
-        e.pool.recycle(a);
+        e.pool.recycle(ss2);
+        e.pool.recycle(b);
         return out;
     }
 };
@@ -659,11 +686,11 @@ class UNetDevice {
             tr("unet.up." + std::to_string(i) + ".out", h);
         }
         if (!skips.empty()) fail(kInternal, "skip stack not consumed");
-        // norm_out + SiLU, then conv_out straight into the caller's eps buffer.
-        DT a = norm_out_.fwd(e, h, nullptr, true);
+        // norm_out + SiLU applied inside conv_out, which writes the caller's eps buffer.
+        float *ss = norm_out_.affine(e, h, nullptr);
+        conv_out_.fwd_gn(e, h, ss, nullptr, eps_dev);
+        pool_.recycle(ss);
         pool_.recycle(h);
-        conv_out_.fwd(e, a, nullptr, eps_dev);
-        pool_.recycle(a);
         pool_.recycle(temb);
         pool_.recycle(temb_silu);
         pool_.recycle(tp);

@@ -151,11 +151,13 @@ def param_count() -> int:
     return sum(int(np.prod(s.shape)) for s in unet_specs())
 
 
-def step_flops(batch: int = 2) -> dict:
+def step_flops(batch: int = 2, winograd: bool = False) -> dict:
     """Algorithmic FLOPs of one denoise step (multiply-add = 2), by kernel
     family, for the architecture above at a 64x64 latent: the GEMM-shaped
     work (1x1 convs and linears, the dense 3x3 convs, the lambda GEMMs) and
-    the vector work (depthwise, tap filter, position term)."""
+    the vector work (depthwise, tap filter, position term). winograd: count
+    the two upsample convs as the Winograd F(2x2,3x3) GEMM work this build
+    executes (else as direct convs)."""
     f = {"gemm_1x1": 0.0, "conv3x3": 0.0, "lambda_gemm": 0.0, "depthwise": 0.0, "tap_filter": 0.0,
          "position_term": 0.0}
 
@@ -200,7 +202,9 @@ def step_flops(batch: int = 2) -> dict:
             tr(p, c)
             h_c = c
         if i + 1 < 3:
-            f["conv3x3"] += 2 * (4 * p) * 9 * c * c
+            # upsample conv: 4p output pixels; as Winograd F(2x2,3x3), 16 plane
+            # GEMMs over p tiles (32 p c^2) instead of the direct 72 p c^2
+            f["conv3x3"] += 32 * p * c * c if winograd else 2 * (4 * p) * 9 * c * c
     f["total"] = sum(f.values())
     return f
 

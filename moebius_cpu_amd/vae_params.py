@@ -114,15 +114,27 @@ def param_count() -> int:
     return sum(int(np.prod(s.shape)) for s in vae_specs())
 
 
-def decode_flops(h: int = 64, w: int = 64) -> float:
-    """Algorithmic FLOPs of one decode of an h x w latent (multiply-add = 2):
-    the 3x3 and 1x1 convs and the mid attention's two products."""
+def _conv3_flops(px: int, ci: int, co: int, winograd: bool, same: bool = True) -> float:
+    """FLOPs of a 3x3 conv with px output pixels: the direct count 2*px*9*ci*co,
+    or, for the stride-1 convs this build runs as Winograd F(2x2,3x3) (both
+    channel counts multiples of 4), the 16 plane GEMMs over px/4 tiles:
+    32 * (px/4) * ci * co = 8*px*ci*co (transforms not counted)."""
+    if winograd and same and ci % 4 == 0 and co % 4 == 0:
+        return 8.0 * px * ci * co
+    return 2.0 * px * 9 * ci * co
+
+
+def decode_flops(h: int = 64, w: int = 64, winograd: bool = False) -> float:
+    """FLOPs of one decode of an h x w latent (multiply-add = 2): the 3x3 and 1x1
+    convs and the mid attention's two products. winograd: count the stride-1
+    3x3 convs as the Winograd GEMM work this build executes (else direct)."""
     f = 0.0
     p = h * w
-    f += 2 * p * LATENT_C * LATENT_C + 2 * p * 9 * LATENT_C * CH[-1]
+    f += 2 * p * LATENT_C * LATENT_C + _conv3_flops(p, LATENT_C, CH[-1], winograd)
 
     def res(px, ci, co):
-        return 2 * px * 9 * (ci * co + co * co) + (2 * px * ci * co if ci != co else 0)
+        return (_conv3_flops(px, ci, co, winograd) + _conv3_flops(px, co, co, winograd)
+                + (2 * px * ci * co if ci != co else 0))
 
     f += 2 * res(p, CH[-1], CH[-1]) + 2 * p * 4 * CH[-1] ** 2 + 4 * p * p * CH[-1]
     c_prev = CH[-1]
@@ -131,20 +143,21 @@ def decode_flops(h: int = 64, w: int = 64) -> float:
             f += res(p, c_prev if j == 0 else c, c)
         if i + 1 < len(CH):
             p *= 4
-            f += 2 * p * 9 * c * c
+            f += _conv3_flops(p, c, c, winograd)
         c_prev = c
-    f += 2 * p * 9 * CH[0] * IMAGE_C
+    f += _conv3_flops(p, CH[0], IMAGE_C, winograd)
     return f
 
 
-def encode_flops(b: int = 2, h: int = 512, w: int = 512) -> float:
-    """Algorithmic FLOPs of encoding b images of h x w."""
+def encode_flops(b: int = 2, h: int = 512, w: int = 512, winograd: bool = False) -> float:
+    """FLOPs of encoding b images of h x w (see decode_flops for winograd)."""
     f = 0.0
     p = h * w
-    f += 2 * p * 9 * IMAGE_C * CH[0]
+    f += _conv3_flops(p, IMAGE_C, CH[0], winograd)
 
     def res(px, ci, co):
-        return 2 * px * 9 * (ci * co + co * co) + (2 * px * ci * co if ci != co else 0)
+        return (_conv3_flops(px, ci, co, winograd) + _conv3_flops(px, co, co, winograd)
+                + (2 * px * ci * co if ci != co else 0))
 
     c_prev = CH[0]
     for i, c in enumerate(CH):
@@ -152,10 +165,10 @@ def encode_flops(b: int = 2, h: int = 512, w: int = 512) -> float:
             f += res(p, c_prev if j == 0 else c, c)
         if i + 1 < len(CH):
             p //= 4
-            f += 2 * p * 9 * c * c
+            f += _conv3_flops(p, c, c, winograd, same=False)  # stride-2 downsample
         c_prev = c
     f += 2 * res(p, CH[-1], CH[-1]) + 2 * p * 4 * CH[-1] ** 2 + 4 * p * p * CH[-1]
-    f += 2 * p * 9 * CH[-1] * 2 * LATENT_C + 2 * p * 64
+    f += _conv3_flops(p, CH[-1], 2 * LATENT_C, winograd) + 2 * p * 64
     return b * f
 
 

@@ -155,9 +155,14 @@ def test_conv3x3_odd_sizes_f16_weights(ctx, n, h, w, ci, co, up):
 
 
 # ---- tests/kernels.rs:172-213
+@pytest.mark.parametrize("tiled", ["1", "0"])
 @pytest.mark.parametrize("h,w,c,ep", [(5, 7, 64, "relu"), (4, 9, 70, "none"), (3, 5, 140, "glu_silu"),
-                                      (2, 4, 64, "glu_silu"), (7, 5, 9, "relu")])
-def test_depthwise_register_blocks_and_tails(ctx, h, w, c, ep):
+                                      (2, 4, 64, "glu_silu"), (7, 5, 9, "relu"),
+                                      # 8x8 LDS tiles with partial tiles and partial 16-quad channel chunks
+                                      (9, 13, 72, "relu"), (17, 6, 136, "none"), (10, 11, 200, "glu_silu"),
+                                      (16, 16, 256, "glu_silu"), (8, 8, 8, "none")])
+def test_depthwise_register_blocks_and_tails(ctx, h, w, c, ep, tiled, monkeypatch):
+    monkeypatch.setenv("MOEBIUS_HIP_DW_TILED", tiled)
     x = hashed(h * w * c, 7919, 211, 211.0, 0.5).reshape(1, h, w, c)
     wt = hashed(9 * c, 31, 17, 17.0, 0.5).reshape(3, 3, c)
     b = (np.arange(c, dtype=np.float32) * np.float32(0.01) - np.float32(0.2)).astype(np.float32)
@@ -170,7 +175,8 @@ def test_depthwise_register_blocks_and_tails(ctx, h, w, c, ep):
 # (src/unet/blocks.rs:89-90): bit-exact to GN apply (norm.rs:132-148) then
 # depthwise3x3 (depthwise.rs:31-59) on the oracle
 @pytest.mark.parametrize("n,h,w,c,ep,silu", [(2, 9, 7, 64, "relu", True), (1, 5, 6, 40, "none", False),
-                                             (2, 4, 5, 140, "glu_silu", True), (1, 6, 3, 18, "relu", True)])
+                                             (2, 4, 5, 140, "glu_silu", True), (1, 6, 3, 18, "relu", True),
+                                             (2, 11, 9, 80, "relu", True), (1, 9, 10, 144, "glu_silu", True)])
 def test_depthwise_gn_prologue_bit_exact(ctx, n, h, w, c, ep, silu):
     rng = np.random.default_rng(h * w + c)
     x = rng.standard_normal((n, h, w, c)).astype(np.float32)

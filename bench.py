@@ -162,9 +162,9 @@ def _components(ctx, steps):
 # HBM bytes per launch of the dominant kernel (below), from rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE over this script's own default run (two UNet steps plus the standalone
 # timing loop), each scaled by the counter's reading for a plain 256 MiB device copy
-# (FETCH_SIZE reads half the copied bytes, WRITE_SIZE all of them): 17.01 MiB fetched +
-# 10.00 MiB written per launch, mean of 95 launches.
-DOMINANT_TRAFFIC_BYTES = int((17.01 + 10.00) * 1048576)
+# (FETCH_SIZE reads half the copied bytes, WRITE_SIZE all of them), averaged over the
+# standalone loop's 51 launches: 13.22 MiB fetched + 10.00 MiB written per launch.
+DOMINANT_TRAFFIC_BYTES = int((13.22 + 10.00) * 1048576)
 
 
 def _dominant_gemm(ctx, steps, fast=False):

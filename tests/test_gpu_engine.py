@@ -347,6 +347,30 @@ def test_group_norm_closed_form_moments(ctx):
     assert np.max(np.abs(y.var(axis=(1, 3)) - var / (var + np.float64(np.float32(eps))))) < 1e-5
 
 
+# ---- GroupNorm statistics: the one-launch path for every tile width it uses
+# (whole groups per tile: 60, 40 and 64 channels, a partial last tile) and the
+# two-launch path for groups wider than 64 channels (2560 / 32 = 80), with and
+# without the per-item add folded into the shift (src/engine/norm.rs:57-105)
+@pytest.mark.parametrize("n,h,w,c,use_add", [(2, 9, 7, 320, True), (2, 16, 16, 1280, False), (1, 13, 11, 960, True),
+                                             (2, 8, 8, 2560, True), (1, 21, 19, 128, False), (2, 5, 6, 96, True),
+                                             (2, 64, 64, 320, False)])
+def test_group_norm_affine_every_tiling(ctx, n, h, w, c, use_add):
+    rng = np.random.default_rng(c + h)
+    x = (rng.standard_normal((n, h, w, c)) * 1.7 - 0.4).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+    beta = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    add = (0.5 * rng.standard_normal((n, c))).astype(np.float32) if use_add else None
+    gn = E.GroupNorm(ctx, 32, 1e-5, gamma, beta)
+    aff = gn.affine(T(ctx, x), E.DeviceArray.from_numpy(ctx, add) if use_add else None, False)
+    sc_want, sh_want = oracle.group_norm_affine(x, 32, 1e-5, gamma, beta, add)
+    assert max_abs_rel(aff.scale.numpy(), sc_want) <= 1e-6
+    assert max_abs_rel(aff.shift.numpy(), sh_want) <= 1e-6
+    # a second call reuses the counters the first one reset
+    aff2 = gn.affine(T(ctx, x), E.DeviceArray.from_numpy(ctx, add) if use_add else None, False)
+    assert np.array_equal(aff2.scale.numpy(), aff.scale.numpy())
+    assert np.array_equal(aff2.shift.numpy(), aff.shift.numpy())
+
+
 def test_group_norm_apply_bit_exact_given_affine(ctx):
     """The apply pass restates apply_affine exactly: same scale/shift -> same bits."""
     rng = np.random.default_rng(5)

@@ -79,7 +79,7 @@ __global__ void mfma_probe_kernel(const float *a, const float *b, float *d) {
 
 void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void *weight, WeightType wt, int c_out,
              const float *bias, const float *residual, float *out, GemmEpilogue epi, const ResidualAffine *raff,
-             const float *residual2) {
+             const float *residual2, GnPartials *gn) {
     MH_REQUIRE(c_in > 0 && c_out > 0, "Conv1x1: empty channel axis");
     MH_REQUIRE(pixels < (int64_t(1) << 31), "Conv1x1: too many pixels");
     if (raff) {
@@ -108,10 +108,15 @@ void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void 
         p.r_rows = raff->rows_per_item;
     }
     p.res2 = residual2;
+    if (gn) {
+        p.gnp = gn->part;
+        p.gn_item_rows = gn->item_rows;
+    }
     if (c_in % 4 == 0 && aligned16(x))
         run_dense(ctx, p, wt, epi, 1, true);
     else
         run_dense(ctx, p, wt, epi, 1, false);
+    if (gn) gn->rows = p.gn_rows;
 }
 
 void conv1x1_segments(Context &ctx, const float *x, int64_t pixels, int c_in, const void *weight, WeightType wt,

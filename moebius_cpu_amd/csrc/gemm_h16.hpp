@@ -129,7 +129,8 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
     }
     constexpr int A_LD = BM * KCH / 256, B_LD = BN * KCH / 256;
     constexpr int SMEM_H = 2 * (BM + BN) * LDS_H;  // halves
-    static_assert(BM * (BN + 8) * 2 <= SMEM_H, "C tile must fit in the staging space");
+    static_assert(BM * (BN + 8) * 2 <= SMEM_H && SMEM_H >= 2 * 2048,
+                  "C tile and GroupNorm sums must fit in the staging space");
     __shared__ __align__(16) _Float16 smem[SMEM_H];
     _Float16(*As)[BM * LDS_H] = reinterpret_cast<_Float16(*)[BM * LDS_H]>(smem);
     _Float16(*Bs)[BN * LDS_H] = reinterpret_cast<_Float16(*)[BN * LDS_H]>(smem + 2 * BM * LDS_H);
@@ -279,6 +280,7 @@ void launch_cfg_h16(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi,
         p.partial = static_cast<float *>(ctx.ws.get(bytes, ctx.stream));
         p.k_split = pl.k_split;
         p.vec_out = (p.N & 3) == 0 && (reinterpret_cast<uintptr_t>(p.partial) & 15) == 0;
+        gn_partials_plan(p, BM, BN, pl.splits, batch);
         dim3 grid(tiles, 1, pl.splits);
         gemm_h16_kernel<BM, BN, MODE, PRO, F16, BVEC, 0, true><<<grid, 256, 0, ctx.stream>>>(p);
         MH_LAUNCH_CHECK();
@@ -299,6 +301,7 @@ void launch_cfg_h16(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi,
     } else {
         p.k_split = p.K;
         p.vec_out = out_vec_ok(p);
+        gn_partials_plan(p, BM, BN, 1, batch);
         const dim3 grid(tiles, unsigned(batch));
         if constexpr (MODE <= kDenseScalar) {
             if (epi == GemmEpilogue::Silu) {

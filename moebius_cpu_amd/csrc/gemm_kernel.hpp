@@ -26,13 +26,13 @@ constexpr int LDS_S = BK + 4;   // padded LDS row stride (floats): conflict-free
 constexpr int K4 = BK / 4;      // float4 per tile row
 constexpr int kMaxSeg = 3;      // column segments of a segmented output
 
-// Matrix instruction: v_mfma_f32_32x32x2f32 (MF = 32) for tiles of 64 or more
-// in both dimensions, v_mfma_f32_16x16x4f32 (MF = 16) for the 32-wide tiles of
-// small GEMMs. Output lane layouts: 16x16: register v of lane l is row
-// 4 * (l / 16) + v, column l % 16; 32x32: row 8 * (v / 4) + 4 * (l / 32) + v % 4,
-// column l % 32.
+// Matrix instruction: v_mfma_f32_32x32x2f32 (MF = 32) when each wave's half
+// of the tile is a multiple of 32 in both dimensions, else v_mfma_f32_16x16x4f32
+// (MF = 16: the 32-row or 32-column tiles of the small GEMMs). Output lane
+// layouts: 16x16: register v of lane l is row 4 * (l / 16) + v, column l % 16;
+// 32x32: row 8 * (v / 4) + 4 * (l / 32) + v % 4, column l % 32.
 template <int BM, int BN>
-constexpr int mf_for() { return (BM >= 64 && BN >= 64) ? 32 : 16; }
+constexpr int mf_for() { return ((BM / 2) % 32 == 0 && (BN / 2) % 32 == 0) ? 32 : 16; }
 
 template <int M>
 struct Mf {
@@ -95,6 +95,13 @@ struct GemmArgs {
     // set by the launcher: the output (or split partials) may be written four
     // adjacent columns at a time with 16-byte accesses (see out_vec_ok)
     int vec_out;
+    // GroupNorm statistics of the output (optional): row tile t writes, per
+    // column, (sum y, sum y*y) over its BM rows of the values stored to
+    // gnp [t][N][2]; gn_item_rows = rows per batch item (tiles must not straddle
+    // items). The launcher clears gnp where it cannot honour it and reports the
+    // rows per partial in gn_rows (0: none written).
+    float *gnp;
+    int gn_item_rows, gn_rows;
 };
 
 // (residual [transformed] + bias) + acc [SiLU] (+ res2): the reference's
@@ -158,9 +165,10 @@ __device__ __forceinline__ float *out_ptr(const GemmArgs &p, int row, int col, i
 }
 
 // epilogue_value for four adjacent columns col..col+3 of one row, with 16-byte
-// loads and one 16-byte store (the caller has checked out_vec_ok).
+// loads and one 16-byte store (the caller has checked out_vec_ok); returns the
+// values stored.
 template <int EPI>
-__device__ __forceinline__ void store4(const GemmArgs &p, int row, int col, float4 s) {
+__device__ __forceinline__ float4 store4(const GemmArgs &p, int row, int col, float4 s) {
     int64_t o;
     float *dst = out_ptr(p, row, col, o);
     float y[4] = {s.x, s.y, s.z, s.w};
@@ -194,7 +202,9 @@ __device__ __forceinline__ void store4(const GemmArgs &p, int row, int col, floa
         const float4 r2 = *reinterpret_cast<const float4 *>(p.res2 + o);
         y[0] = y[0] + r2.x, y[1] = y[1] + r2.y, y[2] = y[2] + r2.z, y[3] = y[3] + r2.w;
     }
-    *reinterpret_cast<float4 *>(dst + o) = float4{y[0], y[1], y[2], y[3]};
+    const float4 r{y[0], y[1], y[2], y[3]};
+    *reinterpret_cast<float4 *>(dst + o) = r;
+    return r;
 }
 
 // Whether the output can be written four adjacent columns at a time: N, the
@@ -413,8 +423,38 @@ __device__ __forceinline__ TileIdx tile_index(int tiles_m, int tiles_n) {
     return r;
 }
 
+// GroupNorm partials of one output tile (GemmArgs::gnp): thread t holds the
+// sums over its rows of column quad t % (BN / 4); the 256 / (BN / 4) threads of
+// a quad are added in thread order through LDS (2048 floats), so the partials
+// are deterministic.
+template <int BM, int BN>
+__device__ __forceinline__ void gn_tile_partials(const GemmArgs &p, float *smem, float4 s, float4 q, int m0, int n0) {
+    constexpr int C4 = BN / 4, R = 256 / C4;
+    const int tid = threadIdx.x;
+    float4 *red = reinterpret_cast<float4 *>(smem);
+    __syncthreads();  // every thread is done with the C tile
+    red[tid] = s;
+    red[256 + tid] = q;
+    __syncthreads();
+    if (tid < C4) {
+        const int col = n0 + tid * 4;
+        if (col < p.N) {
+            float4 ts = red[tid], tq = red[256 + tid];
+#pragma unroll
+            for (int r = 1; r < R; ++r) {
+                const float4 a = red[r * C4 + tid], b = red[256 + r * C4 + tid];
+                ts.x += a.x, ts.y += a.y, ts.z += a.z, ts.w += a.w;
+                tq.x += b.x, tq.y += b.y, tq.z += b.z, tq.w += b.w;
+            }
+            float *dst = p.gnp + (int64_t(m0 / BM) * p.N + col) * 2;
+            *reinterpret_cast<float4 *>(dst) = float4{ts.x, tq.x, ts.y, tq.y};
+            *reinterpret_cast<float4 *>(dst + 4) = float4{ts.z, tq.z, ts.w, tq.w};
+        }
+    }
+}
+
 // Epilogue through LDS, shared by the f32 and f16 kernels (smem holds at least
-// BM * (BN + 8) floats and is free): block (i, j), register v, lane l of wave
+// BM * (BN + 8) floats and 2048 floats, and is free): block (i, j), register v, lane l of wave
 // (wm, wn) holds row acc_row(v, l), column l % MF; the tile is written to LDS,
 // then each thread finishes four adjacent columns of a row at a time (16-byte
 // loads and stores), or one element at a time where that is not possible.
@@ -440,19 +480,32 @@ __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const
     }
     __syncthreads();
     if (p.vec_out) {
-        constexpr int C4 = BN / 4, RPP = 256 / C4;  // float4 per tile row, rows per pass
-        const int cc = (tid % C4) * 4, col = n0 + cc;
-        if (col < p.N) {  // N % 4 == 0: the whole float4 is inside
+        constexpr int C4 = BN / 4;  // float4 per tile row
+        static_assert(BM * C4 % 256 == 0, "whole passes over the C tile");
+        // GroupNorm sums: a thread keeps one column quad over all its rows.
+        constexpr bool kGn = !SPLIT && 256 % C4 == 0;
+        float4 gs{0.f, 0.f, 0.f, 0.f}, gq = gs;
 #pragma unroll
-            for (int it = 0; it < BM / RPP; ++it) {
-                const int rr = tid / C4 + it * RPP, row = m0 + rr;
-                if (row >= p.M) break;
-                const float4 v = *reinterpret_cast<const float4 *>(smem + rr * CS + cc);
-                if (SPLIT)
-                    *reinterpret_cast<float4 *>(p.partial + (int64_t(z) * p.M + row) * p.N + col) = v;
-                else
-                    store4<EPI>(p, row, col, v);
+        for (int it = 0; it < BM * C4 / 256; ++it) {
+            const int e = tid + it * 256, rr = e / C4, cc = (e - rr * C4) * 4;
+            const int row = m0 + rr, col = n0 + cc;
+            if (row >= p.M || col >= p.N) continue;  // N % 4 == 0: the whole float4 is inside
+            const float4 v = *reinterpret_cast<const float4 *>(smem + rr * CS + cc);
+            if (SPLIT) {
+                *reinterpret_cast<float4 *>(p.partial + (int64_t(z) * p.M + row) * p.N + col) = v;
+            } else {
+                const float4 y = store4<EPI>(p, row, col, v);
+                if (kGn && p.gnp) {
+                    gs.x += y.x, gs.y += y.y, gs.z += y.z, gs.w += y.w;
+                    gq.x = __builtin_fmaf(y.x, y.x, gq.x);
+                    gq.y = __builtin_fmaf(y.y, y.y, gq.y);
+                    gq.z = __builtin_fmaf(y.z, y.z, gq.z);
+                    gq.w = __builtin_fmaf(y.w, y.w, gq.w);
+                }
             }
+        }
+        if constexpr (kGn) {
+            if (p.gnp) gn_tile_partials<BM, BN>(p, smem, gs, gq, m0, n0);
         }
     } else {
         // One element per thread and pass; consecutive threads take consecutive
@@ -495,7 +548,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
     // the two row halves of a 32x32 block's store fall on different banks).
     constexpr int CS = BN + 8;
     constexpr int SMEM = 2 * (BM + BN) * LDS_S;
-    static_assert(BM * CS <= SMEM, "C tile must fit in the staging space");
+    static_assert(BM * CS <= SMEM && SMEM >= 2048, "C tile and GroupNorm sums must fit in the staging space");
     __shared__ float smem[SMEM];
     float(*As)[BM * LDS_S] = reinterpret_cast<float(*)[BM * LDS_S]>(smem);
     float(*Bs)[BN * LDS_S] = reinterpret_cast<float(*)[BN * LDS_S]>(smem + 2 * BM * LDS_S);
@@ -668,6 +721,19 @@ struct Plan {
     int bm, bn, splits, k_split;
 };
 
+// Keeps the GroupNorm partials request (GemmArgs::gnp) when a BM x BN tiling
+// without K split can honour it: one output, plain rows, 16-byte stores, a
+// fixed column quad per epilogue thread, tiles inside one item.
+inline void gn_partials_plan(GemmArgs &p, int bm, int bn, int splits, int batch) {
+    p.gn_rows = 0;
+    if (!p.gnp) return;
+    const bool ok = splits == 1 && batch == 1 && p.vec_out && p.nseg == 0 && p.rg <= 1 && 256 % (bn / 4) == 0 &&
+                    p.gn_item_rows > 0 && p.gn_item_rows % bm == 0 && p.M % p.gn_item_rows == 0 &&
+                    (reinterpret_cast<uintptr_t>(p.gnp) & 15) == 0;
+    if (ok) p.gn_rows = bm;
+    else p.gnp = nullptr;
+}
+
 // Tile shape and K split, from sweeps of every (tile, split) on MI355X over
 // the UNet's GEMM shapes (M 2..65536, N 4..6400, K 9..11520) and the VAE's
 // convs (M up to 262144, K 1152..4608):
@@ -680,7 +746,10 @@ struct Plan {
 //    fewer than four 32x32 tiles per CU; otherwise 32x32 tiles (16x16 MFMA),
 //    K split in up to 3 only under two tiles per CU with K >= 1024. Against
 //    64x64 tiles with up to 6 splits this takes 10-30% off the UNet's
-//    16x16- and 32x32-latent GEMMs (2048x640x640: 28.4 -> 19.7 us).
+//    16x16- and 32x32-latent GEMMs (2048x640x640: 28.4 -> 19.7 us). With eight
+//    32x32 tiles per CU or more, N % 64 == 0 and K < 1024, 32x64 tiles (half
+//    the workgroups, two 16x16 blocks per wave): 8192x320x320 21.9 -> 20.6 us
+//    (at K = 1280, 512x6400 with the SiLU epilogue, 32x64 is 5% slower).
 //  - Implicit-GEMM convs otherwise: 64x64 tiles, K split while the grid is under
 //    three times the CU count and each split keeps at least 8 K tiles.
 inline Plan plan_for(int M, int N, int K, int cus, bool dense) {
@@ -710,6 +779,7 @@ inline Plan plan_for(int M, int N, int K, int cus, bool dense) {
             const auto s = split(t32, 2 * int64_t(cus), 3);
             return Plan{32, 32, s.first, s.first > 1 ? s.second : K};
         }
+        if (t32 >= 8 * int64_t(cus) && N % 64 == 0 && K < 1024) return Plan{32, 64, 1, K};
         return Plan{32, 32, 1, K};
     }
     const auto s = split(t64, 3 * int64_t(cus), 6);
@@ -724,6 +794,7 @@ void launch_cfg(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int
         p.partial = static_cast<float *>(ctx.ws.get(bytes, ctx.stream));
         p.k_split = pl.k_split;
         p.vec_out = (p.N & 3) == 0 && (reinterpret_cast<uintptr_t>(p.partial) & 15) == 0;
+        gn_partials_plan(p, BM, BN, pl.splits, batch);
         dim3 grid(tiles, 1, pl.splits);
         gemm_f32_kernel<BM, BN, MODE, PRO, F16, BVEC, 0, true><<<grid, 256, 0, ctx.stream>>>(p);
         MH_LAUNCH_CHECK();
@@ -744,6 +815,7 @@ void launch_cfg(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int
     } else {
         p.k_split = p.K;
         p.vec_out = out_vec_ok(p);
+        gn_partials_plan(p, BM, BN, 1, batch);
         const dim3 grid(tiles, unsigned(batch));
         // The SiLU epilogue is only instantiated for dense operands (the convs never use it).
         if constexpr (MODE <= kDenseScalar) {
@@ -767,14 +839,27 @@ void launch_tiles(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
     // as MOEBIUS_GEMM selects the CPU engine's GEMM backend (src/engine/gemm.rs:57-60).
     if (const char *force = std::getenv("MOEBIUS_HIP_GEMM_PLAN")) {
         int bm = 0, bn = 0, sp = 0;
-        if (std::sscanf(force, "%d,%d,%d", &bm, &bn, &sp) == 3 && (bm == 32 || bm == 64 || bm == 128) &&
-            (bn == 32 || bn == 64 || bn == 128) && (bm == 32) == (bn == 32) && sp >= 1) {
+        const bool parsed = std::sscanf(force, "%d,%d,%d", &bm, &bn, &sp) == 3 && sp >= 1;
+        const bool square = (bm == 32 || bm == 64 || bm == 128) && (bn == 32 || bn == 64 || bn == 128) &&
+                            (bm == 32) == (bn == 32);
+        const bool wide = (bm == 32 && bn == 64) || (bm == 64 && bn == 32);
+        if (parsed && (square || (wide && MODE == kDense && BVEC))) {
             const int ktiles = int(ceil_div(p.K, BK));
             const int per = int(ceil_div(ktiles, sp));
             pl = Plan{bm, bn, int(ceil_div(ktiles, per)), per * BK};
         }
     }
     if (batch > 1) pl.splits = 1;
+    if constexpr (MODE == kDense && BVEC) {  // 32x64 / 64x32 tiles: vector dense operands only
+        if (pl.bm == 32 && pl.bn == 64) {
+            launch_cfg<32, 64, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
+            return;
+        }
+        if (pl.bm == 64 && pl.bn == 32) {
+            launch_cfg<64, 32, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
+            return;
+        }
+    }
     if constexpr (MODE <= kDenseScalar) {  // small tiles for the small dense GEMMs only
         if (pl.bm == 32) {
             launch_cfg<32, 32, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);

@@ -45,6 +45,21 @@ void group_norm_forward(Context &ctx, const float *x, int n, int h, int w, int c
                         int64_t add_ld = 0);
 void layer_norm(Context &ctx, const float *x, int64_t rows, int c, const float *gamma, const float *beta, float eps,
                 float *out);
+// GroupNorm statistics partials written by a producer's epilogue for the
+// GroupNorm that follows it: part [pixels / rows][c][2] = per tile of `rows`
+// pixels (inside one item of item_rows pixels) and channel, (sum y, sum y*y)
+// over the values written. The caller sets part (room for pixels / 32 tiles)
+// and item_rows; the producer sets rows (0: it wrote none).
+struct GnPartials {
+    float *part = nullptr;
+    int item_rows = 0;
+    int rows = 0;
+};
+// group_norm_affine from producer partials (rows > 0) of x alone; add, when
+// given, is folded in here (per partial, in f64) as it would be for x + add.
+void group_norm_affine_partials(Context &ctx, const float *part, int rows, int n, int hw, int c, int groups,
+                                float eps, const float *gamma, const float *beta, const float *add, float *scale,
+                                float *shift, int64_t add_ld = 0);
 // Per-row (mean, rstd) of LayerNorm for consumers that apply it themselves: stats [rows][2].
 void layer_norm_stats(Context &ctx, const float *x, int64_t rows, int c, float eps, float *stats);
 
@@ -61,10 +76,10 @@ struct ResidualAffine {
     bool silu = false;
     int rows_per_item = 0;
 };
-// out = ([res'] + bias) + x . W^T [SiLU] (+ residual2)
+// out = ([res'] + bias) + x . W^T [SiLU] (+ residual2); gn (optional): GroupNorm partials of out.
 void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void *weight, WeightType wt, int c_out,
              const float *bias, const float *residual, float *out, GemmEpilogue epi = GemmEpilogue::None,
-             const ResidualAffine *raff = nullptr, const float *residual2 = nullptr);
+             const ResidualAffine *raff = nullptr, const float *residual2 = nullptr, GnPartials *gn = nullptr);
 // residual2 (optional, [n, ho, wo, c_out]) is added last: out = (bias + conv) + residual2.
 void conv3x3(Context &ctx, const float *x, int n, int h, int w, int c_in, const void *weight, WeightType wt,
              int c_out, const float *bias, int stride, const int pad[4], bool upsample2x, const Affine *prologue,

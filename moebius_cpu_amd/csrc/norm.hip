@@ -97,9 +97,11 @@ __global__ __launch_bounds__(256) void gn_partial_kernel(const float *__restrict
 }
 
 // One block per (group, item): f64 fold of the group's partials, then scale/shift.
+// part_rows > 0: the partials are of x alone, part_rows pixels each, and add
+// is folded in per partial: sum (y + t) = S + r t, sum (y + t)^2 = Q + 2 t S + r t^2.
 __global__ __launch_bounds__(256) void gn_finalize_kernel(const float *__restrict__ part, const float *__restrict__ add,
                                                           int64_t add_ld, int hw, int c, int nchunks, int groups,
-                                                          float eps,
+                                                          int part_rows, float eps,
                                                           const float *__restrict__ gamma,
                                                           const float *__restrict__ beta, float *__restrict__ scale,
                                                           float *__restrict__ shift) {
@@ -111,8 +113,14 @@ __global__ __launch_bounds__(256) void gn_finalize_kernel(const float *__restric
     for (int i = threadIdx.x; i < total; i += 256) {
         const int ch = i / cg, j = i - ch * cg;
         const float2 e = *reinterpret_cast<const float2 *>(pb + (size_t(ch) * c + j) * 2);
-        ds += double(e.x);
-        dq += double(e.y);
+        if (part_rows > 0 && add) {
+            const double t = double(add[size_t(b) * add_ld + size_t(g) * cg + j]), r = double(part_rows);
+            ds += double(e.x) + r * t;
+            dq += double(e.y) + 2.0 * t * double(e.x) + r * t * t;
+        } else {
+            ds += double(e.x);
+            dq += double(e.y);
+        }
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -324,8 +332,20 @@ void group_norm_affine(Context &ctx, const float *x, int n, int h, int w, int c,
     gn_partial_kernel<<<dim3(nchunks, nctiles, n), 256, 0, ctx.stream>>>(x, add, add_ld, hw, c, chunk_px, nchunks,
                                                                         part);
     MH_LAUNCH_CHECK();
-    gn_finalize_kernel<<<dim3(groups, n), 256, 0, ctx.stream>>>(part, add, add_ld, hw, c, nchunks, groups, eps, gamma,
-                                                                beta, scale, shift);
+    gn_finalize_kernel<<<dim3(groups, n), 256, 0, ctx.stream>>>(part, add, add_ld, hw, c, nchunks, groups, 0, eps,
+                                                                gamma, beta, scale, shift);
+    MH_LAUNCH_CHECK();
+}
+
+void group_norm_affine_partials(Context &ctx, const float *part, int rows, int n, int hw, int c, int groups,
+                                float eps, const float *gamma, const float *beta, const float *add, float *scale,
+                                float *shift, int64_t add_ld) {
+    if (add_ld <= 0) add_ld = c;
+    MH_REQUIRE(groups > 0 && c % groups == 0, "channels not divisible by groups");
+    MH_REQUIRE(n > 0 && hw > 0 && rows > 0 && hw % rows == 0, "GroupNorm partials: tiles must divide the item");
+    MH_REQUIRE(aligned16(part), "GroupNorm partials must be 16-byte aligned");
+    gn_finalize_kernel<<<dim3(groups, n), 256, 0, ctx.stream>>>(part, add, add_ld, hw, c, hw / rows, groups, rows,
+                                                                eps, gamma, beta, scale, shift);
     MH_LAUNCH_CHECK();
 }
 

@@ -30,34 +30,27 @@ Pool::~Pool() {
     for (auto &b : bufs_) (void)hipFree(b.p);
 }
 
+// The idle buffer with the least capacity that holds `count` floats (later
+// entries win ties), else a new buffer. The reference's Scratch grows its
+// largest idle buffer in place (best_fit, src/engine/mod.rs:104-117); on the
+// device that takes a stream synchronisation and a hipFree, which stalled the
+// host for 0.3-0.6 ms per growth for several steps, so buffers are never grown
+// or freed here: the set only gains buffers until the step's pattern of sizes
+// is covered, after which no step allocates.
 float *Pool::floats(int64_t count) {
     const uint64_t len = uint64_t(count > 0 ? count : 1);
-    std::vector<uint64_t> lens, caps;
-    std::vector<size_t> idx;
-    for (size_t i = 0; i < bufs_.size(); ++i) {
-        if (bufs_[i].used) continue;
-        lens.push_back(bufs_[i].len);
-        caps.push_back(bufs_[i].cap);
-        idx.push_back(i);
-    }
-    const int64_t pick = best_fit(lens.data(), caps.data(), int64_t(lens.size()), len);
-    if (pick >= 0) {
-        Buf &b = bufs_[idx[size_t(pick)]];
-        if (b.cap < len) {
-            // Grow: queued kernels may still use the old block.
-            HIP_CHECK(hipStreamSynchronize(ctx_.stream));
-            HIP_CHECK(hipFree(b.p));
-            b.p = nullptr;
-            HIP_CHECK(hipMalloc(&b.p, len * sizeof(float)));
-            b.cap = len;
-        }
-        b.len = len;
-        b.used = true;
-        return b.p;
+    Buf *best = nullptr;
+    for (auto &b : bufs_)
+        if (!b.used && b.cap >= len && (!best || b.cap <= best->cap)) best = &b;
+    if (best) {
+        best->len = len;
+        best->used = true;
+        return best->p;
     }
     Buf b{nullptr, len, len, true};
     HIP_CHECK(hipMalloc(&b.p, len * sizeof(float)));
     bufs_.push_back(b);
+    ++allocations_;
     return b.p;
 }
 

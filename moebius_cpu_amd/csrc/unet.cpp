@@ -125,6 +125,24 @@ struct Env {
     Pool &pool;
 };
 
+// GroupNorm partials request for a producer writing a [x.n, x.h, x.w, c] tensor.
+GnPartials gn_request(Env &e, const DT &x, int c) {
+    GnPartials gp;
+    gp.part = e.pool.floats(ceil_div(x.px(), 32) * c * 2);
+    gp.item_rows = x.h * x.w;
+    return gp;
+}
+
+// Attaches the partials the producer wrote to its output, or returns the buffer.
+void gn_attach(Env &e, DT &out, const GnPartials &gp) {
+    if (gp.rows > 0) {
+        out.gn = gp.part;
+        out.gn_rows = gp.rows;
+    } else {
+        e.pool.recycle(gp.part);
+    }
+}
+
 struct Lin {  // Conv1x1 (src/engine/conv.rs:28-55)
     int ci = 0, co = 0;
     DParam w;
@@ -143,6 +161,16 @@ struct Lin {  // Conv1x1 (src/engine/conv.rs:28-55)
         fwd(e, x.p, x.px(), out.p, res ? res->p : nullptr, epi);
         return out;
     }
+    // The same, with the GroupNorm partials of the output attached for the
+    // GroupNorm that reads it next.
+    DT fwd_gnp(Env &e, const DT &x, const DT *res = nullptr) const {
+        DT out = e.pool.tensor(x.n, x.h, x.w, co);
+        GnPartials gp = gn_request(e, x, co);
+        conv1x1(e.ctx, x.p, x.px(), ci, w.p, w.wt, co, b, res ? res->p : nullptr, out.p, GemmEpilogue::None, nullptr,
+                nullptr, &gp);
+        gn_attach(e, out, gp);
+        return out;
+    }
 };
 
 struct GN {
@@ -156,14 +184,25 @@ struct GN {
     }
     DT fwd(Env &e, const DT &x, const float *add, bool silu, int64_t add_ld = 0) const {
         DT out = e.pool.tensor(x.n, x.h, x.w, x.c);
-        group_norm_forward(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, eps, g, b, add, silu, out.p, add_ld);
+        if (x.gn) {
+            float *ss = affine(e, x, add, add_ld);
+            apply_affine(e.ctx, x.p, x.n, x.h, x.w, x.c, ss, ss + int64_t(x.n) * x.c, silu, out.p);
+            e.pool.recycle(ss);
+        } else {
+            group_norm_forward(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, eps, g, b, add, silu, out.p, add_ld);
+        }
         return out;
     }
-    // Statistics only: [scale | shift], each [n * c], for a consumer that applies them.
+    // Statistics only: [scale | shift], each [n * c], for a consumer that
+    // applies them; from the producer's partials when x carries them.
     float *affine(Env &e, const DT &x, const float *add, int64_t add_ld = 0) const {
         float *ss = e.pool.floats(int64_t(2) * x.n * x.c);
-        group_norm_affine(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, eps, g, b, add, ss, ss + int64_t(x.n) * x.c,
-                          add_ld);
+        if (x.gn)
+            group_norm_affine_partials(e.ctx, x.gn, x.gn_rows, x.n, x.h * x.w, x.c, GROUPS, eps, g, b, add, ss,
+                                       ss + int64_t(x.n) * x.c, add_ld);
+        else
+            group_norm_affine(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, eps, g, b, add, ss, ss + int64_t(x.n) * x.c,
+                              add_ld);
         return ss;
     }
 };
@@ -209,8 +248,10 @@ struct DwConv2d {
     // the affine as it stages its input, and the identity residual (c_in ==
     // c_out) is a transformed in the pointwise conv's epilogue. Every value is
     // computed as the separate apply pass would (fma, then SiLU), so the result
-    // is bit-identical to fwd(apply(x)).
-    DT fwd_gn(Env &e, const DT &x, const float *ss, const float *res2 = nullptr, float *out_p = nullptr) const {
+    // is bit-identical to fwd(apply(x)). gn_out: attach the output's GroupNorm
+    // partials (for the GroupNorm that reads it next).
+    DT fwd_gn(Env &e, const DT &x, const float *ss, const float *res2 = nullptr, float *out_p = nullptr,
+              bool gn_out = false) const {
         Affine aff;
         aff.scale = ss;
         aff.shift = ss + int64_t(x.n) * x.c;
@@ -223,8 +264,11 @@ struct DwConv2d {
         ra.shift = aff.shift;
         ra.silu = true;
         ra.rows_per_item = x.h * x.w;
+        GnPartials gp;
+        if (gn_out) gp = gn_request(e, x, co);
         conv1x1(e.ctx, mid.p, mid.px(), ci, pw.w.p, pw.w.wt, co, pw.b, ci == co ? x.p : nullptr, out.p,
-                GemmEpilogue::None, ci == co ? &ra : nullptr, res2);
+                GemmEpilogue::None, ci == co ? &ra : nullptr, res2, gn_out ? &gp : nullptr);
+        if (gn_out) gn_attach(e, out, gp);
         e.pool.recycle(mid);
         return out;
     }
@@ -257,12 +301,12 @@ struct DwResnet {
     // epilogue. The shortcut (or x) is added in conv2's pointwise epilogue.
     DT fwd(Env &e, const DT &x, const float *tp, int64_t tp_ld) const {
         float *ss1 = norm1.affine(e, x, nullptr);
-        DT b = conv1.fwd_gn(e, x, ss1);
+        DT b = conv1.fwd_gn(e, x, ss1, nullptr, nullptr, true);
         e.pool.recycle(ss1);
         float *ss2 = norm2.affine(e, b, tp, tp_ld);
         DT s;
         if (has_shortcut) s = shortcut.fwd(e, x);
-        DT out = conv2.fwd_gn(e, b, ss2, has_shortcut ? s.p : x.p);
+        DT out = conv2.fwd_gn(e, b, ss2, has_shortcut ? s.p : x.p, nullptr, true);
         if (has_shortcut) e.pool.recycle(s);
         e.pool.recycle(ss2);
         e.pool.recycle(b);
@@ -454,7 +498,7 @@ struct MixTransformer {
         DT u = point.fwd(e, g, &h);
         e.pool.recycle(g);
         e.pool.recycle(h);
-        DT out = proj_out.fwd(e, u, &x);
+        DT out = proj_out.fwd_gnp(e, u, &x);
         e.pool.recycle(u);
         return out;
     }

@@ -221,6 +221,18 @@ def test_unet_step_is_deterministic_and_batch_consistent(ctx, gnet):
     assert max_abs_rel(c[0], a[1]) <= TOL  # the cond item of a CFG step is the cond-only step
 
 
+def test_unet_pool_stops_allocating(ctx, gnet):
+    """Once the activation pool covers a step's buffer roles, steps allocate nothing
+    (a device allocation or growth mid-step would stall the host)."""
+    inp = U.unet_input(seed=5006)
+    for _ in range(2):
+        gnet.forward_host(inp.x, inp.timestep, cfg=True)
+    _, held = gnet.memory()
+    for _ in range(2):
+        gnet.forward_host(inp.x, inp.timestep, cfg=True)
+        assert gnet.memory()[1] == held
+
+
 def test_unet_f16_stored_weights(ctx, params, onet):
     """f16-stored GEMM weights, f32 arithmetic: equals the f32 path on the rounded weights."""
     p16 = {k: v for k, v in params.items()}

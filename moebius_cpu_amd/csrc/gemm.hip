@@ -79,7 +79,7 @@ __global__ void mfma_probe_kernel(const float *a, const float *b, float *d) {
 
 void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void *weight, WeightType wt, int c_out,
              const float *bias, const float *residual, float *out, GemmEpilogue epi, const ResidualAffine *raff,
-             const float *residual2, GnPartials *gn) {
+             const float *residual2, GnPartials *gn, const ResidualAffine *x_aff) {
     MH_REQUIRE(c_in > 0 && c_out > 0, "Conv1x1: empty channel axis");
     MH_REQUIRE(pixels < (int64_t(1) << 31), "Conv1x1: too many pixels");
     if (raff) {
@@ -112,10 +112,23 @@ void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void 
         p.gnp = gn->part;
         p.gn_item_rows = gn->item_rows;
     }
-    if (c_in % 4 == 0 && aligned16(x))
+    if (x_aff) {
+        MH_REQUIRE(x_aff->scale && x_aff->shift && x_aff->rows_per_item > 0,
+                   "Conv1x1: input affine needs scale, shift and rows per item");
+        MH_REQUIRE(c_in % 4 == 0 && aligned16(x) && aligned16(x_aff->scale) && aligned16(x_aff->shift) &&
+                       (reinterpret_cast<uintptr_t>(weight) % (wt == kF16 ? 8 : 16)) == 0,
+                   "Conv1x1: input affine needs 4-channel aligned rows");
+        p.psc = x_aff->scale;
+        p.psh = x_aff->shift;
+        p.psilu = x_aff->silu ? 1 : 0;
+        p.pro_rows = x_aff->rows_per_item;
+        if (ctx.precision == Precision::Fast) launch_dense_pro_h16(ctx, p, wt, epi);
+        else launch_dense_pro(ctx, p, wt, epi);
+    } else if (c_in % 4 == 0 && aligned16(x)) {
         run_dense(ctx, p, wt, epi, 1, true);
-    else
+    } else {
         run_dense(ctx, p, wt, epi, 1, false);
+    }
     if (gn) gn->rows = p.gn_rows;
 }
 

@@ -24,6 +24,7 @@ typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 
 // Launchers of the fast kernels (gemm_fast_dense.hip, gemm_fast_conv.hip).
 void launch_dense_h16(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi, int batch, bool vec);
+void launch_dense_pro_h16(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi);
 void launch_conv_h16(Context &ctx, GemmArgs &p, WeightType wt, int mode, bool pro);
 
 namespace {
@@ -62,7 +63,9 @@ __device__ __forceinline__ floatx4 load_a_h(const GemmArgs &p, __amdgpu_buffer_r
                                             int k, int k_end, int tky, int tkx, int tci, int k0) {
     if constexpr (MODE == kDense) {
         const bool ok = m < p.M && k < k_end;
-        return buf_load4(ar, ok ? int((int64_t(m) * p.lda + k) * 4) : kOob);
+        const floatx4 v = buf_load4(ar, ok ? int((int64_t(m) * p.lda + k) * 4) : kOob);
+        if constexpr (PRO) return dense_prologue(p, r.b, k, ok, v);
+        return v;
     } else if constexpr (MODE == kConvAligned || MODE == kConvVec) {
         int ky, kx, c;
         if constexpr (MODE == kConvAligned) {
@@ -147,6 +150,7 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
         if (MODE >= kConvAligned) crow[i] = conv_row(p, m0 + lrow + 16 * i);
+        else if (PRO) crow[i] = ConvRow{min(m0 + lrow + 16 * i, p.M - 1) / p.pro_rows, 0, 0, true};
         else crow[i] = ConvRow{0, 0, 0, true};
     }
 

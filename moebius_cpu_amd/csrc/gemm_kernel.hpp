@@ -102,6 +102,8 @@ struct GemmArgs {
     // rows per partial in gn_rows (0: none written).
     float *gnp;
     int gn_item_rows, gn_rows;
+    // dense operands with the prologue (psc/psh [items][K]): rows per item
+    int pro_rows;
 };
 
 // (residual [transformed] + bias) + acc [SiLU] (+ res2): the reference's
@@ -128,6 +130,8 @@ __device__ __forceinline__ float epilogue_value(const GemmArgs &p, int row, int 
 
 // Launchers, one per A-operand family (gemm_dense.hip, gemm_conv.hip).
 void launch_dense(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi, int batch, bool vec);
+// Dense operands with the GroupNorm prologue (K-contiguous vector rows, no batch).
+void launch_dense_pro(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi);
 void launch_conv(Context &ctx, GemmArgs &p, WeightType wt, int mode, bool pro);
 
 namespace {
@@ -324,12 +328,32 @@ __device__ __forceinline__ floatx4 buf_load4(__amdgpu_buffer_rsrc_t r, int off) 
     return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
+// Prologue of a dense A operand: the consumer-side GroupNorm affine
+// [SiLU](x . scale + shift) of row item b (r.b = row / pro_rows), channels
+// k..k+3 (psc/psh [items][K], K % 4 == 0, 16-byte aligned), computed as the
+// separate apply pass does; zero where the load was out of range.
+__device__ __forceinline__ floatx4 dense_prologue(const GemmArgs &p, int b, int k, bool ok, floatx4 v) {
+    const int64_t i = int64_t(b) * p.K + (ok ? k : 0);
+    const float4 sc = *reinterpret_cast<const float4 *>(p.psc + i);
+    const float4 sh = *reinterpret_cast<const float4 *>(p.psh + i);
+    const float s4[4] = {sc.x, sc.y, sc.z, sc.w}, h4[4] = {sh.x, sh.y, sh.z, sh.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float y = __builtin_fmaf(v[e], s4[e], h4[e]);
+        if (p.psilu) y = ref_silu(y);
+        v[e] = ok ? y : 0.0f;
+    }
+    return v;
+}
+
 template <int MODE, bool PRO>
 __device__ __forceinline__ floatx4 load_a_buf(const GemmArgs &p, __amdgpu_buffer_rsrc_t ar, const ConvRow &r, int m,
                                               int k, int k_end, int tap_ky, int tap_kx, int tap_ci0) {
     if constexpr (MODE == kDense) {
         const bool ok = m < p.M && k < k_end;
-        return buf_load4(ar, ok ? int((int64_t(m) * p.lda + k) * 4) : kOob);
+        const floatx4 v = buf_load4(ar, ok ? int((int64_t(m) * p.lda + k) * 4) : kOob);
+        if constexpr (PRO) return dense_prologue(p, r.b, k, ok, v);
+        return v;
     } else {
         int ky, kx, c;
         if constexpr (MODE == kConvAligned) {
@@ -565,6 +589,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
         if (MODE >= kConvAligned) crow[i] = conv_row(p, m0 + lrow + 32 * i);
+        else if (PRO) crow[i] = ConvRow{min(m0 + lrow + 32 * i, p.M - 1) / p.pro_rows, 0, 0, true};
         else crow[i] = ConvRow{0, 0, 0, true};
     }
 

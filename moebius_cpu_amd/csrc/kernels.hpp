@@ -76,10 +76,13 @@ struct ResidualAffine {
     bool silu = false;
     int rows_per_item = 0;
 };
-// out = ([res'] + bias) + x . W^T [SiLU] (+ residual2); gn (optional): GroupNorm partials of out.
+// out = ([res'] + bias) + x' . W^T [SiLU] (+ residual2); gn (optional): GroupNorm partials of out.
+// x_aff (optional): x' = [SiLU](x . scale + shift) per item (pixel / rows_per_item) and
+// channel, applied as x loads (a GroupNorm's output without it being written); else x' = x.
 void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void *weight, WeightType wt, int c_out,
              const float *bias, const float *residual, float *out, GemmEpilogue epi = GemmEpilogue::None,
-             const ResidualAffine *raff = nullptr, const float *residual2 = nullptr, GnPartials *gn = nullptr);
+             const ResidualAffine *raff = nullptr, const float *residual2 = nullptr, GnPartials *gn = nullptr,
+             const ResidualAffine *x_aff = nullptr);
 // residual2 (optional, [n, ho, wo, c_out]) is added last: out = (bias + conv) + residual2.
 void conv3x3(Context &ctx, const float *x, int n, int h, int w, int c_in, const void *weight, WeightType wt,
              int c_out, const float *bias, int stride, const int pad[4], bool upsample2x, const Affine *prologue,

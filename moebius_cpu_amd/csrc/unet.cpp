@@ -161,6 +161,20 @@ struct Lin {  // Conv1x1 (src/engine/conv.rs:28-55)
         fwd(e, x.p, x.px(), out.p, res ? res->p : nullptr, epi);
         return out;
     }
+    // The same of GroupNorm(x) given its affine (ss = [scale | shift] per item
+    // and channel, no SiLU), applied as x loads: the normalised tensor is not
+    // written, and every value is the one the apply pass would write.
+    DT fwd_gn_in(Env &e, const DT &x, const float *ss) const {
+        DT out = e.pool.tensor(x.n, x.h, x.w, co);
+        ResidualAffine xa;
+        xa.scale = ss;
+        xa.shift = ss + int64_t(x.n) * x.c;
+        xa.silu = false;
+        xa.rows_per_item = x.h * x.w;
+        conv1x1(e.ctx, x.p, x.px(), ci, w.p, w.wt, co, b, nullptr, out.p, GemmEpilogue::None, nullptr, nullptr,
+                nullptr, &xa);
+        return out;
+    }
     // The same, with the GroupNorm partials of the output attached for the
     // GroupNorm that reads it next.
     DT fwd_gnp(Env &e, const DT &x, const DT *res = nullptr) const {
@@ -479,10 +493,24 @@ struct MixTransformer {
         attn2.release();
     }
     DT fwd(Env &e, const DT &x, int br0) const {
-        DT t = norm.fwd(e, x, nullptr, false);
-        DT h = proj_in.fwd(e, t);
-        e.pool.recycle(t);
-        t = ln1.fwd(e, h);
+        // The GroupNorm affine goes into proj_in's operand loads up to 640 channels
+        // (EXACT) / 320 (FAST): the loads cost per K tile, and at 1280 channels
+        // (and 640 in FAST) they cost more than the separate apply pass (whole
+        // steps: EXACT 7.764 ms unfused, 7.728 to 640, 7.773 to 1280; FAST 5.744,
+        // 5.731 to 320, 5.778 to 640).
+        DT h;
+        const char *mc = std::getenv("MOEBIUS_HIP_GN_IN_MAXC");  // tuning override, read per call
+        const int max_c = mc ? std::atoi(mc) : (e.ctx.precision == Precision::Fast ? 320 : 640);
+        if (x.c <= max_c) {
+            float *ss = norm.affine(e, x, nullptr);
+            h = proj_in.fwd_gn_in(e, x, ss);
+            e.pool.recycle(ss);
+        } else {
+            DT t = norm.fwd(e, x, nullptr, false);
+            h = proj_in.fwd(e, t);
+            e.pool.recycle(t);
+        }
+        DT t = ln1.fwd(e, h);
         attn1.fwd_add(e, t, h.p);
         e.pool.recycle(t);
         t = ln2.fwd(e, h);

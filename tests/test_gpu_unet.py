@@ -221,6 +221,22 @@ def test_unet_step_is_deterministic_and_batch_consistent(ctx, gnet):
     assert max_abs_rel(c[0], a[1]) <= TOL  # the cond item of a CFG step is the cond-only step
 
 
+@pytest.mark.parametrize("fast", [False, True])
+def test_unet_groupnorm_into_proj_in_is_bit_exact(ctx, gnet, fast, monkeypatch):
+    """The transformers' GroupNorm applied inside proj_in's operand loads gives the
+    bits of the separate apply pass, at every channel count it is used for."""
+    inp = U.unet_input(seed=5007)
+    ctx.set_precision(fast)
+    try:
+        monkeypatch.setenv("MOEBIUS_HIP_GN_IN_MAXC", "0")
+        apart = gnet.forward_host(inp.x, inp.timestep, cfg=True)
+        monkeypatch.setenv("MOEBIUS_HIP_GN_IN_MAXC", "1280")
+        fused = gnet.forward_host(inp.x, inp.timestep, cfg=True)
+    finally:
+        ctx.set_precision(False)
+    assert np.array_equal(apart, fused)
+
+
 def test_unet_pool_stops_allocating(ctx, gnet):
     """Once the activation pool covers a step's buffer roles, steps allocate nothing
     (a device allocation or growth mid-step would stall the host)."""

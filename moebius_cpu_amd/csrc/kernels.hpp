@@ -122,10 +122,18 @@ void selftest_mfma_f32(Context &ctx, const float *a_host, const float *b_host, f
 // keys [nb][rows][k], v [nb][rows][vd] -> lambda_t [nb][vd][k] (transposed lambda_c).
 void softmax_lambda(Context &ctx, const float *keys, const float *v, int nb, int rows, int k, int vd,
                     float *lambda_t);
+// LayerNorm of a kernel's output rows written beside them (src/engine/norm.rs:151-173):
+// out [rows][c] = (y - mean) * rstd * gamma + beta.
+struct LayerNormOut {
+    const float *gamma = nullptr, *beta = nullptr;
+    float eps = 0.f;
+    float *out = nullptr;
+};
 // out [nb*hh*ww][8*vd] = (residual +) (yc + bias tap + 15x15 taps of v); a_t [nb*hh*ww][226][8]
-// (heads innermost). out may alias yc or residual.
+// (heads innermost). out may alias yc or residual. lno (optional): also the LayerNorm
+// of the out rows.
 void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc, const float *residual, float *out,
-                int nb, int hh, int ww, int vd);
+                int nb, int hh, int ww, int vd, const LayerNormOut *lno = nullptr);
 // out [nb*hw][8*k] = (residual +) (yc + (q . E) . V[branch]); e [hw][10][k]; v_branches [2][10][k].
 // out may alias yc or residual.
 void position_term(Context &ctx, const float *q, const float *e, const float *v_branches, int br0, int nb, int hw,

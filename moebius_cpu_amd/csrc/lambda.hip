@@ -165,6 +165,58 @@ __global__ __launch_bounds__(256) void lambda_finalize_kernel(const float *__res
     }
 }
 
+// LayerNorm of the rows a kernel has just written, for kernels whose block
+// holds whole pixel rows (src/engine/norm.rs:151-173: mean, then the mean of
+// squared deviations, rstd = 1 / sqrt(var + eps), y = (v - mean) * rstd * g + b):
+// thread t of a pixel holds HG float4 of the row; the per_px threads' sums are
+// added in thread order through LDS, so the statistics are deterministic.
+struct LnOut {
+    const float *gamma = nullptr, *beta = nullptr;
+    float eps = 0.f;
+    float *out = nullptr;  // [pixels][c]
+};
+
+template <int HG>
+__device__ __forceinline__ void ln_pixel_rows(const LnOut &ln, const float4 (&u)[HG], bool active, float *red, int p,
+                                              int per_px, int c, int64_t pix, int hg, int jq, int k4) {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < HG; ++i) s += (u[i].x + u[i].y) + (u[i].z + u[i].w);
+    red[threadIdx.x] = active ? s : 0.f;
+    __syncthreads();
+    float tot = 0.f;
+    if (active)
+        for (int j = 0; j < per_px; ++j) tot += red[p * per_px + j];
+    const float mean = tot / float(c);
+    __syncthreads();  // every sum is read before the squares overwrite it
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < HG; ++i) {
+        const float a = u[i].x - mean, b = u[i].y - mean, cc = u[i].z - mean, d = u[i].w - mean;
+        q += (a * a + b * b) + (cc * cc + d * d);
+    }
+    red[threadIdx.x] = active ? q : 0.f;
+    __syncthreads();
+    if (!active) return;  // no barrier follows
+    float vs = 0.f;
+    for (int j = 0; j < per_px; ++j) vs += red[p * per_px + j];
+    const float rstd = 1.0f / sqrtf(vs / float(c) + ln.eps);
+    const float4 *g4 = reinterpret_cast<const float4 *>(ln.gamma);
+    const float4 *b4 = reinterpret_cast<const float4 *>(ln.beta);
+    float4 *o4 = reinterpret_cast<float4 *>(ln.out);
+#pragma unroll
+    for (int i = 0; i < HG; ++i) {
+        const int q4 = (hg * HG + i) * k4 + jq;
+        const float4 g = g4[q4], bb = b4[q4];
+        float4 y;
+        y.x = __builtin_fmaf((u[i].x - mean) * rstd, g.x, bb.x);
+        y.y = __builtin_fmaf((u[i].y - mean) * rstd, g.y, bb.y);
+        y.z = __builtin_fmaf((u[i].z - mean) * rstd, g.z, bb.z);
+        y.w = __builtin_fmaf((u[i].w - mean) * rstd, g.w, bb.w);
+        o4[pix * (kHeads * k4) + q4] = y;
+    }
+}
+
 // HG heads' coefficients of one tap: a_t row [226][8] (heads innermost).
 template <int HG>
 __device__ __forceinline__ void load_heads(const float *__restrict__ p, float (&c)[HG]) {
@@ -188,15 +240,19 @@ __device__ __forceinline__ void load_heads(const float *__restrict__ p, float (&
 // or two 16-byte loads from the tap-major a_t. Per output element the
 // operations are the reference's: (yc + bias) then one fused multiply-add per
 // in-image tap in (dy, dx) order; then residual + u when a residual is given.
-template <int HG>
+template <int HG, bool LN>
 __global__ __launch_bounds__(256) void tap_filter_kernel(const float *__restrict__ a_t, const float *__restrict__ v,
                                                          const float *yc, const float *res, float *out, int nb,
-                                                         int hh, int ww, int vd) {
+                                                         int hh, int ww, int vd, LnOut ln) {
     constexpr int NG = kHeads / HG;
     const int v4 = vd >> 2;
     const int64_t total = int64_t(nb) * hh * ww * NG * v4;
-    const int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (t >= total) return;
+    const int64_t t0 = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const bool active = t0 < total;
+    // With the LayerNorm a block is whole pixels (blockDim a multiple of the
+    // pixel's threads) and every thread stays for its barriers.
+    if (!LN && !active) return;
+    const int64_t t = active ? t0 : 0;
     const int jq = int(t % v4);
     const int64_t r = t / v4;
     const int hg = int(r % NG);
@@ -250,12 +306,16 @@ __global__ __launch_bounds__(256) void tap_filter_kernel(const float *__restrict
     float4 *o4 = reinterpret_cast<float4 *>(out);
 #pragma unroll
     for (int i = 0; i < HG; ++i) {
-        float4 u = acc[i];
         if (res) {
             const float4 h = reinterpret_cast<const float4 *>(res)[obase + i * v4];
-            u = make_float4(h.x + u.x, h.y + u.y, h.z + u.z, h.w + u.w);
+            acc[i] = make_float4(h.x + acc[i].x, h.y + acc[i].y, h.z + acc[i].z, h.w + acc[i].w);
         }
-        o4[obase + i * v4] = u;
+        if (active) o4[obase + i * v4] = acc[i];
+    }
+    if constexpr (LN) {
+        extern __shared__ float red[];  // [blockDim.x]
+        const int tpp = NG * v4;
+        ln_pixel_rows<HG>(ln, acc, active, red, int(threadIdx.x) / tpp, tpp, kHeads * vd, pix, hg, jq, v4);
     }
 }
 
@@ -266,11 +326,11 @@ __global__ __launch_bounds__(256) void tap_filter_kernel(const float *__restrict
 // loads (double-buffered, one barrier per row), so the inner loop reads LDS
 // only and every value and coefficient leaves HBM/L2 once per block. Per output
 // element the operations are tap_filter_kernel's (the reference's order).
-template <int HG>
+template <int HG, bool LN>
 __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__restrict__ a_t,
                                                               const float *__restrict__ v, const float *yc,
                                                               const float *res, float *out, int hh, int ww, int vd,
-                                                              int tx) {
+                                                              int tx, LnOut ln) {
     extern __shared__ float4 sh4[];
     constexpr int kRowC4 = kWin * kHeads / 4;  // float4 of coefficients per pixel and tap row: 30
     constexpr int NG = kHeads / HG;
@@ -354,13 +414,16 @@ __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__res
         const float4 *res4 = reinterpret_cast<const float4 *>(res);
 #pragma unroll
         for (int i = 0; i < HG; ++i) {
-            float4 u = acc[i];
             if (res) {
                 const float4 h = res4[o4 + i * v4];
-                u = make_float4(h.x + u.x, h.y + u.y, h.z + u.z, h.w + u.w);
+                acc[i] = make_float4(h.x + acc[i].x, h.y + acc[i].y, h.z + acc[i].z, h.w + acc[i].w);
             }
-            out4[o4 + i * v4] = u;
+            out4[o4 + i * v4] = acc[i];
         }
+    }
+    if constexpr (LN) {
+        float *red = reinterpret_cast<float *>(cls + 2 * tx * kRowC4);  // [blockDim.x]
+        ln_pixel_rows<HG>(ln, acc, active, red, xl, tpp, kHeads * vd, pix, hg, jq, v4);
     }
 }
 
@@ -596,12 +659,22 @@ void softmax_lambda(Context &ctx, const float *keys, const float *v, int nb, int
 }
 
 void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc, const float *residual, float *out,
-                int nb, int hh, int ww, int vd) {
+                int nb, int hh, int ww, int vd, const LayerNormOut *lno) {
     MH_REQUIRE(vd % 4 == 0, "tap_filter: value width must be a multiple of 4");
     MH_REQUIRE(aligned16(a_t) && aligned16(v) && aligned16(yc) && aligned16(residual) && aligned16(out),
                "tap_filter: buffers must be 16-byte aligned");
     const int64_t pix = int64_t(nb) * hh * ww;
     if (pix == 0) return;
+    LnOut ln;
+    if (lno) {
+        MH_REQUIRE(lno->gamma && lno->beta && lno->out && aligned16(lno->gamma) && aligned16(lno->beta) &&
+                       aligned16(lno->out) && lno->out != out && lno->out != residual && lno->out != yc,
+                   "tap_filter: LayerNorm output needs aligned gamma, beta and a separate output");
+        ln.gamma = lno->gamma;
+        ln.beta = lno->beta;
+        ln.eps = lno->eps;
+        ln.out = lno->out;
+    }
     // Heads per thread: the most (value loads shared by more heads) that still
     // gives the chip about 2048 waves: 4 at 64x64 x 40 channels, 2 at 32x32 x 80,
     // 1 at 16x16 x 160 (batch 2).
@@ -618,14 +691,15 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
     if (force && force[0] == 't') tile_hg = std::atoi(force + 1) == 4 ? 4 : 8;
     if (tile_hg && (kHeads / tile_hg) * v4 <= 256) {
         const int tpp = (kHeads / tile_hg) * v4, tx = std::max(1, std::min(256 / tpp, ww));
-        const size_t lds = (size_t(2) * (tx + kWin - 1) * v4 + size_t(2) * tx * (kWin * kHeads / 4)) * 16;
+        const size_t lds = (size_t(2) * (tx + kWin - 1) * v4 + size_t(2) * tx * (kWin * kHeads / 4)) * 16 +
+                           (lno ? size_t(tx) * tpp * sizeof(float) : 0);
         const int64_t blocks = int64_t(nb) * hh * ceil_div(ww, tx);
-        if (tile_hg == 8)
-            tap_filter_tile_kernel<8><<<unsigned(blocks), unsigned(tx * tpp), lds, ctx.stream>>>(
-                a_t, v, yc, residual, out, hh, ww, vd, tx);
-        else
-            tap_filter_tile_kernel<4><<<unsigned(blocks), unsigned(tx * tpp), lds, ctx.stream>>>(
-                a_t, v, yc, residual, out, hh, ww, vd, tx);
+        auto go = [&](auto kern) {
+            kern<<<unsigned(blocks), unsigned(tx * tpp), lds, ctx.stream>>>(a_t, v, yc, residual, out, hh, ww, vd, tx,
+                                                                           ln);
+        };
+        if (tile_hg == 8) lno ? go(tap_filter_tile_kernel<8, true>) : go(tap_filter_tile_kernel<8, false>);
+        else lno ? go(tap_filter_tile_kernel<4, true>) : go(tap_filter_tile_kernel<4, false>);
         MH_LAUNCH_CHECK();
         return;
     }
@@ -634,13 +708,21 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
         const int want = std::atoi(force);
         if (want == 1 || want == 2 || want == 4 || want == 8) hg = want;
     }
-    const int64_t total = pix * (kHeads / hg) * v4;
-    const unsigned blocks = unsigned(ceil_div(total, 256));
+    const int tpp = (kHeads / hg) * v4;
+    MH_REQUIRE(!lno || tpp <= 256, "tap_filter: LayerNorm output needs a pixel's threads in one block");
+    // With the LayerNorm, blocks of whole pixels (P * tpp threads); else 256.
+    const unsigned threads = lno ? unsigned((256 / tpp) * tpp) : 256u;
+    const size_t lds = lno ? threads * sizeof(float) : 0;
+    const int64_t total = pix * tpp;
+    const unsigned blocks = unsigned(ceil_div(total, threads));
+    auto go = [&](auto kern) {
+        kern<<<blocks, threads, lds, ctx.stream>>>(a_t, v, yc, residual, out, nb, hh, ww, vd, ln);
+    };
     switch (hg) {
-        case 8: tap_filter_kernel<8><<<blocks, 256, 0, ctx.stream>>>(a_t, v, yc, residual, out, nb, hh, ww, vd); break;
-        case 4: tap_filter_kernel<4><<<blocks, 256, 0, ctx.stream>>>(a_t, v, yc, residual, out, nb, hh, ww, vd); break;
-        case 2: tap_filter_kernel<2><<<blocks, 256, 0, ctx.stream>>>(a_t, v, yc, residual, out, nb, hh, ww, vd); break;
-        default: tap_filter_kernel<1><<<blocks, 256, 0, ctx.stream>>>(a_t, v, yc, residual, out, nb, hh, ww, vd);
+        case 8: lno ? go(tap_filter_kernel<8, true>) : go(tap_filter_kernel<8, false>); break;
+        case 4: lno ? go(tap_filter_kernel<4, true>) : go(tap_filter_kernel<4, false>); break;
+        case 2: lno ? go(tap_filter_kernel<2, true>) : go(tap_filter_kernel<2, false>); break;
+        default: lno ? go(tap_filter_kernel<1, true>) : go(tap_filter_kernel<1, false>);
     }
     MH_LAUNCH_CHECK();
 }

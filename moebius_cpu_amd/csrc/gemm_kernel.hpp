@@ -22,7 +22,6 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef _Float16 halfx4 __attribute__((ext_vector_type(4)));
 
 constexpr int BK = 32;          // K per LDS stage
-constexpr int LDS_S = BK + 4;   // padded LDS row stride (floats): conflict-free b128 reads
 constexpr int K4 = BK / 4;      // float4 per tile row
 constexpr int kMaxSeg = 3;      // column segments of a segmented output
 
@@ -571,6 +570,11 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
     // per K tile. The epilogue reuses the space for the C tile (row stride CS:
     // the two row halves of a 32x32 block's store fall on different banks).
     constexpr int CS = BN + 8;
+    // LDS row stride: BK + 4 for the 32x32 instruction; the 16x16 instruction's
+    // lane layout (rows l % 16, K offsets 4 * (l / 16)) took 10% of its LDS
+    // cycles in bank conflicts at that stride, and BK + 8 is 0.5% faster over a
+    // UNet step (BK + 12 and + 20 cost a workgroup of occupancy and are slower).
+    constexpr int LDS_S = MF == 16 ? BK + 8 : BK + 4;
     constexpr int SMEM = 2 * (BM + BN) * LDS_S;
     static_assert(BM * CS <= SMEM && SMEM >= 2048, "C tile and GroupNorm sums must fit in the staging space");
     __shared__ float smem[SMEM];

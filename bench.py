@@ -163,14 +163,14 @@ def _components(ctx, steps):
 # WRITE_SIZE over this script's own default run (two UNet steps plus the standalone
 # timing loop), each scaled by the counter's reading for a plain 256 MiB device copy
 # (FETCH_SIZE reads half the copied bytes, WRITE_SIZE all of them), averaged over the
-# standalone loop's 51 launches: 13.22 MiB fetched + 10.00 MiB written per launch.
-DOMINANT_TRAFFIC_BYTES = int((13.22 + 10.00) * 1048576)
+# standalone loop's 51 launches: 13.28 MiB fetched + 10.00 MiB written per launch.
+DOMINANT_TRAFFIC_BYTES = int((13.28 + 10.00) * 1048576)
 
 
 def _dominant_gemm(ctx, steps, fast=False):
     """The step's most frequent GEMM, timed on its own with events: the 1x1 conv of
-    a [2,64,64,320] map to 320 channels with bias (gemm_f32_kernel, 32x32 tiles on
-    v_mfma_f32_16x16x4f32, 2560 workgroups), i.e. M = 8192, N = 320, K = 320."""
+    a [2,64,64,320] map to 320 channels with bias (gemm_f32_kernel, 32x64 tiles on
+    v_mfma_f32_16x16x4f32, 1280 workgroups), i.e. M = 8192, N = 320, K = 320."""
     from moebius_cpu_amd import engine as E
     from moebius_cpu_amd import synthetic as S
 
@@ -193,7 +193,7 @@ def _dominant_gemm(ctx, steps, fast=False):
                 "work_per_launch": f"algorithmic bytes {nbytes}; {flops / 1e9:.3f} GFLOP "
                                    f"({tf:.1f} TFLOP/s = {tf / PEAK_F16_MFMA_TFLOPS:.3f} of f16 MFMA peak)",
                 "avg_launch_us": round(us, 2)}
-    return {"bound": "mfma", "kernel": "gemm_f32_kernel<32,32,dense> (1x1 conv [2,64,64,320] -> 320, "
+    return {"bound": "mfma", "kernel": "gemm_f32_kernel<32,64,dense> (1x1 conv [2,64,64,320] -> 320, "
                                        "M=8192 N=320 K=320: the step's most frequent GEMM)",
             "achieved": round(tf, 2), "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
             "frac": round(tf / PEAK_F32_MFMA_TFLOPS, 4), "traffic": DOMINANT_TRAFFIC_BYTES,

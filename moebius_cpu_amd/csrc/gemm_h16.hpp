@@ -30,7 +30,7 @@ void launch_conv_h16(Context &ctx, GemmArgs &p, WeightType wt, int mode, bool pr
 namespace {
 
 constexpr int BKH = 64;          // K per LDS stage
-constexpr int LDS_H = BKH + 8;   // padded LDS row stride (halves): 144 bytes, conflict-free b128 reads
+constexpr int LDS_H = BKH + 8;   // padded LDS row stride (halves): 144 bytes (+16 and +24: 0.7% and 2.8% slower steps)
 constexpr int KCH = BKH / 4;     // 4-element chunks per tile row
 
 template <int M>

@@ -304,7 +304,7 @@ void launch_cfg_h16(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi,
         }
     } else {
         p.k_split = p.K;
-        p.vec_out = out_vec_ok(p);
+        p.vec_out = out_vec_ok(p, BM);
         gn_partials_plan(p, BM, BN, 1, batch);
         const dim3 grid(tiles, unsigned(batch));
         if constexpr (MODE <= kDenseScalar) {

@@ -91,8 +91,9 @@ struct GemmArgs {
     // byte extents of one item's A (or conv input) and of B, for the buffer
     // loads' range check (< 2^31): an access at or past the extent reads zero
     uint32_t a_bytes, b_bytes;
-    // set by the launcher: the output (or split partials) may be written four
-    // adjacent columns at a time with 16-byte accesses (see out_vec_ok)
+    // set by the launcher: 1: the output (or split partials) may be written four
+    // adjacent columns at a time with 16-byte accesses (see out_vec_ok); 2: grouped
+    // rows written four rows at a time (see out_vec_ok); 0: one element at a time
     int vec_out;
     // GroupNorm statistics of the output (optional): row tile t writes, per
     // column, (sum y, sum y*y) over its BM rows of the values stored to
@@ -210,17 +211,24 @@ __device__ __forceinline__ float4 store4(const GemmArgs &p, int row, int col, fl
     return r;
 }
 
-// Whether the output can be written four adjacent columns at a time: N, the
-// leading dimensions, batch strides and segment bounds multiples of 4, no row
-// grouping, 16-byte aligned buffers.
-inline bool out_vec_ok(const GemmArgs &p) {
+// How the output can be written 16 bytes at a time (GemmArgs::vec_out): 1 when N,
+// the leading dimensions, batch strides and segment bounds are multiples of 4
+// with no row grouping; 2 for grouped rows with rg % 4 == 0, BM % rg == 0,
+// M % rg == 0, ldc and the batch stride multiples of 4, one output; buffers
+// 16-byte aligned; else 0.
+inline int out_vec_ok(const GemmArgs &p, int bm) {
     auto al = [](const void *q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
-    if (p.rg > 1 || (p.N & 3) || (p.c_bs & 3)) return false;
+    if (p.rg > 1) {
+        const bool ok = p.rg % 4 == 0 && bm % p.rg == 0 && p.M % p.rg == 0 && (p.ldc & 3) == 0 &&
+                        (p.c_bs & 3) == 0 && p.nseg == 0 && al(p.out) && al(p.res) && al(p.res2);
+        return ok ? 2 : 0;
+    }
+    if ((p.N & 3) || (p.c_bs & 3)) return false;
     if (!al(p.bias) || !al(p.res) || !al(p.res2) || !al(p.rsc) || !al(p.rsh)) return false;
-    if (p.nseg == 0) return (p.ldc & 3) == 0 && al(p.out);
+    if (p.nseg == 0) return ((p.ldc & 3) == 0 && al(p.out)) ? 1 : 0;
     for (int s = 0; s < p.nseg; ++s)
-        if ((p.seg_col[s] & 3) || (p.seg_col[s + 1] & 3) || !al(p.seg_out[s])) return false;
-    return true;
+        if ((p.seg_col[s] & 3) || (p.seg_col[s + 1] & 3) || !al(p.seg_out[s])) return 0;
+    return 1;
 }
 
 __device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
@@ -502,7 +510,7 @@ __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const
                     smem[(r0 + i * MF + MI::acc_row(v, lane)) * CS + c0 + j * MF] = acc[i][j][v];
     }
     __syncthreads();
-    if (p.vec_out) {
+    if (p.vec_out == 1) {
         constexpr int C4 = BN / 4;  // float4 per tile row
         static_assert(BM * C4 % 256 == 0, "whole passes over the C tile");
         // GroupNorm sums: a thread keeps one column quad over all its rows.
@@ -529,6 +537,23 @@ __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const
         }
         if constexpr (kGn) {
             if (p.gnp) gn_tile_partials<BM, BN>(p, smem, gs, gq, m0, n0);
+        }
+    } else if (p.vec_out == 2) {
+        // Grouped rows (out index (row / rg) * ldc + col * rg + row % rg, rg % 4 == 0,
+        // BM % rg == 0): rows 4j..4j+3 of a group at one column are four adjacent
+        // floats, written as one 16-byte store; consecutive threads take the group's
+        // row quads, then columns, so a wave writes contiguous runs.
+        const int rq = p.rg >> 2;
+        for (int e = tid; e < BM * BN / 4; e += 256) {
+            const int hq = e % rq, rest = e / rq, cc = rest % BN, rr = (rest / BN) * p.rg + hq * 4;
+            const int row = m0 + rr, col = n0 + cc;
+            if (row >= p.M || col >= p.N) continue;  // M % rg == 0: the whole quad is inside
+            const int64_t o = out_index(p, row, col);
+            const float bcol = p.bias ? p.bias[col] : 0.f;
+            float y[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) y[j] = epilogue_value<EPI>(p, row + j, col, o + j, smem[(rr + j) * CS + cc], bcol);
+            *reinterpret_cast<float4 *>(p.out + o) = float4{y[0], y[1], y[2], y[3]};
         }
     } else {
         // One element per thread and pass; consecutive threads take consecutive
@@ -742,7 +767,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int spli
 
 // Whether the split-K reduction may use 16-byte accesses (see splitk_reduce_kernel).
 inline bool reduce_vec_ok(const GemmArgs &p) {
-    return out_vec_ok(p) && (reinterpret_cast<uintptr_t>(p.partial) & 15) == 0 &&
+    return out_vec_ok(p, 1) == 1 && (reinterpret_cast<uintptr_t>(p.partial) & 15) == 0 &&
            int64_t(p.M) * p.N < (int64_t(1) << 31);
 }
 
@@ -756,7 +781,7 @@ struct Plan {
 inline void gn_partials_plan(GemmArgs &p, int bm, int bn, int splits, int batch) {
     p.gn_rows = 0;
     if (!p.gnp) return;
-    const bool ok = splits == 1 && batch == 1 && p.vec_out && p.nseg == 0 && p.rg <= 1 && 256 % (bn / 4) == 0 &&
+    const bool ok = splits == 1 && batch == 1 && p.vec_out == 1 && p.nseg == 0 && p.rg <= 1 && 256 % (bn / 4) == 0 &&
                     p.gn_item_rows > 0 && p.gn_item_rows % bm == 0 && p.M % p.gn_item_rows == 0 &&
                     (reinterpret_cast<uintptr_t>(p.gnp) & 15) == 0;
     if (ok) p.gn_rows = bm;
@@ -843,7 +868,7 @@ void launch_cfg(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int
         }
     } else {
         p.k_split = p.K;
-        p.vec_out = out_vec_ok(p);
+        p.vec_out = out_vec_ok(p, BM);
         gn_partials_plan(p, BM, BN, 1, batch);
         const dim3 grid(tiles, unsigned(batch));
         // The SiLU epilogue is only instantiated for dense operands (the convs never use it).

@@ -129,25 +129,32 @@ def test_cross_lambda_kernel(ctx, br0, nb, hw, k):
         assert max_abs_rel(got_res[b], h[b] + want) < 1e-5
 
 
-@pytest.mark.parametrize("row_group", [0, 8])
+# Grouped rows (out[m / g][n][m % g], the self-lambda's [pixel][tap][head] A) take
+# 16-byte stores of four rows when g % 4 == 0; plain rows, a ragged last tile,
+# a K split and the bias epilogue around them.
+@pytest.mark.parametrize("row_group", [0, 4, 8])
 @pytest.mark.parametrize("plan", [None, "32,32,1", "64,64,1", "64,64,2"])
-def test_gemm_nt_kernel(ctx, row_group, plan, monkeypatch):
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_gemm_nt_kernel(ctx, row_group, plan, with_bias, monkeypatch):
     if plan:
         monkeypatch.setenv("MOEBIUS_HIP_GEMM_PLAN", plan)
     rng = np.random.default_rng(9)
     m, n, k = 304, 226, 40
     a = rng.standard_normal((m, k)).astype(np.float32)
     b = rng.standard_normal((n, k)).astype(np.float32)
-    want = a.astype(np.float64) @ b.astype(np.float64).T
+    bias = rng.standard_normal(n).astype(np.float32)
+    want = a.astype(np.float64) @ b.astype(np.float64).T + (bias.astype(np.float64) if with_bias else 0.0)
     ad, bd = D(ctx, a), D(ctx, b)
+    biasd = D(ctx, bias) if with_bias else None  # kept alive until the kernel has run
+    bp = biasd.ptr if with_bias else None
     if row_group:
         g = row_group
         c = E.DeviceArray(ctx, (m // g, n, g))
-        E.check(E.lib().mh_gemm_nt(ctx.h, ad.ptr, k, bd.ptr, 0, k, m, n, k, None, None, c.ptr, n * g, g))
+        E.check(E.lib().mh_gemm_nt(ctx.h, ad.ptr, k, bd.ptr, 0, k, m, n, k, bp, None, c.ptr, n * g, g))
         got = c.numpy().transpose(0, 2, 1).reshape(m, n)
     else:
         c = E.DeviceArray(ctx, (m, n))
-        E.check(E.lib().mh_gemm_nt(ctx.h, ad.ptr, k, bd.ptr, 0, k, m, n, k, None, None, c.ptr, n, 0))
+        E.check(E.lib().mh_gemm_nt(ctx.h, ad.ptr, k, bd.ptr, 0, k, m, n, k, bp, None, c.ptr, n, 0))
         got = c.numpy()
     assert max_abs_rel(got, want) < 1e-5
 

@@ -141,13 +141,16 @@ __global__ __launch_bounds__(256) void depthwise_kernel(const typename Vec<VW>::
 }
 
 // LDS-tiled variant for channel counts that are multiples of 4: a workgroup
-// stages the (8+2) x (8+2) input pixels of an 8x8 output tile for 16 channel
+// stages the (16+2) x (16+2) input pixels of a 16x16 output tile for 4 channel
 // quads (and the matching gate quads for GLU) in LDS once, then each thread
 // computes four adjacent output pixels of one quad from LDS. Every input value
-// is read from L2/HBM about (10*10)/(8*8) = 1.6 times instead of 4.5, and the
+// is read from L2/HBM about (18*18)/(16*16) = 1.27 times instead of 4.5, and the
 // optional GroupNorm prologue is applied once per staged value. The tap order
-// and the skipped out-of-image rows are those of depthwise_kernel.
-constexpr int kDwTH = 8, kDwTW = 8, kDwCQ = 16;
+// and the skipped out-of-image rows are those of depthwise_kernel. (Measured
+// against 8x8 tiles of 16 quads, 8x16 / 16x8 of 8 and 4x16 of 16: the 32x32 GLU
+// 19.6 -> 17.7 us, UNet step -30 us.)
+constexpr int kDwTH = 16, kDwTW = 16, kDwCQ = 4;
+static_assert(kDwCQ * kDwTH * (kDwTW / 4) == 256, "one thread per 4 outputs of a quad");
 constexpr int kDwNP = (kDwTH + 2) * (kDwTW + 2);
 
 template <int EPI, bool PRO>

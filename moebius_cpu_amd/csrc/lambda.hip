@@ -751,15 +751,22 @@ void cross_lambda(Context &ctx, const float *q, const float *e, const float *lam
     MH_REQUIRE(out != q, "cross_lambda: out must not alias q");
     const int64_t npix = int64_t(nb) * hw;
     if (npix == 0) return;
-    // Heads per thread: the most that still gives every CU a block (8, 4 or 2).
+    // Heads per thread: 4 while that still gives every CU a block, else 2
+    // (measured at the UNet's sizes: 64x64 / k 40 15.6 us with 4 against 21.1
+    // with 8, 32x32 / k 80 14.3 against 16.5 with 2, 16x16 / k 160 16.0 with 2
+    // against 18.6 with 4); 8 only when forced.
     const int k4 = k / 4;
     int hg = 2;
-    for (int cand : {8, 4}) {
+    for (int cand : {4}) {
         const int P = 256 / ((kHeads / cand) * k4);
         if (P >= 1 && ceil_div(npix, P) >= ctx.cu_count) {
             hg = cand;
             break;
         }
+    }
+    if (const char *f = std::getenv("MOEBIUS_HIP_CROSS_HEADS")) {  // A/B override: 2, 4 or 8
+        const int want = std::atoi(f);
+        if ((want == 2 || want == 4 || want == 8) && 256 / ((kHeads / want) * k4) >= 1) hg = want;
     }
     const int P = std::max(1, 256 / ((kHeads / hg) * k4));
     const unsigned threads = unsigned(P * (kHeads / hg) * k4);

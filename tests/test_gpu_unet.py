@@ -100,10 +100,16 @@ def test_position_term_kernel_bit_exact(ctx, br0, nb, k):
 # CrossLambda::forward after to_q (src/unet/lambda.rs:258-271) in one kernel:
 # with lambda_c = 0 the Yc part is exactly +0 and the rest must be the
 # position term bit for bit; with a real lambda_c, Yc = Q . lambda_c (f64
-# reference) within the f32 bar. Sizes select each heads-per-thread variant
-# (8 at 64x64 / k 40, 4 at 32x32 / k 80, 2 at 16x16 / k 160) plus a ragged block.
+# reference) within the f32 bar. Sizes select the default heads-per-thread
+# variants (4 at 64x64 / k 40 and 32x32 / k 80, 2 at 16x16 / k 160) plus a ragged
+# block; MOEBIUS_HIP_CROSS_HEADS forces each variant, 8 included.
 @pytest.mark.parametrize("br0,nb,hw,k", [(0, 2, 4096, 40), (0, 2, 1024, 80), (0, 2, 256, 160), (1, 1, 37, 40)])
-def test_cross_lambda_kernel(ctx, br0, nb, hw, k):
+@pytest.mark.parametrize("heads", [None, "2", "4", "8"])
+def test_cross_lambda_kernel(ctx, br0, nb, hw, k, heads, monkeypatch):
+    if heads:
+        monkeypatch.setenv("MOEBIUS_HIP_CROSS_HEADS", heads)
+    else:
+        monkeypatch.delenv("MOEBIUS_HIP_CROSS_HEADS", raising=False)
     rng = np.random.default_rng(k + hw)
     q = rng.standard_normal((nb, hw, 8 * k)).astype(np.float32)
     e = rng.standard_normal((hw, 10, k)).astype(np.float32)

@@ -326,6 +326,8 @@ __global__ __launch_bounds__(256) void tap_filter_kernel(const float *__restrict
 // loads (double-buffered, one barrier per row), so the inner loop reads LDS
 // only and every value and coefficient leaves HBM/L2 once per block. Per output
 // element the operations are tap_filter_kernel's (the reference's order).
+constexpr int kStageRegs = 4;  // float4 per thread of a staged value / coefficient row
+
 template <int HG, bool LN>
 __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__restrict__ a_t,
                                                               const float *__restrict__ v, const float *yc,
@@ -366,24 +368,60 @@ __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__res
     const int ky0 = max(kPad - y, 0), ky1 = min(kWin, hh + kPad - y);
     const int kx0 = max(kPad - x, 0), kx1 = min(kWin, ww + kPad - x);
     const float4 *vb = reinterpret_cast<const float4 *>(v) + int64_t(b) * hh * ww * v4;
-    auto stage = [&](int ky, int buf) {
+    // Staging of tap row ky in two halves: load() issues the row's global loads
+    // into registers (up to kStageRegs float4 per thread for the value row and
+    // for the coefficient row), commit() writes them to LDS buffer buf, so the
+    // loads of row ky + 1 land while row ky is computed.
+    float4 sv[kStageRegs], sc[kStageRegs];
+    auto load = [&](int ky) {
         const int iy = y + ky - kPad;
+#pragma unroll
+        for (int i = 0; i < kStageRegs; ++i) {
+            const int t = int(threadIdx.x) + i * int(blockDim.x);
+            const int c = t / v4, q = t - c * v4, ix = x0 - kPad + c;
+            sv[i] = (t < span * v4 && ix >= 0 && ix < ww) ? vb[(int64_t(iy) * ww + ix) * v4 + q]
+                                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int i = 0; i < kStageRegs; ++i) {
+            const int t = int(threadIdx.x) + i * int(blockDim.x);
+            const int p = t / kRowC4, w = t - p * kRowC4;
+            sc[i] = t < ntx * kRowC4 ? a4[(pix0 + p) * (kTapsB * kHeads / 4) + ky * kRowC4 + w]
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    // commit() also copies directly whatever the registers do not hold (small
+    // blocks whose rows exceed kStageRegs float4 per thread).
+    auto commit = [&](int ky, int buf) {
+        const int iy = y + ky - kPad, reg_end = kStageRegs * int(blockDim.x);
         float4 *vd4 = vls + buf * span * v4;
-        for (int t = threadIdx.x; t < span * v4; t += blockDim.x) {
+#pragma unroll
+        for (int i = 0; i < kStageRegs; ++i) {
+            const int t = int(threadIdx.x) + i * int(blockDim.x);
+            if (t < span * v4) vd4[t] = sv[i];
+        }
+        for (int t = int(threadIdx.x) + reg_end; t < span * v4; t += blockDim.x) {
             const int c = t / v4, q = t - c * v4, ix = x0 - kPad + c;
             vd4[t] = (ix >= 0 && ix < ww) ? vb[(int64_t(iy) * ww + ix) * v4 + q] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
         float4 *cd4 = cls + buf * tx * kRowC4;
-        for (int t = threadIdx.x; t < ntx * kRowC4; t += blockDim.x) {
+#pragma unroll
+        for (int i = 0; i < kStageRegs; ++i) {
+            const int t = int(threadIdx.x) + i * int(blockDim.x);
+            if (t < ntx * kRowC4) cd4[t] = sc[i];
+        }
+        for (int t = int(threadIdx.x) + reg_end; t < ntx * kRowC4; t += blockDim.x) {
             const int p = t / kRowC4, w = t - p * kRowC4;
             cd4[t] = a4[(pix0 + p) * (kTapsB * kHeads / 4) + ky * kRowC4 + w];
         }
     };
-    stage(ky0, 0);
+    load(ky0);
+    commit(ky0, 0);
     __syncthreads();
     for (int ky = ky0; ky < ky1; ++ky) {
         const int buf = (ky - ky0) & 1;
-        if (ky + 1 < ky1) stage(ky + 1, buf ^ 1);
+        const bool next = ky + 1 < ky1;
+        if (next) load(ky + 1);
         if (active) {
             const float4 *vr = vls + buf * span * v4 + xl * v4 + jq;
             const float4 *cr = cls + buf * tx * kRowC4 + xl * kRowC4 + hg * (HG / 4);
@@ -407,6 +445,7 @@ __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__res
                 }
             }
         }
+        if (next) commit(ky + 1, buf ^ 1);
         __syncthreads();
     }
     if (active) {

@@ -455,25 +455,36 @@ __device__ __forceinline__ TileIdx tile_index(int tiles_m, int tiles_n) {
 }
 
 // GroupNorm partials of one output tile (GemmArgs::gnp): thread t holds the
-// sums over its rows of column quad t % (BN / 4); the 256 / (BN / 4) threads of
-// a quad are added in thread order through LDS (2048 floats), so the partials
+// sums over its rows of column quad t % (BN / 4). The lanes of a wave that
+// share a quad are added with an xor butterfly (every lane ends with the same
+// bits), then the four waves' sums in wave order through LDS, so the partials
 // are deterministic.
 template <int BM, int BN>
 __device__ __forceinline__ void gn_tile_partials(const GemmArgs &p, float *smem, float4 s, float4 q, int m0, int n0) {
-    constexpr int C4 = BN / 4, R = 256 / C4;
-    const int tid = threadIdx.x;
+    constexpr int C4 = BN / 4;
+    static_assert(C4 <= 64 && 64 % C4 == 0, "whole column quads per wave");
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int off = C4; off < 64; off <<= 1) {
+        s.x += __shfl_xor(s.x, off, 64), s.y += __shfl_xor(s.y, off, 64);
+        s.z += __shfl_xor(s.z, off, 64), s.w += __shfl_xor(s.w, off, 64);
+        q.x += __shfl_xor(q.x, off, 64), q.y += __shfl_xor(q.y, off, 64);
+        q.z += __shfl_xor(q.z, off, 64), q.w += __shfl_xor(q.w, off, 64);
+    }
     float4 *red = reinterpret_cast<float4 *>(smem);
     __syncthreads();  // every thread is done with the C tile
-    red[tid] = s;
-    red[256 + tid] = q;
+    if (lane < C4) {
+        red[wave * C4 + lane] = s;
+        red[4 * C4 + wave * C4 + lane] = q;
+    }
     __syncthreads();
     if (tid < C4) {
         const int col = n0 + tid * 4;
         if (col < p.N) {
-            float4 ts = red[tid], tq = red[256 + tid];
+            float4 ts = red[tid], tq = red[4 * C4 + tid];
 #pragma unroll
-            for (int r = 1; r < R; ++r) {
-                const float4 a = red[r * C4 + tid], b = red[256 + r * C4 + tid];
+            for (int r = 1; r < 4; ++r) {
+                const float4 a = red[r * C4 + tid], b = red[4 * C4 + r * C4 + tid];
                 ts.x += a.x, ts.y += a.y, ts.z += a.z, ts.w += a.w;
                 tq.x += b.x, tq.y += b.y, tq.z += b.z, tq.w += b.w;
             }

@@ -739,10 +739,9 @@ class UNetDevice {
             if (down_[i].has_sample) skips.push_back(down_[i].sample.fwd(e, skips.back()));
             tr("unet.down." + std::to_string(i) + ".out", skips.back());
         }
-        // The last down output is both the hidden state and the first skip.
-        DT h = pool_.tensor(skips.back().n, skips.back().h, skips.back().w, skips.back().c);
-        HIP_CHECK(hipMemcpyAsync(h.p, skips.back().p, size_t(h.numel()) * sizeof(float), hipMemcpyDeviceToDevice,
-                                 ctx_.stream));
+        // The last down output is both the hidden state and the first skip: h
+        // starts as that same buffer (read twice by the first concat, returned once).
+        DT h = skips.back();
         for (size_t i = 0; i < up_.size(); ++i) {
             for (size_t j = 0; j < up_[i].res.size(); ++j) {
                 DT skip = skips.back();
@@ -750,7 +749,7 @@ class UNetDevice {
                 DT cat = pool_.tensor(h.n, h.h, h.w, h.c + skip.c);
                 concat_channels(ctx_, h.p, h.c, skip.p, skip.c, h.px(), cat.p);
                 pool_.recycle(skip);
-                pool_.recycle(h);
+                if (h.p != skip.p) pool_.recycle(h);
                 const DwResnet &r = up_[i].res[j];
                 DT a = r.fwd(e, cat, tp + r.temb_off, temb_total_);
                 pool_.recycle(cat);

@@ -159,8 +159,11 @@ __global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__res
                                                              const float4 *__restrict__ bias, DwPrologue pro,
                                                              float4 *__restrict__ out) {
     using V = Vec<4>;
+    // GLU (EPI 2) convolves two input halves. They pass through one LDS tile in
+    // turn (20.7 KB instead of 41.5 KB: seven workgroups fit a CU's 160 KB
+    // instead of three); the loads of both are issued up front.
     constexpr int PARTS = EPI == 2 ? 2 : 1;
-    __shared__ float4 tile[PARTS][kDwNP][kDwCQ];
+    __shared__ float4 tile[kDwNP][kDwCQ];
     const int co_v = EPI == 2 ? cv / 2 : cv;
     const int tiles_x = (w + kDwTW - 1) / kDwTW, tiles_y = (h + kDwTH - 1) / kDwTH;
     int bid = blockIdx.x;
@@ -171,7 +174,7 @@ __global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__res
     const int q0 = blockIdx.y * kDwCQ;
     const int oy0 = ty * kDwTH, ox0 = tx * kDwTW;
     // Staging: every load of the thread is issued before the first LDS store,
-    // so a thread has all of its (up to 13) 16-byte loads in flight at once.
+    // so a thread has all of its (up to 11) 16-byte loads in flight at once.
     constexpr int TOTAL = PARTS * kDwNP * kDwCQ;
     constexpr int PER = (TOTAL + 255) / 256;
     float4 v[PER];
@@ -186,53 +189,58 @@ __global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__res
         if (idx < TOTAL && q0 + qq < co_v && iy >= 0 && iy < h && ix >= 0 && ix < w)
             v[i] = x[(size_t(b) * h + iy) * size_t(w) * cv + size_t(ix) * cv + q0 + qq + part * co_v];
     }
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int idx = threadIdx.x + 256 * i;
-        if (idx >= TOTAL) break;
-        const int part = idx / (kDwNP * kDwCQ);
-        const int r = idx - part * (kDwNP * kDwCQ);
-        const int pix = r / kDwCQ, qq = r - pix * kDwCQ;
-        if (PRO) {
-            const int iy = oy0 - 1 + pix / (kDwTW + 2), ix = ox0 - 1 + pix % (kDwTW + 2);
-            if (q0 + qq < co_v && iy >= 0 && iy < h && ix >= 0 && ix < w) {
-                const int qin = q0 + qq + part * co_v;
-                v[i] = V::fma(v[i], reinterpret_cast<const float4 *>(pro.scale)[size_t(b) * cv + qin],
-                              reinterpret_cast<const float4 *>(pro.shift)[size_t(b) * cv + qin]);
-                if (pro.silu) v[i] = V::silu(v[i]);
-            }
-        }
-        tile[part][pix][qq] = v[i];
-    }
-    __syncthreads();
     const int qq = threadIdx.x % kDwCQ, g = threadIdx.x / kDwCQ;
     const int r = g / (kDwTW / 4), c0 = (g % (kDwTW / 4)) * 4;
     const int q = q0 + qq, oy = oy0 + r;
-    if (q >= co_v || oy >= h) return;  // no barrier follows
+    const bool active = q < co_v && oy < h;  // inactive threads still reach every barrier
     float4 acc[PARTS][4];
 #pragma unroll
     for (int part = 0; part < PARTS; ++part) {
-        const int qw = q + part * co_v;
-        const float4 bv = bias[qw];
+        if (part > 0) __syncthreads();  // the previous half's reads are done
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[part][j] = bv;
+        for (int i = 0; i < PER; ++i) {
+            const int idx = threadIdx.x + 256 * i;
+            if (idx >= TOTAL) break;
+            const int ip = idx / (kDwNP * kDwCQ);
+            if (ip != part) continue;
+            const int rr = idx - ip * (kDwNP * kDwCQ);
+            const int pix = rr / kDwCQ, pq = rr - pix * kDwCQ;
+            if (PRO) {
+                const int iy = oy0 - 1 + pix / (kDwTW + 2), ix = ox0 - 1 + pix % (kDwTW + 2);
+                if (q0 + pq < co_v && iy >= 0 && iy < h && ix >= 0 && ix < w) {
+                    const int qin = q0 + pq + ip * co_v;
+                    v[i] = V::fma(v[i], reinterpret_cast<const float4 *>(pro.scale)[size_t(b) * cv + qin],
+                                  reinterpret_cast<const float4 *>(pro.shift)[size_t(b) * cv + qin]);
+                    if (pro.silu) v[i] = V::silu(v[i]);
+                }
+            }
+            tile[pix][pq] = v[i];
+        }
+        __syncthreads();
+        if (active) {
+            const int qw = q + part * co_v;
+            const float4 bv = bias[qw];
 #pragma unroll
-        for (int ky = 0; ky < 3; ++ky) {
-            const int iy = oy + ky - 1;
-            if (iy < 0 || iy >= h) continue;
-            float4 win[6];
+            for (int j = 0; j < 4; ++j) acc[part][j] = bv;
 #pragma unroll
-            for (int j = 0; j < 6; ++j) win[j] = tile[part][(r + ky) * (kDwTW + 2) + c0 + j][qq];
-            const float4 w0 = wt[(ky * 3 + 0) * cv + qw], w1 = wt[(ky * 3 + 1) * cv + qw],
-                         w2 = wt[(ky * 3 + 2) * cv + qw];
+            for (int ky = 0; ky < 3; ++ky) {
+                const int iy = oy + ky - 1;
+                if (iy < 0 || iy >= h) continue;
+                float4 win[6];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                acc[part][j] = V::fma(w0, win[j], acc[part][j]);
-                acc[part][j] = V::fma(w1, win[j + 1], acc[part][j]);
-                acc[part][j] = V::fma(w2, win[j + 2], acc[part][j]);
+                for (int j = 0; j < 6; ++j) win[j] = tile[(r + ky) * (kDwTW + 2) + c0 + j][qq];
+                const float4 w0 = wt[(ky * 3 + 0) * cv + qw], w1 = wt[(ky * 3 + 1) * cv + qw],
+                             w2 = wt[(ky * 3 + 2) * cv + qw];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    acc[part][j] = V::fma(w0, win[j], acc[part][j]);
+                    acc[part][j] = V::fma(w1, win[j + 1], acc[part][j]);
+                    acc[part][j] = V::fma(w2, win[j + 2], acc[part][j]);
+                }
             }
         }
     }
+    if (!active) return;
     float4 *dst = out + (size_t(b) * h + oy) * size_t(w) * co_v + q;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {

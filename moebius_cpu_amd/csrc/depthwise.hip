@@ -160,8 +160,8 @@ __global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__res
                                                              float4 *__restrict__ out) {
     using V = Vec<4>;
     // GLU (EPI 2) convolves two input halves. They pass through one LDS tile in
-    // turn (20.7 KB instead of 41.5 KB: seven workgroups fit a CU's 160 KB
-    // instead of three); the loads of both are issued up front.
+    // turn (20.7 KB instead of 41.5 KB: LDS allows seven workgroups per CU
+    // instead of three, registers five); the loads of both are issued up front.
     constexpr int PARTS = EPI == 2 ? 2 : 1;
     __shared__ float4 tile[kDwNP][kDwCQ];
     const int co_v = EPI == 2 ? cv / 2 : cv;

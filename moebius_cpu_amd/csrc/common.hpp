@@ -70,13 +70,6 @@ struct Context {
     int cu_count = 0;
     std::string arch;
     Workspace ws;
-    // Self-resetting completion counters for "last block finalises" kernels.
-    // Zeroed once at creation; every kernel that increments one returns it
-    // to zero, so no memset is ever queued (graph-capture safe).
-    unsigned int *counters = nullptr;
-    static constexpr int kCounters = 4096;
-    int next_counter = 0;
-    unsigned int *counter_block(int n);
 
     explicit Context(int dev);
     ~Context();

@@ -45,26 +45,11 @@ Context::Context(int dev) : device(dev) {
     }
     cu_count = prop.multiProcessorCount;
     HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
-    HIP_CHECK(hipMalloc(&counters, kCounters * sizeof(unsigned int)));
-    HIP_CHECK(hipMemset(counters, 0, kCounters * sizeof(unsigned int)));
-    HIP_CHECK(hipDeviceSynchronize());
 }
 
 Context::~Context() {
     if (stream) (void)hipStreamSynchronize(stream);
-    if (counters) (void)hipFree(counters);
     if (stream) (void)hipStreamDestroy(stream);
-}
-
-// Counter slots are handed out round-robin. A slot is only in use while its
-// kernel runs, and kernels on the one stream run in order, so reuse is safe as
-// long as one launch takes fewer slots than the ring holds.
-unsigned int *Context::counter_block(int n) {
-    if (n > kCounters) fail(kInternal, "counter request exceeds the counter ring");
-    if (next_counter + n > kCounters) next_counter = 0;
-    unsigned int *p = counters + next_counter;
-    next_counter += n;
-    return p;
 }
 
 }  // namespace mh

@@ -225,6 +225,19 @@ int32_t mh_group_norm_forward(MhContext *ctx, const float *x, uint32_t n, uint32
                               uint32_t groups, float eps, const float *gamma, const float *beta, const float *add,
                               uint32_t silu, float *out);
 
+/* No counterpart in the reference: mh_group_norm_forward for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments and result bits; its
+ * statistics partials and scale/shift live in a fixed 1 MiB device array per
+ * GPU (262144 floats, held until the process ends) instead of the context
+ * workspace, so it calls no hipMalloc/hipFree. Shapes whose scratch exceeds the
+ * array (partials plus 2 * n * c floats; e.g. n * c > 65536 on maps of a few
+ * pixels) return MH_ERR_INVALID_ARGUMENT. Every call on a GPU shares that GPU's
+ * array: calls that overlap on one GPU (two contexts' streams) race. */
+int32_t mh_group_norm_forward_noalloc(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w,
+                                      uint32_t c, uint32_t groups, float eps, const float *gamma, const float *beta,
+                                      const float *add, uint32_t silu, float *out);
+
 /* src/engine/norm.rs:132-148 `apply_affine` over n items: out = [SiLU](x.scale + shift). */
 int32_t mh_apply_affine(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
                         const float *scale, const float *shift, uint32_t silu, float *out);

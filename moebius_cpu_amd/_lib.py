@@ -78,6 +78,8 @@ SIGNATURES = {
     "mh_depthwise3x3_fused": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _vp, _vp, _u32, _vp]),
     "mh_group_norm_affine": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _f32, _vp, _vp, _vp, _vp, _vp]),
     "mh_group_norm_forward": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _f32, _vp, _vp, _vp, _u32, _vp]),
+    "mh_group_norm_forward_noalloc": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _f32, _vp, _vp, _vp, _u32,
+                                             _vp]),
     "mh_apply_affine": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _vp]),
     "mh_layer_norm": (_i32, [_vp, _vp, _u64, _u32, _vp, _vp, _f32, _vp]),
     "mh_silu_inplace": (_i32, [_vp, _vp, _u64]),

@@ -448,6 +448,20 @@ int32_t mh_group_norm_forward(MhContext *ctx, const float *x, uint32_t n, uint32
     });
 }
 
+int32_t mh_group_norm_forward_noalloc(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w,
+                                      uint32_t c, uint32_t groups, float eps, const float *gamma, const float *beta,
+                                      const float *add, uint32_t silu, float *out) {
+    return guard([&] {
+        mh::Context &cc = C(ctx);
+        need(x, "x");
+        need(gamma, "gamma");
+        need(beta, "beta");
+        need(out, "out");
+        mh::group_norm_forward_noalloc(cc, x, dim(n, "n"), dim(h, "h"), dim(w, "w"), dim(c, "c"),
+                                       dim(groups, "groups"), eps, gamma, beta, add, silu != 0, out);
+    });
+}
+
 int32_t mh_apply_affine(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
                         const float *scale, const float *shift, uint32_t silu, float *out) {
     return guard([&] {

@@ -3,6 +3,7 @@
 #include <sstream>
 
 #include "common.hpp"
+#include "kernels.hpp"
 
 namespace mh {
 
@@ -44,6 +45,8 @@ Context::Context(int dev) : device(dev) {
         fail(kUnsupportedDevice, "this library is built for gfx950 (MI355X) only; device is " + arch);
     }
     cu_count = prop.multiProcessorCount;
+    // The no-allocation entry points' fixed scratch: its device address on this GPU.
+    noalloc_scratch_setup(dev);
     HIP_CHECK(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking));
 }
 

@@ -45,6 +45,15 @@ void group_norm_forward(Context &ctx, const float *x, int n, int h, int w, int c
                         int64_t add_ld = 0);
 void layer_norm(Context &ctx, const float *x, int64_t rows, int c, const float *gamma, const float *beta, float eps,
                 float *out);
+// group_norm_forward (no add row stride) with its scratch in a fixed per-device
+// array instead of the context workspace: no device allocation. Shapes whose
+// scratch exceeds group_norm_noalloc_max_floats() are rejected. Calls that
+// overlap on one GPU share the array and race.
+void group_norm_forward_noalloc(Context &ctx, const float *x, int n, int h, int w, int c, int groups, float eps,
+                                const float *gamma, const float *beta, const float *add, bool silu, float *out);
+int64_t group_norm_noalloc_max_floats();
+// Takes the no-allocation scratch's device address for `device` (current), once.
+void noalloc_scratch_setup(int device);
 // GroupNorm statistics partials written by a producer's epilogue for the
 // GroupNorm that follows it: part [pixels / rows][c][2] = per tile of `rows`
 // pixels (inside one item of item_rows pixels) and channel, (sum y, sum y*y)

@@ -12,6 +12,8 @@
 // deterministic. The apply pass is a separate kernel, or is fused into the
 // consumer (the depthwise and GEMM prologues) with the scale/shift produced here.
 #include <cstdlib>
+#include <mutex>
+#include <string>
 
 #include "common.hpp"
 #include "dmath.hpp"
@@ -315,26 +317,47 @@ __global__ __launch_bounds__(256) void layer_norm_generic_kernel(const float *__
 
 }  // namespace
 
-void group_norm_affine(Context &ctx, const float *x, int n, int h, int w, int c, int groups, float eps,
-                       const float *gamma, const float *beta, const float *add, float *scale, float *shift,
-                       int64_t add_ld) {
-    if (add_ld <= 0) add_ld = c;
-    MH_REQUIRE(add_ld % 4 == 0, "GroupNorm: add row stride must be a multiple of 4");
-    MH_REQUIRE(groups > 0 && c % groups == 0, "channels not divisible by groups");
-    MH_REQUIRE(c % 4 == 0, "GroupNorm: channel count must be a multiple of 4 on the GPU path");
-    MH_REQUIRE(n > 0 && h > 0 && w > 0, "GroupNorm: empty tensor");
-    MH_REQUIRE(aligned16(x) && aligned16(add), "GroupNorm: x and add must be 16-byte aligned");
+namespace {
+
+// Floats of the statistics partials group_norm_affine writes for this shape.
+int64_t gn_partial_floats(int n, int hw, int c) {
+    return int64_t(n) * ceil_div(hw, gn_chunk_px(n, hw, c)) * c * 2;
+}
+
+// group_norm_affine with its partials at `part` (gn_partial_floats of them).
+void group_norm_affine_into(Context &ctx, const float *x, int n, int h, int w, int c, int groups, float eps,
+                            const float *gamma, const float *beta, const float *add, float *scale, float *shift,
+                            int64_t add_ld, float *part) {
     const int hw = h * w;
     const int chunk_px = gn_chunk_px(n, hw, c);
     const int nchunks = int(ceil_div(hw, chunk_px));
     const int nctiles = int(ceil_div(c, kGnTileC));
-    float *part = static_cast<float *>(ctx.ws.get(size_t(n) * nchunks * c * 2 * sizeof(float), ctx.stream));
     gn_partial_kernel<<<dim3(nchunks, nctiles, n), 256, 0, ctx.stream>>>(x, add, add_ld, hw, c, chunk_px, nchunks,
                                                                         part);
     MH_LAUNCH_CHECK();
     gn_finalize_kernel<<<dim3(groups, n), 256, 0, ctx.stream>>>(part, add, add_ld, hw, c, nchunks, groups, 0, eps,
                                                                 gamma, beta, scale, shift);
     MH_LAUNCH_CHECK();
+}
+
+void gn_check(int n, int h, int w, int c, int groups, const float *x, const float *add, int64_t add_ld) {
+    MH_REQUIRE(add_ld % 4 == 0, "GroupNorm: add row stride must be a multiple of 4");
+    MH_REQUIRE(groups > 0 && c % groups == 0, "channels not divisible by groups");
+    MH_REQUIRE(c % 4 == 0, "GroupNorm: channel count must be a multiple of 4 on the GPU path");
+    MH_REQUIRE(n > 0 && h > 0 && w > 0, "GroupNorm: empty tensor");
+    MH_REQUIRE(aligned16(x) && aligned16(add), "GroupNorm: x and add must be 16-byte aligned");
+}
+
+}  // namespace
+
+void group_norm_affine(Context &ctx, const float *x, int n, int h, int w, int c, int groups, float eps,
+                       const float *gamma, const float *beta, const float *add, float *scale, float *shift,
+                       int64_t add_ld) {
+    if (add_ld <= 0) add_ld = c;
+    gn_check(n, h, w, c, groups, x, add, add_ld);
+    float *part = static_cast<float *>(
+        ctx.ws.get(size_t(gn_partial_floats(n, h * w, c)) * sizeof(float), ctx.stream));
+    group_norm_affine_into(ctx, x, n, h, w, c, groups, eps, gamma, beta, add, scale, shift, add_ld, part);
 }
 
 void group_norm_affine_partials(Context &ctx, const float *part, int rows, int n, int hw, int c, int groups,
@@ -388,20 +411,90 @@ void apply_affine(Context &ctx, const float *x, int n, int h, int w, int c, cons
     MH_LAUNCH_CHECK();
 }
 
+namespace {
+
+// Floats group_norm_forward needs beyond its input and output: the statistics
+// partials, then (from the next 256-byte boundary) scale and shift [n * c] each.
+struct GnForwardScratch {
+    int64_t aff_off, total;
+};
+
+GnForwardScratch gn_forward_scratch(int n, int h, int w, int c) {
+    GnForwardScratch s;
+    s.aff_off = (gn_partial_floats(n, h * w, c) + 63) & ~int64_t(63);
+    s.total = s.aff_off + 2 * int64_t(n) * c;
+    return s;
+}
+
+void group_norm_forward_in(Context &ctx, const float *x, int n, int h, int w, int c, int groups, float eps,
+                           const float *gamma, const float *beta, const float *add, bool silu, float *out,
+                           int64_t add_ld, float *base, int64_t aff_off) {
+    float *scale = base + aff_off;
+    float *shift = scale + int64_t(n) * c;
+    group_norm_affine_into(ctx, x, n, h, w, c, groups, eps, gamma, beta, add, scale, shift, add_ld, base);
+    apply_affine(ctx, x, n, h, w, c, scale, shift, silu, out);
+}
+
+}  // namespace
+
 void group_norm_forward(Context &ctx, const float *x, int n, int h, int w, int c, int groups, float eps,
                         const float *gamma, const float *beta, const float *add, bool silu, float *out,
                         int64_t add_ld) {
     if (add_ld <= 0) add_ld = c;
-    MH_REQUIRE(groups > 0 && c % groups == 0, "channels not divisible by groups");
-    // scale/shift live in the tail of the workspace's partial block.
-    const size_t part_bytes =
-        size_t(n) * ceil_div(int64_t(h) * w, gn_chunk_px(n, h * w, c)) * c * 2 * sizeof(float);
-    const size_t aff_off = (part_bytes + 255) & ~size_t(255);
-    char *ws = static_cast<char *>(ctx.ws.get(aff_off + size_t(n) * c * 2 * sizeof(float), ctx.stream));
-    float *scale = reinterpret_cast<float *>(ws + aff_off);
-    float *shift = scale + size_t(n) * c;
-    group_norm_affine(ctx, x, n, h, w, c, groups, eps, gamma, beta, add, scale, shift, add_ld);
-    apply_affine(ctx, x, n, h, w, c, scale, shift, silu, out);
+    gn_check(n, h, w, c, groups, x, add, add_ld);
+    const GnForwardScratch s = gn_forward_scratch(n, h, w, c);
+    float *base = static_cast<float *>(ctx.ws.get(size_t(s.total) * sizeof(float), ctx.stream));
+    group_norm_forward_in(ctx, x, n, h, w, c, groups, eps, gamma, beta, add, silu, out, add_ld, base, s.aff_off);
+}
+
+// ---- GroupNorm forward without allocation ----
+// Its scratch (the statistics partials, scale and shift) is this fixed device
+// array, one copy per GPU, held until the process ends. Host code never passes
+// `scratch` itself to a kernel (on the host the name is only a stand-in): the
+// device address comes from hipGetSymbolAddress, taken once per device when a
+// context is created on it (noalloc_scratch_setup) and kept in g_scratch_ptr.
+constexpr int64_t kNoAllocScratchFloats = int64_t(1) << 18;  // 1 MiB
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float *g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+void noalloc_scratch_setup(int device) {
+    MH_REQUIRE(device >= 0 && device < kMaxDevices, "device ordinal beyond the library's device table");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[device]) return;
+    int cur = -1;
+    HIP_CHECK(hipGetDevice(&cur));
+    if (cur != device) fail(kInternal, "noalloc scratch set-up: the device is not current");
+    void *ptr = nullptr;
+    HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    if (!ptr) fail(kInternal, "hipGetSymbolAddress returned no address for the GroupNorm scratch");
+    g_scratch_ptr[device] = static_cast<float *>(ptr);
+}
+
+int64_t group_norm_noalloc_max_floats() { return kNoAllocScratchFloats; }
+
+void group_norm_forward_noalloc(Context &ctx, const float *x, int n, int h, int w, int c, int groups, float eps,
+                                const float *gamma, const float *beta, const float *add, bool silu, float *out) {
+    const int64_t add_ld = c;
+    gn_check(n, h, w, c, groups, x, add, add_ld);
+    const GnForwardScratch s = gn_forward_scratch(n, h, w, c);
+    if (s.total > kNoAllocScratchFloats) {
+        fail(kInvalidArgument, "GroupNorm (no allocation): this shape needs " + std::to_string(s.total) +
+                                   " floats of scratch (statistics partials plus scale/shift for n * c = " +
+                                   std::to_string(int64_t(n) * c) + "), more than the fixed " +
+                                   std::to_string(kNoAllocScratchFloats) + " (1 MiB)");
+    }
+    float *base = nullptr;
+    {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        base = ctx.device >= 0 && ctx.device < kMaxDevices ? g_scratch_ptr[ctx.device] : nullptr;
+    }
+    if (!base) fail(kInternal, "GroupNorm (no allocation): scratch address not set up for this device");
+    group_norm_forward_in(ctx, x, n, h, w, c, groups, eps, gamma, beta, add, silu, out, add_ld, base, s.aff_off);
 }
 
 void layer_norm(Context &ctx, const float *x, int64_t rows, int c, const float *gamma, const float *beta, float eps,

@@ -87,12 +87,13 @@ def vae_specs() -> list[Spec]:
 
 
 @functools.lru_cache(maxsize=2)
-def random_vae(seed: int = 6000, std: float = 0.02) -> dict[str, np.ndarray]:
-    """Random init of every tensor: weights N(0, 0.5 / sqrt(fan_in)), so that
-    activations keep their scale through the deep chain (the GroupNorms
-    renormalise every resnet input), biases N(0, std), norm gamma
-    1 + N(0, std), beta N(0, std). Cached per (seed, std): treat the arrays as
-    read-only."""
+def random_vae(seed: int = 6000, bias_std: float = 0.02, norm_std: float = 0.05) -> dict[str, np.ndarray]:
+    """Random init of every tensor, as the VAE benchmark configuration states it:
+    Kaiming-normal weights (std sqrt(2 / fan_in), fan_in = 9 * c_in for the 3x3
+    convs and c_in for the 1x1 convs and the attention projections, which are
+    the same [o, i] GEMMs), GroupNorm gamma = 1 + N(0, norm_std) and
+    beta = N(0, norm_std); the configuration leaves biases open, they are
+    N(0, bias_std). Cached per argument set: treat the arrays as read-only."""
     import concurrent.futures as cf
     import os
 
@@ -101,8 +102,8 @@ def random_vae(seed: int = 6000, std: float = 0.02) -> dict[str, np.ndarray]:
     def gen(i):
         s = specs[i]
         if s.kind == "weight":
-            fan_in = int(np.prod(s.shape[1:]))
-            return S.normal(seed * 100003 + i, s.shape, std=0.5 / float(np.sqrt(fan_in)))
+            return S.kaiming(seed * 100003 + i, s.shape, int(np.prod(s.shape[1:])))
+        std = norm_std if s.kind in ("norm_w", "norm_b") else bias_std
         return S.normal(seed * 100003 + i, s.shape, std=std, mean=1.0 if s.kind == "norm_w" else 0.0)
 
     with cf.ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 1)) as ex:

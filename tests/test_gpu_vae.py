@@ -1,7 +1,8 @@
 """GPU parity of the VAE path, through the C ABI: the mid attention's row
 softmax and the posterior sample bit for bit against the oracle, then encode
-and decode (random-init SDXL-VAE weights) against the oracle block by block,
-at small sizes and at the pipeline's 512x512 / 64x64 shapes."""
+and decode (random-init SDXL-VAE weights: Kaiming convs, GroupNorm noise
+N(0, 0.05)) against the oracle block by block, at small sizes and at the
+pipeline's 512x512 / 64x64 shapes."""
 from __future__ import annotations
 
 import numpy as np
@@ -96,20 +97,38 @@ def test_encode_small_matches_oracle(gvae, ovae):
     assert max_abs_rel(got, want) <= TOL
 
 
+# The 512x512 configuration as stated for the VAE benchmark: Kaiming-normal
+# weights, GroupNorm gamma = 1 + N(0, 0.05), beta = N(0, 0.05) (vae_params.random_vae).
+# Activations grow through the decoder (block outputs reach std ~68 and |x| ~470
+# at 512x512x128) and the bar stays max-abs <= 1e-4 * max|ref| per traced block.
 def test_decode_512_matches_oracle(gvae, ovae):
-    """The pipeline's decode: a [1,64,64,4] latent to a [1,512,512,3] image."""
+    """The pipeline's decode: a [1,64,64,4] latent to a [1,512,512,3] image, block by block."""
     lat = S.normal(24, (1, 64, 64, 4))
-    want = ovae.decode(lat)
-    got = gvae.decode_host(lat)
+    want, tr_o = ovae.decode(lat, trace=True)
+    got, tr_g = gvae.decode_traced(lat)
+    _compare_traces(tr_g, tr_o)
     assert max_abs_rel(got, want) <= TOL and rel_l2(got, want) <= 1e-5
     # quantised as the pipeline does (src/imaging/blend.rs:21-24): the images differ
     # only where an f32-rounding difference crosses a level, by one level
     u8g, u8o = oracle.to_u8(got), oracle.to_u8(want)
-    assert np.mean(u8g != u8o) < 1e-3
+    diff = int(np.count_nonzero(u8g != u8o))
+    print(f"decode 512x512: {diff} of {u8g.size} u8 bytes differ from the oracle's "
+          f"(max |d| {np.abs(u8g.astype(np.int32) - u8o.astype(np.int32)).max()})")
+    assert diff < 1e-3 * u8g.size
     assert np.abs(u8g.astype(np.int32) - u8o.astype(np.int32)).max() <= 1
 
 
 def test_encode_512_matches_oracle(gvae, ovae):
+    """One [1,512,512,3] image in U[-1,1] with posterior noise, block by block."""
+    images = V.vae_images(seed=25, b=1, h=512, w=512)
+    noise = S.normal(26, (1, 64, 64, 4))
+    want, tr_o = ovae.encode(images, noise, trace=True)
+    got, tr_g = gvae.encode_traced(images, noise)
+    _compare_traces(tr_g, tr_o)
+    assert max_abs_rel(got, want) <= TOL and rel_l2(got, want) <= 1e-5
+
+
+def test_encode_512_pipeline_batch_matches_oracle(gvae, ovae):
     """The pipeline's encode: image and masked image as a batch of 2 at 512x512."""
     images = V.vae_images(seed=25, b=2, h=512, w=512)
     noise = S.normal(26, (2, 64, 64, 4))

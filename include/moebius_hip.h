@@ -214,8 +214,9 @@ int32_t mh_depthwise3x3_fused(MhContext *ctx, const float *x, uint32_t n, uint32
 
 /* src/engine/norm.rs:57-105 `GroupNorm::affine`: per item and channel
  * scale/shift ([n * c] each, device) with GN(x + add) = x.scale + shift.
- * add [n * c] or NULL. Statistics: f32 per-channel partials over 256-pixel
- * chunks, folded per group in f64. */
+ * add [n * c] or NULL. Statistics: f32 per-channel (sum, sum of squares) over
+ * pixel chunks (64 pixels, doubled until at most 512 partial blocks remain),
+ * folded per group in f64 in a fixed order. */
 int32_t mh_group_norm_affine(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
                              uint32_t groups, float eps, const float *gamma, const float *beta, const float *add,
                              float *scale, float *shift);
@@ -262,13 +263,13 @@ int32_t mh_to_u8(MhContext *ctx, const float *x, uint64_t len, uint8_t *out);
  * the reference's Cephes polynomial, for bit-exact checks of the device math. */
 int32_t mh_math_eval(MhContext *ctx, uint32_t which, const float *x, uint64_t len, float *y);
 
-/* src/unet/lambda.rs:452-489 `softmax_lambda` per item: keys [nb][rows][k]
+/* src/unet/lambda.rs:322-359 `softmax_lambda` per item: keys [nb][rows][k]
  * (read only), v [nb][rows][vd] -> lambda_t [nb][vd][k], the TRANSPOSE of the
  * reference's lambda_c [k][vd]. k, vd <= 160. */
 int32_t mh_softmax_lambda(MhContext *ctx, const float *keys, const float *v, uint32_t nb, uint32_t rows, uint32_t k,
                           uint32_t vd, float *lambda_t);
 
-/* src/unet/lambda.rs:288-314 `tap_filter` over nb items of hh x ww pixels, per
+/* src/unet/lambda.rs:154-185 `tap_filter` over nb items of hh x ww pixels, per
  * pixel, head and value channel: u = (yc + A[225]) then + A[dy*15+dx] * v[pixel +
  * (dy-7, dx-7)] over the in-image taps in (dy, dx) order; out = u, or residual + u
  * when residual is given (the block's following `add_inplace`). a_t is the
@@ -277,7 +278,7 @@ int32_t mh_softmax_lambda(MhContext *ctx, const float *keys, const float *v, uin
 int32_t mh_tap_filter(MhContext *ctx, const float *a_t, const float *v, const float *yc, const float *residual,
                       float *out, uint32_t nb, uint32_t hh, uint32_t ww, uint32_t vd);
 
-/* src/unet/lambda.rs:406-425 `position_term`: u = yc + (q . E) . V[branch], per
+/* src/unet/lambda.rs:276-295 `position_term`: u = yc + (q . E) . V[branch], per
  * element in the reference's order; out = u, or residual + u when residual is
  * given. e [hw][10][k], v_branches [2][10][k], item i using branch br0 + i;
  * q, yc, residual, out [nb*hw][8*k]; out may alias yc or residual. */
@@ -285,7 +286,7 @@ int32_t mh_position_term(MhContext *ctx, const float *q, const float *e, const f
                          uint32_t nb, uint32_t hw, uint32_t k, const float *yc, const float *residual, float *out);
 
 /* src/unet/lambda.rs:258-271, the body of `CrossLambda::forward` after to_q, in
- * one pass: u = q . lambda_c[branch] (src/unet/lambda.rs:266) + (q . E) . V[branch]
+ * one pass: u = q . lambda_c[branch] (src/unet/lambda.rs:265) + (q . E) . V[branch]
  * (the position term as mh_position_term computes it); out = u, or residual + u.
  * lambda_c [2][k][k] row-major; e, v_branches, q, residual, out as for
  * mh_position_term. out may alias residual, not q. k a multiple of 8, <= 256. */

@@ -8,13 +8,13 @@
 //      the sums, as the reference folds its chunk sums in f64), row kk scaled by
 //      (f32)(1 / sum[kk]); written transposed ([j][kk]) so Yc = Q . lambda_c is
 //      an NT GEMM.
-// tap_filter (lambda.rs:288-314): per pixel, head and value channel,
+// tap_filter (lambda.rs:154-185): per pixel, head and value channel,
 //   o = Yc + A[., 225] then + A[., dy*15+dx] * V[pixel + (dy-7, dx-7)] over the
 //   in-image taps in (dy, dx) order with fused multiply-adds: the reference's
 //   per-element operation order. A arrives tap-major ([pixel][226][8], written
 //   that way by the GEMM that makes it) so one thread's heads share each value
 //   load; the block's residual add can be folded into the store.
-// position_term (lambda.rs:406-425): per pixel, B[h][m] = q_h . E[n][m] with
+// position_term (lambda.rs:276-295): per pixel, B[h][m] = q_h . E[n][m] with
 //   the reference's 8-lane dot, then o_h += B[h][m] * V[m] for m = 0..9; the
 //   block's residual add can be folded into the store.
 #include <cstdlib>
@@ -466,7 +466,7 @@ __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__res
     }
 }
 
-// 8-lane dot of src/unet/lambda.rs:429-439 (k a multiple of 8).
+// 8-lane dot of src/unet/lambda.rs:297-309 (k a multiple of 8).
 __device__ __forceinline__ float dot8_ref(const float *__restrict__ a, const float *__restrict__ b, int k) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int i = 0; i < k; i += 8) {

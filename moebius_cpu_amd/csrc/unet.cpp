@@ -328,7 +328,7 @@ struct DwResnet {
     }
 };
 
-// src/unet/lambda.rs:203-282
+// src/unet/lambda.rs:73-152
 struct SelfLambda {
     int c = 0, k = 0;
     Lin to_q, to_k, to_v;
@@ -409,7 +409,7 @@ struct SelfLambda {
     }
 };
 
-// src/unet/lambda.rs:317-425
+// src/unet/lambda.rs:187-274
 struct CrossLambda {
     int c = 0, k = 0, n = 0;
     Lin to_q;
@@ -430,7 +430,7 @@ struct CrossLambda {
             const float *x = ehs_dev + int64_t(br) * TOKENS * XDIM;
             gemm_nt(env.ctx, x, XDIM, 0, wk.p, wk.wt, XDIM, 0, TOKENS, k, XDIM, 1, nullptr, nullptr,
                     keys + int64_t(br) * TOKENS * k, k, 0);
-            // v = ehs . Wv^T, then + bias (src/unet/lambda.rs:362-365)
+            // v = ehs . Wv^T, then + bias (src/unet/lambda.rs:225-235)
             gemm_nt(env.ctx, x, XDIM, 0, wv.p, wv.wt, XDIM, 0, TOKENS, k, XDIM, 1, nullptr, nullptr,
                     v + int64_t(br) * TOKENS * k, k, 0);
             bias_residual_add(env.ctx, v + int64_t(br) * TOKENS * k, TOKENS, k, bv, nullptr,

@@ -3,7 +3,7 @@ random initialisation of it.
 
 Names and layouts are those the reference's loader asks for
 (src/unet/load.rs:51-97, blocks.rs:31-113, transformer.rs:65-87,
-lambda.rs:214-234 / 335-378, embed.rs:428-471, mod.rs:86-140) after the
+lambda.rs:86-104, 205-249 / 335-378, embed.rs:40-83, mod.rs:86-140) after the
 converter (tools/convert_weights.py:13-33): BatchNorms folded into conv_dw /
 conv_pw / to_q / to_v biases, 1x1 [o, i], dense 3x3 [o, 3, 3, i], depthwise
 [3, 3, c], pos_conv [k, 225], rel_pos_emb [N, 10, k].

@@ -327,6 +327,8 @@ def _declare_unet(L):
     L.orc_dot8.restype = ctypes.c_float
     L.orc_dot8.argtypes = [vp, vp, _i64]
     L.orc_position_term.argtypes = [vp, vp, vp, vp, _i64, _i64]
+    L.orc_unet_flops.argtypes = [vp]
+    L.orc_unet_flops_reset.argtypes = []
     L.orc_block_forward.restype = ctypes.c_int
     L.orc_block_forward.argtypes = [ctypes.c_int, ctypes.POINTER(_Named), ctypes.c_int, ctypes.c_char_p, vp, _i64,
                                     _i64, _i64, _i64, _i64, vp, vp, vp, ctypes.c_char_p, ctypes.c_int]
@@ -342,7 +344,7 @@ def timestep_sinusoid(t: int) -> np.ndarray:
 
 
 def softmax_lambda(keys, v):
-    """src/unet/lambda.rs:452-489: keys [rows, k], v [rows, vd] -> lambda [k, vd]."""
+    """src/unet/lambda.rs:322-359: keys [rows, k], v [rows, vd] -> lambda [k, vd]."""
     L = lib()
     _declare_unet(L)
     keys = _f32(keys).copy()
@@ -355,7 +357,7 @@ def softmax_lambda(keys, v):
 
 
 def tap_filter(a, v, o, hh, ww):
-    """src/unet/lambda.rs:288-314 over a whole item: a [hw, 8, 226], v [hw, k], o [hw, 8*k] (updated)."""
+    """src/unet/lambda.rs:154-185 over a whole item: a [hw, 8, 226], v [hw, k], o [hw, 8*k] (updated)."""
     L = lib()
     _declare_unet(L)
     a, v = _f32(a), _f32(v)
@@ -365,7 +367,7 @@ def tap_filter(a, v, o, hh, ww):
 
 
 def position_term(q, e, v, o):
-    """src/unet/lambda.rs:409-425: q, o [px, 8k]; e [px, 10, k]; v [10, k]; returns the updated o."""
+    """src/unet/lambda.rs:279-295: q, o [px, 8k]; e [px, 10, k]; v [10, k]; returns the updated o."""
     L = lib()
     _declare_unet(L)
     q, e, v = _f32(q), _f32(e), _f32(v)
@@ -375,7 +377,7 @@ def position_term(q, e, v, o):
 
 
 def dot8(a, b):
-    """src/unet/lambda.rs:429-439"""
+    """src/unet/lambda.rs:297-309"""
     L = lib()
     _declare_unet(L)
     a, b = _f32(a), _f32(b)
@@ -414,6 +416,21 @@ class UNet:
         if st != 0:
             raise RuntimeError("oracle UNet forward failed")
         return (eps, traced) if trace else eps
+
+    FLOP_KINDS = ("1x1", "3x3 dense", "3x3 stride 2", "depthwise", "lambda pos_conv", "matmul")
+
+    @staticmethod
+    def flops_reset() -> None:
+        lib().orc_unet_flops_reset()
+
+    @staticmethod
+    def flops() -> dict:
+        """FLOPs of the forwards run since flops_reset(), tallied per layer at the
+        shapes it ran, as the upstream model computes them (the unfolded
+        lambda's position Conv3d and products), by category."""
+        out = (ctypes.c_double * len(UNet.FLOP_KINDS))()
+        lib().orc_unet_flops(out)
+        return {k: float(v) for k, v in zip(UNet.FLOP_KINDS, out)}
 
     def __del__(self):
         try:

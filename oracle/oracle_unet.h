@@ -35,22 +35,27 @@ int orc_unet_forward(void *unet, const float *x, int timestep, int guidance, flo
                      void *user);
 
 /* One block alone: kind 0 DwConv2d (blocks.rs:31-54), 1 DwResnet (blocks.rs:56-113,
- * temb [n,1280]), 2 SelfLambda (lambda.rs:203-282), 3 CrossLambda (lambda.rs:317-404),
+ * temb [n,1280]), 2 SelfLambda (lambda.rs:73-152), 3 CrossLambda (lambda.rs:187-274),
  * 4 MixTransformer (transformer.rs:49-130); weights under `prefix`; branches [n]
  * for kinds 3/4. out [n,h,w,c_out]. 0 on success, else 1 with the message in err. */
 int orc_block_forward(int kind, const OrcNamed *tensors, int count, const char *prefix, const float *x, int64_t n,
                       int64_t h, int64_t w, int64_t c_in, int64_t c_out, const float *temb, const int *branches,
                       float *out, char *err, int err_len);
 
-/* src/unet/lambda.rs:452-489; keys [rows,k] is overwritten; lambda [k,vd]. */
+/* src/unet/lambda.rs:322-359; keys [rows,k] is overwritten; lambda [k,vd]. */
 void orc_softmax_lambda(float *keys, const float *v, int64_t rows, int64_t k, int64_t vd, float *lambda);
-/* src/unet/lambda.rs:288-314 */
+/* src/unet/lambda.rs:154-185 */
 void orc_tap_filter(const float *a, const float *v, float *o, int64_t first, int64_t count, int64_t hh, int64_t ww,
                     int64_t vd);
-/* src/unet/lambda.rs:409-425 over count pixels: q, o [count][8k]; e [count][10][k]; v [10][k]. */
+/* src/unet/lambda.rs:279-295 over count pixels: q, o [count][8k]; e [count][10][k]; v [10][k]. */
 void orc_position_term(const float *q, const float *e, const float *v, float *o, int64_t count, int64_t k);
-/* src/unet/lambda.rs:429-439 */
+/* src/unet/lambda.rs:297-309 */
 float orc_dot8(const float *a, const float *b, int64_t k);
+/* FLOPs of the UNet steps run since the last reset, as the upstream model
+ * computes them (unfolded lambda), by category: out[6] = 1x1 convs, dense 3x3,
+ * stride-2 3x3, depthwise, self-lambda position Conv3d, matrix products. */
+void orc_unet_flops(double *out);
+void orc_unet_flops_reset(void);
 
 #ifdef __cplusplus
 }

@@ -34,9 +34,22 @@ constexpr int XDIM = 768;
 constexpr float RESNET_EPS = 1e-5f;
 constexpr float TGN_EPS = 1e-6f;
 constexpr float LN_EPS = 1e-5f;
-// src/unet/lambda.rs:187-201
+// src/unet/lambda.rs:56-71
 constexpr int WIN = 15, TAPS = WIN * WIN, PAD = WIN / 2, TAPS_B = TAPS + 1;
 constexpr int SOFTMAX_CHUNK = 256;
+
+// FLOPs of the step as the upstream model executes it, tallied per layer from
+// the shapes each call runs at, in the categories of the reference's
+// meta-device count (tools/count_flops.py: conv kinds by kernel, everything
+// else FlopCounterMode counts as matrix products): 1x1 convs, dense 3x3,
+// stride-2 3x3, depthwise, the self-lambda's position Conv3d, and the matrix
+// products (linears, lambda einsums). Multiply-add = 2. The oracle runs the
+// folded lambda (lambda.rs:7-24); its layers tally the unfolded products they
+// stand for (pos_conv over [b, k, v, N] x 225 taps, Yp = Q.lambda_p), which is
+// what the 632 GFLOP of docs/PLAN.md:56 counts.
+enum FlopKind { kF1x1 = 0, kFDense3, kFStride2, kFDepthwise, kFPosConv, kFMatmul, kFKinds };
+double g_flops[kFKinds] = {};
+void tally(FlopKind k, double f) { g_flops[k] += f; }
 
 struct LNp {  // LayerNormParams (src/unet/transformer.rs:33-47)
     const float *g = nullptr, *b = nullptr;
@@ -68,6 +81,8 @@ struct DwConv2d {
         mid.set(x.n, x.h, x.w, x.c);
         orc_depthwise3x3(x.p(), x.n, x.h, x.w, x.c, dw, dwb, 1, mid.p());
         pw.fwd(mid, out, ci == co ? &x : nullptr);
+        tally(kFDepthwise, 18.0 * double(x.px()) * ci);
+        tally(kF1x1, 2.0 * double(x.px()) * ci * co);
     }
 };
 
@@ -97,10 +112,12 @@ struct DwResnet {
         orc_silu_inplace(t.data(), int64_t(t.size()));
         Vec tp(size_t(x.n * co));
         temb_proj.fwd(t.data(), x.n, tp.data());
+        tally(kFMatmul, 2.0 * double(x.n) * TIME_EMBED * co);
         norm2.fwd(b, tp.data(), true, a);
         conv2.fwd(a, out);
         if (has_shortcut) {
             shortcut.fwd(x, b);
+            tally(kF1x1, 2.0 * double(x.px()) * ci * co);
             orc_add_inplace(out.p(), b.p(), int64_t(out.d.size()));
         } else {
             orc_add_inplace(out.p(), x.p(), int64_t(out.d.size()));
@@ -108,7 +125,7 @@ struct DwResnet {
     }
 };
 
-// src/unet/lambda.rs:452-489
+// src/unet/lambda.rs:322-359
 Vec softmax_lambda(float *keys, const float *v, int64_t rows, int64_t k, int64_t vd) {
     const int64_t chunks = (rows + SOFTMAX_CHUNK - 1) / SOFTMAX_CHUNK;
     Vec mx(size_t(k), -INFINITY);
@@ -136,7 +153,7 @@ Vec softmax_lambda(float *keys, const float *v, int64_t rows, int64_t k, int64_t
     return lambda;
 }
 
-// src/unet/lambda.rs:288-314: adds the 15x15 position filter of V to o.
+// src/unet/lambda.rs:154-185: adds the 15x15 position filter of V to o.
 void tap_filter(const float *a, const float *v, float *o, int64_t first, int64_t count, int64_t hh, int64_t ww,
                 int64_t vd) {
     const int64_t c = HEADS * vd;
@@ -166,7 +183,7 @@ void tap_filter(const float *a, const float *v, float *o, int64_t first, int64_t
     }
 }
 
-// src/unet/lambda.rs:203-282
+// src/unet/lambda.rs:73-152
 struct SelfLambda {
     int c = 0, k = 0;
     Lin to_q, to_k, to_v;
@@ -190,6 +207,12 @@ struct SelfLambda {
         to_q.fwd(x, q);
         to_k.fwd(x, kt);
         to_v.fwd(x, vt);
+        {
+            const double bn = double(x.n) * hw, kv = double(k) * k;
+            tally(kF1x1, 2.0 * double(x.px()) * c * (c + 2 * k));
+            tally(kFPosConv, 2.0 * bn * kv * TAPS);                   // lambda_p = Conv3d(V), 15x15
+            tally(kFMatmul, 2.0 * bn * kv * (1 + 2 * HEADS));         // lambda_c, Yc, Yp
+        }
         out.set(x.n, hh, ww, c);
         const int64_t band_rows = 16;
         Vec a(size_t(std::min<int64_t>(band_rows, hh) * ww * HEADS * TAPS_B));
@@ -208,7 +231,7 @@ struct SelfLambda {
     }
 };
 
-// src/unet/lambda.rs:429-439: 8 fused-multiply-add lanes, then lanes summed in order.
+// src/unet/lambda.rs:297-309: 8 fused-multiply-add lanes, then lanes summed in order.
 float dot8(const float *a, const float *b, int64_t k) {
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     const int64_t full = k / 8 * 8;
@@ -221,7 +244,7 @@ float dot8(const float *a, const float *b, int64_t k) {
     return s + tail;
 }
 
-// src/unet/lambda.rs:317-425
+// src/unet/lambda.rs:187-274
 struct CrossLambda {
     int c = 0, k = 0;
     int64_t n = 0;
@@ -252,6 +275,14 @@ struct CrossLambda {
         if (hw != n) throw std::runtime_error("CrossLambda input size does not match the position table");
         T4 q;
         to_q.fwd(x, q);
+        {
+            const double bn = double(x.n) * hw, kv = double(k) * k;
+            tally(kF1x1, 2.0 * double(x.px()) * c * c);
+            // per step upstream: to_k / to_v of the text states, lambda_c = K.V^T,
+            // Yc, lambda_p = E.V over the m = 10 tokens, Yp
+            tally(kFMatmul, 2.0 * 2.0 * double(x.n) * TOKENS * XDIM * k + 2.0 * double(x.n) * kv * TOKENS +
+                                2.0 * bn * kv * HEADS * 2 + 2.0 * bn * TOKENS * kv);
+        }
         out.set(x.n, x.h, x.w, c);
         for (int64_t b = 0; b < x.n; ++b) {
             const int br = branches[size_t(b)];
@@ -304,6 +335,8 @@ struct MixTransformer {
     }
     void fwd(const T4 &x, const std::vector<int> &branches, T4 &out) const {
         T4 t, u, h;
+        tally(kF1x1, 2.0 * double(x.px()) * (2.0 * c * c + 3.0 * c * hidden));  // proj_in/out, inverted, point
+        tally(kFDepthwise, 18.0 * double(x.px()) * 2 * hidden);
         norm.fwd(x, nullptr, false, t);
         proj_in.fwd(t, h);
         ln1.fwd(h, t);
@@ -338,6 +371,7 @@ struct Conv3 {  // Downsample / Upsample (src/unet/blocks.rs:116-145)
         orc_conv3x3_output_hw(x.h, x.w, stride, pad, up, &ho, &wo);
         out.set(x.n, ho, wo, c);
         orc_conv3x3_forward(x.p(), x.n, x.h, x.w, x.c, w, c, b, stride, pad, up, nullptr, nullptr, 0, out.p());
+        tally(stride > 1 ? kFStride2 : kFDense3, 2.0 * double(out.px()) * 9 * x.c * c);
     }
 };
 
@@ -433,6 +467,10 @@ struct UNet {
         lin1.fwd(sinus, 1, a1.data());
         orc_silu_inplace(a1.data(), TIME_EMBED);
         lin2.fwd(a1.data(), 1, a2.data());
+        // upstream runs the time embedding on the batch and projects the text
+        // states every step (the oracle does the latter once, at load)
+        tally(kFMatmul, 2.0 * double(b) * (TIME_PROJ * TIME_EMBED + TIME_EMBED * TIME_EMBED) +
+                            2.0 * double(b) * TOKENS * EHS * XDIM);
         T4 temb;
         temb.set(b, 1, 1, TIME_EMBED);
         for (int64_t i = 0; i < b; ++i) std::memcpy(temb.p() + i * TIME_EMBED, a2.data(), TIME_EMBED * sizeof(float));
@@ -490,6 +528,16 @@ struct UNet {
 };
 
 }  // namespace
+
+// The FLOP tally since the last reset: out[6] = 1x1, dense 3x3, stride-2 3x3,
+// depthwise, position Conv3d, matrix products.
+extern "C" void orc_unet_flops(double *out) {
+    for (int i = 0; i < kFKinds; ++i) out[i] = g_flops[i];
+}
+
+extern "C" void orc_unet_flops_reset(void) {
+    for (int i = 0; i < kFKinds; ++i) g_flops[i] = 0.0;
+}
 
 // src/unet/embed.rs:21-30: [cos | sin] of t * exp(-ln(10000) * i / 160), f32 with libm.
 extern "C" void orc_timestep_sinusoid(int t, float *out) {
@@ -617,7 +665,7 @@ extern "C" void orc_tap_filter(const float *a, const float *v, float *o, int64_t
 
 extern "C" float orc_dot8(const float *a, const float *b, int64_t k) { return dot8(a, b, k); }
 
-// src/unet/lambda.rs:409-425 over `count` pixels: q, o [count][8k]; e [count][10][k]; v [10][k].
+// src/unet/lambda.rs:279-295 over `count` pixels: q, o [count][8k]; e [count][10][k]; v [10][k].
 extern "C" void orc_position_term(const float *q, const float *e, const float *v, float *o, int64_t count, int64_t k) {
     const int64_t c = HEADS * k;
     for (int64_t i = 0; i < count; ++i) {

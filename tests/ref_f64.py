@@ -1,7 +1,7 @@
 """float64 numpy restatements of the UNet blocks from their mathematical
 definitions (not from the reference's folded / banded implementation): used
 to pin the oracle. The lambda layers are written in the upstream, unfolded
-form documented at src/unet/lambda.rs:131-172: the self-lambda position
+form documented at src/unet/lambda.rs:7-43: the self-lambda position
 lambda lambda_p materialised by the 15x15 Conv3d, the cross-lambda position
 lambda as E . V per pixel."""
 from __future__ import annotations

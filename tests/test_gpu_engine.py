@@ -158,7 +158,7 @@ def test_conv3x3_odd_sizes_f16_weights(ctx, n, h, w, ci, co, up):
 @pytest.mark.parametrize("tiled", ["1", "0"])
 @pytest.mark.parametrize("h,w,c,ep", [(5, 7, 64, "relu"), (4, 9, 70, "none"), (3, 5, 140, "glu_silu"),
                                       (2, 4, 64, "glu_silu"), (7, 5, 9, "relu"),
-                                      # 8x8 LDS tiles with partial tiles and partial 16-quad channel chunks
+                                      # 16x16 LDS tiles of 4 channel quads, with partial tiles and partial quad groups
                                       (9, 13, 72, "relu"), (17, 6, 136, "none"), (10, 11, 200, "glu_silu"),
                                       (16, 16, 256, "glu_silu"), (8, 8, 8, "none")])
 def test_depthwise_register_blocks_and_tails(ctx, h, w, c, ep, tiled, monkeypatch):
@@ -347,10 +347,10 @@ def test_group_norm_closed_form_moments(ctx):
     assert np.max(np.abs(y.var(axis=(1, 3)) - var / (var + np.float64(np.float32(eps))))) < 1e-5
 
 
-# ---- GroupNorm statistics: the one-launch path for every tile width it uses
-# (whole groups per tile: 60, 40 and 64 channels, a partial last tile) and the
-# two-launch path for groups wider than 64 channels (2560 / 32 = 80), with and
-# without the per-item add folded into the shift (src/engine/norm.rs:57-105)
+# ---- GroupNorm statistics (partials over pixel chunks, f64 fold per group) at
+# channel counts with whole and partial 64-channel tiles and groups wider than
+# one tile (2560 / 32 = 80), with and without the per-item add folded into the
+# shift (src/engine/norm.rs:57-105)
 @pytest.mark.parametrize("n,h,w,c,use_add", [(2, 9, 7, 320, True), (2, 16, 16, 1280, False), (1, 13, 11, 960, True),
                                              (2, 8, 8, 2560, True), (1, 21, 19, 128, False), (2, 5, 6, 96, True),
                                              (2, 64, 64, 320, False)])
@@ -365,7 +365,7 @@ def test_group_norm_affine_every_tiling(ctx, n, h, w, c, use_add):
     sc_want, sh_want = oracle.group_norm_affine(x, 32, 1e-5, gamma, beta, add)
     assert max_abs_rel(aff.scale.numpy(), sc_want) <= 1e-6
     assert max_abs_rel(aff.shift.numpy(), sh_want) <= 1e-6
-    # a second call reuses the counters the first one reset
+    # a second call gives the same bits (fixed-order fold)
     aff2 = gn.affine(T(ctx, x), E.DeviceArray.from_numpy(ctx, add) if use_add else None, False)
     assert np.array_equal(aff2.scale.numpy(), aff.scale.numpy())
     assert np.array_equal(aff2.shift.numpy(), aff.shift.numpy())

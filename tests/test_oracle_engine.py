@@ -178,7 +178,7 @@ def test_matmul_strided_operands_accumulate():
     assert np.max(np.abs(got - (want + 0.5))) < 1e-4
     oracle.matmul(a, w.T, got, accumulate=False)
     assert np.max(np.abs(got - want)) < 1e-4
-    # transposed A (keys^T in softmax_lambda, src/unet/lambda.rs:483) and large k past one block
+    # transposed A (keys^T in softmax_lambda, src/unet/lambda.rs:353) and large k past one block
     k2 = 700
     at = np.sin(np.arange(k2 * m, dtype=np.float32)).reshape(k2, m).astype(np.float32)
     b2 = np.cos(np.arange(k2 * n, dtype=np.float32)).reshape(k2, n).astype(np.float32)

@@ -4,12 +4,16 @@ in their unfolded upstream form, the norms and convs from their formulas) and
 to invariants of the whole network. CPU only."""
 from __future__ import annotations
 
+import ast
+import os
+
 import numpy as np
 import pytest
 
 import oracle
 from moebius_cpu_amd import synthetic as S
 from moebius_cpu_amd import unet_params as U
+from moebius_cpu_amd import vae_params as V
 from tests import ref_f64 as R
 from tests.util import max_abs_rel
 
@@ -175,3 +179,133 @@ def test_unet_trace_names_and_shapes(unet):
     a2 = R.silu(a1.astype(np.float64)) @ P["diff_model.time_embedding.linear_2.weight"].T.astype(np.float64)
     a2 += P["diff_model.time_embedding.linear_2.bias"]
     assert max_abs_rel(tr["unet.temb"].reshape(-1), a2) < 1e-5
+
+
+# ---- the whole network against the reference's published model facts
+
+MANIFEST = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "weights-manifest.txt")
+BN_TARGETS = {"bn1": "conv_dw", "bn2": "conv_pw", "norm_q": "to_q", "norm_v": "to_v"}
+BN_KEYS = ("weight", "bias", "running_mean", "running_var", "num_batches_tracked")
+
+
+def read_manifest():
+    """{section: {name: shape}} of the reference's docs/weights-manifest.txt (a copy in tests/golden)."""
+    sections, cur = {}, None
+    for line in open(MANIFEST, encoding="utf-8"):
+        line = line.rstrip("\n")
+        if not line or line.startswith("#"):
+            continue
+        if line.startswith("["):
+            cur = sections.setdefault(line.strip("[]"), {})
+            continue
+        name, shape = line.split("\t")
+        cur[name] = tuple(ast.literal_eval(shape))
+    return sections
+
+
+def converted_shapes(upstream):
+    """The converter's rewrites of an upstream state dict's names and shapes
+    (tools/convert_weights.py:13-33): eval BatchNorms (found by their
+    running_var) are dropped and folded into the layer beside them, which gains
+    a bias; 1x1 [o,i,1,1] -> [o,i]; dense 3x3 [o,i,3,3] -> [o,3,3,i];
+    depthwise [c,1,3,3] -> [3,3,c]; pos_conv [k,1,1,15,15] -> [k,225];
+    rel_pos_emb [N,10,k,1] -> [N,10,k]."""
+    bns = {}
+    for name in upstream:
+        mod, _, leaf = name.rpartition(".")
+        if leaf == "running_var":
+            parent, _, bn = mod.rpartition(".")
+            assert bn in BN_TARGETS, f"BatchNorm {mod} has no fold target"
+            bns[mod] = f"{parent}.{BN_TARGETS[bn]}"
+    skip = {f"{bn}.{k}" for bn in bns for k in BN_KEYS}
+    out = {}
+    for name, shape in upstream.items():
+        if name in skip:
+            continue
+        mod, _, leaf = name.rpartition(".")
+        if mod in bns.values() and leaf == "weight":
+            out[f"{mod}.bias"] = (shape[0],)
+        if leaf == "rel_pos_emb":
+            assert len(shape) == 4 and shape[-1] == 1
+            shape = shape[:3]
+        elif leaf == "weight" and len(shape) == 5:
+            assert shape[1:3] == (1, 1)
+            shape = (shape[0], shape[3] * shape[4])
+        elif leaf == "weight" and len(shape) == 4:
+            o, i, kh, kw = shape
+            if (kh, kw) == (1, 1):
+                shape = (o, i)
+            elif i == 1:
+                shape = (kh, kw, o)
+            else:
+                shape = (o, kh, kw, i)
+        out[name] = tuple(shape)
+    return out
+
+
+def test_unet_tensor_set_is_the_manifest_after_conversion():
+    """The converted UNet tensor set (names and layouts the oracle and the device
+    load) equals the reference's manifest [unet] section after the converter's
+    rewrites: 1 203 upstream entries, 124 BatchNorms folded."""
+    up = read_manifest()["unet"]
+    assert len(up) == 1203
+    want = converted_shapes(up)
+    got = {s.name: tuple(s.shape) for s in U.unet_specs()}
+    assert sorted(set(want) - set(got)) == [] and sorted(set(got) - set(want)) == []
+    bad = {k: (got[k], want[k]) for k in want if got[k] != want[k]}
+    assert not bad, f"shape differences: {list(bad.items())[:5]}"
+
+
+def test_vae_tensor_set_is_the_manifest_after_conversion():
+    up = read_manifest()["vae"]
+    want = converted_shapes(up)
+    got = {s.name: tuple(s.shape) for s in V.vae_specs()}
+    assert got == want
+
+
+def test_unet_parameter_count_is_226_0_million():
+    """docs/PLAN.md:30: 226.0 M parameters (the upstream module's parameters:
+    no token embedding, BatchNorm affine included, running statistics not).
+    The converted set holds exactly those minus the folded BatchNorm affines,
+    plus the biases the folds add, plus the embedding table."""
+    up = read_manifest()["unet"]
+    numel = {k: int(np.prod(v, dtype=np.int64)) for k, v in up.items()}
+    module = sum(n for k, n in numel.items()
+                 if not k.startswith("embedding_layer.") and not k.rsplit(".", 1)[1].startswith(("running_", "num_")))
+    assert round(module / 1e6, 1) == 226.0
+    bn = [k.rsplit(".", 1)[0] for k in up if k.endswith(".running_var")]
+    bn_affine = sum(2 * up[f"{m}.weight"][0] for m in bn)
+    added_bias = sum(up[f"{m}.weight"][0] for m in bn
+                     if f"{m.rsplit('.', 1)[0]}.{BN_TARGETS[m.rsplit('.', 1)[1]]}.bias" not in up)
+    assert U.param_count() == module - bn_affine + added_bias + numel["embedding_layer.weight"]
+
+
+def test_unet_step_flops_match_the_published_split(unet):
+    """docs/PLAN.md:56: one CFG step (batch 2) is 632 GFLOP, 1x1 62.5%, dense 3x3
+    19.1%, lambda pos-conv 14.0%, stride-2 1.2%, depthwise 0.5%
+    (tools/count_flops.py's categories). The oracle tallies each layer's FLOPs
+    at the shapes it runs (the unfolded lambda's products where it runs the
+    folded form), so this checks the wiring it executes: which layers run, at
+    which level and with which channel counts."""
+    inp = U.unet_input(seed=5000)
+    oracle.UNet.flops_reset()
+    unet.forward(inp.x, inp.timestep, cfg=True)
+    f = oracle.UNet.flops()
+    total = sum(f.values())
+    assert round(total / 1e9) == 632
+    share = {k: round(100.0 * v / total, 1) for k, v in f.items()}
+    assert share["1x1"] == 62.5
+    assert share["3x3 dense"] == 19.1
+    assert share["lambda pos_conv"] == 14.0
+    assert share["3x3 stride 2"] == 1.2
+    assert share["depthwise"] == 0.5
+    # the device's FLOP model (bench.py's step roofline) is the folded count of the same layers
+    mine = U.step_flops(2)
+    temb_proj = sum(2 * 2 * s.shape[1] * s.shape[0] for s in U.unet_specs() if s.name.endswith("time_emb_proj.weight"))
+    assert abs(mine["gemm_1x1"] - f["1x1"] - temb_proj) < 1e6
+    assert abs(mine["conv3x3"] - f["3x3 dense"] - f["3x3 stride 2"]) < 1e6
+    assert abs(mine["depthwise"] - f["depthwise"]) < 1e6
+    # cond-only runs half of every per-item product
+    oracle.UNet.flops_reset()
+    unet.forward(inp.x, inp.timestep, cfg=False)
+    assert abs(sum(oracle.UNet.flops().values()) - total / 2) < 1e-9 * total

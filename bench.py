@@ -1,12 +1,24 @@
 """Benchmark of the MI355X conv/norm hot path.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu] [--no-configs]
 
 Prints ONE JSON line. A step is one pass of the workload over synthetic
 seeded inputs already resident in HBM; the timed region is K steps between two
-HIP events on the library's stream (synchronised on both sides). Also
-reported: the dominant kernel's roofline (algorithmic work / its average
-duration, timed the same way) and the CPU oracle timed on the host cores.
+HIP events on the library's stream (synchronised on both sides). The headline
+is one 512x512 UNet denoise step (CFG batch 2, f32). Also reported: the
+dominant kernel's roofline (algorithmic work / its average duration, timed the
+same way), and, under "configs", every benchmark configuration:
+
+  cfg1  3x3 conv 64x64x320 -> 320 + GroupNorm(32)+SiLU
+  cfg2  kernel sweep at (64,320) (32,640) (16,1280) (8,1280): 1x1 C->C (f32 and
+        f16-stored weights), depthwise 3x3, GroupNorm(32)+SiLU, bias + residual;
+        plus GroupNorm+add+SiLU at 2x64x64x320
+  cfg3  ResNet block 32x32, 320 -> 640 with a time embedding
+  cfg4  the UNet step in EXACT (batch 2 and 1) and FAST (f16 MFMA; batch 2 and 1)
+  cfg5  VAE encode [1,512,512,3] and decode [1,64,64,4] -> [1,512,512,3]
+
+each with its time, its rate and roofline fraction, and the CPU oracle on the
+same inputs, timed in the same run (a child process on the host cores).
 One GPU only: --gpus above 1 exits with a message.
 """
 from __future__ import annotations
@@ -15,7 +27,6 @@ import argparse
 import json
 import os
 import sys
-import time
 
 import numpy as np
 
@@ -33,7 +44,7 @@ def log(msg):
 
 
 def time_region(ctx, fn, steps):
-    """Average ms of fn() over `steps` calls between two events on the stream."""
+    """Average ms of fn() over `steps` back-to-back calls between two events on the stream."""
     ctx.synchronize()
     e0, e1 = ctx.event(), ctx.event()
     e0.record()
@@ -45,132 +56,162 @@ def time_region(ctx, fn, steps):
     return ms / steps
 
 
+def warm_time(ctx, fn, steps, warmup=1):
+    for _ in range(max(warmup, 1)):
+        fn()
+    return time_region(ctx, fn, steps)
+
+
 def cpu_threads():
     return int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
 
 
-def cpu_baseline(workload, extra=(), note=""):
-    """Times the CPU oracle on the same workload in a child process that never
-    touches the GPU (oracle/baseline.py); a failure there is reported, not fatal."""
+def r(v, nd=5):
+    return None if v is None else round(float(v), nd)
+
+
+def mfma_entry(ms, flops, peak=PEAK_F32_MFMA_TFLOPS):
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"ms": r(ms), "tflops": r(tf, 2), "bound": "mfma", "peak_tflops": peak, "frac": r(tf / peak, 4),
+            "gflop": r(flops / 1e9, 4)}
+
+
+def hbm_entry(ms, nbytes):
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    return {"ms": r(ms), "gbps": r(gbps, 1), "bound": "hbm", "peak_gbps": PEAK_HBM_GBPS,
+            "frac": r(gbps / PEAK_HBM_GBPS, 4), "bytes": int(nbytes)}
+
+
+def cpu_run(workload, extra=(), timeout=900):
+    """Runs the CPU oracle on a workload in a child process that never touches the
+    GPU (oracle/baseline.py); returns its JSON, or an error record."""
     import subprocess
 
     cmd = [sys.executable, "-X", "faulthandler", "-m", "oracle.baseline", "--workload", workload,
            "--threads", str(cpu_threads()), *extra]
     log("CPU baseline: " + " ".join(cmd[1:]))
     try:
-        r = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=600)
+        p = subprocess.run(cmd, cwd=ROOT, capture_output=True, text=True, timeout=timeout)
     except subprocess.TimeoutExpired:
-        return {"value": None, "unit": "ms", "cores": cpu_threads(), "kind": "port", "error": "timed out"}
-    if r.returncode != 0:
-        log(r.stderr[-2000:])
-        return {"value": None, "unit": "ms", "cores": cpu_threads(), "kind": "port",
-                "error": f"baseline process exited with {r.returncode}"}
-    res = json.loads(r.stdout.strip().splitlines()[-1])
-    return {"value": res["value"], "unit": "ms", "cores": res["cores"], "kind": "port",
-            "sample": res["sample"] + note}
+        return {"error": "timed out"}
+    if p.returncode != 0:
+        log(p.stderr[-2000:])
+        return {"error": f"baseline process exited with {p.returncode}"}
+    return json.loads(p.stdout.strip().splitlines()[-1])
 
 
-def bench_conv_gn(args):
-    """conv3x3 64x64x320 -> 320 + GroupNorm(32, eps 1e-5) + SiLU, f32. The conv
-    runs as Winograd F(2x2,3x3) (the CPU engine's algorithm for stride-1 convs);
-    the implicit-GEMM conv is timed beside it."""
+def cpu_record(ms, cores, sample):
+    return {"value": r(ms, 3), "unit": "ms", "cores": cores, "kind": "port", "sample": sample}
+
+
+# ---------------------------------------------------------------- cfg1
+
+def cfg1_conv_gn(ctx, steps):
+    """conv3x3 64x64x320 -> 320 + GroupNorm(32, eps 1e-5) + SiLU, f32. The conv runs
+    as Winograd F(2x2,3x3) (the CPU engine's algorithm for stride-1 convs); the
+    implicit-GEMM conv is timed beside it for the f32-MFMA utilisation."""
     from moebius_cpu_amd import engine as E
     from moebius_cpu_amd import workloads as W
 
-    ctx = E.Context(0)
     wl = W.conv3x3_gn_silu()
     x = E.Tensor.from_numpy(ctx, wl.x)
-    conv = E.Conv3x3.same(ctx, 320, 320, E.Param(ctx, wl.w), wl.b, winograd=True)
-    conv_g = E.Conv3x3.same(ctx, 320, 320, E.Param(ctx, wl.w), wl.b)
+    w = E.Param(ctx, wl.w)
+    conv_w = E.Conv3x3.same(ctx, 320, 320, w, wl.b, winograd=True)
+    conv_g = E.Conv3x3.same(ctx, 320, 320, w, wl.b)
     gn = E.GroupNorm(ctx, wl.groups, wl.eps, wl.gamma, wl.beta)
-    y, z = E.Tensor(ctx, *wl.x.shape[:3], 320), E.Tensor(ctx, *wl.x.shape[:3], 320)
+    y, z = E.Tensor(ctx), E.Tensor(ctx)
 
     def step():
-        conv.forward(x, y)
+        conv_w.forward(x, y)
         gn.forward(y, None, True, z)
 
-    for _ in range(args.warmup):
-        step()
-    ms = time_region(ctx, step, args.steps)
-    conv_ms = time_region(ctx, lambda: conv.forward(x, y), args.steps)
-    conv_g.forward(x, y)
-    gemm_ms = time_region(ctx, lambda: conv_g.forward(x, y), args.steps)
-    gn_ms = time_region(ctx, lambda: gn.forward(y, None, True, z), args.steps)
-    elems = y.pixels() * 320
-    wino_flops = 16 * 2.0 * (64 // 2) * (64 // 2) * 320 * 320  # 16 plane GEMMs over 32x32 tiles
-    conv_tflops = wino_flops / (conv_ms * 1e-3) / 1e12
-    gemm_tflops = wl.flops / (gemm_ms * 1e-3) / 1e12
-    gn_gbps = 8.0 * elems / (gn_ms * 1e-3) / 1e9
-
-    out = {
-        "metric": METRIC, "value": round(ms, 5), "unit": "ms", "higher_is_better": False,
-        "ms_per_step": round(ms, 5), "dtype": "f32",
-        "config": {"workload": "conv3x3 64x64x320->320 (Winograd F(2x2,3x3)) + GroupNorm(32)+SiLU (f32, batch 1)",
-                   "input": [1, 64, 64, 320], "weight": [320, 3, 3, 320], "groups": 32, "eps": 1e-5},
-        "roofline": {"bound": "mfma", "kernel": "Winograd conv3x3 (input transform, 16 batched gemm_f32_kernel "
-                                                "plane GEMMs, output transform)",
-                     "achieved": round(conv_tflops, 3), "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(conv_tflops / PEAK_F32_MFMA_TFLOPS, 4), "traffic": None,
-                     "work_per_launch": f"{wino_flops / 1e9:.3f} GFLOP of plane GEMMs per conv (direct conv: "
-                                        f"{wl.flops / 1e9:.3f} GFLOP, {wl.flops / (conv_ms * 1e-3) / 1e12:.1f} "
-                                        "TFLOP/s equivalent)", "avg_launch_ms": round(conv_ms, 5)},
-        "components": {"conv_winograd_ms": round(conv_ms, 5), "conv_implicit_gemm_ms": round(gemm_ms, 5),
-                       "conv_implicit_gemm_mfma_util": round(gemm_tflops / PEAK_F32_MFMA_TFLOPS, 4),
-                       "groupnorm_silu_ms": round(gn_ms, 5), "groupnorm_gbps_8B_per_elem": round(gn_gbps, 1)},
-    }
-    ctx.close()
-    if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline("conv3x3_gn_silu", note=" (C++ restatement of the CPU engine: "
-                                           "Winograd F(2x2,3x3) conv + GroupNorm, OpenMP)")
+    total = warm_time(ctx, step, steps)
+    wino = warm_time(ctx, lambda: conv_w.forward(x, y), steps)
+    gemm = warm_time(ctx, lambda: conv_g.forward(x, y), steps)
+    gn_ms = warm_time(ctx, lambda: gn.forward(y, None, True, z), steps)
+    elems = 64 * 64 * 320
+    wino_flops = 16 * 2.0 * 32 * 32 * 320 * 320  # 16 plane GEMMs over 32x32 tiles
+    out = {"workload": "conv3x3 [1,64,64,320] -> 320 (stride 1, pad 1) + GroupNorm(32, eps 1e-5) + SiLU, f32",
+           "ms": r(total),
+           "conv_winograd": {**mfma_entry(wino, wino_flops),
+                             "direct_equivalent_tflops": r(wl.flops / (wino * 1e-3) / 1e12, 2)},
+           "conv_implicit_gemm": mfma_entry(gemm, wl.flops),
+           "groupnorm_silu": {**hbm_entry(gn_ms, 8.0 * elems), "convention": "8 B/elem (read + write)"}}
     return out
 
 
-def _components(ctx, steps):
-    """Standalone per-kernel figures of the metric: the 3x3 conv's f32 MFMA
-    utilisation (64x64x320 -> 320, implicit GEMM), the same conv as Winograd
-    F(2x2,3x3), and GroupNorm+SiLU HBM GB/s at the VAE's 512x512x128 map
-    (8 B/element: one read, one write)."""
+# ---------------------------------------------------------------- cfg2
+
+def cfg2_sweep(ctx, steps):
+    """The kernel sweep at the four (S, C) points, plus GroupNorm+add+SiLU at 2x64x64x320."""
     from moebius_cpu_amd import engine as E
     from moebius_cpu_amd import synthetic as S
     from moebius_cpu_amd import workloads as W
 
-    wl = W.conv3x3_gn_silu()
-    x = E.Tensor.from_numpy(ctx, wl.x)
-    conv = E.Conv3x3.same(ctx, 320, 320, E.Param(ctx, wl.w), wl.b)
-    y = E.Tensor(ctx, 1, 64, 64, 320)
-    conv.forward(x, y)
-    conv_ms = time_region(ctx, lambda: conv.forward(x, y), steps)
-    wconv = E.Conv3x3.same(ctx, 320, 320, E.Param(ctx, wl.w), wl.b, winograd=True)
-    wconv.forward(x, y)
-    wino_ms = time_region(ctx, lambda: wconv.forward(x, y), steps)
-    xg = E.Tensor.from_numpy(ctx, S.normal(77, (1, 512, 512, 128)))
-    gn = E.GroupNorm(ctx, 32, 1e-6, S.normal(78, (128,), 0.1, 1.0), S.normal(79, (128,), 0.1))
-    z = E.Tensor(ctx, 1, 512, 512, 128)
-    gn.forward(xg, None, True, z)
-    gn_ms = time_region(ctx, lambda: gn.forward(xg, None, True, z), steps)
-    conv_tf = wl.flops / (conv_ms * 1e-3) / 1e12
-    gn_gbps = 8.0 * 512 * 512 * 128 / (gn_ms * 1e-3) / 1e9
-    return {"conv3x3_64x64x320_ms": round(conv_ms, 5),
-            "conv3x3_mfma_util": round(conv_tf / PEAK_F32_MFMA_TFLOPS, 4),
-            "conv3x3_64x64x320_winograd_ms": round(wino_ms, 5),
-            "conv3x3_winograd_direct_equivalent_tflops": round(wl.flops / (wino_ms * 1e-3) / 1e12, 1),
-            "groupnorm_silu_512x512x128_ms": round(gn_ms, 5),
-            "groupnorm_silu_gbps_8B_per_elem": round(gn_gbps, 1),
-            "groupnorm_hbm_frac": round(gn_gbps / PEAK_HBM_GBPS, 4)}
+    D = lambda a: E.DeviceArray.from_numpy(ctx, np.ascontiguousarray(a, np.float32))  # noqa: E731
+    points = []
+    for s, c in W.SWEEP:
+        p = W.sweep_point(s, c)
+        x = E.Tensor.from_numpy(ctx, p.x)
+        res = E.Tensor.from_numpy(ctx, p.residual)
+        out = E.Tensor(ctx)
+        conv32 = E.Conv1x1(ctx, c, c, E.Param(ctx, p.w1), p.b1)
+        conv16 = E.Conv1x1(ctx, c, c, E.Param(ctx, p.w1, f16=True), p.b1)
+        dw_w, dw_b, bias = D(p.dw_w), D(p.dw_b), D(p.bias)
+        gn = E.GroupNorm(ctx, 32, 1e-5, p.gamma, p.beta)
+        flops = 2.0 * s * s * c * c
+        elems = s * s * c
+        e = {"S": s, "C": c}
+        e["conv1x1_f32"] = mfma_entry(warm_time(ctx, lambda: conv32.forward(x, out), steps), flops)
+        e["conv1x1_f16w"] = {**mfma_entry(warm_time(ctx, lambda: conv16.forward(x, out), steps), flops),
+                             "note": "f16-stored weight widened to f32 in the tile loader; f32 MFMA"}
+        e["depthwise"] = hbm_entry(warm_time(ctx, lambda: E.depthwise3x3(x, dw_w, dw_b, "none", out), steps),
+                                   8.0 * elems + 40.0 * c)
+        e["groupnorm_silu"] = hbm_entry(warm_time(ctx, lambda: gn.forward(x, None, True, out), steps), 8.0 * elems)
+        e["bias_residual"] = hbm_entry(warm_time(ctx, lambda: E.bias_residual_add(x, bias, res, out), steps),
+                                       12.0 * elems)
+        points.append(e)
+    # src/engine GroupNorm+add+SiLU at 2x64x64x320 (the CPU engine's kernel benchmark)
+    xg = E.Tensor.from_numpy(ctx, S.normal(2501, (2, 64, 64, 320)))
+    add = D(S.normal(2502, (2, 320), 0.5))
+    gn = E.GroupNorm(ctx, 32, 1e-5, S.normal(2503, (320,), 0.1, 1.0), S.normal(2504, (320,), 0.1))
+    out = E.Tensor(ctx)
+    gna = hbm_entry(warm_time(ctx, lambda: gn.forward(xg, add, True, out), steps), 8.0 * 2 * 64 * 64 * 320)
+    return {"workload": "kernel sweep, f32 activations; depthwise, GroupNorm and bias+residual have no "
+                        "f16-stored operand (the converter keeps them f32), so only the 1x1 has an f16w variant",
+            "points": points, "groupnorm_add_silu_2x64x64x320": gna}
 
 
-# HBM bytes per launch of the dominant kernel (below), from rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE over this script's own default run (two UNet steps plus the standalone
-# timing loop), each scaled by the counter's reading for a plain 256 MiB device copy
-# (FETCH_SIZE reads half the copied bytes, WRITE_SIZE all of them), averaged over the
-# standalone loop's 51 launches: 13.28 MiB fetched + 10.00 MiB written per launch.
+# ---------------------------------------------------------------- cfg3
+
+def cfg3_resnet(ctx, steps):
+    from moebius_cpu_amd import workloads as W
+
+    wl = W.resnet_block()
+    blk = W.ResnetBlockGpu(ctx, wl)
+    ms = warm_time(ctx, blk.forward, steps)
+    # executed matrix work: the two 3x3 convs as 16 Winograd plane GEMMs over 16x16 tiles
+    p = 32 * 32
+    exe = 8.0 * p * (320 * 640 + 640 * 640) + 2.0 * p * 320 * 640 + 2.0 * 1280 * 640
+    return {"workload": "ResNet block [1,32,32,320] -> 640 with time embedding [1280] (Linear 1280->640 on "
+                        "SiLU(temb)), GN(32, eps 1e-5)+SiLU before each 3x3 conv (applied inside the Winograd "
+                        "input transform), 1x1 skip, residual add; f32",
+            **mfma_entry(ms, exe), "direct_gflop": r(wl.flops / 1e9, 3),
+            "direct_equivalent_tflops": r(wl.flops / (ms * 1e-3) / 1e12, 2)}
+
+
+# ---------------------------------------------------------------- cfg4
+
 DOMINANT_TRAFFIC_BYTES = int((13.28 + 10.00) * 1048576)
+# HBM bytes per launch of the dominant kernel (below), from rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE over this script's own run, each scaled by the counter's reading for a plain
+# 256 MiB device copy (FETCH_SIZE reads half the copied bytes, WRITE_SIZE all of them),
+# averaged over the standalone loop's launches: 13.28 MiB fetched + 10.00 MiB written.
 
 
 def _dominant_gemm(ctx, steps, fast=False):
     """The step's most frequent GEMM, timed on its own with events: the 1x1 conv of
-    a [2,64,64,320] map to 320 channels with bias (gemm_f32_kernel, 32x64 tiles on
-    v_mfma_f32_16x16x4f32, 1280 workgroups), i.e. M = 8192, N = 320, K = 320."""
+    a [2,64,64,320] map to 320 channels with bias, M = 8192, N = 320, K = 320."""
     from moebius_cpu_amd import engine as E
     from moebius_cpu_amd import synthetic as S
 
@@ -182,8 +223,6 @@ def _dominant_gemm(ctx, steps, fast=False):
     flops = 2.0 * 8192 * 320 * 320
     tf = flops / (us * 1e-6) / 1e12
     if fast:
-        # f16 products at 16x the f32 rate leave this shape bound by its operand
-        # traffic: x read and y written in f32, the weight read in f16.
         nbytes = 8192 * 320 * 4 * 2 + 320 * 320 * 2 + 320 * 4
         gbps = nbytes / (us * 1e-6) / 1e9
         return {"bound": "hbm", "kernel": "gemm_h16_kernel (f16 MFMA, f32 accumulate; 1x1 conv [2,64,64,320] -> "
@@ -201,14 +240,62 @@ def _dominant_gemm(ctx, steps, fast=False):
             "avg_launch_us": round(us, 2)}
 
 
+def _components(ctx, steps):
+    """Per-kernel figures of the metric: the 3x3 conv's f32 MFMA utilisation
+    (64x64x320 -> 320, implicit GEMM), the same conv as Winograd F(2x2,3x3), and
+    GroupNorm+SiLU HBM GB/s at the VAE's 512x512x128 map (8 B/element)."""
+    from moebius_cpu_amd import engine as E
+    from moebius_cpu_amd import synthetic as S
+    from moebius_cpu_amd import workloads as W
+
+    wl = W.conv3x3_gn_silu()
+    x = E.Tensor.from_numpy(ctx, wl.x)
+    y = E.Tensor(ctx, 1, 64, 64, 320)
+    conv = E.Conv3x3.same(ctx, 320, 320, E.Param(ctx, wl.w), wl.b)
+    conv_ms = warm_time(ctx, lambda: conv.forward(x, y), steps)
+    wconv = E.Conv3x3.same(ctx, 320, 320, E.Param(ctx, wl.w), wl.b, winograd=True)
+    wino_ms = warm_time(ctx, lambda: wconv.forward(x, y), steps)
+    xg = E.Tensor.from_numpy(ctx, S.normal(77, (1, 512, 512, 128)))
+    gn = E.GroupNorm(ctx, 32, 1e-6, S.normal(78, (128,), 0.1, 1.0), S.normal(79, (128,), 0.1))
+    z = E.Tensor(ctx, 1, 512, 512, 128)
+    gn_ms = warm_time(ctx, lambda: gn.forward(xg, None, True, z), steps)
+    conv_tf = wl.flops / (conv_ms * 1e-3) / 1e12
+    gn_gbps = 8.0 * 512 * 512 * 128 / (gn_ms * 1e-3) / 1e9
+    return {"conv3x3_64x64x320_ms": round(conv_ms, 5),
+            "conv3x3_mfma_util": round(conv_tf / PEAK_F32_MFMA_TFLOPS, 4),
+            "conv3x3_64x64x320_winograd_ms": round(wino_ms, 5),
+            "conv3x3_winograd_direct_equivalent_tflops": round(wl.flops / (wino_ms * 1e-3) / 1e12, 1),
+            "groupnorm_silu_512x512x128_ms": round(gn_ms, 5),
+            "groupnorm_silu_gbps_8B_per_elem": round(gn_gbps, 1),
+            "groupnorm_hbm_frac": round(gn_gbps / PEAK_HBM_GBPS, 4)}
+
+
+def _unet_step_entry(ctx, net, inp, cfg, steps, warmup, fast):
+    from moebius_cpu_amd import engine as E
+    from moebius_cpu_amd import unet_params as U
+
+    b = 2 if cfg else 1
+    x = E.DeviceArray.from_numpy(ctx, inp.x)
+    eps = E.DeviceArray(ctx, (b, 64, 64, 4))
+    step = lambda: net.forward(x, inp.timestep, cfg, eps)  # noqa: E731
+    ms = warm_time(ctx, step, steps, warmup)
+    flops = U.step_flops(b, winograd=True)["total"]
+    direct = U.step_flops(b)["total"]
+    peak = PEAK_F16_MFMA_TFLOPS if fast else PEAK_F32_MFMA_TFLOPS
+    tf = flops / (ms * 1e-3) / 1e12
+    return ms, {"ms": r(ms, 4), "batch": b, "tflops_executed": r(tf, 2), "peak_tflops": peak, "frac": r(tf / peak, 4),
+                "gflop_executed": r(flops / 1e9, 1), "gflop_direct": r(direct / 1e9, 1),
+                "direct_equivalent_tflops": r(direct / (ms * 1e-3) / 1e12, 2)}
+
+
 def bench_unet(args):
-    """One full 512^2 denoise step: 64x64x9 latent stack, CFG batch 2, f32 Exact."""
+    """One full 512^2 denoise step: 64x64x9 latent stack, CFG batch 2, f32 Exact (the
+    headline); with configs, also batch 1 and the FAST precision at batch 2 and 1."""
     from moebius_cpu_amd import engine as E
     from moebius_cpu_amd import unet_params as U
     from moebius_cpu_amd.unet import UNet
 
     cfg = not args.cond_only
-    b = 2 if cfg else 1
     log("generating random-init weights")
     params = U.random_unet(seed=4000)
     inp = U.unet_input(seed=5000)
@@ -216,20 +303,10 @@ def bench_unet(args):
     if args.fast:
         ctx.set_precision(True)
     net = UNet(ctx, params, f16_gemm=args.f16_weights or args.fast)
-    x = E.DeviceArray.from_numpy(ctx, inp.x)
-    eps = E.DeviceArray(ctx, (b, 64, 64, 4))
-    step = lambda: net.forward(x, inp.timestep, cfg, eps)  # noqa: E731
-    log("warm-up")
-    for _ in range(max(args.warmup, 1)):
-        step()
-    ctx.synchronize()
-    log("timed steps")
-    ms = time_region(ctx, step, args.steps)
-    flops = U.step_flops(b, winograd=True)  # the upsample convs run as Winograd F(2x2,3x3)
-    direct = U.step_flops(b)["total"]
-    achieved = flops["total"] / (ms * 1e-3) / 1e12
+    log("warm-up and timed steps")
+    ms, head = _unet_step_entry(ctx, net, inp, cfg, args.steps, args.warmup, args.fast)
+    b = head["batch"]
     wbytes, pbytes = net.memory()
-    peak = PEAK_F16_MFMA_TFLOPS if args.fast else PEAK_F32_MFMA_TFLOPS
     if args.fast:
         arith = "FAST: f16-stored GEMM weights, GEMM operands rounded to f16 on f16 MFMA with f32 accumulate"
     else:
@@ -242,75 +319,164 @@ def bench_unet(args):
                    "latent": [1, 64, 64, 9], "batch": b, "timestep": inp.timestep,
                    "params_M": round(U.param_count() / 1e6, 1), "weight_bytes": wbytes, "pool_bytes": pbytes},
         "step_roofline": {"bound": "mfma", "kernel": "whole step (all kernels, one stream)",
-                          "achieved": round(achieved, 2), "peak": peak, "unit": "TFLOP/s",
-                          "frac": round(achieved / peak, 4),
-                          "work": f"{flops['total'] / 1e9:.1f} GFLOP per step (matrix-core work as executed: "
-                                  f"the upsample convs as Winograd GEMMs; {direct / 1e9:.1f} GFLOP with direct convs)",
-                          "direct_equivalent_tflops": round(direct / (ms * 1e-3) / 1e12, 2)},
+                          "achieved": head["tflops_executed"], "peak": head["peak_tflops"], "unit": "TFLOP/s",
+                          "frac": head["frac"],
+                          "work": f"{head['gflop_executed']} GFLOP per step (matrix-core work as executed: the "
+                                  f"upsample convs as Winograd GEMMs; {head['gflop_direct']} GFLOP with direct convs)",
+                          "direct_equivalent_tflops": head["direct_equivalent_tflops"]},
     }
     log("dominant kernel and component kernels")
     out["roofline"] = _dominant_gemm(ctx, 50, fast=args.fast)
     ctx.set_precision(False)
     out["components"] = _components(ctx, 20)
-    del net, x, eps
-    ctx.close()
-    if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline("unet_step", () if cfg else ("--cond-only",),
-                                           note=" (C++ restatement of the CPU engine's UNet, OpenMP)")
-    return out
+    unet_entries = None
+    if args.configs and not args.fast and not args.f16_weights and cfg:
+        log("cfg4: EXACT batch 1, FAST batch 2 and 1")
+        unet_entries = {"exact_b2": head}
+        _, unet_entries["exact_b1"] = _unet_step_entry(ctx, net, inp, False, args.steps, args.warmup, False)
+        del net
+        ctx.set_precision(True)
+        fnet = UNet(ctx, params, f16_gemm=True)
+        _, unet_entries["fast_b2"] = _unet_step_entry(ctx, fnet, inp, True, args.steps, args.warmup, True)
+        _, unet_entries["fast_b1"] = _unet_step_entry(ctx, fnet, inp, False, args.steps, args.warmup, True)
+        fnet.close()
+        del fnet
+        ctx.set_precision(False)
+    else:
+        del net
+    return out, ctx, unet_entries
 
 
-def _vae_run(args, which):
-    """VAE decode ([1,64,64,4] latent -> [1,512,512,3]) or encode (2 x 512x512 images), f32."""
+# ---------------------------------------------------------------- cfg5
+
+def cfg5_vae(ctx, steps, f16_weights=False):
+    """VAE encode of one [1,512,512,3] image in U[-1,1] (and the pipeline's batch of
+    2) and decode of a [1,64,64,4] latent, f32 end to end."""
     from moebius_cpu_amd import engine as E
     from moebius_cpu_amd import synthetic as S
     from moebius_cpu_amd import vae_params as V
     from moebius_cpu_amd.vae import Vae
 
-    log("generating random-init VAE weights")
-    params = V.random_vae()
-    ctx = E.Context(0)
-    vae = Vae(ctx, params, f16_gemm=args.f16_weights)
-    if which == "decode":
-        lat = E.DeviceArray.from_numpy(ctx, S.normal(24, (1, 64, 64, 4)))
-        out = E.DeviceArray(ctx, (1, 512, 512, 3))
-        step = lambda: vae.decode(lat, out)  # noqa: E731
-        flops, direct = V.decode_flops(64, 64, winograd=True), V.decode_flops(64, 64)
-        wl = "Moebius VAE decode, [1,64,64,4] latent -> [1,512,512,3] image"
-    else:
-        img = E.DeviceArray.from_numpy(ctx, V.vae_images(seed=25, b=2, h=512, w=512))
-        noise = E.DeviceArray.from_numpy(ctx, S.normal(26, (2, 64, 64, 4)))
-        z = E.DeviceArray(ctx, (2, 64, 64, 4))
-        step = lambda: vae.encode(img, noise, z)  # noqa: E731
-        flops, direct = V.encode_flops(2, 512, 512, winograd=True), V.encode_flops(2, 512, 512)
-        wl = "Moebius VAE encode, 2 x [512,512,3] images (image + masked image) -> [2,64,64,4]"
-    for _ in range(max(args.warmup, 1)):
-        step()
-    ctx.synchronize()
-    ms = time_region(ctx, step, args.steps)
-    achieved = flops / (ms * 1e-3) / 1e12
-    wbytes, pbytes = vae.memory()
-    res = {
-        "metric": METRIC, "value": round(ms, 4), "unit": "ms", "higher_is_better": False,
-        "ms_per_step": round(ms, 4), "dtype": "f32",
-        "config": {"workload": wl + (", f16-stored weights" if args.f16_weights else "") + ", f32 arithmetic",
-                   "params_M": round(V.param_count() / 1e6, 1), "weight_bytes": wbytes, "pool_bytes": pbytes},
-        "roofline": {"bound": "mfma", "kernel": "whole pass (all kernels, one stream)",
-                     "achieved": round(achieved, 2), "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_F32_MFMA_TFLOPS, 4), "traffic": None,
-                     "work_per_launch": f"{flops / 1e9:.1f} GFLOP per pass (stride-1 3x3 convs as Winograd GEMMs; "
-                                        f"{direct / 1e9:.1f} GFLOP with direct convs)", "avg_launch_ms": round(ms, 4),
-                     "direct_equivalent_tflops": round(direct / (ms * 1e-3) / 1e12, 2)},
-    }
+    log("cfg5: generating random-init VAE weights")
+    vae = Vae(ctx, V.random_vae(), f16_gemm=f16_weights)
+    lat = E.DeviceArray.from_numpy(ctx, S.normal(24, (1, 64, 64, 4)))
+    img = E.DeviceArray(ctx, (1, 512, 512, 3))
+    dec_ms = warm_time(ctx, lambda: vae.decode(lat, img), steps)
+    res = {"workload": "Moebius VAE (SDXL AutoencoderKL f8d4), Kaiming weights, GroupNorm gamma 1 + N(0,0.05), "
+                       "beta N(0,0.05), f32" + (", f16-stored weights" if f16_weights else "")}
+    res["decode"] = {**mfma_entry(dec_ms, V.decode_flops(64, 64, winograd=True)),
+                     "direct_gflop": r(V.decode_flops(64, 64) / 1e9, 1),
+                     "direct_equivalent_tflops": r(V.decode_flops(64, 64) / (dec_ms * 1e-3) / 1e12, 2)}
+    for b in (1, 2):
+        im = E.DeviceArray.from_numpy(ctx, V.vae_images(seed=25, b=b, h=512, w=512))
+        nz = E.DeviceArray.from_numpy(ctx, S.normal(26, (b, 64, 64, 4)))
+        z = E.DeviceArray(ctx, (b, 64, 64, 4))
+        ms = warm_time(ctx, lambda: vae.encode(im, nz, z), steps)
+        res[f"encode_b{b}"] = {**mfma_entry(ms, V.encode_flops(b, 512, 512, winograd=True)),
+                               "direct_gflop": r(V.encode_flops(b, 512, 512) / 1e9, 1),
+                               "direct_equivalent_tflops": r(V.encode_flops(b, 512, 512) / (ms * 1e-3) / 1e12, 2)}
     vae.close()
-    ctx.close()
-    if not args.no_cpu:
-        res["cpu_baseline"] = cpu_baseline(f"vae_{which}", note=" (C++ restatement of the CPU engine's VAE, OpenMP)")
     return res
 
 
-WORKLOADS = {"unet_step": bench_unet, "conv3x3_gn_silu": bench_conv_gn,
-             "vae_decode": lambda a: _vae_run(a, "decode"), "vae_encode": lambda a: _vae_run(a, "encode")}
+# ---------------------------------------------------------------- assembly
+
+def attach_cpu(configs, cpu):
+    """Puts the CPU oracle's time next to each GPU entry (same inputs, same run)."""
+    if "error" in cpu:
+        configs["cpu_error"] = cpu["error"]
+        return
+    cores, c = cpu["cores"], cpu["configs"]
+    note = lambda s: {"cores": cores, "kind": "port", "sample": s}  # noqa: E731
+    if "cfg1" in configs and "cfg1" in c:
+        configs["cfg1"]["cpu"] = {"ms": c["cfg1"]["total_ms"], "conv_ms": c["cfg1"]["conv_ms"],
+                                  "groupnorm_silu_ms": c["cfg1"]["gn_silu_ms"],
+                                  **note("conv3x3 (Winograd) + GroupNorm+SiLU, median after one warm-up")}
+    if "cfg2" in configs and "sweep" in c:
+        for e in configs["cfg2"]["points"]:
+            k = f"{e['S']}x{e['C']}"
+            for name in ("conv1x1_f32", "conv1x1_f16w", "depthwise", "groupnorm_silu", "bias_residual"):
+                e[name]["cpu_ms"] = c["sweep"][k][name]
+        configs["cfg2"]["groupnorm_add_silu_2x64x64x320"]["cpu_ms"] = c["gn_add_silu_2x64x64x320"]
+        configs["cfg2"]["cpu"] = note("each kernel alone, median of >= 5 runs after one warm-up; the f16w 1x1 "
+                                      "on the f16-rounded weights")
+    if "cfg3" in configs and "resnet_block" in c:
+        configs["cfg3"]["cpu"] = {"ms": c["resnet_block"], **note("the same block, median after one warm-up")}
+    if "cfg4" in configs and "unet_b2" in c:
+        u = configs["cfg4"]
+        for key, ck in (("exact_b2", "unet_b2"), ("exact_b1", "unet_b1"), ("fast_b2", "unet_b2"),
+                        ("fast_b1", "unet_b1")):
+            u[key]["cpu_ms"] = c[ck]
+        u["cpu"] = note("the same step, median after one warm-up; the CPU engine's Fast preset keeps f32 "
+                        "arithmetic (f16-stored weights widened), so FAST is compared with the same CPU step")
+    if "cfg5" in configs and "vae_decode" in c:
+        v = configs["cfg5"]
+        v["decode"]["cpu_ms"] = c["vae_decode"]
+        v["encode_b1"]["cpu_ms"] = c["vae_encode_b1"]
+        v["encode_b2"]["cpu_ms"] = c.get("vae_encode_b2")
+        v["cpu"] = note("the same passes, median after one warm-up")
+
+
+def run_all(args):
+    out, ctx, unet_entries = bench_unet(args)
+    cpu_sets = []
+    if args.configs and unet_entries is not None:
+        configs = {}
+        log("cfg1: conv3x3 + GroupNorm+SiLU 64x64x320")
+        configs["cfg1"] = cfg1_conv_gn(ctx, args.steps)
+        log("cfg2: kernel sweep")
+        configs["cfg2"] = cfg2_sweep(ctx, args.steps)
+        log("cfg3: ResNet block 32x32")
+        configs["cfg3"] = cfg3_resnet(ctx, args.steps)
+        configs["cfg4"] = {"workload": "UNet denoise step, 512x512 (64x64x9 latent stack); EXACT = f32 MFMA; "
+                                       "FAST = f16-stored weights on f16 MFMA with f32 accumulate",
+                           **unet_entries}
+        configs["cfg5"] = cfg5_vae(ctx, max(3, args.steps // 4))
+        out["configs"] = configs
+        cpu_sets = ["configs"]
+    ctx.close()
+    if not args.no_cpu:
+        if cpu_sets:
+            cpu = cpu_run("configs")
+            attach_cpu(out["configs"], cpu)
+            if "error" not in cpu:
+                key = "unet_b2" if not args.cond_only else "unet_b1"
+                out["cpu_baseline"] = cpu_record(cpu["configs"][key], cpu["cores"],
+                                                 "the same denoise step (same seeded weights and inputs), median "
+                                                 "after one warm-up (C++ restatement of the CPU engine's UNet, "
+                                                 "OpenMP)")
+        else:
+            cpu = cpu_run("unet_step", () if not args.cond_only else ("--cond-only",))
+            if "error" not in cpu:
+                out["cpu_baseline"] = cpu_record(cpu["value"], cpu["cores"], cpu["sample"] +
+                                                 " (C++ restatement of the CPU engine's UNet, OpenMP)")
+    return out
+
+
+def single(args):
+    """One configuration alone (profiling runs): the headline-style line for it."""
+    from moebius_cpu_amd import engine as E
+
+    ctx = E.Context(0)
+    w = args.workload
+    if w == "conv3x3_gn_silu":
+        res = cfg1_conv_gn(ctx, args.steps)
+        ms = res["ms"]
+    elif w == "sweep":
+        res = cfg2_sweep(ctx, args.steps)
+        ms = sum(e[k]["ms"] for e in res["points"] for k in ("conv1x1_f32", "depthwise", "groupnorm_silu",
+                                                               "bias_residual"))
+    elif w == "resnet_block":
+        res = cfg3_resnet(ctx, args.steps)
+        ms = res["ms"]
+    elif w in ("vae_decode", "vae_encode"):
+        res = cfg5_vae(ctx, args.steps, args.f16_weights)
+        ms = res["decode"]["ms"] if w == "vae_decode" else res["encode_b1"]["ms"]
+    else:
+        raise SystemExit(f"unknown workload {w}")
+    ctx.close()
+    return {"metric": METRIC, "value": ms, "unit": "ms", "higher_is_better": False, "ms_per_step": ms,
+            "dtype": "f32", "config": {"workload": w}, "result": res}
 
 
 def main():
@@ -318,12 +484,15 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="unet_step", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="unet_step",
+                    choices=["unet_step", "conv3x3_gn_silu", "sweep", "resnet_block", "vae_decode", "vae_encode"])
     ap.add_argument("--cond-only", action="store_true", help="UNet: batch 1 (no CFG)")
     ap.add_argument("--f16-weights", action="store_true", help="UNet / VAE: f16-stored GEMM weights")
     ap.add_argument("--fast", action="store_true",
                     help="UNet: FAST precision (f16-stored weights, f16 MFMA with f32 accumulate)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-configs", dest="configs", action="store_false",
+                    help="UNet: the headline only, without the per-configuration block")
     ap.add_argument("--calibration-copy", action="store_true",
                     help="end with one 256 MiB device-to-device copy (the known-size reference that "
                          "scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -332,7 +501,7 @@ def main():
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}); the multi-GPU design is described in "
               "DESIGN.md and no multi-GPU figure is produced.", file=sys.stderr)
         sys.exit(2)
-    res = WORKLOADS[args.workload](args)
+    res = run_all(args) if args.workload == "unet_step" else single(args)
     if args.calibration_copy:
         from moebius_cpu_amd import engine as E
 

@@ -121,3 +121,46 @@ def resnet_block(seed: int = 3000, s=32, c_in=320, c_out=640, temb_dim=1280) -> 
         ws=S.kaiming(seed + 12, (c_out, c_in), c_in),
         bs=S.normal(seed + 13, (c_out,), std=0.02),
     )
+
+
+class ResnetBlockGpu:
+    """ResNet block 32x32 on the device: GN1+SiLU applied inside the Winograd conv1
+    (the reference's forward_prologue), time projection Linear(SiLU(temb)) folded
+    into GN2's shift, GN2+SiLU inside conv2, 1x1 skip with conv2's output as its
+    residual. Buffers are allocated once; a call allocates nothing."""
+
+    def __init__(self, ctx, wl, winograd=True):
+        from . import engine as E
+
+        self.E, self.ctx, self.wl = E, ctx, wl
+        c_in, c_out = wl.w1.shape[3], wl.w1.shape[0]
+        self.c_out = c_out
+        self.x = E.Tensor.from_numpy(ctx, wl.x)
+        self.gn1 = E.GroupNorm(ctx, 32, wl.eps, wl.gn1_g, wl.gn1_b)
+        self.gn2 = E.GroupNorm(ctx, 32, wl.eps, wl.gn2_g, wl.gn2_b)
+        self.conv1 = E.Conv3x3.same(ctx, c_in, c_out, E.Param(ctx, wl.w1), wl.b1, winograd=winograd)
+        self.conv2 = E.Conv3x3.same(ctx, c_out, c_out, E.Param(ctx, wl.w2), wl.b2, winograd=winograd)
+        self.lin = E.Conv1x1(ctx, wl.lin_w.shape[1], c_out, E.Param(ctx, wl.lin_w), wl.lin_b)
+        self.skip = E.Conv1x1(ctx, c_in, c_out, E.Param(ctx, wl.ws), wl.bs)
+        self.temb = E.Tensor.from_numpy(ctx, wl.temb.reshape(1, 1, 1, -1))
+        self.t = E.Tensor(ctx, *self.temb.shape)
+        self.tp, self.h, self.out, self.res = E.Tensor(ctx), E.Tensor(ctx), E.Tensor(ctx), E.Tensor(ctx)
+        n = self.x.n
+        self.aff1 = E.Affine(E.DeviceArray(ctx, (n * c_in,)), E.DeviceArray(ctx, (n * c_in,)), True)
+        self.aff2 = E.Affine(E.DeviceArray(ctx, (n * c_out,)), E.DeviceArray(ctx, (n * c_out,)), True)
+
+    def forward(self):
+        E, ctx = self.E, self.ctx
+        L = E.lib()
+        x, g1, g2 = self.x, self.gn1, self.gn2
+        E.check(L.mh_group_norm_affine(ctx.h, x.ptr, x.n, x.h, x.w, x.c, 32, g1.eps, g1.gamma.ptr, g1.beta.ptr,
+                                       None, self.aff1.scale.ptr, self.aff1.shift.ptr))
+        self.conv1.forward_prologue(x, self.aff1, self.h)
+        E.check(L.mh_math_eval(ctx.h, 1, self.temb.ptr, self.temb.nbytes // 4, self.t.ptr))  # SiLU(temb)
+        self.lin.forward(self.t, self.tp)
+        h = self.h
+        E.check(L.mh_group_norm_affine(ctx.h, h.ptr, h.n, h.h, h.w, h.c, 32, g2.eps, g2.gamma.ptr, g2.beta.ptr,
+                                       self.tp.ptr, self.aff2.scale.ptr, self.aff2.shift.ptr))
+        self.conv2.forward_prologue(h, self.aff2, self.out)
+        self.skip.forward(x, self.res, self.out)
+        return self.res

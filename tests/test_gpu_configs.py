@@ -65,24 +65,13 @@ def test_kernel_sweep(ctx, s, c, f16):
     assert np.array_equal(out.numpy().reshape(-1, c), oracle.add(pre, p.x.reshape(-1, c)))
 
 
-def _resnet_gpu(ctx, wl: W.ResnetBlock):
-    c_in, c_out = wl.w1.shape[3], wl.w1.shape[0]
-    x = T(ctx, wl.x)
-    gn1 = E.GroupNorm(ctx, 32, wl.eps, wl.gn1_g, wl.gn1_b)
-    conv1 = E.Conv3x3.same(ctx, c_in, c_out, E.Param(ctx, wl.w1), wl.b1)
-    lin = E.Conv1x1(ctx, wl.lin_w.shape[1], c_out, E.Param(ctx, wl.lin_w), wl.lin_b)
-    gn2 = E.GroupNorm(ctx, 32, wl.eps, wl.gn2_g, wl.gn2_b)
-    conv2 = E.Conv3x3.same(ctx, c_out, c_out, E.Param(ctx, wl.w2), wl.b2)
-    skip = E.Conv1x1(ctx, c_in, c_out, E.Param(ctx, wl.ws), wl.bs)
-    h, out, res = E.Tensor(ctx), E.Tensor(ctx), E.Tensor(ctx)
-    conv1.forward_prologue(x, gn1.affine(x, None, True), h)
-    t = T(ctx, wl.temb.reshape(1, 1, 1, -1))
-    E.silu_inplace(t)
-    tp = E.Tensor(ctx)
-    lin.forward(t, tp)
-    conv2.forward_prologue(h, gn2.affine(h, tp, True), out)
-    skip.forward(x, res, out)
-    return res.numpy()
+def _resnet_gpu(ctx, wl: W.ResnetBlock, winograd=True):
+    """The device chain bench.py times (workloads.ResnetBlockGpu), run twice: a
+    second call on the same buffers gives the same bits."""
+    blk = W.ResnetBlockGpu(ctx, wl, winograd=winograd)
+    first = blk.forward().numpy()
+    assert np.array_equal(blk.forward().numpy(), first)
+    return first
 
 
 def _resnet_oracle(wl: W.ResnetBlock):
@@ -94,9 +83,10 @@ def _resnet_oracle(wl: W.ResnetBlock):
     return oracle.conv1x1(wl.x, wl.ws, wl.bs, residual=out)
 
 
-def test_resnet_block_32x32_320_to_640(ctx):
+@pytest.mark.parametrize("winograd", [True, False])
+def test_resnet_block_32x32_320_to_640(ctx, winograd):
     wl = W.resnet_block()
-    got = _resnet_gpu(ctx, wl)
+    got = _resnet_gpu(ctx, wl, winograd)
     want = _resnet_oracle(wl)
     assert max_abs_rel(got, want) <= TOL
 

@@ -201,6 +201,26 @@ def test_unet_step_fast_matches_oracle(ctx, params):
     assert np.array_equal(net.forward_host(inp.x, inp.timestep, cfg=True), net.forward_host(inp.x, inp.timestep, cfg=True))
 
 
+def test_unet_fast_cond_only_matches_oracle(ctx, params):
+    """FAST at batch 1 (the cond-only steps of the Fast preset after its CFG steps,
+    src/preset.rs:76-82) against the oracle on the f16-rounded weights, per traced
+    block, at the FAST bar."""
+    gemm = {s.name for s in U.unet_specs() if s.gemm}
+    rounded = {k: (v.astype(np.float16).astype(np.float32) if k in gemm else v) for k, v in params.items()}
+    net = UNet(ctx, params, f16_gemm=True)
+    inp = U.unet_input(seed=5008)
+    eps_o, tr_o = oracle.UNet(rounded).forward(inp.x, inp.timestep, cfg=False, trace=True)
+    eps_g, tr_g = net.forward_traced(inp.x, inp.timestep, cfg=False)
+    assert list(tr_g) == list(tr_o) and eps_g.shape == (1, 64, 64, 4)
+    worst = 0.0
+    for name in tr_o:
+        err = max_abs_rel(tr_g[name], tr_o[name])
+        worst = max(worst, err)
+        assert err <= FAST_TOL, f"{name}: max-abs/max|ref| {err:.3e}"
+    print(f"cond-only: worst block max-abs/max|ref| = {worst:.3e}")
+    assert max_abs_rel(eps_g, eps_o) <= FAST_TOL
+
+
 def test_vae_keeps_f32_on_fast_context(ctx):
     """The VAE computes in f32 whatever the context precision (the SDXL VAE's
     activations overflow f16): the f32 bar holds on a FAST context."""

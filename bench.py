@@ -349,7 +349,7 @@ def bench_unet(args):
 
 # ---------------------------------------------------------------- cfg5
 
-def cfg5_vae(ctx, steps, f16_weights=False):
+def cfg5_vae(ctx, steps, f16_weights=False, which=("decode", "encode_b1", "encode_b2")):
     """VAE encode of one [1,512,512,3] image in U[-1,1] (and the pipeline's batch of
     2) and decode of a [1,64,64,4] latent, f32 end to end."""
     from moebius_cpu_amd import engine as E
@@ -361,13 +361,16 @@ def cfg5_vae(ctx, steps, f16_weights=False):
     vae = Vae(ctx, V.random_vae(), f16_gemm=f16_weights)
     lat = E.DeviceArray.from_numpy(ctx, S.normal(24, (1, 64, 64, 4)))
     img = E.DeviceArray(ctx, (1, 512, 512, 3))
-    dec_ms = warm_time(ctx, lambda: vae.decode(lat, img), steps)
     res = {"workload": "Moebius VAE (SDXL AutoencoderKL f8d4), Kaiming weights, GroupNorm gamma 1 + N(0,0.05), "
                        "beta N(0,0.05), f32" + (", f16-stored weights" if f16_weights else "")}
-    res["decode"] = {**mfma_entry(dec_ms, V.decode_flops(64, 64, winograd=True)),
-                     "direct_gflop": r(V.decode_flops(64, 64) / 1e9, 1),
-                     "direct_equivalent_tflops": r(V.decode_flops(64, 64) / (dec_ms * 1e-3) / 1e12, 2)}
+    if "decode" in which:
+        dec_ms = warm_time(ctx, lambda: vae.decode(lat, img), steps)
+        res["decode"] = {**mfma_entry(dec_ms, V.decode_flops(64, 64, winograd=True)),
+                         "direct_gflop": r(V.decode_flops(64, 64) / 1e9, 1),
+                         "direct_equivalent_tflops": r(V.decode_flops(64, 64) / (dec_ms * 1e-3) / 1e12, 2)}
     for b in (1, 2):
+        if f"encode_b{b}" not in which:
+            continue
         im = E.DeviceArray.from_numpy(ctx, V.vae_images(seed=25, b=b, h=512, w=512))
         nz = E.DeviceArray.from_numpy(ctx, S.normal(26, (b, 64, 64, 4)))
         z = E.DeviceArray(ctx, (b, 64, 64, 4))
@@ -469,9 +472,12 @@ def single(args):
     elif w == "resnet_block":
         res = cfg3_resnet(ctx, args.steps)
         ms = res["ms"]
-    elif w in ("vae_decode", "vae_encode"):
-        res = cfg5_vae(ctx, args.steps, args.f16_weights)
-        ms = res["decode"]["ms"] if w == "vae_decode" else res["encode_b1"]["ms"]
+    elif w == "vae_decode":
+        res = cfg5_vae(ctx, args.steps, args.f16_weights, which=("decode",))
+        ms = res["decode"]["ms"]
+    elif w == "vae_encode":
+        res = cfg5_vae(ctx, args.steps, args.f16_weights, which=("encode_b1",))
+        ms = res["encode_b1"]["ms"]
     else:
         raise SystemExit(f"unknown workload {w}")
     ctx.close()

@@ -117,6 +117,16 @@ void mh_context_destroy(MhContext *ctx) {
     delete ctx;
 }
 
+int32_t mh_context_set_tuning(MhContext *ctx, const char *key, const char *value) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(key, "key");
+        if (!mh::set_tuning(c.tune, key, value))
+            mh::fail(mh::kInvalidArgument, std::string("unknown tuning key or bad value: ") + key + " = " +
+                                               (value ? value : "(default)"));
+    });
+}
+
 int32_t mh_context_set_precision(MhContext *ctx, uint32_t precision) {
     return guard([&] {
         mh::Context &c = C(ctx);

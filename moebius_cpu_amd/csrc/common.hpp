@@ -45,6 +45,23 @@ struct Error : std::runtime_error {
 
 enum class Precision : uint32_t { Exact = 0, Fast = 1 };
 
+// Tuning overrides for A/B runs and tests, read once from the environment
+// (MOEBIUS_HIP_GEMM_PLAN, _GN_IN_MAXC, _DW_TILED, _TAP_HEADS, _CROSS_HEADS)
+// when a context is created and changed with set_tuning (mh_context_set_tuning).
+// The defaults are the measured choices; nothing on the hot path reads the
+// environment.
+struct Tuning {
+    int gemm_bm = 0, gemm_bn = 0, gemm_splits = 0;  // forced GEMM tiling, 0: the planner's
+    int gn_in_maxc = -1;   // GroupNorm applied in proj_in's loads up to this width; -1: per precision
+    int dw_tiled = 1;      // 0: the register-window depthwise kernel
+    int tap_tile = -1;     // tap filter: -1 default; 0 the per-thread kernel; 4 / 8 the tile kernel's heads
+    int tap_heads = 0;     // per-thread tap filter heads per thread (0: default)
+    int cross_heads = 0;   // cross-lambda heads per thread (0: default)
+};
+// Sets `key` from its text form (the environment variable's syntax); value NULL
+// or "" restores the default. False for an unknown key or a malformed value.
+bool set_tuning(Tuning &t, const char *key, const char *value);
+
 // Device arena for kernel scratch (split-K partials, norm partials): grown on
 // demand, kept for the context's life, like the reference's `Scratch` panels
 // (src/engine/mod.rs:25-34). Growth synchronises the stream first, since
@@ -70,6 +87,7 @@ struct Context {
     int cu_count = 0;
     std::string arch;
     Workspace ws;
+    Tuning tune;
 
     explicit Context(int dev);
     ~Context();

@@ -1,4 +1,6 @@
 // Context, workspace and error plumbing.
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <sstream>
 
@@ -32,7 +34,59 @@ void *Workspace::get(size_t bytes, hipStream_t stream) {
     return ptr_;
 }
 
+bool set_tuning(Tuning &t, const char *key, const char *value) {
+    const std::string k = key ? key : "";
+    const bool clear = !value || !*value;
+    const std::string v = clear ? "" : value;
+    auto to_int = [&](int &dst, int def) {
+        if (clear) {
+            dst = def;
+            return true;
+        }
+        char *end = nullptr;
+        const long x = std::strtol(v.c_str(), &end, 10);
+        if (!end || *end) return false;
+        dst = int(x);
+        return true;
+    };
+    if (k == "gemm_plan") {
+        if (clear) {
+            t.gemm_bm = t.gemm_bn = t.gemm_splits = 0;
+            return true;
+        }
+        int bm = 0, bn = 0, sp = 0;
+        if (std::sscanf(v.c_str(), "%d,%d,%d", &bm, &bn, &sp) != 3 || sp < 1) return false;
+        t.gemm_bm = bm, t.gemm_bn = bn, t.gemm_splits = sp;
+        return true;
+    }
+    if (k == "gn_in_maxc") return to_int(t.gn_in_maxc, -1);
+    if (k == "dw_tiled") return to_int(t.dw_tiled, 1);
+    if (k == "cross_heads") return to_int(t.cross_heads, 0);
+    if (k == "tap_heads") {
+        if (clear) {
+            t.tap_tile = -1, t.tap_heads = 0;
+            return true;
+        }
+        if (v[0] == 't') {
+            t.tap_tile = std::atoi(v.c_str() + 1) == 4 ? 4 : 8;
+            t.tap_heads = 0;
+        } else {
+            t.tap_tile = 0;
+            if (!to_int(t.tap_heads, 0)) return false;
+        }
+        return true;
+    }
+    return false;
+}
+
 Context::Context(int dev) : device(dev) {
+    static const char *const env_keys[][2] = {{"MOEBIUS_HIP_GEMM_PLAN", "gemm_plan"},
+                                              {"MOEBIUS_HIP_GN_IN_MAXC", "gn_in_maxc"},
+                                              {"MOEBIUS_HIP_DW_TILED", "dw_tiled"},
+                                              {"MOEBIUS_HIP_TAP_HEADS", "tap_heads"},
+                                              {"MOEBIUS_HIP_CROSS_HEADS", "cross_heads"}};
+    for (const auto &kv : env_keys)
+        if (const char *e = std::getenv(kv[0])) set_tuning(tune, kv[1], e);
     int count = 0;
     HIP_CHECK(hipGetDeviceCount(&count));
     if (dev < 0 || dev >= count) fail(kInvalidArgument, "device ordinal out of range");

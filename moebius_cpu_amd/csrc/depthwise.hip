@@ -312,8 +312,7 @@ void depthwise3x3(Context &ctx, const float *x, int n, int h, int w, int c, cons
     }
     const bool vec4 = co % 4 == 0 && aligned16(x) && aligned16(weight) && aligned16(bias) && aligned16(out) &&
                       aligned16(pro.scale) && aligned16(pro.shift);
-    const char *tiled_env = std::getenv("MOEBIUS_HIP_DW_TILED");  // A/B override: 0 = register-window kernel
-    const int tiled = tiled_env ? std::atoi(tiled_env) : 1;
+    const int tiled = ctx.tune.dw_tiled;  // A/B override: 0 = register-window kernel
     if (vec4 && tiled) {
         if (prologue) launch_dw_tile<true>(ctx, x, n, h, w, c, weight, bias, epilogue, pro, out);
         else launch_dw_tile<false>(ctx, x, n, h, w, c, weight, bias, epilogue, pro, out);

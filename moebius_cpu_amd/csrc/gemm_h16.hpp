@@ -324,11 +324,10 @@ void launch_cfg_h16(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi,
 template <int MODE, bool PRO, bool F16, bool BVEC>
 void launch_tiles_h16(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
     Plan pl = plan_h16(p.M, p.N, p.K, int(ceil_div(ctx.cu_count, batch)), MODE <= kDenseScalar);
-    // MOEBIUS_HIP_GEMM_PLAN="bm,bn,splits" forces the tiling, as for the f32 kernel.
-    if (const char *force = std::getenv("MOEBIUS_HIP_GEMM_PLAN")) {
-        int bm = 0, bn = 0, sp = 0;
-        if (std::sscanf(force, "%d,%d,%d", &bm, &bn, &sp) == 3 && bm == bn && (bm == 32 || bm == 64 || bm == 128) &&
-            sp >= 1) {
+    // The context's gemm_plan tuning forces the tiling, as for the f32 kernel.
+    if (ctx.tune.gemm_splits > 0) {
+        const int bm = ctx.tune.gemm_bm, bn = ctx.tune.gemm_bn, sp = ctx.tune.gemm_splits;
+        if (bm == bn && (bm == 32 || bm == 64 || bm == 128)) {
             const int ktiles = int(ceil_div(p.K, BKH));
             const int per = int(ceil_div(ktiles, sp));
             pl = Plan{bm, bn, int(ceil_div(ktiles, per)), per * BKH};

@@ -900,11 +900,12 @@ void launch_cfg(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int
 template <int MODE, bool PRO, bool F16, bool BVEC>
 void launch_tiles(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
     Plan pl = plan_for(p.M, p.N, p.K, int(ceil_div(ctx.cu_count, batch)), MODE <= kDenseScalar);
-    // MOEBIUS_HIP_GEMM_PLAN="bm,bn,splits" forces the tiling (tuning and A/B runs),
-    // as MOEBIUS_GEMM selects the CPU engine's GEMM backend (src/engine/gemm.rs:57-60).
-    if (const char *force = std::getenv("MOEBIUS_HIP_GEMM_PLAN")) {
-        int bm = 0, bn = 0, sp = 0;
-        const bool parsed = std::sscanf(force, "%d,%d,%d", &bm, &bn, &sp) == 3 && sp >= 1;
+    // The context's gemm_plan tuning ("bm,bn,splits") forces the tiling (tuning and
+    // A/B runs), as MOEBIUS_GEMM selects the CPU engine's GEMM backend
+    // (src/engine/gemm.rs:57-60).
+    if (ctx.tune.gemm_splits > 0) {
+        const int bm = ctx.tune.gemm_bm, bn = ctx.tune.gemm_bn, sp = ctx.tune.gemm_splits;
+        const bool parsed = true;
         const bool square = (bm == 32 || bm == 64 || bm == 128) && (bn == 32 || bn == 64 || bn == 128) &&
                             (bm == 32) == (bn == 32);
         const bool wide = (bm == 32 && bn == 64) || (bm == 64 && bn == 32);

@@ -723,11 +723,11 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
     // pixels (its value rows are then staged at most 2.4 times over: 64x64 x 40
     // 59.6 -> 47.2 us), else the per-thread kernel with 4 heads per thread
     // (32x32 x 80: 28.4 us, 16x16 x 160: 18.7 us; the tile kernel 34.7 / 35.0).
-    // MOEBIUS_HIP_TAP_HEADS forces a variant for A/B runs: "t8" / "t4" the tile
-    // kernel with 8 / 4 heads per thread; 1, 2, 4 or 8 the per-thread kernel.
-    const char *force = std::getenv("MOEBIUS_HIP_TAP_HEADS");
-    int tile_hg = (!force && std::min(256 / (2 * v4), ww) >= 10) ? 4 : 0;
-    if (force && force[0] == 't') tile_hg = std::atoi(force + 1) == 4 ? 4 : 8;
+    // The context's tap_heads tuning forces a variant for A/B runs: "t8" / "t4" the
+    // tile kernel with 8 / 4 heads per thread; 1, 2, 4 or 8 the per-thread kernel.
+    const bool forced = ctx.tune.tap_tile >= 0;
+    int tile_hg = (!forced && std::min(256 / (2 * v4), ww) >= 10) ? 4 : 0;
+    if (forced) tile_hg = ctx.tune.tap_tile;
     if (tile_hg && (kHeads / tile_hg) * v4 <= 256) {
         const int tpp = (kHeads / tile_hg) * v4, tx = std::max(1, std::min(256 / tpp, ww));
         const size_t lds = (size_t(2) * (tx + kWin - 1) * v4 + size_t(2) * tx * (kWin * kHeads / 4)) * 16 +
@@ -743,8 +743,8 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
         return;
     }
     int hg = 4;
-    if (force) {
-        const int want = std::atoi(force);
+    if (forced) {
+        const int want = ctx.tune.tap_heads;
         if (want == 1 || want == 2 || want == 4 || want == 8) hg = want;
     }
     const int tpp = (kHeads / hg) * v4;
@@ -803,8 +803,8 @@ void cross_lambda(Context &ctx, const float *q, const float *e, const float *lam
             break;
         }
     }
-    if (const char *f = std::getenv("MOEBIUS_HIP_CROSS_HEADS")) {  // A/B override: 2, 4 or 8
-        const int want = std::atoi(f);
+    if (ctx.tune.cross_heads) {  // A/B override: 2, 4 or 8
+        const int want = ctx.tune.cross_heads;
         if ((want == 2 || want == 4 || want == 8) && 256 / ((kHeads / want) * k4) >= 1) hg = want;
     }
     const int P = std::max(1, 256 / ((kHeads / hg) * k4));

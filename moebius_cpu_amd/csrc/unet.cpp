@@ -499,8 +499,8 @@ struct MixTransformer {
         // steps: EXACT 7.764 ms unfused, 7.728 to 640, 7.773 to 1280; FAST 5.744,
         // 5.731 to 320, 5.778 to 640).
         DT h;
-        const char *mc = std::getenv("MOEBIUS_HIP_GN_IN_MAXC");  // tuning override, read per call
-        const int max_c = mc ? std::atoi(mc) : (e.ctx.precision == Precision::Fast ? 320 : 640);
+        const int max_c = e.ctx.tune.gn_in_maxc >= 0 ? e.ctx.tune.gn_in_maxc
+                                                      : (e.ctx.precision == Precision::Fast ? 320 : 640);
         if (x.c <= max_c) {
             float *ss = norm.affine(e, x, nullptr);
             h = proj_in.fwd_gn_in(e, x, ss);

@@ -50,6 +50,10 @@ class Context:
     def set_precision(self, fast: bool):
         check(lib().mh_context_set_precision(self.h, _lib.PRECISION_FAST if fast else _lib.PRECISION_EXACT))
 
+    def set_tuning(self, key: str, value=None):
+        """One tuning override of this context (mh_context_set_tuning); None restores the default."""
+        check(lib().mh_context_set_tuning(self.h, key.encode(), None if value is None else str(value).encode()))
+
     @property
     def arch(self) -> str:
         buf = ctypes.create_string_buffer(64)

@@ -161,8 +161,8 @@ def test_conv3x3_odd_sizes_f16_weights(ctx, n, h, w, ci, co, up):
                                       # 16x16 LDS tiles of 4 channel quads, with partial tiles and partial quad groups
                                       (9, 13, 72, "relu"), (17, 6, 136, "none"), (10, 11, 200, "glu_silu"),
                                       (16, 16, 256, "glu_silu"), (8, 8, 8, "none")])
-def test_depthwise_register_blocks_and_tails(ctx, h, w, c, ep, tiled, monkeypatch):
-    monkeypatch.setenv("MOEBIUS_HIP_DW_TILED", tiled)
+def test_depthwise_register_blocks_and_tails(ctx, h, w, c, ep, tiled, tune):
+    tune("dw_tiled", tiled)
     x = hashed(h * w * c, 7919, 211, 211.0, 0.5).reshape(1, h, w, c)
     wt = hashed(9 * c, 31, 17, 17.0, 0.5).reshape(3, 3, c)
     b = (np.arange(c, dtype=np.float32) * np.float32(0.01) - np.float32(0.2)).astype(np.float32)
@@ -231,7 +231,7 @@ def test_conv1x1_residual_transform_and_second_residual(ctx, n, h, w, c, f16):
 # each within the f32 bar of the oracle
 @pytest.mark.parametrize("plan", ["32,32,1", "32,32,3", "64,64,1", "64,64,2", "128,64,1", "64,128,3", "128,128,2"])
 @pytest.mark.parametrize("c_out", [72, 70])
-def test_conv1x1_every_tiling(ctx, plan, c_out, monkeypatch):
+def test_conv1x1_every_tiling(ctx, plan, c_out, tune):
     rng = np.random.default_rng(c_out)
     n, h, w, c = 2, 9, 11, 200
     x = rng.standard_normal((n, h, w, c)).astype(np.float32)
@@ -246,7 +246,7 @@ def test_conv1x1_every_tiling(ctx, plan, c_out, monkeypatch):
     param = E.Param(ctx, wt)
     dev = {k: E.DeviceArray.from_numpy(ctx, v) for k, v in dict(x=x, r=r, r2=r2, b=b, sc=sc, sh=sh).items()}
     out = E.DeviceArray(ctx, (n, h, w, c_out))
-    monkeypatch.setenv("MOEBIUS_HIP_GEMM_PLAN", plan)
+    tune("gemm_plan", plan)
     E.check(E.lib().mh_conv1x1_fused(ctx.h, dev["x"].ptr, n, h, w, c, param.ptr, param.dtype, c_out, dev["b"].ptr,
                                      dev["r"].ptr, dev["sc"].ptr, dev["sh"].ptr, 1, dev["r2"].ptr, out.ptr))
     got = out.numpy()

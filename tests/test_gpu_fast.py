@@ -67,9 +67,9 @@ def conv3(ctx, x, w, b=None, stride=1, pad=(1, 1, 1, 1), up=False, prologue=None
 @pytest.mark.parametrize("plan", [None, "32,32,1", "32,32,3", "64,64,1", "64,64,2", "128,128,1", "128,128,2"])
 @pytest.mark.parametrize("c_out,c_in", [(72, 320), (70, 200), (40, 9)])
 @pytest.mark.parametrize("f16", [False, True])
-def test_conv1x1_fast_every_tiling(ctx, plan, c_out, c_in, f16, monkeypatch):
+def test_conv1x1_fast_every_tiling(ctx, plan, c_out, c_in, f16, tune):
     if plan:
-        monkeypatch.setenv("MOEBIUS_HIP_GEMM_PLAN", plan)
+        tune("gemm_plan", plan)
     rng = np.random.default_rng(c_out * 1000 + c_in)
     x = rng.standard_normal((2, 11, 13, c_in)).astype(np.float32)
     w = (rng.standard_normal((c_out, c_in)) * np.sqrt(2.0 / c_in)).astype(np.float32)
@@ -118,9 +118,9 @@ def test_conv3x3_fast_gn_prologue(ctx, ci, up):
 
 @pytest.mark.parametrize("row_group", [0, 8])
 @pytest.mark.parametrize("plan", [None, "32,32,1", "64,64,1", "64,64,2"])
-def test_gemm_nt_fast(ctx, row_group, plan, monkeypatch):
+def test_gemm_nt_fast(ctx, row_group, plan, tune):
     if plan:
-        monkeypatch.setenv("MOEBIUS_HIP_GEMM_PLAN", plan)
+        tune("gemm_plan", plan)
     rng = np.random.default_rng(9)
     m, n, k = 304, 226, 40
     a = rng.standard_normal((m, k)).astype(np.float32)

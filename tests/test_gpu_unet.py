@@ -51,11 +51,11 @@ def test_softmax_lambda_kernel(ctx, nb, rows, k):
 @pytest.mark.parametrize("nb,hh,ww,vd", [(2, 16, 12, 40), (1, 7, 5, 8), (2, 16, 16, 160), (1, 20, 9, 80),
                                          (1, 9, 70, 40)])
 @pytest.mark.parametrize("heads_per_thread", ["default", "t8", "t4", "8", "4", "2"])
-def test_tap_filter_kernel_bit_exact(ctx, nb, hh, ww, vd, heads_per_thread, monkeypatch):
+def test_tap_filter_kernel_bit_exact(ctx, nb, hh, ww, vd, heads_per_thread, tune):
     if heads_per_thread == "default":
-        monkeypatch.delenv("MOEBIUS_HIP_TAP_HEADS", raising=False)
+        tune("tap_heads", None)
     else:
-        monkeypatch.setenv("MOEBIUS_HIP_TAP_HEADS", heads_per_thread)
+        tune("tap_heads", heads_per_thread)
     rng = np.random.default_rng(hh * ww + vd)
     a = rng.standard_normal((nb, hh * ww, 8, 226)).astype(np.float32)
     v = rng.standard_normal((nb, hh * ww, vd)).astype(np.float32)
@@ -105,11 +105,11 @@ def test_position_term_kernel_bit_exact(ctx, br0, nb, k):
 # block; MOEBIUS_HIP_CROSS_HEADS forces each variant, 8 included.
 @pytest.mark.parametrize("br0,nb,hw,k", [(0, 2, 4096, 40), (0, 2, 1024, 80), (0, 2, 256, 160), (1, 1, 37, 40)])
 @pytest.mark.parametrize("heads", [None, "2", "4", "8"])
-def test_cross_lambda_kernel(ctx, br0, nb, hw, k, heads, monkeypatch):
+def test_cross_lambda_kernel(ctx, br0, nb, hw, k, heads, tune):
     if heads:
-        monkeypatch.setenv("MOEBIUS_HIP_CROSS_HEADS", heads)
+        tune("cross_heads", heads)
     else:
-        monkeypatch.delenv("MOEBIUS_HIP_CROSS_HEADS", raising=False)
+        tune("cross_heads", None)
     rng = np.random.default_rng(k + hw)
     q = rng.standard_normal((nb, hw, 8 * k)).astype(np.float32)
     e = rng.standard_normal((hw, 10, k)).astype(np.float32)
@@ -141,9 +141,9 @@ def test_cross_lambda_kernel(ctx, br0, nb, hw, k, heads, monkeypatch):
 @pytest.mark.parametrize("row_group", [0, 4, 8])
 @pytest.mark.parametrize("plan", [None, "32,32,1", "64,64,1", "64,64,2"])
 @pytest.mark.parametrize("with_bias", [False, True])
-def test_gemm_nt_kernel(ctx, row_group, plan, with_bias, monkeypatch):
+def test_gemm_nt_kernel(ctx, row_group, plan, with_bias, tune):
     if plan:
-        monkeypatch.setenv("MOEBIUS_HIP_GEMM_PLAN", plan)
+        tune("gemm_plan", plan)
     rng = np.random.default_rng(9)
     m, n, k = 304, 226, 40
     a = rng.standard_normal((m, k)).astype(np.float32)
@@ -235,15 +235,15 @@ def test_unet_step_is_deterministic_and_batch_consistent(ctx, gnet):
 
 
 @pytest.mark.parametrize("fast", [False, True])
-def test_unet_groupnorm_into_proj_in_is_bit_exact(ctx, gnet, fast, monkeypatch):
+def test_unet_groupnorm_into_proj_in_is_bit_exact(ctx, gnet, fast, tune):
     """The transformers' GroupNorm applied inside proj_in's operand loads gives the
     bits of the separate apply pass, at every channel count it is used for."""
     inp = U.unet_input(seed=5007)
     ctx.set_precision(fast)
     try:
-        monkeypatch.setenv("MOEBIUS_HIP_GN_IN_MAXC", "0")
+        tune("gn_in_maxc", "0")
         apart = gnet.forward_host(inp.x, inp.timestep, cfg=True)
-        monkeypatch.setenv("MOEBIUS_HIP_GN_IN_MAXC", "1280")
+        tune("gn_in_maxc", "1280")
         fused = gnet.forward_host(inp.x, inp.timestep, cfg=True)
     finally:
         ctx.set_precision(False)

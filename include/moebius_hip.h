@@ -334,6 +334,64 @@ int32_t mh_unet_forward_traced(MhUNet *unet, const float *x_dev, uint32_t timest
 /* HBM held by the weights and by the activation pool. */
 int32_t mh_unet_memory(MhUNet *unet, uint64_t *weight_bytes, uint64_t *pool_bytes);
 
+/* ---- samplers and the denoise loop (src/scheduler.rs, src/pipeline.rs) ---- */
+
+#define MH_SPACING_LEADING 0u  /* src/scheduler.rs:24-29 */
+#define MH_SPACING_TRAILING 1u
+#define MH_SOLVER_DDIM 0u      /* src/preset.rs: Solver */
+#define MH_SOLVER_DPMPP_2M 1u
+
+/* src/scheduler.rs:30-76 `Ddim::new(steps, strength, spacing).timesteps()`, on the
+ * host: out (room for 1000) receives the timesteps denoised, *count their number,
+ * *pure_noise 1 when the loop starts from noise alone (strength >= 1). */
+int32_t mh_schedule_timesteps(uint32_t steps, double strength, uint32_t spacing, uint32_t *out, uint32_t *count,
+                              uint32_t *pure_noise);
+/* src/scheduler.rs:159-172, on the host: the 1000 f32 cumulative alpha products. */
+int32_t mh_schedule_alphas_cumprod(float *out);
+
+/* src/scheduler.rs `Ddim` + `Dpm2M` over device arrays of len floats. */
+typedef struct MhScheduler MhScheduler;
+int32_t mh_scheduler_create(MhContext *ctx, uint32_t steps, double strength, uint32_t spacing, uint64_t len,
+                            MhScheduler **out);
+void mh_scheduler_destroy(MhScheduler *s);
+/* src/scheduler.rs:80-86: out = sqrt(at) x0 + sqrt(1 - at) noise. */
+int32_t mh_scheduler_add_noise(MhScheduler *s, const float *x0, const float *noise, uint32_t t, float *out);
+/* src/pipeline.rs:330-336 then src/scheduler.rs:88-97: eps = eps_c ? eps_u +
+ * guidance (eps_c - eps_u) : eps_u; one DDIM step of x (in place) at timestep t. */
+int32_t mh_scheduler_ddim_step(MhScheduler *s, const float *eps_u, const float *eps_c, float guidance, uint32_t t,
+                               float *x);
+/* The same combine, then src/scheduler.rs:123-156: one DPM-Solver++(2M) step of
+ * x from timesteps[i] to the next timestep (first order after create/restart). */
+int32_t mh_scheduler_dpm_step(MhScheduler *s, const float *eps_u, const float *eps_c, float guidance, uint32_t i,
+                              float *x);
+/* src/scheduler.rs:117-120 */
+int32_t mh_scheduler_dpm_restart(MhScheduler *s);
+
+/* The sampling fields of src/preset.rs:27-50 `InpaintParams`. */
+typedef struct MhDenoiseParams {
+    double strength;  /* 0.99 in both presets */
+    float guidance;   /* CFG scale, 2.5 */
+    uint32_t steps;   /* 1..1000 (Exact 20, Fast 10) */
+    uint32_t spacing; /* MH_SPACING_* */
+    uint32_t solver;  /* MH_SOLVER_* */
+    int32_t cfg_steps; /* < 0: CFG on every step; n: the first n steps, then cond-only (Fast: 3) */
+    uint32_t reserved; /* 0 */
+} MhDenoiseParams;
+
+/* Called on the caller's thread after each finished step; nonzero cancels. */
+typedef int32_t (*MhStepFn)(void *user, uint32_t done, uint32_t total);
+
+/* src/pipeline.rs:295-345 (steps 7-8) resident on the device. Device arrays:
+ * z_img, init, z_masked, latents [1,64,64,4]; mask_lat [64 * 64]. x starts as init
+ * (strength >= 1; z_img may then be NULL) or add_noise(z_img, init, t0); each step
+ * runs the UNet on [x | mask | z_masked] (CFG batch 2 while CFG is on), combines
+ * u + g (c - u) and updates x with the solver (DPM restarts where CFG stops);
+ * progress(user, done, total) after each step. latents receives the final x.
+ * Returns when done; MH_ERR_CANCELLED leaves latents untouched. */
+int32_t mh_unet_denoise(MhUNet *unet, const float *z_img, const float *init, const float *mask_lat,
+                        const float *z_masked, const MhDenoiseParams *params, MhStepFn progress, void *user,
+                        float *latents);
+
 /* ---- VAE (src/vae) ---- */
 
 /* src/vae/mod.rs:88-103 `Vae::load` from the converter tensors of vae.safetensors

@@ -100,6 +100,15 @@ SIGNATURES = {
     "mh_unet_forward_host": (_i32, [_vp, _vp, _u32, _u32, _vp]),
     "mh_unet_forward_traced": (_i32, [_vp, _vp, _u32, _u32, _vp, _vp, _vp]),
     "mh_unet_memory": (_i32, [_vp, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
+    "mh_schedule_timesteps": (_i32, [_u32, ctypes.c_double, _u32, _u32p, _u32p, _u32p]),
+    "mh_schedule_alphas_cumprod": (_i32, [_vp]),
+    "mh_scheduler_create": (_i32, [_vp, _u32, ctypes.c_double, _u32, _u64, ctypes.POINTER(_vp)]),
+    "mh_scheduler_destroy": (None, [_vp]),
+    "mh_scheduler_add_noise": (_i32, [_vp, _vp, _vp, _u32, _vp]),
+    "mh_scheduler_ddim_step": (_i32, [_vp, _vp, _vp, _f32, _u32, _vp]),
+    "mh_scheduler_dpm_step": (_i32, [_vp, _vp, _vp, _f32, _u32, _vp]),
+    "mh_scheduler_dpm_restart": (_i32, [_vp]),
+    "mh_unet_denoise": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "mh_vae_create": (_i32, [_vp, _vp, _u32, _vp]),
     "mh_vae_destroy": (None, [_vp]),
     "mh_vae_encode": (_i32, [_vp, _vp, _u32, _u32, _u32, _vp, _vp, _vp, _vp]),
@@ -121,6 +130,17 @@ class NamedTensor(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char_p), ("data", ctypes.c_void_p), ("dtype", ctypes.c_uint32),
                 ("reserved", ctypes.c_uint32), ("numel", ctypes.c_uint64)]
 
+
+class DenoiseParams(ctypes.Structure):
+    """include/moebius_hip.h MhDenoiseParams (src/preset.rs InpaintParams' sampling fields)."""
+    _fields_ = [("strength", ctypes.c_double), ("guidance", ctypes.c_float), ("steps", ctypes.c_uint32),
+                ("spacing", ctypes.c_uint32), ("solver", ctypes.c_uint32), ("cfg_steps", ctypes.c_int32),
+                ("reserved", ctypes.c_uint32)]
+
+
+SPACING = {"leading": 0, "trailing": 1}
+SOLVER = {"ddim": 0, "dpm": 1}
+STEP_FN = ctypes.CFUNCTYPE(ctypes.c_int32, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32)
 
 TRACE_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p, ctypes.c_uint32,
                             ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32)

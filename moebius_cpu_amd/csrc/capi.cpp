@@ -3,14 +3,17 @@
 // exception into a status code plus a thread-local message, mirroring the
 // reference's FFI guard (src/ffi.rs:90-103) and moebius_last_error
 // (include/moebius_cpu.h:50-51). Nothing throws across the boundary.
+#include <algorithm>
 #include <cstring>
 #include <exception>
 #include <memory>
 #include <new>
 #include <string>
+#include <vector>
 
 #include "../../include/moebius_hip.h"
 #include "common.hpp"
+#include "denoise.hpp"
 #include "kernels.hpp"
 #include "pool.hpp"
 #include "unet.hpp"
@@ -29,6 +32,11 @@ struct MhUNet {
         if (x_dev) (void)hipFree(x_dev);
         if (eps_dev) (void)hipFree(eps_dev);
     }
+};
+
+struct MhScheduler {
+    MhContext *owner;
+    std::unique_ptr<mh::Sampler> s;
 };
 
 struct MhVae {
@@ -852,3 +860,114 @@ int32_t mh_selftest_mfma_f32(MhContext *ctx, const float *a, const float *b, flo
 }
 
 }  // extern "C"
+
+// ---- samplers and the denoise loop
+
+static mh::Spacing spacing_of(uint32_t v) {
+    if (v == MH_SPACING_LEADING) return mh::Spacing::Leading;
+    if (v == MH_SPACING_TRAILING) return mh::Spacing::Trailing;
+    mh::fail(mh::kInvalidArgument, "unknown spacing");
+}
+
+int32_t mh_schedule_timesteps(uint32_t steps, double strength, uint32_t spacing, uint32_t *out, uint32_t *count,
+                              uint32_t *pure_noise) {
+    return guard([&] {
+        need(out, "out");
+        need(count, "count");
+        const mh::Schedule s(int(std::min<uint32_t>(steps, 1u << 30)), strength, spacing_of(spacing));
+        for (size_t i = 0; i < s.timesteps.size(); ++i) out[i] = uint32_t(s.timesteps[i]);
+        *count = uint32_t(s.timesteps.size());
+        if (pure_noise) *pure_noise = s.pure_noise_start ? 1u : 0u;
+    });
+}
+
+int32_t mh_schedule_alphas_cumprod(float *out) {
+    return guard([&] {
+        need(out, "out");
+        const std::vector<float> a = mh::scaled_linear_alphas_cumprod();
+        std::memcpy(out, a.data(), a.size() * sizeof(float));
+    });
+}
+
+int32_t mh_scheduler_create(MhContext *ctx, uint32_t steps, double strength, uint32_t spacing, uint64_t len,
+                            MhScheduler **out) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(out, "out");
+        *out = nullptr;
+        auto s = std::make_unique<MhScheduler>();
+        s->owner = ctx;
+        s->s = std::make_unique<mh::Sampler>(c, int(std::min<uint32_t>(steps, 1u << 30)), strength,
+                                             spacing_of(spacing), int64_t(len));
+        *out = s.release();
+    });
+}
+
+void mh_scheduler_destroy(MhScheduler *s) {
+    if (!s) return;
+    (void)hipSetDevice(s->owner->ctx.device);
+    delete s;
+}
+
+static mh::Sampler &sampler(MhScheduler *s) {
+    if (!s) mh::fail(mh::kInvalidArgument, "scheduler is NULL");
+    C(s->owner);
+    return *s->s;
+}
+
+int32_t mh_scheduler_add_noise(MhScheduler *s, const float *x0, const float *noise, uint32_t t, float *out) {
+    return guard([&] {
+        mh::Sampler &p = sampler(s);
+        need(x0, "x0");
+        need(noise, "noise");
+        need(out, "out");
+        p.add_noise(x0, noise, int(std::min<uint32_t>(t, 1u << 30)), out);
+    });
+}
+
+int32_t mh_scheduler_ddim_step(MhScheduler *s, const float *eps_u, const float *eps_c, float guidance, uint32_t t,
+                               float *x) {
+    return guard([&] {
+        mh::Sampler &p = sampler(s);
+        need(eps_u, "eps");
+        need(x, "x");
+        p.ddim_step(eps_u, eps_c, guidance, int(std::min<uint32_t>(t, 1u << 30)), x);
+    });
+}
+
+int32_t mh_scheduler_dpm_step(MhScheduler *s, const float *eps_u, const float *eps_c, float guidance, uint32_t i,
+                              float *x) {
+    return guard([&] {
+        mh::Sampler &p = sampler(s);
+        need(eps_u, "eps");
+        need(x, "x");
+        p.dpm_step(eps_u, eps_c, guidance, int(std::min<uint32_t>(i, 1u << 30)), x);
+    });
+}
+
+int32_t mh_scheduler_dpm_restart(MhScheduler *s) {
+    return guard([&] { sampler(s).restart(); });
+}
+
+int32_t mh_unet_denoise(MhUNet *unet, const float *z_img, const float *init, const float *mask_lat,
+                        const float *z_masked, const MhDenoiseParams *params, MhStepFn progress, void *user,
+                        float *latents) {
+    return guard([&] {
+        mh::Context &c = unet_ctx(unet);
+        need(params, "params");
+        need(init, "init");
+        need(mask_lat, "mask_lat");
+        need(z_masked, "z_masked");
+        need(latents, "latents");
+        mh::DenoiseParams p;
+        p.steps = params->steps;
+        p.strength = params->strength;
+        p.spacing = spacing_of(params->spacing);
+        if (params->solver == MH_SOLVER_DDIM) p.solver = mh::Solver::Ddim;
+        else if (params->solver == MH_SOLVER_DPMPP_2M) p.solver = mh::Solver::DpmPp2M;
+        else mh::fail(mh::kInvalidArgument, "unknown solver");
+        p.guidance = params->guidance;
+        p.cfg_steps = params->cfg_steps;
+        mh::unet_denoise(c, *unet->net, z_img, init, mask_lat, z_masked, p, progress, user, latents);
+    });
+}

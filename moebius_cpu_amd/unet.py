@@ -86,3 +86,75 @@ class UNet:
         w, p = ctypes.c_uint64(), ctypes.c_uint64()
         check(lib().mh_unet_memory(self.h, ctypes.byref(w), ctypes.byref(p)))
         return int(w.value), int(p.value)
+
+
+class Scheduler:
+    """src/scheduler.rs `Ddim` + `Dpm2M` on device arrays of `length` floats
+    (mh_scheduler_*): timesteps and alphas on the host, updates on the device."""
+
+    def __init__(self, ctx: Context, steps: int, strength: float, spacing: str = "leading", length: int = 64 * 64 * 4):
+        self.ctx = ctx
+        h = ctypes.c_void_p()
+        check(lib().mh_scheduler_create(ctx.h, int(steps), float(strength), _lib.SPACING[spacing], int(length),
+                                        ctypes.byref(h)))
+        self.h = h
+        self.timesteps, self.pure_noise_start = schedule_timesteps(steps, strength, spacing)
+        ctx.adopt(self)
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().mh_scheduler_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def add_noise(self, x0: DeviceArray, noise: DeviceArray, t: int, out: DeviceArray):
+        check(lib().mh_scheduler_add_noise(self.h, x0.ptr, noise.ptr, int(t), out.ptr))
+
+    def ddim_step(self, eps_u: DeviceArray, eps_c, guidance: float, t: int, x: DeviceArray):
+        check(lib().mh_scheduler_ddim_step(self.h, eps_u.ptr, eps_c.ptr if eps_c is not None else None,
+                                           float(guidance), int(t), x.ptr))
+
+    def dpm_step(self, eps_u: DeviceArray, eps_c, guidance: float, i: int, x: DeviceArray):
+        check(lib().mh_scheduler_dpm_step(self.h, eps_u.ptr, eps_c.ptr if eps_c is not None else None,
+                                          float(guidance), int(i), x.ptr))
+
+    def dpm_restart(self):
+        check(lib().mh_scheduler_dpm_restart(self.h))
+
+
+def schedule_timesteps(steps: int, strength: float, spacing: str = "leading"):
+    """(timesteps, pure_noise_start) of src/scheduler.rs:30-76, computed by the library on the host."""
+    out = (ctypes.c_uint32 * 1000)()
+    n, pure = ctypes.c_uint32(), ctypes.c_uint32()
+    check(lib().mh_schedule_timesteps(int(steps), float(strength), _lib.SPACING[spacing], out, ctypes.byref(n),
+                                      ctypes.byref(pure)))
+    return [int(out[i]) for i in range(n.value)], bool(pure.value)
+
+
+def schedule_alphas_cumprod() -> np.ndarray:
+    out = np.empty(1000, np.float32)
+    check(lib().mh_schedule_alphas_cumprod(out.ctypes.data))
+    return out
+
+
+def denoise(net: "UNet", z_img, init, mask_lat, z_masked, steps: int = 20, strength: float = 0.99,
+            spacing: str = "leading", solver: str = "ddim", guidance: float = 2.5, cfg_steps=None, progress=None):
+    """src/pipeline.rs:295-345 on the device (mh_unet_denoise) from host arrays:
+    z_img, init, z_masked [1,64,64,4], mask_lat [1,64,64,1]; returns the final
+    latents [1,64,64,4]. progress(done, total) -> truthy cancels."""
+    ctx = net.ctx
+    arrs = [None if a is None else DeviceArray.from_numpy(ctx, np.ascontiguousarray(a, np.float32))
+            for a in (z_img, init, mask_lat, z_masked)]
+    out = DeviceArray(ctx, (1, 64, 64, 4))
+    prm = _lib.DenoiseParams(strength=float(strength), guidance=float(guidance), steps=int(steps),
+                             spacing=_lib.SPACING[spacing], solver=_lib.SOLVER[solver],
+                             cfg_steps=-1 if cfg_steps is None else int(cfg_steps), reserved=0)
+    cb = _lib.STEP_FN(lambda _u, done, total: 1 if progress is not None and progress(done, total) else 0)
+    check(lib().mh_unet_denoise(net.h, arrs[0].ptr if arrs[0] is not None else None, arrs[1].ptr, arrs[2].ptr,
+                                arrs[3].ptr, ctypes.byref(prm), cb, None, out.ptr))
+    return out.numpy()

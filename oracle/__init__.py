@@ -588,3 +588,93 @@ class Vae:
             lib().orc_vae_destroy(self.h)
         except Exception:
             pass
+
+
+# ---- samplers and denoise loop (oracle/pipeline.cpp: src/scheduler.rs, src/pipeline.rs)
+
+def _declare_pipeline(L):
+    vp, i64, c_int, c_double = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_double
+    L.orc_alphas_cumprod.argtypes = [vp]
+    L.orc_sched_create.restype = vp
+    L.orc_sched_create.argtypes = [c_int, c_double, c_int]
+    L.orc_sched_destroy.argtypes = [vp]
+    L.orc_sched_timesteps.restype = c_int
+    L.orc_sched_timesteps.argtypes = [vp, vp, vp]
+    L.orc_sched_add_noise.argtypes = [vp, vp, vp, i64, c_int, vp]
+    L.orc_sched_ddim_step.argtypes = [vp, vp, i64, c_int, vp]
+    L.orc_sched_dpm_step.argtypes = [vp, vp, i64, c_int, vp]
+    L.orc_sched_dpm_restart.argtypes = [vp]
+    L.orc_denoise.restype = c_int
+    L.orc_denoise.argtypes = [vp, vp, vp, vp, vp, c_int, c_double, c_int, c_int, ctypes.c_float, c_int, vp,
+                              ctypes.c_char_p, c_int]
+
+
+SPACING = {"leading": 0, "trailing": 1}
+SOLVER = {"ddim": 0, "dpm": 1}
+
+
+def alphas_cumprod() -> np.ndarray:
+    """src/scheduler.rs:159-172"""
+    L = lib()
+    _declare_pipeline(L)
+    out = np.empty(1000, np.float32)
+    L.orc_alphas_cumprod(_p(out))
+    return out
+
+
+class Scheduler:
+    """src/scheduler.rs `Ddim` (+ the `Dpm2M` state): timesteps, add_noise, DDIM and DPM-Solver++(2M) steps."""
+
+    def __init__(self, steps: int, strength: float, spacing: str = "leading"):
+        L = lib()
+        _declare_pipeline(L)
+        self.h = L.orc_sched_create(int(steps), float(strength), SPACING[spacing])
+        if not self.h:
+            raise ValueError(f"steps must be 1..=1000, got {steps}")
+        ts = np.empty(1000, np.int32)
+        pure = ctypes.c_int()
+        n = L.orc_sched_timesteps(self.h, _p(ts), ctypes.byref(pure))
+        self.timesteps = [int(t) for t in ts[:n]]
+        self.pure_noise_start = bool(pure.value)
+
+    def add_noise(self, x0, noise, t: int) -> np.ndarray:
+        x0, noise = _f32(x0), _f32(noise)
+        out = np.empty_like(x0)
+        lib().orc_sched_add_noise(self.h, _p(x0), _p(noise), x0.size, int(t), _p(out))
+        return out
+
+    def ddim_step(self, eps, t: int, x) -> np.ndarray:
+        eps, x = _f32(eps), np.array(_f32(x), copy=True)
+        lib().orc_sched_ddim_step(self.h, _p(eps), x.size, int(t), _p(x))
+        return x
+
+    def dpm_step(self, eps, i: int, x) -> np.ndarray:
+        eps, x = _f32(eps), np.array(_f32(x), copy=True)
+        lib().orc_sched_dpm_step(self.h, _p(eps), x.size, int(i), _p(x))
+        return x
+
+    def dpm_restart(self):
+        lib().orc_sched_dpm_restart(self.h)
+
+    def __del__(self):
+        try:
+            lib().orc_sched_destroy(self.h)
+        except Exception:
+            pass
+
+
+def denoise(unet: "UNet", z_img, init, mask_lat, z_masked, steps: int, strength: float, spacing: str = "leading",
+            solver: str = "ddim", guidance: float = 2.5, cfg_steps=None) -> np.ndarray:
+    """src/pipeline.rs:295-345 (steps 7-8) over the oracle UNet: the final latents [1,64,64,4]."""
+    L = lib()
+    _declare_pipeline(L)
+    z_img, init, z_masked = _f32(z_img), _f32(init), _f32(z_masked)
+    mask_lat = _f32(mask_lat)
+    out = np.empty((1, 64, 64, 4), np.float32)
+    err = ctypes.create_string_buffer(512)
+    st = L.orc_denoise(unet.h, _p(z_img), _p(init), _p(mask_lat), _p(z_masked), int(steps), float(strength),
+                       SPACING[spacing], SOLVER[solver], float(guidance), -1 if cfg_steps is None else int(cfg_steps),
+                       _p(out), err, 512)
+    if st != 0:
+        raise RuntimeError("oracle denoise failed: " + err.value.decode())
+    return out

@@ -334,6 +334,23 @@ int32_t mh_unet_forward_traced(MhUNet *unet, const float *x_dev, uint32_t timest
 /* HBM held by the weights and by the activation pool. */
 int32_t mh_unet_memory(MhUNet *unet, uint64_t *weight_bytes, uint64_t *pool_bytes);
 
+/* ---- weights from the converter's safetensors files (src/weights.rs) ---- */
+
+#define MH_MODEL_UNET 0u
+#define MH_MODEL_VAE 1u
+
+/* src/weights.rs:40-96 on the host, no device needed: maps `path`, parses the
+ * safetensors header, requires the "format" metadata "moebius-cpu/1" (and, for the
+ * VAE, "scaling_factor" 0.13025: src/vae/mod.rs:88-93), and checks that every
+ * tensor the model loads is present with its converted shape, stored F16 or F32.
+ * MH_ERR_IO when the file cannot be read, MH_ERR_WEIGHTS otherwise. */
+int32_t mh_weights_validate(const char *path, uint32_t model);
+/* UNet::load / Vae::load (src/unet/mod.rs:86-140, src/vae/mod.rs:88-95) from
+ * unet.safetensors / vae.safetensors: the file is validated as above, each tensor
+ * copied to HBM in its stored precision, and the mapping closed again. */
+int32_t mh_unet_create_from_file(MhContext *ctx, const char *path, MhUNet **out);
+int32_t mh_vae_create_from_file(MhContext *ctx, const char *path, MhVae **out);
+
 /* ---- samplers and the denoise loop (src/scheduler.rs, src/pipeline.rs) ---- */
 
 #define MH_SPACING_LEADING 0u  /* src/scheduler.rs:24-29 */

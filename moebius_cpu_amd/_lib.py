@@ -100,6 +100,9 @@ SIGNATURES = {
     "mh_unet_forward_host": (_i32, [_vp, _vp, _u32, _u32, _vp]),
     "mh_unet_forward_traced": (_i32, [_vp, _vp, _u32, _u32, _vp, _vp, _vp]),
     "mh_unet_memory": (_i32, [_vp, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
+    "mh_weights_validate": (_i32, [ctypes.c_char_p, _u32]),
+    "mh_unet_create_from_file": (_i32, [_vp, ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "mh_vae_create_from_file": (_i32, [_vp, ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "mh_schedule_timesteps": (_i32, [_u32, ctypes.c_double, _u32, _u32p, _u32p, _u32p]),
     "mh_schedule_alphas_cumprod": (_i32, [_vp]),
     "mh_scheduler_create": (_i32, [_vp, _u32, ctypes.c_double, _u32, _u64, ctypes.POINTER(_vp)]),
@@ -138,6 +141,8 @@ class DenoiseParams(ctypes.Structure):
                 ("reserved", ctypes.c_uint32)]
 
 
+MODEL_UNET = 0
+MODEL_VAE = 1
 SPACING = {"leading": 0, "trailing": 1}
 SOLVER = {"ddim": 0, "dpm": 1}
 STEP_FN = ctypes.CFUNCTYPE(ctypes.c_int32, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32)

@@ -18,6 +18,7 @@
 #include "pool.hpp"
 #include "unet.hpp"
 #include "vae.hpp"
+#include "weights.hpp"
 
 struct MhContext {
     mh::Context ctx;
@@ -969,5 +970,54 @@ int32_t mh_unet_denoise(MhUNet *unet, const float *z_img, const float *init, con
         p.guidance = params->guidance;
         p.cfg_steps = params->cfg_steps;
         mh::unet_denoise(c, *unet->net, z_img, init, mask_lat, z_masked, p, progress, user, latents);
+    });
+}
+
+// ---- weights from files
+
+static mh::ModelKind model_of(uint32_t m) {
+    if (m == MH_MODEL_UNET) return mh::ModelKind::UNet;
+    if (m == MH_MODEL_VAE) return mh::ModelKind::Vae;
+    mh::fail(mh::kInvalidArgument, "unknown model");
+}
+
+int32_t mh_weights_validate(const char *path, uint32_t model) {
+    return guard([&] {
+        need(path, "path");
+        const mh::ModelKind kind = model_of(model);
+        const mh::WeightsFile f(path);
+        (void)mh::model_tensors(f, kind);
+    });
+}
+
+int32_t mh_unet_create_from_file(MhContext *ctx, const char *path, MhUNet **out) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(out, "out");
+        *out = nullptr;
+        need(path, "path");
+        const mh::WeightsFile f(path);
+        const std::vector<mh::NamedTensor> t = mh::model_tensors(f, mh::ModelKind::UNet);
+        auto u = std::make_unique<MhUNet>();
+        u->owner = ctx;
+        u->net = std::make_unique<mh::UNet>(c, t.data(), int(t.size()));
+        HIP_CHECK(hipStreamSynchronize(c.stream));  // the uploads have read the mapping
+        *out = u.release();
+    });
+}
+
+int32_t mh_vae_create_from_file(MhContext *ctx, const char *path, MhVae **out) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(out, "out");
+        *out = nullptr;
+        need(path, "path");
+        const mh::WeightsFile f(path);
+        const std::vector<mh::NamedTensor> t = mh::model_tensors(f, mh::ModelKind::Vae);
+        auto v = std::make_unique<MhVae>();
+        v->owner = ctx;
+        v->vae = std::make_unique<mh::Vae>(c, t.data(), int(t.size()));
+        HIP_CHECK(hipStreamSynchronize(c.stream));
+        *out = v.release();
     });
 }

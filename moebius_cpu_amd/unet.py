@@ -40,6 +40,17 @@ class UNet:
         self.h = h
         ctx.adopt(self)
 
+    @classmethod
+    def from_file(cls, ctx: Context, path: str) -> "UNet":
+        """Loads a converter safetensors file (mh_unet_create_from_file): format-tag and shape checked."""
+        self = cls.__new__(cls)
+        self.ctx = ctx
+        h = ctypes.c_void_p()
+        check(lib().mh_unet_create_from_file(ctx.h, str(path).encode(), ctypes.byref(h)))
+        self.h = h
+        ctx.adopt(self)
+        return self
+
     def close(self):
         if getattr(self, "h", None):
             lib().mh_unet_destroy(self.h)

@@ -38,6 +38,17 @@ class Vae:
         self.h = h
         ctx.adopt(self)
 
+    @classmethod
+    def from_file(cls, ctx: Context, path: str) -> "Vae":
+        """Loads a converter safetensors file (mh_vae_create_from_file): format-tag and shape checked."""
+        self = cls.__new__(cls)
+        self.ctx = ctx
+        h = ctypes.c_void_p()
+        check(lib().mh_vae_create_from_file(ctx.h, str(path).encode(), ctypes.byref(h)))
+        self.h = h
+        ctx.adopt(self)
+        return self
+
     def close(self):
         if getattr(self, "h", None):
             lib().mh_vae_destroy(self.h)

@@ -351,6 +351,30 @@ int32_t mh_weights_validate(const char *path, uint32_t model);
 int32_t mh_unet_create_from_file(MhContext *ctx, const char *path, MhUNet **out);
 int32_t mh_vae_create_from_file(MhContext *ctx, const char *path, MhVae **out);
 
+/* ---- pixel-space steps around the model window (src/imaging), on the host ---- */
+
+#define MH_PASTE_NONE 1u               /* src/preset.rs Paste; MOEBIUS_PASTE_* values */
+#define MH_PASTE_FEATHER 2u
+#define MH_PASTE_FEATHER_COMPENSATE 3u
+
+/* src/imaging/mod.rs:31-46: rect {x, y, w, h} of the pixels >= 128; *found 0 when none. */
+int32_t mh_mask_bbox(const uint8_t *mask, uint32_t width, uint32_t height, uint32_t stride, uint32_t *rect,
+                     uint32_t *found);
+/* src/imaging/mod.rs:48-77: out [height * width] = 0 / 255 mask dilated by a k x k kernel (cv2 anchor). */
+int32_t mh_mask_dilate(const uint8_t *mask, uint32_t width, uint32_t height, uint32_t stride, uint32_t k,
+                       uint8_t *out);
+/* src/imaging/crop.rs:27-51: the square window {x, y, side} for a mask bbox {x, y, w, h}. */
+int32_t mh_crop_plan(const uint32_t *bbox, uint32_t img_w, uint32_t img_h, int64_t *x, int64_t *y, uint32_t *side);
+/* src/imaging/blend.rs:91-110: Pillow GaussianBlur(radius) of an 8-bit single-channel image. */
+int32_t mh_gaussian_blur(const uint8_t *src, uint32_t width, uint32_t height, float radius, uint8_t *out);
+/* src/imaging/blend.rs:155-232: pastes result (side x side RGB) over the image inside the
+ * window {plan_x, plan_y, side}; mode MH_PASTE_*; changed {x, y, w, h} may be NULL. */
+int32_t mh_paste(uint8_t *pixels, uint32_t width, uint32_t height, uint32_t stride, uint32_t channels,
+                 const uint8_t *mask, uint32_t mask_stride, const uint8_t *result, int64_t plan_x, int64_t plan_y,
+                 uint32_t side, uint32_t mode, uint32_t *changed);
+/* src/vae/mod.rs:60-78: latent window {x, y, w, h} of a 64 x 64 mask, grown by margin. */
+int32_t mh_roi_window(const float *mask_lat, uint32_t margin, uint32_t *rect, uint32_t *found);
+
 /* ---- samplers and the denoise loop (src/scheduler.rs, src/pipeline.rs) ---- */
 
 #define MH_SPACING_LEADING 0u  /* src/scheduler.rs:24-29 */

@@ -103,6 +103,14 @@ SIGNATURES = {
     "mh_weights_validate": (_i32, [ctypes.c_char_p, _u32]),
     "mh_unet_create_from_file": (_i32, [_vp, ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "mh_vae_create_from_file": (_i32, [_vp, ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "mh_mask_bbox": (_i32, [_vp, _u32, _u32, _u32, _u32p, _u32p]),
+    "mh_mask_dilate": (_i32, [_vp, _u32, _u32, _u32, _u32, _vp]),
+    "mh_crop_plan": (_i32, [_u32p, _u32, _u32, ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64),
+                            _u32p]),
+    "mh_gaussian_blur": (_i32, [_vp, _u32, _u32, _f32, _vp]),
+    "mh_paste": (_i32, [_vp, _u32, _u32, _u32, _u32, _vp, _u32, _vp, ctypes.c_int64, ctypes.c_int64, _u32, _u32,
+                        _u32p]),
+    "mh_roi_window": (_i32, [_vp, _u32, _u32p, _u32p]),
     "mh_schedule_timesteps": (_i32, [_u32, ctypes.c_double, _u32, _u32p, _u32p, _u32p]),
     "mh_schedule_alphas_cumprod": (_i32, [_vp]),
     "mh_scheduler_create": (_i32, [_vp, _u32, ctypes.c_double, _u32, _u64, ctypes.POINTER(_vp)]),

@@ -14,6 +14,7 @@
 #include "../../include/moebius_hip.h"
 #include "common.hpp"
 #include "denoise.hpp"
+#include "imaging.hpp"
 #include "kernels.hpp"
 #include "pool.hpp"
 #include "unet.hpp"
@@ -1019,5 +1020,93 @@ int32_t mh_vae_create_from_file(MhContext *ctx, const char *path, MhVae **out) {
         v->vae = std::make_unique<mh::Vae>(c, t.data(), int(t.size()));
         HIP_CHECK(hipStreamSynchronize(c.stream));
         *out = v.release();
+    });
+}
+
+// ---- imaging (host)
+
+int32_t mh_mask_bbox(const uint8_t *mask, uint32_t width, uint32_t height, uint32_t stride, uint32_t *rect,
+                     uint32_t *found) {
+    return guard([&] {
+        need(mask, "mask");
+        need(rect, "rect");
+        MH_REQUIRE(stride >= width, "mask stride below its width");
+        mh::img::Rect r;
+        const bool f = mh::img::mask_bbox({mask, width, height, stride}, &r);
+        rect[0] = uint32_t(r.x), rect[1] = uint32_t(r.y), rect[2] = uint32_t(r.w), rect[3] = uint32_t(r.h);
+        if (found) *found = f ? 1u : 0u;
+    });
+}
+
+int32_t mh_mask_dilate(const uint8_t *mask, uint32_t width, uint32_t height, uint32_t stride, uint32_t k,
+                       uint8_t *out) {
+    return guard([&] {
+        need(mask, "mask");
+        need(out, "out");
+        MH_REQUIRE(stride >= width, "mask stride below its width");
+        const std::vector<uint8_t> d = mh::img::dilate({mask, width, height, stride}, k);
+        std::memcpy(out, d.data(), d.size());
+    });
+}
+
+int32_t mh_crop_plan(const uint32_t *bbox, uint32_t img_w, uint32_t img_h, int64_t *x, int64_t *y, uint32_t *side) {
+    return guard([&] {
+        need(bbox, "bbox");
+        need(x, "x");
+        need(y, "y");
+        need(side, "side");
+        MH_REQUIRE(bbox[2] > 0 && bbox[3] > 0 && uint64_t(bbox[0]) + bbox[2] <= img_w &&
+                       uint64_t(bbox[1]) + bbox[3] <= img_h,
+                   "mask bbox outside the image");
+        const mh::img::CropPlan p = mh::img::crop_plan({bbox[0], bbox[1], bbox[2], bbox[3]}, img_w, img_h);
+        *x = p.x, *y = p.y, *side = uint32_t(p.side);
+    });
+}
+
+int32_t mh_gaussian_blur(const uint8_t *src, uint32_t width, uint32_t height, float radius, uint8_t *out) {
+    return guard([&] {
+        need(src, "src");
+        need(out, "out");
+        const std::vector<uint8_t> b = mh::img::gaussian_blur(src, width, height, radius);
+        std::memcpy(out, b.data(), b.size());
+    });
+}
+
+static mh::img::Paste paste_of(uint32_t m) {
+    if (m == MH_PASTE_NONE) return mh::img::Paste::None;
+    if (m == MH_PASTE_FEATHER) return mh::img::Paste::Feather;
+    if (m == MH_PASTE_FEATHER_COMPENSATE) return mh::img::Paste::FeatherCompensate;
+    mh::fail(mh::kInvalidArgument, "unknown paste mode " + std::to_string(m));
+}
+
+int32_t mh_paste(uint8_t *pixels, uint32_t width, uint32_t height, uint32_t stride, uint32_t channels,
+                 const uint8_t *mask, uint32_t mask_stride, const uint8_t *result, int64_t plan_x, int64_t plan_y,
+                 uint32_t side, uint32_t mode, uint32_t *changed) {
+    return guard([&] {
+        need(pixels, "pixels");
+        need(mask, "mask");
+        need(result, "result");
+        MH_REQUIRE(channels == 3 || channels == 4, "image must be RGB or RGBA");
+        MH_REQUIRE(stride >= uint64_t(width) * channels && mask_stride >= width, "bad dimensions or stride");
+        mh::img::ImageView im{pixels, width, height, stride, channels};
+        mh::img::CropPlan p;
+        p.x = plan_x, p.y = plan_y, p.side = side;
+        MH_REQUIRE(side > 0 && plan_x < int64_t(width) && plan_y < int64_t(height) && plan_x + int64_t(side) > 0 &&
+                       plan_y + int64_t(side) > 0,
+                   "paste window does not overlap the image");
+        const mh::img::Rect r = mh::img::paste(im, {mask, width, height, mask_stride}, result, p, paste_of(mode));
+        if (changed) changed[0] = uint32_t(r.x), changed[1] = uint32_t(r.y), changed[2] = uint32_t(r.w),
+                     changed[3] = uint32_t(r.h);
+    });
+}
+
+int32_t mh_roi_window(const float *mask_lat, uint32_t margin, uint32_t *rect, uint32_t *found) {
+    return guard([&] {
+        need(mask_lat, "mask_lat");
+        need(rect, "rect");
+        mh::img::LatentRect r;
+        const bool f = mh::img::roi_window(mask_lat, margin, &r);
+        rect[0] = uint32_t(r.x), rect[1] = uint32_t(r.y), rect[2] = uint32_t(r.w), rect[3] = uint32_t(r.h);
+        if (found) *found = f ? 1u : 0u;
     });
 }

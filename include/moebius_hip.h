@@ -372,6 +372,12 @@ int32_t mh_gaussian_blur(const uint8_t *src, uint32_t width, uint32_t height, fl
 int32_t mh_paste(uint8_t *pixels, uint32_t width, uint32_t height, uint32_t stride, uint32_t channels,
                  const uint8_t *mask, uint32_t mask_stride, const uint8_t *result, int64_t plan_x, int64_t plan_y,
                  uint32_t side, uint32_t mode, uint32_t *changed);
+/* src/imaging/resize.rs:15-24 `resize_u8` on the device: Lanczos3 resize of an 8-bit
+ * image [from_h][from_w][channels] (1, 3 or 4) to [to_h][to_w][channels], device
+ * pointers, PIL's LANCZOS convolution in 22-bit fixed point (horizontal pass first);
+ * same size is a copy. Returns after the stream has finished the resize. */
+int32_t mh_resize_u8(MhContext *ctx, const uint8_t *src, uint32_t from_w, uint32_t from_h, uint32_t to_w,
+                     uint32_t to_h, uint32_t channels, uint8_t *dst);
 /* src/vae/mod.rs:60-78: latent window {x, y, w, h} of a 64 x 64 mask, grown by margin. */
 int32_t mh_roi_window(const float *mask_lat, uint32_t margin, uint32_t *rect, uint32_t *found);
 

@@ -1,4 +1,5 @@
-"""ctypes declarations of include/moebius_hip.h over libmoebius_hip.so.
+"""ctypes declarations of include/moebius_hip.h and include/moebius_engine.h
+over libmoebius_hip.so.
 
 Loading fails loudly when the library is missing: there is no CPU fallback.
 """
@@ -10,6 +11,8 @@ import os
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmoebius_hip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "moebius_hip.h")
+ENGINE_HEADER = os.path.join(os.path.dirname(HERE), "include", "moebius_engine.h")
+HEADERS = (HEADER, ENGINE_HEADER)
 
 OK = 0
 ERR_INVALID_ARGUMENT = 1
@@ -43,7 +46,7 @@ _i32 = ctypes.c_int32
 _f32 = ctypes.c_float
 _u32p = ctypes.POINTER(ctypes.c_uint32)
 
-# name -> (restype, argtypes); every function include/moebius_hip.h declares.
+# name -> (restype, argtypes); every function the two headers declare.
 SIGNATURES = {
     "mh_abi_version": (_u32, []),
     "mh_last_error": (ctypes.c_char_p, []),
@@ -110,6 +113,7 @@ SIGNATURES = {
     "mh_gaussian_blur": (_i32, [_vp, _u32, _u32, _f32, _vp]),
     "mh_paste": (_i32, [_vp, _u32, _u32, _u32, _u32, _vp, _u32, _vp, ctypes.c_int64, ctypes.c_int64, _u32, _u32,
                         _u32p]),
+    "mh_resize_u8": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _vp]),
     "mh_roi_window": (_i32, [_vp, _u32, _u32p, _u32p]),
     "mh_schedule_timesteps": (_i32, [_u32, ctypes.c_double, _u32, _u32p, _u32p, _u32p]),
     "mh_schedule_alphas_cumprod": (_i32, [_vp]),
@@ -131,6 +135,17 @@ SIGNATURES = {
     "mh_vae_sample": (_i32, [_vp, _vp, _vp, _u64, _vp]),
     "mh_timestep_sinusoid": (None, [_u32, _vp]),
     "mh_scratch_best_fit": (ctypes.c_int64, [_vp, _vp, _u64, _u64]),
+    # include/moebius_engine.h
+    "moebius_abi_version": (_u32, []),
+    "moebius_last_error": (ctypes.c_char_p, []),
+    "moebius_engine_create": (_i32, [ctypes.c_char_p, _u32, ctypes.POINTER(_vp)]),
+    "moebius_engine_destroy": (None, [_vp]),
+    "moebius_inpaint": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _u32, _vp, _vp, _vp, _vp]),
+    "mh_inpaint_params": (_i32, [_vp, _vp]),
+    "mh_sample_noise": (_i32, [_u64, _vp]),
+    "mh_engine_create": (_i32, [_i32, ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "mh_inpaint_with_noise": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "mh_engine_memory": (_i32, [_vp, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
 }
 
 GUIDANCE_CFG = 0
@@ -154,6 +169,32 @@ MODEL_VAE = 1
 SPACING = {"leading": 0, "trailing": 1}
 SOLVER = {"ddim": 0, "dpm": 1}
 STEP_FN = ctypes.CFUNCTYPE(ctypes.c_int32, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32)
+
+PRESET = {"exact": 0, "fast": 1}
+PASTE = {"default": 0, "none": 1, "feather": 2, "feather_compensate": 3}
+PROGRESS_FN = ctypes.CFUNCTYPE(ctypes.c_int32, ctypes.c_void_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32)
+NOISE_FLOATS = 3 * 64 * 64 * 4 + 4
+
+
+class MoebiusParams(ctypes.Structure):
+    """include/moebius_engine.h MoebiusParams (src/ffi.rs:43-53)."""
+    _fields_ = [("preset", ctypes.c_uint32), ("steps", ctypes.c_uint32), ("guidance", ctypes.c_float),
+                ("seed", ctypes.c_uint64), ("paste", ctypes.c_uint32), ("mask_dilate", ctypes.c_uint32)]
+
+
+class MoebiusRect(ctypes.Structure):
+    _fields_ = [("x", ctypes.c_uint32), ("y", ctypes.c_uint32), ("width", ctypes.c_uint32),
+                ("height", ctypes.c_uint32)]
+
+
+class InpaintParams(ctypes.Structure):
+    """include/moebius_engine.h MhInpaintParams (src/preset.rs:34-58 InpaintParams + precision)."""
+    _fields_ = [("steps", ctypes.c_uint32), ("spacing", ctypes.c_uint32), ("solver", ctypes.c_uint32),
+                ("cfg_steps", ctypes.c_int32), ("strength", ctypes.c_double), ("guidance", ctypes.c_float),
+                ("noise_offset", ctypes.c_float), ("seed", ctypes.c_uint64), ("roi_encode", ctypes.c_uint32),
+                ("roi_decode", ctypes.c_uint32), ("paste", ctypes.c_uint32), ("mask_dilate", ctypes.c_uint32),
+                ("precision", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+
 
 TRACE_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_char_p, ctypes.c_void_p, ctypes.c_uint32,
                             ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32)

@@ -32,7 +32,7 @@ FLAGS = [
 def _compile(src: str, incremental: bool = False) -> str:
     obj = os.path.join(OBJ, os.path.basename(src) + ".o")
     if incremental and os.path.exists(obj):
-        deps = [src, *glob.glob(os.path.join(CSRC, "*.hpp")), os.path.join(HERE, "..", "include", "moebius_hip.h")]
+        deps = [src, *glob.glob(os.path.join(CSRC, "*.hpp")), *glob.glob(os.path.join(HERE, "..", "include", "*.h"))]
         if os.path.getmtime(obj) >= max(os.path.getmtime(d) for d in deps if os.path.exists(d)):
             return obj
     cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]

@@ -12,6 +12,7 @@
 #include <vector>
 
 #include "../../include/moebius_hip.h"
+#include "capi_guard.hpp"
 #include "common.hpp"
 #include "denoise.hpp"
 #include "imaging.hpp"
@@ -53,37 +54,13 @@ struct MhEvent {
 
 namespace {
 
-thread_local std::string g_last_error = "no error";
-
-int32_t set_error(int32_t code, const std::string &msg) {
-    g_last_error = msg;
-    return code;
-}
-
-template <typename F>
-int32_t guard(F &&f) {
-    try {
-        f();
-        return mh::kOk;
-    } catch (const mh::Error &e) {
-        return set_error(e.code, e.what());
-    } catch (const std::bad_alloc &) {
-        return set_error(mh::kOutOfMemory, "host allocation failed");
-    } catch (const std::exception &e) {
-        return set_error(mh::kInternal, std::string("internal error: ") + e.what());
-    } catch (...) {
-        return set_error(mh::kInternal, "internal error: unknown exception");
-    }
-}
+using mh::capi::guard;
+using mh::capi::need;
 
 mh::Context &C(MhContext *c) {
     if (!c) mh::fail(mh::kInvalidArgument, "context is NULL");
     HIP_CHECK(hipSetDevice(c->ctx.device));
     return c->ctx;
-}
-
-void need(const void *p, const char *what) {
-    if (!p) mh::fail(mh::kInvalidArgument, std::string(what) + " is NULL");
 }
 
 mh::WeightType wtype(uint32_t dt) {
@@ -111,7 +88,7 @@ extern "C" {
 
 uint32_t mh_abi_version(void) { return MH_ABI_VERSION; }
 
-const char *mh_last_error(void) { return g_last_error.c_str(); }
+const char *mh_last_error(void) { return mh::capi::last_error.c_str(); }
 
 int32_t mh_context_create(int32_t device, MhContext **out) {
     return guard([&] {
@@ -1108,5 +1085,16 @@ int32_t mh_roi_window(const float *mask_lat, uint32_t margin, uint32_t *rect, ui
         const bool f = mh::img::roi_window(mask_lat, margin, &r);
         rect[0] = uint32_t(r.x), rect[1] = uint32_t(r.y), rect[2] = uint32_t(r.w), rect[3] = uint32_t(r.h);
         if (found) *found = f ? 1u : 0u;
+    });
+}
+
+int32_t mh_resize_u8(MhContext *ctx, const uint8_t *src, uint32_t from_w, uint32_t from_h, uint32_t to_w,
+                     uint32_t to_h, uint32_t channels, uint8_t *dst) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(src, "src");
+        need(dst, "dst");
+        MH_REQUIRE(from_w <= 65536 && from_h <= 65536 && to_w <= 65536 && to_h <= 65536, "resize: image too large");
+        mh::resize_u8(c, src, int(from_w), int(from_h), int(to_w), int(to_h), int(channels), dst);
     });
 }

@@ -72,6 +72,13 @@ void group_norm_affine_partials(Context &ctx, const float *part, int rows, int n
 // Per-row (mean, rstd) of LayerNorm for consumers that apply it themselves: stats [rows][2].
 void layer_norm_stats(Context &ctx, const float *x, int64_t rows, int c, float eps, float *stats);
 
+// ---- resampling (resize.hip) ----
+// Lanczos3 resize of an 8-bit image [from_h][from_w][channels] to [to_h][to_w][channels]
+// (PIL's LANCZOS formulation: separable 22-bit fixed-point passes, horizontal first);
+// same size is a copy. Device pointers; uses the workspace; synchronises the stream.
+void resize_u8(Context &ctx, const uint8_t *src, int from_w, int from_h, int to_w, int to_h, int channels,
+               uint8_t *dst);
+
 // ---- depthwise (depthwise.hip) ----
 // prologue (optional): GroupNorm affine [+SiLU] applied to in-image inputs as they load.
 void depthwise3x3(Context &ctx, const float *x, int n, int h, int w, int c, const float *weight, const float *bias,

@@ -678,3 +678,15 @@ def denoise(unet: "UNet", z_img, init, mask_lat, z_masked, steps: int, strength:
     if st != 0:
         raise RuntimeError("oracle denoise failed: " + err.value.decode())
     return out
+
+
+def resize_u8(img, to_w: int, to_h: int) -> np.ndarray:
+    """src/imaging/resize.rs:15-24 (PIL LANCZOS, 22-bit fixed point): [h, w(, c)] uint8 -> [to_h, to_w(, c)]."""
+    L = lib()
+    L.orc_resize_u8.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                ctypes.c_void_p]
+    a = np.ascontiguousarray(img, np.uint8)
+    c = 1 if a.ndim == 2 else a.shape[2]
+    out = np.empty((to_h, to_w) + (() if a.ndim == 2 else (c,)), np.uint8)
+    L.orc_resize_u8(a.ctypes.data, a.shape[1], a.shape[0], int(to_w), int(to_h), c, out.ctypes.data)
+    return out

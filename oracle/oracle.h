@@ -104,6 +104,10 @@ void orc_concat_channels(const float *a, int64_t ca, const float *b, int64_t cb,
 /* src/imaging/blend.rs:21-24 */
 void orc_to_u8(const float *x, int64_t len, uint8_t *out);
 
+/* src/imaging/resize.rs:15-24: Lanczos3 (PIL LANCZOS) resize of an 8-bit image
+ * [from_h][from_w][channels] to [to_h][to_w][channels]; same size is a copy. */
+void orc_resize_u8(const uint8_t *src, int from_w, int from_h, int to_w, int to_h, int channels, uint8_t *dst);
+
 /* OpenMP threads the oracle uses (0 = runtime default). */
 void orc_set_threads(int threads);
 int orc_get_threads(void);

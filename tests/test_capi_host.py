@@ -1,6 +1,6 @@
 """CPU-side checks of the C ABI library: it was built, it loads, it exports
-every function include/moebius_hip.h declares (and the binding declares no
-more), and its host-only paths behave (argument errors, output_hw). No kernel
+every function include/moebius_hip.h and include/moebius_engine.h declare (and
+the binding declares no more), and its host-only paths behave (argument errors, output_hw). No kernel
 is launched here."""
 from __future__ import annotations
 
@@ -14,9 +14,11 @@ from moebius_cpu_amd import _lib
 
 
 def header_functions():
-    text = open(_lib.HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(mh_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in _lib.HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names.update(re.findall(r"\b((?:mh|moebius)_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol():
@@ -24,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     names = header_functions()
     assert len(names) >= 30
     missing = [n for n in names if not hasattr(L, n)]
-    assert not missing, f"declared in include/moebius_hip.h but not exported: {missing}"
+    assert not missing, f"declared in include/*.h but not exported: {missing}"
     assert sorted(_lib.SIGNATURES) == names, "the ctypes table and the header disagree"
 
 

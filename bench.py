@@ -17,6 +17,10 @@ same way), and, under "configs", every benchmark configuration:
   cfg4  the UNet step in EXACT (batch 2 and 1) and FAST (f16 MFMA; batch 2 and 1)
   cfg5  VAE encode [1,512,512,3] and decode [1,64,64,4] -> [1,512,512,3]
 
+and "inpaint": one whole inpainting call through the moebius_inpaint C API
+(Exact and Fast presets, 1024x768 RGB image, 400x300 mask: an 800 px window
+resampled to 512 and back), wall time per call with its stage split,
+
 each with its time, its rate and roofline fraction, and the CPU oracle on the
 same inputs, timed in the same run (a child process on the host cores).
 One GPU only: --gpus above 1 exits with a message.
@@ -382,6 +386,75 @@ def cfg5_vae(ctx, steps, f16_weights=False, which=("decode", "encode_b1", "encod
     return res
 
 
+# ---------------------------------------------------------------- whole inpaint
+
+def inpaint_bench(reps=3):
+    """Wall time of whole moebius_inpaint calls (host in, host out, synchronous),
+    after one warm-up call per preset, with the stage split the progress
+    callback sees. Models: random-init UNet (f16-stored GEMM weights, the
+    converter's default; f32 arithmetic) and VAE, loaded from safetensors files."""
+    import ctypes
+    import tempfile
+    import time
+
+    from moebius_cpu_amd import _lib
+    from moebius_cpu_amd import unet_params as U
+    from moebius_cpu_amd import vae_params as V
+    from moebius_cpu_amd.weights_io import write_weights
+
+    log("inpaint: writing the model files")
+    tmp = tempfile.mkdtemp(prefix="moebius-bench-")
+    gemm = sorted(s.name for s in U.unet_specs() if s.gemm)
+    write_weights(os.path.join(tmp, "unet.safetensors"), U.random_unet(seed=4000), gemm, f16=True)
+    write_weights(os.path.join(tmp, "vae.safetensors"), V.random_vae(), metadata={"scaling_factor": "0.13025"})
+    L = _lib.lib()
+    eng = ctypes.c_void_p()
+    _lib.check(L.moebius_engine_create(tmp.encode(), 0, ctypes.byref(eng)))
+    for f in os.listdir(tmp):
+        os.remove(os.path.join(tmp, f))
+    os.rmdir(tmp)
+    h, w = 768, 1024
+    yy, xx = np.mgrid[0:h, 0:w]
+    img0 = np.stack([xx * 255 // (w - 1), yy * 255 // (h - 1), (xx + yy) % 256], -1).astype(np.uint8)
+    mask = np.zeros((h, w), np.uint8)
+    mask[234:534, 312:712] = 255
+    marks = []
+
+    def cb(_u, stage, done, total):
+        marks.append((stage, done, total, time.perf_counter()))
+        return 0
+    fn = _lib.PROGRESS_FN(cb)
+    res = {"workload": "moebius_inpaint, 1024x768 RGB, 400x300 mask (800 px window <-> 512), random-init models "
+                       "from safetensors (UNet GEMM weights f16-stored, f32 arithmetic), feather paste; wall "
+                       "time per call, host buffers in and out"}
+    for name, preset in (("exact", 0), ("fast", 1)):
+        p = _lib.MoebiusParams(preset=preset, steps=0, guidance=0.0, seed=1, paste=0, mask_dilate=0)
+        runs = []
+        for i in range(reps + 1):
+            img = img0.copy()
+            marks.clear()
+            t0 = time.perf_counter()
+            _lib.check(L.moebius_inpaint(eng, img.ctypes.data, w, h, w * 3, 3, mask.ctypes.data, w,
+                                         ctypes.byref(p), fn, None, None))
+            t1 = time.perf_counter()
+            if i == 0:
+                continue  # first call: the pools are allocated
+            at = {(s, d): t for s, d, _, t in marks}
+            n = marks[-3][2]  # denoise steps
+            runs.append({"total": (t1 - t0) * 1e3, "prepare": (at[(0, 0)] - t0) * 1e3,
+                         "encode": (at[(0, 1)] - at[(0, 0)]) * 1e3, "denoise": (at[(1, n)] - at[(0, 1)]) * 1e3,
+                         "decode": (at[(2, 1)] - at[(2, 0)]) * 1e3, "finish": (t1 - at[(2, 1)]) * 1e3,
+                         "steps": n})
+        med = {k: float(np.median([r_[k] for r_ in runs])) for k in runs[0]}
+        res[name] = {"ms": r(med["total"], 2), "denoise_steps": int(med["steps"]),
+                     "stages_ms": {k: r(med[k], 2) for k in ("prepare", "encode", "denoise", "decode", "finish")},
+                     "ms_per_denoise_step": r(med["denoise"] / med["steps"], 3), "runs": reps}
+    L.moebius_engine_destroy(eng)
+    res["reference_published"] = {"fast_s": [10.7, 11.9], "hardware": "i7-13620H, 10 threads",
+                                  "source": "src/preset.rs:2-4 (per 512-px inpaint, from cool)"}
+    return res
+
+
 # ---------------------------------------------------------------- assembly
 
 def attach_cpu(configs, cpu):
@@ -418,6 +491,17 @@ def attach_cpu(configs, cpu):
         v["encode_b1"]["cpu_ms"] = c["vae_encode_b1"]
         v["encode_b2"]["cpu_ms"] = c.get("vae_encode_b2")
         v["cpu"] = note("the same passes, median after one warm-up")
+    if "inpaint" in configs and "unet_b2" in c and "vae_decode" in c:
+        ip = configs["inpaint"]
+        # The oracle is not run end to end (about 25 s per Exact call on 16 cores): its estimate is the
+        # sum of the parts it ran in this same run. Exact: encode batch 2 + 19 CFG steps + decode; Fast:
+        # encode batch 1 (the ROI encode of the image window is left out) + 3 CFG + 6 cond-only + decode.
+        ip["exact"]["cpu_ms_estimate"] = r(c["vae_encode_b2"] + ip["exact"]["denoise_steps"] * c["unet_b2"]
+                                           + c["vae_decode"], 1)
+        nf = ip["fast"]["denoise_steps"]
+        ip["fast"]["cpu_ms_estimate"] = r(c["vae_encode_b1"] + 3 * c["unet_b2"] + (nf - 3) * c["unet_b1"]
+                                          + c["vae_decode"], 1)
+        ip["cpu"] = note("estimate: the sum of the oracle's measured encode, steps and decode in this run")
 
 
 def run_all(args):
@@ -435,6 +519,7 @@ def run_all(args):
                                        "FAST = f16-stored weights on f16 MFMA with f32 accumulate",
                            **unet_entries}
         configs["cfg5"] = cfg5_vae(ctx, max(3, args.steps // 4))
+        configs["inpaint"] = inpaint_bench()
         out["configs"] = configs
         cpu_sets = ["configs"]
     ctx.close()
@@ -478,6 +563,9 @@ def single(args):
     elif w == "vae_encode":
         res = cfg5_vae(ctx, args.steps, args.f16_weights, which=("encode_b1",))
         ms = res["encode_b1"]["ms"]
+    elif w == "inpaint":
+        res = inpaint_bench(max(1, args.steps))
+        ms = res["exact"]["ms"]
     else:
         raise SystemExit(f"unknown workload {w}")
     ctx.close()
@@ -491,7 +579,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="unet_step",
-                    choices=["unet_step", "conv3x3_gn_silu", "sweep", "resnet_block", "vae_decode", "vae_encode"])
+                    choices=["unet_step", "conv3x3_gn_silu", "sweep", "resnet_block", "vae_decode", "vae_encode",
+                             "inpaint"])
     ap.add_argument("--cond-only", action="store_true", help="UNet: batch 1 (no CFG)")
     ap.add_argument("--f16-weights", action="store_true", help="UNet / VAE: f16-stored GEMM weights")
     ap.add_argument("--fast", action="store_true",

@@ -142,8 +142,16 @@ int32_t mh_inpaint_with_noise(const MoebiusEngine *engine,
                               MoebiusProgressFn progress, void *user,
                               MoebiusRect *changed, float *latents_out);
 
-/* Device memory the engine holds: weights, and the activation pools. */
+/* Device memory the engine holds: weights, and the activation pools plus the
+ * transform workspace. */
 int32_t mh_engine_memory(const MoebiusEngine *engine, uint64_t *weight_bytes, uint64_t *pool_bytes);
+
+/* Frees the activation pools and the workspace (Scratch::release_below,
+ * src/engine/mod.rs:87-91). The CPU engine does this inside every call
+ * (src/pipeline.rs:290-292); this engine keeps them resident between calls,
+ * so that a repeated call allocates nothing, and frees them only on request.
+ * The next call allocates them again. */
+int32_t mh_engine_release_scratch(const MoebiusEngine *engine);
 
 #ifdef __cplusplus
 }

@@ -146,6 +146,7 @@ SIGNATURES = {
     "mh_engine_create": (_i32, [_i32, ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "mh_inpaint_with_noise": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _u32, _vp, _vp, _vp, _vp, _vp, _vp]),
     "mh_engine_memory": (_i32, [_vp, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]),
+    "mh_engine_release_scratch": (_i32, [_vp]),
 }
 
 GUIDANCE_CFG = 0

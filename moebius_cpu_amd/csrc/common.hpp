@@ -73,6 +73,8 @@ class Workspace {
     Workspace &operator=(const Workspace &) = delete;
     ~Workspace();
     void *get(size_t bytes, hipStream_t stream);
+    // Frees the buffer once the stream has drained; the next get allocates again.
+    void release(hipStream_t stream);
     size_t capacity() const { return cap_; }
 
   private:

@@ -22,6 +22,14 @@ Workspace::~Workspace() {
     if (ptr_) (void)hipFree(ptr_);
 }
 
+void Workspace::release(hipStream_t stream) {
+    if (!ptr_) return;
+    HIP_CHECK(hipStreamSynchronize(stream));
+    HIP_CHECK(hipFree(ptr_));
+    ptr_ = nullptr;
+    cap_ = 0;
+}
+
 void *Workspace::get(size_t bytes, hipStream_t stream) {
     if (bytes <= cap_) return ptr_;
     HIP_CHECK(hipStreamSynchronize(stream));

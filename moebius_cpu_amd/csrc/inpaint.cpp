@@ -63,8 +63,13 @@ std::vector<float> normals(uint64_t seed, size_t n) {
     return out;
 }
 
-void report(ProgressFn fn, void *user, uint32_t stage, uint32_t done, uint32_t total) {
-    if (fn && fn(user, stage, done, total) != 0) fail(kCancelled, "cancelled");
+// A stage is reported done once its kernels have finished, as the CPU engine
+// reports it after the work (so the callback's clock and cancellation points
+// line up with the reference's stages).
+void report(Context &ctx, ProgressFn fn, void *user, uint32_t stage, uint32_t done, uint32_t total) {
+    if (!fn) return;
+    if (done == total) HIP_CHECK(hipStreamSynchronize(ctx.stream));
+    if (fn(user, stage, done, total) != 0) fail(kCancelled, "cancelled");
 }
 
 struct StepAdapter {
@@ -134,7 +139,7 @@ img::Rect inpaint(Engine &e, img::ImageView &im, const img::MaskView &mask_in, c
     const size_t side = plan.side;
 
     // 2-3: the window (edge-replicated image, mask zero outside) -> 512x512 on the device.
-    report(progress, user, 0, 0, 1);
+    report(ctx, progress, user, 0, 0, 1);
     std::vector<uint8_t> win(side * side * 3), wbin(side * side);
     const int64_t w = int64_t(im.width), h = int64_t(im.height);
     for (size_t wy = 0; wy < side; ++wy) {
@@ -191,7 +196,7 @@ img::Rect inpaint(Engine &e, img::ImageView &im, const img::MaskView &mask_in, c
     }
     // The CPU engine frees the encoder's 512x512 maps here (src/pipeline.rs:290-292);
     // with HBM to spare the VAE's pool stays resident, so a later call allocates nothing.
-    report(progress, user, 0, 1, 1);
+    report(ctx, progress, user, 0, 1, 1);
 
     // 6-8: init = N(0,1) + noise_offset * N(0,1)[per channel], then the denoise loop.
     std::vector<float> init(static_cast<size_t>(kLatN));
@@ -207,7 +212,7 @@ img::Rect inpaint(Engine &e, img::ImageView &im, const img::MaskView &mask_in, c
     if (latents_out) d2h(ctx, latents_out, d_lat.p, size_t(kLatN) * sizeof(float));
 
     // 9: decode (the whole frame, or the ROI window over the model-input image).
-    report(progress, user, 2, 0, 1);
+    report(ctx, progress, user, 2, 0, 1);
     DevBuf d_dec(model_px * 3 * sizeof(float));
     img::LatentRect rd;
     if (p.roi_decode && img::roi_window(mask_lat.data(), kRoiMargin, &rd) &&
@@ -220,7 +225,7 @@ img::Rect inpaint(Engine &e, img::ImageView &im, const img::MaskView &mask_in, c
     } else {
         e.vae->decode(d_lat.f(), kLat, kLat, d_dec.f());
     }
-    report(progress, user, 2, 1, 1);
+    report(ctx, progress, user, 2, 1, 1);
 
     // 10: 8-bit truncation, resampled back to the window, pasted on the host.
     DevBuf d_u8(model_px * 3), d_res(side * side * 3);

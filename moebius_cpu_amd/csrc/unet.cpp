@@ -782,6 +782,7 @@ class UNetDevice {
 
     size_t weight_bytes() const { return W_.bytes(); }
     size_t pool_bytes() const { return pool_.bytes_held(); }
+    void release_scratch() { pool_.release_below(INT64_MAX); }
 
   private:
     struct Block {
@@ -812,5 +813,6 @@ void UNet::forward(const float *x_dev, int timestep, bool cfg, float *eps_dev, T
 }
 size_t UNet::weight_bytes() const { return d_->weight_bytes(); }
 size_t UNet::pool_bytes() const { return d_->pool_bytes(); }
+void UNet::release_scratch() { d_->release_scratch(); }
 
 }  // namespace mh

@@ -73,6 +73,8 @@ class UNet {
                  void *user = nullptr);
     size_t weight_bytes() const;
     size_t pool_bytes() const;
+    // Frees the pool's idle buffers (Scratch::release_below(usize::MAX), src/engine/mod.rs:87-91).
+    void release_scratch();
 
   private:
     std::unique_ptr<UNetDevice> d_;

@@ -366,6 +366,7 @@ class VaeDevice {
 
     size_t weight_bytes() const { return W_.bytes(); }
     size_t pool_bytes() const { return pool_.bytes_held(); }
+    void release_scratch() { pool_.release_below(INT64_MAX); }
 
   private:
     Context &ctx_;
@@ -390,5 +391,6 @@ void Vae::decode(const float *latents_dev, int h, int w, float *out_dev, TraceFn
 }
 size_t Vae::weight_bytes() const { return d_->weight_bytes(); }
 size_t Vae::pool_bytes() const { return d_->pool_bytes(); }
+void Vae::release_scratch() { d_->release_scratch(); }
 
 }  // namespace mh

@@ -189,6 +189,10 @@ class Engine:
         _lib.check(_lib.lib().mh_engine_memory(self._h, ctypes.byref(wb), ctypes.byref(pb)))
         return wb.value, pb.value
 
+    def release_scratch(self) -> None:
+        """Frees the activation pools and workspace until the next call."""
+        _lib.check(_lib.lib().mh_engine_release_scratch(self._h))
+
     @staticmethod
     def _progress(fn: Optional[Callable[[Progress], Control]]):
         if fn is None:

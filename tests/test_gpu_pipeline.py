@@ -207,6 +207,12 @@ def test_seeded_c_api_equals_the_same_noise_given_explicitly(engine):
     engine.inpaint_with_noise(img.copy(), mask, InpaintParams.resolve(preset=1, steps=2, seed=99),
                               NoiseSet.sample(99))
     assert engine.memory() == before
+    # released on request, allocated again by the next call, same result
+    engine.release_scratch()
+    assert engine.memory()[1] < before[1] and engine.memory()[0] == before[0]
+    c = img.copy()
+    engine.inpaint_with_noise(c, mask, InpaintParams.resolve(preset=1, steps=2, seed=99), NoiseSet.sample(99))
+    assert np.array_equal(c, a)
 
 
 @pytest.fixture(scope="module")

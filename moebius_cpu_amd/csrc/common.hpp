@@ -46,7 +46,8 @@ struct Error : std::runtime_error {
 enum class Precision : uint32_t { Exact = 0, Fast = 1 };
 
 // Tuning overrides for A/B runs and tests, read once from the environment
-// (MOEBIUS_HIP_GEMM_PLAN, _GN_IN_MAXC, _DW_TILED, _TAP_HEADS, _CROSS_HEADS)
+// (MOEBIUS_HIP_GEMM_PLAN, _GN_IN_MAXC, _DW_TILED, _TAP_HEADS, _CROSS_HEADS,
+// _GN_BLOCKS, _GN_APPLY)
 // when a context is created and changed with set_tuning (mh_context_set_tuning).
 // The defaults are the measured choices; nothing on the hot path reads the
 // environment.
@@ -57,6 +58,8 @@ struct Tuning {
     int tap_tile = -1;     // tap filter: -1 default; 0 the per-thread kernel; 4 / 8 the tile kernel's heads
     int tap_heads = 0;     // per-thread tap filter heads per thread (0: default)
     int cross_heads = 0;   // cross-lambda heads per thread (0: default)
+    int gn_blocks = 512;   // GroupNorm statistics: at most this many partial blocks per launch
+    int gn_apply = 0;      // GroupNorm apply pass: 1 walks the map from its end
 };
 // Sets `key` from its text form (the environment variable's syntax); value NULL
 // or "" restores the default. False for an unknown key or a malformed value.

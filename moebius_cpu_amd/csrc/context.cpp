@@ -70,6 +70,8 @@ bool set_tuning(Tuning &t, const char *key, const char *value) {
     if (k == "gn_in_maxc") return to_int(t.gn_in_maxc, -1);
     if (k == "dw_tiled") return to_int(t.dw_tiled, 1);
     if (k == "cross_heads") return to_int(t.cross_heads, 0);
+    if (k == "gn_blocks") return to_int(t.gn_blocks, 512) && t.gn_blocks >= 64;
+    if (k == "gn_apply") return to_int(t.gn_apply, 0) && t.gn_apply >= 0 && t.gn_apply <= 1;
     if (k == "tap_heads") {
         if (clear) {
             t.tap_tile = -1, t.tap_heads = 0;
@@ -92,7 +94,9 @@ Context::Context(int dev) : device(dev) {
                                               {"MOEBIUS_HIP_GN_IN_MAXC", "gn_in_maxc"},
                                               {"MOEBIUS_HIP_DW_TILED", "dw_tiled"},
                                               {"MOEBIUS_HIP_TAP_HEADS", "tap_heads"},
-                                              {"MOEBIUS_HIP_CROSS_HEADS", "cross_heads"}};
+                                              {"MOEBIUS_HIP_CROSS_HEADS", "cross_heads"},
+                                              {"MOEBIUS_HIP_GN_BLOCKS", "gn_blocks"},
+                                              {"MOEBIUS_HIP_GN_APPLY", "gn_apply"}};
     for (const auto &kv : env_keys)
         if (const char *e = std::getenv(kv[0])) set_tuning(tune, kv[1], e);
     int count = 0;

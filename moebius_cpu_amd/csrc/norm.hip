@@ -26,21 +26,13 @@ constexpr int kGnTileC = 64;   // channels per block: 16 lanes x float4
 constexpr int kGnRows = 16;    // pixel rows per block pass
 
 // Pixels per statistics chunk: 64, doubled until the partials grid is at most
-// kGnMaxBlocks blocks, so small maps get many blocks and large maps few
-// enough partials for the fold to stay short.
-int gn_max_blocks() {
-    static const int v = [] {
-        const char *e = std::getenv("MOEBIUS_HIP_GN_BLOCKS");  // tuning override
-        const int b = e ? std::atoi(e) : 0;
-        return b >= 64 ? b : 512;  // 512x512x128: 4096 blocks 78 us, 512 blocks 66 us (stats + SiLU apply)
-    }();
-    return v;
-}
-
-int gn_chunk_px(int n, int hw, int c) {
+// max_blocks blocks (Tuning::gn_blocks, 512: at 512x512x128, 4096 blocks took
+// 78 us and 512 blocks 66 us for statistics + SiLU apply), so small maps get
+// many blocks and large maps few enough partials for the fold to stay short.
+int gn_chunk_px(int n, int hw, int c, int max_blocks) {
     const int64_t ctiles = ceil_div(c, kGnTileC);
     int chunk = 64;
-    while (chunk < hw && ceil_div(hw, chunk) * ctiles * n > gn_max_blocks()) chunk *= 2;
+    while (chunk < hw && ceil_div(hw, chunk) * ctiles * n > max_blocks) chunk *= 2;
     return chunk;
 }
 
@@ -191,8 +183,9 @@ __global__ __launch_bounds__(256) void affine_apply_kernel(const float4 *__restr
                                                            const float4 *__restrict__ scale,
                                                            const float4 *__restrict__ shift, int item4, int c4,
                                                            int silu, int reverse, float4 *__restrict__ out) {
+    // reverse (Tuning::gn_apply): blocks walk the map from its end, where the
+    // statistics pass read last (measured equal at 512x512x128)
     const int b = blockIdx.y;
-    // reverse: blocks walk the map from its end, where the statistics pass read last.
     const int bx = reverse ? int(gridDim.x) - 1 - int(blockIdx.x) : int(blockIdx.x);
     const int e0 = bx * (256 * ITER) + threadIdx.x;
     if (e0 >= item4) return;
@@ -320,8 +313,8 @@ __global__ __launch_bounds__(256) void layer_norm_generic_kernel(const float *__
 namespace {
 
 // Floats of the statistics partials group_norm_affine writes for this shape.
-int64_t gn_partial_floats(int n, int hw, int c) {
-    return int64_t(n) * ceil_div(hw, gn_chunk_px(n, hw, c)) * c * 2;
+int64_t gn_partial_floats(const Context &ctx, int n, int hw, int c) {
+    return int64_t(n) * ceil_div(hw, gn_chunk_px(n, hw, c, ctx.tune.gn_blocks)) * c * 2;
 }
 
 // group_norm_affine with its partials at `part` (gn_partial_floats of them).
@@ -329,7 +322,7 @@ void group_norm_affine_into(Context &ctx, const float *x, int n, int h, int w, i
                             const float *gamma, const float *beta, const float *add, float *scale, float *shift,
                             int64_t add_ld, float *part) {
     const int hw = h * w;
-    const int chunk_px = gn_chunk_px(n, hw, c);
+    const int chunk_px = gn_chunk_px(n, hw, c, ctx.tune.gn_blocks);
     const int nchunks = int(ceil_div(hw, chunk_px));
     const int nctiles = int(ceil_div(c, kGnTileC));
     gn_partial_kernel<<<dim3(nchunks, nctiles, n), 256, 0, ctx.stream>>>(x, add, add_ld, hw, c, chunk_px, nchunks,
@@ -356,7 +349,7 @@ void group_norm_affine(Context &ctx, const float *x, int n, int h, int w, int c,
     if (add_ld <= 0) add_ld = c;
     gn_check(n, h, w, c, groups, x, add, add_ld);
     float *part = static_cast<float *>(
-        ctx.ws.get(size_t(gn_partial_floats(n, h * w, c)) * sizeof(float), ctx.stream));
+        ctx.ws.get(size_t(gn_partial_floats(ctx, n, h * w, c)) * sizeof(float), ctx.stream));
     group_norm_affine_into(ctx, x, n, h, w, c, groups, eps, gamma, beta, add, scale, shift, add_ld, part);
 }
 
@@ -395,13 +388,9 @@ void apply_affine(Context &ctx, const float *x, int n, int h, int w, int c, cons
         constexpr int ITER = 8;
         const int item4 = int(item / 4);
         dim3 grid(unsigned(ceil_div(item4, 256 * ITER)), n);
-        static const int reverse = [] {
-            const char *e = std::getenv("MOEBIUS_HIP_GN_REVERSE");  // tuning override
-            return e ? std::atoi(e) : 0;
-        }();
         affine_apply_kernel<ITER><<<grid, 256, 0, ctx.stream>>>(
             reinterpret_cast<const float4 *>(x), reinterpret_cast<const float4 *>(scale),
-            reinterpret_cast<const float4 *>(shift), item4, c / 4, silu ? 1 : 0, reverse,
+            reinterpret_cast<const float4 *>(shift), item4, c / 4, silu ? 1 : 0, ctx.tune.gn_apply,
             reinterpret_cast<float4 *>(out));
     } else {
         const int64_t total = item * n;
@@ -419,9 +408,9 @@ struct GnForwardScratch {
     int64_t aff_off, total;
 };
 
-GnForwardScratch gn_forward_scratch(int n, int h, int w, int c) {
+GnForwardScratch gn_forward_scratch(const Context &ctx, int n, int h, int w, int c) {
     GnForwardScratch s;
-    s.aff_off = (gn_partial_floats(n, h * w, c) + 63) & ~int64_t(63);
+    s.aff_off = (gn_partial_floats(ctx, n, h * w, c) + 63) & ~int64_t(63);
     s.total = s.aff_off + 2 * int64_t(n) * c;
     return s;
 }
@@ -442,7 +431,7 @@ void group_norm_forward(Context &ctx, const float *x, int n, int h, int w, int c
                         int64_t add_ld) {
     if (add_ld <= 0) add_ld = c;
     gn_check(n, h, w, c, groups, x, add, add_ld);
-    const GnForwardScratch s = gn_forward_scratch(n, h, w, c);
+    const GnForwardScratch s = gn_forward_scratch(ctx, n, h, w, c);
     float *base = static_cast<float *>(ctx.ws.get(size_t(s.total) * sizeof(float), ctx.stream));
     group_norm_forward_in(ctx, x, n, h, w, c, groups, eps, gamma, beta, add, silu, out, add_ld, base, s.aff_off);
 }
@@ -481,7 +470,7 @@ void group_norm_forward_noalloc(Context &ctx, const float *x, int n, int h, int 
                                 const float *gamma, const float *beta, const float *add, bool silu, float *out) {
     const int64_t add_ld = c;
     gn_check(n, h, w, c, groups, x, add, add_ld);
-    const GnForwardScratch s = gn_forward_scratch(n, h, w, c);
+    const GnForwardScratch s = gn_forward_scratch(ctx, n, h, w, c);
     if (s.total > kNoAllocScratchFloats) {
         fail(kInvalidArgument, "GroupNorm (no allocation): this shape needs " + std::to_string(s.total) +
                                    " floats of scratch (statistics partials plus scale/shift for n * c = " +

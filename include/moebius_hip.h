@@ -94,7 +94,8 @@ int32_t mh_context_set_precision(MhContext *ctx, uint32_t precision);
  * the CPU engine's GEMM backend (src/engine/gemm.rs:57-60); no other reference
  * counterpart. key: "gemm_plan" ("bm,bn,splits"), "gn_in_maxc", "dw_tiled",
  * "tap_heads" ("t8", "t4", "8", "4", "2", "1"), "cross_heads", "gn_blocks" (>= 64),
- * "gn_apply" (1: the GroupNorm apply pass walks the map from its end); value NULL or ""
+ * "gn_apply" (1: the GroupNorm apply pass walks the map from its end), "wino_fused" (-1:
+ * Winograd convs in one kernel where that is faster, 1: wherever it fits, 0: never); value NULL or ""
  * restores the measured default. The same settings are read once from the
  * MOEBIUS_HIP_<KEY> environment variables when the context is created. */
 int32_t mh_context_set_tuning(MhContext *ctx, const char *key, const char *value);

@@ -47,7 +47,7 @@ enum class Precision : uint32_t { Exact = 0, Fast = 1 };
 
 // Tuning overrides for A/B runs and tests, read once from the environment
 // (MOEBIUS_HIP_GEMM_PLAN, _GN_IN_MAXC, _DW_TILED, _TAP_HEADS, _CROSS_HEADS,
-// _GN_BLOCKS, _GN_APPLY)
+// _GN_BLOCKS, _GN_APPLY, _WINO_FUSED)
 // when a context is created and changed with set_tuning (mh_context_set_tuning).
 // The defaults are the measured choices; nothing on the hot path reads the
 // environment.
@@ -60,6 +60,7 @@ struct Tuning {
     int cross_heads = 0;   // cross-lambda heads per thread (0: default)
     int gn_blocks = 512;   // GroupNorm statistics: at most this many partial blocks per launch
     int gn_apply = 0;      // GroupNorm apply pass: 1 walks the map from its end
+    int wino_fused = -1;   // Winograd convs in one kernel: -1 where faster, 1 wherever it fits, 0 never
 };
 // Sets `key` from its text form (the environment variable's syntax); value NULL
 // or "" restores the default. False for an unknown key or a malformed value.

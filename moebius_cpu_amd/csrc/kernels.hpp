@@ -128,6 +128,11 @@ void winograd_input_transform(Context &ctx, const float *x, int n, int h, int w,
 // m [16][tiles][c_out] -> out [n, H, W, c_out] = A^T m A + bias (+ residual2).
 void winograd_output_transform(Context &ctx, const float *m, int n, int h, int w, int c_out, bool upsample2x,
                                const float *bias, const float *residual2, float *out);
+// The whole conv in one kernel (winograd_fused.hip) for f32 u, c_in % 32 == 0,
+// c_out % 64 == 0 and operands under 2 GiB; false (nothing launched) otherwise.
+bool conv3x3_winograd_fused(Context &ctx, const float *x, int n, int h, int w, int c_in, const float *u, int c_out,
+                            const float *bias, bool upsample2x, const Affine *prologue, float *out,
+                            const float *residual2);
 // The whole conv: u from winograd_weight_transform (ut kF32) or an f16 copy of it.
 void conv3x3_winograd(Context &ctx, const float *x, int n, int h, int w, int c_in, const void *u, WeightType ut,
                       int c_out, const float *bias, bool upsample2x, const Affine *prologue, float *out,

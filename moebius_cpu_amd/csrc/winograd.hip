@@ -229,6 +229,11 @@ void conv3x3_winograd(Context &ctx, const float *x, int n, int h, int w, int c_i
     MH_REQUIRE(tiles < (int64_t(1) << 31) && tiles * std::max(c_in, c_out) * 4 < (int64_t(1) << 31),
                "Winograd conv: plane above 2 GiB");
     if (tiles == 0) return;
+    // EXACT arithmetic on f32 kernels: the fused kernel, where it takes the shape
+    if (ut == kF32 && ctx.precision == Precision::Exact &&
+        conv3x3_winograd_fused(ctx, x, n, h, w, c_in, static_cast<const float *>(u), c_out, bias, upsample2x,
+                               prologue, out, residual2))
+        return;
     // V and M share one workspace block; the batched GEMM (batch > 1) never splits K,
     // so it does not touch the workspace itself.
     const size_t vbytes = (size_t(16) * tiles * c_in * sizeof(float) + 255) & ~size_t(255);

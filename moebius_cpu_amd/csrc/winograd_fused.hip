@@ -1,0 +1,296 @@
+// Winograd F(2x2, 3x3) conv in one kernel (src/engine/winograd.rs:48-120):
+// the input transform, the 16 plane products and the output transform of a
+// block of 32 tiles x 64 output channels stay on chip, so V and M (16 planes
+// of tiles x channels each) never reach HBM. The separate path writes and
+// reads both: about 4.2 GB per 512x512x128 conv of the VAE decoder.
+//
+// Workgroup: 256 threads, one per CU (LDS: two V stages of 72 KB). Per chunk
+// of 32 input channels every thread transforms one tile's 4x4 patch for four
+// channels (the reference's operation order, as wino_input_kernel) into the
+// V stage [plane][tile][channel]; wave w then multiplies planes 4w..4w+3 on
+// v_mfma_f32_32x32x2f32 (tiles x 64 channels, two 32x32 blocks per plane),
+// reading V from LDS and U [plane][co][ci] from global memory (L2 resident).
+// The next chunk's patch loads are in flight during the current chunk's
+// last products. At the end the 16 planes go through LDS and each thread applies
+// the output transform (winograd.rs:329-352, as wino_output_kernel) to one
+// tile and four channels, adding bias and the optional residual.
+#include "common.hpp"
+#include "dmath.hpp"
+#include "kernels.hpp"
+
+namespace mh {
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kFT = 32;        // tiles per workgroup
+constexpr int kFC = 64;        // output channels per workgroup
+constexpr int kFK = 32;        // input channels per chunk
+constexpr int kVS = kFK + 4;   // V row stride in LDS (floats)
+constexpr int kMS = kFC + 4;   // M row stride in LDS (floats)
+constexpr int kVStage = 16 * kFT * kVS;
+constexpr int kLds = 2 * kVStage;  // 36864 floats = 144 KB
+static_assert(16 * kFT * kMS <= kLds, "the M exchange fits in the V stages");
+constexpr int kOob = int(0x80000000u);
+
+struct FGeo {
+    int h, w, hi, wi, th, tw;
+    int64_t tiles;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), short(0), int(bytes), 0x00020000);
+}
+
+__device__ __forceinline__ floatx4 ld4(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+__device__ __forceinline__ floatx4 sub4(floatx4 a, floatx4 b) { return floatx4{a[0] - b[0], a[1] - b[1], a[2] - b[2], a[3] - b[3]}; }
+__device__ __forceinline__ floatx4 add4(floatx4 a, floatx4 b) { return floatx4{a[0] + b[0], a[1] + b[1], a[2] + b[2], a[3] + b[3]}; }
+
+template <int UP, bool PRO>
+__global__ __launch_bounds__(256, 1) void wino_fused_kernel(const float *__restrict__ x, uint32_t x_bytes, FGeo g,
+                                                            int ci, const float *__restrict__ u, uint32_t u_bytes,
+                                                            int co, const float *__restrict__ psc,
+                                                            const float *__restrict__ psh, int psilu,
+                                                            const float *__restrict__ bias,
+                                                            const float *__restrict__ res2, float *__restrict__ out,
+                                                            int nco_blocks, int nwork) {
+    __shared__ float lds[kLds];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // Work order: channel block outer, tile block inner; workgroup i runs on
+    // XCD i % 8 (round-robin dispatch), and each XCD takes one contiguous
+    // eighth of the order, so it works through few channel blocks and their
+    // U panels stay in its L2. The grid is padded to a multiple of 8; the
+    // padding workgroups have no work.
+    const int ntb = nwork / nco_blocks;
+    const int per_xcd = int(gridDim.x) / 8;
+    const int work = (int(blockIdx.x) % 8) * per_xcd + int(blockIdx.x) / 8;
+    if (work >= nwork) return;
+    const int64_t t0 = int64_t(work % ntb) * kFT;
+    const int co0 = (work / ntb) * kFC;
+    const __amdgpu_buffer_rsrc_t xr = rsrc(x, x_bytes), ur = rsrc(u, u_bytes);
+
+    // Producer role: tile vt of the block, channel quad vq of the chunk.
+    const int vt = tid & (kFT - 1), vq = tid >> 5;
+    const int64_t tv = t0 + vt;
+    const int per_item = g.th * g.tw;
+    const int vb = int(tv / per_item), vrem = int(tv - int64_t(vb) * per_item);
+    const int vty = vrem / g.tw, vtx = vrem - vty * g.tw;
+    int poff[16];  // byte offset of each patch pixel's channel 0, or kOob outside the image
+    unsigned valid = 0;
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+        const int iy = 2 * vty + (kk >> 2) - 1, ix = 2 * vtx + (kk & 3) - 1;
+        const bool in = tv < g.tiles && iy >= 0 && iy < g.hi && ix >= 0 && ix < g.wi;
+        poff[kk] = in ? (((vb * g.h + (iy >> UP)) * g.w + (ix >> UP)) * ci + 4 * vq) * 4 : kOob;
+        valid |= in ? (1u << kk) : 0u;
+    }
+    floatx4 d[16];
+    auto produce = [&](int kc) {
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) d[kk] = ld4(xr, poff[kk] == kOob ? kOob : poff[kk] + kc * kFK * 4);
+    };
+    auto transform_store = [&](int kc, int stage) {
+        if constexpr (PRO) {
+            const int c = kc * kFK + 4 * vq;
+            const floatx4 sc = *reinterpret_cast<const floatx4 *>(psc + int64_t(vb) * ci + c);
+            const floatx4 sh = *reinterpret_cast<const floatx4 *>(psh + int64_t(vb) * ci + c);
+#pragma unroll
+            for (int kk = 0; kk < 16; ++kk) {
+                if (valid & (1u << kk)) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float y = __builtin_fmaf(d[kk][e], sc[e], sh[e]);
+                        if (psilu) y = ref_silu(y);
+                        d[kk][e] = y;
+                    }
+                }
+            }
+        }
+        floatx4 tt[16];
+#pragma unroll
+        for (int col = 0; col < 4; ++col) {
+            const floatx4 d0 = d[col], d1 = d[4 + col], d2 = d[8 + col], d3 = d[12 + col];
+            tt[col] = sub4(d0, d2);
+            tt[4 + col] = add4(d1, d2);
+            tt[8 + col] = sub4(d2, d1);
+            tt[12 + col] = sub4(d1, d3);
+        }
+        float *vs = lds + stage * kVStage + vt * kVS + 4 * vq;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const floatx4 *q = tt + r * 4;
+            *reinterpret_cast<floatx4 *>(vs + (r * 4) * kFT * kVS) = sub4(q[0], q[2]);
+            *reinterpret_cast<floatx4 *>(vs + (r * 4 + 1) * kFT * kVS) = add4(q[1], q[2]);
+            *reinterpret_cast<floatx4 *>(vs + (r * 4 + 2) * kFT * kVS) = sub4(q[2], q[1]);
+            *reinterpret_cast<floatx4 *>(vs + (r * 4 + 3) * kFT * kVS) = sub4(q[1], q[3]);
+        }
+    };
+
+    // Consumer role: wave w, planes 4w..4w+3, two 32x32 blocks of 64 channels.
+    // Lane l reads a float4 along K of row l % 32 at K offset 4 (l / 32); MFMA t
+    // takes its component t, so both operands pair k = 8 s + 4 (l / 32) + t.
+    floatx16 acc[4][2];
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[p][j][v] = 0.f;
+    const int row = lane & 31, kq = 4 * (lane >> 5);
+    // U [16][co][ci]: plane 4w + p, channel co0 + 32 j + row, K offset kq
+    int uoff[4][2];
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) uoff[p][j] = (((4 * wave + p) * co + co0 + 32 * j + row) * ci + kq) * 4;
+    // Loads are waited for in issue order, so the order is chosen to never
+    // wait on more than the next operands: U for sub-step s + 1 is issued with
+    // sub-step s, the next chunk's patch with the last sub-step (it lands
+    // during those products and the transform waits for it), and U for the
+    // next chunk's first sub-step after that, to land during the transform.
+    floatx4 b[4][2], bn[4][2];
+    auto load_b = [&](floatx4 (&dst)[4][2], int kc, int s) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) dst[p][j] = ld4(ur, uoff[p][j] + kc * kFK * 4 + s * 32);
+    };
+    const int nk = ci / kFK;
+    produce(0);
+    load_b(b, 0, 0);
+    transform_store(0, 0);
+    __syncthreads();
+    for (int kc = 0; kc < nk; ++kc) {
+        const bool more = kc + 1 < nk;
+        const float *vs = lds + (kc & 1) * kVStage + row * kVS + kq;
+#pragma unroll
+        for (int s = 0; s < kFK / 8; ++s) {
+            const bool last = s + 1 == kFK / 8;
+            if (!last) load_b(bn, kc, s + 1);
+            else if (more) produce(kc + 1);
+            floatx4 a[4];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) a[p] = *reinterpret_cast<const floatx4 *>(vs + (4 * wave + p) * kFT * kVS + 8 * s);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int p = 0; p < 4; ++p)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[p][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[p][t], b[p][j][t], acc[p][j], 0, 0, 0);
+            if (!last) {
+#pragma unroll
+                for (int p = 0; p < 4; ++p)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) b[p][j] = bn[p][j];
+            } else if (more) {
+                load_b(b, kc + 1, 0);
+            }
+        }
+        if (more) transform_store(kc + 1, (kc + 1) & 1);
+        __syncthreads();
+    }
+
+    // M [16][tile][channel] through LDS: register v of lane l holds row
+    // 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32 of its block.
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int tr = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
+                lds[((4 * wave + p) * kFT + tr) * kMS + 32 * j + row] = acc[p][j][v];
+            }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < (kFT * kFC / 4) / 256; ++r) {
+        const int item = tid + 256 * r;
+        const int tl = item / (kFC / 4), q = item - tl * (kFC / 4);
+        const int64_t t = t0 + tl;
+        if (t >= g.tiles) continue;
+        const int b = int(t / per_item), rem = int(t - int64_t(b) * per_item);
+        const int ty = rem / g.tw, tx = rem - ty * g.tw;
+        const float *src = lds + tl * kMS + 4 * q;
+        floatx4 u0[4], u1[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const floatx4 a = *reinterpret_cast<const floatx4 *>(src + (rr * 4) * kFT * kMS);
+            const floatx4 bb = *reinterpret_cast<const floatx4 *>(src + (rr * 4 + 1) * kFT * kMS);
+            const floatx4 cc = *reinterpret_cast<const floatx4 *>(src + (rr * 4 + 2) * kFT * kMS);
+            const floatx4 dd = *reinterpret_cast<const floatx4 *>(src + (rr * 4 + 3) * kFT * kMS);
+            u0[rr] = add4(add4(a, bb), cc);
+            u1[rr] = sub4(sub4(bb, cc), dd);
+        }
+        const int c = co0 + 4 * q;
+        const floatx4 bv = bias ? *reinterpret_cast<const floatx4 *>(bias + c) : floatx4{0.f, 0.f, 0.f, 0.f};
+        floatx4 y[4];
+        y[0] = add4(add4(add4(u0[0], u0[1]), u0[2]), bv);
+        y[1] = add4(add4(add4(u1[0], u1[1]), u1[2]), bv);
+        y[2] = add4(sub4(sub4(u0[1], u0[2]), u0[3]), bv);
+        y[3] = add4(sub4(sub4(u1[1], u1[2]), u1[3]), bv);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const int oy = 2 * ty + (kk >> 1), ox = 2 * tx + (kk & 1);
+            if (oy >= g.hi || ox >= g.wi) continue;
+            const int64_t o = ((int64_t(b) * g.hi + oy) * g.wi + ox) * co + c;
+            floatx4 rv = y[kk];
+            if (res2) rv = add4(rv, *reinterpret_cast<const floatx4 *>(res2 + o));
+            *reinterpret_cast<floatx4 *>(out + o) = rv;
+        }
+    }
+}
+
+template <int UP, bool PRO>
+void launch_fused(Context &ctx, int nwork, const float *x, uint32_t xb, const FGeo &g, int ci, const float *u,
+                  uint32_t ub, int co, const Affine *pro, const float *bias, const float *res2, float *out) {
+    // padded to a multiple of 8 workgroups (see the work order in the kernel)
+    const unsigned grid = unsigned(ceil_div(nwork, 8) * 8);
+    wino_fused_kernel<UP, PRO><<<grid, 256, 0, ctx.stream>>>(x, xb, g, ci, u, ub, co, pro ? pro->scale : nullptr,
+                                                             pro ? pro->shift : nullptr, pro && pro->silu ? 1 : 0,
+                                                             bias, res2, out, co / kFC, nwork);
+}
+
+}  // namespace
+
+bool conv3x3_winograd_fused(Context &ctx, const float *x, int n, int h, int w, int c_in, const float *u, int c_out,
+                            const float *bias, bool upsample2x, const Affine *prologue, float *out,
+                            const float *residual2) {
+    if (ctx.tune.wino_fused == 0 || c_in % kFK || c_out % kFC) return false;
+    // Where it is faster (A/B per conv on MI355X): 512x512x128 -> 128 733 -> 546 us,
+    // 256x256x256 -> 256 516 -> 512 us (upsampled input 1803 -> 1741 us). Above
+    // 256 channels the batched plane GEMM reaches 83% of f32 MFMA peak, this
+    // kernel about 45% (one wave per SIMD), and its saved V / M traffic is smaller
+    // than the loss (128x128x512 -> 512: 426 -> 487 us): those keep three kernels.
+    if (ctx.tune.wino_fused < 0 && (c_in > 256 || c_out > 256)) return false;
+    if (!aligned16(x) || !aligned16(u) || !aligned16(out) || !aligned16(bias) || !aligned16(residual2)) return false;
+    if (prologue && (!aligned16(prologue->scale) || !aligned16(prologue->shift))) return false;
+    const int64_t x_bytes = int64_t(n) * h * w * c_in * 4, u_bytes = int64_t(16) * c_out * c_in * 4;
+    if (x_bytes >= (int64_t(1) << 31) || u_bytes >= (int64_t(1) << 31)) return false;
+    FGeo g;
+    const int up = upsample2x ? 1 : 0;
+    g.h = h, g.w = w, g.hi = h << up, g.wi = w << up;
+    g.th = (g.hi + 1) / 2, g.tw = (g.wi + 1) / 2;
+    g.tiles = int64_t(n) * g.th * g.tw;
+    if (ctx.tune.wino_fused < 0 && g.tiles < 16384) return false;
+    if (g.tiles == 0) return true;
+    const int64_t blocks = ceil_div(g.tiles, kFT) * (c_out / kFC);
+    if (blocks >= (int64_t(1) << 30)) return false;
+    const int nwork = int(blocks);
+    const uint32_t xb = uint32_t(x_bytes), ub = uint32_t(u_bytes);
+    if (up) {
+        if (prologue) launch_fused<1, true>(ctx, nwork, x, xb, g, c_in, u, ub, c_out, prologue, bias, residual2, out);
+        else launch_fused<1, false>(ctx, nwork, x, xb, g, c_in, u, ub, c_out, prologue, bias, residual2, out);
+    } else {
+        if (prologue) launch_fused<0, true>(ctx, nwork, x, xb, g, c_in, u, ub, c_out, prologue, bias, residual2, out);
+        else launch_fused<0, false>(ctx, nwork, x, xb, g, c_in, u, ub, c_out, prologue, bias, residual2, out);
+    }
+    MH_LAUNCH_CHECK();
+    return true;
+}
+
+}  // namespace mh

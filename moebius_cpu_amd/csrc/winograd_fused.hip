@@ -4,16 +4,22 @@
 // of tiles x channels each) never reach HBM. The separate path writes and
 // reads both: about 4.2 GB per 512x512x128 conv of the VAE decoder.
 //
-// Workgroup: 256 threads, one per CU (LDS: two V stages of 72 KB). Per chunk
-// of 32 input channels every thread transforms one tile's 4x4 patch for four
-// channels (the reference's operation order, as wino_input_kernel) into the
-// V stage [plane][tile][channel]; wave w then multiplies planes 4w..4w+3 on
-// v_mfma_f32_32x32x2f32 (tiles x 64 channels, two 32x32 blocks per plane),
-// reading V from LDS and U [plane][co][ci] from global memory (L2 resident).
-// The next chunk's patch loads are in flight during the current chunk's
-// last products. At the end the 16 planes go through LDS and each thread applies
+// Workgroup: 512 threads, one per CU (LDS: two V stages of 72 KB). Per chunk
+// of 32 input channels each of the first 256 threads transforms one tile's
+// 4x4 patch for four channels (the reference's operation order, as
+// wino_input_kernel) into the V stage [plane][tile][channel]; wave w (of 8,
+// two per SIMD) then multiplies planes 2w and 2w + 1 on v_mfma_f32_32x32x2f32
+// (tiles x 64 channels, two 32x32 blocks per plane), reading V from LDS and
+// U [plane][co][ci] from global memory (L2 resident). The next chunk's patch
+// loads are in flight during the current chunk's last three quarters of
+// products. At the end the 16 planes go through LDS and each thread applies
 // the output transform (winograd.rs:329-352, as wino_output_kernel) to one
 // tile and four channels, adding bias and the optional residual.
+//
+// Timed per workgroup at 512x512x128 (in-kernel clock): first chunk ready
+// 4.0 us, chunks 6.5-6.8 us (4.3 us for the last, which transforms nothing),
+// output transform 2.0 us; 16 rounds of 256 workgroups: 505 us against 730
+// us for transforms + batched GEMM.
 #include "common.hpp"
 #include "dmath.hpp"
 #include "kernels.hpp"
@@ -50,8 +56,11 @@ __device__ __forceinline__ floatx4 ld4(__amdgpu_buffer_rsrc_t r, int off) {
 __device__ __forceinline__ floatx4 sub4(floatx4 a, floatx4 b) { return floatx4{a[0] - b[0], a[1] - b[1], a[2] - b[2], a[3] - b[3]}; }
 __device__ __forceinline__ floatx4 add4(floatx4 a, floatx4 b) { return floatx4{a[0] + b[0], a[1] + b[1], a[2] + b[2], a[3] + b[3]}; }
 
+constexpr int kFThreads = 512;  // 8 waves, two per SIMD
+constexpr int kFPlanes = 16 / (kFThreads / 64);  // planes per wave
+
 template <int UP, bool PRO>
-__global__ __launch_bounds__(256, 1) void wino_fused_kernel(const float *__restrict__ x, uint32_t x_bytes, FGeo g,
+__global__ __launch_bounds__(kFThreads, 2) void wino_fused_kernel(const float *__restrict__ x, uint32_t x_bytes, FGeo g,
                                                             int ci, const float *__restrict__ u, uint32_t u_bytes,
                                                             int co, const float *__restrict__ psc,
                                                             const float *__restrict__ psh, int psilu,
@@ -74,7 +83,8 @@ __global__ __launch_bounds__(256, 1) void wino_fused_kernel(const float *__restr
     const __amdgpu_buffer_rsrc_t xr = rsrc(x, x_bytes), ur = rsrc(u, u_bytes);
 
     // Producer role: tile vt of the block, channel quad vq of the chunk.
-    const int vt = tid & (kFT - 1), vq = tid >> 5;
+    const bool producer = tid < kFT * (kFK / 4);
+    const int vt = tid & (kFT - 1), vq = (tid >> 5) & (kFK / 4 - 1);
     const int64_t tv = t0 + vt;
     const int per_item = g.th * g.tw;
     const int vb = int(tv / per_item), vrem = int(tv - int64_t(vb) * per_item);
@@ -84,7 +94,7 @@ __global__ __launch_bounds__(256, 1) void wino_fused_kernel(const float *__restr
 #pragma unroll
     for (int kk = 0; kk < 16; ++kk) {
         const int iy = 2 * vty + (kk >> 2) - 1, ix = 2 * vtx + (kk & 3) - 1;
-        const bool in = tv < g.tiles && iy >= 0 && iy < g.hi && ix >= 0 && ix < g.wi;
+        const bool in = producer && tv < g.tiles && iy >= 0 && iy < g.hi && ix >= 0 && ix < g.wi;
         poff[kk] = in ? (((vb * g.h + (iy >> UP)) * g.w + (ix >> UP)) * ci + 4 * vq) * 4 : kOob;
         valid |= in ? (1u << kk) : 0u;
     }
@@ -94,6 +104,7 @@ __global__ __launch_bounds__(256, 1) void wino_fused_kernel(const float *__restr
         for (int kk = 0; kk < 16; ++kk) d[kk] = ld4(xr, poff[kk] == kOob ? kOob : poff[kk] + kc * kFK * 4);
     };
     auto transform_store = [&](int kc, int stage) {
+        if (!producer) return;
         if constexpr (PRO) {
             const int c = kc * kFK + 4 * vq;
             const floatx4 sc = *reinterpret_cast<const floatx4 *>(psc + int64_t(vb) * ci + c);
@@ -130,86 +141,88 @@ __global__ __launch_bounds__(256, 1) void wino_fused_kernel(const float *__restr
         }
     };
 
-    // Consumer role: wave w, planes 4w..4w+3, two 32x32 blocks of 64 channels.
+    // Consumer role: wave w, planes kFPlanes w .. + kFPlanes - 1, two 32x32 blocks of 64 channels.
     // Lane l reads a float4 along K of row l % 32 at K offset 4 (l / 32); MFMA t
     // takes its component t, so both operands pair k = 8 s + 4 (l / 32) + t.
-    floatx16 acc[4][2];
+    floatx16 acc[kFPlanes][2];
 #pragma unroll
-    for (int p = 0; p < 4; ++p)
+    for (int p = 0; p < kFPlanes; ++p)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[p][j][v] = 0.f;
     const int row = lane & 31, kq = 4 * (lane >> 5);
     // U [16][co][ci]: plane 4w + p, channel co0 + 32 j + row, K offset kq
-    int uoff[4][2];
+    int uoff[kFPlanes][2];
 #pragma unroll
-    for (int p = 0; p < 4; ++p)
+    for (int p = 0; p < kFPlanes; ++p)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) uoff[p][j] = (((4 * wave + p) * co + co0 + 32 * j + row) * ci + kq) * 4;
+        for (int j = 0; j < 2; ++j) uoff[p][j] = (((kFPlanes * wave + p) * co + co0 + 32 * j + row) * ci + kq) * 4;
     // Loads are waited for in issue order, so the order is chosen to never
-    // wait on more than the next operands: U for sub-step s + 1 is issued with
-    // sub-step s, the next chunk's patch with the last sub-step (it lands
-    // during those products and the transform waits for it), and U for the
-    // next chunk's first sub-step after that, to land during the transform.
-    floatx4 b[4][2], bn[4][2];
-    auto load_b = [&](floatx4 (&dst)[4][2], int kc, int s) {
+    // wait on more than the next operands: U for sub-step 1 is issued with
+    // sub-step 0, U for sub-steps 2 and 3 with sub-step 1 and after them the
+    // next chunk's patch (it lands during the last three sub-steps' products;
+    // the transform waits for it), and U for the next chunk's first sub-step
+    // after the last products, to land during the transform.
+    static_assert(kFK / 8 == 4, "four K sub-steps per chunk");
+    floatx4 b0[kFPlanes][2], b1[kFPlanes][2], b2[kFPlanes][2], b3[kFPlanes][2];
+    auto load_b = [&](floatx4 (&dst)[kFPlanes][2], int kc, int s) {
 #pragma unroll
-        for (int p = 0; p < 4; ++p)
+        for (int p = 0; p < kFPlanes; ++p)
 #pragma unroll
             for (int j = 0; j < 2; ++j) dst[p][j] = ld4(ur, uoff[p][j] + kc * kFK * 4 + s * 32);
     };
+    auto mfma_step = [&](const float *vs, int s, const floatx4 (&b)[kFPlanes][2]) {
+        floatx4 a[kFPlanes];
+#pragma unroll
+        for (int p = 0; p < kFPlanes; ++p)
+            a[p] = *reinterpret_cast<const floatx4 *>(vs + (kFPlanes * wave + p) * kFT * kVS + 8 * s);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int p = 0; p < kFPlanes; ++p)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[p][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[p][t], b[p][j][t], acc[p][j], 0, 0, 0);
+    };
     const int nk = ci / kFK;
     produce(0);
-    load_b(b, 0, 0);
+    load_b(b0, 0, 0);
     transform_store(0, 0);
     __syncthreads();
     for (int kc = 0; kc < nk; ++kc) {
         const bool more = kc + 1 < nk;
         const float *vs = lds + (kc & 1) * kVStage + row * kVS + kq;
-#pragma unroll
-        for (int s = 0; s < kFK / 8; ++s) {
-            const bool last = s + 1 == kFK / 8;
-            if (!last) load_b(bn, kc, s + 1);
-            else if (more) produce(kc + 1);
-            floatx4 a[4];
-#pragma unroll
-            for (int p = 0; p < 4; ++p) a[p] = *reinterpret_cast<const floatx4 *>(vs + (4 * wave + p) * kFT * kVS + 8 * s);
-#pragma unroll
-            for (int t = 0; t < 4; ++t)
-#pragma unroll
-                for (int p = 0; p < 4; ++p)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j)
-                        acc[p][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[p][t], b[p][j][t], acc[p][j], 0, 0, 0);
-            if (!last) {
-#pragma unroll
-                for (int p = 0; p < 4; ++p)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) b[p][j] = bn[p][j];
-            } else if (more) {
-                load_b(b, kc + 1, 0);
-            }
+        load_b(b1, kc, 1);
+        mfma_step(vs, 0, b0);
+        load_b(b2, kc, 2);
+        load_b(b3, kc, 3);
+        if (more) produce(kc + 1);
+        mfma_step(vs, 1, b1);
+        mfma_step(vs, 2, b2);
+        mfma_step(vs, 3, b3);
+        if (more) {
+            load_b(b0, kc + 1, 0);
+            transform_store(kc + 1, (kc + 1) & 1);
         }
-        if (more) transform_store(kc + 1, (kc + 1) & 1);
         __syncthreads();
     }
 
     // M [16][tile][channel] through LDS: register v of lane l holds row
     // 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32 of its block.
 #pragma unroll
-    for (int p = 0; p < 4; ++p)
+    for (int p = 0; p < kFPlanes; ++p)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int tr = 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-                lds[((4 * wave + p) * kFT + tr) * kMS + 32 * j + row] = acc[p][j][v];
+                lds[((kFPlanes * wave + p) * kFT + tr) * kMS + 32 * j + row] = acc[p][j][v];
             }
     __syncthreads();
 #pragma unroll
-    for (int r = 0; r < (kFT * kFC / 4) / 256; ++r) {
-        const int item = tid + 256 * r;
+    for (int r = 0; r < (kFT * kFC / 4) / kFThreads; ++r) {
+        const int item = tid + kFThreads * r;
         const int tl = item / (kFC / 4), q = item - tl * (kFC / 4);
         const int64_t t = t0 + tl;
         if (t >= g.tiles) continue;
@@ -250,7 +263,7 @@ void launch_fused(Context &ctx, int nwork, const float *x, uint32_t xb, const FG
                   uint32_t ub, int co, const Affine *pro, const float *bias, const float *res2, float *out) {
     // padded to a multiple of 8 workgroups (see the work order in the kernel)
     const unsigned grid = unsigned(ceil_div(nwork, 8) * 8);
-    wino_fused_kernel<UP, PRO><<<grid, 256, 0, ctx.stream>>>(x, xb, g, ci, u, ub, co, pro ? pro->scale : nullptr,
+    wino_fused_kernel<UP, PRO><<<grid, kFThreads, 0, ctx.stream>>>(x, xb, g, ci, u, ub, co, pro ? pro->scale : nullptr,
                                                              pro ? pro->shift : nullptr, pro && pro->silu ? 1 : 0,
                                                              bias, res2, out, co / kFC, nwork);
 }
@@ -261,11 +274,11 @@ bool conv3x3_winograd_fused(Context &ctx, const float *x, int n, int h, int w, i
                             const float *bias, bool upsample2x, const Affine *prologue, float *out,
                             const float *residual2) {
     if (ctx.tune.wino_fused == 0 || c_in % kFK || c_out % kFC) return false;
-    // Where it is faster (A/B per conv on MI355X): 512x512x128 -> 128 733 -> 546 us,
-    // 256x256x256 -> 256 516 -> 512 us (upsampled input 1803 -> 1741 us). Above
-    // 256 channels the batched plane GEMM reaches 83% of f32 MFMA peak, this
-    // kernel about 45% (one wave per SIMD), and its saved V / M traffic is smaller
-    // than the loss (128x128x512 -> 512: 426 -> 487 us): those keep three kernels.
+    // Where it is faster (A/B per conv on MI355X): 512x512x128 -> 128 720 -> 540 us,
+    // 256x256x256 -> 256 about equal (528 / 524 us). Above 256 channels the
+    // batched plane GEMM reaches 83% of f32 MFMA peak, this kernel about 45%,
+    // and the V / M traffic it saves is smaller than that loss (128x128x512 ->
+    // 512: 413 -> 504 us): those keep three kernels.
     if (ctx.tune.wino_fused < 0 && (c_in > 256 || c_out > 256)) return false;
     if (!aligned16(x) || !aligned16(u) || !aligned16(out) || !aligned16(bias) || !aligned16(residual2)) return false;
     if (prologue && (!aligned16(prologue->scale) || !aligned16(prologue->shift))) return false;

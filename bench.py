@@ -215,15 +215,17 @@ DOMINANT_TRAFFIC_BYTES = int((13.28 + 10.00) * 1048576)
 
 def _dominant_gemm(ctx, steps, fast=False):
     """The step's most frequent GEMM, timed on its own with events: the 1x1 conv of
-    a [2,64,64,320] map to 320 channels with bias, M = 8192, N = 320, K = 320."""
+    a [2,64,64,320] map to 320 channels with bias, M = 8192, N = 320, K = 320.
+    Timed after `steps` warm-up launches (about 4 ms at 200): a freshly created
+    operand set timed after a single launch reads 10-15% slow while clocks and
+    caches settle, which no launch inside a denoise step sees."""
     from moebius_cpu_amd import engine as E
     from moebius_cpu_amd import synthetic as S
 
     x = E.Tensor.from_numpy(ctx, S.normal(81, (2, 64, 64, 320)))
     conv = E.Conv1x1(ctx, 320, 320, E.Param(ctx, S.normal(82, (320, 320), 0.05), f16=fast), S.normal(83, (320,), 0.02))
     y = E.Tensor(ctx)
-    conv.forward(x, y)
-    us = time_region(ctx, lambda: conv.forward(x, y), steps) * 1e3
+    us = warm_time(ctx, lambda: conv.forward(x, y), steps, warmup=steps) * 1e3
     flops = 2.0 * 8192 * 320 * 320
     tf = flops / (us * 1e-6) / 1e12
     if fast:
@@ -330,7 +332,7 @@ def bench_unet(args):
                           "direct_equivalent_tflops": head["direct_equivalent_tflops"]},
     }
     log("dominant kernel and component kernels")
-    out["roofline"] = _dominant_gemm(ctx, 50, fast=args.fast)
+    out["roofline"] = _dominant_gemm(ctx, 200, fast=args.fast)
     ctx.set_precision(False)
     out["components"] = _components(ctx, 20)
     unet_entries = None

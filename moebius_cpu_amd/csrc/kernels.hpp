@@ -128,15 +128,19 @@ void winograd_input_transform(Context &ctx, const float *x, int n, int h, int w,
 // m [16][tiles][c_out] -> out [n, H, W, c_out] = A^T m A + bias (+ residual2).
 void winograd_output_transform(Context &ctx, const float *m, int n, int h, int w, int c_out, bool upsample2x,
                                const float *bias, const float *residual2, float *out);
+// u [16][c_out][c_in] -> uf [16][c_in / 8][c_out][8], the fused kernel's operand order.
+void winograd_fused_weights(Context &ctx, const float *u, int c_out, int c_in, float *uf);
 // The whole conv in one kernel (winograd_fused.hip) for f32 u, c_in % 32 == 0,
 // c_out % 64 == 0 and operands under 2 GiB; false (nothing launched) otherwise.
-bool conv3x3_winograd_fused(Context &ctx, const float *x, int n, int h, int w, int c_in, const float *u, int c_out,
-                            const float *bias, bool upsample2x, const Affine *prologue, float *out,
-                            const float *residual2);
-// The whole conv: u from winograd_weight_transform (ut kF32) or an f16 copy of it.
+// uf: u in the fused order, or NULL (then made in the workspace for this call).
+bool conv3x3_winograd_fused(Context &ctx, const float *x, int n, int h, int w, int c_in, const float *u,
+                            const float *uf, int c_out, const float *bias, bool upsample2x, const Affine *prologue,
+                            float *out, const float *residual2);
+// The whole conv: u from winograd_weight_transform (ut kF32) or an f16 copy of it;
+// uf (optional) its fused-order copy for the one-kernel path.
 void conv3x3_winograd(Context &ctx, const float *x, int n, int h, int w, int c_in, const void *u, WeightType ut,
                       int c_out, const float *bias, bool upsample2x, const Affine *prologue, float *out,
-                      const float *residual2 = nullptr);
+                      const float *residual2 = nullptr, const float *uf = nullptr);
 void selftest_mfma_f32(Context &ctx, const float *a_host, const float *b_host, float *d_host);
 
 // ---- lambda layers (lambda.hip), src/unet/lambda.rs

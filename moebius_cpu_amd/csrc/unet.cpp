@@ -95,6 +95,16 @@ const float *WeightStore::winograd_kernel(const DParam &w, int co, int ci) const
     return static_cast<const float *>(u);
 }
 
+const float *WeightStore::winograd_kernel_fused(const float *u, int co, int ci) const {
+    const size_t bytes = size_t(16) * co * ci * sizeof(float);
+    void *uf = nullptr;
+    HIP_CHECK(hipMalloc(&uf, bytes));
+    derived_.push_back(uf);
+    derived_bytes_ += bytes;
+    winograd_fused_weights(ctx_, u, co, ci, static_cast<float *>(uf));
+    return static_cast<const float *>(uf);
+}
+
 DParam WeightStore::get(const std::string &name, int64_t numel, bool gemm) const {
     auto it = m_.find(name);
     if (it == m_.end()) fail(kWeights, "missing tensor " + name);

@@ -44,6 +44,8 @@ class WeightStore {
     // Winograd kernel U = G g G^T [16][co][ci] (f32) of a 3x3 conv weight
     // [co][3][3][ci], built on the device once and owned by the store.
     const float *winograd_kernel(const DParam &w, int co, int ci) const;
+    // u (from winograd_kernel) in the one-kernel Winograd path's order.
+    const float *winograd_kernel_fused(const float *u, int co, int ci) const;
     size_t bytes() const { return bytes_ + derived_bytes_; }
 
   private:

@@ -57,6 +57,7 @@ struct Conv3v {
     bool up = false;
     DParam w;
     const float *u = nullptr;
+    const float *uf = nullptr;  // u in the one-kernel path's order (channel counts it takes)
     const float *b = nullptr;
     void load(const WeightStore &W, const std::string &p, int ci_, int co_, int stride_ = 1,
               const int *pad_ = nullptr, bool up_ = false) {
@@ -67,6 +68,7 @@ struct Conv3v {
         b = W.get(p + ".bias", co, false).f();
         const bool same = stride == 1 && pad[0] == 1 && pad[1] == 1 && pad[2] == 1 && pad[3] == 1;
         if (same && ci % 4 == 0 && co % 4 == 0) u = W.winograd_kernel(w, co, ci);
+        if (u && ci % 32 == 0 && co % 64 == 0) uf = W.winograd_kernel_fused(u, co, ci);
     }
     // res2 (optional) added last: out = (bias + conv) + res2.
     DT fwd(Env &e, const DT &x, const float *res2 = nullptr, float *out_p = nullptr) const {
@@ -74,7 +76,7 @@ struct Conv3v {
         conv3x3_output_hw(x.h, x.w, stride, pad, up, &ho, &wo);
         DT out = out_p ? DT{out_p, x.n, ho, wo, co} : e.pool.tensor(x.n, ho, wo, co);
         if (u)
-            conv3x3_winograd(e.ctx, x.p, x.n, x.h, x.w, x.c, u, kF32, co, b, up, nullptr, out.p, res2);
+            conv3x3_winograd(e.ctx, x.p, x.n, x.h, x.w, x.c, u, kF32, co, b, up, nullptr, out.p, res2, uf);
         else
             conv3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, w.p, w.wt, co, b, stride, pad, up, nullptr, out.p, res2);
         return out;

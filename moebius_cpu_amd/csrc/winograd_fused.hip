@@ -10,16 +10,22 @@
 // wino_input_kernel) into the V stage [plane][tile][channel]; wave w (of 8,
 // two per SIMD) then multiplies planes 2w and 2w + 1 on v_mfma_f32_32x32x2f32
 // (tiles x 64 channels, two 32x32 blocks per plane), reading V from LDS and
-// U [plane][co][ci] from global memory (L2 resident). The next chunk's patch
-// loads are in flight during the current chunk's last three quarters of
-// products. At the end the 16 planes go through LDS and each thread applies
+// U from global memory (L2 resident), in the fused order [16][ci / 8][co][8]:
+// the 32 channels of one block at one K sub-step are 1 KB of consecutive
+// bytes, so each U load of a wave reads whole cache lines (from [16][co][ci]
+// a load touches 32 lines for 32 bytes each). The next chunk's patch loads
+// are in flight during the current chunk's last three quarters of products.
+// A producer's four channels are adjacent to its neighbours' (the eight quads
+// of a tile on eight consecutive lanes), so a patch load reads 128-byte runs. At the end the 16 planes go through LDS and each thread applies
 // the output transform (winograd.rs:329-352, as wino_output_kernel) to one
 // tile and four channels, adding bias and the optional residual.
 //
-// Timed per workgroup at 512x512x128 (in-kernel clock): first chunk ready
-// 4.0 us, chunks 6.5-6.8 us (4.3 us for the last, which transforms nothing),
-// output transform 2.0 us; 16 rounds of 256 workgroups: 505 us against 730
-// us for transforms + batched GEMM.
+// At 512x512x128 -> 128: 372 us against 730 us for transforms + batched
+// GEMM (with U in [16][co][ci] order and a tile per lane, 495 us; the same
+// kernel with its MFMAs removed took 490 us, so the operand loads bound it).
+// The products alone run at 91% of the f32 MFMA peak.
+#include <algorithm>
+
 #include "common.hpp"
 #include "dmath.hpp"
 #include "kernels.hpp"
@@ -84,7 +90,7 @@ __global__ __launch_bounds__(kFThreads, 2) void wino_fused_kernel(const float *_
 
     // Producer role: tile vt of the block, channel quad vq of the chunk.
     const bool producer = tid < kFT * (kFK / 4);
-    const int vt = tid & (kFT - 1), vq = (tid >> 5) & (kFK / 4 - 1);
+    const int vq = tid & (kFK / 4 - 1), vt = (tid >> 3) & (kFT - 1);
     const int64_t tv = t0 + vt;
     const int per_item = g.th * g.tw;
     const int vb = int(tv / per_item), vrem = int(tv - int64_t(vb) * per_item);
@@ -152,12 +158,13 @@ __global__ __launch_bounds__(kFThreads, 2) void wino_fused_kernel(const float *_
 #pragma unroll
             for (int v = 0; v < 16; ++v) acc[p][j][v] = 0.f;
     const int row = lane & 31, kq = 4 * (lane >> 5);
-    // U [16][co][ci]: plane 4w + p, channel co0 + 32 j + row, K offset kq
+    // U [16][ci / 8][co][8]: plane kFPlanes w + p, channel co0 + 32 j + row,
+    // K offset kq within the sub-step's 8; sub-step k8 adds k8 * co * 8 floats.
     int uoff[kFPlanes][2];
 #pragma unroll
     for (int p = 0; p < kFPlanes; ++p)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) uoff[p][j] = (((kFPlanes * wave + p) * co + co0 + 32 * j + row) * ci + kq) * 4;
+        for (int j = 0; j < 2; ++j) uoff[p][j] = ((((kFPlanes * wave + p) * (ci / 8)) * co + co0 + 32 * j + row) * 8 + kq) * 4;
     // Loads are waited for in issue order, so the order is chosen to never
     // wait on more than the next operands: U for sub-step 1 is issued with
     // sub-step 0, U for sub-steps 2 and 3 with sub-step 1 and after them the
@@ -170,7 +177,7 @@ __global__ __launch_bounds__(kFThreads, 2) void wino_fused_kernel(const float *_
 #pragma unroll
         for (int p = 0; p < kFPlanes; ++p)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) dst[p][j] = ld4(ur, uoff[p][j] + kc * kFK * 4 + s * 32);
+            for (int j = 0; j < 2; ++j) dst[p][j] = ld4(ur, uoff[p][j] + (kc * (kFK / 8) + s) * co * 32);
     };
     auto mfma_step = [&](const float *vs, int s, const floatx4 (&b)[kFPlanes][2]) {
         floatx4 a[kFPlanes];
@@ -258,6 +265,19 @@ __global__ __launch_bounds__(kFThreads, 2) void wino_fused_kernel(const float *_
     }
 }
 
+// u [16][co][ci] -> uf [16][ci / 8][co][8], one float4 per thread.
+__global__ void wino_u_fused_kernel(const float *__restrict__ u, int co, int ci, float *__restrict__ uf) {
+    const int64_t total4 = int64_t(16) * co * ci / 4;
+    for (int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; e < total4; e += int64_t(gridDim.x) * blockDim.x) {
+        const int64_t f = e * 4, plane_sz = int64_t(co) * ci;
+        const int64_t plane = f / plane_sz, rem = f - plane * plane_sz;
+        const int k8 = int(rem / (int64_t(co) * 8));
+        const int r2 = int(rem - int64_t(k8) * co * 8), c = r2 >> 3, kk = r2 & 7;
+        *reinterpret_cast<floatx4 *>(uf + f) =
+            *reinterpret_cast<const floatx4 *>(u + (plane * co + c) * ci + k8 * 8 + kk);
+    }
+}
+
 template <int UP, bool PRO>
 void launch_fused(Context &ctx, int nwork, const float *x, uint32_t xb, const FGeo &g, int ci, const float *u,
                   uint32_t ub, int co, const Affine *pro, const float *bias, const float *res2, float *out) {
@@ -270,16 +290,27 @@ void launch_fused(Context &ctx, int nwork, const float *x, uint32_t xb, const FG
 
 }  // namespace
 
-bool conv3x3_winograd_fused(Context &ctx, const float *x, int n, int h, int w, int c_in, const float *u, int c_out,
-                            const float *bias, bool upsample2x, const Affine *prologue, float *out,
-                            const float *residual2) {
+void winograd_fused_weights(Context &ctx, const float *u, int c_out, int c_in, float *uf) {
+    MH_REQUIRE(c_in % 8 == 0 && aligned16(u) && aligned16(uf), "Winograd fused weights: c_in % 8, 16-byte aligned");
+    const int64_t total4 = int64_t(16) * c_out * c_in / 4;
+    if (total4 == 0) return;
+    const unsigned blocks = unsigned(std::min<int64_t>(ceil_div(total4, 256), 65536));
+    wino_u_fused_kernel<<<blocks, 256, 0, ctx.stream>>>(u, c_out, c_in, uf);
+    MH_LAUNCH_CHECK();
+}
+
+bool conv3x3_winograd_fused(Context &ctx, const float *x, int n, int h, int w, int c_in, const float *u,
+                            const float *uf, int c_out, const float *bias, bool upsample2x, const Affine *prologue,
+                            float *out, const float *residual2) {
     if (ctx.tune.wino_fused == 0 || c_in % kFK || c_out % kFC) return false;
-    // Where it is faster (A/B per conv on MI355X): 512x512x128 -> 128 720 -> 540 us,
-    // 256x256x256 -> 256 about equal (528 / 524 us). Above 256 channels the
-    // batched plane GEMM reaches 83% of f32 MFMA peak, this kernel about 45%,
-    // and the V / M traffic it saves is smaller than that loss (128x128x512 ->
-    // 512: 413 -> 504 us): those keep three kernels.
-    if (ctx.tune.wino_fused < 0 && (c_in > 256 || c_out > 256)) return false;
+    // Where it is faster (A/B per conv on MI355X, three kernels -> this one):
+    // 512x512x128 746 -> 419 us, 256x256x256 552 -> 401, the same upsampled
+    // 1824 -> 1352, 128x128x512 437 -> 402, the same upsampled 1471 -> 1335;
+    // slower on small maps, where the batched plane GEMM fills the chip at 83%
+    // of f32 MFMA peak and the V / M traffic is small: 64x64x512 100 -> 117 us,
+    // the UNet's 2x64x64x320 92 -> 124, 2x32x32x640 upsampled 281 -> 348. So:
+    // at least 4096 tiles, up to the measured 512 channels.
+    if (ctx.tune.wino_fused < 0 && (c_in > 512 || c_out > 512)) return false;
     if (!aligned16(x) || !aligned16(u) || !aligned16(out) || !aligned16(bias) || !aligned16(residual2)) return false;
     if (prologue && (!aligned16(prologue->scale) || !aligned16(prologue->shift))) return false;
     const int64_t x_bytes = int64_t(n) * h * w * c_in * 4, u_bytes = int64_t(16) * c_out * c_in * 4;
@@ -289,12 +320,20 @@ bool conv3x3_winograd_fused(Context &ctx, const float *x, int n, int h, int w, i
     g.h = h, g.w = w, g.hi = h << up, g.wi = w << up;
     g.th = (g.hi + 1) / 2, g.tw = (g.wi + 1) / 2;
     g.tiles = int64_t(n) * g.th * g.tw;
-    if (ctx.tune.wino_fused < 0 && g.tiles < 16384) return false;
+    if (ctx.tune.wino_fused < 0 && g.tiles < 4096) return false;
     if (g.tiles == 0) return true;
     const int64_t blocks = ceil_div(g.tiles, kFT) * (c_out / kFC);
     if (blocks >= (int64_t(1) << 30)) return false;
     const int nwork = int(blocks);
     const uint32_t xb = uint32_t(x_bytes), ub = uint32_t(u_bytes);
+    if (!uf) {  // no precomputed fused-order copy: make one in the workspace
+        float *tmp = static_cast<float *>(ctx.ws.get(size_t(u_bytes), ctx.stream));
+        winograd_fused_weights(ctx, u, c_out, c_in, tmp);
+        uf = tmp;
+    } else if (!aligned16(uf)) {
+        return false;
+    }
+    u = uf;
     if (up) {
         if (prologue) launch_fused<1, true>(ctx, nwork, x, xb, g, c_in, u, ub, c_out, prologue, bias, residual2, out);
         else launch_fused<1, false>(ctx, nwork, x, xb, g, c_in, u, ub, c_out, prologue, bias, residual2, out);

@@ -75,39 +75,72 @@ __global__ __launch_bounds__(kFThreads, 2) void wino_fused_kernel(const float *_
                                                             int nco_blocks, int nwork) {
     __shared__ float lds[kLds];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // Work order: channel block outer, tile block inner; workgroup i runs on
-    // XCD i % 8 (round-robin dispatch), and each XCD takes one contiguous
-    // eighth of the order, so it works through few channel blocks and their
-    // U panels stay in its L2. The grid is padded to a multiple of 8; the
-    // padding workgroups have no work.
+    // Work items (channel block, tile block), channel block outer. Workgroup i
+    // runs on XCD i % 8 (round-robin dispatch); each XCD takes one contiguous
+    // eighth of the items, so it works through few channel blocks and their U
+    // panels stay in its L2, and its workgroups take every (grid / 8)-th item
+    // of that range. The grid holds one workgroup per CU, and a workgroup
+    // issues its next item's first patch and U loads before the current
+    // item's last products and output transform, which hide their latency.
     const int ntb = nwork / nco_blocks;
-    const int per_xcd = int(gridDim.x) / 8;
-    const int work = (int(blockIdx.x) % 8) * per_xcd + int(blockIdx.x) / 8;
-    if (work >= nwork) return;
-    const int64_t t0 = int64_t(work % ntb) * kFT;
-    const int co0 = (work / ntb) * kFC;
+    const int per_xcd = (nwork + 7) / 8;
+    const int slots = int(gridDim.x) / 8;
+    const int item_end = min(nwork, (int(blockIdx.x) % 8 + 1) * per_xcd);
+    int item = (int(blockIdx.x) % 8) * per_xcd + int(blockIdx.x) / 8;
+    if (item >= item_end) return;
     const __amdgpu_buffer_rsrc_t xr = rsrc(x, x_bytes), ur = rsrc(u, u_bytes);
+    const int per_item = g.th * g.tw;
+    const int n_items = int(g.tiles / per_item);
 
     // Producer role: tile vt of the block, channel quad vq of the chunk.
     const bool producer = tid < kFT * (kFK / 4);
     const int vq = tid & (kFK / 4 - 1), vt = (tid >> 3) & (kFT - 1);
-    const int64_t tv = t0 + vt;
-    const int per_item = g.th * g.tw;
-    const int vb = int(tv / per_item), vrem = int(tv - int64_t(vb) * per_item);
-    const int vty = vrem / g.tw, vtx = vrem - vty * g.tw;
-    int poff[16];  // byte offset of each patch pixel's channel 0, or kOob outside the image
+    // Consumer role: wave w, planes kFPlanes w .. + kFPlanes - 1, two 32x32 blocks of 64 channels.
+    // Lane l reads a float4 along K of row l % 32 at K offset 4 (l / 32); MFMA t
+    // takes its component t, so both operands pair k = 8 s + 4 (l / 32) + t.
+    const int row = lane & 31, kq = 4 * (lane >> 5);
+    // Per item: the block's first tile and channel; the producer's patch
+    // origin (byte offset of source pixel (sy - 1, sx - 1), channel 4 vq; the
+    // patch's rows and columns sit at -1, 0, 1, 2 from (sy, sx), or -1, 0, 0, 1
+    // when upsampling) with one bit per pixel inside the image, and its batch
+    // item; the consumer's U offsets in [16][ci / 8][co][8] (plane
+    // kFPlanes w + p, channel co0 + 32 j + row, K offset kq within the
+    // sub-step's 8; sub-step k8 adds k8 * co * 8 floats).
+    int64_t t0 = 0;
+    int co0 = 0, vb = 0, porg = 0;
     unsigned valid = 0;
+    int uoff[kFPlanes][2];
+    const int prow = g.w * ci * 4, pcol = ci * 4;  // bytes per source row, per pixel
+    constexpr int kStep[4] = {0, 1, 2 - UP, 3 - UP};  // patch row / column k -> source offset + 1
+    auto setup = [&](int it) {
+        t0 = int64_t(it % ntb) * kFT;
+        co0 = (it / ntb) * kFC;
+        const int64_t tv = t0 + vt;
+        const int b = int(tv / per_item), rem = int(tv - int64_t(b) * per_item);
+        const int ty = rem / g.tw, tx = rem - ty * g.tw;
+        vb = min(b, n_items - 1);  // a tile past the end reads nothing, but keeps its prologue loads in range
+        const int sy = (2 * ty) >> UP, sx = (2 * tx) >> UP;
+        porg = tv < g.tiles ? (((b * g.h + sy - 1) * g.w + sx - 1) * ci + 4 * vq) * 4 : 0;
+        valid = 0;
 #pragma unroll
-    for (int kk = 0; kk < 16; ++kk) {
-        const int iy = 2 * vty + (kk >> 2) - 1, ix = 2 * vtx + (kk & 3) - 1;
-        const bool in = producer && tv < g.tiles && iy >= 0 && iy < g.hi && ix >= 0 && ix < g.wi;
-        poff[kk] = in ? (((vb * g.h + (iy >> UP)) * g.w + (ix >> UP)) * ci + 4 * vq) * 4 : kOob;
-        valid |= in ? (1u << kk) : 0u;
-    }
+        for (int kk = 0; kk < 16; ++kk) {
+            const int iy = 2 * ty + (kk >> 2) - 1, ix = 2 * tx + (kk & 3) - 1;
+            const bool in = producer && tv < g.tiles && iy >= 0 && iy < g.hi && ix >= 0 && ix < g.wi;
+            valid |= in ? (1u << kk) : 0u;
+        }
+#pragma unroll
+        for (int p = 0; p < kFPlanes; ++p)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                uoff[p][j] = ((((kFPlanes * wave + p) * (ci / 8)) * co + co0 + 32 * j + row) * 8 + kq) * 4;
+    };
     floatx4 d[16];
     auto produce = [&](int kc) {
 #pragma unroll
-        for (int kk = 0; kk < 16; ++kk) d[kk] = ld4(xr, poff[kk] == kOob ? kOob : poff[kk] + kc * kFK * 4);
+        for (int kk = 0; kk < 16; ++kk) {
+            const int off = porg + kStep[kk >> 2] * prow + kStep[kk & 3] * pcol + kc * kFK * 4;
+            d[kk] = ld4(xr, (valid >> kk) & 1u ? off : kOob);
+        }
     };
     auto transform_store = [&](int kc, int stage) {
         if (!producer) return;
@@ -147,24 +180,7 @@ __global__ __launch_bounds__(kFThreads, 2) void wino_fused_kernel(const float *_
         }
     };
 
-    // Consumer role: wave w, planes kFPlanes w .. + kFPlanes - 1, two 32x32 blocks of 64 channels.
-    // Lane l reads a float4 along K of row l % 32 at K offset 4 (l / 32); MFMA t
-    // takes its component t, so both operands pair k = 8 s + 4 (l / 32) + t.
     floatx16 acc[kFPlanes][2];
-#pragma unroll
-    for (int p = 0; p < kFPlanes; ++p)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[p][j][v] = 0.f;
-    const int row = lane & 31, kq = 4 * (lane >> 5);
-    // U [16][ci / 8][co][8]: plane kFPlanes w + p, channel co0 + 32 j + row,
-    // K offset kq within the sub-step's 8; sub-step k8 adds k8 * co * 8 floats.
-    int uoff[kFPlanes][2];
-#pragma unroll
-    for (int p = 0; p < kFPlanes; ++p)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) uoff[p][j] = ((((kFPlanes * wave + p) * (ci / 8)) * co + co0 + 32 * j + row) * 8 + kq) * 4;
     // Loads are waited for in issue order, so the order is chosen to never
     // wait on more than the next operands: U for sub-step 1 is issued with
     // sub-step 0, U for sub-steps 2 and 3 with sub-step 1 and after them the
@@ -193,27 +209,46 @@ __global__ __launch_bounds__(kFThreads, 2) void wino_fused_kernel(const float *_
                     acc[p][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[p][t], b[p][j][t], acc[p][j], 0, 0, 0);
     };
     const int nk = ci / kFK;
+    setup(item);
     produce(0);
     load_b(b0, 0, 0);
-    transform_store(0, 0);
-    __syncthreads();
-    for (int kc = 0; kc < nk; ++kc) {
-        const bool more = kc + 1 < nk;
-        const float *vs = lds + (kc & 1) * kVStage + row * kVS + kq;
-        load_b(b1, kc, 1);
-        mfma_step(vs, 0, b0);
-        load_b(b2, kc, 2);
-        load_b(b3, kc, 3);
-        if (more) produce(kc + 1);
-        mfma_step(vs, 1, b1);
-        mfma_step(vs, 2, b2);
-        mfma_step(vs, 3, b3);
-        if (more) {
-            load_b(b0, kc + 1, 0);
-            transform_store(kc + 1, (kc + 1) & 1);
-        }
+    for (;;) {
+        transform_store(0, 0);
+#pragma unroll
+        for (int p = 0; p < kFPlanes; ++p)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[p][j][v] = 0.f;
         __syncthreads();
-    }
+        const int next = item + slots;
+        const bool has_next = next < item_end;
+        const int64_t et0 = t0;
+        const int eco0 = co0;
+        for (int kc = 0; kc < nk; ++kc) {
+            const bool more = kc + 1 < nk;
+            const float *vs = lds + (kc & 1) * kVStage + row * kVS + kq;
+            load_b(b1, kc, 1);
+            mfma_step(vs, 0, b0);
+            load_b(b2, kc, 2);
+            load_b(b3, kc, 3);
+            if (more) {
+                produce(kc + 1);
+            } else if (has_next) {  // this item's U loads are all issued: switch to the next
+                setup(next);
+                produce(0);
+            }
+            mfma_step(vs, 1, b1);
+            mfma_step(vs, 2, b2);
+            mfma_step(vs, 3, b3);
+            if (more) {
+                load_b(b0, kc + 1, 0);
+                transform_store(kc + 1, (kc + 1) & 1);
+            } else if (has_next) {
+                load_b(b0, 0, 0);
+            }
+            __syncthreads();
+        }
 
     // M [16][tile][channel] through LDS: register v of lane l holds row
     // 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32 of its block.
@@ -231,7 +266,7 @@ __global__ __launch_bounds__(kFThreads, 2) void wino_fused_kernel(const float *_
     for (int r = 0; r < (kFT * kFC / 4) / kFThreads; ++r) {
         const int item = tid + kFThreads * r;
         const int tl = item / (kFC / 4), q = item - tl * (kFC / 4);
-        const int64_t t = t0 + tl;
+        const int64_t t = et0 + tl;
         if (t >= g.tiles) continue;
         const int b = int(t / per_item), rem = int(t - int64_t(b) * per_item);
         const int ty = rem / g.tw, tx = rem - ty * g.tw;
@@ -246,7 +281,7 @@ __global__ __launch_bounds__(kFThreads, 2) void wino_fused_kernel(const float *_
             u0[rr] = add4(add4(a, bb), cc);
             u1[rr] = sub4(sub4(bb, cc), dd);
         }
-        const int c = co0 + 4 * q;
+        const int c = eco0 + 4 * q;
         const floatx4 bv = bias ? *reinterpret_cast<const floatx4 *>(bias + c) : floatx4{0.f, 0.f, 0.f, 0.f};
         floatx4 y[4];
         y[0] = add4(add4(add4(u0[0], u0[1]), u0[2]), bv);
@@ -262,6 +297,10 @@ __global__ __launch_bounds__(kFThreads, 2) void wino_fused_kernel(const float *_
             if (res2) rv = add4(rv, *reinterpret_cast<const floatx4 *>(res2 + o));
             *reinterpret_cast<floatx4 *>(out + o) = rv;
         }
+    }
+        if (!has_next) break;
+        __syncthreads();  // the output transform's reads of M are done before V stage 0 is written
+        item = next;
     }
 }
 
@@ -281,8 +320,10 @@ __global__ void wino_u_fused_kernel(const float *__restrict__ u, int co, int ci,
 template <int UP, bool PRO>
 void launch_fused(Context &ctx, int nwork, const float *x, uint32_t xb, const FGeo &g, int ci, const float *u,
                   uint32_t ub, int co, const Affine *pro, const float *bias, const float *res2, float *out) {
-    // padded to a multiple of 8 workgroups (see the work order in the kernel)
-    const unsigned grid = unsigned(ceil_div(nwork, 8) * 8);
+    // one workgroup per CU (its LDS holds one), a multiple of 8 (see the work
+    // order in the kernel), no more than the items of one XCD's share need
+    const int64_t per_xcd = ceil_div(nwork, 8);
+    const unsigned grid = unsigned(8 * std::max<int64_t>(1, std::min<int64_t>(ctx.cu_count / 8, per_xcd)));
     wino_fused_kernel<UP, PRO><<<grid, kFThreads, 0, ctx.stream>>>(x, xb, g, ci, u, ub, co, pro ? pro->scale : nullptr,
                                                              pro ? pro->shift : nullptr, pro && pro->silu ? 1 : 0,
                                                              bias, res2, out, co / kFC, nwork);

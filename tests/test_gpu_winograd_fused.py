@@ -5,7 +5,7 @@ winograd.rs:48-120) at the f32 bar and against the three-kernel path
 (transforms + batched GEMM; tuning "wino_fused" 0): odd sizes with partial
 tiles, batch 2, the nearest-2x upsample, the GroupNorm prologue, the VAE's
 and the UNet's channel counts, and shapes the kernel does not take (they fall
-back). The transforms restate the reference's operation order in both paths;
+back), and maps with several work items per workgroup. The transforms restate the reference's operation order in both paths;
 only the plane products' summation order differs."""
 from __future__ import annotations
 
@@ -42,7 +42,9 @@ def conv(ctx, x, w, b, up=False, prologue=None, fused=True):
 
 SHAPES = [(2, 9, 11, 64, 64, False), (1, 7, 5, 32, 64, True), (1, 64, 64, 128, 128, False),
           (1, 32, 32, 512, 512, False), (1, 24, 40, 256, 128, True), (2, 16, 16, 640, 640, True),
-          (1, 8, 8, 1280, 1280, True), (1, 9, 7, 48, 64, False), (1, 9, 7, 64, 40, True)]
+          (1, 8, 8, 1280, 1280, True), (1, 9, 7, 48, 64, False), (1, 9, 7, 64, 40, True),
+          # several work items per workgroup (one workgroup per CU), partial last tile block
+          (1, 200, 180, 32, 128, False), (1, 130, 250, 64, 64, True)]
 
 
 @pytest.mark.parametrize("n,h,w,ci,co,up", SHAPES)

@@ -213,6 +213,8 @@ void conv3x3(Context &ctx, const float *x, int n, int h, int w, int c_in, const 
     const int64_t m = int64_t(n) * ho * wo;
     MH_REQUIRE(m < (int64_t(1) << 31), "Conv3x3: too many output pixels");
     if (m == 0) return;
+    const bool same = stride == 1 && pad[0] == 1 && pad[1] == 1 && pad[2] == 1 && pad[3] == 1 && !upsample2x;
+    if (same && conv3x3_small_co(ctx, x, n, h, w, c_in, weight, wt, c_out, bias, prologue, out, residual2)) return;
     GemmArgs p{};
     p.a = x;
     p.M = int(m);

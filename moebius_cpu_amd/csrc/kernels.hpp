@@ -130,6 +130,11 @@ void winograd_output_transform(Context &ctx, const float *m, int n, int h, int w
                                const float *bias, const float *residual2, float *out);
 // u [16][c_out][c_in] -> uf [16][c_in / 8][c_out][8], the fused kernel's operand order.
 void winograd_fused_weights(Context &ctx, const float *u, int c_out, int c_in, float *uf);
+// Direct 3x3 conv, stride 1 / pad 1, for c_out <= 8 on maps of at least 65536
+// pixels (conv_small.hip), with the optional GN(+SiLU) prologue; false (nothing
+// launched) where it does not apply.
+bool conv3x3_small_co(Context &ctx, const float *x, int n, int h, int w, int c_in, const void *weight, WeightType wt,
+                      int c_out, const float *bias, const Affine *prologue, float *out, const float *residual2);
 // The whole conv in one kernel (winograd_fused.hip) for f32 u, c_in % 32 == 0,
 // c_out % 64 == 0 and operands under 2 GiB; false (nothing launched) otherwise.
 // uf: u in the fused order, or NULL (then made in the workspace for this call).

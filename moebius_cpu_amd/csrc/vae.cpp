@@ -44,6 +44,12 @@ struct GNv {  // GroupNorm, eps 1e-6 (src/engine/norm.rs:22-105)
         group_norm_forward(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, VAE_EPS, g, b, nullptr, silu, out.p);
         return out;
     }
+    // Statistics only: [scale | shift], each [n * c], for a consumer that applies them.
+    float *affine(Env &e, const DT &x) const {
+        float *ss = e.pool.floats(int64_t(2) * x.n * x.c);
+        group_norm_affine(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, VAE_EPS, g, b, nullptr, ss, ss + int64_t(x.n) * x.c);
+        return ss;
+    }
 };
 
 // Conv3x3 (src/engine/conv.rs:60-102). Stride-1 / pad-1 convs run as
@@ -85,7 +91,19 @@ struct Conv3v {
     // (Applying GN + SiLU inside the conv's gather, as the reference's
     // forward_prologue does, re-evaluates SiLU for every tap and column tile:
     // on the matrix cores that costs more than one extra pass over the map.)
+    // The exception is the image conv (c_out <= 8, no Winograd kernel): its
+    // direct kernel stages each input value once per tile, so it applies
+    // GN + SiLU itself and the normalised map is never written.
     DT fwd_gn(Env &e, const GNv &gn, const DT &x, const float *res2 = nullptr, float *out_p = nullptr) const {
+        const bool same = stride == 1 && pad[0] == 1 && pad[1] == 1 && pad[2] == 1 && pad[3] == 1 && !up;
+        if (co <= 8 && !u && same) {
+            float *ss = gn.affine(e, x);
+            const Affine a{ss, ss + int64_t(x.n) * x.c, true};
+            DT out = out_p ? DT{out_p, x.n, x.h, x.w, co} : e.pool.tensor(x.n, x.h, x.w, co);
+            conv3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, w.p, w.wt, co, b, stride, pad, up, &a, out.p, res2);
+            e.pool.recycle(ss);
+            return out;
+        }
         DT a = gn.fwd(e, x, true);
         DT out = fwd(e, a, res2, out_p);
         e.pool.recycle(a);

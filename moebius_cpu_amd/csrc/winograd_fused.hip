@@ -4,26 +4,30 @@
 // of tiles x channels each) never reach HBM. The separate path writes and
 // reads both: about 4.2 GB per 512x512x128 conv of the VAE decoder.
 //
-// Workgroup: 512 threads, one per CU (LDS: two V stages of 72 KB). Per chunk
-// of 32 input channels each of the first 256 threads transforms one tile's
-// 4x4 patch for four channels (the reference's operation order, as
-// wino_input_kernel) into the V stage [plane][tile][channel]; wave w (of 8,
-// two per SIMD) then multiplies planes 2w and 2w + 1 on v_mfma_f32_32x32x2f32
-// (tiles x 64 channels, two 32x32 blocks per plane), reading V from LDS and
-// U from global memory (L2 resident), in the fused order [16][ci / 8][co][8]:
-// the 32 channels of one block at one K sub-step are 1 KB of consecutive
-// bytes, so each U load of a wave reads whole cache lines (from [16][co][ci]
-// a load touches 32 lines for 32 bytes each). The next chunk's patch loads
-// are in flight during the current chunk's last three quarters of products.
-// A producer's four channels are adjacent to its neighbours' (the eight quads
-// of a tile on eight consecutive lanes), so a patch load reads 128-byte runs. At the end the 16 planes go through LDS and each thread applies
-// the output transform (winograd.rs:329-352, as wino_output_kernel) to one
-// tile and four channels, adding bias and the optional residual.
+// Workgroup: 512 threads, one per CU (LDS: two V stages of 72 KB), walking
+// a share of the (channel block, tile block) items. Per chunk of 32 input
+// channels every thread transforms one tile's 4x4 patch for two channels (the
+// reference's operation order, as wino_input_kernel) into the V stage
+// [plane][tile][channel]; the 16 channel pairs of a tile sit on adjacent
+// lanes, so a patch load reads 128-byte runs. Wave w (of 8, two per SIMD)
+// multiplies planes 2w and 2w + 1 on v_mfma_f32_32x32x2f32 (tiles x 64
+// channels, two 32x32 blocks per plane), reading V from LDS and U from global
+// memory (L2 resident) in the fused order [16][ci / 8][co][8]: the 32
+// channels of one block at one K sub-step are 1 KB of consecutive bytes, so
+// each U load of a wave reads whole cache lines (from [16][co][ci] a load
+// touches 32 lines for 32 bytes each). The next chunk's patch loads are in
+// flight during the current chunk's last three quarters of products. At the
+// end the 16 planes go through LDS and each thread applies the output
+// transform (winograd.rs:329-352, as wino_output_kernel) to one tile and four
+// channels, adding bias and the optional residual.
 //
-// At 512x512x128 -> 128: 372 us against 730 us for transforms + batched
-// GEMM (with U in [16][co][ci] order and a tile per lane, 495 us; the same
-// kernel with its MFMAs removed took 490 us, so the operand loads bound it).
-// The products alone run at 91% of the f32 MFMA peak.
+// At 512x512x128 -> 128 (A/B on MI355X): 730 us for transforms + batched
+// GEMM; this kernel with U in [16][co][ci] order and a tile's channels on
+// lanes 32 apart, 495 us (with its MFMAs removed it still took 490 us: the
+// operand loads bound it); with the layouts above 372 us; one workgroup per
+// CU with the next item's loads issued early, 361 us; every thread a
+// producer, 358 us (256x256x256: 347 -> 334, upsampled 128x128x512:
+// 1327 -> 1286). The products alone run at 91% of the f32 MFMA peak.
 #include <algorithm>
 
 #include "common.hpp"
@@ -35,6 +39,7 @@ namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx2 __attribute__((ext_vector_type(2)));
 
 constexpr int kFT = 32;        // tiles per workgroup
 constexpr int kFC = 64;        // output channels per workgroup
@@ -57,6 +62,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_
 
 __device__ __forceinline__ floatx4 ld4(__amdgpu_buffer_rsrc_t r, int off) {
     return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+__device__ __forceinline__ floatx2 ld2(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(floatx2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
 }
 
 __device__ __forceinline__ floatx4 sub4(floatx4 a, floatx4 b) { return floatx4{a[0] - b[0], a[1] - b[1], a[2] - b[2], a[3] - b[3]}; }
@@ -92,9 +101,10 @@ __global__ __launch_bounds__(kFThreads, 2) void wino_fused_kernel(const float *_
     const int per_item = g.th * g.tw;
     const int n_items = int(g.tiles / per_item);
 
-    // Producer role: tile vt of the block, channel quad vq of the chunk.
-    const bool producer = tid < kFT * (kFK / 4);
-    const int vq = tid & (kFK / 4 - 1), vt = (tid >> 3) & (kFT - 1);
+    // Producer role (every thread, so the transform's work is spread over
+    // both waves of each SIMD): tile vt of the block, channel pair vq of the
+    // chunk; the 16 pairs of a tile sit on 16 adjacent lanes (128-byte runs).
+    const int vq = tid & (kFK / 2 - 1), vt = (tid >> 4) & (kFT - 1);
     // Consumer role: wave w, planes kFPlanes w .. + kFPlanes - 1, two 32x32 blocks of 64 channels.
     // Lane l reads a float4 along K of row l % 32 at K offset 4 (l / 32); MFMA t
     // takes its component t, so both operands pair k = 8 s + 4 (l / 32) + t.
@@ -120,12 +130,12 @@ __global__ __launch_bounds__(kFThreads, 2) void wino_fused_kernel(const float *_
         const int ty = rem / g.tw, tx = rem - ty * g.tw;
         vb = min(b, n_items - 1);  // a tile past the end reads nothing, but keeps its prologue loads in range
         const int sy = (2 * ty) >> UP, sx = (2 * tx) >> UP;
-        porg = tv < g.tiles ? (((b * g.h + sy - 1) * g.w + sx - 1) * ci + 4 * vq) * 4 : 0;
+        porg = tv < g.tiles ? (((b * g.h + sy - 1) * g.w + sx - 1) * ci + 2 * vq) * 4 : 0;
         valid = 0;
 #pragma unroll
         for (int kk = 0; kk < 16; ++kk) {
             const int iy = 2 * ty + (kk >> 2) - 1, ix = 2 * tx + (kk & 3) - 1;
-            const bool in = producer && tv < g.tiles && iy >= 0 && iy < g.hi && ix >= 0 && ix < g.wi;
+            const bool in = tv < g.tiles && iy >= 0 && iy < g.hi && ix >= 0 && ix < g.wi;
             valid |= in ? (1u << kk) : 0u;
         }
 #pragma unroll
@@ -134,25 +144,24 @@ __global__ __launch_bounds__(kFThreads, 2) void wino_fused_kernel(const float *_
             for (int j = 0; j < 2; ++j)
                 uoff[p][j] = ((((kFPlanes * wave + p) * (ci / 8)) * co + co0 + 32 * j + row) * 8 + kq) * 4;
     };
-    floatx4 d[16];
+    floatx2 d[16];
     auto produce = [&](int kc) {
 #pragma unroll
         for (int kk = 0; kk < 16; ++kk) {
             const int off = porg + kStep[kk >> 2] * prow + kStep[kk & 3] * pcol + kc * kFK * 4;
-            d[kk] = ld4(xr, (valid >> kk) & 1u ? off : kOob);
+            d[kk] = ld2(xr, (valid >> kk) & 1u ? off : kOob);
         }
     };
     auto transform_store = [&](int kc, int stage) {
-        if (!producer) return;
         if constexpr (PRO) {
-            const int c = kc * kFK + 4 * vq;
-            const floatx4 sc = *reinterpret_cast<const floatx4 *>(psc + int64_t(vb) * ci + c);
-            const floatx4 sh = *reinterpret_cast<const floatx4 *>(psh + int64_t(vb) * ci + c);
+            const int c = kc * kFK + 2 * vq;
+            const floatx2 sc = *reinterpret_cast<const floatx2 *>(psc + int64_t(vb) * ci + c);
+            const floatx2 sh = *reinterpret_cast<const floatx2 *>(psh + int64_t(vb) * ci + c);
 #pragma unroll
             for (int kk = 0; kk < 16; ++kk) {
                 if (valid & (1u << kk)) {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
+                    for (int e = 0; e < 2; ++e) {
                         float y = __builtin_fmaf(d[kk][e], sc[e], sh[e]);
                         if (psilu) y = ref_silu(y);
                         d[kk][e] = y;
@@ -160,23 +169,23 @@ __global__ __launch_bounds__(kFThreads, 2) void wino_fused_kernel(const float *_
                 }
             }
         }
-        floatx4 tt[16];
+        floatx2 tt[16];
 #pragma unroll
         for (int col = 0; col < 4; ++col) {
-            const floatx4 d0 = d[col], d1 = d[4 + col], d2 = d[8 + col], d3 = d[12 + col];
-            tt[col] = sub4(d0, d2);
-            tt[4 + col] = add4(d1, d2);
-            tt[8 + col] = sub4(d2, d1);
-            tt[12 + col] = sub4(d1, d3);
+            const floatx2 d0 = d[col], d1 = d[4 + col], d2 = d[8 + col], d3 = d[12 + col];
+            tt[col] = d0 - d2;
+            tt[4 + col] = d1 + d2;
+            tt[8 + col] = d2 - d1;
+            tt[12 + col] = d1 - d3;
         }
-        float *vs = lds + stage * kVStage + vt * kVS + 4 * vq;
+        float *vs = lds + stage * kVStage + vt * kVS + 2 * vq;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const floatx4 *q = tt + r * 4;
-            *reinterpret_cast<floatx4 *>(vs + (r * 4) * kFT * kVS) = sub4(q[0], q[2]);
-            *reinterpret_cast<floatx4 *>(vs + (r * 4 + 1) * kFT * kVS) = add4(q[1], q[2]);
-            *reinterpret_cast<floatx4 *>(vs + (r * 4 + 2) * kFT * kVS) = sub4(q[2], q[1]);
-            *reinterpret_cast<floatx4 *>(vs + (r * 4 + 3) * kFT * kVS) = sub4(q[1], q[3]);
+            const floatx2 *q = tt + r * 4;
+            *reinterpret_cast<floatx2 *>(vs + (r * 4) * kFT * kVS) = q[0] - q[2];
+            *reinterpret_cast<floatx2 *>(vs + (r * 4 + 1) * kFT * kVS) = q[1] + q[2];
+            *reinterpret_cast<floatx2 *>(vs + (r * 4 + 2) * kFT * kVS) = q[2] - q[1];
+            *reinterpret_cast<floatx2 *>(vs + (r * 4 + 3) * kFT * kVS) = q[1] - q[3];
         }
     };
 

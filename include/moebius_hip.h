@@ -147,6 +147,19 @@ int32_t mh_conv1x1_fused(MhContext *ctx, const float *x, uint32_t n, uint32_t h,
                          const float *residual, const float *residual_scale, const float *residual_shift,
                          uint32_t residual_silu, const float *residual2, float *out);
 
+/* No counterpart in the reference, whose GroupNorm always reads its input
+ * (src/engine/norm.rs:57-105): the GroupNorm statistics a 1x1 conv's epilogue
+ * writes, which this library's UNet hands to the next GroupNorm instead of a
+ * statistics pass; exposed so they can be checked. out as mh_conv1x1_forward;
+ * part [pixels / *rows][c_out][2]: per output tile of *rows pixels, each
+ * channel's sum and sum of squares of the values stored (needs
+ * ceil(pixels / 32) * c_out * 2 floats, 16-byte aligned). *rows is 0 (part not
+ * written) when the chosen tiling cannot write them (split K, rows per item not
+ * a multiple of the tile). */
+int32_t mh_conv1x1_gn_partials(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c_in,
+                               const void *weight, uint32_t weight_dtype, uint32_t c_out, const float *bias,
+                               const float *residual, float *out, float *part, uint32_t *rows);
+
 /* src/engine/conv.rs:77-81 `Conv3x3::output_hw`. pad = [top, left, bottom, right]. */
 int32_t mh_conv3x3_output_hw(uint32_t h, uint32_t w, uint32_t stride, const uint32_t pad[4], uint32_t upsample2x,
                              uint32_t *ho, uint32_t *wo);
@@ -229,6 +242,13 @@ int32_t mh_depthwise3x3_fused(MhContext *ctx, const float *x, uint32_t n, uint32
 int32_t mh_group_norm_affine(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c,
                              uint32_t groups, float eps, const float *gamma, const float *beta, const float *add,
                              float *scale, float *shift);
+
+/* mh_group_norm_affine from the partials of mh_conv1x1_gn_partials (rows from
+ * there; no counterpart in the reference, see above): the same f64 fold per
+ * (item, group) and scale/shift, add folded per partial as GN(x + add). */
+int32_t mh_group_norm_affine_partials(MhContext *ctx, const float *part, uint32_t rows, uint32_t n, uint32_t h,
+                                      uint32_t w, uint32_t c, uint32_t groups, float eps, const float *gamma,
+                                      const float *beta, const float *add, float *scale, float *shift);
 
 /* src/engine/norm.rs:41-53 `GroupNorm::forward`: out = [SiLU](GN(x + add)). */
 int32_t mh_group_norm_forward(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c,

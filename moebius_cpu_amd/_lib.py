@@ -70,6 +70,9 @@ SIGNATURES = {
     "mh_conv1x1_forward": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _u32, _u32, _vp, _vp, _vp]),
     "mh_conv1x1_fused": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _u32, _u32, _vp, _vp, _vp, _vp, _u32, _vp,
                                  _vp]),
+    "mh_conv1x1_gn_partials": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _u32, _u32, _vp, _vp, _vp, _vp, _u32p]),
+    "mh_group_norm_affine_partials": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _f32, _vp, _vp, _vp, _vp,
+                                             _vp]),
     "mh_conv3x3_output_hw": (_i32, [_u32, _u32, _u32, _u32p, _u32, _u32p, _u32p]),
     "mh_conv3x3_forward": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _u32, _u32, _vp, _u32, _u32p, _u32,
                                   _vp, _vp, _u32, _vp]),

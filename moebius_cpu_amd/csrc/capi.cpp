@@ -250,6 +250,28 @@ int32_t mh_conv1x1_forward(MhContext *ctx, const float *x, uint32_t n, uint32_t 
     });
 }
 
+int32_t mh_conv1x1_gn_partials(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c_in,
+                               const void *weight, uint32_t weight_dtype, uint32_t c_out, const float *bias,
+                               const float *residual, float *out, float *part, uint32_t *rows) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(x, "x");
+        need(weight, "weight");
+        need(out, "out");
+        need(part, "part");
+        need(rows, "rows");
+        *rows = 0;
+        MH_REQUIRE(int64_t(h) * w < (int64_t(1) << 31), "conv1x1 partials: map too large");
+        mh::GnPartials gp;
+        gp.part = part;
+        gp.item_rows = int(dim(h, "h")) * int(dim(w, "w"));
+        const int64_t pixels = int64_t(n) * h * w;
+        mh::conv1x1(c, x, pixels, dim(c_in, "c_in"), weight, wtype(weight_dtype), dim(c_out, "c_out"), bias, residual,
+                    out, mh::GemmEpilogue::None, nullptr, nullptr, &gp);
+        *rows = uint32_t(gp.rows);
+    });
+}
+
 int32_t mh_conv1x1_fused(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w, uint32_t c_in,
                          const void *weight, uint32_t weight_dtype, uint32_t c_out, const float *bias,
                          const float *residual, const float *residual_scale, const float *residual_shift,
@@ -428,6 +450,23 @@ int32_t mh_group_norm_affine(MhContext *ctx, const float *x, uint32_t n, uint32_
         need(shift, "shift");
         mh::group_norm_affine(cc, x, dim(n, "n"), dim(h, "h"), dim(w, "w"), dim(c, "c"), dim(groups, "groups"), eps,
                               gamma, beta, add, scale, shift);
+    });
+}
+
+int32_t mh_group_norm_affine_partials(MhContext *ctx, const float *part, uint32_t rows, uint32_t n, uint32_t h,
+                                      uint32_t w, uint32_t c, uint32_t groups, float eps, const float *gamma,
+                                      const float *beta, const float *add, float *scale, float *shift) {
+    return guard([&] {
+        mh::Context &cc = C(ctx);
+        need(part, "part");
+        need(gamma, "gamma");
+        need(beta, "beta");
+        need(scale, "scale");
+        need(shift, "shift");
+        MH_REQUIRE(int64_t(h) * w < (int64_t(1) << 31), "GroupNorm partials: map too large");
+        mh::group_norm_affine_partials(cc, part, int(dim(rows, "rows")), dim(n, "n"),
+                                       int(dim(h, "h")) * int(dim(w, "w")), dim(c, "c"), dim(groups, "groups"), eps,
+                                       gamma, beta, add, scale, shift);
     });
 }
 

@@ -138,14 +138,17 @@ bool conv3x3_small_co(Context &ctx, const float *x, int n, int h, int w, int c_i
 // The whole conv in one kernel (winograd_fused.hip) for f32 u, c_in % 32 == 0,
 // c_out % 64 == 0 and operands under 2 GiB; false (nothing launched) otherwise.
 // uf: u in the fused order, or NULL (then made in the workspace for this call).
+// gn (optional): GroupNorm partials of out, blocks of 128 pixels (gn->rows set,
+// 0 where not written: odd output sizes, tiles per item not a multiple of 32).
 bool conv3x3_winograd_fused(Context &ctx, const float *x, int n, int h, int w, int c_in, const float *u,
                             const float *uf, int c_out, const float *bias, bool upsample2x, const Affine *prologue,
-                            float *out, const float *residual2);
+                            float *out, const float *residual2, GnPartials *gn = nullptr);
 // The whole conv: u from winograd_weight_transform (ut kF32) or an f16 copy of it;
-// uf (optional) its fused-order copy for the one-kernel path.
+// uf (optional) its fused-order copy for the one-kernel path; gn as above (only
+// the one-kernel path writes partials).
 void conv3x3_winograd(Context &ctx, const float *x, int n, int h, int w, int c_in, const void *u, WeightType ut,
                       int c_out, const float *bias, bool upsample2x, const Affine *prologue, float *out,
-                      const float *residual2 = nullptr, const float *uf = nullptr);
+                      const float *residual2 = nullptr, const float *uf = nullptr, GnPartials *gn = nullptr);
 void selftest_mfma_f32(Context &ctx, const float *a_host, const float *b_host, float *d_host);
 
 // ---- lambda layers (lambda.hip), src/unet/lambda.rs

@@ -93,48 +93,80 @@ __global__ __launch_bounds__(256) void gn_partial_kernel(const float *__restrict
 // One block per (group, item): f64 fold of the group's partials, then scale/shift.
 // part_rows > 0: the partials are of x alone, part_rows pixels each, and add
 // is folded in per partial: sum (y + t) = S + r t, sum (y + t)^2 = Q + 2 t S + r t^2.
-__global__ __launch_bounds__(256) void gn_finalize_kernel(const float *__restrict__ part, const float *__restrict__ add,
-                                                          int64_t add_ld, int hw, int c, int nchunks, int groups,
-                                                          int part_rows, float eps,
-                                                          const float *__restrict__ gamma,
-                                                          const float *__restrict__ beta, float *__restrict__ scale,
-                                                          float *__restrict__ shift) {
+// Each thread keeps kFin independent sums with all their loads in flight (the
+// producers' partials run to 16K values per group at 512x512x128), added in a
+// fixed order, so the fold is deterministic.
+constexpr int kFinThreads = 512, kFin = 8;
+__global__ __launch_bounds__(kFinThreads) void gn_finalize_kernel(const float *__restrict__ part,
+                                                                  const float *__restrict__ add, int64_t add_ld,
+                                                                  int hw, int c, int nchunks, int groups,
+                                                                  int part_rows, float eps,
+                                                                  const float *__restrict__ gamma,
+                                                                  const float *__restrict__ beta,
+                                                                  float *__restrict__ scale,
+                                                                  float *__restrict__ shift) {
     const int g = blockIdx.x, b = blockIdx.y;
     const int cg = c / groups;
     const int total = nchunks * cg;
     const float *pb = part + size_t(b) * nchunks * c * 2 + size_t(g) * cg * 2;
-    double ds = 0.0, dq = 0.0;
-    for (int i = threadIdx.x; i < total; i += 256) {
-        const int ch = i / cg, j = i - ch * cg;
-        const float2 e = *reinterpret_cast<const float2 *>(pb + (size_t(ch) * c + j) * 2);
-        if (part_rows > 0 && add) {
-            const double t = double(add[size_t(b) * add_ld + size_t(g) * cg + j]), r = double(part_rows);
-            ds += double(e.x) + r * t;
-            dq += double(e.y) + 2.0 * t * double(e.x) + r * t * t;
-        } else {
-            ds += double(e.x);
-            dq += double(e.y);
+    const bool fold = part_rows > 0 && add;
+    const double r = double(part_rows);
+    double ds[kFin], dq[kFin];
+#pragma unroll
+    for (int u = 0; u < kFin; ++u) ds[u] = dq[u] = 0.0;
+    for (int i0 = threadIdx.x; i0 < total; i0 += kFin * kFinThreads) {
+        float2 e[kFin];
+#pragma unroll
+        for (int u = 0; u < kFin; ++u) {
+            const int i = i0 + u * kFinThreads;
+            const int ch = i / cg, j = i - ch * cg;
+            e[u] = i < total ? *reinterpret_cast<const float2 *>(pb + (size_t(ch) * c + j) * 2) : make_float2(0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < kFin; ++u) {
+            const int i = i0 + u * kFinThreads;
+            if (i >= total) break;
+            if (fold) {
+                const int j = i % cg;
+                const double t = double(add[size_t(b) * add_ld + size_t(g) * cg + j]);
+                ds[u] += double(e[u].x) + r * t;
+                dq[u] += double(e[u].y) + 2.0 * t * double(e[u].x) + r * t * t;
+            } else {
+                ds[u] += double(e[u].x);
+                dq[u] += double(e[u].y);
+            }
         }
     }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        ds += __shfl_xor(ds, off, 64);
-        dq += __shfl_xor(dq, off, 64);
+    for (int u = 1; u < kFin; ++u) {
+        ds[0] += ds[u];
+        dq[0] += dq[u];
     }
-    __shared__ double red[2][4];
+    double s0 = ds[0], q0 = dq[0];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        s0 += __shfl_xor(s0, off, 64);
+        q0 += __shfl_xor(q0, off, 64);
+    }
+    constexpr int kW = kFinThreads / 64;
+    __shared__ double red[2][kW];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (lane == 0) {
-        red[0][wave] = ds;
-        red[1][wave] = dq;
+        red[0][wave] = s0;
+        red[1][wave] = q0;
     }
     __syncthreads();
-    const double sum = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
-    const double sumsq = (red[1][0] + red[1][1]) + (red[1][2] + red[1][3]);
+    double sum = red[0][0], sumsq = red[1][0];
+#pragma unroll
+    for (int w = 1; w < kW; ++w) {
+        sum += red[0][w];
+        sumsq += red[1][w];
+    }
     const double count = double(hw) * double(cg);
     const double mean = sum / count;
     const double var = fmax(sumsq / count - mean * mean, 0.0);
     const double rstd = 1.0 / sqrt(var + double(eps));
-    for (int j = threadIdx.x; j < cg; j += 256) {
+    for (int j = threadIdx.x; j < cg; j += kFinThreads) {
         const int ch = g * cg + j;
         const double sc = rstd * double(gamma[ch]);
         const double pre = add ? double(add[size_t(b) * add_ld + ch]) : 0.0;
@@ -328,7 +360,7 @@ void group_norm_affine_into(Context &ctx, const float *x, int n, int h, int w, i
     gn_partial_kernel<<<dim3(nchunks, nctiles, n), 256, 0, ctx.stream>>>(x, add, add_ld, hw, c, chunk_px, nchunks,
                                                                         part);
     MH_LAUNCH_CHECK();
-    gn_finalize_kernel<<<dim3(groups, n), 256, 0, ctx.stream>>>(part, add, add_ld, hw, c, nchunks, groups, 0, eps,
+    gn_finalize_kernel<<<dim3(groups, n), kFinThreads, 0, ctx.stream>>>(part, add, add_ld, hw, c, nchunks, groups, 0, eps,
                                                                 gamma, beta, scale, shift);
     MH_LAUNCH_CHECK();
 }
@@ -360,7 +392,7 @@ void group_norm_affine_partials(Context &ctx, const float *part, int rows, int n
     MH_REQUIRE(groups > 0 && c % groups == 0, "channels not divisible by groups");
     MH_REQUIRE(n > 0 && hw > 0 && rows > 0 && hw % rows == 0, "GroupNorm partials: tiles must divide the item");
     MH_REQUIRE(aligned16(part), "GroupNorm partials must be 16-byte aligned");
-    gn_finalize_kernel<<<dim3(groups, n), 256, 0, ctx.stream>>>(part, add, add_ld, hw, c, hw / rows, groups, rows,
+    gn_finalize_kernel<<<dim3(groups, n), kFinThreads, 0, ctx.stream>>>(part, add, add_ld, hw, c, hw / rows, groups, rows,
                                                                 eps, gamma, beta, scale, shift);
     MH_LAUNCH_CHECK();
 }

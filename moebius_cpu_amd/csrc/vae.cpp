@@ -31,6 +31,17 @@ struct Env {
     Pool &pool;
 };
 
+// Attaches the GroupNorm partials a producer wrote to its output, or returns the buffer.
+void attach(Env &e, DT &out, const GnPartials &gp) {
+    if (!gp.part) return;
+    if (gp.rows > 0) {
+        out.gn = gp.part;
+        out.gn_rows = gp.rows;
+    } else {
+        e.pool.recycle(gp.part);
+    }
+}
+
 struct GNv {  // GroupNorm, eps 1e-6 (src/engine/norm.rs:22-105)
     int c = 0;
     const float *g = nullptr, *b = nullptr;
@@ -39,15 +50,28 @@ struct GNv {  // GroupNorm, eps 1e-6 (src/engine/norm.rs:22-105)
         g = W.get(p + ".weight", c, false).f();
         b = W.get(p + ".bias", c, false).f();
     }
+    // The statistics come from the producer's partials where it wrote them
+    // (the one-kernel Winograd conv, the 1x1 GEMMs), else from a pass over x.
     DT fwd(Env &e, const DT &x, bool silu = false) const {
         DT out = e.pool.tensor(x.n, x.h, x.w, x.c);
-        group_norm_forward(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, VAE_EPS, g, b, nullptr, silu, out.p);
+        if (x.gn) {
+            float *ss = affine(e, x);
+            apply_affine(e.ctx, x.p, x.n, x.h, x.w, x.c, ss, ss + int64_t(x.n) * x.c, silu, out.p);
+            e.pool.recycle(ss);
+        } else {
+            group_norm_forward(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, VAE_EPS, g, b, nullptr, silu, out.p);
+        }
         return out;
     }
     // Statistics only: [scale | shift], each [n * c], for a consumer that applies them.
     float *affine(Env &e, const DT &x) const {
         float *ss = e.pool.floats(int64_t(2) * x.n * x.c);
-        group_norm_affine(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, VAE_EPS, g, b, nullptr, ss, ss + int64_t(x.n) * x.c);
+        if (x.gn)
+            group_norm_affine_partials(e.ctx, x.gn, x.gn_rows, x.n, x.h * x.w, x.c, GROUPS, VAE_EPS, g, b, nullptr, ss,
+                                       ss + int64_t(x.n) * x.c);
+        else
+            group_norm_affine(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, VAE_EPS, g, b, nullptr, ss,
+                              ss + int64_t(x.n) * x.c);
         return ss;
     }
 };
@@ -81,10 +105,19 @@ struct Conv3v {
         int ho, wo;
         conv3x3_output_hw(x.h, x.w, stride, pad, up, &ho, &wo);
         DT out = out_p ? DT{out_p, x.n, ho, wo, co} : e.pool.tensor(x.n, ho, wo, co);
-        if (u)
-            conv3x3_winograd(e.ctx, x.p, x.n, x.h, x.w, x.c, u, kF32, co, b, up, nullptr, out.p, res2, uf);
-        else
+        if (u) {
+            // GroupNorm partials for the next GroupNorm, where the one-kernel path runs
+            GnPartials gp;
+            if (uf && !out_p) {
+                gp.part = e.pool.floats(ceil_div(winograd_tiles(x.n, x.h, x.w, up), 32) * co * 2);
+                gp.item_rows = ho * wo;
+            }
+            conv3x3_winograd(e.ctx, x.p, x.n, x.h, x.w, x.c, u, kF32, co, b, up, nullptr, out.p, res2, uf,
+                             gp.part ? &gp : nullptr);
+            attach(e, out, gp);
+        } else {
             conv3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, w.p, w.wt, co, b, stride, pad, up, nullptr, out.p, res2);
+        }
         return out;
     }
     // conv(SiLU(GN(x))): the normalised map is written once and read by the conv.
@@ -122,7 +155,14 @@ struct Lin {  // Conv1x1 (src/engine/conv.rs:28-55)
     }
     DT fwd(Env &e, const DT &x, const float *res = nullptr) const {
         DT out = e.pool.tensor(x.n, x.h, x.w, co);
-        conv1x1(e.ctx, x.p, x.px(), ci, w.p, w.wt, co, b, res, out.p);
+        GnPartials gp;  // for a following GroupNorm (channel counts that have one)
+        if (co % GROUPS == 0) {
+            gp.part = e.pool.floats(ceil_div(x.px(), 32) * co * 2);
+            gp.item_rows = x.h * x.w;
+        }
+        conv1x1(e.ctx, x.p, x.px(), ci, w.p, w.wt, co, b, res, out.p, GemmEpilogue::None, nullptr, nullptr,
+                gp.part ? &gp : nullptr);
+        attach(e, out, gp);
         return out;
     }
 };

@@ -222,7 +222,8 @@ void winograd_output_transform(Context &ctx, const float *m, int n, int h, int w
 
 void conv3x3_winograd(Context &ctx, const float *x, int n, int h, int w, int c_in, const void *u, WeightType ut,
                       int c_out, const float *bias, bool upsample2x, const Affine *prologue, float *out,
-                      const float *residual2, const float *uf) {
+                      const float *residual2, const float *uf, GnPartials *gn) {
+    if (gn) gn->rows = 0;
     MH_REQUIRE(c_in > 0 && c_out > 0 && c_in % 4 == 0 && c_out % 4 == 0,
                "Winograd conv: channel counts must be multiples of 4");
     const int64_t tiles = winograd_tiles(n, h, w, upsample2x);
@@ -232,7 +233,7 @@ void conv3x3_winograd(Context &ctx, const float *x, int n, int h, int w, int c_i
     // EXACT arithmetic on f32 kernels: the fused kernel, where it takes the shape
     if (ut == kF32 && ctx.precision == Precision::Exact &&
         conv3x3_winograd_fused(ctx, x, n, h, w, c_in, static_cast<const float *>(u), uf, c_out, bias, upsample2x,
-                               prologue, out, residual2))
+                               prologue, out, residual2, gn))
         return;
     // V and M share one workspace block; the batched GEMM (batch > 1) never splits K,
     // so it does not touch the workspace itself.

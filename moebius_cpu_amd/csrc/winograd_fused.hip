@@ -49,6 +49,8 @@ constexpr int kMS = kFC + 4;   // M row stride in LDS (floats)
 constexpr int kVStage = 16 * kFT * kVS;
 constexpr int kLds = 2 * kVStage;  // 36864 floats = 144 KB
 static_assert(16 * kFT * kMS <= kLds, "the M exchange fits in the V stages");
+constexpr int kRed = 16 * kFT * kMS;  // GroupNorm reduction scratch, past the M exchange
+static_assert(kRed + 2 * 8 * 64 <= kLds && kRed >= kVStage, "reduction scratch fits, in V stage 1");
 constexpr int kOob = int(0x80000000u);
 
 struct FGeo {
@@ -81,7 +83,7 @@ __global__ __launch_bounds__(kFThreads, 2) void wino_fused_kernel(const float *_
                                                             const float *__restrict__ psh, int psilu,
                                                             const float *__restrict__ bias,
                                                             const float *__restrict__ res2, float *__restrict__ out,
-                                                            int nco_blocks, int nwork) {
+                                                            float *__restrict__ gnp, int nco_blocks, int nwork) {
     __shared__ float lds[kLds];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // Work items (channel block, tile block), channel block outer. Workgroup i
@@ -292,6 +294,7 @@ __global__ __launch_bounds__(kFThreads, 2) void wino_fused_kernel(const float *_
         }
         const int c = eco0 + 4 * q;
         const floatx4 bv = bias ? *reinterpret_cast<const floatx4 *>(bias + c) : floatx4{0.f, 0.f, 0.f, 0.f};
+        floatx4 gs{0.f, 0.f, 0.f, 0.f}, gq = gs;  // GroupNorm sums of the values stored
         floatx4 y[4];
         y[0] = add4(add4(add4(u0[0], u0[1]), u0[2]), bv);
         y[1] = add4(add4(add4(u1[0], u1[1]), u1[2]), bv);
@@ -305,6 +308,43 @@ __global__ __launch_bounds__(kFThreads, 2) void wino_fused_kernel(const float *_
             floatx4 rv = y[kk];
             if (res2) rv = add4(rv, *reinterpret_cast<const floatx4 *>(res2 + o));
             *reinterpret_cast<floatx4 *>(out + o) = rv;
+            if (gnp) {
+                gs = add4(gs, rv);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) gq[e] = __builtin_fmaf(rv[e], rv[e], gq[e]);
+            }
+        }
+        if (gnp) {
+            // GroupNorm partials of this block (per channel: sum and sum of
+            // squares over its 128 pixels), for the next GroupNorm's fold in
+            // place of a statistics pass: the four threads of a wave that hold
+            // channel quad q (tiles 4w .. 4w + 3) by xor butterfly, then the
+            // eight waves in order through LDS past the M exchange (V stage 1,
+            // not written again before the next item's second chunk).
+#pragma unroll
+            for (int off = 16; off < 64; off <<= 1)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    gs[e] += __shfl_xor(gs[e], off, 64);
+                    gq[e] += __shfl_xor(gq[e], off, 64);
+                }
+            floatx4 *red = reinterpret_cast<floatx4 *>(lds + kRed);
+            if (lane < kFC / 4) {
+                red[wave * (kFC / 4) + lane] = gs;
+                red[(kFThreads / 64 + wave) * (kFC / 4) + lane] = gq;
+            }
+            __syncthreads();
+            if (tid < kFC / 4) {
+                floatx4 ts = red[tid], tq = red[(kFThreads / 64) * (kFC / 4) + tid];
+#pragma unroll
+                for (int w8 = 1; w8 < kFThreads / 64; ++w8) {
+                    ts = add4(ts, red[w8 * (kFC / 4) + tid]);
+                    tq = add4(tq, red[(kFThreads / 64 + w8) * (kFC / 4) + tid]);
+                }
+                float *dst = gnp + ((et0 / kFT) * co + eco0 + 4 * tid) * 2;
+                *reinterpret_cast<floatx4 *>(dst) = floatx4{ts[0], tq[0], ts[1], tq[1]};
+                *reinterpret_cast<floatx4 *>(dst + 4) = floatx4{ts[2], tq[2], ts[3], tq[3]};
+            }
         }
     }
         if (!has_next) break;
@@ -328,14 +368,15 @@ __global__ void wino_u_fused_kernel(const float *__restrict__ u, int co, int ci,
 
 template <int UP, bool PRO>
 void launch_fused(Context &ctx, int nwork, const float *x, uint32_t xb, const FGeo &g, int ci, const float *u,
-                  uint32_t ub, int co, const Affine *pro, const float *bias, const float *res2, float *out) {
+                  uint32_t ub, int co, const Affine *pro, const float *bias, const float *res2, float *out,
+                  float *gnp) {
     // one workgroup per CU (its LDS holds one), a multiple of 8 (see the work
     // order in the kernel), no more than the items of one XCD's share need
     const int64_t per_xcd = ceil_div(nwork, 8);
     const unsigned grid = unsigned(8 * std::max<int64_t>(1, std::min<int64_t>(ctx.cu_count / 8, per_xcd)));
     wino_fused_kernel<UP, PRO><<<grid, kFThreads, 0, ctx.stream>>>(x, xb, g, ci, u, ub, co, pro ? pro->scale : nullptr,
                                                              pro ? pro->shift : nullptr, pro && pro->silu ? 1 : 0,
-                                                             bias, res2, out, co / kFC, nwork);
+                                                             bias, res2, out, gnp, co / kFC, nwork);
 }
 
 }  // namespace
@@ -351,7 +392,8 @@ void winograd_fused_weights(Context &ctx, const float *u, int c_out, int c_in, f
 
 bool conv3x3_winograd_fused(Context &ctx, const float *x, int n, int h, int w, int c_in, const float *u,
                             const float *uf, int c_out, const float *bias, bool upsample2x, const Affine *prologue,
-                            float *out, const float *residual2) {
+                            float *out, const float *residual2, GnPartials *gn) {
+    if (gn) gn->rows = 0;
     if (ctx.tune.wino_fused == 0 || c_in % kFK || c_out % kFC) return false;
     // Where it is faster (A/B per conv on MI355X, three kernels -> this one):
     // 512x512x128 746 -> 419 us, 256x256x256 552 -> 401, the same upsampled
@@ -384,12 +426,19 @@ bool conv3x3_winograd_fused(Context &ctx, const float *x, int n, int h, int w, i
         return false;
     }
     u = uf;
+    // GroupNorm partials: blocks of 32 whole tiles (128 pixels) within one item
+    float *gnp = nullptr;
+    if (gn && gn->part && aligned16(gn->part) && g.hi % 2 == 0 && g.wi % 2 == 0 &&
+        int64_t(g.th) * g.tw % kFT == 0 && gn->item_rows == g.hi * g.wi) {
+        gnp = gn->part;
+        gn->rows = 4 * kFT;
+    }
     if (up) {
-        if (prologue) launch_fused<1, true>(ctx, nwork, x, xb, g, c_in, u, ub, c_out, prologue, bias, residual2, out);
-        else launch_fused<1, false>(ctx, nwork, x, xb, g, c_in, u, ub, c_out, prologue, bias, residual2, out);
+        if (prologue) launch_fused<1, true>(ctx, nwork, x, xb, g, c_in, u, ub, c_out, prologue, bias, residual2, out, gnp);
+        else launch_fused<1, false>(ctx, nwork, x, xb, g, c_in, u, ub, c_out, prologue, bias, residual2, out, gnp);
     } else {
-        if (prologue) launch_fused<0, true>(ctx, nwork, x, xb, g, c_in, u, ub, c_out, prologue, bias, residual2, out);
-        else launch_fused<0, false>(ctx, nwork, x, xb, g, c_in, u, ub, c_out, prologue, bias, residual2, out);
+        if (prologue) launch_fused<0, true>(ctx, nwork, x, xb, g, c_in, u, ub, c_out, prologue, bias, residual2, out, gnp);
+        else launch_fused<0, false>(ctx, nwork, x, xb, g, c_in, u, ub, c_out, prologue, bias, residual2, out, gnp);
     }
     MH_LAUNCH_CHECK();
     return true;

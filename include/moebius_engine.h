@@ -7,8 +7,9 @@
  * The `moebius_*` declarations below have the reference's names, types,
  * struct layouts, constants and error behaviour, so a host built against
  * include/moebius_cpu.h links this library unchanged. Differences:
- *  - `threads` of moebius_engine_create is accepted and ignored: the engine
- *    runs on GPU 0 (mh_engine_create picks another device).
+ *  - `threads` of moebius_engine_create sets the host threads of the paste
+ *    around the device run (blur and blend; 0 = one per core, at most 16);
+ *    the models run on GPU 0 (mh_engine_create picks another device).
  *  - MOEBIUS_ERR_UNSUPPORTED_CPU (3) reports a missing or unusable GPU.
  *  - A seed gives other noise than the CPU engine's generator (the library
  *    draws its own seeded normals, mh_sample_noise); feed recorded noise

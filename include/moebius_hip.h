@@ -390,7 +390,8 @@ int32_t mh_crop_plan(const uint32_t *bbox, uint32_t img_w, uint32_t img_h, int64
 /* src/imaging/blend.rs:91-110: Pillow GaussianBlur(radius) of an 8-bit single-channel image. */
 int32_t mh_gaussian_blur(const uint8_t *src, uint32_t width, uint32_t height, float radius, uint8_t *out);
 /* src/imaging/blend.rs:155-232: pastes result (side x side RGB) over the image inside the
- * window {plan_x, plan_y, side}; mode MH_PASTE_*; changed {x, y, w, h} may be NULL. */
+ * window {plan_x, plan_y, side}; mode MH_PASTE_*; changed {x, y, w, h} may be NULL.
+ * The blur and blend run on up to 16 host threads (the bytes do not depend on it). */
 int32_t mh_paste(uint8_t *pixels, uint32_t width, uint32_t height, uint32_t stride, uint32_t channels,
                  const uint8_t *mask, uint32_t mask_stride, const uint8_t *result, int64_t plan_x, int64_t plan_y,
                  uint32_t side, uint32_t mode, uint32_t *changed);

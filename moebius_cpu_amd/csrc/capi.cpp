@@ -9,6 +9,7 @@
 #include <memory>
 #include <new>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/moebius_hip.h"
@@ -76,6 +77,9 @@ void pad4(const uint32_t *pad, int out[4]) {
         out[i] = int(pad[i]);
     }
 }
+
+// Host threads of the imaging entry points (their bytes do not depend on it): one per core, at most 16.
+unsigned host_threads() { return std::min(16u, std::max(1u, std::thread::hardware_concurrency())); }
 
 int dim(uint32_t v, const char *what) {
     if (v > (1u << 30)) mh::fail(mh::kInvalidArgument, std::string(what) + " too large");
@@ -1083,7 +1087,7 @@ int32_t mh_gaussian_blur(const uint8_t *src, uint32_t width, uint32_t height, fl
     return guard([&] {
         need(src, "src");
         need(out, "out");
-        const std::vector<uint8_t> b = mh::img::gaussian_blur(src, width, height, radius);
+        const std::vector<uint8_t> b = mh::img::gaussian_blur(src, width, height, radius, host_threads());
         std::memcpy(out, b.data(), b.size());
     });
 }
@@ -1110,7 +1114,8 @@ int32_t mh_paste(uint8_t *pixels, uint32_t width, uint32_t height, uint32_t stri
         MH_REQUIRE(side > 0 && plan_x < int64_t(width) && plan_y < int64_t(height) && plan_x + int64_t(side) > 0 &&
                        plan_y + int64_t(side) > 0,
                    "paste window does not overlap the image");
-        const mh::img::Rect r = mh::img::paste(im, {mask, width, height, mask_stride}, result, p, paste_of(mode));
+        const mh::img::Rect r = mh::img::paste(im, {mask, width, height, mask_stride}, result, p, paste_of(mode),
+                                               host_threads());
         if (changed) changed[0] = uint32_t(r.x), changed[1] = uint32_t(r.y), changed[2] = uint32_t(r.w),
                      changed[3] = uint32_t(r.h);
     });

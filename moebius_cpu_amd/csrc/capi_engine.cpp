@@ -1,8 +1,10 @@
 // The whole-pipeline C ABI of include/moebius_engine.h: the reference's
 // moebius_* entry points (src/ffi.rs) and the mh_ extensions for parity runs.
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/moebius_engine.h"
@@ -96,11 +98,15 @@ void load_models(MoebiusEngine &m, const std::string &dir) {
     HIP_CHECK(hipStreamSynchronize(c.stream));
 }
 
-int32_t create(int32_t device, const char *weights_dir, MoebiusEngine **out) {
+// threads (the reference's worker count, 0 = one per core): here the host
+// threads of the paste's blur and blend, at most 16.
+int32_t create(int32_t device, const char *weights_dir, uint32_t threads, MoebiusEngine **out) {
     if (!weights_dir || !out) return mh::capi::set_error(MOEBIUS_ERR_INVALID_ARGUMENT, "null argument");
     *out = nullptr;
     return guard([&] {
         auto m = std::make_unique<MoebiusEngine>(device);
+        const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
+        m->e.host_threads = std::min(16u, threads ? unsigned(threads) : hw);
         load_models(*m, weights_dir);
         *out = m.release();
     });
@@ -133,12 +139,11 @@ uint32_t moebius_abi_version(void) { return MOEBIUS_ABI_VERSION; }
 const char *moebius_last_error(void) { return mh::capi::last_error.c_str(); }
 
 int32_t moebius_engine_create(const char *weights_dir, uint32_t threads, MoebiusEngine **out) {
-    (void)threads;
-    return create(0, weights_dir, out);
+    return create(0, weights_dir, threads, out);
 }
 
 int32_t mh_engine_create(int32_t device, const char *weights_dir, MoebiusEngine **out) {
-    return create(device, weights_dir, out);
+    return create(device, weights_dir, 0, out);
 }
 
 void moebius_engine_destroy(MoebiusEngine *engine) {

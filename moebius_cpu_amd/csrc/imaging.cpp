@@ -7,6 +7,8 @@
 #include <array>
 #include <cmath>
 #include <optional>
+#include <thread>
+#include <vector>
 
 #include "common.hpp"
 
@@ -132,24 +134,48 @@ void box_line(const uint8_t *src, uint8_t *dst, size_t n, size_t radius, uint32_
     }
 }
 
-void box_rows(uint8_t *buf, size_t w, size_t h, float fradius, uint32_t passes) {
+// Runs f(first, last) over [0, n) in up to `threads` contiguous row ranges
+// (at least 16 rows each), the calling thread taking the first. Every row's
+// result depends on that row alone, so the bytes do not depend on the split.
+template <class F>
+void parallel_rows(size_t n, unsigned threads, F &&f) {
+    const size_t t = std::max<size_t>(1, std::min<size_t>(threads, (n + 15) / 16));
+    if (t == 1) {
+        f(size_t(0), n);
+        return;
+    }
+    const size_t chunk = (n + t - 1) / t;
+    std::vector<std::thread> pool;
+    for (size_t i = 1; i < t; ++i) {
+        const size_t a = i * chunk, b = std::min(n, a + chunk);
+        if (a < b) pool.emplace_back([&f, a, b] { f(a, b); });
+    }
+    f(size_t(0), std::min(n, chunk));
+    for (std::thread &th : pool) th.join();
+}
+
+void box_rows(uint8_t *buf, size_t w, size_t h, float fradius, uint32_t passes, unsigned threads) {
     const size_t radius = size_t(fradius);
     const uint32_t ww = uint32_t(float(1u << 24) / (fradius * 2.0f + 1.0f));
     const uint32_t fw = ((1u << 24) - uint32_t(radius * 2 + 1) * ww) / 2;
-    std::vector<uint8_t> tmp(w);
-    for (size_t y = 0; y < h; ++y) {
-        uint8_t *row = buf + y * w;
-        for (uint32_t p = 0; p < passes; ++p) {
-            box_line(row, tmp.data(), w, radius, ww, fw);
-            std::copy(tmp.begin(), tmp.end(), row);
+    parallel_rows(h, threads, [&](size_t y0, size_t y1) {
+        std::vector<uint8_t> tmp(w);
+        for (size_t y = y0; y < y1; ++y) {
+            uint8_t *row = buf + y * w;
+            for (uint32_t p = 0; p < passes; ++p) {
+                box_line(row, tmp.data(), w, radius, ww, fw);
+                std::copy(tmp.begin(), tmp.end(), row);
+            }
         }
-    }
+    });
 }
 
-std::vector<uint8_t> transpose(const std::vector<uint8_t> &src, size_t w, size_t h) {
+std::vector<uint8_t> transpose(const std::vector<uint8_t> &src, size_t w, size_t h, unsigned threads) {
     std::vector<uint8_t> out(src.size());
-    for (size_t y = 0; y < h; ++y)
-        for (size_t x = 0; x < w; ++x) out[x * h + y] = src[y * w + x];
+    parallel_rows(w, threads, [&](size_t x0, size_t x1) {
+        for (size_t x = x0; x < x1; ++x)
+            for (size_t y = 0; y < h; ++y) out[x * h + y] = src[y * w + x];
+    });
     return out;
 }
 
@@ -162,18 +188,19 @@ uint8_t u8_of(double v) {
 
 }  // namespace
 
-std::vector<uint8_t> gaussian_blur(const uint8_t *src, size_t w, size_t h, float radius) {
+std::vector<uint8_t> gaussian_blur(const uint8_t *src, size_t w, size_t h, float radius, unsigned threads) {
     constexpr uint32_t kPasses = 3;
     std::vector<uint8_t> buf(src, src + w * h);
     if (radius <= 0.0f || w == 0 || h == 0) return buf;
     const float fr = gaussian_box_radius(radius, kPasses);
-    box_rows(buf.data(), w, h, fr, kPasses);
-    std::vector<uint8_t> t = transpose(buf, w, h);
-    box_rows(t.data(), h, w, fr, kPasses);
-    return transpose(t, h, w);
+    box_rows(buf.data(), w, h, fr, kPasses, threads);
+    std::vector<uint8_t> t = transpose(buf, w, h, threads);
+    box_rows(t.data(), h, w, fr, kPasses, threads);
+    return transpose(t, h, w, threads);
 }
 
-Rect paste(ImageView &img, const MaskView &mask, const uint8_t *result, const CropPlan &plan, Paste mode) {
+Rect paste(ImageView &img, const MaskView &mask, const uint8_t *result, const CropPlan &plan, Paste mode,
+           unsigned threads) {
     const Rect src = source_rect(plan, img.width, img.height);
     if (src.w == 0 || src.h == 0) return Rect{};
     const size_t ox = size_t(int64_t(src.x) - plan.x), oy = size_t(int64_t(src.y) - plan.y);
@@ -195,7 +222,7 @@ Rect paste(ImageView &img, const MaskView &mask, const uint8_t *result, const Cr
     std::vector<uint8_t> region(rw * rh);
     for (size_t y = ry0; y < ry1; ++y)
         for (size_t x = rx0; x < rx1; ++x) region[(y - ry0) * rw + x - rx0] = mask.data[y * mask.stride + x] >= lo ? 255 : 0;
-    const std::vector<uint8_t> blurred = gaussian_blur(region.data(), rw, rh, 3.0f);
+    const std::vector<uint8_t> blurred = gaussian_blur(region.data(), rw, rh, 3.0f, threads);
     std::optional<std::array<double, 3>> shift;
     if (compensate) {
         // src/imaging/blend.rs:117-153 (ring_delta): the mask bbox grown by 10 px
@@ -210,13 +237,25 @@ Rect paste(ImageView &img, const MaskView &mask, const uint8_t *result, const Cr
             const size_t cr = (r0 + r1) / 2, cc = (c0 + c1) / 2;
             const size_t y0 = cr >= hh ? cr - hh : 0, y1 = std::min(cr + hh, src.h - 1);
             const size_t x0 = cc >= hw ? cc - hw : 0, x1 = std::min(cc + hw, src.w - 1);
+            // integer sums: exact in any order, so each thread sums its own rows
+            const size_t nr = y1 - y0 + 1;
+            const size_t nt = std::max<size_t>(1, std::min<size_t>(threads, (nr + 15) / 16));
+            std::vector<std::array<uint64_t, 7>> part(nt, std::array<uint64_t, 7>{});
+            const size_t chunk = (nr + nt - 1) / nt;
+            parallel_rows(nr, unsigned(nt), [&](size_t a, size_t b) {
+                std::array<uint64_t, 7> &q = part[a / chunk];
+                for (size_t y = y0 + a; y < y0 + b; ++y)
+                    for (size_t x = x0; x <= x1; ++x) {
+                        if (set(x, y)) continue;
+                        ++q[6];
+                        for (int c = 0; c < 3; ++c) q[size_t(c)] += dst_px(x, y)[c], q[3 + size_t(c)] += result_px(x, y)[c];
+                    }
+            });
             uint64_t ssrc[3] = {0, 0, 0}, sres[3] = {0, 0, 0}, n = 0;
-            for (size_t y = y0; y <= y1; ++y)
-                for (size_t x = x0; x <= x1; ++x) {
-                    if (set(x, y)) continue;
-                    ++n;
-                    for (int c = 0; c < 3; ++c) ssrc[c] += dst_px(x, y)[c], sres[c] += result_px(x, y)[c];
-                }
+            for (const auto &q : part) {
+                for (int c = 0; c < 3; ++c) ssrc[c] += q[size_t(c)], sres[c] += q[3 + size_t(c)];
+                n += q[6];
+            }
             if (n > 0) {
                 std::array<double, 3> d;
                 for (int c = 0; c < 3; ++c)
@@ -225,20 +264,22 @@ Rect paste(ImageView &img, const MaskView &mask, const uint8_t *result, const Cr
             }
         }
     }
-    for (size_t y = 0; y < src.h; ++y)
-        for (size_t x = 0; x < src.w; ++x) {
-            const double m = double(blurred[(src.y + y - ry0) * rw + src.x + x - rx0]) / 255.0;
-            const uint8_t *r = result_px(x, y);
-            uint8_t *o = dst_px(x, y);
-            for (int c = 0; c < 3; ++c) {
-                double res = double(r[c]) / 255.0;
-                const double orig = double(o[c]) / 255.0;
-                if (shift) res += (*shift)[size_t(c)];
-                double out = res * m + (1.0 - m) * orig;
-                if (shift) out = std::clamp(out, 0.0, 1.0);
-                o[c] = u8_of(out * 255.0);
+    parallel_rows(src.h, threads, [&](size_t ya, size_t yb) {
+        for (size_t y = ya; y < yb; ++y)
+            for (size_t x = 0; x < src.w; ++x) {
+                const double m = double(blurred[(src.y + y - ry0) * rw + src.x + x - rx0]) / 255.0;
+                const uint8_t *r = result_px(x, y);
+                uint8_t *o = dst_px(x, y);
+                for (int c = 0; c < 3; ++c) {
+                    double res = double(r[c]) / 255.0;
+                    const double orig = double(o[c]) / 255.0;
+                    if (shift) res += (*shift)[size_t(c)];
+                    double out = res * m + (1.0 - m) * orig;
+                    if (shift) out = std::clamp(out, 0.0, 1.0);
+                    o[c] = u8_of(out * 255.0);
+                }
             }
-        }
+    });
     return src;
 }
 

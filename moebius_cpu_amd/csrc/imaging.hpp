@@ -45,7 +45,8 @@ Rect source_rect(const CropPlan &p, size_t img_w, size_t img_h);
 // src/imaging/blend.rs:39-110: Pillow's GaussianBlur(radius) of an 8-bit
 // single-channel image (three fractional box-blur passes per axis, 24-bit
 // fixed point, 8-bit rounding after every pass).
-std::vector<uint8_t> gaussian_blur(const uint8_t *src, size_t w, size_t h, float radius);
+// threads: host threads for the row passes (the bytes do not depend on it).
+std::vector<uint8_t> gaussian_blur(const uint8_t *src, size_t w, size_t h, float radius, unsigned threads = 1);
 
 enum class Paste : uint32_t { None = 1, Feather = 2, FeatherCompensate = 3 };
 
@@ -54,7 +55,8 @@ enum class Paste : uint32_t { None = 1, Feather = 2, FeatherCompensate = 3 };
 // raw (None), through the mask blurred with radius 3 (Feather, f64 blend), or
 // additionally shifted by 1.1 x the ring's mean-colour difference
 // (FeatherCompensate). Returns the rectangle written.
-Rect paste(ImageView &img, const MaskView &mask, const uint8_t *result, const CropPlan &plan, Paste mode);
+Rect paste(ImageView &img, const MaskView &mask, const uint8_t *result, const CropPlan &plan, Paste mode,
+           unsigned threads = 1);
 
 // src/vae/mod.rs:60-78: bounding box of the 64 x 64 latent mask's nonzero
 // entries grown by margin and clamped; false for an empty mask.

@@ -233,7 +233,7 @@ img::Rect inpaint(Engine &e, img::ImageView &im, const img::MaskView &mask_in, c
     resize_u8(ctx, d_u8.u8(), kSide, kSide, int(side), int(side), 3, d_res.u8());
     std::vector<uint8_t> result(side * side * 3);
     d2h(ctx, result.data(), d_res.p, result.size());
-    return img::paste(im, mask, result.data(), plan, p.paste);
+    return img::paste(im, mask, result.data(), plan, p.paste, e.host_threads);
 }
 
 }  // namespace mh

@@ -48,6 +48,7 @@ struct Engine {
     Context ctx;
     std::unique_ptr<UNet> unet;
     std::unique_ptr<Vae> vae;
+    unsigned host_threads = 1;  // host threads for the paste around the device run
     explicit Engine(int device) : ctx(device) {}
 };
 

@@ -3,6 +3,8 @@
 // channel concatenation (src/engine/tensor.rs:59-73), 8-bit quantisation
 // (src/imaging/blend.rs:21-24), and device evaluation of the reference's
 // exp/SiLU. float4 accesses whenever the row length allows.
+#include <hip/hip_fp16.h>
+
 #include <algorithm>
 
 #include "common.hpp"
@@ -91,6 +93,12 @@ __global__ void to_u8_kernel(const float *__restrict__ x, int64_t len, uint8_t *
     }
 }
 
+// f16 -> f32 (exact: every f16 value is an f32 value).
+__global__ void widen_f16_kernel(const _Float16 *__restrict__ src, int64_t len, float *__restrict__ dst) {
+    for (int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; e < len; e += int64_t(gridDim.x) * blockDim.x)
+        dst[e] = float(src[e]);
+}
+
 __global__ void math_eval_kernel(int which, const float *__restrict__ x, int64_t len, float *__restrict__ y) {
     for (int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; e < len; e += int64_t(gridDim.x) * blockDim.x)
         y[e] = which == 0 ? ref_exp(x[e]) : ref_silu(x[e]);
@@ -159,6 +167,12 @@ void concat_channels(Context &ctx, const float *a, int ca, const float *b, int c
 void to_u8(Context &ctx, const float *x, int64_t len, uint8_t *out) {
     if (len == 0) return;
     to_u8_kernel<<<grid_for(len), 256, 0, ctx.stream>>>(x, len, out);
+    MH_LAUNCH_CHECK();
+}
+
+void widen_f16(Context &ctx, const void *src, int64_t len, float *dst) {
+    if (len == 0) return;
+    widen_f16_kernel<<<grid_for(len), 256, 0, ctx.stream>>>(static_cast<const _Float16 *>(src), len, dst);
     MH_LAUNCH_CHECK();
 }
 

@@ -31,6 +31,8 @@ void silu_inplace(Context &ctx, float *x, int64_t len);
 void add_inplace(Context &ctx, float *a, const float *b, int64_t len);
 void concat_channels(Context &ctx, const float *a, int ca, const float *b, int cb, int64_t pixels, float *out);
 void to_u8(Context &ctx, const float *x, int64_t len, uint8_t *out);
+// f16 [len] -> f32 [len], exact.
+void widen_f16(Context &ctx, const void *src, int64_t len, float *dst);
 void math_eval(Context &ctx, int which, const float *x, int64_t len, float *y);
 
 // ---- normalisation (norm.hip) ----

@@ -76,6 +76,24 @@ WeightStore::WeightStore(Context &ctx, const NamedTensor *t, int count) : ctx_(c
         e.host_dtype = t[i].dtype;
         if (!m_.emplace(t[i].name, e).second) fail(kInvalidArgument, std::string("duplicate tensor ") + t[i].name);
     }
+    // f32 widenings of the f16-stored (GEMM) weights, for EXACT arithmetic
+    size_t wide = 0;
+    for (auto &kv : m_)
+        if (kv.second.d.wt == kF16) wide += (size_t(kv.second.d.numel) * 4 + 255) & ~size_t(255);
+    if (wide) {
+        void *blk = nullptr;
+        HIP_CHECK(hipMalloc(&blk, wide));
+        derived_.push_back(blk);
+        derived_bytes_ += wide;
+        char *dst = static_cast<char *>(blk);
+        for (auto &kv : m_) {
+            DParam &d = kv.second.d;
+            if (d.wt != kF16) continue;
+            widen_f16(ctx, d.p, d.numel, reinterpret_cast<float *>(dst));
+            d.p32 = reinterpret_cast<const float *>(dst);
+            dst += (size_t(d.numel) * 4 + 255) & ~size_t(255);
+        }
+    }
     HIP_CHECK(hipStreamSynchronize(ctx.stream));
 }
 
@@ -164,7 +182,8 @@ struct Lin {  // Conv1x1 (src/engine/conv.rs:28-55)
     }
     void fwd(Env &e, const float *x, int64_t px, float *out, const float *res = nullptr,
              GemmEpilogue epi = GemmEpilogue::None) const {
-        conv1x1(e.ctx, x, px, ci, w.p, w.wt, co, b, res, out, epi);
+        const DParam wd = w.at(e.ctx);
+        conv1x1(e.ctx, x, px, ci, wd.p, wd.wt, co, b, res, out, epi);
     }
     DT fwd(Env &e, const DT &x, const DT *res = nullptr, GemmEpilogue epi = GemmEpilogue::None) const {
         DT out = e.pool.tensor(x.n, x.h, x.w, co);
@@ -181,7 +200,8 @@ struct Lin {  // Conv1x1 (src/engine/conv.rs:28-55)
         xa.shift = ss + int64_t(x.n) * x.c;
         xa.silu = false;
         xa.rows_per_item = x.h * x.w;
-        conv1x1(e.ctx, x.p, x.px(), ci, w.p, w.wt, co, b, nullptr, out.p, GemmEpilogue::None, nullptr, nullptr,
+        const DParam wd = w.at(e.ctx);
+        conv1x1(e.ctx, x.p, x.px(), ci, wd.p, wd.wt, co, b, nullptr, out.p, GemmEpilogue::None, nullptr, nullptr,
                 nullptr, &xa);
         return out;
     }
@@ -190,7 +210,8 @@ struct Lin {  // Conv1x1 (src/engine/conv.rs:28-55)
     DT fwd_gnp(Env &e, const DT &x, const DT *res = nullptr) const {
         DT out = e.pool.tensor(x.n, x.h, x.w, co);
         GnPartials gp = gn_request(e, x, co);
-        conv1x1(e.ctx, x.p, x.px(), ci, w.p, w.wt, co, b, res ? res->p : nullptr, out.p, GemmEpilogue::None, nullptr,
+        const DParam wd = w.at(e.ctx);
+        conv1x1(e.ctx, x.p, x.px(), ci, wd.p, wd.wt, co, b, res ? res->p : nullptr, out.p, GemmEpilogue::None, nullptr,
                 nullptr, &gp);
         gn_attach(e, out, gp);
         return out;
@@ -262,7 +283,8 @@ struct DwConv2d {
         DT mid = e.pool.tensor(x.n, x.h, x.w, x.c);
         depthwise3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, dw, dwb, 1, mid.p);
         DT out = out_p ? DT{out_p, x.n, x.h, x.w, co} : e.pool.tensor(x.n, x.h, x.w, co);
-        conv1x1(e.ctx, mid.p, mid.px(), ci, pw.w.p, pw.w.wt, co, pw.b, ci == co ? x.p : nullptr, out.p,
+        const DParam wd = pw.w.at(e.ctx);
+        conv1x1(e.ctx, mid.p, mid.px(), ci, wd.p, wd.wt, co, pw.b, ci == co ? x.p : nullptr, out.p,
                 GemmEpilogue::None, nullptr, res2);
         e.pool.recycle(mid);
         return out;
@@ -290,7 +312,8 @@ struct DwConv2d {
         ra.rows_per_item = x.h * x.w;
         GnPartials gp;
         if (gn_out) gp = gn_request(e, x, co);
-        conv1x1(e.ctx, mid.p, mid.px(), ci, pw.w.p, pw.w.wt, co, pw.b, ci == co ? x.p : nullptr, out.p,
+        const DParam wd = pw.w.at(e.ctx);
+        conv1x1(e.ctx, mid.p, mid.px(), ci, wd.p, wd.wt, co, pw.b, ci == co ? x.p : nullptr, out.p,
                 GemmEpilogue::None, ci == co ? &ra : nullptr, res2, gn_out ? &gp : nullptr);
         if (gn_out) gn_attach(e, out, gp);
         e.pool.recycle(mid);
@@ -344,6 +367,7 @@ struct SelfLambda {
     Lin to_q, to_k, to_v;
     float *w_aug_t = nullptr;  // [226][k]: column d of the folded filter per row
     void *wqkv = nullptr;      // [c + 2k][c]: to_q | to_k | to_v
+    float *wqkv32 = nullptr;   // its f32 widening when stored f16 (EXACT reads it)
     float *bqkv = nullptr;
     WeightType wt = kF32;
     void load(Env &e, const WeightStore &W, const std::string &p, int c_) {
@@ -373,6 +397,10 @@ struct SelfLambda {
                                  e.ctx.stream));
         HIP_CHECK(hipMemcpyAsync(dst + size_t(c + k) * c * esz, to_v.w.p, size_t(k) * c * esz,
                                  hipMemcpyDeviceToDevice, e.ctx.stream));
+        if (wt == kF16) {
+            HIP_CHECK(hipMalloc(&wqkv32, size_t(c + 2 * k) * c * sizeof(float)));
+            widen_f16(e.ctx, wqkv, int64_t(c + 2 * k) * c, wqkv32);
+        }
         std::vector<float> zeros(size_t(k), 0.0f);
         HIP_CHECK(hipMemcpyAsync(bqkv, to_q.b, size_t(c) * sizeof(float), hipMemcpyDeviceToDevice, e.ctx.stream));
         HIP_CHECK(hipMemcpy(bqkv + c, zeros.data(), size_t(k) * sizeof(float), hipMemcpyHostToDevice));
@@ -383,9 +411,11 @@ struct SelfLambda {
     void release() {
         if (w_aug_t) (void)hipFree(w_aug_t);
         if (wqkv) (void)hipFree(wqkv);
+        if (wqkv32) (void)hipFree(wqkv32);
         if (bqkv) (void)hipFree(bqkv);
         w_aug_t = nullptr;
         wqkv = nullptr;
+        wqkv32 = nullptr;
         bqkv = nullptr;
     }
     // h [x.px()][c] += SelfLambda(x): the block's residual add is folded into the tap filter.
@@ -397,7 +427,8 @@ struct SelfLambda {
         {
             const int widths[3] = {c, k, k};
             float *const outs[3] = {q.p, kt.p, vt.p};
-            conv1x1_segments(e.ctx, x.p, x.px(), c, wqkv, wt, bqkv, 3, widths, outs);
+            const bool w32 = wqkv32 && e.ctx.precision == Precision::Exact;
+            conv1x1_segments(e.ctx, x.p, x.px(), c, w32 ? wqkv32 : wqkv, w32 ? kF32 : wt, bqkv, 3, widths, outs);
         }
         float *lam_t = e.pool.floats(int64_t(x.n) * k * k);
         softmax_lambda(e.ctx, kt.p, vt.p, x.n, hw, k, k, lam_t);
@@ -577,7 +608,8 @@ struct Conv3 {
         if (u)
             conv3x3_winograd(e.ctx, x.p, x.n, x.h, x.w, x.c, u, kF32, c, b, up, nullptr, out.p);
         else
-            conv3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, w.p, w.wt, c, b, stride, pad, up, nullptr, out.p);
+            conv3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, w.at(e.ctx).p, w.at(e.ctx).wt, c, b, stride, pad, up, nullptr,
+                    out.p);
         return out;
     }
 };
@@ -665,6 +697,10 @@ class UNetDevice {
                 HIP_CHECK(hipMemcpyAsync(temb_b_ + r->temb_off, r->temb_proj.b, size_t(r->co) * sizeof(float),
                                          hipMemcpyDeviceToDevice, ctx_.stream));
             }
+            if (temb_wt_ == kF16) {
+                HIP_CHECK(hipMalloc(&temb_w32_, size_t(temb_total_) * TIME_EMBED * sizeof(float)));
+                widen_f16(ctx_, temb_w_, int64_t(temb_total_) * TIME_EMBED, temb_w32_);
+            }
         }
         lin1_.load(W_, d + ".time_embedding.linear_1", TIME_PROJ, TIME_EMBED, true);
         lin2_.load(W_, d + ".time_embedding.linear_2", TIME_EMBED, TIME_EMBED, true);
@@ -689,6 +725,7 @@ class UNetDevice {
                 for (auto &a : b.attn) a.release();
         if (sinus_dev_) (void)hipFree(sinus_dev_);
         if (temb_w_) (void)hipFree(temb_w_);
+        if (temb_w32_) (void)hipFree(temb_w32_);
         if (temb_b_) (void)hipFree(temb_b_);
     }
 
@@ -726,7 +763,9 @@ class UNetDevice {
         silu_inplace(ctx_, temb_silu, int64_t(b) * TIME_EMBED);
         // all resnets' time projections: tp [b][temb_total_]
         float *tp = pool_.floats(int64_t(b) * temb_total_);
-        conv1x1(ctx_, temb_silu, b, TIME_EMBED, temb_w_, temb_wt_, temb_total_, temb_b_, nullptr, tp);
+        const bool t32 = temb_w32_ && ctx_.precision == Precision::Exact;
+        conv1x1(ctx_, temb_silu, b, TIME_EMBED, t32 ? temb_w32_ : temb_w_, t32 ? kF32 : temb_wt_, temb_total_, temb_b_,
+                nullptr, tp);
 
         DT input = pool_.tensor(b, 64, 64, 9);
         for (int i = 0; i < b; ++i)
@@ -811,6 +850,7 @@ class UNetDevice {
     static constexpr int kSinusSteps = 1000;
     float *sinus_dev_ = nullptr;  // [kSinusSteps + 1][TIME_PROJ]
     void *temb_w_ = nullptr;  // [temb_total_][1280]: every resnet's time_emb_proj.weight
+    float *temb_w32_ = nullptr;  // its f32 widening when stored f16 (EXACT reads it)
     float *temb_b_ = nullptr;
     WeightType temb_wt_ = kF32;
     int temb_total_ = 0;

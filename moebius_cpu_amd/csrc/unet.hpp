@@ -23,11 +23,21 @@ struct NamedTensor {
 };
 
 // Device copy of a tensor in its stored precision (src/engine/param.rs:14-17).
+// An f16-stored GEMM weight also has its f32 widening (p32), which EXACT
+// arithmetic reads: the same products the f16-weight kernels form after
+// widening each value as they load it, without the conversion in the loop
+// and with the f32 kernels' tilings.
 struct DParam {
     const void *p = nullptr;
     WeightType wt = kF32;
     int64_t numel = 0;
+    const float *p32 = nullptr;
     const float *f() const { return static_cast<const float *>(p); }
+    // The copy the context's precision reads.
+    DParam at(const Context &ctx) const {
+        if (p32 && ctx.precision == Precision::Exact) return DParam{p32, kF32, numel, nullptr};
+        return *this;
+    }
 };
 
 // Uploads tensors into one HBM block; GEMM weights keep their dtype, every

@@ -263,18 +263,22 @@ def test_unet_pool_stops_allocating(ctx, gnet):
 
 
 def test_unet_f16_stored_weights(ctx, params, onet):
-    """f16-stored GEMM weights, f32 arithmetic: equals the f32 path on the rounded weights."""
+    """f16-stored GEMM weights, f32 arithmetic: EXACT reads the weights' f32
+    widening, so the step is bit for bit the f32 model's on the rounded weights,
+    and within the f32 bar of the oracle; the f16 copy stays beside it for FAST."""
     p16 = {k: v for k, v in params.items()}
     gemm = {s.name for s in U.unet_specs() if s.gemm}
     rounded = {k: (v.astype(np.float16).astype(np.float32) if k in gemm else v) for k, v in p16.items()}
     net16 = UNet(ctx, params, f16_gemm=True)
     inp = U.unet_input(seed=5005)
     got = net16.forward_host(inp.x, inp.timestep, cfg=False)
+    net_r = UNet(ctx, rounded)
+    assert np.array_equal(got, net_r.forward_host(inp.x, inp.timestep, cfg=False))
     want = oracle.UNet(rounded).forward(inp.x, inp.timestep, cfg=False)
     assert max_abs_rel(got, want) <= TOL
     w, _ = net16.memory()
-    w32, _ = UNet(ctx, params).memory()
-    assert w < 0.6 * w32  # GEMM weights really stored at half width
+    w32, _ = net_r.memory()
+    assert w32 < w < 1.5 * w32  # the f16 GEMM weights plus their f32 widening
 
 
 def test_missing_weight_is_a_weights_error(ctx, params):

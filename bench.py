@@ -206,11 +206,11 @@ def cfg3_resnet(ctx, steps):
 
 # ---------------------------------------------------------------- cfg4
 
-DOMINANT_TRAFFIC_BYTES = int((13.28 + 10.00) * 1048576)
 # HBM bytes per launch of the dominant kernel (below), from rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE over this script's own run, each scaled by the counter's reading for a plain
 # 256 MiB device copy (FETCH_SIZE reads half the copied bytes, WRITE_SIZE all of them),
-# averaged over the standalone loop's launches: 13.28 MiB fetched + 10.00 MiB written.
+# averaged over the timed standalone loop's 200 launches: 13.27 MiB fetched + 10.00 MiB written.
+DOMINANT_TRAFFIC_BYTES = 24398640
 
 
 def _dominant_gemm(ctx, steps, fast=False):

@@ -53,7 +53,7 @@ void timestep_sinusoid(int t, float *out) {
 }
 
 // ---------------------------------------------------------------- weights
-WeightStore::WeightStore(Context &ctx, const NamedTensor *t, int count) : ctx_(ctx) {
+WeightStore::WeightStore(Context &ctx, const NamedTensor *t, int count, bool widen) : ctx_(ctx) {
     std::vector<size_t> off(static_cast<size_t>(count));
     size_t total = 0;
     for (int i = 0; i < count; ++i) {
@@ -79,7 +79,7 @@ WeightStore::WeightStore(Context &ctx, const NamedTensor *t, int count) : ctx_(c
     // f32 widenings of the f16-stored (GEMM) weights, for EXACT arithmetic
     size_t wide = 0;
     for (auto &kv : m_)
-        if (kv.second.d.wt == kF16) wide += (size_t(kv.second.d.numel) * 4 + 255) & ~size_t(255);
+        if (widen && kv.second.d.wt == kF16) wide += (size_t(kv.second.d.numel) * 4 + 255) & ~size_t(255);
     if (wide) {
         void *blk = nullptr;
         HIP_CHECK(hipMalloc(&blk, wide));
@@ -619,7 +619,7 @@ struct Conv3 {
 // ---------------------------------------------------------------- model
 class UNetDevice {
   public:
-    UNetDevice(Context &ctx, const NamedTensor *t, int count) : ctx_(ctx), pool_(ctx), W_(ctx, t, count) {
+    UNetDevice(Context &ctx, const NamedTensor *t, int count) : ctx_(ctx), pool_(ctx), W_(ctx, t, count, true) {
         Env env{ctx_, pool_};
         // embed::conditioning (src/unet/embed.rs:72-83): [uncond = rows 10..20, cond = rows 0..10]
         const DParam table = W_.get("embedding_layer.weight", int64_t(20) * EHS, false);

@@ -44,7 +44,9 @@ struct DParam {
 // other tensor is stored f32.
 class WeightStore {
   public:
-    WeightStore(Context &ctx, const NamedTensor *t, int count);
+    // widen_f16: also keep the f32 widening of every f16-stored tensor (DParam::p32),
+    // for a model whose EXACT arithmetic reads its GEMM weights through DParam::at.
+    WeightStore(Context &ctx, const NamedTensor *t, int count, bool widen_f16);
     ~WeightStore();
     WeightStore(const WeightStore &) = delete;
     WeightStore &operator=(const WeightStore &) = delete;

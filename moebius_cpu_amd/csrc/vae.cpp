@@ -288,7 +288,9 @@ struct MidBlock {
 
 class VaeDevice {
   public:
-    VaeDevice(Context &ctx, const NamedTensor *t, int count) : ctx_(ctx), pool_(ctx), W_(ctx, t, count) {
+    // The VAE's 3x3 convs read f32 Winograd kernels built at load, so its f16-stored
+    // weights are not widened: the GEMMs that read them directly are a small share.
+    VaeDevice(Context &ctx, const NamedTensor *t, int count) : ctx_(ctx), pool_(ctx), W_(ctx, t, count, false) {
         const std::string e = "encoder";
         int c_prev = VCH[0];
         for (int i = 0; i < 4; ++i) {

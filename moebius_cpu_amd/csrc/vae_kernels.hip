@@ -16,8 +16,52 @@ constexpr int kLatentC = 4;
 // One wave per row (src/vae/mod.rs:275-294): the maximum (order-free), then
 // e = exp((v - max) * scale) or 0 below the flush threshold into LDS, summed by
 // one lane in row order in f32 (the reference's order), then v = e * (1 / sum).
+//
+// The sum is one chain of adds over the LDS copy of e, read 32 floats at a time
+// into two register blocks that alternate: the next block's reads are in flight
+// while the current one is added. e is zero-padded to sum_pad(n) floats; adding
+// +0 to a sum of non-negative terms leaves it unchanged, so the padding does not
+// alter the result.
+__host__ __device__ constexpr int sum_pad(int n) { return ((n + 63) / 64) * 64 + 32; }
+
+__device__ __forceinline__ void add_block(float &sum, const float4 (&b)[8]) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        sum += b[u].x;
+        sum += b[u].y;
+        sum += b[u].z;
+        sum += b[u].w;
+    }
+}
+
+__device__ __forceinline__ void load_block(float4 (&b)[8], const float4 *p) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) b[u] = p[u];
+}
+
+__device__ __forceinline__ float sum_in_order(const float4 *e4, int n) {
+    const int pairs = (n + 63) / 64;
+    float4 a[8], b[8];
+    float sum = 0.0f;
+    load_block(a, e4);
+    for (int p = 0; p < pairs; ++p) {
+        load_block(b, e4 + 16 * p + 8);
+        add_block(sum, a);
+        load_block(a, e4 + 16 * p + 16);
+        add_block(sum, b);
+    }
+    return sum;
+}
+
+__device__ __forceinline__ float flushed_exp(float v, float mx, float scale) {
+    const float a = (v - mx) * scale;
+    return a < kFlush ? 0.0f : ref_exp(a);
+}
+
+// Any row length: the row is read twice from memory, e kept in LDS.
 __global__ __launch_bounds__(64) void softmax_rows_kernel(float *__restrict__ rows, int n, float scale) {
-    extern __shared__ float e[];
+    extern __shared__ float4 e_lds[];  // sum_pad(n) floats
+    float *e = reinterpret_cast<float *>(e_lds);
     __shared__ float inv_s;
     float *row = rows + int64_t(blockIdx.x) * n;
     const int lane = threadIdx.x;
@@ -25,19 +69,53 @@ __global__ __launch_bounds__(64) void softmax_rows_kernel(float *__restrict__ ro
     for (int j = lane; j < n; j += 64) mx = fmaxf(mx, row[j]);
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-    for (int j = lane; j < n; j += 64) {
-        const float a = (row[j] - mx) * scale;
-        e[j] = a < kFlush ? 0.0f : ref_exp(a);
-    }
+    for (int j = lane; j < n; j += 64) e[j] = flushed_exp(row[j], mx, scale);
+    for (int j = n + lane; j < sum_pad(n); j += 64) e[j] = 0.0f;
     __syncthreads();
-    if (lane == 0) {
-        float sum = 0.0f;
-        for (int j = 0; j < n; ++j) sum += e[j];
-        inv_s = 1.0f / sum;
-    }
+    if (lane == 0) inv_s = 1.0f / sum_in_order(e_lds, n);
     __syncthreads();
     const float inv = inv_s;
     for (int j = lane; j < n; j += 64) row[j] = e[j] * inv;
+}
+
+// Rows of at most 64 * 4 * kRegF4 floats, a multiple of 4, 16-byte aligned: the
+// row is read once, all its float4 loads in flight together, and stays in
+// registers (a read per element per pass left each wave waiting on memory
+// latency 128 times per row). Same arithmetic as softmax_rows_kernel.
+constexpr int kRegF4 = 16;
+__global__ __launch_bounds__(64) void softmax_rows_reg_kernel(float *__restrict__ rows, int n, float scale) {
+    __shared__ float4 e4[sum_pad(64 * 4 * kRegF4) / 4];
+    __shared__ float inv_s;
+    float4 *row = reinterpret_cast<float4 *>(rows + int64_t(blockIdx.x) * n);
+    const int lane = threadIdx.x, n4 = n / 4;
+    float4 v[kRegF4];
+#pragma unroll
+    for (int i = 0; i < kRegF4; ++i) {
+        const int j = i * 64 + lane;
+        v[i] = j < n4 ? row[j] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kRegF4; ++i) mx = fmaxf(mx, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+#pragma unroll
+    for (int i = 0; i < kRegF4; ++i) {
+        const int j = i * 64 + lane;
+        v[i] = make_float4(flushed_exp(v[i].x, mx, scale), flushed_exp(v[i].y, mx, scale),
+                           flushed_exp(v[i].z, mx, scale), flushed_exp(v[i].w, mx, scale));
+        if (j < n4) e4[j] = v[i];
+    }
+    for (int j = n4 + lane; j < sum_pad(n) / 4; j += 64) e4[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    __syncthreads();
+    if (lane == 0) inv_s = 1.0f / sum_in_order(e4, n);
+    __syncthreads();
+    const float inv = inv_s;
+#pragma unroll
+    for (int i = 0; i < kRegF4; ++i) {
+        const int j = i * 64 + lane;
+        if (j < n4) row[j] = make_float4(v[i].x * inv, v[i].y * inv, v[i].z * inv, v[i].w * inv);
+    }
 }
 
 // out [cols][rows] = in [rows][cols] (row stride ld_in), 32x32 tiles through LDS.
@@ -83,7 +161,10 @@ void softmax_rows(Context &ctx, float *rows, int64_t nrows, int n, float scale) 
     MH_REQUIRE(n > 0 && n <= 15360, "softmax_rows: row length must be in 1..15360");
     MH_REQUIRE(nrows < (int64_t(1) << 31), "softmax_rows: too many rows");
     if (nrows == 0) return;
-    softmax_rows_kernel<<<unsigned(nrows), 64, size_t(n) * sizeof(float), ctx.stream>>>(rows, n, scale);
+    if (n % 4 == 0 && n <= 64 * 4 * kRegF4 && aligned16(rows))
+        softmax_rows_reg_kernel<<<unsigned(nrows), 64, 0, ctx.stream>>>(rows, n, scale);
+    else
+        softmax_rows_kernel<<<unsigned(nrows), 64, size_t(sum_pad(n)) * sizeof(float), ctx.stream>>>(rows, n, scale);
     MH_LAUNCH_CHECK();
 }
 

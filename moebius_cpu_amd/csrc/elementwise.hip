@@ -93,6 +93,21 @@ __global__ void to_u8_kernel(const float *__restrict__ x, int64_t len, uint8_t *
     }
 }
 
+// dst [n][item] = src [item] for every item (float4 when item4 > 0).
+__global__ void tile_items4_kernel(const float4 *__restrict__ src, int64_t item4, int n, float4 *__restrict__ dst) {
+    for (int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; e < item4; e += int64_t(gridDim.x) * blockDim.x) {
+        const float4 v = src[e];
+        for (int i = 0; i < n; ++i) dst[int64_t(i) * item4 + e] = v;
+    }
+}
+
+__global__ void tile_items_kernel(const float *__restrict__ src, int64_t item, int n, float *__restrict__ dst) {
+    for (int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; e < item; e += int64_t(gridDim.x) * blockDim.x) {
+        const float v = src[e];
+        for (int i = 0; i < n; ++i) dst[int64_t(i) * item + e] = v;
+    }
+}
+
 // f16 -> f32 (exact: every f16 value is an f32 value).
 __global__ void widen_f16_kernel(const _Float16 *__restrict__ src, int64_t len, float *__restrict__ dst) {
     for (int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; e < len; e += int64_t(gridDim.x) * blockDim.x)
@@ -167,6 +182,17 @@ void concat_channels(Context &ctx, const float *a, int ca, const float *b, int c
 void to_u8(Context &ctx, const float *x, int64_t len, uint8_t *out) {
     if (len == 0) return;
     to_u8_kernel<<<grid_for(len), 256, 0, ctx.stream>>>(x, len, out);
+    MH_LAUNCH_CHECK();
+}
+
+void tile_items(Context &ctx, const float *src, int64_t item, int n, float *dst) {
+    MH_REQUIRE(n >= 1 && item >= 0, "tile_items: bad item count or size");
+    if (item == 0) return;
+    if (item % 4 == 0 && aligned16(src) && aligned16(dst))
+        tile_items4_kernel<<<grid_for(item / 4), 256, 0, ctx.stream>>>(reinterpret_cast<const float4 *>(src), item / 4,
+                                                                     n, reinterpret_cast<float4 *>(dst));
+    else
+        tile_items_kernel<<<grid_for(item), 256, 0, ctx.stream>>>(src, item, n, dst);
     MH_LAUNCH_CHECK();
 }
 

@@ -34,6 +34,8 @@ void to_u8(Context &ctx, const float *x, int64_t len, uint8_t *out);
 // f16 [len] -> f32 [len], exact.
 void widen_f16(Context &ctx, const void *src, int64_t len, float *dst);
 void math_eval(Context &ctx, int which, const float *x, int64_t len, float *y);
+// dst [n][item] = src [item]: one item repeated over a batch.
+void tile_items(Context &ctx, const float *src, int64_t item, int n, float *dst);
 
 // ---- normalisation (norm.hip) ----
 // add (optional): per item and channel, item b's row at add + b * add_ld (add_ld 0: c).

@@ -171,6 +171,14 @@ void gn_attach(Env &e, DT &out, const GnPartials &gp) {
     }
 }
 
+// t repeated to a batch of n items (t holds one); t is recycled.
+DT widen(Env &e, DT &t, int n) {
+    DT w = e.pool.tensor(n, t.h, t.w, t.c);
+    tile_items(e.ctx, t.p, int64_t(t.h) * t.w * t.c, n, w.p);
+    e.pool.recycle(t);
+    return w;
+}
+
 struct Lin {  // Conv1x1 (src/engine/conv.rs:28-55)
     int ci = 0, co = 0;
     DParam w;
@@ -533,7 +541,14 @@ struct MixTransformer {
         attn1.release();
         attn2.release();
     }
-    DT fwd(Env &e, const DT &x, int br0) const {
+    DT fwd(Env &e, const DT &x, int br0) const { return fwd(e, x, x, br0); }
+    // xs: the input for everything before the cross-lambda, xr: the same at the
+    // full batch, the residual of proj_out. With CFG both branches see the same
+    // values until the first cross-lambda, so the first block runs that part
+    // on one item (xs.n == 1) and repeats h and LayerNorm 2's output to the batch
+    // just before the cross-lambda; the results equal a batch-2 run's.
+    DT fwd(Env &e, const DT &xs, const DT &xr, int br0) const {
+        const DT &x = xs;
         // The GroupNorm affine goes into proj_in's operand loads up to 640 channels
         // (EXACT) / 320 (FAST): the loads cost per K tile, and at 1280 channels
         // (and 640 in FAST) they cost more than the separate apply pass (whole
@@ -564,6 +579,10 @@ struct MixTransformer {
         lno2.out = t2.p;
         attn1.fwd_add(e, t, h.p, &lno2);
         e.pool.recycle(t);
+        if (xs.n != xr.n) {
+            h = widen(e, h, xr.n);
+            t2 = widen(e, t2, xr.n);
+        }
         attn2.fwd_add(e, t2, br0, h.p);
         e.pool.recycle(t2);
         t = ln3.fwd(e, h);
@@ -576,7 +595,7 @@ struct MixTransformer {
         DT u = point.fwd(e, g, &h);
         e.pool.recycle(g);
         e.pool.recycle(h);
-        DT out = proj_out.fwd_gnp(e, u, &x);
+        DT out = proj_out.fwd_gnp(e, u, &xr);
         e.pool.recycle(u);
         return out;
     }
@@ -767,20 +786,42 @@ class UNetDevice {
         conv1x1(ctx_, temb_silu, b, TIME_EMBED, t32 ? temb_w32_ : temb_w_, t32 ? kF32 : temb_wt_, temb_total_, temb_b_,
                 nullptr, tp);
 
-        DT input = pool_.tensor(b, 64, 64, 9);
-        for (int i = 0; i < b; ++i)
-            HIP_CHECK(hipMemcpyAsync(input.p + int64_t(i) * 64 * 64 * 9, x_dev, 64 * 64 * 9 * sizeof(float),
-                                     hipMemcpyDeviceToDevice, ctx_.stream));
+        // Both CFG branches take the same input, time embedding and weights until
+        // the first cross-lambda (the only place the text conditioning enters):
+        // conv_in, the first resnet and the first transformer's self-lambda run
+        // once, on one item, and are repeated to the batch where needed (the
+        // conv_in skip, the resnet's output as the transformer's residual, and h
+        // before the cross-lambda). Every kernel computes each item on its own,
+        // so this equals the batch-2 run.
+        const int bs = cfg ? 1 : b;
+        DT input = pool_.tensor(bs, 64, 64, 9);
+        HIP_CHECK(hipMemcpyAsync(input.p, x_dev, 64 * 64 * 9 * sizeof(float), hipMemcpyDeviceToDevice, ctx_.stream));
         std::vector<DT> skips;
-        skips.push_back(conv_in_.fwd(e, input));
+        DT c0 = conv_in_.fwd(e, input);
         pool_.recycle(input);
+        DT c0b;
+        if (bs != b) {
+            c0b = pool_.tensor(b, c0.h, c0.w, c0.c);
+            tile_items(ctx_, c0.p, int64_t(c0.h) * c0.w * c0.c, b, c0b.p);
+        } else {
+            c0b = c0;
+        }
+        skips.push_back(c0b);
         tr("unet.conv_in", skips.back());
         for (size_t i = 0; i < down_.size(); ++i) {
             for (size_t j = 0; j < down_[i].res.size(); ++j) {
                 const DwResnet &r = down_[i].res[j];
-                DT a = r.fwd(e, skips.back(), tp + r.temb_off, temb_total_);
-                tr("unet.down." + std::to_string(i) + ".res." + std::to_string(j), a);
-                DT h = down_[i].attn[j].fwd(e, a, br0);
+                const bool shared = bs != b && i == 0 && j == 0;
+                DT a = r.fwd(e, shared ? c0 : skips.back(), tp + r.temb_off, temb_total_);
+                if (shared) pool_.recycle(c0);
+                DT ab = a;
+                if (shared) {
+                    ab = pool_.tensor(b, a.h, a.w, a.c);
+                    tile_items(ctx_, a.p, int64_t(a.h) * a.w * a.c, b, ab.p);
+                }
+                tr("unet.down." + std::to_string(i) + ".res." + std::to_string(j), ab);
+                DT h = down_[i].attn[j].fwd(e, a, ab, br0);
+                if (shared) pool_.recycle(ab);
                 pool_.recycle(a);
                 tr("unet.down." + std::to_string(i) + ".attn." + std::to_string(j), h);
                 skips.push_back(h);

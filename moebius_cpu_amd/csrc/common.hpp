@@ -61,6 +61,7 @@ struct Tuning {
     int gn_blocks = 512;   // GroupNorm statistics: at most this many partial blocks per launch
     int gn_apply = 0;      // GroupNorm apply pass: 1 walks the map from its end
     int wino_fused = -1;   // Winograd convs in one kernel: -1 where faster, 1 wherever it fits, 0 never
+    int up_concat = 0;     // 1: the UNet's up path writes [h | skip] before each resnet (the reference's order)
 };
 // Sets `key` from its text form (the environment variable's syntax); value NULL
 // or "" restores the default. False for an unknown key or a malformed value.

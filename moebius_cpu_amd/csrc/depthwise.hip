@@ -153,11 +153,14 @@ constexpr int kDwTH = 16, kDwTW = 16, kDwCQ = 4;
 static_assert(kDwCQ * kDwTH * (kDwTW / 4) == 256, "one thread per 4 outputs of a quad");
 constexpr int kDwNP = (kDwTH + 2) * (kDwTW + 2);
 
+// x2 (optional): the input is [x | x2] per pixel, x holding quads [0, cv1)
+// (cv1 a multiple of kDwCQ, so a block reads one of the two) and x2 the rest.
 template <int EPI, bool PRO>
 __global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__restrict__ x, int n, int h, int w,
                                                              int cv, const float4 *__restrict__ wt,
                                                              const float4 *__restrict__ bias, DwPrologue pro,
-                                                             float4 *__restrict__ out) {
+                                                             float4 *__restrict__ out,
+                                                             const float4 *__restrict__ x2, int cv1) {
     using V = Vec<4>;
     // GLU (EPI 2) convolves two input halves. They pass through one LDS tile in
     // turn (20.7 KB instead of 41.5 KB: LDS allows seven workgroups per CU
@@ -177,6 +180,9 @@ __global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__res
     // so a thread has all of its (up to 11) 16-byte loads in flight at once.
     constexpr int TOTAL = PARTS * kDwNP * kDwCQ;
     constexpr int PER = (TOTAL + 255) / 256;
+    const bool sec = x2 && q0 >= cv1;
+    const float4 *xs = sec ? x2 : x;
+    const int xld = x2 ? (sec ? cv - cv1 : cv1) : cv, xq0 = sec ? q0 - cv1 : q0;
     float4 v[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
@@ -187,7 +193,7 @@ __global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__res
         const int iy = oy0 - 1 + pix / (kDwTW + 2), ix = ox0 - 1 + pix % (kDwTW + 2);
         v[i] = V::zero();
         if (idx < TOTAL && q0 + qq < co_v && iy >= 0 && iy < h && ix >= 0 && ix < w)
-            v[i] = x[(size_t(b) * h + iy) * size_t(w) * cv + size_t(ix) * cv + q0 + qq + part * co_v];
+            v[i] = xs[(size_t(b) * h + iy) * size_t(w) * xld + size_t(ix) * xld + xq0 + qq + part * co_v];
     }
     const int qq = threadIdx.x % kDwCQ, g = threadIdx.x / kDwCQ;
     const int r = g / (kDwTW / 4), c0 = (g % (kDwTW / 4)) * 4;
@@ -256,7 +262,7 @@ __global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__res
 
 template <bool PRO>
 void launch_dw_tile(Context &ctx, const float *x, int n, int h, int w, int c, const float *wt, const float *bias,
-                    int epilogue, const DwPrologue &pro, float *out) {
+                    int epilogue, const DwPrologue &pro, float *out, const float *x2 = nullptr, int c2 = 0) {
     const int cv = c / 4;
     const int co_v = epilogue == 2 ? cv / 2 : cv;
     const int64_t tiles = int64_t(n) * ceil_div(h, kDwTH) * ceil_div(w, kDwTW);
@@ -266,10 +272,12 @@ void launch_dw_tile(Context &ctx, const float *x, int n, int h, int w, int c, co
     const float4 *wv = reinterpret_cast<const float4 *>(wt);
     const float4 *bv = reinterpret_cast<const float4 *>(bias);
     float4 *ov = reinterpret_cast<float4 *>(out);
+    const float4 *x2v = reinterpret_cast<const float4 *>(x2);
+    const int cv1 = (c - c2) / 4;
     switch (epilogue) {
-        case 0: depthwise_tile_kernel<0, PRO><<<grid, 256, 0, ctx.stream>>>(xv, n, h, w, cv, wv, bv, pro, ov); break;
-        case 1: depthwise_tile_kernel<1, PRO><<<grid, 256, 0, ctx.stream>>>(xv, n, h, w, cv, wv, bv, pro, ov); break;
-        default: depthwise_tile_kernel<2, PRO><<<grid, 256, 0, ctx.stream>>>(xv, n, h, w, cv, wv, bv, pro, ov); break;
+        case 0: depthwise_tile_kernel<0, PRO><<<grid, 256, 0, ctx.stream>>>(xv, n, h, w, cv, wv, bv, pro, ov, x2v, cv1); break;
+        case 1: depthwise_tile_kernel<1, PRO><<<grid, 256, 0, ctx.stream>>>(xv, n, h, w, cv, wv, bv, pro, ov, x2v, cv1); break;
+        default: depthwise_tile_kernel<2, PRO><<<grid, 256, 0, ctx.stream>>>(xv, n, h, w, cv, wv, bv, pro, ov, x2v, cv1); break;
     }
     MH_LAUNCH_CHECK();
 }
@@ -298,10 +306,34 @@ void launch_dw(Context &ctx, const float *x, int n, int h, int w, int c, const f
 }  // namespace
 
 void depthwise3x3(Context &ctx, const float *x, int n, int h, int w, int c, const float *weight, const float *bias,
-                  int epilogue, float *out, const Affine *prologue) {
+                  int epilogue, float *out, const Affine *prologue, const float *x2, int c2) {
     MH_REQUIRE(epilogue >= 0 && epilogue <= 2, "depthwise: unknown epilogue");
     if (epilogue == 2) MH_REQUIRE(c % 2 == 0, "GLU needs an even channel count");
     if (int64_t(n) * h * w * c == 0) return;
+    if (x2) {
+        MH_REQUIRE(epilogue <= 1 && c2 > 0 && c2 < c && (c - c2) % (4 * kDwCQ) == 0 && c2 % 4 == 0,
+                   "depthwise over two inputs: NONE or RELU, first part a multiple of 16 channels, second of 4");
+        const bool tiled = ctx.tune.dw_tiled && aligned16(x) && aligned16(x2) && aligned16(weight) &&
+                           aligned16(bias) && aligned16(out) && (!prologue || (aligned16(prologue->scale) &&
+                                                                                aligned16(prologue->shift)));
+        if (!tiled) {  // the other kernels read one input: concatenate first
+            float *cat = static_cast<float *>(ctx.ws.get(size_t(n) * h * w * c * sizeof(float), ctx.stream));
+            concat_channels(ctx, x, c - c2, x2, c2, int64_t(n) * h * w, cat);
+            depthwise3x3(ctx, cat, n, h, w, c, weight, bias, epilogue, out, prologue);
+            return;
+        }
+        DwPrologue pro;
+        if (prologue) {
+            MH_REQUIRE(prologue->scale && prologue->shift, "depthwise prologue needs scale and shift");
+            pro.scale = prologue->scale;
+            pro.shift = prologue->shift;
+            pro.silu = prologue->silu ? 1 : 0;
+            launch_dw_tile<true>(ctx, x, n, h, w, c, weight, bias, epilogue, pro, out, x2, c2);
+        } else {
+            launch_dw_tile<false>(ctx, x, n, h, w, c, weight, bias, epilogue, pro, out, x2, c2);
+        }
+        return;
+    }
     const int co = epilogue == 2 ? c / 2 : c;
     DwPrologue pro;
     if (prologue) {

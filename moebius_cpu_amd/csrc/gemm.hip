@@ -79,9 +79,15 @@ __global__ void mfma_probe_kernel(const float *a, const float *b, float *d) {
 
 void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void *weight, WeightType wt, int c_out,
              const float *bias, const float *residual, float *out, GemmEpilogue epi, const ResidualAffine *raff,
-             const float *residual2, GnPartials *gn, const ResidualAffine *x_aff) {
+             const float *residual2, GnPartials *gn, const ResidualAffine *x_aff, const float *x2, int c2) {
     MH_REQUIRE(c_in > 0 && c_out > 0, "Conv1x1: empty channel axis");
     MH_REQUIRE(pixels < (int64_t(1) << 31), "Conv1x1: too many pixels");
+    if (x2) {
+        const int c1 = c_in - c2;
+        MH_REQUIRE(c2 > 0 && c1 > 0 && c1 % 64 == 0 && c2 % 4 == 0 && !x_aff && aligned16(x) && aligned16(x2),
+                   "Conv1x1 over two inputs: first part a multiple of 64 channels, second of 4, 16-byte aligned, "
+                   "no input affine");
+    }
     if (raff) {
         MH_REQUIRE(residual && raff->scale && raff->shift && raff->rows_per_item > 0,
                    "Conv1x1: residual transform needs the residual, scale, shift and rows per item");
@@ -89,13 +95,19 @@ void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void 
     if (pixels == 0) return;
     GemmArgs p{};
     p.a = x;
-    p.lda = c_in;
+    p.lda = c_in - (x2 ? c2 : 0);
     p.M = int(pixels);
     p.N = c_out;
     p.K = c_in;
     p.b = weight;
     p.ldb = c_in;
-    p.a_bytes = extent(pixels, c_in, c_in, 4);
+    p.a_bytes = extent(pixels, int(p.lda), int(p.lda), 4);
+    if (x2) {
+        p.a2 = x2;
+        p.lda2 = c2;
+        p.ka = c_in - c2;
+        p.a2_bytes = extent(pixels, c2, c2, 4);
+    }
     p.b_bytes = extent(c_out, c_in, c_in, wt == kF16 ? 2 : 4);
     p.bias = bias;
     p.res = residual;

@@ -60,10 +60,10 @@ __device__ __forceinline__ halfx4 to_h4(floatx4 v) {
 // tap the aligned conv gather shares across the tile).
 template <int MODE, bool PRO>
 __device__ __forceinline__ floatx4 load_a_h(const GemmArgs &p, __amdgpu_buffer_rsrc_t ar, const ConvRow &r, int m,
-                                            int k, int k_end, int tky, int tkx, int tci, int k0) {
+                                            int k, int k_end, int tky, int tkx, int tci, int k0, int64_t lda = -1) {
     if constexpr (MODE == kDense) {
         const bool ok = m < p.M && k < k_end;
-        const floatx4 v = buf_load4(ar, ok ? int((int64_t(m) * p.lda + k) * 4) : kOob);
+        const floatx4 v = buf_load4(ar, ok ? int((int64_t(m) * (lda < 0 ? p.lda : lda) + k) * 4) : kOob);
         if constexpr (PRO) return dense_prologue(p, r.b, k, ok, v);
         return v;
     } else if constexpr (MODE == kConvAligned || MODE == kConvVec) {
@@ -155,6 +155,7 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
     }
 
     const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(p.a, p.a_bytes);
+    const __amdgpu_buffer_rsrc_t a2_rsrc = make_rsrc(p.a2 ? p.a2 : p.a, p.a2 ? p.a2_bytes : p.a_bytes);
     const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(p.b, p.b_bytes);
     using BT = typename BChunk<F16, BVEC>::T;
     floatx4 ra0[A_LD], ra1[A_LD];
@@ -169,9 +170,13 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
             tkx = tap - tky * 3;
         }
         const int k = k0 + lc * 4;
+        // a tile past ka reads the second operand (whole tiles: ka % BKH == 0)
+        const bool sec = MODE == kDense && p.a2 && k0 >= p.ka;
 #pragma unroll
         for (int i = 0; i < A_LD; ++i)
-            ra[i] = load_a_h<MODE, PRO>(p, a_rsrc, crow[i], m0 + lrow + 16 * i, k, k_end, tky, tkx, tci, k0);
+            ra[i] = sec ? load_a_h<MODE, PRO>(p, a2_rsrc, crow[i], m0 + lrow + 16 * i, k - p.ka, k_end - p.ka, tky, tkx,
+                                              tci, k0 - p.ka, p.lda2)
+                        : load_a_h<MODE, PRO>(p, a_rsrc, crow[i], m0 + lrow + 16 * i, k, k_end, tky, tkx, tci, k0);
 #pragma unroll
         for (int i = 0; i < B_LD; ++i) rb[i] = load_b_h<F16, BVEC>(p, b_rsrc, n0 + lrow + 16 * i, k, k_end);
     };

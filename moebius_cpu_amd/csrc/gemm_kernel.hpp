@@ -104,6 +104,13 @@ struct GemmArgs {
     int gn_item_rows, gn_rows;
     // dense operands with the prologue (psc/psh [items][K]): rows per item
     int pro_rows;
+    // dense operands only: the A row is [a row (ka columns) | a2 row], a2
+    // [M][lda2] holding columns ka.. (ka a multiple of 64, so each K tile reads
+    // one of the two); a2_bytes its extent. a2 null: one operand.
+    const float *a2;
+    int64_t lda2;
+    int ka;
+    uint32_t a2_bytes;
 };
 
 // (residual [transformed] + bias) + acc [SiLU] (+ res2): the reference's
@@ -355,10 +362,11 @@ __device__ __forceinline__ floatx4 dense_prologue(const GemmArgs &p, int b, int 
 
 template <int MODE, bool PRO>
 __device__ __forceinline__ floatx4 load_a_buf(const GemmArgs &p, __amdgpu_buffer_rsrc_t ar, const ConvRow &r, int m,
-                                              int k, int k_end, int tap_ky, int tap_kx, int tap_ci0) {
+                                              int k, int k_end, int tap_ky, int tap_kx, int tap_ci0,
+                                              int64_t lda = -1) {
     if constexpr (MODE == kDense) {
         const bool ok = m < p.M && k < k_end;
-        const floatx4 v = buf_load4(ar, ok ? int((int64_t(m) * p.lda + k) * 4) : kOob);
+        const floatx4 v = buf_load4(ar, ok ? int((int64_t(m) * (lda < 0 ? p.lda : lda) + k) * 4) : kOob);
         if constexpr (PRO) return dense_prologue(p, r.b, k, ok, v);
         return v;
     } else {
@@ -634,6 +642,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
     }
 
     const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(p.a, p.a_bytes);
+    const __amdgpu_buffer_rsrc_t a2_rsrc = make_rsrc(p.a2 ? p.a2 : p.a, p.a2 ? p.a2_bytes : p.a_bytes);
     const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(p.b, p.b_bytes);
     // Two register stages (tiles kt+1 and kt+2 in flight while LDS stage kt&1
     // is consumed), two LDS stages: a load has two compute phases to land.
@@ -648,9 +657,15 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
             tkx = tap - tky * 3;
         }
         const int k = k0 + lc4 * 4;
+        // a tile past ka reads the second operand (whole tiles: ka % BK == 0)
+        const bool sec = MODE == kDense && p.a2 && k0 >= p.ka;
 #pragma unroll
         for (int i = 0; i < A_LD; ++i) {
-            if constexpr (MODE == kDense || MODE == kConvAligned || MODE == kConvVec)
+            if constexpr (MODE == kDense)
+                ra[i] = sec ? load_a_buf<MODE, PRO>(p, a2_rsrc, crow[i], m0 + lrow + 32 * i, k - p.ka, k_end - p.ka,
+                                                    tky, tkx, tci, p.lda2)
+                            : load_a_buf<MODE, PRO>(p, a_rsrc, crow[i], m0 + lrow + 32 * i, k, k_end, tky, tkx, tci);
+            else if constexpr (MODE == kConvAligned || MODE == kConvVec)
                 ra[i] = load_a_buf<MODE, PRO>(p, a_rsrc, crow[i], m0 + lrow + 32 * i, k, k_end, tky, tkx, tci);
             else
                 ra[i] = (k < k_end) ? load_a<MODE, PRO>(p, crow[i], m0 + lrow + 32 * i, k, tky, tkx, tci) : zero4();

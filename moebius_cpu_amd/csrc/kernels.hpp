@@ -39,9 +39,11 @@ void tile_items(Context &ctx, const float *src, int64_t item, int n, float *dst)
 
 // ---- normalisation (norm.hip) ----
 // add (optional): per item and channel, item b's row at add + b * add_ld (add_ld 0: c).
+// x2 (optional): the input is [x | x2] per pixel, x holding the first c - c2
+// channels (a multiple of 64) and x2 the last c2.
 void group_norm_affine(Context &ctx, const float *x, int n, int h, int w, int c, int groups, float eps,
                        const float *gamma, const float *beta, const float *add, float *scale, float *shift,
-                       int64_t add_ld = 0);
+                       int64_t add_ld = 0, const float *x2 = nullptr, int c2 = 0);
 void apply_affine(Context &ctx, const float *x, int n, int h, int w, int c, const float *scale, const float *shift,
                   bool silu, float *out);
 void group_norm_forward(Context &ctx, const float *x, int n, int h, int w, int c, int groups, float eps,
@@ -85,8 +87,11 @@ void resize_u8(Context &ctx, const uint8_t *src, int from_w, int from_h, int to_
 
 // ---- depthwise (depthwise.hip) ----
 // prologue (optional): GroupNorm affine [+SiLU] applied to in-image inputs as they load.
+// x2 (optional): the input is [x | x2] per pixel, x holding the first c - c2
+// channels (a multiple of 16) and x2 the last c2 (epilogue NONE or RELU).
 void depthwise3x3(Context &ctx, const float *x, int n, int h, int w, int c, const float *weight, const float *bias,
-                  int epilogue, float *out, const Affine *prologue = nullptr);
+                  int epilogue, float *out, const Affine *prologue = nullptr, const float *x2 = nullptr,
+                  int c2 = 0);
 
 // ---- GEMM-shaped convs (gemm.hip) ----
 // Per item and channel transform of a GEMM residual: res' = [SiLU](res . scale + shift),
@@ -99,10 +104,13 @@ struct ResidualAffine {
 // out = ([res'] + bias) + x' . W^T [SiLU] (+ residual2); gn (optional): GroupNorm partials of out.
 // x_aff (optional): x' = [SiLU](x . scale + shift) per item (pixel / rows_per_item) and
 // channel, applied as x loads (a GroupNorm's output without it being written); else x' = x.
+// x2 (optional): the input is [x | x2] per pixel, x holding the first
+// c_in - c2 channels (a multiple of 64) and x2 the last c2, read from the two
+// buffers in place of their concatenation (not with x_aff).
 void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void *weight, WeightType wt, int c_out,
              const float *bias, const float *residual, float *out, GemmEpilogue epi = GemmEpilogue::None,
              const ResidualAffine *raff = nullptr, const float *residual2 = nullptr, GnPartials *gn = nullptr,
-             const ResidualAffine *x_aff = nullptr);
+             const ResidualAffine *x_aff = nullptr, const float *x2 = nullptr, int c2 = 0);
 // residual2 (optional, [n, ho, wo, c_out]) is added last: out = (bias + conv) + residual2.
 void conv3x3(Context &ctx, const float *x, int n, int h, int w, int c_in, const void *weight, WeightType wt,
              int c_out, const float *bias, int stride, const int pad[4], bool upsample2x, const Affine *prologue,

@@ -37,9 +37,12 @@ int gn_chunk_px(int n, int hw, int c, int max_blocks) {
 }
 
 // part [n][chunks][c][2] = per-channel (sum y, sum y*y) over the chunk, y = x (+ add).
+// x2 (optional): x is [x | x2] per pixel, x holding channels [0, c1) (c1 a
+// multiple of kGnTileC, so a block reads one of the two) and x2 the rest.
 __global__ __launch_bounds__(256) void gn_partial_kernel(const float *__restrict__ x, const float *__restrict__ add,
                                                          int64_t add_ld, int hw, int c, int chunk_px, int nchunks,
-                                                         float *__restrict__ part) {
+                                                         float *__restrict__ part, const float *__restrict__ x2,
+                                                         int c1) {
     const int chunk = blockIdx.x, ct = blockIdx.y, b = blockIdx.z;
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
     const int c0 = ct * kGnTileC + tx * 4;
@@ -47,11 +50,13 @@ __global__ __launch_bounds__(256) void gn_partial_kernel(const float *__restrict
     if (c0 < c) {
         float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
         if (add) a = *reinterpret_cast<const float4 *>(add + size_t(b) * add_ld + c0);
-        const float *xb = x + size_t(b) * hw * c + c0;
+        const bool sec = x2 && ct * kGnTileC >= c1;
+        const int ld = x2 ? (sec ? c - c1 : c1) : c;
+        const float *xb = sec ? x2 + size_t(b) * hw * ld + (c0 - c1) : x + size_t(b) * hw * ld + c0;
         const int p1 = min(hw, (chunk + 1) * chunk_px);
 #pragma unroll 4
         for (int p = chunk * chunk_px + ty; p < p1; p += kGnRows) {
-            float4 v = *reinterpret_cast<const float4 *>(xb + size_t(p) * c);
+            float4 v = *reinterpret_cast<const float4 *>(xb + size_t(p) * ld);
             if (add) {
                 v.x = v.x + a.x;
                 v.y = v.y + a.y;
@@ -352,13 +357,13 @@ int64_t gn_partial_floats(const Context &ctx, int n, int hw, int c) {
 // group_norm_affine with its partials at `part` (gn_partial_floats of them).
 void group_norm_affine_into(Context &ctx, const float *x, int n, int h, int w, int c, int groups, float eps,
                             const float *gamma, const float *beta, const float *add, float *scale, float *shift,
-                            int64_t add_ld, float *part) {
+                            int64_t add_ld, float *part, const float *x2 = nullptr, int c2 = 0) {
     const int hw = h * w;
     const int chunk_px = gn_chunk_px(n, hw, c, ctx.tune.gn_blocks);
     const int nchunks = int(ceil_div(hw, chunk_px));
     const int nctiles = int(ceil_div(c, kGnTileC));
     gn_partial_kernel<<<dim3(nchunks, nctiles, n), 256, 0, ctx.stream>>>(x, add, add_ld, hw, c, chunk_px, nchunks,
-                                                                        part);
+                                                                        part, x2, c - c2);
     MH_LAUNCH_CHECK();
     gn_finalize_kernel<<<dim3(groups, n), kFinThreads, 0, ctx.stream>>>(part, add, add_ld, hw, c, nchunks, groups, 0, eps,
                                                                 gamma, beta, scale, shift);
@@ -377,12 +382,16 @@ void gn_check(int n, int h, int w, int c, int groups, const float *x, const floa
 
 void group_norm_affine(Context &ctx, const float *x, int n, int h, int w, int c, int groups, float eps,
                        const float *gamma, const float *beta, const float *add, float *scale, float *shift,
-                       int64_t add_ld) {
+                       int64_t add_ld, const float *x2, int c2) {
     if (add_ld <= 0) add_ld = c;
     gn_check(n, h, w, c, groups, x, add, add_ld);
+    if (x2)
+        MH_REQUIRE(c2 > 0 && c2 < c && (c - c2) % kGnTileC == 0 && c2 % 4 == 0 && aligned16(x2),
+                   "GroupNorm over two inputs: first part a multiple of 64 channels, second of 4, 16-byte aligned");
     float *part = static_cast<float *>(
         ctx.ws.get(size_t(gn_partial_floats(ctx, n, h * w, c)) * sizeof(float), ctx.stream));
-    group_norm_affine_into(ctx, x, n, h, w, c, groups, eps, gamma, beta, add, scale, shift, add_ld, part);
+    group_norm_affine_into(ctx, x, n, h, w, c, groups, eps, gamma, beta, add, scale, shift, add_ld, part, x2,
+                           x2 ? c2 : 0);
 }
 
 void group_norm_affine_partials(Context &ctx, const float *part, int rows, int n, int hw, int c, int groups,

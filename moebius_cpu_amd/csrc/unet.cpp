@@ -198,6 +198,14 @@ struct Lin {  // Conv1x1 (src/engine/conv.rs:28-55)
         fwd(e, x.p, x.px(), out.p, res ? res->p : nullptr, epi);
         return out;
     }
+    // The same of [xa | xb] per pixel, read from the two tensors.
+    DT fwd2(Env &e, const DT &xa, const DT &xb) const {
+        DT out = e.pool.tensor(xa.n, xa.h, xa.w, co);
+        const DParam wd = w.at(e.ctx);
+        conv1x1(e.ctx, xa.p, xa.px(), ci, wd.p, wd.wt, co, b, nullptr, out.p, GemmEpilogue::None, nullptr, nullptr,
+                nullptr, nullptr, xb.p, xb.c);
+        return out;
+    }
     // The same of GroupNorm(x) given its affine (ss = [scale | shift] per item
     // and channel, no SiLU), applied as x loads: the normalised tensor is not
     // written, and every value is the one the apply pass would write.
@@ -245,6 +253,14 @@ struct GN {
             group_norm_forward(e.ctx, x.p, x.n, x.h, x.w, x.c, GROUPS, eps, g, b, add, silu, out.p, add_ld);
         }
         return out;
+    }
+    // The same of [xa | xb] per pixel (the up path's concatenation, not written).
+    float *affine2(Env &e, const DT &xa, const DT &xb) const {
+        const int cc = xa.c + xb.c;
+        float *ss = e.pool.floats(int64_t(2) * xa.n * cc);
+        group_norm_affine(e.ctx, xa.p, xa.n, xa.h, xa.w, cc, GROUPS, eps, g, b, nullptr, ss, ss + int64_t(xa.n) * cc,
+                          0, xb.p, xb.c);
+        return ss;
     }
     // Statistics only: [scale | shift], each [n * c], for a consumer that
     // applies them; from the producer's partials when x carries them.
@@ -304,6 +320,27 @@ struct DwConv2d {
     // computed as the separate apply pass would (fma, then SiLU), so the result
     // is bit-identical to fwd(apply(x)). gn_out: attach the output's GroupNorm
     // partials (for the GroupNorm that reads it next).
+    // fwd_gn of [xa | xb] per pixel (c_in = xa.c + xb.c != c_out), read from
+    // the two tensors: the depthwise conv stages from both.
+    DT fwd_gn2(Env &e, const DT &xa, const DT &xb, const float *ss, bool gn_out) const {
+        const int cc = xa.c + xb.c;
+        if (cc != ci || ci == co) fail(kInternal, "DwConv2d over two inputs: channel mismatch");
+        Affine aff;
+        aff.scale = ss;
+        aff.shift = ss + int64_t(xa.n) * cc;
+        aff.silu = true;
+        DT mid = e.pool.tensor(xa.n, xa.h, xa.w, cc);
+        depthwise3x3(e.ctx, xa.p, xa.n, xa.h, xa.w, cc, dw, dwb, 1, mid.p, &aff, xb.p, xb.c);
+        DT out = e.pool.tensor(xa.n, xa.h, xa.w, co);
+        GnPartials gp;
+        if (gn_out) gp = gn_request(e, xa, co);
+        const DParam wd = pw.w.at(e.ctx);
+        conv1x1(e.ctx, mid.p, mid.px(), ci, wd.p, wd.wt, co, pw.b, nullptr, out.p, GemmEpilogue::None, nullptr,
+                nullptr, gn_out ? &gp : nullptr);
+        if (gn_out) gn_attach(e, out, gp);
+        e.pool.recycle(mid);
+        return out;
+    }
     DT fwd_gn(Env &e, const DT &x, const float *ss, const float *res2 = nullptr, float *out_p = nullptr,
               bool gn_out = false) const {
         Affine aff;
@@ -363,6 +400,26 @@ struct DwResnet {
         if (has_shortcut) s = shortcut.fwd(e, x);
         DT out = conv2.fwd_gn(e, b, ss2, has_shortcut ? s.p : x.p, nullptr, true);
         if (has_shortcut) e.pool.recycle(s);
+        e.pool.recycle(ss2);
+        e.pool.recycle(b);
+        return out;
+    }
+    // fwd of [xa | xb] per pixel (the up path's skip concatenation,
+    // src/unet/mod.rs:208-213) without writing it: norm1's statistics, conv1's
+    // depthwise staging and the shortcut read both tensors. Needs a shortcut
+    // (c_in != c_out) and xa.c a multiple of 64.
+    bool takes_two(const DT &xa, const DT &xb) const {
+        return has_shortcut && xa.c + xb.c == ci && xa.c % 64 == 0 && xb.c % 4 == 0 && xa.n == xb.n &&
+               xa.h == xb.h && xa.w == xb.w;
+    }
+    DT fwd2(Env &e, const DT &xa, const DT &xb, const float *tp, int64_t tp_ld) const {
+        float *ss1 = norm1.affine2(e, xa, xb);
+        DT b = conv1.fwd_gn2(e, xa, xb, ss1, true);
+        e.pool.recycle(ss1);
+        float *ss2 = norm2.affine(e, b, tp, tp_ld);
+        DT s = shortcut.fwd2(e, xa, xb);
+        DT out = conv2.fwd_gn(e, b, ss2, s.p, nullptr, true);
+        e.pool.recycle(s);
         e.pool.recycle(ss2);
         e.pool.recycle(b);
         return out;
@@ -836,13 +893,18 @@ class UNetDevice {
             for (size_t j = 0; j < up_[i].res.size(); ++j) {
                 DT skip = skips.back();
                 skips.pop_back();
-                DT cat = pool_.tensor(h.n, h.h, h.w, h.c + skip.c);
-                concat_channels(ctx_, h.p, h.c, skip.p, skip.c, h.px(), cat.p);
+                const DwResnet &r = up_[i].res[j];
+                DT a;
+                if (!ctx_.tune.up_concat && r.takes_two(h, skip)) {  // [h | skip] read in place
+                    a = r.fwd2(e, h, skip, tp + r.temb_off, temb_total_);
+                } else {
+                    DT cat = pool_.tensor(h.n, h.h, h.w, h.c + skip.c);
+                    concat_channels(ctx_, h.p, h.c, skip.p, skip.c, h.px(), cat.p);
+                    a = r.fwd(e, cat, tp + r.temb_off, temb_total_);
+                    pool_.recycle(cat);
+                }
                 pool_.recycle(skip);
                 if (h.p != skip.p) pool_.recycle(h);
-                const DwResnet &r = up_[i].res[j];
-                DT a = r.fwd(e, cat, tp + r.temb_off, temb_total_);
-                pool_.recycle(cat);
                 tr("unet.up." + std::to_string(i) + ".res." + std::to_string(j), a);
                 h = up_[i].attn[j].fwd(e, a, br0);
                 pool_.recycle(a);

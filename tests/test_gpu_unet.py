@@ -234,6 +234,25 @@ def test_unet_step_is_deterministic_and_batch_consistent(ctx, gnet):
     assert max_abs_rel(c[0], a[1]) <= TOL  # the cond item of a CFG step is the cond-only step
 
 
+@pytest.mark.parametrize("cfg", [False, True])
+@pytest.mark.parametrize("fast", [False, True])
+def test_unet_up_path_two_inputs_is_bit_exact(ctx, gnet, fast, cfg, tune):
+    """The up path's resnets read [h | skip] from the two tensors (GroupNorm
+    statistics, the depthwise staging and the shortcut GEMM each take two base
+    pointers) and give the bits of writing the concatenation first, as the
+    reference does (src/unet/mod.rs:208-213)."""
+    inp = U.unet_input(seed=5011)
+    ctx.set_precision(fast)
+    try:
+        tune("up_concat", "1")
+        cat = gnet.forward_host(inp.x, inp.timestep, cfg=cfg)
+        tune("up_concat", "0")
+        two = gnet.forward_host(inp.x, inp.timestep, cfg=cfg)
+    finally:
+        ctx.set_precision(False)
+    assert np.array_equal(cat, two)
+
+
 @pytest.mark.parametrize("fast", [False, True])
 def test_unet_groupnorm_into_proj_in_is_bit_exact(ctx, gnet, fast, tune):
     """The transformers' GroupNorm applied inside proj_in's operand loads gives the

@@ -62,6 +62,7 @@ struct Tuning {
     int gn_apply = 0;      // GroupNorm apply pass: 1 walks the map from its end
     int wino_fused = -1;   // Winograd convs in one kernel: -1 where faster, 1 wherever it fits, 0 never
     int up_concat = 0;     // 1: the UNet's up path writes [h | skip] before each resnet (the reference's order)
+    int lambda_taps = 1;   // 0: the self-lambda's position coefficients through the general GEMM
 };
 // Sets `key` from its text form (the environment variable's syntax); value NULL
 // or "" restores the default. False for an unknown key or a malformed value.

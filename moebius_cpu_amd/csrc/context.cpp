@@ -74,6 +74,7 @@ bool set_tuning(Tuning &t, const char *key, const char *value) {
     if (k == "gn_apply") return to_int(t.gn_apply, 0) && t.gn_apply >= 0 && t.gn_apply <= 1;
     if (k == "wino_fused") return to_int(t.wino_fused, -1) && t.wino_fused >= -1 && t.wino_fused <= 1;
     if (k == "up_concat") return to_int(t.up_concat, 0) && t.up_concat >= 0 && t.up_concat <= 1;
+    if (k == "lambda_taps") return to_int(t.lambda_taps, 1) && t.lambda_taps >= 0 && t.lambda_taps <= 1;
     if (k == "tap_heads") {
         if (clear) {
             t.tap_tile = -1, t.tap_heads = 0;
@@ -100,7 +101,8 @@ Context::Context(int dev) : device(dev) {
                                               {"MOEBIUS_HIP_GN_BLOCKS", "gn_blocks"},
                                               {"MOEBIUS_HIP_GN_APPLY", "gn_apply"},
                                               {"MOEBIUS_HIP_WINO_FUSED", "wino_fused"},
-                                              {"MOEBIUS_HIP_UP_CONCAT", "up_concat"}};
+                                              {"MOEBIUS_HIP_UP_CONCAT", "up_concat"},
+                                              {"MOEBIUS_HIP_LAMBDA_TAPS", "lambda_taps"}};
     for (const auto &kv : env_keys)
         if (const char *e = std::getenv(kv[0])) set_tuning(tune, kv[1], e);
     int count = 0;

@@ -179,6 +179,11 @@ struct LayerNormOut {
 // of the out rows.
 void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc, const float *residual, float *out,
                 int nb, int hh, int ww, int vd, const LayerNormOut *lno = nullptr);
+// Position coefficients A = Q . W_aug (src/unet/lambda.rs:131-137) on the matrix cores:
+// q [npx][8][k] (pixel, head rows of k), w_aug_t [226][k] -> a_t [npx][226][8], the
+// tap-major layout tap_filter reads. k must pass lambda_taps_ok (40 or 80).
+bool lambda_taps_ok(int k);
+void lambda_taps(Context &ctx, const float *q, const float *w_aug_t, int64_t npx, int k, float *a_t);
 // out [nb*hw][8*k] = (residual +) (yc + (q . E) . V[branch]); e [hw][10][k]; v_branches [2][10][k].
 // out may alias yc or residual.
 void position_term(Context &ctx, const float *q, const float *e, const float *v_branches, int br0, int nb, int hw,

@@ -503,10 +503,16 @@ struct SelfLambda {
         gemm_nt(e.ctx, q.p, k, int64_t(hw) * c, lam_t, kF32, k, int64_t(k) * k, hw * HEADS, k, k, x.n, nullptr,
                 nullptr, yc.p, k, int64_t(hw) * c);
         e.pool.recycle(lam_t);
-        // A = Q . W_aug over every pixel and head of the batch, stored [pixel][tap][head].
+        // A = Q . W_aug over every pixel and head of the batch, stored [pixel][tap][head]:
+        // EXACT by the dedicated kernel at k = 40 / 80 (64x64 x 40 at batch 2: 34.5 -> 21.2 us,
+        // 32x32 x 80: 14.0 -> 10.5 us; whole step 7.66 -> 7.60 ms), else (FAST, whose GEMMs
+        // take f16 products, and k = 160) the general GEMM.
         float *a = e.pool.floats(x.px() * HEADS * TAPS_B);
-        gemm_nt(e.ctx, q.p, k, 0, w_aug_t, kF32, k, 0, int(x.px() * HEADS), TAPS_B, k, 1, nullptr, nullptr, a,
-                int64_t(TAPS_B) * HEADS, 0, GemmEpilogue::None, HEADS);
+        if (e.ctx.precision == Precision::Exact && e.ctx.tune.lambda_taps && lambda_taps_ok(k))
+            lambda_taps(e.ctx, q.p, w_aug_t, x.px(), k, a);
+        else
+            gemm_nt(e.ctx, q.p, k, 0, w_aug_t, kF32, k, 0, int(x.px() * HEADS), TAPS_B, k, 1, nullptr, nullptr, a,
+                    int64_t(TAPS_B) * HEADS, 0, GemmEpilogue::None, HEADS);
         tap_filter(e.ctx, a, vt.p, yc.p, h, h, x.n, x.h, x.w, k, lno);
         e.pool.recycle(a);
         e.pool.recycle(yc);

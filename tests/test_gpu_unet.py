@@ -76,6 +76,33 @@ def test_tap_filter_kernel_bit_exact(ctx, nb, hh, ww, vd, heads_per_thread, tune
         assert np.array_equal(got_res[b], h[b] + want)
 
 
+# Position coefficients A = Q . W_aug (lambda.rs:131-137) by the matrix-core
+# kernel, tap-major: against the f64 product and against the general GEMM's
+# row-grouped output of the same product; odd pixel counts leave a half pair.
+@pytest.mark.parametrize("npx,k", [(8192, 40), (2048, 80), (7, 40), (1, 80), (301, 80)])
+def test_lambda_position_coeffs_kernel(ctx, npx, k):
+    rng = np.random.default_rng(npx + k)
+    q = rng.standard_normal((npx, 8, k)).astype(np.float32)
+    w = rng.standard_normal((226, k)).astype(np.float32)
+    want = (q.reshape(npx * 8, k).astype(np.float64) @ w.astype(np.float64).T).reshape(npx, 8, 226)
+    want = want.transpose(0, 2, 1)
+    qd, wd = D(ctx, q), D(ctx, w)
+    out = E.DeviceArray(ctx, (npx, 226, 8))
+    E.check(E.lib().mh_lambda_position_coeffs(ctx.h, qd.ptr, wd.ptr, npx, k, out.ptr))
+    got = out.numpy()
+    assert max_abs_rel(got, want) < 1e-5
+    g = E.DeviceArray(ctx, (npx, 226, 8))
+    E.check(E.lib().mh_gemm_nt(ctx.h, qd.ptr, k, wd.ptr, 0, k, npx * 8, 226, k, None, None, g.ptr, 226 * 8, 8))
+    assert max_abs_rel(got, g.numpy()) < 1e-5
+
+
+def test_lambda_position_coeffs_rejects_other_widths(ctx):
+    q = E.DeviceArray(ctx, (2, 8, 160))
+    w = E.DeviceArray(ctx, (226, 160))
+    out = E.DeviceArray(ctx, (2, 226, 8))
+    assert E.lib().mh_lambda_position_coeffs(ctx.h, q.ptr, w.ptr, 2, 160, out.ptr) != 0
+
+
 @pytest.mark.parametrize("br0,nb,k", [(0, 2, 40), (1, 1, 80), (0, 2, 160)])
 def test_position_term_kernel_bit_exact(ctx, br0, nb, k):
     hw = 37

@@ -308,13 +308,16 @@ int32_t mh_tap_filter(MhContext *ctx, const float *a_t, const float *v, const fl
                       float *out, uint32_t nb, uint32_t hh, uint32_t ww, uint32_t vd);
 
 /* src/unet/lambda.rs:131-137, the position path's `matmul` A = Q . W_aug
- * over npx pixels: q [npx][8][k] (the pixel's 8 head rows of k), w_aug_t
- * [226][k] (the reference's w_aug [k][226] transposed: tap d < 225 is the
- * position conv's weight, tap 225 its bias) -> a_t [npx][226][8], the layout
- * mh_tap_filter takes. k must be 40 or 80 (the UNet's 64x64 and 32x32 levels);
- * f32 products on the matrix cores, summed in f32. */
-int32_t mh_lambda_position_coeffs(MhContext *ctx, const float *q, const float *w_aug_t, uint32_t npx, uint32_t k,
-                                  float *a_t);
+ * over nb items of hw pixels: q [nb*hw][8][k] (a pixel's 8 head rows of k),
+ * w_aug_t [226][k] (the reference's w_aug [k][226] transposed: tap d < 225 is
+ * the position conv's weight, tap 225 its bias) -> a_t [nb*hw][226][8], the
+ * layout mh_tap_filter takes. With lambda_t [nb][k][k] (mh_softmax_lambda's
+ * output) also the content path's `matmul` yc = Q . lambda_c per item
+ * (lambda.rs:123), yc [nb*hw][8][k]; lambda_t and yc are both NULL or both
+ * given. k must be 40 or 80 (the UNet's 64x64 and 32x32 levels); f32 products
+ * on the matrix cores, summed in f32. */
+int32_t mh_lambda_position_coeffs(MhContext *ctx, const float *q, const float *w_aug_t, const float *lambda_t,
+                                  uint32_t nb, uint32_t hw, uint32_t k, float *a_t, float *yc);
 
 /* src/unet/lambda.rs:276-295 `position_term`: u = yc + (q . E) . V[branch], per
  * element in the reference's order; out = u, or residual + u when residual is

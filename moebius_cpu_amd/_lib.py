@@ -97,7 +97,7 @@ SIGNATURES = {
     "mh_selftest_mfma_f32": (_i32, [_vp, _vp, _vp, _vp]),
     "mh_softmax_lambda": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
     "mh_tap_filter": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32]),
-    "mh_lambda_position_coeffs": (_i32, [_vp, _vp, _vp, _u32, _u32, _vp]),
+    "mh_lambda_position_coeffs": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp]),
     "mh_position_term": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     "mh_cross_lambda": (_i32, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp]),
     "mh_gemm_nt": (_i32, [_vp, _vp, _u64, _vp, _u32, _u64, _u32, _u32, _u32, _vp, _vp, _vp, _u64, _u32]),

@@ -595,15 +595,17 @@ int32_t mh_tap_filter(MhContext *ctx, const float *a_t, const float *v, const fl
     });
 }
 
-int32_t mh_lambda_position_coeffs(MhContext *ctx, const float *q, const float *w_aug_t, uint32_t npx, uint32_t k,
-                                  float *a_t) {
+int32_t mh_lambda_position_coeffs(MhContext *ctx, const float *q, const float *w_aug_t, const float *lambda_t,
+                                  uint32_t nb, uint32_t hw, uint32_t k, float *a_t, float *yc) {
     return guard([&] {
         mh::Context &c = C(ctx);
         need(q, "q");
         need(w_aug_t, "w_aug_t");
         need(a_t, "a_t");
         if (!mh::lambda_taps_ok(int(k))) mh::fail(mh::kInvalidArgument, "lambda position coefficients: k must be 40 or 80");
-        mh::lambda_taps(c, q, w_aug_t, int64_t(npx), int(k), a_t);
+        if ((lambda_t == nullptr) != (yc == nullptr))
+            mh::fail(mh::kInvalidArgument, "lambda position coefficients: lambda_t and yc go together");
+        mh::lambda_taps(c, q, w_aug_t, lambda_t, dim(nb, "nb"), dim(hw, "hw"), int(k), a_t, yc);
     });
 }
 

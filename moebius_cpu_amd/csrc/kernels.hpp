@@ -180,10 +180,13 @@ struct LayerNormOut {
 void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc, const float *residual, float *out,
                 int nb, int hh, int ww, int vd, const LayerNormOut *lno = nullptr);
 // Position coefficients A = Q . W_aug (src/unet/lambda.rs:131-137) on the matrix cores:
-// q [npx][8][k] (pixel, head rows of k), w_aug_t [226][k] -> a_t [npx][226][8], the
-// tap-major layout tap_filter reads. k must pass lambda_taps_ok (40 or 80).
+// q [nb*hw][8][k] (pixel, head rows of k), w_aug_t [226][k] -> a_t [nb*hw][226][8], the
+// tap-major layout tap_filter reads; with lambda_t [nb][k][k] (softmax_lambda's
+// transposed lambda_c) also the content term yc [nb*hw][8][k] = Q . lambda_c per item
+// (lambda.rs:123). k must pass lambda_taps_ok (40 or 80).
 bool lambda_taps_ok(int k);
-void lambda_taps(Context &ctx, const float *q, const float *w_aug_t, int64_t npx, int k, float *a_t);
+void lambda_taps(Context &ctx, const float *q, const float *w_aug_t, const float *lambda_t, int nb, int hw, int k,
+                 float *a_t, float *yc);
 // out [nb*hw][8*k] = (residual +) (yc + (q . E) . V[branch]); e [hw][10][k]; v_branches [2][10][k].
 // out may alias yc or residual.
 void position_term(Context &ctx, const float *q, const float *e, const float *v_branches, int br0, int nb, int hw,

@@ -467,58 +467,67 @@ __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__res
 }
 
 // Position coefficients A = Q . W_aug (lambda.rs:131-137) written tap-major,
-// a [pixel][226][8], on the matrix cores. The general GEMM writes this 7.2 KB
-// per pixel output through a tile epilogue per 64x64 tile with K = 40 or 80,
-// which leaves it at 1.5 TB/s. Here the 226 taps (padded to 240 = 15 row
-// blocks of 16) are split in kTapParts parts of 80 (grid y); a workgroup
-// stages its part of W_aug in LDS once, and a wave computes the transposed
-// product for two pixels (16 columns = 2 pixels x 8 heads) over the part's 5
-// row blocks: register v of lane l is tap 16 blk + 4 (l / 16) + v of column
-// l % 16. The wave writes its 2 x 80 x 8 results to its own LDS rows in the
-// output's order, then stores each pixel's contiguous run with 16-byte stores.
-// K runs in float4 chunks of 16 (lane group g holds k = 16 f + 4 g + t for
-// instruction t), then k % 16 in single instructions (k = 16 NF + 4 u + g).
+// a [pixel][226][8], and optionally the content term Yc = Q . lambda_c
+// (lambda.rs:123), on the matrix cores. The general GEMM writes A, 7.2 KB per
+// pixel, through a tile epilogue per 64x64 tile with K = 40 or 80, which
+// leaves it at 1.5 TB/s. Here the 226 taps (padded to 240 = 15 row blocks of
+// 16) are split in kTapParts parts of 80 (grid y), and Yc is one more part
+// whose rows are the item's lambda_t [vd][k] (grid z: the item); a workgroup
+// stages its part's rows in LDS once, and a wave computes the transposed
+// product for two pixels (16 columns = 2 pixels x 8 heads) over the part's row
+// blocks: register v of lane l is row 16 blk + 4 (l / 16) + v of column l % 16.
+// The wave writes its results to its own LDS rows in the output's order, then
+// stores each pixel's contiguous run with 16-byte stores. K runs in float4
+// chunks of 16 (lane group g holds k = 16 f + 4 g + t for instruction t), then
+// k % 16 in single instructions (k = 16 NF + 4 u + g).
 constexpr int kTapRows = 240, kTapParts = 3, kPartRows = kTapRows / kTapParts;  // 80
 constexpr int kStageLd = kPartRows * kHeads + 8;  // one pixel's staged run (+8: the two pixels on other banks)
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 template <int NF, int TAIL>
 __global__ __launch_bounds__(256) void lambda_taps_kernel(const float *__restrict__ q,
-                                                          const float *__restrict__ w_aug_t, int64_t npx,
-                                                          float *__restrict__ a) {
+                                                          const float *__restrict__ w_aug_t,
+                                                          const float *__restrict__ lam_t, int hw,
+                                                          float *__restrict__ a, float *__restrict__ yc) {
     constexpr int K = 16 * NF + 4 * TAIL, K4 = K / 4;
     constexpr int WS = K + 4;  // LDS row stride: (K + 4) / 4 odd puts the 16 rows of a read on distinct banks
-    static_assert((WS / 4) % 2 == 1, "LDS row stride");
+    static_assert((WS / 4) % 2 == 1 && K <= kPartRows && K * kHeads <= kStageLd, "LDS layout");
     __shared__ float ws[kPartRows * WS];
     __shared__ float4 st4[4][2 * kStageLd / 4];  // per wave: two pixels' runs
-    const int part = int(blockIdx.y), r0 = part * kPartRows;
+    const int part = int(blockIdx.y), item = int(blockIdx.z);
+    const bool content = part == kTapParts;  // the Yc part
+    const int r0 = content ? 0 : part * kPartRows;
+    const int rows = content ? K : min(kPartRows, kTapsB - r0);  // valid rows of the part
+    const float4 *src4 = reinterpret_cast<const float4 *>(content ? lam_t + int64_t(item) * K * K : w_aug_t) +
+                         int64_t(r0) * K4;
     for (int i = threadIdx.x; i < kPartRows * K4; i += blockDim.x) {
         const int r = i / K4, c4 = i - r * K4;
-        const float4 v = r0 + r < kTapsB ? reinterpret_cast<const float4 *>(w_aug_t)[int64_t(r0 + r) * K4 + c4]
-                                         : make_float4(0.f, 0.f, 0.f, 0.f);
-        *reinterpret_cast<float4 *>(ws + r * WS + 4 * c4) = v;
+        *reinterpret_cast<float4 *>(ws + r * WS + 4 * c4) =
+            r < rows ? src4[int64_t(r) * K4 + c4] : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 15, g = lane >> 4, h = col & 7, pc = col >> 3;
     float *st = reinterpret_cast<float *>(st4[wave]);
-    const int run = min(kPartRows, kTapsB - r0) * kHeads;  // floats of a pixel's run in this part
-    const int64_t ntask = (npx + 1) >> 1, stride = int64_t(gridDim.x) * 4;
+    const int nblk = (rows + 15) >> 4;
+    const int run = rows * kHeads;  // floats of a pixel's run in this part
+    const int64_t px0 = int64_t(item) * hw;
+    const int ntask = (hw + 1) >> 1, stride = int(gridDim.x) * 4;
     // Q of a task's 16 (pixel, head) rows: loaded one task ahead, so the loads
     // land while the previous task computes and stores
     floatx4 bq[NF > 0 ? NF : 1];
     float bt[TAIL > 0 ? TAIL : 1];
-    auto load_q = [&](int64_t task, floatx4(&fq)[NF > 0 ? NF : 1], float(&ft)[TAIL > 0 ? TAIL : 1]) {
-        const int64_t px = 2 * task + pc;
-        const bool pv = task < ntask && px < npx;
-        const float *qr = q + (pv ? (px * kHeads + h) * K : 0);
+    auto load_q = [&](int task, floatx4(&fq)[NF > 0 ? NF : 1], float(&ft)[TAIL > 0 ? TAIL : 1]) {
+        const int p = 2 * task + pc;
+        const bool pv = task < ntask && p < hw;
+        const float *qr = q + (pv ? ((px0 + p) * kHeads + h) * K : 0);
 #pragma unroll
         for (int f = 0; f < NF; ++f)
             fq[f] = pv ? *reinterpret_cast<const floatx4 *>(qr + 16 * f + 4 * g) : floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int u = 0; u < TAIL; ++u) ft[u] = pv ? qr[16 * NF + 4 * u + g] : 0.f;
     };
-    int64_t task = int64_t(blockIdx.x) * 4 + wave;
+    int task = int(blockIdx.x) * 4 + wave;
     load_q(task, bq, bt);
     for (; task < ntask; task += stride) {
         floatx4 nq[NF > 0 ? NF : 1];
@@ -530,6 +539,7 @@ __global__ __launch_bounds__(256) void lambda_taps_kernel(const float *__restric
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
         for (int blk = 0; blk < kPartRows / 16; ++blk) {
+            if (blk >= nblk) break;
             const float *wr = ws + (blk * 16 + col) * WS;
             floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -541,18 +551,25 @@ __global__ __launch_bounds__(256) void lambda_taps_kernel(const float *__restric
 #pragma unroll
             for (int u = 0; u < TAIL; ++u)
                 acc = __builtin_amdgcn_mfma_f32_16x16x4f32(wr[16 * NF + 4 * u + g], bt[u], acc, 0, 0, 0);
+            // A: [tap][head] per pixel; Yc: [head][channel] per pixel
 #pragma unroll
-            for (int v = 0; v < 4; ++v) st[pc * kStageLd + (blk * 16 + 4 * g + v) * kHeads + h] = acc[v];
+            for (int v = 0; v < 4; ++v) {
+                const int r = blk * 16 + 4 * g + v;
+                if (!content) st[pc * kStageLd + r * kHeads + h] = acc[v];
+                else if (r < K) st[pc * kStageLd + h * K + r] = acc[v];
+            }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         const int run4 = run >> 2;
+        float *dst = content ? yc : a + r0 * kHeads;
+        const int64_t pitch = content ? int64_t(kHeads) * K : int64_t(kTapsB) * kHeads;
         for (int i = lane; i < 2 * run4; i += 64) {
             const int p = i >= run4, j = i - p * run4;
-            const int64_t pxo = 2 * task + p;
-            if (pxo < npx)
-                *reinterpret_cast<float4 *>(a + pxo * (kTapsB * kHeads) + r0 * kHeads + 4 * j) =
+            const int pp = 2 * task + p;
+            if (pp < hw)
+                *reinterpret_cast<float4 *>(dst + (px0 + pp) * pitch + 4 * j) =
                     *reinterpret_cast<const float4 *>(st + p * kStageLd + 4 * j);
         }
 #pragma unroll
@@ -864,23 +881,26 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
 
 bool lambda_taps_ok(int k) { return k == 40 || k == 80; }
 
-void lambda_taps(Context &ctx, const float *q, const float *w_aug_t, int64_t npx, int k, float *a_t) {
+void lambda_taps(Context &ctx, const float *q, const float *w_aug_t, const float *lambda_t, int nb, int hw, int k,
+                 float *a_t, float *yc) {
     MH_REQUIRE(lambda_taps_ok(k), "lambda position coefficients: k must be 40 or 80");
-    MH_REQUIRE(npx >= 0 && aligned16(q) && aligned16(w_aug_t) && aligned16(a_t),
-               "lambda position coefficients: operands must be 16-byte aligned");
-    if (npx == 0) return;
-    // LDS per workgroup: its part of W_aug (80 rows of k + 4) and 4 waves' staging.
+    MH_REQUIRE(nb >= 0 && hw >= 0 && aligned16(q) && aligned16(w_aug_t) && aligned16(a_t) && aligned16(lambda_t) &&
+                   aligned16(yc) && (lambda_t == nullptr) == (yc == nullptr),
+               "lambda position coefficients: operands must be 16-byte aligned, lambda_t and yc given together");
+    if (nb == 0 || hw == 0) return;
+    // LDS per workgroup: its part's rows (80 of k + 4) and 4 waves' staging.
     const size_t lds = size_t(kPartRows) * (k + 4) * sizeof(float) + size_t(4) * 2 * kStageLd * sizeof(float);
-    const int64_t tasks = (npx + 1) / 2;
+    const int parts = kTapParts + (lambda_t ? 1 : 0);
+    const int64_t tasks = (hw + 1) / 2;
     // Workgroups of 4 waves, at most as many as fit on the chip at once, each
-    // wave looping over pixel pairs.
+    // wave looping over its item's pixel pairs.
     const int per_cu = int(std::max<size_t>(1, (160 * 1024) / lds));
-    const int64_t cap = std::max<int64_t>(1, int64_t(ctx.cu_count) * per_cu / kTapParts);
-    const dim3 grid(unsigned(std::min<int64_t>(ceil_div(tasks, 4), cap)), kTapParts);
+    const int64_t cap = std::max<int64_t>(1, int64_t(ctx.cu_count) * per_cu / (parts * nb));
+    const dim3 grid(unsigned(std::min<int64_t>(ceil_div(tasks, 4), cap)), unsigned(parts), unsigned(nb));
     if (k == 40)
-        lambda_taps_kernel<2, 2><<<grid, 256, 0, ctx.stream>>>(q, w_aug_t, npx, a_t);
+        lambda_taps_kernel<2, 2><<<grid, 256, 0, ctx.stream>>>(q, w_aug_t, lambda_t, hw, a_t, yc);
     else
-        lambda_taps_kernel<5, 0><<<grid, 256, 0, ctx.stream>>>(q, w_aug_t, npx, a_t);
+        lambda_taps_kernel<5, 0><<<grid, 256, 0, ctx.stream>>>(q, w_aug_t, lambda_t, hw, a_t, yc);
     MH_LAUNCH_CHECK();
 }
 

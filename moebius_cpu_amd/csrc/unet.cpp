@@ -499,20 +499,21 @@ struct SelfLambda {
         softmax_lambda(e.ctx, kt.p, vt.p, x.n, hw, k, k, lam_t);
         e.pool.recycle(kt);
         DT yc = e.pool.tensor(x.n, x.h, x.w, c);
-        // Yc = Q . lambda_c per item, Q viewed as [(hw*8) x k].
-        gemm_nt(e.ctx, q.p, k, int64_t(hw) * c, lam_t, kF32, k, int64_t(k) * k, hw * HEADS, k, k, x.n, nullptr,
-                nullptr, yc.p, k, int64_t(hw) * c);
-        e.pool.recycle(lam_t);
-        // A = Q . W_aug over every pixel and head of the batch, stored [pixel][tap][head]:
-        // EXACT by the dedicated kernel at k = 40 / 80 (64x64 x 40 at batch 2: 34.5 -> 21.2 us,
-        // 32x32 x 80: 14.0 -> 10.5 us; whole step 7.66 -> 7.60 ms), else (FAST, whose GEMMs
-        // take f16 products, and k = 160) the general GEMM.
+        // A = Q . W_aug over every pixel and head of the batch, stored [pixel][tap][head],
+        // and Yc = Q . lambda_c per item (Q viewed as [(hw*8) x k]): EXACT at k = 40 / 80
+        // both by one dedicated kernel (64x64 x 40, batch 2: 25.4 us for both against
+        // 34.5 + 12 us for the two GEMMs; whole step 7.60 -> 7.50 ms), else (FAST, whose
+        // GEMMs take f16 products, and k = 160) two general GEMMs.
         float *a = e.pool.floats(x.px() * HEADS * TAPS_B);
-        if (e.ctx.precision == Precision::Exact && e.ctx.tune.lambda_taps && lambda_taps_ok(k))
-            lambda_taps(e.ctx, q.p, w_aug_t, x.px(), k, a);
-        else
+        if (e.ctx.precision == Precision::Exact && e.ctx.tune.lambda_taps && lambda_taps_ok(k)) {
+            lambda_taps(e.ctx, q.p, w_aug_t, lam_t, x.n, hw, k, a, yc.p);
+        } else {
+            gemm_nt(e.ctx, q.p, k, int64_t(hw) * c, lam_t, kF32, k, int64_t(k) * k, hw * HEADS, k, k, x.n, nullptr,
+                    nullptr, yc.p, k, int64_t(hw) * c);
             gemm_nt(e.ctx, q.p, k, 0, w_aug_t, kF32, k, 0, int(x.px() * HEADS), TAPS_B, k, 1, nullptr, nullptr, a,
                     int64_t(TAPS_B) * HEADS, 0, GemmEpilogue::None, HEADS);
+        }
+        e.pool.recycle(lam_t);
         tap_filter(e.ctx, a, vt.p, yc.p, h, h, x.n, x.h, x.w, k, lno);
         e.pool.recycle(a);
         e.pool.recycle(yc);

@@ -77,30 +77,47 @@ def test_tap_filter_kernel_bit_exact(ctx, nb, hh, ww, vd, heads_per_thread, tune
 
 
 # Position coefficients A = Q . W_aug (lambda.rs:131-137) by the matrix-core
-# kernel, tap-major: against the f64 product and against the general GEMM's
-# row-grouped output of the same product; odd pixel counts leave a half pair.
-@pytest.mark.parametrize("npx,k", [(8192, 40), (2048, 80), (7, 40), (1, 80), (301, 80)])
-def test_lambda_position_coeffs_kernel(ctx, npx, k):
-    rng = np.random.default_rng(npx + k)
+# kernel, tap-major, and with lambda_t the content term Yc = Q . lambda_c per
+# item (lambda.rs:123): against the f64 products and against the general
+# GEMM's outputs of the same products; odd pixel counts leave a half pair.
+@pytest.mark.parametrize("nb,hw,k", [(2, 4096, 40), (2, 1024, 80), (1, 7, 40), (3, 1, 80), (2, 301, 80)])
+@pytest.mark.parametrize("content", [False, True])
+def test_lambda_position_coeffs_kernel(ctx, nb, hw, k, content):
+    rng = np.random.default_rng(nb * hw + k)
+    npx = nb * hw
     q = rng.standard_normal((npx, 8, k)).astype(np.float32)
     w = rng.standard_normal((226, k)).astype(np.float32)
-    want = (q.reshape(npx * 8, k).astype(np.float64) @ w.astype(np.float64).T).reshape(npx, 8, 226)
-    want = want.transpose(0, 2, 1)
-    qd, wd = D(ctx, q), D(ctx, w)
+    lam_t = rng.standard_normal((nb, k, k)).astype(np.float32)  # [item][j][kk]
+    q64 = q.reshape(npx * 8, k).astype(np.float64)
+    want = (q64 @ w.astype(np.float64).T).reshape(npx, 8, 226).transpose(0, 2, 1)
+    qd, wd, ld = D(ctx, q), D(ctx, w), D(ctx, lam_t)
     out = E.DeviceArray(ctx, (npx, 226, 8))
-    E.check(E.lib().mh_lambda_position_coeffs(ctx.h, qd.ptr, wd.ptr, npx, k, out.ptr))
+    yc = E.DeviceArray(ctx, (npx, 8, k)) if content else None
+    E.check(E.lib().mh_lambda_position_coeffs(ctx.h, qd.ptr, wd.ptr, ld.ptr if content else None, nb, hw, k, out.ptr,
+                                              yc.ptr if content else None))
     got = out.numpy()
     assert max_abs_rel(got, want) < 1e-5
     g = E.DeviceArray(ctx, (npx, 226, 8))
     E.check(E.lib().mh_gemm_nt(ctx.h, qd.ptr, k, wd.ptr, 0, k, npx * 8, 226, k, None, None, g.ptr, 226 * 8, 8))
     assert max_abs_rel(got, g.numpy()) < 1e-5
+    if content:
+        qi = q.reshape(nb, hw * 8, k).astype(np.float64)
+        want_yc = np.stack([qi[b] @ lam_t[b].astype(np.float64).T for b in range(nb)]).reshape(npx, 8, k)
+        got_yc = yc.numpy()
+        assert max_abs_rel(got_yc, want_yc) < 1e-5
+        gy = E.DeviceArray(ctx, (npx, 8, k))
+        E.check(E.lib().mh_gemm_nt(ctx.h, qd.ptr, k, ld.ptr, 0, k, hw * 8, k, k, None, None, gy.ptr, k, 0))
+        if nb == 1:
+            assert max_abs_rel(got_yc, gy.numpy()) < 1e-5
 
 
-def test_lambda_position_coeffs_rejects_other_widths(ctx):
+def test_lambda_position_coeffs_rejects_bad_arguments(ctx):
     q = E.DeviceArray(ctx, (2, 8, 160))
     w = E.DeviceArray(ctx, (226, 160))
     out = E.DeviceArray(ctx, (2, 226, 8))
-    assert E.lib().mh_lambda_position_coeffs(ctx.h, q.ptr, w.ptr, 2, 160, out.ptr) != 0
+    assert E.lib().mh_lambda_position_coeffs(ctx.h, q.ptr, w.ptr, None, 1, 2, 160, out.ptr, None) != 0
+    # lambda_t without yc
+    assert E.lib().mh_lambda_position_coeffs(ctx.h, q.ptr, w.ptr, w.ptr, 1, 2, 40, out.ptr, None) != 0
 
 
 @pytest.mark.parametrize("br0,nb,k", [(0, 2, 40), (1, 1, 80), (0, 2, 160)])

@@ -479,12 +479,30 @@ __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__res
 // The wave writes its results to its own LDS rows in the output's order, then
 // stores each pixel's contiguous run with 16-byte stores. K runs in float4
 // chunks of 16 (lane group g holds k = 16 f + 4 g + t for instruction t), then
-// k % 16 in single instructions (k = 16 NF + 4 u + g).
+// k % 16 in single instructions (k = 16 NF + 4 u + g). R16 (the FAST
+// precision): every operand is rounded to f16 (nearest even, saturating at
+// +-65504) as it is loaded, so the products are those of f16 operands, summed in
+// f32 as the f16 GEMM does.
 constexpr int kTapRows = 240, kTapParts = 3, kPartRows = kTapRows / kTapParts;  // 80
 constexpr int kStageLd = kPartRows * kHeads + 8;  // one pixel's staged run (+8: the two pixels on other banks)
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-template <int NF, int TAIL>
+template <bool R16>
+__device__ __forceinline__ float op_round(float v) {
+    if constexpr (R16) {
+        const float x = __builtin_fabsf(v) > 65504.0f ? __builtin_copysignf(65504.0f, v) : v;
+        return float(static_cast<_Float16>(x));
+    } else {
+        return v;
+    }
+}
+
+template <bool R16>
+__device__ __forceinline__ float4 op_round4(float4 v) {
+    return make_float4(op_round<R16>(v.x), op_round<R16>(v.y), op_round<R16>(v.z), op_round<R16>(v.w));
+}
+
+template <int NF, int TAIL, bool R16>
 __global__ __launch_bounds__(256) void lambda_taps_kernel(const float *__restrict__ q,
                                                           const float *__restrict__ w_aug_t,
                                                           const float *__restrict__ lam_t, int hw,
@@ -503,7 +521,7 @@ __global__ __launch_bounds__(256) void lambda_taps_kernel(const float *__restric
     for (int i = threadIdx.x; i < kPartRows * K4; i += blockDim.x) {
         const int r = i / K4, c4 = i - r * K4;
         *reinterpret_cast<float4 *>(ws + r * WS + 4 * c4) =
-            r < rows ? src4[int64_t(r) * K4 + c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+            r < rows ? op_round4<R16>(src4[int64_t(r) * K4 + c4]) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     __syncthreads();
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -522,10 +540,13 @@ __global__ __launch_bounds__(256) void lambda_taps_kernel(const float *__restric
         const bool pv = task < ntask && p < hw;
         const float *qr = q + (pv ? ((px0 + p) * kHeads + h) * K : 0);
 #pragma unroll
-        for (int f = 0; f < NF; ++f)
+        for (int f = 0; f < NF; ++f) {
             fq[f] = pv ? *reinterpret_cast<const floatx4 *>(qr + 16 * f + 4 * g) : floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int u = 0; u < TAIL; ++u) ft[u] = pv ? qr[16 * NF + 4 * u + g] : 0.f;
+            for (int t = 0; t < 4; ++t) fq[f][t] = op_round<R16>(fq[f][t]);
+        }
+#pragma unroll
+        for (int u = 0; u < TAIL; ++u) ft[u] = pv ? op_round<R16>(qr[16 * NF + 4 * u + g]) : 0.f;
     };
     int task = int(blockIdx.x) * 4 + wave;
     load_q(task, bq, bt);
@@ -897,10 +918,11 @@ void lambda_taps(Context &ctx, const float *q, const float *w_aug_t, const float
     const int per_cu = int(std::max<size_t>(1, (160 * 1024) / lds));
     const int64_t cap = std::max<int64_t>(1, int64_t(ctx.cu_count) * per_cu / (parts * nb));
     const dim3 grid(unsigned(std::min<int64_t>(ceil_div(tasks, 4), cap)), unsigned(parts), unsigned(nb));
-    if (k == 40)
-        lambda_taps_kernel<2, 2><<<grid, 256, 0, ctx.stream>>>(q, w_aug_t, lambda_t, hw, a_t, yc);
-    else
-        lambda_taps_kernel<5, 0><<<grid, 256, 0, ctx.stream>>>(q, w_aug_t, lambda_t, hw, a_t, yc);
+    // FAST contexts take the products of f16-rounded operands, as their GEMMs do.
+    auto go = [&](auto kern) { kern<<<grid, 256, 0, ctx.stream>>>(q, w_aug_t, lambda_t, hw, a_t, yc); };
+    const bool r16 = ctx.precision == Precision::Fast;
+    if (k == 40) r16 ? go(lambda_taps_kernel<2, 2, true>) : go(lambda_taps_kernel<2, 2, false>);
+    else r16 ? go(lambda_taps_kernel<5, 0, true>) : go(lambda_taps_kernel<5, 0, false>);
     MH_LAUNCH_CHECK();
 }
 

@@ -111,6 +111,36 @@ def test_lambda_position_coeffs_kernel(ctx, nb, hw, k, content):
             assert max_abs_rel(got_yc, gy.numpy()) < 1e-5
 
 
+def _h16(a):
+    return np.clip(a, -65504, 65504).astype(np.float16).astype(np.float64)
+
+
+# FAST contexts: the products of f16-rounded operands (as the FAST GEMMs take
+# them), summed in f32: against the f64 sums of the same products and against
+# the FAST GEMM's output.
+@pytest.mark.parametrize("nb,hw,k", [(2, 4096, 40), (2, 1024, 80), (1, 7, 40)])
+def test_lambda_position_coeffs_fast(ctx, nb, hw, k):
+    rng = np.random.default_rng(7 * hw + k)
+    npx = nb * hw
+    q = rng.standard_normal((npx, 8, k)).astype(np.float32)
+    w = rng.standard_normal((226, k)).astype(np.float32)
+    lam_t = rng.standard_normal((nb, k, k)).astype(np.float32)
+    want = (_h16(q.reshape(npx * 8, k)) @ _h16(w).T).reshape(npx, 8, 226).transpose(0, 2, 1)
+    qi = _h16(q.reshape(nb, hw * 8, k))
+    want_yc = np.stack([qi[b] @ _h16(lam_t[b]).T for b in range(nb)]).reshape(npx, 8, k)
+    qd, wd, ld = D(ctx, q), D(ctx, w), D(ctx, lam_t)
+    out, yc, g = E.DeviceArray(ctx, (npx, 226, 8)), E.DeviceArray(ctx, (npx, 8, k)), E.DeviceArray(ctx, (npx, 226, 8))
+    ctx.set_precision(True)
+    try:
+        E.check(E.lib().mh_lambda_position_coeffs(ctx.h, qd.ptr, wd.ptr, ld.ptr, nb, hw, k, out.ptr, yc.ptr))
+        E.check(E.lib().mh_gemm_nt(ctx.h, qd.ptr, k, wd.ptr, 0, k, npx * 8, 226, k, None, None, g.ptr, 226 * 8, 8))
+    finally:
+        ctx.set_precision(False)
+    assert max_abs_rel(out.numpy(), want) < 1e-5
+    assert max_abs_rel(yc.numpy(), want_yc) < 1e-5
+    assert max_abs_rel(out.numpy(), g.numpy()) < 1e-5
+
+
 def test_lambda_position_coeffs_rejects_bad_arguments(ctx):
     q = E.DeviceArray(ctx, (2, 8, 160))
     w = E.DeviceArray(ctx, (226, 160))

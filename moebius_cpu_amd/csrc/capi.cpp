@@ -600,11 +600,11 @@ int32_t mh_lambda_position_coeffs(MhContext *ctx, const float *q, const float *w
     return guard([&] {
         mh::Context &c = C(ctx);
         need(q, "q");
-        need(w_aug_t, "w_aug_t");
-        need(a_t, "a_t");
         if (!mh::lambda_taps_ok(int(k))) mh::fail(mh::kInvalidArgument, "lambda position coefficients: k must be 40 or 80");
-        if ((lambda_t == nullptr) != (yc == nullptr))
-            mh::fail(mh::kInvalidArgument, "lambda position coefficients: lambda_t and yc go together");
+        if ((lambda_t == nullptr) != (yc == nullptr) || (w_aug_t == nullptr) != (a_t == nullptr) ||
+            (!w_aug_t && !lambda_t))
+            mh::fail(mh::kInvalidArgument,
+                     "lambda position coefficients: w_aug_t with a_t, lambda_t with yc, at least one pair");
         mh::lambda_taps(c, q, w_aug_t, lambda_t, dim(nb, "nb"), dim(hw, "hw"), int(k), a_t, yc);
     });
 }

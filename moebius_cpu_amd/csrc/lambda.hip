@@ -506,13 +506,13 @@ template <int NF, int TAIL, bool R16>
 __global__ __launch_bounds__(256) void lambda_taps_kernel(const float *__restrict__ q,
                                                           const float *__restrict__ w_aug_t,
                                                           const float *__restrict__ lam_t, int hw,
-                                                          float *__restrict__ a, float *__restrict__ yc) {
+                                                          float *__restrict__ a, float *__restrict__ yc, int part0) {
     constexpr int K = 16 * NF + 4 * TAIL, K4 = K / 4;
     constexpr int WS = K + 4;  // LDS row stride: (K + 4) / 4 odd puts the 16 rows of a read on distinct banks
     static_assert((WS / 4) % 2 == 1 && K <= kPartRows && K * kHeads <= kStageLd, "LDS layout");
     __shared__ float ws[kPartRows * WS];
     __shared__ float4 st4[4][2 * kStageLd / 4];  // per wave: two pixels' runs
-    const int part = int(blockIdx.y), item = int(blockIdx.z);
+    const int part = int(blockIdx.y) + part0, item = int(blockIdx.z);
     const bool content = part == kTapParts;  // the Yc part
     const int r0 = content ? 0 : part * kPartRows;
     const int rows = content ? K : min(kPartRows, kTapsB - r0);  // valid rows of the part
@@ -906,12 +906,14 @@ void lambda_taps(Context &ctx, const float *q, const float *w_aug_t, const float
                  float *a_t, float *yc) {
     MH_REQUIRE(lambda_taps_ok(k), "lambda position coefficients: k must be 40 or 80");
     MH_REQUIRE(nb >= 0 && hw >= 0 && aligned16(q) && aligned16(w_aug_t) && aligned16(a_t) && aligned16(lambda_t) &&
-                   aligned16(yc) && (lambda_t == nullptr) == (yc == nullptr),
-               "lambda position coefficients: operands must be 16-byte aligned, lambda_t and yc given together");
+                   aligned16(yc) && (lambda_t == nullptr) == (yc == nullptr) &&
+                   (w_aug_t == nullptr) == (a_t == nullptr) && (w_aug_t || lambda_t),
+               "lambda position coefficients: operands 16-byte aligned; w_aug_t with a_t, lambda_t with yc");
     if (nb == 0 || hw == 0) return;
     // LDS per workgroup: its part's rows (80 of k + 4) and 4 waves' staging.
     const size_t lds = size_t(kPartRows) * (k + 4) * sizeof(float) + size_t(4) * 2 * kStageLd * sizeof(float);
-    const int parts = kTapParts + (lambda_t ? 1 : 0);
+    const int part0 = w_aug_t ? 0 : kTapParts;  // no w_aug_t: the content part alone
+    const int parts = (w_aug_t ? kTapParts : 0) + (lambda_t ? 1 : 0);
     const int64_t tasks = (hw + 1) / 2;
     // Workgroups of 4 waves, at most as many as fit on the chip at once, each
     // wave looping over its item's pixel pairs.
@@ -919,7 +921,7 @@ void lambda_taps(Context &ctx, const float *q, const float *w_aug_t, const float
     const int64_t cap = std::max<int64_t>(1, int64_t(ctx.cu_count) * per_cu / (parts * nb));
     const dim3 grid(unsigned(std::min<int64_t>(ceil_div(tasks, 4), cap)), unsigned(parts), unsigned(nb));
     // FAST contexts take the products of f16-rounded operands, as their GEMMs do.
-    auto go = [&](auto kern) { kern<<<grid, 256, 0, ctx.stream>>>(q, w_aug_t, lambda_t, hw, a_t, yc); };
+    auto go = [&](auto kern) { kern<<<grid, 256, 0, ctx.stream>>>(q, w_aug_t, lambda_t, hw, a_t, yc, part0); };
     const bool r16 = ctx.precision == Precision::Fast;
     if (k == 40) r16 ? go(lambda_taps_kernel<2, 2, true>) : go(lambda_taps_kernel<2, 2, false>);
     else r16 ? go(lambda_taps_kernel<5, 0, true>) : go(lambda_taps_kernel<5, 0, false>);

@@ -111,6 +111,23 @@ def test_lambda_position_coeffs_kernel(ctx, nb, hw, k, content):
             assert max_abs_rel(got_yc, gy.numpy()) < 1e-5
 
 
+# The content term alone (the cross-lambda's Yc = Q . lambda_c[branch], item b
+# on branch br0 + b): lambda_t points at the first item's branch.
+@pytest.mark.parametrize("br0,nb,hw,k", [(0, 2, 4096, 40), (1, 1, 1024, 80), (0, 2, 37, 40)])
+def test_lambda_content_term_alone(ctx, br0, nb, hw, k):
+    rng = np.random.default_rng(br0 + hw + k)
+    npx = nb * hw
+    q = rng.standard_normal((npx, 8, k)).astype(np.float32)
+    lam_t = rng.standard_normal((2, k, k)).astype(np.float32)
+    qd, ld = D(ctx, q), D(ctx, lam_t)
+    yc = E.DeviceArray(ctx, (npx, 8, k))
+    first = ctypes.c_void_p(ld.ptr + br0 * k * k * 4)
+    E.check(E.lib().mh_lambda_position_coeffs(ctx.h, qd.ptr, None, first, nb, hw, k, None, yc.ptr))
+    qi = q.reshape(nb, hw * 8, k).astype(np.float64)
+    want = np.stack([qi[b] @ lam_t[br0 + b].astype(np.float64).T for b in range(nb)]).reshape(npx, 8, k)
+    assert max_abs_rel(yc.numpy(), want) < 1e-5
+
+
 def _h16(a):
     return np.clip(a, -65504, 65504).astype(np.float16).astype(np.float64)
 

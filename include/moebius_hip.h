@@ -316,7 +316,7 @@ int32_t mh_tap_filter(MhContext *ctx, const float *a_t, const float *v, const fl
  * (lambda.rs:123), yc [nb*hw][8][k]; lambda_t and yc are both NULL or both
  * given, and so are w_aug_t and a_t (both NULL: yc alone, as the cross-lambda's
  * content term Q . lambda_c[branch] with lambda_t pointing at the first item's
- * branch). k must be 40 or 80 (the UNet's 64x64 and 32x32 levels); f32 products
+ * branch). k must be 40, 80 or 160 (the UNet's three levels); f32 products
  * on the matrix cores, summed in f32. */
 int32_t mh_lambda_position_coeffs(MhContext *ctx, const float *q, const float *w_aug_t, const float *lambda_t,
                                   uint32_t nb, uint32_t hw, uint32_t k, float *a_t, float *yc);

@@ -600,7 +600,7 @@ int32_t mh_lambda_position_coeffs(MhContext *ctx, const float *q, const float *w
     return guard([&] {
         mh::Context &c = C(ctx);
         need(q, "q");
-        if (!mh::lambda_taps_ok(int(k))) mh::fail(mh::kInvalidArgument, "lambda position coefficients: k must be 40 or 80");
+        if (!mh::lambda_taps_ok(int(k))) mh::fail(mh::kInvalidArgument, "lambda position coefficients: k must be 40, 80 or 160");
         if ((lambda_t == nullptr) != (yc == nullptr) || (w_aug_t == nullptr) != (a_t == nullptr) ||
             (!w_aug_t && !lambda_t))
             mh::fail(mh::kInvalidArgument,

@@ -183,7 +183,7 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
 // q [nb*hw][8][k] (pixel, head rows of k), w_aug_t [226][k] -> a_t [nb*hw][226][8], the
 // tap-major layout tap_filter reads; with lambda_t [nb][k][k] (softmax_lambda's
 // transposed lambda_c) also the content term yc [nb*hw][8][k] = Q . lambda_c per item
-// (lambda.rs:123); w_aug_t and a_t null: yc alone. k must pass lambda_taps_ok (40 or 80).
+// (lambda.rs:123); w_aug_t and a_t null: yc alone. k must pass lambda_taps_ok (40, 80, 160).
 bool lambda_taps_ok(int k);
 void lambda_taps(Context &ctx, const float *q, const float *w_aug_t, const float *lambda_t, int nb, int hw, int k,
                  float *a_t, float *yc);

@@ -509,13 +509,14 @@ __global__ __launch_bounds__(256) void lambda_taps_kernel(const float *__restric
                                                           float *__restrict__ a, float *__restrict__ yc, int part0) {
     constexpr int K = 16 * NF + 4 * TAIL, K4 = K / 4;
     constexpr int WS = K + 4;  // LDS row stride: (K + 4) / 4 odd puts the 16 rows of a read on distinct banks
-    static_assert((WS / 4) % 2 == 1 && K <= kPartRows && K * kHeads <= kStageLd, "LDS layout");
+    static_assert((WS / 4) % 2 == 1 && K % kPartRows % 4 == 0, "LDS layout");
     __shared__ float ws[kPartRows * WS];
     __shared__ float4 st4[4][2 * kStageLd / 4];  // per wave: two pixels' runs
     const int part = int(blockIdx.y) + part0, item = int(blockIdx.z);
-    const bool content = part == kTapParts;  // the Yc part
-    const int r0 = content ? 0 : part * kPartRows;
-    const int rows = content ? K : min(kPartRows, kTapsB - r0);  // valid rows of the part
+    // parts past the taps: Yc, lambda_t's rows (value channels j) 80 at a time
+    const bool content = part >= kTapParts;
+    const int r0 = (content ? part - kTapParts : part) * kPartRows;
+    const int rows = min(kPartRows, (content ? K : kTapsB) - r0);  // valid rows of the part
     const float4 *src4 = reinterpret_cast<const float4 *>(content ? lam_t + int64_t(item) * K * K : w_aug_t) +
                          int64_t(r0) * K4;
     for (int i = threadIdx.x; i < kPartRows * K4; i += blockDim.x) {
@@ -577,20 +578,23 @@ __global__ __launch_bounds__(256) void lambda_taps_kernel(const float *__restric
             for (int v = 0; v < 4; ++v) {
                 const int r = blk * 16 + 4 * g + v;
                 if (!content) st[pc * kStageLd + r * kHeads + h] = acc[v];
-                else if (r < K) st[pc * kStageLd + h * K + r] = acc[v];
+                else if (r < rows) st[pc * kStageLd + h * rows + r] = acc[v];
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const int run4 = run >> 2;
-        float *dst = content ? yc : a + r0 * kHeads;
+        // A: one run of the pixel's row per part; Yc: eight runs (one per head) of
+        // the part's rows values at channel r0
+        const int run4 = run >> 2, seg4 = content ? rows >> 2 : run4;
+        float *dst = content ? yc + r0 : a + r0 * kHeads;
         const int64_t pitch = content ? int64_t(kHeads) * K : int64_t(kTapsB) * kHeads;
         for (int i = lane; i < 2 * run4; i += 64) {
             const int p = i >= run4, j = i - p * run4;
+            const int hh = j / seg4, j4 = j - hh * seg4;
             const int pp = 2 * task + p;
             if (pp < hw)
-                *reinterpret_cast<float4 *>(dst + (px0 + pp) * pitch + 4 * j) =
+                *reinterpret_cast<float4 *>(dst + (px0 + pp) * pitch + hh * K + 4 * j4) =
                     *reinterpret_cast<const float4 *>(st + p * kStageLd + 4 * j);
         }
 #pragma unroll
@@ -900,11 +904,11 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
     MH_LAUNCH_CHECK();
 }
 
-bool lambda_taps_ok(int k) { return k == 40 || k == 80; }
+bool lambda_taps_ok(int k) { return k == 40 || k == 80 || k == 160; }
 
 void lambda_taps(Context &ctx, const float *q, const float *w_aug_t, const float *lambda_t, int nb, int hw, int k,
                  float *a_t, float *yc) {
-    MH_REQUIRE(lambda_taps_ok(k), "lambda position coefficients: k must be 40 or 80");
+    MH_REQUIRE(lambda_taps_ok(k), "lambda position coefficients: k must be 40, 80 or 160");
     MH_REQUIRE(nb >= 0 && hw >= 0 && aligned16(q) && aligned16(w_aug_t) && aligned16(a_t) && aligned16(lambda_t) &&
                    aligned16(yc) && (lambda_t == nullptr) == (yc == nullptr) &&
                    (w_aug_t == nullptr) == (a_t == nullptr) && (w_aug_t || lambda_t),
@@ -913,7 +917,7 @@ void lambda_taps(Context &ctx, const float *q, const float *w_aug_t, const float
     // LDS per workgroup: its part's rows (80 of k + 4) and 4 waves' staging.
     const size_t lds = size_t(kPartRows) * (k + 4) * sizeof(float) + size_t(4) * 2 * kStageLd * sizeof(float);
     const int part0 = w_aug_t ? 0 : kTapParts;  // no w_aug_t: the content part alone
-    const int parts = (w_aug_t ? kTapParts : 0) + (lambda_t ? 1 : 0);
+    const int parts = (w_aug_t ? kTapParts : 0) + (lambda_t ? int(ceil_div(k, kPartRows)) : 0);
     const int64_t tasks = (hw + 1) / 2;
     // Workgroups of 4 waves, at most as many as fit on the chip at once, each
     // wave looping over its item's pixel pairs.
@@ -924,7 +928,8 @@ void lambda_taps(Context &ctx, const float *q, const float *w_aug_t, const float
     auto go = [&](auto kern) { kern<<<grid, 256, 0, ctx.stream>>>(q, w_aug_t, lambda_t, hw, a_t, yc, part0); };
     const bool r16 = ctx.precision == Precision::Fast;
     if (k == 40) r16 ? go(lambda_taps_kernel<2, 2, true>) : go(lambda_taps_kernel<2, 2, false>);
-    else r16 ? go(lambda_taps_kernel<5, 0, true>) : go(lambda_taps_kernel<5, 0, false>);
+    else if (k == 80) r16 ? go(lambda_taps_kernel<5, 0, true>) : go(lambda_taps_kernel<5, 0, false>);
+    else r16 ? go(lambda_taps_kernel<10, 0, true>) : go(lambda_taps_kernel<10, 0, false>);
     MH_LAUNCH_CHECK();
 }
 

@@ -500,10 +500,10 @@ struct SelfLambda {
         e.pool.recycle(kt);
         DT yc = e.pool.tensor(x.n, x.h, x.w, c);
         // A = Q . W_aug over every pixel and head of the batch, stored [pixel][tap][head],
-        // and Yc = Q . lambda_c per item (Q viewed as [(hw*8) x k]): at k = 40 / 80 both
-        // by one dedicated kernel (64x64 x 40, batch 2: 25.4 us for both against 34.5 + 12
-        // us for the two GEMMs; whole EXACT step 7.60 -> 7.50 ms; in FAST on f16-rounded
-        // operands, as the FAST GEMMs take them), else (k = 160) two general GEMMs.
+        // and Yc = Q . lambda_c per item (Q viewed as [(hw*8) x k]), both by one dedicated
+        // kernel (64x64 x 40, batch 2: 25.4 us for both against 34.5 + 12 us for the two
+        // GEMMs; whole EXACT step 7.60 -> 7.50 ms; in FAST on f16-rounded operands, as the
+        // FAST GEMMs take them), or (the lambda_taps tuning off) two general GEMMs.
         float *a = e.pool.floats(x.px() * HEADS * TAPS_B);
         if (e.ctx.tune.lambda_taps && lambda_taps_ok(k)) {
             lambda_taps(e.ctx, q.p, w_aug_t, lam_t, x.n, hw, k, a, yc.p);

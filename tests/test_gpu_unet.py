@@ -80,7 +80,8 @@ def test_tap_filter_kernel_bit_exact(ctx, nb, hh, ww, vd, heads_per_thread, tune
 # kernel, tap-major, and with lambda_t the content term Yc = Q . lambda_c per
 # item (lambda.rs:123): against the f64 products and against the general
 # GEMM's outputs of the same products; odd pixel counts leave a half pair.
-@pytest.mark.parametrize("nb,hw,k", [(2, 4096, 40), (2, 1024, 80), (1, 7, 40), (3, 1, 80), (2, 301, 80)])
+@pytest.mark.parametrize("nb,hw,k", [(2, 4096, 40), (2, 1024, 80), (2, 256, 160), (1, 7, 40), (3, 1, 80),
+                                     (2, 301, 80), (1, 9, 160)])
 @pytest.mark.parametrize("content", [False, True])
 def test_lambda_position_coeffs_kernel(ctx, nb, hw, k, content):
     rng = np.random.default_rng(nb * hw + k)
@@ -113,7 +114,7 @@ def test_lambda_position_coeffs_kernel(ctx, nb, hw, k, content):
 
 # The content term alone (the cross-lambda's Yc = Q . lambda_c[branch], item b
 # on branch br0 + b): lambda_t points at the first item's branch.
-@pytest.mark.parametrize("br0,nb,hw,k", [(0, 2, 4096, 40), (1, 1, 1024, 80), (0, 2, 37, 40)])
+@pytest.mark.parametrize("br0,nb,hw,k", [(0, 2, 4096, 40), (1, 1, 1024, 80), (0, 2, 256, 160), (0, 2, 37, 40)])
 def test_lambda_content_term_alone(ctx, br0, nb, hw, k):
     rng = np.random.default_rng(br0 + hw + k)
     npx = nb * hw
@@ -135,7 +136,7 @@ def _h16(a):
 # FAST contexts: the products of f16-rounded operands (as the FAST GEMMs take
 # them), summed in f32: against the f64 sums of the same products and against
 # the FAST GEMM's output.
-@pytest.mark.parametrize("nb,hw,k", [(2, 4096, 40), (2, 1024, 80), (1, 7, 40)])
+@pytest.mark.parametrize("nb,hw,k", [(2, 4096, 40), (2, 1024, 80), (2, 256, 160), (1, 7, 40)])
 def test_lambda_position_coeffs_fast(ctx, nb, hw, k):
     rng = np.random.default_rng(7 * hw + k)
     npx = nb * hw
@@ -159,10 +160,10 @@ def test_lambda_position_coeffs_fast(ctx, nb, hw, k):
 
 
 def test_lambda_position_coeffs_rejects_bad_arguments(ctx):
-    q = E.DeviceArray(ctx, (2, 8, 160))
-    w = E.DeviceArray(ctx, (226, 160))
+    q = E.DeviceArray(ctx, (2, 8, 120))
+    w = E.DeviceArray(ctx, (226, 120))
     out = E.DeviceArray(ctx, (2, 226, 8))
-    assert E.lib().mh_lambda_position_coeffs(ctx.h, q.ptr, w.ptr, None, 1, 2, 160, out.ptr, None) != 0
+    assert E.lib().mh_lambda_position_coeffs(ctx.h, q.ptr, w.ptr, None, 1, 2, 120, out.ptr, None) != 0
     # lambda_t without yc
     assert E.lib().mh_lambda_position_coeffs(ctx.h, q.ptr, w.ptr, w.ptr, 1, 2, 40, out.ptr, None) != 0
 

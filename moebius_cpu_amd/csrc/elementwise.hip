@@ -59,6 +59,14 @@ __global__ void silu_kernel(float *__restrict__ x, int64_t len) {
         x[e] = ref_silu(x[e]);
 }
 
+// dst [n][item] = SiLU(src [item]) for every copy.
+__global__ void silu_tile_kernel(const float *__restrict__ src, int64_t item, int n, float *__restrict__ dst) {
+    for (int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; e < item; e += int64_t(gridDim.x) * blockDim.x) {
+        const float v = ref_silu(src[e]);
+        for (int i = 0; i < n; ++i) dst[int64_t(i) * item + e] = v;
+    }
+}
+
 __global__ void add_kernel(float *__restrict__ a, const float *__restrict__ b, int64_t len) {
     for (int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; e < len; e += int64_t(gridDim.x) * blockDim.x)
         a[e] = a[e] + b[e];
@@ -152,6 +160,12 @@ void bias_residual_add(Context &ctx, const float *x, int64_t rows, int cols, con
 void silu_inplace(Context &ctx, float *x, int64_t len) {
     if (len == 0) return;
     silu_kernel<<<grid_for(len), 256, 0, ctx.stream>>>(x, len);
+    MH_LAUNCH_CHECK();
+}
+
+void silu_tile(Context &ctx, const float *src, int64_t item, int n, float *dst) {
+    if (item == 0 || n == 0) return;
+    silu_tile_kernel<<<grid_for(item), 256, 0, ctx.stream>>>(src, item, n, dst);
     MH_LAUNCH_CHECK();
 }
 

@@ -28,6 +28,8 @@ struct Affine {
 void bias_residual_add(Context &ctx, const float *x, int64_t rows, int cols, const float *bias,
                        const float *residual, float *out);
 void silu_inplace(Context &ctx, float *x, int64_t len);
+// dst [n][item] = SiLU(src [item]), n copies.
+void silu_tile(Context &ctx, const float *src, int64_t item, int n, float *dst);
 void add_inplace(Context &ctx, float *a, const float *b, int64_t len);
 void concat_channels(Context &ctx, const float *a, int ca, const float *b, int cb, int64_t pixels, float *out);
 void to_u8(Context &ctx, const float *x, int64_t len, uint8_t *out);

@@ -836,14 +836,15 @@ class UNetDevice {
         DT temb = pool_.tensor(b, 1, 1, TIME_EMBED);
         lin2_.fwd(e, a1, 1, temb.p);
         pool_.recycle(a1);
-        for (int i = 1; i < b; ++i)
-            HIP_CHECK(hipMemcpyAsync(temb.p + int64_t(i) * TIME_EMBED, temb.p, TIME_EMBED * sizeof(float),
-                                     hipMemcpyDeviceToDevice, ctx_.stream));
-        tr("unet.temb", temb);
+        if (trace) {  // the traced tensor holds every item's row
+            for (int i = 1; i < b; ++i)
+                HIP_CHECK(hipMemcpyAsync(temb.p + int64_t(i) * TIME_EMBED, temb.p, TIME_EMBED * sizeof(float),
+                                         hipMemcpyDeviceToDevice, ctx_.stream));
+            tr("unet.temb", temb);
+        }
+        // SiLU(temb) written once per item in one launch
         float *temb_silu = pool_.floats(int64_t(b) * TIME_EMBED);
-        HIP_CHECK(hipMemcpyAsync(temb_silu, temb.p, size_t(b) * TIME_EMBED * sizeof(float), hipMemcpyDeviceToDevice,
-                                 ctx_.stream));
-        silu_inplace(ctx_, temb_silu, int64_t(b) * TIME_EMBED);
+        silu_tile(ctx_, temb.p, TIME_EMBED, b, temb_silu);
         // all resnets' time projections: tp [b][temb_total_]
         float *tp = pool_.floats(int64_t(b) * temb_total_);
         const bool t32 = temb_w32_ && ctx_.precision == Precision::Exact;

@@ -47,7 +47,7 @@ enum class Precision : uint32_t { Exact = 0, Fast = 1 };
 
 // Tuning overrides for A/B runs and tests, read once from the environment
 // (MOEBIUS_HIP_GEMM_PLAN, _GN_IN_MAXC, _DW_TILED, _TAP_HEADS, _CROSS_HEADS,
-// _GN_BLOCKS, _GN_APPLY, _WINO_FUSED)
+// _GN_BLOCKS, _GN_APPLY, _WINO_FUSED, _UP_CONCAT, _LAMBDA_TAPS, _GEMM_LOG)
 // when a context is created and changed with set_tuning (mh_context_set_tuning).
 // The defaults are the measured choices; nothing on the hot path reads the
 // environment.
@@ -63,6 +63,7 @@ struct Tuning {
     int wino_fused = -1;   // Winograd convs in one kernel: -1 where faster, 1 wherever it fits, 0 never
     int up_concat = 0;     // 1: the UNet's up path writes [h | skip] before each resnet (the reference's order)
     int lambda_taps = 1;   // 0: the self-lambda's position coefficients through the general GEMM
+    int gemm_log = 0;      // 1: print each GEMM launch's shape and tiling to stderr (launch census)
 };
 // Sets `key` from its text form (the environment variable's syntax); value NULL
 // or "" restores the default. False for an unknown key or a malformed value.

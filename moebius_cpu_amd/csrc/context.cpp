@@ -75,6 +75,7 @@ bool set_tuning(Tuning &t, const char *key, const char *value) {
     if (k == "wino_fused") return to_int(t.wino_fused, -1) && t.wino_fused >= -1 && t.wino_fused <= 1;
     if (k == "up_concat") return to_int(t.up_concat, 0) && t.up_concat >= 0 && t.up_concat <= 1;
     if (k == "lambda_taps") return to_int(t.lambda_taps, 1) && t.lambda_taps >= 0 && t.lambda_taps <= 1;
+    if (k == "gemm_log") return to_int(t.gemm_log, 0);
     if (k == "tap_heads") {
         if (clear) {
             t.tap_tile = -1, t.tap_heads = 0;
@@ -102,7 +103,8 @@ Context::Context(int dev) : device(dev) {
                                               {"MOEBIUS_HIP_GN_APPLY", "gn_apply"},
                                               {"MOEBIUS_HIP_WINO_FUSED", "wino_fused"},
                                               {"MOEBIUS_HIP_UP_CONCAT", "up_concat"},
-                                              {"MOEBIUS_HIP_LAMBDA_TAPS", "lambda_taps"}};
+                                              {"MOEBIUS_HIP_LAMBDA_TAPS", "lambda_taps"},
+                                              {"MOEBIUS_HIP_GEMM_LOG", "gemm_log"}};
     for (const auto &kv : env_keys)
         if (const char *e = std::getenv(kv[0])) set_tuning(tune, kv[1], e);
     int count = 0;

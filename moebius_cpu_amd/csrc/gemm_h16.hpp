@@ -284,6 +284,7 @@ inline Plan plan_h16(int M, int N, int K, int cus, bool dense) {
 template <int BM, int BN, int MODE, bool PRO, bool F16, bool BVEC>
 void launch_cfg_h16(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int batch) {
     const unsigned tiles = unsigned(ceil_div(p.M, BM) * ceil_div(p.N, BN));
+    log_gemm(ctx, "f16", p, BM, BN, pl.splits, MODE, PRO, F16, epi, batch);
     if (pl.splits > 1) {
         const size_t bytes = size_t(pl.splits) * p.M * p.N * sizeof(float);
         p.partial = static_cast<float *>(ctx.ws.get(bytes, ctx.stream));

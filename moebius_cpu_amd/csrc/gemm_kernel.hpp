@@ -866,9 +866,23 @@ inline Plan plan_for(int M, int N, int K, int cus, bool dense) {
     return Plan{64, 64, s.first, s.first > 1 ? s.second : K};
 }
 
+// The launch census (Tuning::gemm_log): one line per GEMM launch with its shape,
+// tiling and epilogue, in launch order, to match against a kernel trace.
+inline void log_gemm(const Context &ctx, const char *family, const GemmArgs &p, int bm, int bn, int splits, int mode,
+                     bool pro, bool f16, GemmEpilogue epi, int batch) {
+    if (!ctx.tune.gemm_log) return;
+    std::fprintf(stderr,
+                 "[gemm] %s M=%d N=%d K=%d batch=%d tile=%dx%d splits=%d mode=%d pro=%d f16w=%d silu=%d bias=%d "
+                 "res=%d rsc=%d res2=%d gnp=%d nseg=%d rg=%d a2=%d\n",
+                 family, p.M, p.N, p.K, batch, bm, bn, splits, mode, int(pro), int(f16), int(epi == GemmEpilogue::Silu),
+                 int(p.bias != nullptr), int(p.res != nullptr), int(p.rsc != nullptr), int(p.res2 != nullptr),
+                 int(p.gnp != nullptr), p.nseg, p.rg, int(p.a2 != nullptr));
+}
+
 template <int BM, int BN, int MODE, bool PRO, bool F16, bool BVEC>
 void launch_cfg(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int batch) {
     const unsigned tiles = unsigned(ceil_div(p.M, BM) * ceil_div(p.N, BN));
+    log_gemm(ctx, "f32", p, BM, BN, pl.splits, MODE, PRO, F16, epi, batch);
     if (pl.splits > 1) {
         const size_t bytes = size_t(pl.splits) * p.M * p.N * sizeof(float);
         p.partial = static_cast<float *>(ctx.ws.get(bytes, ctx.stream));

@@ -145,6 +145,29 @@ const float *WeightStore::host_f32(const std::string &name, int64_t numel, std::
     return scratch.data();
 }
 
+WeightGroup concat_weights(Context &ctx, const DParam *members, int count) {
+    WeightGroup g;
+    bool all_f16 = true;
+    int64_t total = 0;
+    for (int i = 0; i < count; ++i) {
+        all_f16 = all_f16 && members[i].wt == kF16;
+        total += members[i].numel;
+    }
+    g.wt = all_f16 ? kF16 : kF32;
+    const size_t esz = all_f16 ? 2 : 4;
+    HIP_CHECK(hipMalloc(&g.p, size_t(total) * esz));
+    char *dst = static_cast<char *>(g.p);
+    for (int i = 0; i < count; ++i) {
+        const DParam &m = members[i];
+        if (m.wt == g.wt)
+            HIP_CHECK(hipMemcpyAsync(dst, m.p, size_t(m.numel) * esz, hipMemcpyDeviceToDevice, ctx.stream));
+        else  // an f16 member of an f32 group
+            widen_f16(ctx, m.p, m.numel, reinterpret_cast<float *>(dst));
+        dst += size_t(m.numel) * esz;
+    }
+    return g;
+}
+
 // ---------------------------------------------------------------- layers
 namespace {
 
@@ -451,17 +474,11 @@ struct SelfLambda {
         to_k.load(W, p + ".to_k", c, k, false);
         to_v.load(W, p + ".to_v", c, k, true);
         // q | k | v weights [c + 2k][c] and bias (k has none: zeros), for one GEMM.
-        wt = to_q.w.wt;
-        if (to_k.w.wt != wt || to_v.w.wt != wt) fail(kWeights, "lambda q/k/v weights must share one dtype");
-        const size_t esz = wt == kF16 ? 2 : 4;
-        HIP_CHECK(hipMalloc(&wqkv, size_t(c + 2 * k) * c * esz));
+        const DParam members[3] = {to_q.w, to_k.w, to_v.w};
+        const WeightGroup grp = concat_weights(e.ctx, members, 3);
+        wqkv = grp.p;
+        wt = grp.wt;
         HIP_CHECK(hipMalloc(&bqkv, size_t(c + 2 * k) * sizeof(float)));
-        char *dst = static_cast<char *>(wqkv);
-        HIP_CHECK(hipMemcpyAsync(dst, to_q.w.p, size_t(c) * c * esz, hipMemcpyDeviceToDevice, e.ctx.stream));
-        HIP_CHECK(hipMemcpyAsync(dst + size_t(c) * c * esz, to_k.w.p, size_t(k) * c * esz, hipMemcpyDeviceToDevice,
-                                 e.ctx.stream));
-        HIP_CHECK(hipMemcpyAsync(dst + size_t(c + k) * c * esz, to_v.w.p, size_t(k) * c * esz,
-                                 hipMemcpyDeviceToDevice, e.ctx.stream));
         if (wt == kF16) {
             HIP_CHECK(hipMalloc(&wqkv32, size_t(c + 2 * k) * c * sizeof(float)));
             widen_f16(e.ctx, wqkv, int64_t(c + 2 * k) * c, wqkv32);
@@ -763,23 +780,20 @@ class UNetDevice {
             for (auto *v : {&down_, &up_})
                 for (auto &blk : *v)
                     for (auto &r : blk.res) rs.push_back(&r);
-            temb_wt_ = rs.front()->temb_proj.w.wt;
             temb_total_ = 0;
+            std::vector<DParam> members;
             for (DwResnet *r : rs) {
-                if (r->temb_proj.w.wt != temb_wt_) fail(kWeights, "time_emb_proj weights must share one dtype");
                 r->temb_off = temb_total_;
                 temb_total_ += r->co;
+                members.push_back(r->temb_proj.w);
             }
-            const size_t esz = temb_wt_ == kF16 ? 2 : 4;
-            HIP_CHECK(hipMalloc(&temb_w_, size_t(temb_total_) * TIME_EMBED * esz));
+            const WeightGroup grp = concat_weights(ctx_, members.data(), int(members.size()));
+            temb_w_ = grp.p;
+            temb_wt_ = grp.wt;
             HIP_CHECK(hipMalloc(&temb_b_, size_t(temb_total_) * sizeof(float)));
-            for (DwResnet *r : rs) {
-                HIP_CHECK(hipMemcpyAsync(static_cast<char *>(temb_w_) + size_t(r->temb_off) * TIME_EMBED * esz,
-                                         r->temb_proj.w.p, size_t(r->co) * TIME_EMBED * esz, hipMemcpyDeviceToDevice,
-                                         ctx_.stream));
+            for (DwResnet *r : rs)
                 HIP_CHECK(hipMemcpyAsync(temb_b_ + r->temb_off, r->temb_proj.b, size_t(r->co) * sizeof(float),
                                          hipMemcpyDeviceToDevice, ctx_.stream));
-            }
             if (temb_wt_ == kF16) {
                 HIP_CHECK(hipMalloc(&temb_w32_, size_t(temb_total_) * TIME_EMBED * sizeof(float)));
                 widen_f16(ctx_, temb_w_, int64_t(temb_total_) * TIME_EMBED, temb_w32_);

@@ -74,6 +74,19 @@ class WeightStore {
     mutable size_t derived_bytes_ = 0;
 };
 
+// Several GEMM weights [rows_i][cols] stacked into one [sum rows_i][cols]
+// matrix, so one GEMM writes all their outputs (self-lambda q | k | v, every
+// resnet's time projection, the VAE attention's q | k | v). Stored f16 when every
+// member is f16; otherwise f32, with the f16 members widened exactly: the
+// converter keeps a GEMM weight f32 when its f16 copy would overflow
+// (tools/convert_weights.py:27-30), and the reference reads each tensor in its
+// own stored precision (src/engine/param.rs:14-59). The caller frees `p`.
+struct WeightGroup {
+    void *p = nullptr;
+    WeightType wt = kF32;
+};
+WeightGroup concat_weights(Context &ctx, const DParam *members, int count);
+
 using TraceFn = void (*)(void *user, const char *name, const float *dev, int n, int h, int w, int c);
 
 class UNetDevice;

@@ -218,18 +218,13 @@ struct MidAttention {
             ws[i] = W.get(p + names[i] + ".weight", int64_t(c) * c, true);
             bs[i] = W.get(p + names[i] + ".bias", c, false).f();
         }
-        wt = ws[0].wt;
-        if (ws[1].wt != wt || ws[2].wt != wt) fail(kWeights, "attention q/k/v weights must share one dtype");
-        const size_t esz = wt == kF16 ? 2 : 4;
-        const size_t wbytes = size_t(c) * c * esz;
-        HIP_CHECK(hipMalloc(&wqkv, 3 * wbytes));
+        const WeightGroup grp = concat_weights(ctx, ws, 3);
+        wqkv = grp.p;
+        wt = grp.wt;
         HIP_CHECK(hipMalloc(&bqkv, 3 * size_t(c) * sizeof(float)));
-        for (int i = 0; i < 3; ++i) {
-            HIP_CHECK(hipMemcpyAsync(static_cast<char *>(wqkv) + i * wbytes, ws[i].p, wbytes, hipMemcpyDeviceToDevice,
-                                     ctx.stream));
+        for (int i = 0; i < 3; ++i)
             HIP_CHECK(hipMemcpyAsync(bqkv + i * c, bs[i], size_t(c) * sizeof(float), hipMemcpyDeviceToDevice,
                                      ctx.stream));
-        }
         out.load(W, p + ".to_out.0", c, c);
     }
     void release() {

@@ -9,6 +9,7 @@ tests read like the reference's own tests/kernels.rs. Tensors live in HBM;
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
 import weakref
 
@@ -16,6 +17,22 @@ import numpy as np
 
 from . import _lib
 from ._lib import MoebiusError, check, lib, u32x4
+
+
+# Contexts still open when the interpreter exits are closed (their models first)
+# by an atexit hook, which runs before module teardown: at that point the
+# library handle is still loaded, so every destroy call reaches the C ABI in a
+# fixed order instead of depending on the order of garbage collection.
+_live_contexts: "weakref.WeakSet[Context]" = weakref.WeakSet()
+
+
+@atexit.register
+def _close_live_contexts():
+    for c in list(_live_contexts):
+        try:
+            c.close()
+        except Exception:
+            pass
 
 
 class Context:
@@ -26,6 +43,7 @@ class Context:
         check(lib().mh_context_create(int(device), ctypes.byref(h)))
         self.h = h
         self._models = weakref.WeakSet()  # UNet / Vae objects, destroyed before the context
+        _live_contexts.add(self)
 
     def adopt(self, model):
         """Registers a model (anything with close()) to be closed before this context."""

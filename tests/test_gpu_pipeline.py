@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import ctypes
 import dataclasses
+import os
 
 import numpy as np
 import pytest
@@ -237,3 +238,34 @@ def test_device_resize_is_byte_exact_to_the_oracle(ctx, src_hw, dst_hw, c):
     print(f"resize {src_hw} -> {dst_hw} x{c}", flush=True)
     _lib.check(_lib.lib().mh_resize_u8(ctx.h, d_src.ptr, fw, fh, tw, th, c, d_dst.ptr))
     assert np.array_equal(d_dst.numpy(), want)
+
+
+def _pillow_cases():
+    import json
+    import os
+
+    golden = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "lanczos.json")
+    with open(golden, encoding="utf-8") as f:
+        return [c for c in json.load(f)["cases"] if c["from"] != c["to"]]
+
+
+@pytest.mark.parametrize("case", _pillow_cases(), ids=lambda c: f"{c['kind']}-{c['from'][0]}x{c['from'][1]}-"
+                                                             f"{c['to'][0]}x{c['to'][1]}-c{c['channels']}")
+def test_device_resize_matches_pillow_lanczos(ctx, case):
+    """The device resampler against Pillow's LANCZOS bytes directly (SHA-256 of the
+    output; tests/golden/lanczos.json), on the reference's pixel types U8 and U8x3."""
+    import hashlib
+    import sys
+
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+    from make_lanczos_fixture import image
+
+    (fw, fh), (tw, th), c = case["from"], case["to"], case["channels"]
+    src = image(case["kind"], case["seed"], fw, fh, c)
+    d_src = E.DeviceArray.from_numpy(ctx, src)
+    d_dst = E.DeviceArray(ctx, (th, tw) if c == 1 else (th, tw, c), np.uint8)
+    print(f"pillow case {case['kind']} {fw}x{fh} -> {tw}x{th} x{c}", flush=True)
+    _lib.check(_lib.lib().mh_resize_u8(ctx.h, d_src.ptr, fw, fh, tw, th, c, d_dst.ptr))
+    got = d_dst.numpy().tobytes()
+    assert got[:48].hex() == case["head"]
+    assert hashlib.sha256(got).hexdigest() == case["sha256"]

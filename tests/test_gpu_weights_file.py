@@ -54,6 +54,49 @@ def test_vae_from_file_equals_vae_from_table(ctx, tmp_path):
     assert np.array_equal(got, want)
 
 
+# The converter keeps a GEMM weight f32 when its f16 copy would overflow
+# (tools/convert_weights.py:27-30), so an f16 file can hold F32 members inside the
+# groups the device fuses into one GEMM: self-lambda q | k | v, the stacked time
+# projections, the VAE attention's q | k | v.
+UNET_F32_MEMBERS = ("diff_model.down_blocks.1.resnets.0.time_emb_proj.weight",
+                    "diff_model.down_blocks.0.attentions.1.transformer_blocks.0.attn1.to_k.weight")
+VAE_F32_MEMBERS = ("decoder.mid_block.attentions.0.to_k.weight",)
+
+
+def _round_f16(params, names):
+    return {k: (v.astype(np.float16).astype(np.float32) if k in names else v) for k, v in params.items()}
+
+
+def test_unet_file_with_f32_members_in_fused_groups(ctx, tmp_path):
+    """Loads, and computes what an all-f32 model holding the same values computes
+    (EXACT reads f16-stored weights through their exact f32 widening), bit for bit."""
+    params = U.random_unet(seed=4000)
+    gemm16 = [s.name for s in U.unet_specs() if s.gemm and s.name not in UNET_F32_MEMBERS]
+    path = tmp_path / "unet_mixed.safetensors"
+    write_weights(str(path), params, gemm16, f16=True)
+    inp = U.unet_input(seed=5012)
+    a = UNet.from_file(ctx, str(path))
+    got = a.forward_host(inp.x, inp.timestep, cfg=True)
+    a.close()
+    b = UNet(ctx, _round_f16(params, set(gemm16)))
+    want = b.forward_host(inp.x, inp.timestep, cfg=True)
+    b.close()
+    assert np.array_equal(got, want)
+
+
+def test_vae_file_with_an_f32_member_in_the_attention_group(ctx, tmp_path):
+    params = V.random_vae()
+    gemm16 = [s.name for s in V.vae_specs() if s.gemm and s.name not in VAE_F32_MEMBERS]
+    path = tmp_path / "vae_mixed.safetensors"
+    write_weights(str(path), params, gemm16, f16=True, metadata={"scaling_factor": "0.13025"})
+    lat = S.normal(31, (1, 16, 16, 4))
+    a = Vae.from_file(ctx, str(path))
+    got = a.decode_host(lat)
+    a.close()
+    want = Vae(ctx, _round_f16(params, set(gemm16))).decode_host(lat)
+    assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))
+
+
 def test_bad_file_is_a_weights_error_before_any_upload(ctx, tmp_path):
     path = tmp_path / "vae.safetensors"
     write_weights(str(path), {"x": np.zeros(3, np.float32)}, metadata={"scaling_factor": "0.13025"})

@@ -81,7 +81,8 @@ def wconv(ctx, x, w, b, up=False, prologue=None, f16=False):
 
 @pytest.mark.parametrize("n,h,w,ci,co,up", [(2, 9, 11, 64, 48, False), (1, 7, 5, 32, 20, True),
                                             (2, 16, 16, 320, 320, False), (1, 8, 8, 1280, 1280, True),
-                                            (2, 16, 16, 640, 640, True)])
+                                            (2, 16, 16, 640, 640, True),
+                                            (1, 64, 64, 320, 320, False)])  # the 64x64x320 conv bench.py times
 def test_winograd_conv_matches_oracle(ctx, n, h, w, ci, co, up):
     rng = np.random.default_rng(ci + co + h)
     x = rng.standard_normal((n, h, w, ci)).astype(np.float32)

@@ -1,18 +1,40 @@
 """The oracle's window resampling (oracle/imaging.cpp: PIL's LANCZOS in 22-bit
 fixed point, the formulation src/imaging/resize.rs's fast_image_resize 6.1.0
-follows) pinned by the reference's resize tests (src/imaging/resize.rs:66-147),
-by closed forms (a constant image stays exactly constant; same size is a copy)
-and by an f64 separable Lanczos3 convolution (within one 8-bit level per
-pass). Per-byte equality with fast_image_resize itself is not pinned: the
-crate is not vendored. CPU only."""
+follows) pinned byte for byte to Pillow's LANCZOS on the reference's pixel
+types (U8 and U8x3, up and down, 800 <-> 512 among them; fixture written by
+tests/golden/make_lanczos_fixture.py), by the reference's resize tests
+(src/imaging/resize.rs:66-147), by closed forms (a constant image stays exactly
+constant; same size is a copy) and by an f64 separable Lanczos3 convolution
+(within one 8-bit level per pass). Per-byte equality with fast_image_resize
+itself is not pinned: the crate is not vendored. CPU only."""
 from __future__ import annotations
 
+import hashlib
+import json
 import math
+import os
+import sys
 
 import numpy as np
 import pytest
 
 import oracle
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+sys.path.insert(0, GOLDEN)
+from make_lanczos_fixture import image  # noqa: E402
+
+PILLOW_CASES = json.load(open(os.path.join(GOLDEN, "lanczos.json"), encoding="utf-8"))["cases"]
+
+
+@pytest.mark.parametrize("case", PILLOW_CASES, ids=lambda c: f"{c['kind']}-{c['from'][0]}x{c['from'][1]}-"
+                                                          f"{c['to'][0]}x{c['to'][1]}-c{c['channels']}")
+def test_matches_pillow_lanczos_byte_for_byte(case):
+    """Pillow's LANCZOS output (SHA-256 of its bytes) for seeded L and RGB images."""
+    img = image(case["kind"], case["seed"], *case["from"], case["channels"])
+    got = oracle.resize_u8(img, *case["to"]).tobytes()
+    assert got[:48].hex() == case["head"]
+    assert hashlib.sha256(got).hexdigest() == case["sha256"]
 
 
 def test_same_size_is_a_copy():

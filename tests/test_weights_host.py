@@ -46,6 +46,18 @@ def test_unet_file_in_the_converter_format_is_accepted(unet_file):
     assert st == _lib.ERR_WEIGHTS and "scaling_factor" in msg
 
 
+def test_f32_members_of_an_f16_file_are_accepted(tmp_path):
+    """The converter keeps a GEMM weight f32 when its f16 copy would overflow
+    (tools/convert_weights.py:27-30): an f16 file may hold F32 GEMM weights, also
+    inside the groups the device fuses (self-lambda q | k | v, the time projections)."""
+    specs = U.unet_specs()
+    keep32 = {"diff_model.down_blocks.1.resnets.0.time_emb_proj.weight",
+              "diff_model.down_blocks.0.attentions.1.transformer_blocks.0.attn1.to_k.weight"}
+    p = tmp_path / "unet_mixed.safetensors"
+    write_weights(str(p), zeros(specs), [s.name for s in specs if s.gemm and s.name not in keep32], f16=True)
+    assert validate(p, _lib.MODEL_UNET)[0] == _lib.OK
+
+
 def test_vae_file_needs_its_scaling_factor(tmp_path, vae_table):
     p = tmp_path / "vae.safetensors"
     write_weights(str(p), vae_table, metadata={"scaling_factor": "0.13025"})

@@ -276,6 +276,19 @@ int32_t mh_apply_affine(MhContext *ctx, const float *x, uint32_t n, uint32_t h, 
 int32_t mh_layer_norm(MhContext *ctx, const float *x, uint64_t rows, uint32_t c, const float *gamma,
                       const float *beta, float eps, float *out);
 
+/* layer_norm followed by Conv1x1::forward, as a transformer block runs them
+ * (src/unet/transformer.rs:100-126 with src/engine/norm.rs:151-173 and
+ * src/engine/conv.rs:38-55), in one GEMM: out [rows][c_out] = [SiLU](LayerNorm(x)
+ * . W^T + bias) (silu 1: the inverted 1x1's SiLU), with the LayerNorm folded into
+ * the product as rstd . (x . (W . diag gamma)^T - mean . rowsum) + W . beta +
+ * bias, so LayerNorm(x) is never written. The folded weights are built in the
+ * context's workspace on each call (the UNet builds them once at load). c_in and
+ * c_out multiples of 4; x and out 16-byte aligned; FAST contexts multiply on the
+ * f16 rounding of the folded weights. */
+int32_t mh_conv1x1_layer_norm(MhContext *ctx, const float *x, uint64_t rows, uint32_t c_in, const float *gamma,
+                              const float *beta, float eps, const void *weight, uint32_t weight_dtype, uint32_t c_out,
+                              const float *bias, uint32_t silu, float *out);
+
 /* src/engine/ops.rs:11-13 `silu_inplace` (in place). */
 int32_t mh_silu_inplace(MhContext *ctx, float *x, uint64_t len);
 /* src/engine/ops.rs:16-19 `add_inplace`: a += b (in place on a). */

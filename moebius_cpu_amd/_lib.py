@@ -89,6 +89,7 @@ SIGNATURES = {
                                              _vp]),
     "mh_apply_affine": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _vp]),
     "mh_layer_norm": (_i32, [_vp, _vp, _u64, _u32, _vp, _vp, _f32, _vp]),
+    "mh_conv1x1_layer_norm": (_i32, [_vp, _vp, _u64, _u32, _vp, _vp, _f32, _vp, _u32, _u32, _vp, _u32, _vp]),
     "mh_silu_inplace": (_i32, [_vp, _vp, _u64]),
     "mh_add_inplace": (_i32, [_vp, _vp, _vp, _u64]),
     "mh_concat_channels": (_i32, [_vp, _vp, _u32, _vp, _u32, _u64, _vp]),

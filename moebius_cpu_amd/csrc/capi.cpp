@@ -526,6 +526,38 @@ int32_t mh_layer_norm(MhContext *ctx, const float *x, uint64_t rows, uint32_t c,
     });
 }
 
+int32_t mh_conv1x1_layer_norm(MhContext *ctx, const float *x, uint64_t rows, uint32_t c_in, const float *gamma,
+                              const float *beta, float eps, const void *weight, uint32_t weight_dtype, uint32_t c_out,
+                              const float *bias, uint32_t silu, float *out) {
+    return guard([&] {
+        mh::Context &cc = C(ctx);
+        need(x, "x");
+        need(gamma, "gamma");
+        need(beta, "beta");
+        need(weight, "weight");
+        need(out, "out");
+        const int ci = dim(c_in, "c_in"), co = dim(c_out, "c_out");
+        MH_REQUIRE(ci % 4 == 0 && co % 4 == 0, "Conv1x1 (LayerNorm): c_in and c_out must be multiples of 4");
+        MH_REQUIRE(rows < (uint64_t(1) << 31), "Conv1x1 (LayerNorm): too many rows");
+        auto al = [](size_t b) { return (b + 255) & ~size_t(255); };
+        const size_t nk = size_t(co) * ci;
+        const size_t o16 = al(nk * 4), oc1 = o16 + al(nk * 2), oc16 = oc1 + al(size_t(co) * 4),
+                     oc2 = oc16 + al(size_t(co) * 4), total = oc2 + al(size_t(co) * 4);
+        char *ws = static_cast<char *>(cc.ws.get(total, cc.stream));
+        float *w32 = reinterpret_cast<float *>(ws);
+        float *c1_32 = reinterpret_cast<float *>(ws + oc1), *c1_16 = reinterpret_cast<float *>(ws + oc16);
+        float *c2 = reinterpret_cast<float *>(ws + oc2);
+        mh::ln_fold_weights(cc, weight, wtype(weight_dtype), co, ci, gamma, beta, bias, w32, ws + o16, c1_32, c1_16,
+                            c2);
+        mh::LnFolded f;
+        f.w32 = w32, f.c1_32 = c1_32, f.w16 = ws + o16, f.c1_16 = c1_16, f.c2 = c2, f.eps = eps;
+        const int width = co;
+        float *const outs[1] = {out};
+        mh::conv1x1_ln(cc, x, int64_t(rows), ci, f, 1, &width, outs,
+                       silu ? mh::GemmEpilogue::Silu : mh::GemmEpilogue::None);
+    });
+}
+
 int32_t mh_silu_inplace(MhContext *ctx, float *x, uint64_t len) {
     return guard([&] {
         mh::Context &cc = C(ctx);

@@ -47,12 +47,16 @@ enum class Precision : uint32_t { Exact = 0, Fast = 1 };
 
 // Tuning overrides for A/B runs and tests, read once from the environment
 // (MOEBIUS_HIP_GEMM_PLAN, _GN_IN_MAXC, _DW_TILED, _TAP_HEADS, _CROSS_HEADS,
-// _GN_BLOCKS, _GN_APPLY, _WINO_FUSED, _UP_CONCAT, _LAMBDA_TAPS, _GEMM_LOG)
+// _GN_BLOCKS, _GN_APPLY, _WINO_FUSED, _UP_CONCAT, _LAMBDA_TAPS, _GEMM_LOG,
+// _GEMM_WIDE, _LN_FOLD)
 // when a context is created and changed with set_tuning (mh_context_set_tuning).
 // The defaults are the measured choices; nothing on the hot path reads the
 // environment.
 struct Tuning {
     int gemm_bm = 0, gemm_bn = 0, gemm_splits = 0;  // forced GEMM tiling, 0: the planner's
+    int gemm_wm = 2, gemm_wn = 2, gemm_wk = 1;       // and its wave layout (f32 kernel)
+    int gemm_pipe = 0;                               // and its main loop (1: pipelined)
+    int gemm_bk = 32;                                // and its K per LDS stage
     int gn_in_maxc = -1;   // GroupNorm applied in proj_in's loads up to this width; -1: per precision
     int dw_tiled = 1;      // 0: the register-window depthwise kernel
     int tap_tile = -1;     // tap filter: -1 default; 0 the per-thread kernel; 4 / 8 the tile kernel's heads
@@ -64,6 +68,8 @@ struct Tuning {
     int up_concat = 0;     // 1: the UNet's up path writes [h | skip] before each resnet (the reference's order)
     int lambda_taps = 1;   // 0: the self-lambda's position coefficients through the general GEMM
     int gemm_log = 0;      // 1: print each GEMM launch's shape and tiling to stderr (launch census)
+    int gemm_wide = 1;     // 0: the square tilings only (no wide wave layouts from the planner)
+    int ln_fold = 0;       // 1: the transformers' LayerNorms 1 and 3 folded into the GEMMs that read them
 };
 // Sets `key` from its text form (the environment variable's syntax); value NULL
 // or "" restores the default. False for an unknown key or a malformed value.

@@ -57,14 +57,19 @@ bool set_tuning(Tuning &t, const char *key, const char *value) {
         dst = int(x);
         return true;
     };
-    if (k == "gemm_plan") {
+    if (k == "gemm_plan") {  // "bm,bn,splits" or "bm,bn,splits,wm,wn,wk[,pipe[,bk]]"
+        t.gemm_wm = 2, t.gemm_wn = 2, t.gemm_wk = 1, t.gemm_pipe = 0, t.gemm_bk = 32;
         if (clear) {
             t.gemm_bm = t.gemm_bn = t.gemm_splits = 0;
             return true;
         }
-        int bm = 0, bn = 0, sp = 0;
-        if (std::sscanf(v.c_str(), "%d,%d,%d", &bm, &bn, &sp) != 3 || sp < 1) return false;
+        int bm = 0, bn = 0, sp = 0, wm = 2, wn = 2, wk = 1, pipe = 0, bk = 32;
+        const int got = std::sscanf(v.c_str(), "%d,%d,%d,%d,%d,%d,%d,%d", &bm, &bn, &sp, &wm, &wn, &wk, &pipe, &bk);
+        if ((got != 3 && got < 6) || sp < 1 || wm < 1 || wn < 1 || wk < 1 || pipe < 0 || pipe > 1 ||
+            (bk != 16 && bk != 32))
+            return false;
         t.gemm_bm = bm, t.gemm_bn = bn, t.gemm_splits = sp;
+        t.gemm_wm = wm, t.gemm_wn = wn, t.gemm_wk = wk, t.gemm_pipe = pipe, t.gemm_bk = bk;
         return true;
     }
     if (k == "gn_in_maxc") return to_int(t.gn_in_maxc, -1);
@@ -76,6 +81,8 @@ bool set_tuning(Tuning &t, const char *key, const char *value) {
     if (k == "up_concat") return to_int(t.up_concat, 0) && t.up_concat >= 0 && t.up_concat <= 1;
     if (k == "lambda_taps") return to_int(t.lambda_taps, 1) && t.lambda_taps >= 0 && t.lambda_taps <= 1;
     if (k == "gemm_log") return to_int(t.gemm_log, 0);
+    if (k == "gemm_wide") return to_int(t.gemm_wide, 1) && t.gemm_wide >= 0 && t.gemm_wide <= 1;
+    if (k == "ln_fold") return to_int(t.ln_fold, 0) && t.ln_fold >= 0 && t.ln_fold <= 1;
     if (k == "tap_heads") {
         if (clear) {
             t.tap_tile = -1, t.tap_heads = 0;
@@ -104,7 +111,9 @@ Context::Context(int dev) : device(dev) {
                                               {"MOEBIUS_HIP_WINO_FUSED", "wino_fused"},
                                               {"MOEBIUS_HIP_UP_CONCAT", "up_concat"},
                                               {"MOEBIUS_HIP_LAMBDA_TAPS", "lambda_taps"},
-                                              {"MOEBIUS_HIP_GEMM_LOG", "gemm_log"}};
+                                              {"MOEBIUS_HIP_GEMM_LOG", "gemm_log"},
+                                              {"MOEBIUS_HIP_GEMM_WIDE", "gemm_wide"},
+                                              {"MOEBIUS_HIP_LN_FOLD", "ln_fold"}};
     for (const auto &kv : env_keys)
         if (const char *e = std::getenv(kv[0])) set_tuning(tune, kv[1], e);
     int count = 0;

@@ -122,6 +122,47 @@ __global__ void widen_f16_kernel(const _Float16 *__restrict__ src, int64_t len, 
         dst[e] = float(src[e]);
 }
 
+// One workgroup per weight row n (LnFolded, kernels.hpp): W' = W . gamma and its
+// f16 rounding (nearest, saturated at +-65504 as the f16 GEMM rounds f32
+// operands), their row sums and W . beta + bias, each summed in f64 per thread
+// (thread t takes k = t, t + 256, ...) and then over the threads in a fixed tree.
+__global__ __launch_bounds__(256) void ln_fold_kernel(const void *__restrict__ w, int f16, int k,
+                                                      const float *__restrict__ gamma, const float *__restrict__ beta,
+                                                      const float *__restrict__ bias, float *__restrict__ w32,
+                                                      _Float16 *__restrict__ w16, float *__restrict__ c1_32,
+                                                      float *__restrict__ c1_16, float *__restrict__ c2) {
+    const int n = blockIdx.x, tid = threadIdx.x;
+    const int64_t row = int64_t(n) * k;
+    double s32 = 0.0, s16 = 0.0, sb = 0.0;
+    for (int i = tid; i < k; i += 256) {
+        const float wv = f16 ? float(static_cast<const _Float16 *>(w)[row + i]) : static_cast<const float *>(w)[row + i];
+        const float wg = wv * gamma[i];
+        w32[row + i] = wg;
+        const float sat = __builtin_fabsf(wg) > 65504.0f ? __builtin_copysignf(65504.0f, wg) : wg;
+        const _Float16 h = static_cast<_Float16>(sat);
+        w16[row + i] = h;
+        s32 += double(wg);
+        s16 += double(float(h));
+        sb += double(wv) * double(beta[i]);
+    }
+    __shared__ double red[3][256];
+    red[0][tid] = s32, red[1][tid] = s16, red[2][tid] = sb;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) {
+            red[0][tid] += red[0][tid + o];
+            red[1][tid] += red[1][tid + o];
+            red[2][tid] += red[2][tid + o];
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        c1_32[n] = float(red[0][0]);
+        c1_16[n] = float(red[1][0]);
+        c2[n] = float(red[2][0] + (bias ? double(bias[n]) : 0.0));
+    }
+}
+
 __global__ void math_eval_kernel(int which, const float *__restrict__ x, int64_t len, float *__restrict__ y) {
     for (int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; e < len; e += int64_t(gridDim.x) * blockDim.x)
         y[e] = which == 0 ? ref_exp(x[e]) : ref_silu(x[e]);
@@ -213,6 +254,15 @@ void tile_items(Context &ctx, const float *src, int64_t item, int n, float *dst)
 void widen_f16(Context &ctx, const void *src, int64_t len, float *dst) {
     if (len == 0) return;
     widen_f16_kernel<<<grid_for(len), 256, 0, ctx.stream>>>(static_cast<const _Float16 *>(src), len, dst);
+    MH_LAUNCH_CHECK();
+}
+
+void ln_fold_weights(Context &ctx, const void *w, WeightType wt, int n, int k, const float *gamma, const float *beta,
+                     const float *bias, float *w32, void *w16, float *c1_32, float *c1_16, float *c2) {
+    MH_REQUIRE(n > 0 && k > 0 && w && gamma && beta && w32 && w16 && c1_32 && c1_16 && c2,
+               "ln_fold_weights: missing tensors");
+    ln_fold_kernel<<<unsigned(n), 256, 0, ctx.stream>>>(w, wt == kF16 ? 1 : 0, k, gamma, beta, bias, w32,
+                                                       static_cast<_Float16 *>(w16), c1_32, c1_16, c2);
     MH_LAUNCH_CHECK();
 }
 

@@ -173,6 +173,52 @@ void conv1x1_segments(Context &ctx, const float *x, int64_t pixels, int c_in, co
     run_dense(ctx, p, wt, GemmEpilogue::None, 1, c_in % 4 == 0 && aligned16(x));
 }
 
+void conv1x1_ln(Context &ctx, const float *x, int64_t pixels, int c_in, const LnFolded &f, int nseg, const int *widths,
+                float *const *outs, GemmEpilogue epi) {
+    MH_REQUIRE(nseg >= 1 && nseg <= kMaxSeg, "Conv1x1 (LayerNorm): 1 to 3 outputs");
+    MH_REQUIRE(pixels < (int64_t(1) << 31), "Conv1x1: too many pixels");
+    MH_REQUIRE(c_in % 4 == 0 && aligned16(x) && f.w32 && f.c1_32 && f.w16 && f.c1_16 && f.c2 && aligned16(f.c2) &&
+                   aligned16(f.c1_32) && aligned16(f.c1_16),
+               "Conv1x1 (LayerNorm): 4-channel aligned rows and the folded tensors");
+    if (pixels == 0) return;
+    GemmArgs p{};
+    p.a = x;
+    p.lda = c_in;
+    p.M = int(pixels);
+    int n = 0;
+    p.nseg = nseg;
+    for (int i = 0; i < nseg; ++i) {
+        MH_REQUIRE(widths[i] > 0 && widths[i] % 4 == 0 && outs[i] && aligned16(outs[i]),
+                   "Conv1x1 (LayerNorm): segments of whole, aligned column quads");
+        p.seg_col[i] = n;
+        p.seg_out[i] = outs[i];
+        n += widths[i];
+    }
+    p.seg_col[nseg] = n;
+    if (nseg == 1) {  // one plain output
+        p.nseg = 0;
+        p.out = outs[0];
+    }
+    p.N = n;
+    p.K = c_in;
+    p.ldb = c_in;
+    p.a_bytes = extent(pixels, c_in, c_in, 4);
+    p.bias = f.c2;
+    p.ldc = n;
+    p.ln_eps = f.eps;
+    if (ctx.precision == Precision::Fast) {
+        p.b = f.w16;
+        p.ln_c1 = f.c1_16;
+        p.b_bytes = extent(n, c_in, c_in, 2);
+        launch_dense_ln_h16(ctx, p, kF16, epi);
+    } else {
+        p.b = f.w32;
+        p.ln_c1 = f.c1_32;
+        p.b_bytes = extent(n, c_in, c_in, 4);
+        launch_dense_ln(ctx, p, kF32, epi);
+    }
+}
+
 void gemm_nt(Context &ctx, const float *a, int64_t lda, int64_t a_bs, const void *b, WeightType wt, int64_t ldb,
              int64_t b_bs, int m, int n, int k, int batch, const float *bias, const float *residual, float *out,
              int64_t ldc, int64_t c_bs, GemmEpilogue epi, int row_group) {

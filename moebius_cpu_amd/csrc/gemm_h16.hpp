@@ -25,6 +25,7 @@ typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 // Launchers of the fast kernels (gemm_fast_dense.hip, gemm_fast_conv.hip).
 void launch_dense_h16(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi, int batch, bool vec);
 void launch_dense_pro_h16(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi);
+void launch_dense_ln_h16(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi);
 void launch_conv_h16(Context &ctx, GemmArgs &p, WeightType wt, int mode, bool pro);
 
 namespace {
@@ -58,13 +59,13 @@ __device__ __forceinline__ halfx4 to_h4(floatx4 v) {
 
 // Four consecutive K of A row m, starting at k (k0: first K of the tile, whose
 // tap the aligned conv gather shares across the tile).
-template <int MODE, bool PRO>
+template <int MODE, int PRO>
 __device__ __forceinline__ floatx4 load_a_h(const GemmArgs &p, __amdgpu_buffer_rsrc_t ar, const ConvRow &r, int m,
                                             int k, int k_end, int tky, int tkx, int tci, int k0, int64_t lda = -1) {
     if constexpr (MODE == kDense) {
         const bool ok = m < p.M && k < k_end;
         const floatx4 v = buf_load4(ar, ok ? int((int64_t(m) * (lda < 0 ? p.lda : lda) + k) * 4) : kOob);
-        if constexpr (PRO) return dense_prologue(p, r.b, k, ok, v);
+        if constexpr (PRO == kProAffine) return dense_prologue(p, r.b, k, ok, v);
         return v;
     } else if constexpr (MODE == kConvAligned || MODE == kConvVec) {
         int ky, kx, c;
@@ -81,7 +82,7 @@ __device__ __forceinline__ floatx4 load_a_h(const GemmArgs &p, __amdgpu_buffer_r
         const int64_t src = conv_src(p, r, ky, kx);
         const bool ok = k < k_end && src >= 0;
         floatx4 v = buf_load4(ar, ok ? int((src + c) * 4) : kOob);
-        if constexpr (PRO) {
+        if constexpr (PRO == kProAffine) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = ok ? prologue1(p, r.b, c + e, v[e]) : 0.0f;
         }
@@ -115,7 +116,7 @@ __device__ __forceinline__ typename BChunk<F16, BVEC>::T load_b_h(const GemmArgs
 __device__ __forceinline__ halfx4 as_h4(halfx4 v) { return v; }
 __device__ __forceinline__ halfx4 as_h4(floatx4 v) { return to_h4(v); }
 
-template <int BM, int BN, int MODE, bool PRO, bool F16, bool BVEC, int EPI, bool SPLIT>
+template <int BM, int BN, int MODE, int PRO, bool F16, bool BVEC, int EPI, bool SPLIT>
 __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
     constexpr int MF = mf_for<BM, BN>();
     using MI = MfH<MF>;
@@ -150,7 +151,7 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
         if (MODE >= kConvAligned) crow[i] = conv_row(p, m0 + lrow + 16 * i);
-        else if (PRO) crow[i] = ConvRow{min(m0 + lrow + 16 * i, p.M - 1) / p.pro_rows, 0, 0, true};
+        else if (PRO == kProAffine) crow[i] = ConvRow{min(m0 + lrow + 16 * i, p.M - 1) / p.pro_rows, 0, 0, true};
         else crow[i] = ConvRow{0, 0, 0, true};
     }
 
@@ -160,6 +161,9 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
     using BT = typename BChunk<F16, BVEC>::T;
     floatx4 ra0[A_LD], ra1[A_LD];
     BT rb0[B_LD], rb1[B_LD];
+    double ln_s1[A_LD], ln_s2[A_LD];  // kProLn: row sums of the f32 values as loaded (before rounding)
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) ln_s1[i] = ln_s2[i] = 0.0;
     auto fetch = [&](int kt, floatx4 (&ra)[A_LD], BT (&rb)[B_LD]) {
         const int k0 = k_begin + kt * BKH;
         int tky = 0, tkx = 0, tci = 0;
@@ -177,6 +181,14 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
             ra[i] = sec ? load_a_h<MODE, PRO>(p, a2_rsrc, crow[i], m0 + lrow + 16 * i, k - p.ka, k_end - p.ka, tky, tkx,
                                               tci, k0 - p.ka, p.lda2)
                         : load_a_h<MODE, PRO>(p, a_rsrc, crow[i], m0 + lrow + 16 * i, k, k_end, tky, tkx, tci, k0);
+        if constexpr (PRO == kProLn) {
+#pragma unroll
+            for (int i = 0; i < A_LD; ++i) {
+                const double a0 = ra[i][0], a1 = ra[i][1], a2 = ra[i][2], a3 = ra[i][3];
+                ln_s1[i] += (a0 + a1) + (a2 + a3);
+                ln_s2[i] += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
+            }
+        }
 #pragma unroll
         for (int i = 0; i < B_LD; ++i) rb[i] = load_b_h<F16, BVEC>(p, b_rsrc, n0 + lrow + 16 * i, k, k_end);
     };
@@ -247,8 +259,11 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
             compute(0);
         }
     }
+    __shared__ float ln_st[PRO == kProLn ? 2 * BM : 1];
+    if constexpr (PRO == kProLn) ln_row_stats<A_LD, 16, KCH, BM>(p, ln_s1, ln_s2, lrow, lc, ln_st);
     __syncthreads();
-    write_tile<BM, BN, MF, EPI, SPLIT>(p, reinterpret_cast<float *>(smem), acc, m0, n0, ti.z);
+    write_tile<BM, BN, 2, 2, 1, MF, EPI, SPLIT>(p, reinterpret_cast<float *>(smem), acc, m0, n0, ti.z,
+                                                PRO == kProLn ? ln_st : nullptr);
 }
 
 // Tile shape and K split of the fast kernel, from sweeps of every (tile,
@@ -281,7 +296,7 @@ inline Plan plan_h16(int M, int N, int K, int cus, bool dense) {
     return plan(64, 1);
 }
 
-template <int BM, int BN, int MODE, bool PRO, bool F16, bool BVEC>
+template <int BM, int BN, int MODE, int PRO, bool F16, bool BVEC>
 void launch_cfg_h16(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int batch) {
     const unsigned tiles = unsigned(ceil_div(p.M, BM) * ceil_div(p.N, BN));
     log_gemm(ctx, "f16", p, BM, BN, pl.splits, MODE, PRO, F16, epi, batch);
@@ -327,7 +342,7 @@ void launch_cfg_h16(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi,
     MH_LAUNCH_CHECK();
 }
 
-template <int MODE, bool PRO, bool F16, bool BVEC>
+template <int MODE, int PRO, bool F16, bool BVEC>
 void launch_tiles_h16(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
     Plan pl = plan_h16(p.M, p.N, p.K, int(ceil_div(ctx.cu_count, batch)), MODE <= kDenseScalar);
     // The context's gemm_plan tuning forces the tiling, as for the f32 kernel.
@@ -339,7 +354,7 @@ void launch_tiles_h16(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
             pl = Plan{bm, bn, int(ceil_div(ktiles, per)), per * BKH};
         }
     }
-    if (batch > 1) pl.splits = 1;
+    if (batch > 1 || PRO == kProLn) pl.splits = 1;  // the folded LayerNorm needs whole rows of K
     if (pl.splits == 1) pl.k_split = p.K;
     if constexpr (MODE <= kDenseScalar) {
         if (pl.bm == 32) {
@@ -353,7 +368,7 @@ void launch_tiles_h16(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
         launch_cfg_h16<64, 64, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
 }
 
-template <int MODE, bool PRO>
+template <int MODE, int PRO>
 void launch_b_h16(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi, int batch = 1) {
     const int esz = wt == kF16 ? 2 : 4;
     const bool bvec = p.K % 4 == 0 && p.ldb % 4 == 0 && (reinterpret_cast<uintptr_t>(p.b) % (4 * esz)) == 0 &&

@@ -48,6 +48,13 @@ struct Mf {
     }
 };
 
+// A-operand prologue kinds (the PRO template argument): none; the GroupNorm
+// affine [SiLU](x . scale + shift) per (item, channel) as values load; or the
+// LayerNorm of each row folded into the product (kProLn, dense operands: the
+// workgroup sums its rows' values in f64 as they load, and the epilogue forms
+// rstd . (acc - mean . ln_c1) with B = W . diag(gamma), bias = W . beta + b).
+constexpr int kProNone = 0, kProAffine = 1, kProLn = 2;
+
 enum AMode : int {
     kDense = 0,      // A[m][k] row-major with leading dimension lda, K % 4 == 0
     kDenseScalar,    // same, any K
@@ -111,6 +118,10 @@ struct GemmArgs {
     int64_t lda2;
     int ka;
     uint32_t a2_bytes;
+    // kProLn: per output column, the sum over K of the folded weights (the
+    // mean's coefficient), and the LayerNorm epsilon; the row width is K
+    const float *ln_c1;
+    float ln_eps;
 };
 
 // (residual [transformed] + bias) + acc [SiLU] (+ res2): the reference's
@@ -139,6 +150,8 @@ __device__ __forceinline__ float epilogue_value(const GemmArgs &p, int row, int 
 void launch_dense(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi, int batch, bool vec);
 // Dense operands with the GroupNorm prologue (K-contiguous vector rows, no batch).
 void launch_dense_pro(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi);
+// Dense operands whose rows enter through a folded LayerNorm (kProLn; no batch).
+void launch_dense_ln(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi);
 void launch_conv(Context &ctx, GemmArgs &p, WeightType wt, int mode, bool pro);
 
 namespace {
@@ -272,7 +285,7 @@ __device__ __forceinline__ float prologue1(const GemmArgs &p, int b, int c, floa
     return p.psilu ? ref_silu(y) : y;
 }
 
-template <int MODE, bool PRO>
+template <int MODE, int PRO>
 __device__ __forceinline__ floatx4 load_a(const GemmArgs &p, const ConvRow &r, int m, int k, int tap_ky,
                                           int tap_kx, int tap_ci0) {
     if (MODE == kDense) {
@@ -302,7 +315,7 @@ __device__ __forceinline__ floatx4 load_a(const GemmArgs &p, const ConvRow &r, i
         const int64_t off = conv_src(p, r, ky, kx);
         if (off < 0) return zero4();
         floatx4 v = *reinterpret_cast<const floatx4 *>(p.a + off + c);
-        if (PRO) {
+        if (PRO == kProAffine) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = prologue1(p, r.b, c + e, v[e]);
         }
@@ -319,7 +332,7 @@ __device__ __forceinline__ floatx4 load_a(const GemmArgs &p, const ConvRow &r, i
             const int64_t off = conv_src(p, r, ky, kx);
             if (off >= 0) {
                 float x = p.a[off + c];
-                if (PRO) x = prologue1(p, r.b, c, x);
+                if (PRO == kProAffine) x = prologue1(p, r.b, c, x);
                 v[e] = x;
             }
         }
@@ -360,14 +373,14 @@ __device__ __forceinline__ floatx4 dense_prologue(const GemmArgs &p, int b, int 
     return v;
 }
 
-template <int MODE, bool PRO>
+template <int MODE, int PRO>
 __device__ __forceinline__ floatx4 load_a_buf(const GemmArgs &p, __amdgpu_buffer_rsrc_t ar, const ConvRow &r, int m,
                                               int k, int k_end, int tap_ky, int tap_kx, int tap_ci0,
                                               int64_t lda = -1) {
     if constexpr (MODE == kDense) {
         const bool ok = m < p.M && k < k_end;
         const floatx4 v = buf_load4(ar, ok ? int((int64_t(m) * (lda < 0 ? p.lda : lda) + k) * 4) : kOob);
-        if constexpr (PRO) return dense_prologue(p, r.b, k, ok, v);
+        if constexpr (PRO == kProAffine) return dense_prologue(p, r.b, k, ok, v);
         return v;
     } else {
         int ky, kx, c;
@@ -384,7 +397,7 @@ __device__ __forceinline__ floatx4 load_a_buf(const GemmArgs &p, __amdgpu_buffer
         const int64_t src = conv_src(p, r, ky, kx);
         const bool ok = k < k_end && src >= 0;
         floatx4 v = buf_load4(ar, ok ? int((src + c) * 4) : kOob);
-        if constexpr (PRO) {
+        if constexpr (PRO == kProAffine) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = ok ? prologue1(p, r.b, c + e, v[e]) : 0.0f;
         }
@@ -503,59 +516,208 @@ __device__ __forceinline__ void gn_tile_partials(const GemmArgs &p, float *smem,
     }
 }
 
+// Mean and 1 / sqrt(var + eps) of the A rows a workgroup loaded (kProLn):
+// slot i of this thread covers row lrow + RPP * i, its KL lanes (adjacent, one
+// wave) hold the row's partial sums; biased variance, as LayerNorm's.
+template <int A_LD, int RPP, int KL, int BM>
+__device__ __forceinline__ void ln_row_stats(const GemmArgs &p, const double (&s1)[A_LD], const double (&s2)[A_LD],
+                                             int lrow, int lc, float *st) {
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+        double a = s1[i], b = s2[i];
+#pragma unroll
+        for (int o = 1; o < KL; o <<= 1) {
+            a += __shfl_xor(a, o, 64);
+            b += __shfl_xor(b, o, 64);
+        }
+        const int r = lrow + RPP * i;
+        if (lc == 0 && r < BM) {
+            const double mean = a / double(p.K);
+            const double var = fmax(b / double(p.K) - mean * mean, 0.0);
+            st[2 * r] = float(mean);
+            st[2 * r + 1] = float(1.0 / sqrt(var + double(p.ln_eps)));
+        }
+    }
+}
+
+// The folded LayerNorm's correction of four adjacent columns of tile row rr:
+// rstd . (acc - mean . c1[col]).
+__device__ __forceinline__ float4 ln_correct(const GemmArgs &p, const float *st, int rr, int col, float4 v) {
+    const float mean = st[2 * rr], rs = st[2 * rr + 1];
+    const float4 c = *reinterpret_cast<const float4 *>(p.ln_c1 + col);
+    v.x = rs * __builtin_fmaf(-mean, c.x, v.x);
+    v.y = rs * __builtin_fmaf(-mean, c.y, v.y);
+    v.z = rs * __builtin_fmaf(-mean, c.z, v.z);
+    v.w = rs * __builtin_fmaf(-mean, c.w, v.w);
+    return v;
+}
+
+// GroupNorm partials of one output tile from the stored values, for wave
+// layouts other than the 2x2 one (any number of column quads): the store pass
+// has written y over the C tile (row stride CS); thread t sums column quad
+// t % C4 over rows g, g + G, ... (g = t / C4, G = NT / C4 row groups), then
+// the G group sums are added in group order through LDS past the C tile.
+template <int BM, int BN, int NT, int CS>
+__device__ __forceinline__ void gn_tile_partials_lds(const GemmArgs &p, float *smem, int m0, int n0) {
+    constexpr int C4 = BN / 4;
+    constexpr int G = NT / C4;
+    static_assert(G >= 1, "a thread per column quad");
+    float4 *red = reinterpret_cast<float4 *>(smem + BM * CS);  // [2][G][C4]
+    const int tid = threadIdx.x;
+    if (tid < G * C4) {
+        const int q = tid % C4, g = tid / C4;
+        float4 s{0.f, 0.f, 0.f, 0.f}, sq = s;
+        for (int r = g; r < BM && m0 + r < p.M; r += G) {  // rows past M were not stored
+            const float4 y = *reinterpret_cast<const float4 *>(smem + r * CS + q * 4);
+            s.x += y.x, s.y += y.y, s.z += y.z, s.w += y.w;
+            sq.x = __builtin_fmaf(y.x, y.x, sq.x);
+            sq.y = __builtin_fmaf(y.y, y.y, sq.y);
+            sq.z = __builtin_fmaf(y.z, y.z, sq.z);
+            sq.w = __builtin_fmaf(y.w, y.w, sq.w);
+        }
+        red[g * C4 + q] = s;
+        red[(G + g) * C4 + q] = sq;
+    }
+    __syncthreads();
+    if (tid < C4) {
+        const int col = n0 + tid * 4;
+        if (col < p.N) {
+            float4 ts = red[tid], tq = red[G * C4 + tid];
+            for (int g = 1; g < G; ++g) {
+                const float4 a = red[g * C4 + tid], b = red[(G + g) * C4 + tid];
+                ts.x += a.x, ts.y += a.y, ts.z += a.z, ts.w += a.w;
+                tq.x += b.x, tq.y += b.y, tq.z += b.z, tq.w += b.w;
+            }
+            float *dst = p.gnp + (int64_t(m0 / BM) * p.N + col) * 2;
+            *reinterpret_cast<float4 *>(dst) = float4{ts.x, tq.x, ts.y, tq.y};
+            *reinterpret_cast<float4 *>(dst + 4) = float4{ts.z, tq.z, ts.w, tq.w};
+        }
+    }
+}
+
+// Wave layout of a workgroup: WM x WN waves over the output tile, each owning
+// a (BM / WM) x (BN / WN) block of it, times WK wave groups that split every
+// LDS stage's K between them (their sums are added in group order in the
+// epilogue). 2x2x1 is the original layout of the square tiles.
+template <int BM, int BN, int WM, int WN, int WK>
+struct Waves {
+    static constexpr int kWaves = WM * WN * WK;
+    static constexpr int kThreads = 64 * kWaves;
+    static constexpr int TM = BM / WM, TN = BN / WN;
+    static constexpr int MF = (TM % 32 == 0 && TN % 32 == 0) ? 32 : 16;
+    static constexpr int FM = TM / MF, FN = TN / MF;
+    static constexpr int CS = BN + (MF == 16 ? 4 : 8);  // C tile row stride (floats)
+    // The 2x2 layout's epilogue, where each thread keeps one column quad over its
+    // rows for the GroupNorm sums (256 threads, 256 % (BN / 4) == 0); every
+    // other layout sums them from LDS.
+    static constexpr bool kFixedQuads = WM == 2 && WN == 2 && WK == 1 && 256 % (BN / 4) == 0 &&
+                                        (BM * (BN / 4)) % 256 == 0;
+    static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tiles of whole 16x16 blocks");
+    static __device__ __forceinline__ void index(int wave, int &wm, int &wn, int &wk) {
+        wk = wave / (WM * WN);
+        const int r = wave - wk * (WM * WN);
+        wm = r / WN;
+        wn = r - wm * WN;
+    }
+};
+
 // Epilogue through LDS, shared by the f32 and f16 kernels (smem holds at least
-// BM * (BN + 8) floats and 2048 floats, and is free): block (i, j), register v, lane l of wave
-// (wm, wn) holds row acc_row(v, l), column l % MF; the tile is written to LDS,
-// then each thread finishes four adjacent columns of a row at a time (16-byte
-// loads and stores), or one element at a time where that is not possible.
-template <int BM, int BN, int MF, int EPI, bool SPLIT, typename Acc, int FM, int FN>
+// WK * BM * CS floats, plus 2048 floats or, outside the 2x2 layout, BM * CS +
+// 8 * NT for the GroupNorm sums, and is free): block (i, j), register v, lane l
+// of wave (wm, wn, wk) holds row acc_row(v, l), column l % MF of its group's
+// partial sum; the K groups' tiles are added in LDS, then each thread finishes
+// four adjacent columns of a row at a time (16-byte loads and stores), or one
+// element at a time where that is not possible.
+template <int BM, int BN, int WM, int WN, int WK, int MF, int EPI, bool SPLIT, typename Acc, int FM, int FN>
 __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const Acc (&acc)[FM][FN], int m0, int n0,
-                                           int z) {
+                                           int z, const float *ln_st = nullptr) {
     using MI = Mf<MF>;
+    using L = Waves<BM, BN, WM, WN, WK>;
+    constexpr int NT = L::kThreads;
     // C tile row stride: the lane groups of one register's store sit 4 rows
     // apart (16x16 blocks: 16 columns per group) or 4 rows apart in two halves
     // (32x32: 32 columns); BN + 4 (resp. + 8) puts those groups on disjoint banks.
-    constexpr int CS = BN + (MF == 16 ? 4 : 8);
+    constexpr int CS = L::CS;
+    static_assert(MF == L::MF && FM == L::FM && FN == L::FN, "accumulators of the wave layout");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    int wm, wn, wk;
+    L::index(wave, wm, wn, wk);
     {
-        const int r0 = wm * (BM / 2), c0 = wn * (BN / 2) + (lane % MF);
+        float *slab = smem + wk * (BM * CS);
+        const int r0 = wm * L::TM, c0 = wn * L::TN + (lane % MF);
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j)
 #pragma unroll
                 for (int v = 0; v < MI::kAccRegs; ++v)
-                    smem[(r0 + i * MF + MI::acc_row(v, lane)) * CS + c0 + j * MF] = acc[i][j][v];
+                    slab[(r0 + i * MF + MI::acc_row(v, lane)) * CS + c0 + j * MF] = acc[i][j][v];
     }
     __syncthreads();
+    if constexpr (WK > 1) {  // K groups' partial tiles summed in group order into the first
+        constexpr int C4 = BN / 4;
+        for (int e = tid; e < BM * C4; e += NT) {
+            const int rr = e / C4, cc = (e - rr * C4) * 4;
+            float4 t = *reinterpret_cast<const float4 *>(smem + rr * CS + cc);
+#pragma unroll
+            for (int w = 1; w < WK; ++w) {
+                const float4 u = *reinterpret_cast<const float4 *>(smem + w * BM * CS + rr * CS + cc);
+                t.x += u.x, t.y += u.y, t.z += u.z, t.w += u.w;
+            }
+            *reinterpret_cast<float4 *>(smem + rr * CS + cc) = t;
+        }
+        __syncthreads();
+    }
     if (p.vec_out == 1) {
         constexpr int C4 = BN / 4;  // float4 per tile row
-        static_assert(BM * C4 % 256 == 0, "whole passes over the C tile");
-        // GroupNorm sums: a thread keeps one column quad over all its rows.
-        constexpr bool kGn = !SPLIT && 256 % C4 == 0;
-        float4 gs{0.f, 0.f, 0.f, 0.f}, gq = gs;
+        if constexpr (L::kFixedQuads) {
+            static_assert(BM * C4 % 256 == 0, "whole passes over the C tile");
+            // GroupNorm sums: a thread keeps one column quad over all its rows.
+            constexpr bool kGn = !SPLIT && 256 % C4 == 0;
+            float4 gs{0.f, 0.f, 0.f, 0.f}, gq = gs;
 #pragma unroll
-        for (int it = 0; it < BM * C4 / 256; ++it) {
-            const int e = tid + it * 256, rr = e / C4, cc = (e - rr * C4) * 4;
-            const int row = m0 + rr, col = n0 + cc;
-            if (row >= p.M || col >= p.N) continue;  // N % 4 == 0: the whole float4 is inside
-            const float4 v = *reinterpret_cast<const float4 *>(smem + rr * CS + cc);
-            if (SPLIT) {
-                *reinterpret_cast<float4 *>(p.partial + (int64_t(z) * p.M + row) * p.N + col) = v;
-            } else {
-                const float4 y = store4<EPI>(p, row, col, v);
-                if (kGn && p.gnp) {
-                    gs.x += y.x, gs.y += y.y, gs.z += y.z, gs.w += y.w;
-                    gq.x = __builtin_fmaf(y.x, y.x, gq.x);
-                    gq.y = __builtin_fmaf(y.y, y.y, gq.y);
-                    gq.z = __builtin_fmaf(y.z, y.z, gq.z);
-                    gq.w = __builtin_fmaf(y.w, y.w, gq.w);
+            for (int it = 0; it < BM * C4 / 256; ++it) {
+                const int e = tid + it * 256, rr = e / C4, cc = (e - rr * C4) * 4;
+                const int row = m0 + rr, col = n0 + cc;
+                if (row >= p.M || col >= p.N) continue;  // N % 4 == 0: the whole float4 is inside
+                float4 v = *reinterpret_cast<const float4 *>(smem + rr * CS + cc);
+                if (ln_st) v = ln_correct(p, ln_st, rr, col, v);
+                if (SPLIT) {
+                    *reinterpret_cast<float4 *>(p.partial + (int64_t(z) * p.M + row) * p.N + col) = v;
+                } else {
+                    const float4 y = store4<EPI>(p, row, col, v);
+                    if (kGn && p.gnp) {
+                        gs.x += y.x, gs.y += y.y, gs.z += y.z, gs.w += y.w;
+                        gq.x = __builtin_fmaf(y.x, y.x, gq.x);
+                        gq.y = __builtin_fmaf(y.y, y.y, gq.y);
+                        gq.z = __builtin_fmaf(y.z, y.z, gq.z);
+                        gq.w = __builtin_fmaf(y.w, y.w, gq.w);
+                    }
                 }
             }
-        }
-        if constexpr (kGn) {
-            if (p.gnp) gn_tile_partials<BM, BN>(p, smem, gs, gq, m0, n0);
+            if constexpr (kGn) {
+                if (p.gnp) gn_tile_partials<BM, BN>(p, smem, gs, gq, m0, n0);
+            }
+        } else {
+            const bool gn = !SPLIT && p.gnp;
+            for (int e = tid; e < BM * C4; e += NT) {
+                const int rr = e / C4, cc = (e - rr * C4) * 4;
+                const int row = m0 + rr, col = n0 + cc;
+                if (row >= p.M || col >= p.N) continue;
+                float *c = smem + rr * CS + cc;
+                float4 v = *reinterpret_cast<const float4 *>(c);
+                if (ln_st) v = ln_correct(p, ln_st, rr, col, v);
+                if (SPLIT) {
+                    *reinterpret_cast<float4 *>(p.partial + (int64_t(z) * p.M + row) * p.N + col) = v;
+                } else {
+                    const float4 y = store4<EPI>(p, row, col, v);
+                    if (gn) *reinterpret_cast<float4 *>(c) = y;  // the stored values, for the sums
+                }
+            }
+            if (gn) {
+                __syncthreads();
+                gn_tile_partials_lds<BM, BN, NT, CS>(p, smem, m0, n0);
+            }
         }
     } else if (p.vec_out == 2) {
         // Grouped rows (out index (row / rg) * ldc + col * rg + row % rg, rg % 4 == 0,
@@ -563,7 +725,7 @@ __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const
         // floats, written as one 16-byte store; consecutive threads take the group's
         // row quads, then columns, so a wave writes contiguous runs.
         const int rq = p.rg >> 2;
-        for (int e = tid; e < BM * BN / 4; e += 256) {
+        for (int e = tid; e < BM * BN / 4; e += NT) {
             const int hq = e % rq, rest = e / rq, cc = rest % BN, rr = (rest / BN) * p.rg + hq * 4;
             const int row = m0 + rr, col = n0 + cc;
             if (row >= p.M || col >= p.N) continue;  // M % rg == 0: the whole quad is inside
@@ -578,7 +740,7 @@ __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const
         // One element per thread and pass; consecutive threads take consecutive
         // rows when rows are grouped (their outputs are adjacent), else columns.
         const bool by_row = p.rg > 1;
-        for (int e = tid; e < BM * BN; e += 256) {
+        for (int e = tid; e < BM * BN; e += NT) {
             const int rr = by_row ? e % BM : e / BN, cc = by_row ? e / BM : e % BN;
             const int row = m0 + rr, col = n0 + cc;
             if (row >= p.M || col >= p.N) continue;
@@ -594,11 +756,20 @@ __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const
     }
 }
 
-template <int BM, int BN, int MODE, bool PRO, bool F16, bool BVEC, int EPI, bool SPLIT>
-__global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
-    constexpr int MF = mf_for<BM, BN>();
+template <int BM, int BN, int WM, int WN, int WK, int MODE, int PRO, bool F16, bool BVEC, int EPI, bool SPLIT,
+          bool PIPE = false, int BKT = BK>
+__global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(GemmArgs p) {
+    using L = Waves<BM, BN, WM, WN, WK>;
+    constexpr int NT = L::kThreads;
+    constexpr int MF = L::MF;
     using MI = Mf<MF>;
-    constexpr int FM = BM / 2 / MF, FN = BN / 2 / MF;  // MF x MF blocks per wave
+    constexpr int FM = L::FM, FN = L::FN;  // MF x MF blocks per wave
+    // K per LDS stage: BK, or 16 for dense operands in the wide layouts (half
+    // the staging registers and LDS, so big wave tiles keep several waves per SIMD)
+    static_assert(BKT == BK || (BKT == 16 && MODE == kDense), "16-deep stages for dense operands only");
+    constexpr int K4T = BKT / 4;           // float4 per tile row
+    constexpr int KW = BKT / WK;           // K of each LDS stage per wave group
+    static_assert(KW % MI::kKStep == 0, "whole float4 steps per wave group");
     const int tiles_m = (p.M + BM - 1) / BM;
     const int tiles_n = (p.N + BN - 1) / BN;
     const TileIdx ti = tile_index(tiles_m, tiles_n);
@@ -609,35 +780,54 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
         p.out += bz * p.c_bs;
         if (p.res) p.res += bz * p.c_bs;
     }
-    constexpr int A_LD = BM * K4 / 256, B_LD = BN * K4 / 256;
+    // Load slots: NT / K4 rows per pass, one float4 column each; the last pass of
+    // a tile whose rows are not a multiple of that is partial.
+    constexpr int RPP = NT / K4T;
+    constexpr int A_LD = (BM + RPP - 1) / RPP, B_LD = (BN + RPP - 1) / RPP;
     // Two LDS stages: tile kt+1 is written while tile kt is read, one barrier
     // per K tile. The epilogue reuses the space for the C tile (row stride CS:
     // the two row halves of a 32x32 block's store fall on different banks).
-    constexpr int CS = BN + 8;
+    constexpr int CS = L::CS;
     // LDS row stride: BK + 4 for the 32x32 instruction; the 16x16 instruction's
     // lane layout (rows l % 16, K offsets 4 * (l / 16)) took 10% of its LDS
     // cycles in bank conflicts at that stride, and BK + 8 is 0.5% faster over a
     // UNet step (BK + 12 and + 20 cost a workgroup of occupancy and are slower).
-    constexpr int LDS_S = MF == 16 ? BK + 8 : BK + 4;
-    constexpr int SMEM = 2 * (BM + BN) * LDS_S;
-    static_assert(BM * CS <= SMEM && SMEM >= 2048, "C tile and GroupNorm sums must fit in the staging space");
+    // (16-deep stages: BKT + 4, whose 80-byte rows put the 16 rows one read
+    // instruction touches on distinct bank quads.)
+    constexpr int LDS_S = BKT == 16 ? BKT + 4 : (MF == 16 ? BK + 8 : BK + 4);
+    // The pipelined loop stores every load slot (rows past the tile land in
+    // padding rows, read by no wave), so its loop body has no branch.
+    constexpr int BMP = PIPE ? A_LD * RPP : BM, BNP = PIPE ? B_LD * RPP : BN;
+    constexpr int STAGES = 2 * (BMP + BNP) * LDS_S;
+    constexpr int EPI_F = L::kFixedQuads ? WK * BM * CS : (WK * BM * CS > BM * CS + 8 * NT ? WK * BM * CS
+                                                                                        : BM * CS + 8 * NT);
+    // The epilogue reuses the staging space: C tile (and GroupNorm sums past it).
+    constexpr int SMEM = STAGES > EPI_F ? (STAGES > 2048 ? STAGES : 2048) : (EPI_F > 2048 ? EPI_F : 2048);
+    static_assert(WK * BM * CS <= SMEM && SMEM >= 2048, "C tile and GroupNorm sums must fit in the staging space");
+    static_assert(L::kFixedQuads || BM * CS + 8 * NT <= SMEM, "GroupNorm sums past the C tile");
     __shared__ float smem[SMEM];
-    float(*As)[BM * LDS_S] = reinterpret_cast<float(*)[BM * LDS_S]>(smem);
-    float(*Bs)[BN * LDS_S] = reinterpret_cast<float(*)[BN * LDS_S]>(smem + 2 * BM * LDS_S);
+    float(*As)[BMP * LDS_S] = reinterpret_cast<float(*)[BMP * LDS_S]>(smem);
+    float(*Bs)[BNP * LDS_S] = reinterpret_cast<float(*)[BNP * LDS_S]>(smem + 2 * BMP * LDS_S);
 
     const int m0 = ti.tm * BM, n0 = ti.tn * BN;
     const int k_begin = SPLIT ? ti.z * p.k_split : 0;
     const int k_end = SPLIT ? min(p.K, k_begin + p.k_split) : p.K;
-    const int ktiles = (k_end - k_begin + BK - 1) / BK;
+    const int ktiles = (k_end - k_begin + BKT - 1) / BKT;
 
     const int tid = threadIdx.x;
-    const int lrow = tid >> 3, lc4 = tid & 7;  // load slot: row within 32-row pass, float4 column
+    const int lrow = tid / K4T, lc4 = tid % K4T;  // load slot: row within a pass, float4 column
+    // Slot i holds tile row lrow + RPP * i when that is inside the tile; a slot
+    // past it loads from row M / column N (out of range: zeros) and is not stored.
+    auto a_in = [&](int i) { return BM % RPP == 0 || i + 1 < A_LD || lrow + RPP * i < BM; };
+    auto b_in = [&](int i) { return BN % RPP == 0 || i + 1 < B_LD || lrow + RPP * i < BN; };
 
     ConvRow crow[A_LD];
+    int arow[A_LD];
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
-        if (MODE >= kConvAligned) crow[i] = conv_row(p, m0 + lrow + 32 * i);
-        else if (PRO) crow[i] = ConvRow{min(m0 + lrow + 32 * i, p.M - 1) / p.pro_rows, 0, 0, true};
+        arow[i] = a_in(i) ? m0 + lrow + RPP * i : p.M;
+        if (MODE >= kConvAligned) crow[i] = conv_row(p, arow[i]);
+        else if (PRO == kProAffine) crow[i] = ConvRow{min(arow[i], p.M - 1) / p.pro_rows, 0, 0, true};
         else crow[i] = ConvRow{0, 0, 0, true};
     }
 
@@ -647,8 +837,11 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
     // Two register stages (tiles kt+1 and kt+2 in flight while LDS stage kt&1
     // is consumed), two LDS stages: a load has two compute phases to land.
     floatx4 ra0[A_LD], rb0[B_LD], ra1[A_LD], rb1[B_LD];
+    double ln_s1[A_LD], ln_s2[A_LD];  // kProLn: this thread's share of each slot row's sum and sum of squares
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) ln_s1[i] = ln_s2[i] = 0.0;
     auto fetch = [&](int kt, floatx4 (&ra)[A_LD], floatx4 (&rb)[B_LD]) {
-        const int k0 = k_begin + kt * BK;
+        const int k0 = k_begin + kt * BKT;
         int tky = 0, tkx = 0, tci = 0;
         if (MODE == kConvAligned) {
             const int tap = k0 / p.ci;
@@ -657,34 +850,43 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
             tkx = tap - tky * 3;
         }
         const int k = k0 + lc4 * 4;
-        // a tile past ka reads the second operand (whole tiles: ka % BK == 0)
+        // a tile past ka reads the second operand (whole tiles: ka % BKT == 0)
         const bool sec = MODE == kDense && p.a2 && k0 >= p.ka;
 #pragma unroll
         for (int i = 0; i < A_LD; ++i) {
             if constexpr (MODE == kDense)
-                ra[i] = sec ? load_a_buf<MODE, PRO>(p, a2_rsrc, crow[i], m0 + lrow + 32 * i, k - p.ka, k_end - p.ka,
-                                                    tky, tkx, tci, p.lda2)
-                            : load_a_buf<MODE, PRO>(p, a_rsrc, crow[i], m0 + lrow + 32 * i, k, k_end, tky, tkx, tci);
+                ra[i] = sec ? load_a_buf<MODE, PRO>(p, a2_rsrc, crow[i], arow[i], k - p.ka, k_end - p.ka, tky, tkx, tci,
+                                                    p.lda2)
+                            : load_a_buf<MODE, PRO>(p, a_rsrc, crow[i], arow[i], k, k_end, tky, tkx, tci);
             else if constexpr (MODE == kConvAligned || MODE == kConvVec)
-                ra[i] = load_a_buf<MODE, PRO>(p, a_rsrc, crow[i], m0 + lrow + 32 * i, k, k_end, tky, tkx, tci);
+                ra[i] = load_a_buf<MODE, PRO>(p, a_rsrc, crow[i], arow[i], k, k_end, tky, tkx, tci);
             else
-                ra[i] = (k < k_end) ? load_a<MODE, PRO>(p, crow[i], m0 + lrow + 32 * i, k, tky, tkx, tci) : zero4();
+                ra[i] = (k < k_end) ? load_a<MODE, PRO>(p, crow[i], arow[i], k, tky, tkx, tci) : zero4();
+        }
+        if constexpr (PRO == kProLn) {  // row sums of the values as loaded (zeros outside the operand)
+#pragma unroll
+            for (int i = 0; i < A_LD; ++i) {
+                const double a0 = ra[i][0], a1 = ra[i][1], a2 = ra[i][2], a3 = ra[i][3];
+                ln_s1[i] += (a0 + a1) + (a2 + a3);
+                ln_s2[i] += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
+            }
         }
 #pragma unroll
         for (int i = 0; i < B_LD; ++i) {
+            const int n = b_in(i) ? n0 + lrow + RPP * i : p.N;
             if constexpr (BVEC)
-                rb[i] = load_b_buf<F16>(p, b_rsrc, n0 + lrow + 32 * i, k, k_end);
+                rb[i] = load_b_buf<F16>(p, b_rsrc, n, k, k_end);
             else
-                rb[i] = (k < k_end) ? load_b<F16, BVEC>(p, n0 + lrow + 32 * i, k) : zero4();
+                rb[i] = (k < k_end) ? load_b<F16, BVEC>(p, n, k) : zero4();
         }
     };
     auto stash = [&](int buf, const floatx4 (&ra)[A_LD], const floatx4 (&rb)[B_LD]) {
 #pragma unroll
         for (int i = 0; i < A_LD; ++i)
-            *reinterpret_cast<floatx4 *>(As[buf] + (lrow + 32 * i) * LDS_S + lc4 * 4) = ra[i];
+            if (PIPE || a_in(i)) *reinterpret_cast<floatx4 *>(As[buf] + (lrow + RPP * i) * LDS_S + lc4 * 4) = ra[i];
 #pragma unroll
         for (int i = 0; i < B_LD; ++i)
-            *reinterpret_cast<floatx4 *>(Bs[buf] + (lrow + 32 * i) * LDS_S + lc4 * 4) = rb[i];
+            if (PIPE || b_in(i)) *reinterpret_cast<floatx4 *>(Bs[buf] + (lrow + RPP * i) * LDS_S + lc4 * 4) = rb[i];
     };
 
     typename MI::Acc acc[FM][FN];
@@ -696,16 +898,18 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
             for (int v = 0; v < MI::kAccRegs; ++v) acc[i][j][v] = 0.f;
 
     // Lane l reads a float4 along K at row l % MF, K offset 4 * (l / MF): the
-    // four lane groups (two for 32x32) each cover 4 consecutive K.
+    // four lane groups (two for 32x32) each cover 4 consecutive K. Wave group
+    // wk takes K columns [wk * KW, (wk + 1) * KW) of every stage.
     const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int a_off = (wm * (BM / 2) + (lane % MF)) * LDS_S + (lane / MF) * 4;
-    const int b_off = (wn * (BN / 2) + (lane % MF)) * LDS_S + (lane / MF) * 4;
+    int wm, wn, wk;
+    L::index(wave, wm, wn, wk);
+    const int a_off = (wm * L::TM + (lane % MF)) * LDS_S + (lane / MF) * 4 + wk * KW;
+    const int b_off = (wn * L::TN + (lane % MF)) * LDS_S + (lane / MF) * 4 + wk * KW;
     auto compute = [&](int buf) {
         const float *as_w = As[buf] + a_off;
         const float *bs_w = Bs[buf] + b_off;
 #pragma unroll
-        for (int kk = 0; kk < BK; kk += MI::kKStep) {
+        for (int kk = 0; kk < KW; kk += MI::kKStep) {
             floatx4 a[FM], b[FN];
 #pragma unroll
             for (int i = 0; i < FM; ++i) a[i] = *reinterpret_cast<const floatx4 *>(as_w + i * MF * LDS_S + kk);
@@ -720,42 +924,104 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmArgs p) {
         }
     };
 
-    // Even half: LDS 0 holds tile kt, registers 1 hold kt+1, registers 0 kt+2.
-    // Odd half: LDS 1 holds kt+1, registers 0 hold kt+2, registers 1 kt+3.
-    // Tiles past the end are fetched as zeros (out-of-range offsets) and never
-    // computed; the loop body has no per-tile conditions, so the compiler waits
-    // only for the older register stage before each LDS store.
-    fetch(0, ra0, rb0);
-    fetch(1, ra1, rb1);
-    stash(0, ra0, rb0);
-    fetch(2, ra0, rb0);
-    __syncthreads();
-    int kt = 0;
-    for (; kt + 3 < ktiles; kt += 2) {  // four or more tiles left: one pair, no exits inside
-        compute(0);
-        stash(1, ra1, rb1);
-        fetch(kt + 3, ra1, rb1);
-        __syncthreads();
-        compute(1);
+    if constexpr (PIPE) {
+        // One wave per SIMD (the wide layouts): the products of tile t run from
+        // fragments already in registers, after the barrier that publishes tile
+        // t+1 and after issuing that tile's fragment reads, its successor's LDS
+        // store and the next global loads, so the matrix unit covers the barrier,
+        // the LDS latency and the load issue. Two LDS stages, two register stages
+        // (a global load has a whole iteration to land) and two fragment sets.
+        // An LDS stage is rewritten only after a barrier that every wave passed
+        // with its fragments of that stage's previous tile in registers.
+        constexpr int KS = KW / MI::kKStep;  // float4 steps per stage and wave
+        floatx4 fa0[KS][FM], fb0[KS][FN], fa1[KS][FM], fb1[KS][FN];
+        auto read_frag = [&](int buf, floatx4 (&fa)[KS][FM], floatx4 (&fb)[KS][FN]) {
+            const float *as_w = As[buf] + a_off;
+            const float *bs_w = Bs[buf] + b_off;
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+#pragma unroll
+                for (int i = 0; i < FM; ++i)
+                    fa[s][i] = *reinterpret_cast<const floatx4 *>(as_w + i * MF * LDS_S + s * MI::kKStep);
+#pragma unroll
+                for (int j = 0; j < FN; ++j)
+                    fb[s][j] = *reinterpret_cast<const floatx4 *>(bs_w + j * MF * LDS_S + s * MI::kKStep);
+            }
+        };
+        auto products = [&](const floatx4 (&fa)[KS][FM], const floatx4 (&fb)[KS][FN]) {
+#pragma unroll
+            for (int s = 0; s < KS; ++s)
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+#pragma unroll
+                    for (int i = 0; i < FM; ++i)
+#pragma unroll
+                        for (int j = 0; j < FN; ++j) acc[i][j] = MI::mfma(fa[s][i][t], fb[s][j][t], acc[i][j]);
+        };
+        // Tiles past the end are fetched as zeros and never multiplied.
+        fetch(0, ra0, rb0);
+        fetch(1, ra1, rb1);
         stash(0, ra0, rb0);
-        fetch(kt + 4, ra0, rb0);
+        fetch(2, ra0, rb0);
         __syncthreads();
-    }
-    // one to three tiles left: kt in LDS 0, kt+1 in registers 1, kt+2 in registers 0
-    compute(0);
-    if (kt + 1 < ktiles) {
-        stash(1, ra1, rb1);
-        __syncthreads();
-        compute(1);
-        if (kt + 2 < ktiles) {
-            stash(0, ra0, rb0);
+        read_frag(0, fa0, fb0);
+        int t = 0;
+        for (; t + 2 <= ktiles; t += 2) {
+            stash(1, ra1, rb1);  // tile t+1
+            fetch(t + 3, ra1, rb1);
             __syncthreads();
+            read_frag(1, fa1, fb1);
+            products(fa0, fb0);  // tile t
+            stash(0, ra0, rb0);  // tile t+2
+            fetch(t + 4, ra0, rb0);
+            __syncthreads();
+            read_frag(0, fa0, fb0);
+            products(fa1, fb1);  // tile t+1
+        }
+        if (t < ktiles) products(fa0, fb0);  // an odd count: the last tile
+    } else {
+        // Even half: LDS 0 holds tile kt, registers 1 hold kt+1, registers 0 kt+2.
+        // Odd half: LDS 1 holds kt+1, registers 0 hold kt+2, registers 1 kt+3.
+        // Tiles past the end are fetched as zeros (out-of-range offsets) and never
+        // computed; the loop body has no per-tile conditions, so the compiler waits
+        // only for the older register stage before each LDS store.
+        fetch(0, ra0, rb0);
+        fetch(1, ra1, rb1);
+        stash(0, ra0, rb0);
+        fetch(2, ra0, rb0);
+        __syncthreads();
+        int kt = 0;
+        for (; kt + 3 < ktiles; kt += 2) {  // four or more tiles left: one pair, no exits inside
             compute(0);
+            stash(1, ra1, rb1);
+            fetch(kt + 3, ra1, rb1);
+            __syncthreads();
+            compute(1);
+            stash(0, ra0, rb0);
+            fetch(kt + 4, ra0, rb0);
+            __syncthreads();
+        }
+        // one to three tiles left: kt in LDS 0, kt+1 in registers 1, kt+2 in registers 0
+        compute(0);
+        if (kt + 1 < ktiles) {
+            stash(1, ra1, rb1);
+            __syncthreads();
+            compute(1);
+            if (kt + 2 < ktiles) {
+                stash(0, ra0, rb0);
+                __syncthreads();
+                compute(0);
+            }
         }
     }
 
+    // kProLn: each row's mean and 1 / sqrt(var + eps) from the sums of its K4T
+    // load lanes (adjacent lanes of one wave), in f64, for the epilogue.
+    __shared__ float ln_st[PRO == kProLn ? 2 * BM : 1];
+    if constexpr (PRO == kProLn)
+        ln_row_stats<A_LD, RPP, K4T, BM>(p, ln_s1, ln_s2, lrow, lc4, ln_st);
     __syncthreads();
-    write_tile<BM, BN, MF, EPI, SPLIT>(p, smem, acc, m0, n0, ti.z);
+    write_tile<BM, BN, WM, WN, WK, MF, EPI, SPLIT>(p, smem, acc, m0, n0, ti.z, PRO == kProLn ? ln_st : nullptr);
 }
 
 // Sums split-K partials in split order, then (residual + bias) + sum [SiLU].
@@ -799,15 +1065,20 @@ inline bool reduce_vec_ok(const GemmArgs &p) {
 
 struct Plan {
     int bm, bn, splits, k_split;
+    int wm = 2, wn = 2, wk = 1;  // wave layout (Waves)
+    int pipe = 0;                // 1: the pipelined main loop (gemm_f32_kernel PIPE)
+    int bk = BK;                 // K per LDS stage (gemm_f32_kernel BKT)
 };
 
 // Keeps the GroupNorm partials request (GemmArgs::gnp) when a BM x BN tiling
-// without K split can honour it: one output, plain rows, 16-byte stores, a
-// fixed column quad per epilogue thread, tiles inside one item.
-inline void gn_partials_plan(GemmArgs &p, int bm, int bn, int splits, int batch) {
+// without K split can honour it: one output, plain rows, 16-byte stores, tiles
+// inside one item, and in the 2x2 wave layout a fixed column quad per epilogue
+// thread (square: 256 % (BN / 4) == 0); other layouts sum from LDS, any width.
+inline void gn_partials_plan(GemmArgs &p, int bm, int bn, int splits, int batch, bool square = true) {
     p.gn_rows = 0;
     if (!p.gnp) return;
-    const bool ok = splits == 1 && batch == 1 && p.vec_out == 1 && p.nseg == 0 && p.rg <= 1 && 256 % (bn / 4) == 0 &&
+    const bool ok = splits == 1 && batch == 1 && p.vec_out == 1 && p.nseg == 0 && p.rg <= 1 &&
+                    (!square || 256 % (bn / 4) == 0) &&
                     p.gn_item_rows > 0 && p.gn_item_rows % bm == 0 && p.M % p.gn_item_rows == 0 &&
                     (reinterpret_cast<uintptr_t>(p.gnp) & 15) == 0;
     if (ok) p.gn_rows = bm;
@@ -866,31 +1137,61 @@ inline Plan plan_for(int M, int N, int K, int cus, bool dense) {
     return Plan{64, 64, s.first, s.first > 1 ? s.second : K};
 }
 
+// Wide-layout plan for a dense GEMM with vector f32 weights, or bm = 0 to keep
+// plan_for's. Timed inside the UNet step (kernel trace of a whole step, each
+// GEMM in its place: cold weights, its producer's output just written back),
+// which is not what a GEMM repeated on its own operands measures: of the
+// layouts that beat the square tilings alone, these two also win in the step:
+//  - the MixFFN's inverted 1x1 at 32x32 latents (N >= 3200, M >= 2048):
+//    64x80 tiles of four 16x80 waves, pipelined loop (2048x3200x640: 79.8
+//    against 84.2 us per launch);
+//  - batched products of M <= 512 rows (the 16-plane Winograd GEMM of the
+//    16x16 -> 32x32 upsample conv, 16 x 512x1280x1280): 64x80 tiles (224.5
+//    against 248.9 us).
+// Elsewhere the square tilings stay: in the step the wide layouts lost 5-60 us
+// per shape (the 512-row GEMMs at K >= 1920 against the K-split tilings, the
+// 8192x320 and 2048x640 GEMMs at K >= 640, the 512x6400 inverted 1x1).
+inline Plan plan_wide(int M, int N, int K, int cus, int batch) {
+    auto wide = [&](int bm, int bn, int wm, int wn, int wk, int pipe) {
+        Plan p{bm, bn, 1, K, wm, wn, wk, pipe, BK};
+        return p;
+    };
+    if (N % 80) return Plan{0, 0, 1, K};
+    const int64_t t64 = ceil_div(M, 64) * ceil_div(N, 80);
+    if (batch == 1 && N >= 3200 && M >= 2048 && t64 >= 2 * int64_t(cus)) return wide(64, 80, 4, 1, 1, 1);
+    if (batch > 1 && M <= 512 && K >= 640 && t64 >= 2 * int64_t(cus)) return wide(64, 80, 4, 1, 1, 0);
+    return Plan{0, 0, 1, K};
+}
+
 // The launch census (Tuning::gemm_log): one line per GEMM launch with its shape,
 // tiling and epilogue, in launch order, to match against a kernel trace.
 inline void log_gemm(const Context &ctx, const char *family, const GemmArgs &p, int bm, int bn, int splits, int mode,
-                     bool pro, bool f16, GemmEpilogue epi, int batch) {
+                     int pro, bool f16, GemmEpilogue epi, int batch, int wm = 2, int wn = 2, int wk = 1) {
     if (!ctx.tune.gemm_log) return;
     std::fprintf(stderr,
-                 "[gemm] %s M=%d N=%d K=%d batch=%d tile=%dx%d splits=%d mode=%d pro=%d f16w=%d silu=%d bias=%d "
-                 "res=%d rsc=%d res2=%d gnp=%d nseg=%d rg=%d a2=%d\n",
-                 family, p.M, p.N, p.K, batch, bm, bn, splits, mode, int(pro), int(f16), int(epi == GemmEpilogue::Silu),
+                 "[gemm] %s M=%d N=%d K=%d batch=%d tile=%dx%d waves=%dx%dx%d splits=%d mode=%d pro=%d f16w=%d "
+                 "silu=%d bias=%d res=%d rsc=%d res2=%d gnp=%d nseg=%d rg=%d a2=%d\n",
+                 family, p.M, p.N, p.K, batch, bm, bn, wm, wn, wk, splits, mode, int(pro), int(f16),
+                 int(epi == GemmEpilogue::Silu),
                  int(p.bias != nullptr), int(p.res != nullptr), int(p.rsc != nullptr), int(p.res2 != nullptr),
                  int(p.gnp != nullptr), p.nseg, p.rg, int(p.a2 != nullptr));
 }
 
-template <int BM, int BN, int MODE, bool PRO, bool F16, bool BVEC>
+template <int BM, int BN, int WM, int WN, int WK, int MODE, int PRO, bool F16, bool BVEC, bool PIPE = false,
+          int BKT = BK>
 void launch_cfg(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int batch) {
+    constexpr int NT = Waves<BM, BN, WM, WN, WK>::kThreads;
+    constexpr bool kSquare = Waves<BM, BN, WM, WN, WK>::kFixedQuads;
     const unsigned tiles = unsigned(ceil_div(p.M, BM) * ceil_div(p.N, BN));
-    log_gemm(ctx, "f32", p, BM, BN, pl.splits, MODE, PRO, F16, epi, batch);
+    log_gemm(ctx, PIPE ? "f32p" : "f32", p, BM, BN, pl.splits, MODE, PRO, F16, epi, batch, WM, WN, WK);
     if (pl.splits > 1) {
         const size_t bytes = size_t(pl.splits) * p.M * p.N * sizeof(float);
         p.partial = static_cast<float *>(ctx.ws.get(bytes, ctx.stream));
         p.k_split = pl.k_split;
         p.vec_out = (p.N & 3) == 0 && (reinterpret_cast<uintptr_t>(p.partial) & 15) == 0;
-        gn_partials_plan(p, BM, BN, pl.splits, batch);
+        gn_partials_plan(p, BM, BN, pl.splits, batch, kSquare);
         dim3 grid(tiles, 1, pl.splits);
-        gemm_f32_kernel<BM, BN, MODE, PRO, F16, BVEC, 0, true><<<grid, 256, 0, ctx.stream>>>(p);
+        gemm_f32_kernel<BM, BN, WM, WN, WK, MODE, PRO, F16, BVEC, 0, true, PIPE, BKT><<<grid, NT, 0, ctx.stream>>>(p);
         MH_LAUNCH_CHECK();
         const int64_t total = int64_t(p.M) * p.N;
         if (reduce_vec_ok(p)) {
@@ -909,69 +1210,131 @@ void launch_cfg(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int
     } else {
         p.k_split = p.K;
         p.vec_out = out_vec_ok(p, BM);
-        gn_partials_plan(p, BM, BN, 1, batch);
+        gn_partials_plan(p, BM, BN, 1, batch, kSquare);
         const dim3 grid(tiles, unsigned(batch));
         // The SiLU epilogue is only instantiated for dense operands (the convs never use it).
         if constexpr (MODE <= kDenseScalar) {
             if (epi == GemmEpilogue::Silu) {
-                gemm_f32_kernel<BM, BN, MODE, PRO, F16, BVEC, 1, false><<<grid, 256, 0, ctx.stream>>>(p);
+                gemm_f32_kernel<BM, BN, WM, WN, WK, MODE, PRO, F16, BVEC, 1, false, PIPE, BKT><<<grid, NT, 0, ctx.stream>>>(p);
                 MH_LAUNCH_CHECK();
                 return;
             }
         } else {
             MH_REQUIRE(epi == GemmEpilogue::None, "conv GEMM: SiLU epilogue not available");
         }
-        gemm_f32_kernel<BM, BN, MODE, PRO, F16, BVEC, 0, false><<<grid, 256, 0, ctx.stream>>>(p);
+        gemm_f32_kernel<BM, BN, WM, WN, WK, MODE, PRO, F16, BVEC, 0, false, PIPE, BKT><<<grid, NT, 0, ctx.stream>>>(p);
     }
     MH_LAUNCH_CHECK();
 }
 
-template <int MODE, bool PRO, bool F16, bool BVEC>
+// Wide wave layouts for dense operands with vector f32 weight rows: large
+// per-wave tiles (16 or 32 rows x 80 columns, 48 x 48, 80 x 32) and grids of
+// about one workgroup per CU, where the 2x2 layout of the square tiles needs
+// many small workgroups (a 32x32 tile moves 8 KB per 64 KFLOP of products; a
+// 128x80 tile 26 KB per 655 KFLOP). Entries: bm, bn, wm, wn, wk.
+constexpr int kWide[][7] = {
+    // bm, bn, wm, wn, wk, pipelined loop, K per stage: the planner's two
+    // (64x80 of four 16x80 waves, plain and pipelined), and one of each other
+    // code path (partial load passes, K split over wave groups, 16-deep stages)
+    // for the gemm_plan tuning and the tests
+    {64, 80, 4, 1, 1, 1, 32},
+    {64, 80, 4, 1, 1, 0, 32},
+    {128, 80, 4, 1, 1, 1, 32},  // waves 32x80
+    {64, 160, 2, 2, 1, 1, 32},  // waves 32x80
+    {32, 80, 2, 1, 2, 1, 32},   // waves 16x80, K split over two wave groups
+    {32, 80, 2, 1, 2, 0, 32},
+    {160, 64, 2, 2, 1, 1, 32},  // waves 80x32
+    {160, 64, 2, 2, 1, 1, 16},  // 16-deep stages
+    {64, 80, 4, 1, 1, 0, 16},
+    {128, 128, 2, 2, 1, 1, 16},
+};
+constexpr int kWideCount = int(sizeof(kWide) / sizeof(kWide[0]));
+
+inline int wide_index(const Plan &pl) {
+    for (int i = 0; i < kWideCount; ++i)
+        if (kWide[i][0] == pl.bm && kWide[i][1] == pl.bn && kWide[i][2] == pl.wm && kWide[i][3] == pl.wn &&
+            kWide[i][4] == pl.wk && kWide[i][5] == pl.pipe && kWide[i][6] == pl.bk)
+            return i;
+    return -1;
+}
+
+template <int I, int MODE, int PRO, bool F16, bool BVEC>
+void launch_wide(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int batch, int idx) {
+    if constexpr (I < kWideCount) {
+        if (idx == I) {
+            launch_cfg<kWide[I][0], kWide[I][1], kWide[I][2], kWide[I][3], kWide[I][4], MODE, PRO, F16, BVEC,
+                       kWide[I][5] != 0, kWide[I][6]>(ctx, p, pl, epi, batch);
+            return;
+        }
+        launch_wide<I + 1, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch, idx);
+    }
+}
+
+template <int MODE, int PRO, bool F16, bool BVEC>
 void launch_tiles(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
     Plan pl = plan_for(p.M, p.N, p.K, int(ceil_div(ctx.cu_count, batch)), MODE <= kDenseScalar);
-    // The context's gemm_plan tuning ("bm,bn,splits") forces the tiling (tuning and
-    // A/B runs), as MOEBIUS_GEMM selects the CPU engine's GEMM backend
+    constexpr bool kWideOk = MODE == kDense && BVEC && !F16;
+    if constexpr (kWideOk) {
+        const Plan w = ctx.tune.gemm_wide ? plan_wide(p.M, p.N, p.K, int(ceil_div(ctx.cu_count, batch)), batch)
+                                          : Plan{0, 0, 1, p.K};
+        if (w.bm) pl = w;
+    }
+    // The context's gemm_plan tuning ("bm,bn,splits[,wm,wn,wk]") forces the tiling
+    // (tuning and A/B runs), as MOEBIUS_GEMM selects the CPU engine's GEMM backend
     // (src/engine/gemm.rs:57-60).
     if (ctx.tune.gemm_splits > 0) {
         const int bm = ctx.tune.gemm_bm, bn = ctx.tune.gemm_bn, sp = ctx.tune.gemm_splits;
-        const bool parsed = true;
+        Plan f{bm, bn, 1, p.K, ctx.tune.gemm_wm, ctx.tune.gemm_wn, ctx.tune.gemm_wk, ctx.tune.gemm_pipe,
+               ctx.tune.gemm_bk};
         const bool square = (bm == 32 || bm == 64 || bm == 128) && (bn == 32 || bn == 64 || bn == 128) &&
-                            (bm == 32) == (bn == 32);
-        const bool wide = (bm == 32 && bn == 64) || (bm == 64 && bn == 32);
-        if (parsed && (square || (wide && MODE == kDense && BVEC))) {
+                            (bm == 32) == (bn == 32) && f.wm == 2 && f.wn == 2 && f.wk == 1 && !f.pipe &&
+                            f.bk == BK;
+        const bool wide = ((bm == 32 && bn == 64) || (bm == 64 && bn == 32)) && f.wm == 2 && f.wn == 2 && f.wk == 1 &&
+                          !f.pipe && f.bk == BK;
+        if (square || (wide && MODE == kDense && BVEC) || (kWideOk && wide_index(f) >= 0)) {
             const int ktiles = int(ceil_div(p.K, BK));
             const int per = int(ceil_div(ktiles, sp));
-            pl = Plan{bm, bn, int(ceil_div(ktiles, per)), per * BK};
+            f.splits = int(ceil_div(ktiles, per));
+            f.k_split = per * BK;
+            pl = f;
         }
     }
-    if (batch > 1) pl.splits = 1;
+    if (batch > 1 || PRO == kProLn) pl.splits = 1;  // the folded LayerNorm needs whole rows of K
+    if (pl.splits == 1) pl.k_split = p.K;
+    if constexpr (kWideOk) {
+        const int wi = wide_index(pl);
+        if (wi >= 0) {
+            launch_wide<0, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch, wi);
+            return;
+        }
+    }
     if constexpr (MODE == kDense && BVEC) {  // 32x64 / 64x32 tiles: vector dense operands only
         if (pl.bm == 32 && pl.bn == 64) {
-            launch_cfg<32, 64, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
+            launch_cfg<32, 64, 2, 2, 1, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
             return;
         }
         if (pl.bm == 64 && pl.bn == 32) {
-            launch_cfg<64, 32, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
+            launch_cfg<64, 32, 2, 2, 1, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
             return;
         }
     }
     if constexpr (MODE <= kDenseScalar) {  // small tiles for the small dense GEMMs only
         if (pl.bm == 32) {
-            launch_cfg<32, 32, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
+            launch_cfg<32, 32, 2, 2, 1, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
             return;
         }
     }
     if (pl.bm == 128 && pl.bn == 128)
-        launch_cfg<128, 128, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
+        launch_cfg<128, 128, 2, 2, 1, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
     else if (pl.bm == 128)
-        launch_cfg<128, 64, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
+        launch_cfg<128, 64, 2, 2, 1, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
     else if (pl.bn == 128)
-        launch_cfg<64, 128, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
+        launch_cfg<64, 128, 2, 2, 1, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
     else
-        launch_cfg<64, 64, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
+        launch_cfg<64, 64, 2, 2, 1, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
 }
 
-template <int MODE, bool PRO>
+template <int MODE, int PRO>
 void launch_b(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi, int batch = 1) {
     const int esz = wt == kF16 ? 2 : 4;
     const bool bvec = p.K % 4 == 0 && p.ldb % 4 == 0 && (reinterpret_cast<uintptr_t>(p.b) % (4 * esz)) == 0 &&

@@ -122,6 +122,28 @@ void conv3x3_output_hw(int h, int w, int stride, const int pad[4], bool upsample
 // whose output columns land in nseg (<= 3) separate [pixels][widths[i]] buffers.
 void conv1x1_segments(Context &ctx, const float *x, int64_t pixels, int c_in, const void *weight, WeightType wt,
                       const float *bias, int nseg, const int *widths, float *const *outs);
+// LayerNorm folded into a 1x1 conv (LayerNorm 1 -> q | k | v and LayerNorm 3 ->
+// MixFFN inverted, src/unet/transformer.rs:100-126): out = LayerNorm(x) . W^T + b,
+// computed as rstd . (x . W'^T - mean . c1) + c2 with W' = W . diag(gamma),
+// c1 = the row sums of W' as the kernel multiplies them, c2 = W . beta + b
+// (ln_fold_weights); the row statistics come from the x values the GEMM loads.
+// EXACT reads w32 / c1_32, FAST the f16 rounding w16 / c1_16. Output columns in
+// nseg (<= 3) separate buffers of widths[i] columns (multiples of 4).
+struct LnFolded {
+    const float *w32 = nullptr, *c1_32 = nullptr;
+    const void *w16 = nullptr;
+    const float *c1_16 = nullptr;
+    const float *c2 = nullptr;
+    float eps = 1e-5f;
+};
+void conv1x1_ln(Context &ctx, const float *x, int64_t pixels, int c_in, const LnFolded &f, int nseg, const int *widths,
+                float *const *outs, GemmEpilogue epi = GemmEpilogue::None);
+// Builds LnFolded's tensors on the device from W [n][k] (f32 or f16), gamma,
+// beta [k] and bias [n] (or NULL): w32 [n][k] = W . gamma (f32), w16 its
+// round-to-nearest f16 copy, c1_32 / c1_16 their row sums and c2 = W . beta +
+// bias, summed in f64 in a fixed order.
+void ln_fold_weights(Context &ctx, const void *w, WeightType wt, int n, int k, const float *gamma, const float *beta,
+                     const float *bias, float *w32, void *w16, float *c1_32, float *c1_16, float *c2);
 // C[z] = A[z] . B[z]^T (+ bias) (+ residual[z]) [SiLU] for z < batch, all K-contiguous:
 // A [m][lda], B [n][ldb], C [m][ldc]; *_bs are per-item element offsets.
 // row_group g > 1 stores row m, column n at (m / g) * ldc + n * g + m % g.

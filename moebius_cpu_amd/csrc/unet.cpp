@@ -449,6 +449,35 @@ struct DwResnet {
     }
 };
 
+// A LayerNorm folded into the 1x1 conv that reads it (LnFolded): owns the
+// folded weights W . diag(gamma) (f32 and the f16 rounding), their row sums
+// and W . beta + b, built once at load.
+struct LnFold {
+    float *w32 = nullptr, *c1_32 = nullptr, *c1_16 = nullptr, *c2 = nullptr;
+    void *w16 = nullptr;
+    void build(Context &ctx, const void *w, WeightType wt, int n, int k, const float *gamma, const float *beta,
+               const float *bias) {
+        HIP_CHECK(hipMalloc(&w32, size_t(n) * k * sizeof(float)));
+        HIP_CHECK(hipMalloc(&w16, size_t(n) * k * 2));
+        HIP_CHECK(hipMalloc(&c1_32, size_t(n) * sizeof(float)));
+        HIP_CHECK(hipMalloc(&c1_16, size_t(n) * sizeof(float)));
+        HIP_CHECK(hipMalloc(&c2, size_t(n) * sizeof(float)));
+        ln_fold_weights(ctx, w, wt, n, k, gamma, beta, bias, w32, w16, c1_32, c1_16, c2);
+    }
+    LnFolded view(float eps) const {
+        LnFolded f;
+        f.w32 = w32, f.c1_32 = c1_32, f.w16 = w16, f.c1_16 = c1_16, f.c2 = c2, f.eps = eps;
+        return f;
+    }
+    void release() {
+        for (void *q : {static_cast<void *>(w32), w16, static_cast<void *>(c1_32), static_cast<void *>(c1_16),
+                        static_cast<void *>(c2)})
+            if (q) (void)hipFree(q);
+        w32 = c1_32 = c1_16 = c2 = nullptr;
+        w16 = nullptr;
+    }
+};
+
 // src/unet/lambda.rs:73-152
 struct SelfLambda {
     int c = 0, k = 0;
@@ -501,7 +530,9 @@ struct SelfLambda {
         bqkv = nullptr;
     }
     // h [x.px()][c] += SelfLambda(x): the block's residual add is folded into the tap filter.
-    void fwd_add(Env &e, const DT &x, float *h, const LayerNormOut *lno = nullptr) const {
+    // ln: x is the block's hidden state and LayerNorm 1 is folded into the q | k | v GEMM.
+    void fwd_add(Env &e, const DT &x, float *h, const LayerNormOut *lno = nullptr,
+                 const LnFolded *ln = nullptr) const {
         const int hw = x.h * x.w;
         DT q = e.pool.tensor(x.n, x.h, x.w, c);
         DT kt = e.pool.tensor(x.n, x.h, x.w, k);
@@ -510,7 +541,11 @@ struct SelfLambda {
             const int widths[3] = {c, k, k};
             float *const outs[3] = {q.p, kt.p, vt.p};
             const bool w32 = wqkv32 && e.ctx.precision == Precision::Exact;
-            conv1x1_segments(e.ctx, x.p, x.px(), c, w32 ? wqkv32 : wqkv, w32 ? kF32 : wt, bqkv, 3, widths, outs);
+            if (ln)
+                conv1x1_ln(e.ctx, x.p, x.px(), c, *ln, 3, widths, outs);
+            else
+                conv1x1_segments(e.ctx, x.p, x.px(), c, w32 ? wqkv32 : wqkv, w32 ? kF32 : wt, bqkv, 3, widths,
+                                 outs);
         }
         float *lam_t = e.pool.floats(int64_t(x.n) * k * k);
         softmax_lambda(e.ctx, kt.p, vt.p, x.n, hw, k, k, lam_t);
@@ -599,6 +634,7 @@ struct MixTransformer {
     LNp ln1, ln2, ln3;
     SelfLambda attn1;
     CrossLambda attn2;
+    LnFold ln1q, ln3f;  // LayerNorm 1 folded into q | k | v, LayerNorm 3 into the inverted 1x1
     const float *dw = nullptr, *dwb = nullptr;
     void load(Env &env, const WeightStore &W, const std::string &p, int c_, const float *ehs_dev) {
         c = c_;
@@ -617,10 +653,15 @@ struct MixTransformer {
         inverted.load(W, ff + ".inverted_conv.conv", c, 2 * hidden, true);
         point.load(W, ff + ".point_conv.conv", hidden, c, false);
         proj_out.load(W, p + ".proj_out", c, c, true);
+        ln1q.build(env.ctx, attn1.wqkv, attn1.wt, c + 2 * attn1.k, c, ln1.g, ln1.b, attn1.bqkv);
+        ln3f.build(env.ctx, inverted.w.p, inverted.w.wt, 2 * hidden, c, ln3.g, ln3.b, inverted.b);
+        HIP_CHECK(hipStreamSynchronize(env.ctx.stream));
     }
     void release() {
         attn1.release();
         attn2.release();
+        ln1q.release();
+        ln3f.release();
     }
     DT fwd(Env &e, const DT &x, int br0) const { return fwd(e, x, x, br0); }
     // xs: the input for everything before the cross-lambda, xr: the same at the
@@ -651,25 +692,41 @@ struct MixTransformer {
         // separate pass costs a launch and a re-read of h (whole step -29 us EXACT,
         // -36 us FAST). The same in the cross-lambda kernel for LayerNorm 3 measured
         // 160 us slower per step, so LayerNorm 3 stays a pass of its own.
-        DT t = ln1.fwd(e, h);
+        // LayerNorms 1 and 3 are folded into the GEMMs that read them (q | k | v and
+        // the inverted 1x1), which read h itself: no LayerNorm launch or output.
+        const bool fold = e.ctx.tune.ln_fold != 0;
+        const LnFolded lnq = ln1q.view(LN_EPS), lnf = ln3f.view(LN_EPS);
         DT t2 = e.pool.tensor(h.n, h.h, h.w, h.c);
         LayerNormOut lno2;
         lno2.gamma = ln2.g;
         lno2.beta = ln2.b;
         lno2.eps = LN_EPS;
         lno2.out = t2.p;
-        attn1.fwd_add(e, t, h.p, &lno2);
-        e.pool.recycle(t);
+        if (fold) {
+            attn1.fwd_add(e, h, h.p, &lno2, &lnq);
+        } else {
+            DT t = ln1.fwd(e, h);
+            attn1.fwd_add(e, t, h.p, &lno2);
+            e.pool.recycle(t);
+        }
         if (xs.n != xr.n) {
             h = widen(e, h, xr.n);
             t2 = widen(e, t2, xr.n);
         }
         attn2.fwd_add(e, t2, br0, h.p);
         e.pool.recycle(t2);
-        t = ln3.fwd(e, h);
-        // MixFFN (transformer.rs:121-129): SiLU(inverted(t)) -> GLU depthwise -> point + h
-        DT a = inverted.fwd(e, t, nullptr, GemmEpilogue::Silu);
-        e.pool.recycle(t);
+        // MixFFN (transformer.rs:121-129): SiLU(inverted(LN3 h)) -> GLU depthwise -> point + h
+        DT a;
+        if (fold) {
+            a = e.pool.tensor(h.n, h.h, h.w, 2 * hidden);
+            const int width = 2 * hidden;
+            float *const outs[1] = {a.p};
+            conv1x1_ln(e.ctx, h.p, h.px(), c, lnf, 1, &width, outs, GemmEpilogue::Silu);
+        } else {
+            DT t = ln3.fwd(e, h);
+            a = inverted.fwd(e, t, nullptr, GemmEpilogue::Silu);
+            e.pool.recycle(t);
+        }
         DT g = e.pool.tensor(a.n, a.h, a.w, hidden);
         depthwise3x3(e.ctx, a.p, a.n, a.h, a.w, a.c, dw, dwb, 2, g.p);
         e.pool.recycle(a);

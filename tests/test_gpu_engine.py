@@ -226,10 +226,15 @@ def test_conv1x1_residual_transform_and_second_residual(ctx, n, h, w, c, f16):
 
 
 # ---- every tiling the planner can pick (32x32 tiles on 16x16 MFMA, 64/128
-# tiles on 32x32 MFMA, split K with the separate reduction), with edge tiles
-# in M and N and both epilogue store paths (N % 4 == 0: 16-byte, else scalar):
-# each within the f32 bar of the oracle
-@pytest.mark.parametrize("plan", ["32,32,1", "32,32,3", "64,64,1", "64,64,2", "128,64,1", "64,128,3", "128,128,2"])
+# tiles on 32x32 MFMA, split K with the separate reduction, and the wide wave
+# layouts "bm,bn,splits,wm,wn,wk[,pipelined]": partial load passes, K split
+# over wave groups, the pipelined loop), with edge tiles in M and N and both epilogue store paths (N % 4 ==
+# 0: 16-byte, else scalar): each within the f32 bar of the oracle
+WIDE_PLANS = ['64,80,1,4,1,1,1', '64,80,1,4,1,1', '128,80,1,4,1,1,1', '64,160,1,2,2,1,1', '32,80,1,2,1,2,1', '32,80,1,2,1,2', '160,64,1,2,2,1,1', '160,64,1,2,2,1,1,16', '64,80,1,4,1,1,0,16', '128,128,1,2,2,1,1,16']
+
+
+@pytest.mark.parametrize("plan", ["32,32,1", "32,32,3", "64,64,1", "64,64,2", "128,64,1", "64,128,3", "128,128,2",
+                                  *WIDE_PLANS])
 @pytest.mark.parametrize("c_out", [72, 70])
 def test_conv1x1_every_tiling(ctx, plan, c_out, tune):
     rng = np.random.default_rng(c_out)

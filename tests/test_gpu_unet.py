@@ -231,7 +231,8 @@ def test_cross_lambda_kernel(ctx, br0, nb, hw, k, heads, tune):
 # 16-byte stores of four rows when g % 4 == 0; plain rows, a ragged last tile,
 # a K split and the bias epilogue around them.
 @pytest.mark.parametrize("row_group", [0, 4, 8])
-@pytest.mark.parametrize("plan", [None, "32,32,1", "64,64,1", "64,64,2"])
+@pytest.mark.parametrize("plan", [None, "32,32,1", "64,64,1", "64,64,2", "64,80,1,4,1,1,1", "128,80,1,4,1,1,1",
+                                  "32,80,1,2,1,2,1", "160,64,1,2,2,1,1", "160,64,1,2,2,1,1,16", "128,128,1,2,2,1,1,16"])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_gemm_nt_kernel(ctx, row_group, plan, with_bias, tune):
     if plan:

@@ -320,6 +320,14 @@ int32_t mh_softmax_lambda(MhContext *ctx, const float *keys, const float *v, uin
 int32_t mh_tap_filter(MhContext *ctx, const float *a_t, const float *v, const float *yc, const float *residual,
                       float *out, uint32_t nb, uint32_t hh, uint32_t ww, uint32_t vd);
 
+/* mh_tap_filter followed by the transformer block's `layer_norm` of its output
+ * rows (src/unet/transformer.rs:104-108, src/engine/norm.rs:151-173): the same
+ * out, and ln_out [nb*hh*ww][8*vd] = LayerNorm(out) (gamma, beta [8*vd]), written
+ * by the kernel that finishes each row. ln_out must not alias out, yc or residual. */
+int32_t mh_tap_filter_ln(MhContext *ctx, const float *a_t, const float *v, const float *yc, const float *residual,
+                         float *out, uint32_t nb, uint32_t hh, uint32_t ww, uint32_t vd, const float *gamma,
+                         const float *beta, float eps, float *ln_out);
+
 /* src/unet/lambda.rs:131-137, the position path's `matmul` A = Q . W_aug
  * over nb items of hw pixels: q [nb*hw][8][k] (a pixel's 8 head rows of k),
  * w_aug_t [226][k] (the reference's w_aug [k][226] transposed: tap d < 225 is

@@ -627,6 +627,27 @@ int32_t mh_tap_filter(MhContext *ctx, const float *a_t, const float *v, const fl
     });
 }
 
+int32_t mh_tap_filter_ln(MhContext *ctx, const float *a_t, const float *v, const float *yc, const float *residual,
+                         float *out, uint32_t nb, uint32_t hh, uint32_t ww, uint32_t vd, const float *gamma,
+                         const float *beta, float eps, float *ln_out) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(a_t, "a_t");
+        need(v, "v");
+        need(yc, "yc");
+        need(out, "out");
+        need(gamma, "gamma");
+        need(beta, "beta");
+        need(ln_out, "ln_out");
+        mh::LayerNormOut lno;
+        lno.gamma = gamma;
+        lno.beta = beta;
+        lno.eps = eps;
+        lno.out = ln_out;
+        mh::tap_filter(c, a_t, v, yc, residual, out, dim(nb, "nb"), dim(hh, "hh"), dim(ww, "ww"), dim(vd, "vd"), &lno);
+    });
+}
+
 int32_t mh_lambda_position_coeffs(MhContext *ctx, const float *q, const float *w_aug_t, const float *lambda_t,
                                   uint32_t nb, uint32_t hw, uint32_t k, float *a_t, float *yc) {
     return guard([&] {

@@ -83,6 +83,8 @@ bool set_tuning(Tuning &t, const char *key, const char *value) {
     if (k == "gemm_log") return to_int(t.gemm_log, 0);
     if (k == "gemm_wide") return to_int(t.gemm_wide, 1) && t.gemm_wide >= 0 && t.gemm_wide <= 1;
     if (k == "ln_fold") return to_int(t.ln_fold, 0) && t.ln_fold >= 0 && t.ln_fold <= 1;
+    if (k == "tap_split") return to_int(t.tap_split, 0) && (t.tap_split == 0 || t.tap_split == 1 || t.tap_split == 3 ||
+                                                            t.tap_split == 5);
     if (k == "tap_heads") {
         if (clear) {
             t.tap_tile = -1, t.tap_heads = 0;
@@ -113,7 +115,8 @@ Context::Context(int dev) : device(dev) {
                                               {"MOEBIUS_HIP_LAMBDA_TAPS", "lambda_taps"},
                                               {"MOEBIUS_HIP_GEMM_LOG", "gemm_log"},
                                               {"MOEBIUS_HIP_GEMM_WIDE", "gemm_wide"},
-                                              {"MOEBIUS_HIP_LN_FOLD", "ln_fold"}};
+                                              {"MOEBIUS_HIP_LN_FOLD", "ln_fold"},
+                                              {"MOEBIUS_HIP_TAP_SPLIT", "tap_split"}};
     for (const auto &kv : env_keys)
         if (const char *e = std::getenv(kv[0])) set_tuning(tune, kv[1], e);
     int count = 0;

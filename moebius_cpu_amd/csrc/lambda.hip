@@ -240,18 +240,29 @@ __device__ __forceinline__ void load_heads(const float *__restrict__ p, float (&
 // or two 16-byte loads from the tap-major a_t. Per output element the
 // operations are the reference's: (yc + bias) then one fused multiply-add per
 // in-image tap in (dy, dx) order; then residual + u when a residual is given.
-template <int HG, bool LN>
+// RS > 1: the 15 tap rows of an output are split over RS threads of one block
+// (thread s of output o is threadIdx.x = s * opb + o, opb = blockDim.x / RS),
+// which take consecutive row ranges; their sums are added in row order through
+// LDS by the first, which then adds the residual. For maps whose pixel count
+// leaves the chip under one wave per SIMD (the 32x32 and 16x16 latents), where
+// one thread's 225 dependent taps expose the load latency. The sum then runs
+// in three or five partial chains instead of one: f32-rounding close to the
+// reference's order, no longer bit-identical to it.
+template <int HG, bool LN, int RS = 1>
 __global__ __launch_bounds__(256) void tap_filter_kernel(const float *__restrict__ a_t, const float *__restrict__ v,
                                                          const float *yc, const float *res, float *out, int nb,
                                                          int hh, int ww, int vd, LnOut ln) {
     constexpr int NG = kHeads / HG;
     const int v4 = vd >> 2;
     const int64_t total = int64_t(nb) * hh * ww * NG * v4;
-    const int64_t t0 = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    const bool active = t0 < total;
-    // With the LayerNorm a block is whole pixels (blockDim a multiple of the
-    // pixel's threads) and every thread stays for its barriers.
-    if (!LN && !active) return;
+    const int opb = int(blockDim.x) / RS;
+    const int split = RS > 1 ? int(threadIdx.x) / opb : 0;
+    const int lt = RS > 1 ? int(threadIdx.x) - split * opb : int(threadIdx.x);
+    const int64_t t0 = int64_t(blockIdx.x) * opb + lt;
+    const bool active = t0 < total && split < RS;
+    // With the LayerNorm or a row split, a block is whole outputs (pixels with
+    // the LayerNorm) and every thread stays for its barriers.
+    if (!LN && RS == 1 && !active) return;
     const int64_t t = active ? t0 : 0;
     const int jq = int(t % v4);
     const int64_t r = t / v4;
@@ -264,7 +275,7 @@ __global__ __launch_bounds__(256) void tap_filter_kernel(const float *__restrict
     const float *ap = a_t + pix * (kTapsB * kHeads) + hg * HG;
     const int64_t obase = pix * (kHeads * v4) + int64_t(hg) * HG * v4 + jq;  // in float4 units
     float4 acc[HG];
-    {
+    if (split == 0) {
         float bias[HG];
         load_heads<HG>(ap + kTaps * kHeads, bias);
 #pragma unroll
@@ -272,10 +283,14 @@ __global__ __launch_bounds__(256) void tap_filter_kernel(const float *__restrict
             const float4 c = reinterpret_cast<const float4 *>(yc)[obase + i * v4];
             acc[i] = make_float4(c.x + bias[i], c.y + bias[i], c.z + bias[i], c.w + bias[i]);
         }
+    } else {
+#pragma unroll
+        for (int i = 0; i < HG; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     const float4 *vb = reinterpret_cast<const float4 *>(v + int64_t(b) * hw * vd) + jq;
     const int kx0 = max(kPad - x, 0), kx1 = min(kWin, ww + kPad - x);
-    const int ky0 = max(kPad - y, 0), ky1 = min(kWin, hh + kPad - y);
+    constexpr int RR = (kWin + RS - 1) / RS;  // tap rows per split
+    const int ky0 = max(max(kPad - y, 0), split * RR), ky1 = min(min(kWin, hh + kPad - y), split * RR + RR);
     // A whole 15-tap row is loaded before any of it is used (the loads of a
     // thread overlap instead of queueing one tap at a time); columns outside the
     // image are loaded from a clamped, valid address and skipped in the sum.
@@ -303,19 +318,34 @@ __global__ __launch_bounds__(256) void tap_filter_kernel(const float *__restrict
             }
         }
     }
+    extern __shared__ float red[];  // LN: [blockDim.x]; RS > 1: then [RS - 1][opb][HG] float4
+    if constexpr (RS > 1) {
+        float4 *part = reinterpret_cast<float4 *>(red + (LN ? (blockDim.x + 3) / 4 * 4 : 0));  // 16-byte aligned
+        if (split > 0 && active)
+#pragma unroll
+            for (int i = 0; i < HG; ++i) part[((split - 1) * opb + lt) * HG + i] = acc[i];
+        __syncthreads();
+        if (split == 0 && active)
+            for (int s2 = 1; s2 < RS; ++s2)
+#pragma unroll
+                for (int i = 0; i < HG; ++i) {
+                    const float4 u = part[((s2 - 1) * opb + lt) * HG + i];
+                    acc[i] = make_float4(acc[i].x + u.x, acc[i].y + u.y, acc[i].z + u.z, acc[i].w + u.w);
+                }
+    }
+    const bool owner = active && split == 0;
     float4 *o4 = reinterpret_cast<float4 *>(out);
 #pragma unroll
     for (int i = 0; i < HG; ++i) {
-        if (res) {
+        if (res && owner) {
             const float4 h = reinterpret_cast<const float4 *>(res)[obase + i * v4];
             acc[i] = make_float4(h.x + acc[i].x, h.y + acc[i].y, h.z + acc[i].z, h.w + acc[i].w);
         }
-        if (active) o4[obase + i * v4] = acc[i];
+        if (owner) o4[obase + i * v4] = acc[i];
     }
     if constexpr (LN) {
-        extern __shared__ float red[];  // [blockDim.x]
         const int tpp = NG * v4;
-        ln_pixel_rows<HG>(ln, acc, active, red, int(threadIdx.x) / tpp, tpp, kHeads * vd, pix, hg, jq, v4);
+        ln_pixel_rows<HG>(ln, acc, owner, red, lt / tpp, tpp, kHeads * vd, pix, hg, jq, v4);
     }
 }
 
@@ -887,19 +917,48 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
     }
     const int tpp = (kHeads / hg) * v4;
     MH_REQUIRE(!lno || tpp <= 256, "tap_filter: LayerNorm output needs a pixel's threads in one block");
-    // With the LayerNorm, blocks of whole pixels (P * tpp threads); else 256.
-    const unsigned threads = lno ? unsigned((256 / tpp) * tpp) : 256u;
-    const size_t lds = lno ? threads * sizeof(float) : 0;
+    // Row split (tap_split tuning: 1, 3 or 5; default 0 chooses): three threads per
+    // output while the map gives the chip fewer than two waves per SIMD of unsplit
+    // threads and a pixel's 3 * tpp threads fit one block (measured alone with
+    // LayerNorm 2: 32x32 x 80 34.1 -> 28.6 us, 16x16 x 160 22.9 -> 16.0 us; five
+    // threads per output 40.6 / 22.3 us).
+    int rs = ctx.tune.tap_split;
+    if (rs != 1 && rs != 3 && rs != 5) {
+        const int64_t waves = ceil_div(pix * tpp, 64);
+        rs = (waves < 2 * 4 * int64_t(ctx.cu_count) && 3 * tpp <= 256) ? 3 : 1;
+    }
+    if (rs * tpp > 256) rs = 1;
+    // Blocks of whole outputs: with the LayerNorm or a row split, P whole pixels
+    // (P * tpp outputs) times rs threads each; else 256 outputs.
+    const int opb = (lno || rs > 1) ? (256 / (rs * tpp)) * tpp : 256;
+    const unsigned threads = unsigned(opb * rs);
+    const size_t lds = (lno ? (threads + 3) / 4 * 4 * sizeof(float) : 0) + size_t(rs - 1) * opb * hg * 16;
     const int64_t total = pix * tpp;
-    const unsigned blocks = unsigned(ceil_div(total, threads));
+    const unsigned blocks = unsigned(ceil_div(total, opb));
     auto go = [&](auto kern) {
         kern<<<blocks, threads, lds, ctx.stream>>>(a_t, v, yc, residual, out, nb, hh, ww, vd, ln);
     };
+    auto pick = [&](auto k1, auto k3, auto k5) {
+        if (rs == 5) go(k5);
+        else if (rs == 3) go(k3);
+        else go(k1);
+    };
     switch (hg) {
-        case 8: lno ? go(tap_filter_kernel<8, true>) : go(tap_filter_kernel<8, false>); break;
-        case 4: lno ? go(tap_filter_kernel<4, true>) : go(tap_filter_kernel<4, false>); break;
-        case 2: lno ? go(tap_filter_kernel<2, true>) : go(tap_filter_kernel<2, false>); break;
-        default: lno ? go(tap_filter_kernel<1, true>) : go(tap_filter_kernel<1, false>);
+        case 8:
+            lno ? pick(tap_filter_kernel<8, true, 1>, tap_filter_kernel<8, true, 3>, tap_filter_kernel<8, true, 5>)
+                : pick(tap_filter_kernel<8, false, 1>, tap_filter_kernel<8, false, 3>, tap_filter_kernel<8, false, 5>);
+            break;
+        case 4:
+            lno ? pick(tap_filter_kernel<4, true, 1>, tap_filter_kernel<4, true, 3>, tap_filter_kernel<4, true, 5>)
+                : pick(tap_filter_kernel<4, false, 1>, tap_filter_kernel<4, false, 3>, tap_filter_kernel<4, false, 5>);
+            break;
+        case 2:
+            lno ? pick(tap_filter_kernel<2, true, 1>, tap_filter_kernel<2, true, 3>, tap_filter_kernel<2, true, 5>)
+                : pick(tap_filter_kernel<2, false, 1>, tap_filter_kernel<2, false, 3>, tap_filter_kernel<2, false, 5>);
+            break;
+        default:
+            lno ? pick(tap_filter_kernel<1, true, 1>, tap_filter_kernel<1, true, 3>, tap_filter_kernel<1, true, 5>)
+                : pick(tap_filter_kernel<1, false, 1>, tap_filter_kernel<1, false, 3>, tap_filter_kernel<1, false, 5>);
     }
     MH_LAUNCH_CHECK();
 }

@@ -52,6 +52,7 @@ def test_softmax_lambda_kernel(ctx, nb, rows, k):
                                          (1, 9, 70, 40)])
 @pytest.mark.parametrize("heads_per_thread", ["default", "t8", "t4", "8", "4", "2"])
 def test_tap_filter_kernel_bit_exact(ctx, nb, hh, ww, vd, heads_per_thread, tune):
+    tune("tap_split", 1)  # one thread per output: the reference's tap order
     if heads_per_thread == "default":
         tune("tap_heads", None)
     else:
@@ -74,6 +75,39 @@ def test_tap_filter_kernel_bit_exact(ctx, nb, hh, ww, vd, heads_per_thread, tune
         want = oracle.tap_filter(a[b], v[b], o[b], hh, ww)
         assert np.array_equal(got[b], want)
         assert np.array_equal(got_res[b], h[b] + want)
+
+
+# The tap rows split over 3 or 5 threads per output (the 32x32 and 16x16
+# latents' default): the same sums in partial chains added in row order, so
+# within f32 rounding of the reference's order; residual form and LayerNorm 2.
+@pytest.mark.parametrize("nb,hh,ww,vd", [(2, 32, 32, 80), (2, 16, 16, 160), (1, 7, 5, 8), (1, 20, 9, 80)])
+@pytest.mark.parametrize("split", [3, 5])
+@pytest.mark.parametrize("heads_per_thread", ["default", "8", "2"])
+def test_tap_filter_row_split(ctx, nb, hh, ww, vd, split, heads_per_thread, tune):
+    tune("tap_split", split)
+    tune("tap_heads", None if heads_per_thread == "default" else heads_per_thread)
+    rng = np.random.default_rng(hh * ww + vd + split)
+    a = rng.standard_normal((nb, hh * ww, 8, 226)).astype(np.float32)
+    v = rng.standard_normal((nb, hh * ww, vd)).astype(np.float32)
+    o = rng.standard_normal((nb, hh * ww, 8 * vd)).astype(np.float32)
+    h = rng.standard_normal((nb, hh * ww, 8 * vd)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(8 * vd)).astype(np.float32)
+    be = (0.1 * rng.standard_normal(8 * vd)).astype(np.float32)
+    ad, vdev, yd = D(ctx, a.transpose(0, 1, 3, 2)), D(ctx, v), D(ctx, o)
+    out = E.DeviceArray(ctx, o.shape)
+    print(f"tap split {split} heads {heads_per_thread} {nb}x{hh}x{ww}x{vd}", flush=True)
+    E.check(E.lib().mh_tap_filter(ctx.h, ad.ptr, vdev.ptr, yd.ptr, None, out.ptr, nb, hh, ww, vd))
+    got = out.numpy()
+    hd, gd, bd = D(ctx, h), D(ctx, g), D(ctx, be)
+    ln = E.DeviceArray(ctx, o.shape)
+    E.check(E.lib().mh_tap_filter_ln(ctx.h, ad.ptr, vdev.ptr, yd.ptr, hd.ptr, hd.ptr, nb, hh, ww, vd, gd.ptr, bd.ptr,
+                                     1e-5, ln.ptr))
+    got_res, got_ln = hd.numpy(), ln.numpy()
+    for b in range(nb):
+        want = oracle.tap_filter(a[b], v[b], o[b], hh, ww)
+        assert max_abs_rel(got[b], want) < 1e-5
+        assert max_abs_rel(got_res[b], h[b] + want) < 1e-5
+        assert max_abs_rel(got_ln[b], oracle.layer_norm(h[b] + want, g, be, 1e-5)) < 1e-4
 
 
 # Position coefficients A = Q . W_aug (lambda.rs:131-137) by the matrix-core

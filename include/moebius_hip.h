@@ -263,7 +263,10 @@ int32_t mh_group_norm_forward(MhContext *ctx, const float *x, uint32_t n, uint32
  * workspace, so it calls no hipMalloc/hipFree. Shapes whose scratch exceeds the
  * array (partials plus 2 * n * c floats; e.g. n * c > 65536 on maps of a few
  * pixels) return MH_ERR_INVALID_ARGUMENT. Every call on a GPU shares that GPU's
- * array: calls that overlap on one GPU (two contexts' streams) race. */
+ * array, which keeps the last call's contents. Calls from different contexts'
+ * streams are ordered on the device (a call waits for an event the previous
+ * call recorded, so they do not overlap); calls captured into HIP graphs are
+ * not, and graphs that use it and run concurrently on one GPU race. */
 int32_t mh_group_norm_forward_noalloc(MhContext *ctx, const float *x, uint32_t n, uint32_t h, uint32_t w,
                                       uint32_t c, uint32_t groups, float eps, const float *gamma, const float *beta,
                                       const float *add, uint32_t silu, float *out);
@@ -547,6 +550,12 @@ int64_t mh_scratch_best_fit(const uint64_t *lens, const uint64_t *caps, uint64_t
  * counterpart in the reference): d[32][32] = a[32][2] . b[2][32] through one
  * v_mfma_f32_32x32x2f32, all operands host memory. */
 int32_t mh_selftest_mfma_f32(MhContext *ctx, const float *a, const float *b, float *d);
+
+/* Device allocations (hipMalloc calls) this library has made since it was
+ * loaded, over every context, engine and entry point (no counterpart in the
+ * reference): a caller that wants to show that a call allocates nothing reads
+ * it before and after. Host only; never fails for a non-NULL count. */
+int32_t mh_device_allocations(uint64_t *count);
 
 #ifdef __cplusplus
 }

@@ -118,6 +118,13 @@ int32_t mh_context_set_tuning(MhContext *ctx, const char *key, const char *value
     });
 }
 
+int32_t mh_device_allocations(uint64_t *count) {
+    return guard([&] {
+        need(count, "count");
+        *count = mh::device_allocations();
+    });
+}
+
 int32_t mh_context_set_precision(MhContext *ctx, uint32_t precision) {
     return guard([&] {
         mh::Context &c = C(ctx);
@@ -146,7 +153,7 @@ int32_t mh_malloc(MhContext *ctx, uint64_t bytes, void **out) {
         C(ctx);
         need(out, "out");
         *out = nullptr;
-        HIP_CHECK(hipMalloc(out, bytes ? bytes : 1));
+        mh::dev_malloc(out, bytes ? bytes : 1);
     });
 }
 
@@ -759,8 +766,8 @@ int32_t mh_unet_forward_host(MhUNet *unet, const float *x_host, uint32_t timeste
         need(x_host, "x");
         need(eps_host, "eps");
         const bool cfg = guidance_cfg(guidance);
-        if (!unet->x_dev) HIP_CHECK(hipMalloc(&unet->x_dev, 64 * 64 * 9 * sizeof(float)));
-        if (!unet->eps_dev) HIP_CHECK(hipMalloc(&unet->eps_dev, 2 * 64 * 64 * 4 * sizeof(float)));
+        if (!unet->x_dev) mh::dev_malloc(&unet->x_dev, 64 * 64 * 9 * sizeof(float));
+        if (!unet->eps_dev) mh::dev_malloc(&unet->eps_dev, 2 * 64 * 64 * 4 * sizeof(float));
         HIP_CHECK(hipMemcpyAsync(unet->x_dev, x_host, 64 * 64 * 9 * sizeof(float), hipMemcpyHostToDevice, c.stream));
         unet->net->forward(unet->x_dev, int(timestep), cfg, unet->eps_dev);
         HIP_CHECK(hipMemcpyAsync(eps_host, unet->eps_dev, size_t(cfg ? 2 : 1) * 64 * 64 * 4 * sizeof(float),
@@ -867,7 +874,7 @@ int32_t mh_vae_encode_host(MhVae *vae, const float *images, uint32_t b, uint32_t
         const size_t ib = size_t(b) * h * w * 3 * sizeof(float);
         const size_t zb = size_t(b) * (h / 8) * (w / 8) * 4 * sizeof(float);
         float *d = nullptr;
-        HIP_CHECK(hipMalloc(&d, ib + 2 * zb));
+        mh::dev_malloc(&d, ib + 2 * zb);
         struct Free {
             float *p;
             ~Free() { (void)hipFree(p); }
@@ -889,7 +896,7 @@ int32_t mh_vae_decode_host(MhVae *vae, const float *latents, uint32_t h, uint32_
         const size_t lb = size_t(h) * w * 4 * sizeof(float);
         const size_t ob = size_t(h) * w * 64 * 3 * sizeof(float);
         float *d = nullptr;
-        HIP_CHECK(hipMalloc(&d, lb + ob));
+        mh::dev_malloc(&d, lb + ob);
         struct Free {
             float *p;
             ~Free() { (void)hipFree(p); }

@@ -212,7 +212,8 @@ int32_t mh_engine_memory(const MoebiusEngine *engine, uint64_t *weight_bytes, ui
         auto *m = const_cast<MoebiusEngine *>(engine);
         std::lock_guard<std::mutex> hold(m->lock);
         if (weight_bytes) *weight_bytes = m->e.unet->weight_bytes() + m->e.vae->weight_bytes();
-        if (pool_bytes) *pool_bytes = m->e.unet->pool_bytes() + m->e.vae->pool_bytes() + m->e.ctx.ws.capacity();
+        if (pool_bytes) *pool_bytes = m->e.unet->pool_bytes() + m->e.vae->pool_bytes() + m->e.ctx.ws.capacity() +
+                                    m->e.ctx.state.capacity() + m->e.frames.capacity();
     });
 }
 
@@ -225,6 +226,8 @@ int32_t mh_engine_release_scratch(const MoebiusEngine *engine) {
         m->e.unet->release_scratch();
         m->e.vae->release_scratch();
         m->e.ctx.ws.release(m->e.ctx.stream);
+        m->e.ctx.state.release(m->e.ctx.stream);
+        m->e.frames.release(m->e.ctx.stream);
     });
 }
 

@@ -76,6 +76,18 @@ struct Tuning {
 // or "" restores the default. False for an unknown key or a malformed value.
 bool set_tuning(Tuning &t, const char *key, const char *value);
 
+// Every device allocation the library makes goes through here, so that the
+// count of them (device_allocations, mh_device_allocations) shows which calls
+// allocate.
+void dev_malloc_bytes(void **p, size_t bytes);
+template <class T>
+inline void dev_malloc(T **p, size_t bytes) {
+    void *v = nullptr;
+    dev_malloc_bytes(&v, bytes);
+    *p = static_cast<T *>(v);
+}
+uint64_t device_allocations();
+
 // Device arena for kernel scratch (split-K partials, norm partials): grown on
 // demand, kept for the context's life, like the reference's `Scratch` panels
 // (src/engine/mod.rs:25-34). Growth synchronises the stream first, since
@@ -103,6 +115,10 @@ struct Context {
     int cu_count = 0;
     std::string arch;
     Workspace ws;
+    // State that outlives single kernels inside one multi-step call (the denoise
+    // loop's latents, UNet input, eps and solver history): grow-only like ws,
+    // and apart from it, since the kernels of each step draw on ws.
+    Workspace state;
     Tuning tune;
 
     explicit Context(int dev);

@@ -1,4 +1,5 @@
 // Context, workspace and error plumbing.
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -17,6 +18,17 @@ void hip_fail(hipError_t e, const char *expr, const char *file, int line) {
        << ": " << expr;
     throw Error(e == hipErrorOutOfMemory ? kOutOfMemory : kInternal, os.str());
 }
+
+namespace {
+std::atomic<uint64_t> g_allocations{0};
+}
+
+void dev_malloc_bytes(void **p, size_t bytes) {
+    HIP_CHECK(hipMalloc(p, bytes ? bytes : 1));
+    g_allocations.fetch_add(1, std::memory_order_relaxed);
+}
+
+uint64_t device_allocations() { return g_allocations.load(std::memory_order_relaxed); }
 
 Workspace::~Workspace() {
     if (ptr_) (void)hipFree(ptr_);
@@ -37,7 +49,7 @@ void *Workspace::get(size_t bytes, hipStream_t stream) {
     ptr_ = nullptr;
     cap_ = 0;
     const size_t want = (bytes + (size_t(1) << 20) - 1) & ~((size_t(1) << 20) - 1);
-    HIP_CHECK(hipMalloc(&ptr_, want));
+    dev_malloc(&ptr_, want);
     cap_ = want;
     return ptr_;
 }

@@ -186,7 +186,7 @@ void unet_input(Context &ctx, const float *x, const float *mask_lat, const float
 Sampler::Sampler(Context &ctx, int steps, double strength, Spacing spacing, int64_t len)
     : ctx_(ctx), sched_(steps, strength, spacing), len_(len) {
     MH_REQUIRE(len > 0, "sampler length must be positive");
-    HIP_CHECK(hipMalloc(&prev_, size_t(len) * sizeof(float)));
+    mh::dev_malloc(&prev_, size_t(len) * sizeof(float));
 }
 
 Sampler::~Sampler() {
@@ -217,14 +217,6 @@ void Sampler::add_noise(const float *x0, const float *noise, int t, float *out) 
 
 namespace {
 
-struct DeviceBuffers {
-    float *p = nullptr;
-    explicit DeviceBuffers(size_t floats) { HIP_CHECK(hipMalloc(&p, floats * sizeof(float))); }
-    ~DeviceBuffers() {
-        if (p) (void)hipFree(p);
-    }
-};
-
 struct Events {
     hipEvent_t e[2] = {nullptr, nullptr};
     Events() {
@@ -248,9 +240,9 @@ void unet_denoise(Context &ctx, UNet &unet, const float *z_img, const float *ini
     const int total = int(sched.timesteps.size());
     // the reference indexes timesteps[0] here (src/pipeline.rs:305-313) and panics on an empty schedule
     MH_REQUIRE(total > 0, "steps * strength < 1: the schedule keeps no timestep to denoise");
-    // x | UNet input | eps (two items) | DPM history
-    DeviceBuffers buf(size_t(kN + kPixels * 9 + 2 * kN + kN));
-    float *x = buf.p, *in = x + kN, *eps = in + kPixels * 9, *prev = eps + 2 * kN;
+    // x | UNet input | eps (two items) | DPM history, in the context's grow-only state block
+    float *x = static_cast<float *>(ctx.state.get(size_t(kN + kPixels * 9 + 2 * kN + kN) * sizeof(float), ctx.stream));
+    float *in = x + kN, *eps = in + kPixels * 9, *prev = eps + 2 * kN;
     if (sched.pure_noise_start)
         HIP_CHECK(hipMemcpyAsync(x, init, size_t(kN) * sizeof(float), hipMemcpyDeviceToDevice, ctx.stream));
     else
@@ -291,7 +283,7 @@ void unet_denoise(Context &ctx, UNet &unet, const float *z_img, const float *ini
         report(total);
     }
     HIP_CHECK(hipMemcpyAsync(latents, x, size_t(kN) * sizeof(float), hipMemcpyDeviceToDevice, ctx.stream));
-    HIP_CHECK(hipStreamSynchronize(ctx.stream));  // the loop's buffers are freed on return
+    HIP_CHECK(hipStreamSynchronize(ctx.stream));
 }
 
 }  // namespace mh

@@ -338,7 +338,7 @@ void im2col_gather(Context &ctx, const float *x, int n, int h, int w, int c, int
 
 void selftest_mfma_f32(Context &ctx, const float *a_host, const float *b_host, float *d_host) {
     float *dev = nullptr;
-    HIP_CHECK(hipMalloc(&dev, (64 + 64 + 1024) * sizeof(float)));
+    mh::dev_malloc(&dev, (64 + 64 + 1024) * sizeof(float));
     HIP_CHECK(hipMemcpyAsync(dev, a_host, 64 * sizeof(float), hipMemcpyHostToDevice, ctx.stream));
     HIP_CHECK(hipMemcpyAsync(dev + 64, b_host, 64 * sizeof(float), hipMemcpyHostToDevice, ctx.stream));
     mfma_probe_kernel<<<1, 64, 0, ctx.stream>>>(dev, dev + 64, dev + 128);

@@ -6,6 +6,7 @@
 #include <algorithm>
 #include <array>
 #include <cmath>
+#include <exception>
 #include <optional>
 #include <thread>
 #include <vector>
@@ -137,6 +138,8 @@ void box_line(const uint8_t *src, uint8_t *dst, size_t n, size_t radius, uint32_
 // Runs f(first, last) over [0, n) in up to `threads` contiguous row ranges
 // (at least 16 rows each), the calling thread taking the first. Every row's
 // result depends on that row alone, so the bytes do not depend on the split.
+// A range whose thread cannot be started runs on the calling thread; an
+// exception inside any range is rethrown here once every thread has joined.
 template <class F>
 void parallel_rows(size_t n, unsigned threads, F &&f) {
     const size_t t = std::max<size_t>(1, std::min<size_t>(threads, (n + 15) / 16));
@@ -145,13 +148,31 @@ void parallel_rows(size_t n, unsigned threads, F &&f) {
         return;
     }
     const size_t chunk = (n + t - 1) / t;
+    std::vector<std::exception_ptr> errors(t);
+    auto guarded = [&f, &errors](size_t i, size_t a, size_t b) {
+        try {
+            f(a, b);
+        } catch (...) {
+            errors[i] = std::current_exception();
+        }
+    };
     std::vector<std::thread> pool;
+    std::vector<size_t> inline_ranges;  // ranges whose thread could not be started
+    pool.reserve(t);
     for (size_t i = 1; i < t; ++i) {
         const size_t a = i * chunk, b = std::min(n, a + chunk);
-        if (a < b) pool.emplace_back([&f, a, b] { f(a, b); });
+        if (a >= b) continue;
+        try {
+            pool.emplace_back(guarded, i, a, b);
+        } catch (...) {
+            inline_ranges.push_back(i);
+        }
     }
-    f(size_t(0), std::min(n, chunk));
+    guarded(0, 0, std::min(n, chunk));
+    for (size_t i : inline_ranges) guarded(i, i * chunk, std::min(n, i * chunk + chunk));
     for (std::thread &th : pool) th.join();
+    for (const std::exception_ptr &e : errors)
+        if (e) std::rethrow_exception(e);
 }
 
 void box_rows(uint8_t *buf, size_t w, size_t h, float fradius, uint32_t passes, unsigned threads) {

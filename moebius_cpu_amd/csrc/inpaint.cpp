@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <utility>
 
 #include "kernels.hpp"
 
@@ -19,16 +20,35 @@ constexpr int kSide = 512, kLat = 64, kLatC = 4, kDown = 8;
 constexpr int64_t kLatN = int64_t(kLat) * kLat * kLatC;
 constexpr size_t kRoiMargin = 8;  // src/vae/mod.rs:58
 
-struct DevBuf {
-    void *p = nullptr;
-    explicit DevBuf(size_t bytes) { HIP_CHECK(hipMalloc(&p, std::max<size_t>(bytes, 1))); }
-    ~DevBuf() {
-        if (p) (void)hipFree(p);
+// The call's device frames, carved from the engine's grow-only block in 256-byte
+// aligned pieces; each ROI buffer is sized for the whole frame, so one layout
+// serves every mask at a given window side.
+struct Frames {
+    uint8_t *win, *wbin, *rgb8, *bin8, *u8, *res;
+    float *images, *mask_lat, *z, *noise, *crop, *part, *init, *lat, *dec, *lcrop, *dpart;
+
+    Frames(Workspace &block, hipStream_t stream, size_t side) {
+        const size_t model_px = size_t(kSide) * kSide, lat_b = size_t(kLatN) * sizeof(float);
+        const size_t frame_b = model_px * 3 * sizeof(float);
+        const std::pair<void **, size_t> parts[] = {
+            {(void **)&win, side * side * 3},     {(void **)&wbin, side * side},
+            {(void **)&rgb8, model_px * 3},       {(void **)&bin8, model_px},
+            {(void **)&u8, model_px * 3},         {(void **)&res, side * side * 3},
+            {(void **)&images, 2 * frame_b},      {(void **)&mask_lat, size_t(kLat) * kLat * sizeof(float)},
+            {(void **)&z, 2 * lat_b},             {(void **)&noise, 2 * lat_b},
+            {(void **)&crop, frame_b},            {(void **)&part, lat_b},
+            {(void **)&init, lat_b},              {(void **)&lat, lat_b},
+            {(void **)&dec, frame_b},             {(void **)&lcrop, lat_b},
+            {(void **)&dpart, frame_b}};
+        auto round = [](size_t b) { return (b + 255) & ~size_t(255); };
+        size_t total = 0;
+        for (const auto &q : parts) total += round(q.second);
+        char *base = static_cast<char *>(block.get(total, stream));
+        for (const auto &q : parts) {
+            *q.first = base;
+            base += round(q.second);
+        }
     }
-    DevBuf(const DevBuf &) = delete;
-    DevBuf &operator=(const DevBuf &) = delete;
-    float *f() const { return static_cast<float *>(p); }
-    uint8_t *u8() const { return static_cast<uint8_t *>(p); }
 };
 
 void h2d(Context &ctx, void *dst, const void *src, size_t bytes) {
@@ -153,46 +173,43 @@ img::Rect inpaint(Engine &e, img::ImageView &im, const img::MaskView &mask_in, c
         }
     }
     const size_t model_px = size_t(kSide) * kSide;
-    DevBuf d_win(win.size()), d_wbin(wbin.size()), d_rgb8(model_px * 3), d_bin8(model_px);
-    h2d(ctx, d_win.p, win.data(), win.size());
-    h2d(ctx, d_wbin.p, wbin.data(), wbin.size());
-    resize_u8(ctx, d_win.u8(), int(side), int(side), kSide, kSide, 3, d_rgb8.u8());
-    resize_u8(ctx, d_wbin.u8(), int(side), int(side), kSide, kSide, 1, d_bin8.u8());
-    DevBuf d_images(2 * model_px * 3 * sizeof(float)), d_mask_lat(size_t(kLat) * kLat * sizeof(float));
-    model_inputs(ctx, d_rgb8.u8(), d_bin8.u8(), d_images.f(), d_mask_lat.f());
+    const Frames d(e.frames, ctx.stream, side);
+    h2d(ctx, d.win, win.data(), win.size());
+    h2d(ctx, d.wbin, wbin.data(), wbin.size());
+    resize_u8(ctx, d.win, int(side), int(side), kSide, kSide, 3, d.rgb8);
+    resize_u8(ctx, d.wbin, int(side), int(side), kSide, kSide, 1, d.bin8);
+    model_inputs(ctx, d.rgb8, d.bin8, d.images, d.mask_lat);
     std::vector<float> mask_lat(size_t(kLat) * kLat);
-    d2h(ctx, mask_lat.data(), d_mask_lat.p, mask_lat.size() * sizeof(float));
+    d2h(ctx, mask_lat.data(), d.mask_lat, mask_lat.size() * sizeof(float));
 
     // 4: VAE encode of [image, masked] (or the ROI encode of the Fast preset).
-    DevBuf d_z(size_t(2 * kLatN) * sizeof(float)), d_noise(size_t(2 * kLatN) * sizeof(float));
-    float *z_img = d_z.f(), *z_masked = d_z.f() + kLatN;
+    float *z_img = d.z, *z_masked = d.z + kLatN;
     img::LatentRect r;
     const bool window = img::roi_window(mask_lat.data(), kRoiMargin, &r) && (r.w < size_t(kLat) || r.h < size_t(kLat));
     if (p.roi_encode && window) {
-        h2d(ctx, d_noise.p, noise.vae_masked.data(), size_t(kLatN) * sizeof(float));
-        e.vae->encode(d_images.f() + model_px * 3, 1, kSide, kSide, d_noise.f(), z_masked);
+        h2d(ctx, d.noise, noise.vae_masked.data(), size_t(kLatN) * sizeof(float));
+        e.vae->encode(d.images + model_px * 3, 1, kSide, kSide, d.noise, z_masked);
         const int cw = int(r.w) * kDown, chh = int(r.h) * kDown;
-        DevBuf d_crop(size_t(cw) * chh * 3 * sizeof(float)), d_part(r.w * r.h * kLatC * sizeof(float));
-        crop_window(ctx, d_images.f(), kSide, 3, int(r.x) * kDown, int(r.y) * kDown, cw, chh, d_crop.f());
+        crop_window(ctx, d.images, kSide, 3, int(r.x) * kDown, int(r.y) * kDown, cw, chh, d.crop);
         std::vector<float> crop_noise(r.w * r.h * kLatC);
         for (size_t y = 0; y < r.h; ++y)
             std::memcpy(&crop_noise[y * r.w * kLatC], &noise.vae_img[((r.y + y) * kLat + r.x) * kLatC],
                         r.w * kLatC * sizeof(float));
-        h2d(ctx, d_noise.p, crop_noise.data(), crop_noise.size() * sizeof(float));
-        e.vae->encode(d_crop.f(), 1, chh, cw, d_noise.f(), d_part.f());
+        h2d(ctx, d.noise, crop_noise.data(), crop_noise.size() * sizeof(float));
+        e.vae->encode(d.crop, 1, chh, cw, d.noise, d.part);
         // the window's border latents see zero padding: keep only the part nearer the mask
         img::LatentRect inner;
         img::roi_window(mask_lat.data(), kRoiMargin / 2, &inner);
         HIP_CHECK(hipMemcpyAsync(z_img, z_masked, size_t(kLatN) * sizeof(float), hipMemcpyDeviceToDevice, ctx.stream));
         HIP_CHECK(hipMemcpy2DAsync(z_img + (inner.y * kLat + inner.x) * kLatC, size_t(kLat) * kLatC * sizeof(float),
-                                   d_part.f() + ((inner.y - r.y) * r.w + inner.x - r.x) * kLatC,
+                                   d.part + ((inner.y - r.y) * r.w + inner.x - r.x) * kLatC,
                                    r.w * kLatC * sizeof(float), inner.w * kLatC * sizeof(float), inner.h,
                                    hipMemcpyDeviceToDevice, ctx.stream));
         HIP_CHECK(hipStreamSynchronize(ctx.stream));
     } else {
-        h2d(ctx, d_noise.p, noise.vae_img.data(), size_t(kLatN) * sizeof(float));
-        h2d(ctx, d_noise.f() + kLatN, noise.vae_masked.data(), size_t(kLatN) * sizeof(float));
-        e.vae->encode(d_images.f(), 2, kSide, kSide, d_noise.f(), d_z.f());
+        h2d(ctx, d.noise, noise.vae_img.data(), size_t(kLatN) * sizeof(float));
+        h2d(ctx, d.noise + kLatN, noise.vae_masked.data(), size_t(kLatN) * sizeof(float));
+        e.vae->encode(d.images, 2, kSide, kSide, d.noise, d.z);
     }
     // The CPU engine frees the encoder's 512x512 maps here (src/pipeline.rs:290-292);
     // with HBM to spare the VAE's pool stays resident, so a later call allocates nothing.
@@ -201,38 +218,33 @@ img::Rect inpaint(Engine &e, img::ImageView &im, const img::MaskView &mask_in, c
     // 6-8: init = N(0,1) + noise_offset * N(0,1)[per channel], then the denoise loop.
     std::vector<float> init(static_cast<size_t>(kLatN));
     for (int64_t i = 0; i < kLatN; ++i) init[size_t(i)] = noise.init[size_t(i)] + p.noise_offset * noise.offset[size_t(i % kLatC)];
-    DevBuf d_init(size_t(kLatN) * sizeof(float)), d_lat(size_t(kLatN) * sizeof(float));
-    h2d(ctx, d_init.p, init.data(), init.size() * sizeof(float));
+    h2d(ctx, d.init, init.data(), init.size() * sizeof(float));
     {
         PrecisionScope scope(ctx, p.fast_precision ? Precision::Fast : Precision::Exact);
         StepAdapter a{progress, user};
-        unet_denoise(ctx, *e.unet, z_img, d_init.f(), d_mask_lat.f(), z_masked, p.sampling, &StepAdapter::call, &a,
-                     d_lat.f());
+        unet_denoise(ctx, *e.unet, z_img, d.init, d.mask_lat, z_masked, p.sampling, &StepAdapter::call, &a, d.lat);
     }
-    if (latents_out) d2h(ctx, latents_out, d_lat.p, size_t(kLatN) * sizeof(float));
+    if (latents_out) d2h(ctx, latents_out, d.lat, size_t(kLatN) * sizeof(float));
 
     // 9: decode (the whole frame, or the ROI window over the model-input image).
     report(ctx, progress, user, 2, 0, 1);
-    DevBuf d_dec(model_px * 3 * sizeof(float));
     img::LatentRect rd;
     if (p.roi_decode && img::roi_window(mask_lat.data(), kRoiMargin, &rd) &&
         (rd.w < size_t(kLat) || rd.h < size_t(kLat))) {
-        DevBuf d_lcrop(rd.w * rd.h * kLatC * sizeof(float)), d_dpart(rd.w * rd.h * 64 * 3 * sizeof(float));
-        crop_window(ctx, d_lat.f(), kLat, kLatC, int(rd.x), int(rd.y), int(rd.w), int(rd.h), d_lcrop.f());
-        e.vae->decode(d_lcrop.f(), int(rd.h), int(rd.w), d_dpart.f());
-        roi_frame(ctx, d_images.f(), d_dpart.f(), int(rd.x), int(rd.y), int(rd.w), int(rd.h), d_dec.f());
+        crop_window(ctx, d.lat, kLat, kLatC, int(rd.x), int(rd.y), int(rd.w), int(rd.h), d.lcrop);
+        e.vae->decode(d.lcrop, int(rd.h), int(rd.w), d.dpart);
+        roi_frame(ctx, d.images, d.dpart, int(rd.x), int(rd.y), int(rd.w), int(rd.h), d.dec);
         HIP_CHECK(hipStreamSynchronize(ctx.stream));
     } else {
-        e.vae->decode(d_lat.f(), kLat, kLat, d_dec.f());
+        e.vae->decode(d.lat, kLat, kLat, d.dec);
     }
     report(ctx, progress, user, 2, 1, 1);
 
     // 10: 8-bit truncation, resampled back to the window, pasted on the host.
-    DevBuf d_u8(model_px * 3), d_res(side * side * 3);
-    to_u8(ctx, d_dec.f(), int64_t(model_px) * 3, d_u8.u8());
-    resize_u8(ctx, d_u8.u8(), kSide, kSide, int(side), int(side), 3, d_res.u8());
+    to_u8(ctx, d.dec, int64_t(model_px) * 3, d.u8);
+    resize_u8(ctx, d.u8, kSide, kSide, int(side), int(side), 3, d.res);
     std::vector<uint8_t> result(side * side * 3);
-    d2h(ctx, result.data(), d_res.p, result.size());
+    d2h(ctx, result.data(), d.res, result.size());
     return img::paste(im, mask, result.data(), plan, p.paste, e.host_threads);
 }
 

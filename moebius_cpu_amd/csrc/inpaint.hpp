@@ -49,6 +49,9 @@ struct Engine {
     std::unique_ptr<UNet> unet;
     std::unique_ptr<Vae> vae;
     unsigned host_threads = 1;  // host threads for the paste around the device run
+    // the inpaint call's device frames (window, model inputs, latents, decode),
+    // grow-only: a call at a window side no larger than an earlier one allocates nothing
+    Workspace frames;
     explicit Engine(int device) : ctx(device) {}
 };
 

@@ -483,6 +483,12 @@ void group_norm_forward(Context &ctx, const float *x, int n, int h, int w, int c
 // `scratch` itself to a kernel (on the host the name is only a stand-in): the
 // device address comes from hipGetSymbolAddress, taken once per device when a
 // context is created on it (noalloc_scratch_setup) and kept in g_scratch_ptr.
+// Calls from different streams (two contexts on one GPU) are ordered on the
+// device: each call records g_scratch_done on its stream, and a call from
+// another stream first waits for that event, so its kernels start only after
+// the previous user of the array has finished with it. A stream under graph
+// capture takes no part in this ordering (its graph's launches are ordered by
+// whoever launches them).
 constexpr int64_t kNoAllocScratchFloats = int64_t(1) << 18;  // 1 MiB
 static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
 
@@ -490,6 +496,8 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 float *g_scratch_ptr[kMaxDevices] = {};
+hipEvent_t g_scratch_done[kMaxDevices] = {};
+hipStream_t g_scratch_last[kMaxDevices] = {};  // stream of the last recorded call
 }  // namespace
 
 void noalloc_scratch_setup(int device) {
@@ -502,7 +510,10 @@ void noalloc_scratch_setup(int device) {
     void *ptr = nullptr;
     HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
     if (!ptr) fail(kInternal, "hipGetSymbolAddress returned no address for the GroupNorm scratch");
+    hipEvent_t done = nullptr;
+    HIP_CHECK(hipEventCreateWithFlags(&done, hipEventDisableTiming));
     g_scratch_ptr[device] = static_cast<float *>(ptr);
+    g_scratch_done[device] = done;
 }
 
 int64_t group_norm_noalloc_max_floats() { return kNoAllocScratchFloats; }
@@ -518,13 +529,22 @@ void group_norm_forward_noalloc(Context &ctx, const float *x, int n, int h, int 
                                    std::to_string(int64_t(n) * c) + "), more than the fixed " +
                                    std::to_string(kNoAllocScratchFloats) + " (1 MiB)");
     }
-    float *base = nullptr;
-    {
-        std::lock_guard<std::mutex> lock(g_scratch_mu);
-        base = ctx.device >= 0 && ctx.device < kMaxDevices ? g_scratch_ptr[ctx.device] : nullptr;
-    }
+    // held across the launches, so that host threads take the array in the
+    // order their waits and records were queued
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    const int dev = ctx.device;
+    float *base = dev >= 0 && dev < kMaxDevices ? g_scratch_ptr[dev] : nullptr;
     if (!base) fail(kInternal, "GroupNorm (no allocation): scratch address not set up for this device");
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    HIP_CHECK(hipStreamIsCapturing(ctx.stream, &cap));
+    const bool order = cap == hipStreamCaptureStatusNone;
+    if (order && g_scratch_last[dev] && g_scratch_last[dev] != ctx.stream)
+        HIP_CHECK(hipStreamWaitEvent(ctx.stream, g_scratch_done[dev], 0));
     group_norm_forward_in(ctx, x, n, h, w, c, groups, eps, gamma, beta, add, silu, out, add_ld, base, s.aff_off);
+    if (order) {
+        HIP_CHECK(hipEventRecord(g_scratch_done[dev], ctx.stream));
+        g_scratch_last[dev] = ctx.stream;
+    }
 }
 
 void layer_norm(Context &ctx, const float *x, int64_t rows, int c, const float *gamma, const float *beta, float eps,

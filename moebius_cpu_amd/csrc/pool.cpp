@@ -48,7 +48,7 @@ float *Pool::floats(int64_t count) {
         return best->p;
     }
     Buf b{nullptr, len, len, true};
-    HIP_CHECK(hipMalloc(&b.p, len * sizeof(float)));
+    mh::dev_malloc(&b.p, len * sizeof(float));
     bufs_.push_back(b);
     ++allocations_;
     return b.p;

@@ -62,7 +62,7 @@ WeightStore::WeightStore(Context &ctx, const NamedTensor *t, int count, bool wid
         off[size_t(i)] = total;
         total += (t[i].numel * (t[i].dtype == kF16 ? 2 : 4) + 255) & ~size_t(255);
     }
-    HIP_CHECK(hipMalloc(&block_, total ? total : 256));
+    mh::dev_malloc(&block_, total ? total : 256);
     bytes_ = total;
     for (int i = 0; i < count; ++i) {
         char *dst = static_cast<char *>(block_) + off[size_t(i)];
@@ -82,7 +82,7 @@ WeightStore::WeightStore(Context &ctx, const NamedTensor *t, int count, bool wid
         if (widen && kv.second.d.wt == kF16) wide += (size_t(kv.second.d.numel) * 4 + 255) & ~size_t(255);
     if (wide) {
         void *blk = nullptr;
-        HIP_CHECK(hipMalloc(&blk, wide));
+        mh::dev_malloc(&blk, wide);
         derived_.push_back(blk);
         derived_bytes_ += wide;
         char *dst = static_cast<char *>(blk);
@@ -106,7 +106,7 @@ const float *WeightStore::winograd_kernel(const DParam &w, int co, int ci) const
     if (w.numel != int64_t(co) * 9 * ci) fail(kWeights, "Winograd kernel: 3x3 weight has the wrong size");
     const size_t bytes = size_t(16) * co * ci * sizeof(float);
     void *u = nullptr;
-    HIP_CHECK(hipMalloc(&u, bytes));
+    mh::dev_malloc(&u, bytes);
     derived_.push_back(u);
     derived_bytes_ += bytes;
     winograd_weight_transform(ctx_, w.p, w.wt, co, ci, static_cast<float *>(u));
@@ -116,7 +116,7 @@ const float *WeightStore::winograd_kernel(const DParam &w, int co, int ci) const
 const float *WeightStore::winograd_kernel_fused(const float *u, int co, int ci) const {
     const size_t bytes = size_t(16) * co * ci * sizeof(float);
     void *uf = nullptr;
-    HIP_CHECK(hipMalloc(&uf, bytes));
+    mh::dev_malloc(&uf, bytes);
     derived_.push_back(uf);
     derived_bytes_ += bytes;
     winograd_fused_weights(ctx_, u, co, ci, static_cast<float *>(uf));
@@ -155,7 +155,7 @@ WeightGroup concat_weights(Context &ctx, const DParam *members, int count) {
     }
     g.wt = all_f16 ? kF16 : kF32;
     const size_t esz = all_f16 ? 2 : 4;
-    HIP_CHECK(hipMalloc(&g.p, size_t(total) * esz));
+    mh::dev_malloc(&g.p, size_t(total) * esz);
     char *dst = static_cast<char *>(g.p);
     for (int i = 0; i < count; ++i) {
         const DParam &m = members[i];
@@ -457,11 +457,11 @@ struct LnFold {
     void *w16 = nullptr;
     void build(Context &ctx, const void *w, WeightType wt, int n, int k, const float *gamma, const float *beta,
                const float *bias) {
-        HIP_CHECK(hipMalloc(&w32, size_t(n) * k * sizeof(float)));
-        HIP_CHECK(hipMalloc(&w16, size_t(n) * k * 2));
-        HIP_CHECK(hipMalloc(&c1_32, size_t(n) * sizeof(float)));
-        HIP_CHECK(hipMalloc(&c1_16, size_t(n) * sizeof(float)));
-        HIP_CHECK(hipMalloc(&c2, size_t(n) * sizeof(float)));
+        mh::dev_malloc(&w32, size_t(n) * k * sizeof(float));
+        mh::dev_malloc(&w16, size_t(n) * k * 2);
+        mh::dev_malloc(&c1_32, size_t(n) * sizeof(float));
+        mh::dev_malloc(&c1_16, size_t(n) * sizeof(float));
+        mh::dev_malloc(&c2, size_t(n) * sizeof(float));
         ln_fold_weights(ctx, w, wt, n, k, gamma, beta, bias, w32, w16, c1_32, c1_16, c2);
     }
     LnFolded view(float eps) const {
@@ -497,7 +497,7 @@ struct SelfLambda {
             for (int d = 0; d < TAPS; ++d) t[size_t(d) * k + kk] = w[kk * TAPS + d];
             t[size_t(TAPS) * k + kk] = b[kk];
         }
-        HIP_CHECK(hipMalloc(&w_aug_t, t.size() * sizeof(float)));
+        mh::dev_malloc(&w_aug_t, t.size() * sizeof(float));
         HIP_CHECK(hipMemcpy(w_aug_t, t.data(), t.size() * sizeof(float), hipMemcpyHostToDevice));
         to_q.load(W, p + ".to_q", c, c, true);
         to_k.load(W, p + ".to_k", c, k, false);
@@ -507,9 +507,9 @@ struct SelfLambda {
         const WeightGroup grp = concat_weights(e.ctx, members, 3);
         wqkv = grp.p;
         wt = grp.wt;
-        HIP_CHECK(hipMalloc(&bqkv, size_t(c + 2 * k) * sizeof(float)));
+        mh::dev_malloc(&bqkv, size_t(c + 2 * k) * sizeof(float));
         if (wt == kF16) {
-            HIP_CHECK(hipMalloc(&wqkv32, size_t(c + 2 * k) * c * sizeof(float)));
+            mh::dev_malloc(&wqkv32, size_t(c + 2 * k) * c * sizeof(float));
             widen_f16(e.ctx, wqkv, int64_t(c + 2 * k) * c, wqkv32);
         }
         std::vector<float> zeros(size_t(k), 0.0f);
@@ -588,8 +588,8 @@ struct CrossLambda {
         const DParam wk = W.get(p + ".to_k.weight", int64_t(k) * XDIM, true);
         const DParam wv = W.get(p + ".to_v.weight", int64_t(k) * XDIM, true);
         const float *bv = W.get(p + ".to_v.bias", k, false).f();
-        HIP_CHECK(hipMalloc(&lambda_c, size_t(2) * k * k * sizeof(float)));
-        HIP_CHECK(hipMalloc(&v, size_t(2) * TOKENS * k * sizeof(float)));
+        mh::dev_malloc(&lambda_c, size_t(2) * k * k * sizeof(float));
+        mh::dev_malloc(&v, size_t(2) * TOKENS * k * sizeof(float));
         float *keys = env.pool.floats(int64_t(2) * TOKENS * k);
         for (int br = 0; br < 2; ++br) {
             const float *x = ehs_dev + int64_t(br) * TOKENS * XDIM;
@@ -847,12 +847,12 @@ class UNetDevice {
             const WeightGroup grp = concat_weights(ctx_, members.data(), int(members.size()));
             temb_w_ = grp.p;
             temb_wt_ = grp.wt;
-            HIP_CHECK(hipMalloc(&temb_b_, size_t(temb_total_) * sizeof(float)));
+            mh::dev_malloc(&temb_b_, size_t(temb_total_) * sizeof(float));
             for (DwResnet *r : rs)
                 HIP_CHECK(hipMemcpyAsync(temb_b_ + r->temb_off, r->temb_proj.b, size_t(r->co) * sizeof(float),
                                          hipMemcpyDeviceToDevice, ctx_.stream));
             if (temb_wt_ == kF16) {
-                HIP_CHECK(hipMalloc(&temb_w32_, size_t(temb_total_) * TIME_EMBED * sizeof(float)));
+                mh::dev_malloc(&temb_w32_, size_t(temb_total_) * TIME_EMBED * sizeof(float));
                 widen_f16(ctx_, temb_w_, int64_t(temb_total_) * TIME_EMBED, temb_w32_);
             }
         }
@@ -867,7 +867,7 @@ class UNetDevice {
         // host once, so a step reads its row from HBM with no host copy or sync.
         std::vector<float> sinus(size_t(kSinusSteps + 1) * TIME_PROJ);
         for (int t = 0; t < kSinusSteps; ++t) timestep_sinusoid(t, sinus.data() + size_t(t) * TIME_PROJ);
-        HIP_CHECK(hipMalloc(&sinus_dev_, sinus.size() * sizeof(float)));
+        mh::dev_malloc(&sinus_dev_, sinus.size() * sizeof(float));
         HIP_CHECK(hipMemcpy(sinus_dev_, sinus.data(), size_t(kSinusSteps) * TIME_PROJ * sizeof(float),
                             hipMemcpyHostToDevice));
     }

@@ -221,7 +221,7 @@ struct MidAttention {
         const WeightGroup grp = concat_weights(ctx, ws, 3);
         wqkv = grp.p;
         wt = grp.wt;
-        HIP_CHECK(hipMalloc(&bqkv, 3 * size_t(c) * sizeof(float)));
+        mh::dev_malloc(&bqkv, 3 * size_t(c) * sizeof(float));
         for (int i = 0; i < 3; ++i)
             HIP_CHECK(hipMemcpyAsync(bqkv + i * c, bs[i], size_t(c) * sizeof(float), hipMemcpyDeviceToDevice,
                                      ctx.stream));

@@ -35,6 +35,13 @@ def _close_live_contexts():
             pass
 
 
+def device_allocations() -> int:
+    """Device allocations (hipMalloc calls) the library has made since it was loaded."""
+    n = ctypes.c_uint64()
+    check(lib().mh_device_allocations(ctypes.byref(n)))
+    return int(n.value)
+
+
 class Context:
     """One device, one stream (include/moebius_hip.h `MhContext`)."""
 

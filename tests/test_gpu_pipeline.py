@@ -203,11 +203,13 @@ def test_seeded_c_api_equals_the_same_noise_given_explicitly(engine):
     r2 = engine.inpaint_with_noise(b, mask, InpaintParams.resolve(preset=1, steps=2, seed=99), NoiseSet.sample(99))
     assert np.array_equal(a, b) and (rect.x, rect.y, rect.width, rect.height) == (r2.x, r2.y, r2.w, r2.h)
     assert not np.array_equal(a, img)
-    # the models' buffers stay resident: a repeated call allocates nothing more
-    before = engine.memory()
+    # the models' pools, the frames and the loop state stay resident: a repeated
+    # call makes no device allocation at all
+    before, allocs = engine.memory(), E.device_allocations()
     engine.inpaint_with_noise(img.copy(), mask, InpaintParams.resolve(preset=1, steps=2, seed=99),
                               NoiseSet.sample(99))
     assert engine.memory() == before
+    assert E.device_allocations() == allocs, "a repeated inpaint call allocated device memory"
     # released on request, allocated again by the next call, same result
     engine.release_scratch()
     assert engine.memory()[1] < before[1] and engine.memory()[0] == before[0]

@@ -104,8 +104,11 @@ def cpu_run(workload, extra=(), timeout=900):
     return json.loads(p.stdout.strip().splitlines()[-1])
 
 
-def cpu_record(ms, cores, sample):
-    return {"value": r(ms, 3), "unit": "ms", "cores": cores, "kind": "port", "sample": sample}
+def cpu_record(ms, cores, sample, model=None):
+    rec = {"value": r(ms, 3), "unit": "ms", "cores": cores, "kind": "port", "sample": sample}
+    if model:
+        rec["cpu_model"] = model
+    return rec
 
 
 # ---------------------------------------------------------------- cfg1
@@ -206,11 +209,78 @@ def cfg3_resnet(ctx, steps):
 
 # ---------------------------------------------------------------- cfg4
 
-# HBM bytes per launch of the dominant kernel (below), from rocprofv3 --pmc FETCH_SIZE and
-# WRITE_SIZE over this script's own run, each scaled by the counter's reading for a plain
-# 256 MiB device copy (FETCH_SIZE reads half the copied bytes, WRITE_SIZE all of them),
-# averaged over the timed standalone loop's 200 launches: 13.27 MiB fetched + 10.00 MiB written.
-DOMINANT_TRAFFIC_BYTES = 24420121
+# HBM bytes per launch of the dominant kernel come from the committed rocprofv3 --pmc summary
+# (FETCH_SIZE and WRITE_SIZE passes over this script's own run, each scaled by the counter's
+# reading for a plain device copy), which names the GEMM configuration it measured on a line
+#   traffic_config: <config> | traffic_bytes_per_launch: <bytes>
+# The figure is used only while the live configuration of that GEMM is the same one.
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "unet_step_traffic_pmc.md")
+
+
+def _profiled_traffic(config):
+    """(bytes, note) from the committed PMC summary for this GEMM configuration."""
+    import re
+
+    try:
+        with open(TRAFFIC_PROFILE, encoding="utf-8") as f:
+            text = f.read()
+    except OSError:
+        return None, "no committed PMC summary"
+    m = re.search(r"^traffic_config: (.+?) \| traffic_bytes_per_launch: (\d+)\s*$", text, re.M)
+    if not m:
+        return None, "the PMC summary names no traffic line"
+    if m.group(1).strip() != config:
+        return None, f"the PMC summary measured '{m.group(1).strip()}', not the live '{config}'"
+    return int(m.group(2)), "from " + os.path.relpath(TRAFFIC_PROFILE, ROOT)
+
+
+def _gemm_config(ctx, fn):
+    """The kernel configuration key (mh_context_gemm_times) of the GEMM fn launches."""
+    ctx.set_tuning("gemm_time", 1)
+    try:
+        fn()
+        recs = ctx.gemm_times()
+    finally:
+        ctx.set_tuning("gemm_time", None)
+    return recs[0]["config"] if recs else None
+
+
+def _in_step_gemms(ctx, step, steps, peak, config=None, overhead_us=0.0):
+    """Every GEMM launch of `steps` denoise steps timed with events around it, grouped
+    by kernel configuration: the configuration with the most step time (and the
+    standalone dominant kernel's configuration, when given) with their in-step
+    launch time and rate, and the GEMMs' total per step. overhead_us: what the
+    events add to one launch (the standalone GEMM's evented minus plain launch
+    time), taken off each launch for the `_net` figures."""
+    ctx.set_tuning("gemm_time", 1)
+    try:
+        for _ in range(steps):
+            step()
+        recs = ctx.gemm_times()
+    finally:
+        ctx.set_tuning("gemm_time", None)
+
+    def entry(rec):
+        us = rec["us"] / rec["launches"]
+        tf = rec["flops"] / (rec["us"] * 1e-6) / 1e12
+        net = max(us - overhead_us, 1e-3)
+        tf_net = rec["flops"] / rec["launches"] / (net * 1e-6) / 1e12
+        return {"config": rec["config"], "launches_per_step": rec["launches"] / steps,
+                "us_per_step": r(rec["us"] / steps, 1), "avg_launch_us": r(us, 2), "achieved": r(tf, 2),
+                "unit": "TFLOP/s", "frac": r(tf / peak, 4), "avg_launch_us_net": r(net, 2),
+                "achieved_net": r(tf_net, 2), "frac_net": r(tf_net / peak, 4)}
+
+    recs.sort(key=lambda e: -e["us"])
+    out = {"method": "HIP events recorded before and after every GEMM launch (split-K reduce included) over "
+                     f"{steps} steps run after the timed ones; each launch's time includes its event overhead",
+           "event_overhead_us_per_launch": r(overhead_us, 2),
+           "gemm_us_per_step": r(sum(e["us"] for e in recs) / steps, 1),
+           "gemm_launches_per_step": sum(e["launches"] for e in recs) / steps,
+           "most_time": entry(recs[0]) if recs else None}
+    same = [e for e in recs if e["config"] == config]
+    if same:
+        out["dominant_config_in_step"] = entry(same[0])
+    return out
 
 
 def _dominant_gemm(ctx, steps, fast=False):
@@ -226,6 +296,16 @@ def _dominant_gemm(ctx, steps, fast=False):
     conv = E.Conv1x1(ctx, 320, 320, E.Param(ctx, S.normal(82, (320, 320), 0.05), f16=fast), S.normal(83, (320,), 0.02))
     y = E.Tensor(ctx)
     us = warm_time(ctx, lambda: conv.forward(x, y), steps, warmup=steps) * 1e3
+    config = _gemm_config(ctx, lambda: conv.forward(x, y))
+    # the same launches with an event before and after each (the in-step census's method)
+    ctx.set_tuning("gemm_time", 1)
+    try:
+        for _ in range(steps):
+            conv.forward(x, y)
+        rec = ctx.gemm_times()[0]
+    finally:
+        ctx.set_tuning("gemm_time", None)
+    event_us = rec["us"] / rec["launches"]
     flops = 2.0 * 8192 * 320 * 320
     tf = flops / (us * 1e-6) / 1e12
     if fast:
@@ -237,13 +317,14 @@ def _dominant_gemm(ctx, steps, fast=False):
                 "frac": round(gbps / PEAK_HBM_GBPS, 4), "traffic": None,
                 "work_per_launch": f"algorithmic bytes {nbytes}; {flops / 1e9:.3f} GFLOP "
                                    f"({tf:.1f} TFLOP/s = {tf / PEAK_F16_MFMA_TFLOPS:.3f} of f16 MFMA peak)",
-                "avg_launch_us": round(us, 2)}
-    return {"bound": "mfma", "kernel": "gemm_f32_kernel<32,64,dense> (1x1 conv [2,64,64,320] -> 320, "
-                                       "M=8192 N=320 K=320: the step's most frequent GEMM)",
+                "avg_launch_us": round(us, 2), "config": config, "evented_launch_us": round(event_us, 2)}
+    traffic, note = _profiled_traffic(config)
+    return {"bound": "mfma", "kernel": f"gemm_f32_kernel, {config} (1x1 conv [2,64,64,320] -> 320, "
+                                       "M=8192 N=320 K=320: the step's most frequent GEMM), timed standalone",
             "achieved": round(tf, 2), "peak": PEAK_F32_MFMA_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(tf / PEAK_F32_MFMA_TFLOPS, 4), "traffic": DOMINANT_TRAFFIC_BYTES,
+            "frac": round(tf / PEAK_F32_MFMA_TFLOPS, 4), "traffic": traffic, "traffic_source": note,
             "work_per_launch": f"{flops / 1e9:.3f} GFLOP; algorithmic bytes {(8192 * 320 * 2 + 320 * 320) * 4}",
-            "avg_launch_us": round(us, 2)}
+            "avg_launch_us": round(us, 2), "config": config, "evented_launch_us": round(event_us, 2)}
 
 
 def _components(ctx, steps):
@@ -285,7 +366,7 @@ def _unet_step_entry(ctx, net, inp, cfg, steps, warmup, fast):
     eps = E.DeviceArray(ctx, (b, 64, 64, 4))
     step = lambda: net.forward(x, inp.timestep, cfg, eps)  # noqa: E731
     ms = warm_time(ctx, step, steps, warmup)
-    flops = U.step_flops(b, winograd=True)["total"]
+    flops = U.step_flops(b, winograd=True, cfg_shared=cfg)["total"]
     direct = U.step_flops(b)["total"]
     peak = PEAK_F16_MFMA_TFLOPS if fast else PEAK_F32_MFMA_TFLOPS
     tf = flops / (ms * 1e-3) / 1e12
@@ -333,6 +414,12 @@ def bench_unet(args):
     }
     log("dominant kernel and component kernels")
     out["roofline"] = _dominant_gemm(ctx, 200, fast=args.fast)
+    log("GEMM launches inside the step")
+    xin = E.DeviceArray.from_numpy(ctx, inp.x)
+    eps = E.DeviceArray(ctx, (b, 64, 64, 4))
+    rl = out["roofline"]
+    rl["in_step"] = _in_step_gemms(ctx, lambda: net.forward(xin, inp.timestep, cfg, eps), 3, head["peak_tflops"],
+                                   rl.get("config"), max(0.0, rl["evented_launch_us"] - rl["avg_launch_us"]))
     ctx.set_precision(False)
     out["components"] = _components(ctx, 20)
     unet_entries = None
@@ -464,8 +551,8 @@ def attach_cpu(configs, cpu):
     if "error" in cpu:
         configs["cpu_error"] = cpu["error"]
         return
-    cores, c = cpu["cores"], cpu["configs"]
-    note = lambda s: {"cores": cores, "kind": "port", "sample": s}  # noqa: E731
+    cores, c, model = cpu["cores"], cpu["configs"], cpu.get("cpu_model")
+    note = lambda s: {"cores": cores, "cpu_model": model, "kind": "port", "sample": s}  # noqa: E731
     if "cfg1" in configs and "cfg1" in c:
         configs["cfg1"]["cpu"] = {"ms": c["cfg1"]["total_ms"], "conv_ms": c["cfg1"]["conv_ms"],
                                   "groupnorm_silu_ms": c["cfg1"]["gn_silu_ms"],
@@ -534,12 +621,13 @@ def run_all(args):
                 out["cpu_baseline"] = cpu_record(cpu["configs"][key], cpu["cores"],
                                                  "the same denoise step (same seeded weights and inputs), median "
                                                  "after one warm-up (C++ restatement of the CPU engine's UNet, "
-                                                 "OpenMP)")
+                                                 "OpenMP)", cpu.get("cpu_model"))
         else:
             cpu = cpu_run("unet_step", () if not args.cond_only else ("--cond-only",))
             if "error" not in cpu:
                 out["cpu_baseline"] = cpu_record(cpu["value"], cpu["cores"], cpu["sample"] +
-                                                 " (C++ restatement of the CPU engine's UNet, OpenMP)")
+                                                 " (C++ restatement of the CPU engine's UNet, OpenMP)",
+                                                 cpu.get("cpu_model"))
     return out
 
 

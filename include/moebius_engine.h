@@ -28,7 +28,7 @@
 extern "C" {
 #endif
 
-/* ---- the reference's API (include/moebius_cpu.h:11-80) ------------------- */
+/* ---- the reference's API (include/moebius_cpu.h:11-69) ------------------- */
 
 #define MOEBIUS_ABI_VERSION 1u
 

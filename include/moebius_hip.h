@@ -99,6 +99,15 @@ int32_t mh_context_set_precision(MhContext *ctx, uint32_t precision);
  * restores the measured default. The same settings are read once from the
  * MOEBIUS_HIP_<KEY> environment variables when the context is created. */
 int32_t mh_context_set_tuning(MhContext *ctx, const char *key, const char *value);
+/* GEMM launches timed on the device while the tuning key "gemm_time" is 1 (no
+ * counterpart in the reference): synchronises the context's stream, then writes
+ * into buf, as JSON, one record per kernel configuration (tile, wave layout,
+ * operand mode, grid) in order of first launch: {"config", "launches", "us" (the
+ * summed time between events recorded before and after each launch, its split-K
+ * reduce included), "flops" (2.M.N.K per launch, summed)}, and clears the
+ * records. *needed receives the text's size with its terminator; a buffer
+ * smaller than that returns MH_ERR_INVALID_ARGUMENT and keeps the records. */
+int32_t mh_context_gemm_times(MhContext *ctx, char *buf, uint64_t len, uint64_t *needed);
 /* The context's hipStream_t, for callers that order their own work with it. */
 void *mh_context_stream(MhContext *ctx);
 int32_t mh_synchronize(MhContext *ctx);

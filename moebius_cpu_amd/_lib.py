@@ -55,6 +55,7 @@ SIGNATURES = {
     "mh_context_set_precision": (_i32, [_vp, _u32]),
     "mh_context_set_tuning": (_i32, [_vp, ctypes.c_char_p, ctypes.c_char_p]),
     "mh_device_allocations": (_i32, [ctypes.POINTER(ctypes.c_uint64)]),
+    "mh_context_gemm_times": (_i32, [_vp, ctypes.c_char_p, _u64, ctypes.POINTER(_u64)]),
     "mh_context_stream": (_vp, [_vp]),
     "mh_synchronize": (_i32, [_vp]),
     "mh_device_arch": (_i32, [_vp, ctypes.c_char_p, _u32]),

@@ -136,6 +136,52 @@ int32_t mh_context_set_precision(MhContext *ctx, uint32_t precision) {
 
 void *mh_context_stream(MhContext *ctx) { return ctx ? static_cast<void *>(ctx->ctx.stream) : nullptr; }
 
+int32_t mh_context_gemm_times(MhContext *ctx, char *buf, uint64_t len, uint64_t *needed) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(buf, "buf");
+        need(needed, "needed");
+        HIP_CHECK(hipStreamSynchronize(c.stream));
+        struct Agg {
+            std::string key;
+            int64_t launches = 0;
+            double us = 0.0, flops = 0.0;
+        };
+        std::vector<Agg> aggs;
+        for (const mh::Context::GemmTime &g : c.gemm_times) {
+            float ms = 0.0f;
+            HIP_CHECK(hipEventElapsedTime(&ms, g.start, g.stop));
+            auto it = std::find_if(aggs.begin(), aggs.end(), [&](const Agg &a) { return a.key == g.key; });
+            if (it == aggs.end()) {
+                aggs.push_back(Agg{g.key});
+                it = aggs.end() - 1;
+            }
+            it->launches += 1;
+            it->us += double(ms) * 1e3;
+            it->flops += g.flops;
+        }
+        std::string out = "[";
+        for (size_t i = 0; i < aggs.size(); ++i) {
+            char row[320];
+            std::snprintf(row, sizeof row, "%s{\"config\": \"%s\", \"launches\": %lld, \"us\": %.3f, \"flops\": %.0f}",
+                          i ? ", " : "", aggs[i].key.c_str(), static_cast<long long>(aggs[i].launches), aggs[i].us,
+                          aggs[i].flops);
+            out += row;
+        }
+        out += "]";
+        *needed = out.size() + 1;
+        if (out.size() + 1 > len)
+            mh::fail(mh::kInvalidArgument, "buffer too small for the GEMM timings: " + std::to_string(out.size() + 1) +
+                                               " bytes needed");
+        std::memcpy(buf, out.c_str(), out.size() + 1);
+        for (const mh::Context::GemmTime &g : c.gemm_times) {
+            c.spare_events.push_back(g.start);
+            c.spare_events.push_back(g.stop);
+        }
+        c.gemm_times.clear();
+    });
+}
+
 int32_t mh_synchronize(MhContext *ctx) { return guard([&] { HIP_CHECK(hipStreamSynchronize(C(ctx).stream)); }); }
 
 int32_t mh_device_arch(MhContext *ctx, char *buf, uint32_t len) {

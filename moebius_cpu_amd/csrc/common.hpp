@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 namespace mh {
 
@@ -48,7 +49,7 @@ enum class Precision : uint32_t { Exact = 0, Fast = 1 };
 // Tuning overrides for A/B runs and tests, read once from the environment
 // (MOEBIUS_HIP_GEMM_PLAN, _GN_IN_MAXC, _DW_TILED, _TAP_HEADS, _CROSS_HEADS,
 // _GN_BLOCKS, _GN_APPLY, _WINO_FUSED, _UP_CONCAT, _LAMBDA_TAPS, _GEMM_LOG,
-// _GEMM_WIDE, _LN_FOLD, _TAP_SPLIT)
+// _GEMM_WIDE, _LN_FOLD, _TAP_SPLIT, _GEMM_TIME)
 // when a context is created and changed with set_tuning (mh_context_set_tuning).
 // The defaults are the measured choices; nothing on the hot path reads the
 // environment.
@@ -71,6 +72,7 @@ struct Tuning {
     int gemm_wide = 1;     // 0: the square tilings only (no wide wave layouts from the planner)
     int ln_fold = 0;       // 1: the transformers' LayerNorms 1 and 3 folded into the GEMMs that read them
     int tap_split = 0;     // per-thread tap filter: tap rows split over 1, 3 or 5 threads (0: by map size)
+    int gemm_time = 0;     // 1: record events around each GEMM launch (Context::gemm_times)
 };
 // Sets `key` from its text form (the environment variable's syntax); value NULL
 // or "" restores the default. False for an unknown key or a malformed value.
@@ -120,6 +122,17 @@ struct Context {
     // and apart from it, since the kernels of each step draw on ws.
     Workspace state;
     Tuning tune;
+    // GEMM launches timed on the device while tune.gemm_time is set: events
+    // recorded before and after each launch (its split-K reduce included),
+    // keyed by the kernel configuration, read and cleared by the caller.
+    struct GemmTime {
+        std::string key;
+        double flops;
+        hipEvent_t start, stop;
+    };
+    std::vector<GemmTime> gemm_times;
+    std::vector<hipEvent_t> spare_events;
+    hipEvent_t take_event();
 
     explicit Context(int dev);
     ~Context();

@@ -93,6 +93,7 @@ bool set_tuning(Tuning &t, const char *key, const char *value) {
     if (k == "up_concat") return to_int(t.up_concat, 0) && t.up_concat >= 0 && t.up_concat <= 1;
     if (k == "lambda_taps") return to_int(t.lambda_taps, 1) && t.lambda_taps >= 0 && t.lambda_taps <= 1;
     if (k == "gemm_log") return to_int(t.gemm_log, 0);
+    if (k == "gemm_time") return to_int(t.gemm_time, 0) && t.gemm_time >= 0 && t.gemm_time <= 1;
     if (k == "gemm_wide") return to_int(t.gemm_wide, 1) && t.gemm_wide >= 0 && t.gemm_wide <= 1;
     if (k == "ln_fold") return to_int(t.ln_fold, 0) && t.ln_fold >= 0 && t.ln_fold <= 1;
     if (k == "tap_split") return to_int(t.tap_split, 0) && (t.tap_split == 0 || t.tap_split == 1 || t.tap_split == 3 ||
@@ -127,6 +128,7 @@ Context::Context(int dev) : device(dev) {
                                               {"MOEBIUS_HIP_LAMBDA_TAPS", "lambda_taps"},
                                               {"MOEBIUS_HIP_GEMM_LOG", "gemm_log"},
                                               {"MOEBIUS_HIP_GEMM_WIDE", "gemm_wide"},
+                                              {"MOEBIUS_HIP_GEMM_TIME", "gemm_time"},
                                               {"MOEBIUS_HIP_LN_FOLD", "ln_fold"},
                                               {"MOEBIUS_HIP_TAP_SPLIT", "tap_split"}};
     for (const auto &kv : env_keys)
@@ -150,7 +152,23 @@ Context::Context(int dev) : device(dev) {
 
 Context::~Context() {
     if (stream) (void)hipStreamSynchronize(stream);
+    for (const GemmTime &g : gemm_times) {
+        (void)hipEventDestroy(g.start);
+        (void)hipEventDestroy(g.stop);
+    }
+    for (hipEvent_t e : spare_events) (void)hipEventDestroy(e);
     if (stream) (void)hipStreamDestroy(stream);
+}
+
+hipEvent_t Context::take_event() {
+    if (!spare_events.empty()) {
+        hipEvent_t e = spare_events.back();
+        spare_events.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    HIP_CHECK(hipEventCreate(&e));
+    return e;
 }
 
 }  // namespace mh

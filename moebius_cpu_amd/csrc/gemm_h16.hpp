@@ -300,6 +300,7 @@ template <int BM, int BN, int MODE, int PRO, bool F16, bool BVEC>
 void launch_cfg_h16(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int batch) {
     const unsigned tiles = unsigned(ceil_div(p.M, BM) * ceil_div(p.N, BN));
     log_gemm(ctx, "f16", p, BM, BN, pl.splits, MODE, PRO, F16, epi, batch);
+    const GemmTimer timer(ctx, "f16", p, BM, BN, 2, 2, 1, pl.splits, MODE, batch);
     if (pl.splits > 1) {
         const size_t bytes = size_t(pl.splits) * p.M * p.N * sizeof(float);
         p.partial = static_cast<float *>(ctx.ws.get(bytes, ctx.stream));

@@ -1177,6 +1177,31 @@ inline void log_gemm(const Context &ctx, const char *family, const GemmArgs &p, 
                  int(p.gnp != nullptr), p.nseg, p.rg, int(p.a2 != nullptr));
 }
 
+// Device timing of one GEMM launch (its split-K reduce included) while
+// tune.gemm_time is set: an event before the launch here, one after it when the
+// timer leaves scope, keyed by the kernel configuration and its grid.
+struct GemmTimer {
+    Context &ctx;
+    bool on;
+    GemmTimer(Context &c, const char *family, const GemmArgs &p, int bm, int bn, int wm, int wn, int wk, int splits,
+              int mode, int batch)
+        : ctx(c), on(c.tune.gemm_time != 0) {
+        if (!on) return;
+        const int64_t tiles = ceil_div(p.M, bm) * ceil_div(p.N, bn);
+        char key[160];
+        std::snprintf(key, sizeof key, "%s %dx%d waves %dx%dx%d mode %d grid %lldx%dx%d", family, bm, bn, wm, wn, wk,
+                      mode, static_cast<long long>(tiles), splits > 1 ? 1 : batch, splits);
+        Context::GemmTime g{key, 2.0 * double(p.M) * p.N * p.K * batch, c.take_event(), c.take_event()};
+        HIP_CHECK(hipEventRecord(g.start, c.stream));
+        c.gemm_times.push_back(std::move(g));
+    }
+    ~GemmTimer() {
+        if (on) (void)hipEventRecord(ctx.gemm_times.back().stop, ctx.stream);
+    }
+    GemmTimer(const GemmTimer &) = delete;
+    GemmTimer &operator=(const GemmTimer &) = delete;
+};
+
 template <int BM, int BN, int WM, int WN, int WK, int MODE, int PRO, bool F16, bool BVEC, bool PIPE = false,
           int BKT = BK>
 void launch_cfg(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int batch) {
@@ -1184,6 +1209,7 @@ void launch_cfg(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int
     constexpr bool kSquare = Waves<BM, BN, WM, WN, WK>::kFixedQuads;
     const unsigned tiles = unsigned(ceil_div(p.M, BM) * ceil_div(p.N, BN));
     log_gemm(ctx, PIPE ? "f32p" : "f32", p, BM, BN, pl.splits, MODE, PRO, F16, epi, batch, WM, WN, WK);
+    const GemmTimer timer(ctx, PIPE ? "f32p" : "f32", p, BM, BN, WM, WN, WK, pl.splits, MODE, batch);
     if (pl.splits > 1) {
         const size_t bytes = size_t(pl.splits) * p.M * p.N * sizeof(float);
         p.partial = static_cast<float *>(ctx.ws.get(bytes, ctx.stream));

@@ -52,6 +52,21 @@ class Context:
         self._models = weakref.WeakSet()  # UNet / Vae objects, destroyed before the context
         _live_contexts.add(self)
 
+    def gemm_times(self) -> list:
+        """The GEMM launches timed since the tuning key "gemm_time" was set to 1 (or
+        since the last call), one record per kernel configuration: config,
+        launches, us (summed), flops (summed). Clears the records."""
+        import json
+
+        needed = ctypes.c_uint64()
+        buf = ctypes.create_string_buffer(1 << 16)
+        st = lib().mh_context_gemm_times(self.h, buf, len(buf), ctypes.byref(needed))
+        if st != 0 and needed.value > len(buf):
+            buf = ctypes.create_string_buffer(int(needed.value))
+            st = lib().mh_context_gemm_times(self.h, buf, len(buf), ctypes.byref(needed))
+        check(st)
+        return json.loads(buf.value.decode())
+
     def adopt(self, model):
         """Registers a model (anything with close()) to be closed before this context."""
         self._models.add(model)

@@ -151,15 +151,19 @@ def param_count() -> int:
     return sum(int(np.prod(s.shape)) for s in unet_specs())
 
 
-def step_flops(batch: int = 2, winograd: bool = False) -> dict:
+def step_flops(batch: int = 2, winograd: bool = False, cfg_shared: bool = False) -> dict:
     """Algorithmic FLOPs of one denoise step (multiply-add = 2), by kernel
     family, for the architecture above at a 64x64 latent: the GEMM-shaped
     work (1x1 convs and linears, the dense 3x3 convs, the lambda GEMMs) and
     the vector work (depthwise, tap filter, position term). winograd: count
     the two upsample convs as the Winograd F(2x2,3x3) GEMM work this build
-    executes (else as direct convs)."""
+    executes (else as direct convs). cfg_shared: count the part both CFG
+    branches share (conv_in, the first resnet, and the first transformer up to
+    its self-lambda, everything before the text conditioning enters) once, as
+    the device runs it, instead of per item as the algorithm states it."""
     f = {"gemm_1x1": 0.0, "conv3x3": 0.0, "lambda_gemm": 0.0, "depthwise": 0.0, "tap_filter": 0.0,
          "position_term": 0.0}
+    shared = cfg_shared and batch > 1
 
     def res(p, ci, co):
         f["depthwise"] += 18 * p * (ci + co)
@@ -167,25 +171,33 @@ def step_flops(batch: int = 2, winograd: bool = False) -> dict:
         if ci != co:
             f["gemm_1x1"] += 2 * p * ci * co
 
-    def tr(p, c):
+    def tr(p, c, p_self=None):
+        """p_self: the pixels the part before the cross-lambda runs over (GroupNorm,
+        proj_in, LayerNorm 1, the self-lambda), when that differs from p."""
         k = c // HEADS
         hid = int(c * 2.5)
-        f["gemm_1x1"] += 2 * p * (4 * c * c + 2 * c * k + c * 2 * hid + hid * c)
-        f["lambda_gemm"] += 2 * p * k * k + 2 * p * HEADS * k * k * 2 + 2 * p * HEADS * k * 226
-        f["tap_filter"] += 2 * p * HEADS * 225 * k
+        ps = p if p_self is None else p_self
+        f["gemm_1x1"] += 2 * ps * (2 * c * c + 2 * c * k) + 2 * p * (2 * c * c + c * 2 * hid + hid * c)
+        f["lambda_gemm"] += 2 * ps * (k * k + HEADS * k * k + HEADS * k * 226) + 2 * p * HEADS * k * k
+        f["tap_filter"] += 2 * ps * HEADS * 225 * k
         f["position_term"] += p * HEADS * TOKENS * 4 * k
         f["depthwise"] += 18 * p * 2 * hid
 
     side = [64, 32, 16]
-    f["depthwise"] += 18 * batch * 4096 * 9
-    f["gemm_1x1"] += 2 * batch * 4096 * 9 * CH[0] + 2 * batch * 4096 * CH[0] * 4
-    f["depthwise"] += 18 * batch * 4096 * CH[0]
+    b_in = 1 if shared else batch
+    f["depthwise"] += 18 * b_in * 4096 * 9 + 18 * batch * 4096 * CH[0]
+    f["gemm_1x1"] += 2 * b_in * 4096 * 9 * CH[0] + 2 * batch * 4096 * CH[0] * 4
     c_prev = CH[0]
     for i, c in enumerate(CH):
         p = batch * side[i] ** 2
         for j in range(LAYERS):
-            res(p, c_prev if j == 0 else c, c)
-            tr(p, c)
+            first = shared and i == 0 and j == 0
+            if first:  # (res counts the time projection per item: it still runs at the batch)
+                res(side[i] ** 2, c_prev, c)
+                tr(p, c, p_self=side[i] ** 2)
+            else:
+                res(p, c_prev if j == 0 else c, c)
+                tr(p, c)
         if i + 1 < 3:
             f["conv3x3"] += 2 * (p // 4) * 9 * c * c
         c_prev = c

@@ -21,6 +21,18 @@ if ROOT not in sys.path:
 import oracle  # noqa: E402
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), "unknown" where it is not readable."""
+    try:
+        with open("/proc/cpuinfo", encoding="utf-8", errors="replace") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def _time(fn, budget_s, min_runs, max_runs):
     fn()  # warm-up
     times = []
@@ -163,7 +175,7 @@ def main():
     if args.threads > 0:
         oracle.set_threads(args.threads)
     if args.workload == "configs":
-        print(json.dumps({"cores": oracle.threads(), "configs": configs()}))
+        print(json.dumps({"cores": oracle.threads(), "cpu_model": cpu_model(), "configs": configs()}))
         return
     if args.workload == "unet_step":
         ms, runs, sample = unet_step(not args.cond_only, args.budget_s)
@@ -173,8 +185,8 @@ def main():
         ms, runs, sample = vae_encode(args.budget_s)
     else:
         ms, runs, sample = conv3x3_gn_silu(args.budget_s)
-    print(json.dumps({"value": round(ms, 3), "unit": "ms", "cores": oracle.threads(), "runs": runs,
-                      "sample": sample}))
+    print(json.dumps({"value": round(ms, 3), "unit": "ms", "cores": oracle.threads(), "cpu_model": cpu_model(),
+                      "runs": runs, "sample": sample}))
 
 
 if __name__ == "__main__":

@@ -133,6 +133,14 @@ CASES = {
     "roi_decode_compensate": dict(hwc=(200, 200, 3), mask=("rect", 60, 90, 110, 130), preset=Preset.EXACT,
                                   over=dict(steps=2, strength=0.5, spacing="trailing", roi_decode=True,
                                             paste="feather_compensate")),
+    # The presets unchanged on the benchmark's call: a 1024x768 RGB image with a 400x300 mask, so an
+    # 800 px window resampled to 512 and back. Exact: 19 leading DDIM steps (20 at strength 0.99), CFG
+    # 2.5 on every step, feathered paste. Fast: 9 trailing DPM-Solver++(2M) steps, CFG on the first 3,
+    # the ROI encode (the mask's latent box plus its margin is 48x40 of the 64x64 latents).
+    "exact_full_preset": dict(hwc=(768, 1024, 3), mask=("rect", 312, 234, 712, 534), preset=Preset.EXACT,
+                              over=dict()),
+    "fast_full_preset": dict(hwc=(768, 1024, 3), mask=("rect", 312, 234, 712, 534), preset=Preset.FAST,
+                             over=dict()),
 }
 
 

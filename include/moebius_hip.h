@@ -301,6 +301,27 @@ int32_t mh_conv1x1_layer_norm(MhContext *ctx, const float *x, uint64_t rows, uin
                               const float *beta, float eps, const void *weight, uint32_t weight_dtype, uint32_t c_out,
                               const float *bias, uint32_t silu, float *out);
 
+/* mh_conv1x1_layer_norm with each row's mean and variance from partial sums
+ * written by the producer of x (src/engine/norm.rs:151-173's statistics, summed
+ * in a different order): row_partials [rows][per_row][2] = (sum, sum of
+ * squares) over disjoint column ranges covering the row, as
+ * mh_conv1x1_row_partials and mh_cross_lambda_row_sums write them; summed in
+ * order in f64. 8-byte aligned; per_row 1..4096. */
+int32_t mh_conv1x1_layer_norm_stats(MhContext *ctx, const float *x, uint64_t rows, uint32_t c_in, const float *gamma,
+                                    const float *beta, float eps, const void *weight, uint32_t weight_dtype,
+                                    uint32_t c_out, const float *bias, uint32_t silu, const float *row_partials,
+                                    uint32_t per_row, float *out);
+
+/* src/engine/conv.rs:38-55 `Conv1x1::forward` (bias, no residual) whose
+ * epilogue also writes the LayerNorm row partials of its output for the
+ * LayerNorm that reads it next (the transformers' proj_in before LayerNorm 1,
+ * src/unet/transformer.rs:97-99): row_partials [rows][*per_row][2], room for
+ * rows * ceil(c_out / 32) pairs, 8-byte aligned. *per_row receives the number
+ * written per row (0 where the tiling cannot write them: then out alone). */
+int32_t mh_conv1x1_row_partials(MhContext *ctx, const float *x, uint64_t rows, uint32_t c_in, const void *weight,
+                                uint32_t weight_dtype, uint32_t c_out, const float *bias, float *out,
+                                float *row_partials, uint32_t *per_row);
+
 /* src/engine/ops.rs:11-13 `silu_inplace` (in place). */
 int32_t mh_silu_inplace(MhContext *ctx, float *x, uint64_t len);
 /* src/engine/ops.rs:16-19 `add_inplace`: a += b (in place on a). */
@@ -368,6 +389,14 @@ int32_t mh_position_term(MhContext *ctx, const float *q, const float *e, const f
  * mh_position_term. out may alias residual, not q. k a multiple of 8, <= 256. */
 int32_t mh_cross_lambda(MhContext *ctx, const float *q, const float *e, const float *lambda_c, const float *v_branches,
                         uint32_t br0, uint32_t nb, uint32_t hw, uint32_t k, const float *residual, float *out);
+
+/* mh_cross_lambda that also writes, per output row, the (sum, sum of squares)
+ * of the values written (row_sums [nb * hw][2], 8-byte aligned): the
+ * statistics of LayerNorm 3, which reads the block's hidden state next
+ * (src/unet/transformer.rs:104-107), for mh_conv1x1_layer_norm_stats (per_row 1). */
+int32_t mh_cross_lambda_row_sums(MhContext *ctx, const float *q, const float *e, const float *lambda_c,
+                                 const float *v_branches, uint32_t br0, uint32_t nb, uint32_t hw, uint32_t k,
+                                 const float *residual, float *out, float *row_sums);
 
 /* src/engine/gemm.rs:63-132 `matmul` for K-contiguous operands, on the device:
  * c [m][ldc] = a [m][lda] . b[n][ldb]^T (+ bias[n]) (+ residual [m][ldc]); b F32/F16.

@@ -92,6 +92,9 @@ SIGNATURES = {
     "mh_apply_affine": (_i32, [_vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _u32, _vp]),
     "mh_layer_norm": (_i32, [_vp, _vp, _u64, _u32, _vp, _vp, _f32, _vp]),
     "mh_conv1x1_layer_norm": (_i32, [_vp, _vp, _u64, _u32, _vp, _vp, _f32, _vp, _u32, _u32, _vp, _u32, _vp]),
+    "mh_conv1x1_layer_norm_stats": (_i32, [_vp, _vp, _u64, _u32, _vp, _vp, _f32, _vp, _u32, _u32, _vp, _u32, _vp,
+                                           _u32, _vp]),
+    "mh_conv1x1_row_partials": (_i32, [_vp, _vp, _u64, _u32, _vp, _u32, _u32, _vp, _vp, _vp, ctypes.POINTER(_u32)]),
     "mh_silu_inplace": (_i32, [_vp, _vp, _u64]),
     "mh_add_inplace": (_i32, [_vp, _vp, _vp, _u64]),
     "mh_concat_channels": (_i32, [_vp, _vp, _u32, _vp, _u32, _u64, _vp]),
@@ -104,6 +107,7 @@ SIGNATURES = {
     "mh_lambda_position_coeffs": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp]),
     "mh_position_term": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     "mh_cross_lambda": (_i32, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp]),
+    "mh_cross_lambda_row_sums": (_i32, [_vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),
     "mh_gemm_nt": (_i32, [_vp, _vp, _u64, _vp, _u32, _u64, _u32, _u32, _u32, _vp, _vp, _vp, _u64, _u32]),
     "mh_unet_create": (_i32, [_vp, _vp, _u32, ctypes.POINTER(_vp)]),
     "mh_unet_destroy": (None, [_vp]),

@@ -579,35 +579,78 @@ int32_t mh_layer_norm(MhContext *ctx, const float *x, uint64_t rows, uint32_t c,
     });
 }
 
+static void conv1x1_layer_norm_entry(MhContext *ctx, const float *x, uint64_t rows, uint32_t c_in, const float *gamma,
+                                     const float *beta, float eps, const void *weight, uint32_t weight_dtype,
+                                     uint32_t c_out, const float *bias, uint32_t silu, float *out,
+                                     const mh::LnRowPartials *stats) {
+    mh::Context &cc = C(ctx);
+    need(x, "x");
+    need(gamma, "gamma");
+    need(beta, "beta");
+    need(weight, "weight");
+    need(out, "out");
+    const int ci = dim(c_in, "c_in"), co = dim(c_out, "c_out");
+    MH_REQUIRE(ci % 4 == 0 && co % 4 == 0, "Conv1x1 (LayerNorm): c_in and c_out must be multiples of 4");
+    MH_REQUIRE(rows < (uint64_t(1) << 31), "Conv1x1 (LayerNorm): too many rows");
+    auto al = [](size_t b) { return (b + 255) & ~size_t(255); };
+    const size_t nk = size_t(co) * ci;
+    const size_t o16 = al(nk * 4), oc1 = o16 + al(nk * 2), oc16 = oc1 + al(size_t(co) * 4),
+                 oc2 = oc16 + al(size_t(co) * 4), total = oc2 + al(size_t(co) * 4);
+    char *ws = static_cast<char *>(cc.ws.get(total, cc.stream));
+    float *w32 = reinterpret_cast<float *>(ws);
+    float *c1_32 = reinterpret_cast<float *>(ws + oc1), *c1_16 = reinterpret_cast<float *>(ws + oc16);
+    float *c2 = reinterpret_cast<float *>(ws + oc2);
+    mh::ln_fold_weights(cc, weight, wtype(weight_dtype), co, ci, gamma, beta, bias, w32, ws + o16, c1_32, c1_16, c2);
+    mh::LnFolded f;
+    f.w32 = w32, f.c1_32 = c1_32, f.w16 = ws + o16, f.c1_16 = c1_16, f.c2 = c2, f.eps = eps;
+    const int width = co;
+    float *const outs[1] = {out};
+    mh::conv1x1_ln(cc, x, int64_t(rows), ci, f, 1, &width, outs, silu ? mh::GemmEpilogue::Silu : mh::GemmEpilogue::None,
+                   stats);
+}
+
 int32_t mh_conv1x1_layer_norm(MhContext *ctx, const float *x, uint64_t rows, uint32_t c_in, const float *gamma,
                               const float *beta, float eps, const void *weight, uint32_t weight_dtype, uint32_t c_out,
                               const float *bias, uint32_t silu, float *out) {
     return guard([&] {
+        conv1x1_layer_norm_entry(ctx, x, rows, c_in, gamma, beta, eps, weight, weight_dtype, c_out, bias, silu, out,
+                                 nullptr);
+    });
+}
+
+int32_t mh_conv1x1_layer_norm_stats(MhContext *ctx, const float *x, uint64_t rows, uint32_t c_in, const float *gamma,
+                                    const float *beta, float eps, const void *weight, uint32_t weight_dtype,
+                                    uint32_t c_out, const float *bias, uint32_t silu, const float *row_partials,
+                                    uint32_t per_row, float *out) {
+    return guard([&] {
+        need(row_partials, "row_partials");
+        MH_REQUIRE(per_row > 0 && per_row <= 4096, "Conv1x1 (LayerNorm): 1 to 4096 row partials per row");
+        MH_REQUIRE((reinterpret_cast<uintptr_t>(row_partials) & 7) == 0, "row partials must be 8-byte aligned");
+        mh::LnRowPartials st;
+        st.part = reinterpret_cast<float2 *>(const_cast<float *>(row_partials));
+        st.per_row = int(per_row);
+        conv1x1_layer_norm_entry(ctx, x, rows, c_in, gamma, beta, eps, weight, weight_dtype, c_out, bias, silu, out,
+                                 &st);
+    });
+}
+
+int32_t mh_conv1x1_row_partials(MhContext *ctx, const float *x, uint64_t rows, uint32_t c_in, const void *weight,
+                                uint32_t weight_dtype, uint32_t c_out, const float *bias, float *out,
+                                float *row_partials, uint32_t *per_row) {
+    return guard([&] {
         mh::Context &cc = C(ctx);
         need(x, "x");
-        need(gamma, "gamma");
-        need(beta, "beta");
         need(weight, "weight");
         need(out, "out");
-        const int ci = dim(c_in, "c_in"), co = dim(c_out, "c_out");
-        MH_REQUIRE(ci % 4 == 0 && co % 4 == 0, "Conv1x1 (LayerNorm): c_in and c_out must be multiples of 4");
-        MH_REQUIRE(rows < (uint64_t(1) << 31), "Conv1x1 (LayerNorm): too many rows");
-        auto al = [](size_t b) { return (b + 255) & ~size_t(255); };
-        const size_t nk = size_t(co) * ci;
-        const size_t o16 = al(nk * 4), oc1 = o16 + al(nk * 2), oc16 = oc1 + al(size_t(co) * 4),
-                     oc2 = oc16 + al(size_t(co) * 4), total = oc2 + al(size_t(co) * 4);
-        char *ws = static_cast<char *>(cc.ws.get(total, cc.stream));
-        float *w32 = reinterpret_cast<float *>(ws);
-        float *c1_32 = reinterpret_cast<float *>(ws + oc1), *c1_16 = reinterpret_cast<float *>(ws + oc16);
-        float *c2 = reinterpret_cast<float *>(ws + oc2);
-        mh::ln_fold_weights(cc, weight, wtype(weight_dtype), co, ci, gamma, beta, bias, w32, ws + o16, c1_32, c1_16,
-                            c2);
-        mh::LnFolded f;
-        f.w32 = w32, f.c1_32 = c1_32, f.w16 = ws + o16, f.c1_16 = c1_16, f.c2 = c2, f.eps = eps;
-        const int width = co;
-        float *const outs[1] = {out};
-        mh::conv1x1_ln(cc, x, int64_t(rows), ci, f, 1, &width, outs,
-                       silu ? mh::GemmEpilogue::Silu : mh::GemmEpilogue::None);
+        need(row_partials, "row_partials");
+        need(per_row, "per_row");
+        MH_REQUIRE((reinterpret_cast<uintptr_t>(row_partials) & 7) == 0, "row partials must be 8-byte aligned");
+        MH_REQUIRE(rows < (uint64_t(1) << 31), "Conv1x1: too many rows");
+        mh::LnRowPartials st;
+        st.part = reinterpret_cast<float2 *>(row_partials);
+        mh::conv1x1(cc, x, int64_t(rows), dim(c_in, "c_in"), weight, wtype(weight_dtype), dim(c_out, "c_out"), bias,
+                    nullptr, out, mh::GemmEpilogue::None, nullptr, nullptr, nullptr, nullptr, nullptr, 0, &st);
+        *per_row = uint32_t(st.per_row);
     });
 }
 
@@ -740,6 +783,22 @@ int32_t mh_cross_lambda(MhContext *ctx, const float *q, const float *e, const fl
         need(out, "out");
         mh::cross_lambda(c, q, e, lambda_c, v_branches, dim(br0, "br0"), dim(nb, "nb"), dim(hw, "hw"), dim(k, "k"),
                          residual, out);
+    });
+}
+
+int32_t mh_cross_lambda_row_sums(MhContext *ctx, const float *q, const float *e, const float *lambda_c,
+                                 const float *v_branches, uint32_t br0, uint32_t nb, uint32_t hw, uint32_t k,
+                                 const float *residual, float *out, float *row_sums) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(q, "q");
+        need(e, "e");
+        need(lambda_c, "lambda_c");
+        need(v_branches, "v_branches");
+        need(out, "out");
+        need(row_sums, "row_sums");
+        mh::cross_lambda(c, q, e, lambda_c, v_branches, dim(br0, "br0"), dim(nb, "nb"), dim(hw, "hw"), dim(k, "k"),
+                         residual, out, reinterpret_cast<float2 *>(row_sums));
     });
 }
 

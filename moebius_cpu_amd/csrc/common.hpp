@@ -70,7 +70,9 @@ struct Tuning {
     int lambda_taps = 1;   // 0: the self-lambda's position coefficients through the general GEMM
     int gemm_log = 0;      // 1: print each GEMM launch's shape and tiling to stderr (launch census)
     int gemm_wide = 1;     // 0: the square tilings only (no wide wave layouts from the planner)
-    int ln_fold = 0;       // 1: the transformers' LayerNorms 1 and 3 folded into the GEMMs that read them
+    int ln_fold = 2;       // the transformers' LayerNorms 1 and 3 folded into the GEMMs that read them, with
+                           // the row statistics from the producers' partials (2) or summed by the GEMMs
+                           // (1); 0: LayerNorm passes of their own
     int tap_split = 0;     // per-thread tap filter: tap rows split over 1, 3 or 5 threads (0: by map size)
     int gemm_time = 0;     // 1: record events around each GEMM launch (Context::gemm_times)
 };

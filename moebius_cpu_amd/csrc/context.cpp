@@ -95,7 +95,7 @@ bool set_tuning(Tuning &t, const char *key, const char *value) {
     if (k == "gemm_log") return to_int(t.gemm_log, 0);
     if (k == "gemm_time") return to_int(t.gemm_time, 0) && t.gemm_time >= 0 && t.gemm_time <= 1;
     if (k == "gemm_wide") return to_int(t.gemm_wide, 1) && t.gemm_wide >= 0 && t.gemm_wide <= 1;
-    if (k == "ln_fold") return to_int(t.ln_fold, 0) && t.ln_fold >= 0 && t.ln_fold <= 1;
+    if (k == "ln_fold") return to_int(t.ln_fold, 2) && t.ln_fold >= 0 && t.ln_fold <= 2;
     if (k == "tap_split") return to_int(t.tap_split, 0) && (t.tap_split == 0 || t.tap_split == 1 || t.tap_split == 3 ||
                                                             t.tap_split == 5);
     if (k == "tap_heads") {

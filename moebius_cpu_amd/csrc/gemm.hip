@@ -79,7 +79,8 @@ __global__ void mfma_probe_kernel(const float *a, const float *b, float *d) {
 
 void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void *weight, WeightType wt, int c_out,
              const float *bias, const float *residual, float *out, GemmEpilogue epi, const ResidualAffine *raff,
-             const float *residual2, GnPartials *gn, const ResidualAffine *x_aff, const float *x2, int c2) {
+             const float *residual2, GnPartials *gn, const ResidualAffine *x_aff, const float *x2, int c2,
+             LnRowPartials *lnp) {
     MH_REQUIRE(c_in > 0 && c_out > 0, "Conv1x1: empty channel axis");
     MH_REQUIRE(pixels < (int64_t(1) << 31), "Conv1x1: too many pixels");
     if (x2) {
@@ -124,6 +125,10 @@ void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void 
         p.gnp = gn->part;
         p.gn_item_rows = gn->item_rows;
     }
+    if (lnp) {
+        MH_REQUIRE(lnp->part, "Conv1x1: LayerNorm row partials need their buffer");
+        p.lnp_out = lnp->part;
+    }
     if (x_aff) {
         MH_REQUIRE(x_aff->scale && x_aff->shift && x_aff->rows_per_item > 0,
                    "Conv1x1: input affine needs scale, shift and rows per item");
@@ -142,6 +147,7 @@ void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void 
         run_dense(ctx, p, wt, epi, 1, false);
     }
     if (gn) gn->rows = p.gn_rows;
+    if (lnp) lnp->per_row = p.lnp_out ? p.lnp_ld : 0;
 }
 
 void conv1x1_segments(Context &ctx, const float *x, int64_t pixels, int c_in, const void *weight, WeightType wt,
@@ -174,7 +180,7 @@ void conv1x1_segments(Context &ctx, const float *x, int64_t pixels, int c_in, co
 }
 
 void conv1x1_ln(Context &ctx, const float *x, int64_t pixels, int c_in, const LnFolded &f, int nseg, const int *widths,
-                float *const *outs, GemmEpilogue epi) {
+                float *const *outs, GemmEpilogue epi, const LnRowPartials *stats) {
     MH_REQUIRE(nseg >= 1 && nseg <= kMaxSeg, "Conv1x1 (LayerNorm): 1 to 3 outputs");
     MH_REQUIRE(pixels < (int64_t(1) << 31), "Conv1x1: too many pixels");
     MH_REQUIRE(c_in % 4 == 0 && aligned16(x) && f.w32 && f.c1_32 && f.w16 && f.c1_16 && f.c2 && aligned16(f.c2) &&
@@ -206,6 +212,11 @@ void conv1x1_ln(Context &ctx, const float *x, int64_t pixels, int c_in, const Ln
     p.bias = f.c2;
     p.ldc = n;
     p.ln_eps = f.eps;
+    if (stats && stats->per_row > 0) {
+        MH_REQUIRE(stats->part, "Conv1x1 (LayerNorm): row partials without their buffer");
+        p.lnp_in = stats->part;
+        p.lnp_n = stats->per_row;
+    }
     if (ctx.precision == Precision::Fast) {
         p.b = f.w16;
         p.ln_c1 = f.c1_16;

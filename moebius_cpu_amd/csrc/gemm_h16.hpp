@@ -259,11 +259,12 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
             compute(0);
         }
     }
-    __shared__ float ln_st[PRO == kProLn ? 2 * BM : 1];
+    __shared__ float ln_st[PRO >= kProLn ? 2 * BM : 1];
     if constexpr (PRO == kProLn) ln_row_stats<A_LD, 16, KCH, BM>(p, ln_s1, ln_s2, lrow, lc, ln_st);
+    if constexpr (PRO == kProLnPart) ln_stats_from_parts<BM, 256>(p, m0, ln_st);
     __syncthreads();
     write_tile<BM, BN, 2, 2, 1, MF, EPI, SPLIT>(p, reinterpret_cast<float *>(smem), acc, m0, n0, ti.z,
-                                                PRO == kProLn ? ln_st : nullptr);
+                                                PRO >= kProLn ? ln_st : nullptr);
 }
 
 // Tile shape and K split of the fast kernel, from sweeps of every (tile,
@@ -307,6 +308,7 @@ void launch_cfg_h16(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi,
         p.k_split = pl.k_split;
         p.vec_out = (p.N & 3) == 0 && (reinterpret_cast<uintptr_t>(p.partial) & 15) == 0;
         gn_partials_plan(p, BM, BN, pl.splits, batch);
+        ln_partials_plan(p, BN, pl.splits, batch);
         dim3 grid(tiles, 1, pl.splits);
         gemm_h16_kernel<BM, BN, MODE, PRO, F16, BVEC, 0, true><<<grid, 256, 0, ctx.stream>>>(p);
         MH_LAUNCH_CHECK();
@@ -328,6 +330,7 @@ void launch_cfg_h16(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi,
         p.k_split = p.K;
         p.vec_out = out_vec_ok(p, BM);
         gn_partials_plan(p, BM, BN, 1, batch);
+        ln_partials_plan(p, BN, 1, batch);
         const dim3 grid(tiles, unsigned(batch));
         if constexpr (MODE <= kDenseScalar) {
             if (epi == GemmEpilogue::Silu) {
@@ -355,7 +358,7 @@ void launch_tiles_h16(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
             pl = Plan{bm, bn, int(ceil_div(ktiles, per)), per * BKH};
         }
     }
-    if (batch > 1 || PRO == kProLn) pl.splits = 1;  // the folded LayerNorm needs whole rows of K
+    if (batch > 1 || PRO >= kProLn) pl.splits = 1;  // the folded LayerNorm needs whole rows of K
     if (pl.splits == 1) pl.k_split = p.K;
     if constexpr (MODE <= kDenseScalar) {
         if (pl.bm == 32) {

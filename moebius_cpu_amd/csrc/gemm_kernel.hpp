@@ -52,8 +52,10 @@ struct Mf {
 // affine [SiLU](x . scale + shift) per (item, channel) as values load; or the
 // LayerNorm of each row folded into the product (kProLn, dense operands: the
 // workgroup sums its rows' values in f64 as they load, and the epilogue forms
-// rstd . (acc - mean . ln_c1) with B = W . diag(gamma), bias = W . beta + b).
-constexpr int kProNone = 0, kProAffine = 1, kProLn = 2;
+// rstd . (acc - mean . ln_c1) with B = W . diag(gamma), bias = W . beta + b);
+// or the same fold with each row's statistics from partial sums its producer
+// wrote (kProLnPart: GemmArgs::lnp_in), the A values loading as they are.
+constexpr int kProNone = 0, kProAffine = 1, kProLn = 2, kProLnPart = 3;
 
 enum AMode : int {
     kDense = 0,      // A[m][k] row-major with leading dimension lda, K % 4 == 0
@@ -122,6 +124,16 @@ struct GemmArgs {
     // mean's coefficient), and the LayerNorm epsilon; the row width is K
     const float *ln_c1;
     float ln_eps;
+    // Row statistics of the output for a LayerNorm that reads it next
+    // (optional): lnp_out [M][lnp_ld] = per row and column tile, (sum y, sum
+    // y*y) over the tile's stored values. The launcher sets lnp_ld (tiles
+    // across N), or clears lnp_out where the tiling cannot honour it.
+    float2 *lnp_out;
+    int lnp_ld;
+    // kProLnPart: the same partials of the A rows, lnp_n per row (summed in
+    // order in f64 for each row's mean and variance over K columns).
+    const float2 *lnp_in;
+    int lnp_n;
 };
 
 // (residual [transformed] + bias) + acc [SiLU] (+ res2): the reference's
@@ -595,6 +607,55 @@ __device__ __forceinline__ void gn_tile_partials_lds(const GemmArgs &p, float *s
     }
 }
 
+// LayerNorm row partials of one output tile (GemmArgs::lnp_out) from the
+// stored values in the C tile (row stride CS): 8 adjacent lanes per row, lane
+// s summing column quads s, s + 8, ... in order, then an xor butterfly over
+// the 8 lanes; rows past M and columns past N were not stored and are skipped.
+template <int BM, int BN, int NT, int CS>
+__device__ __forceinline__ void ln_tile_partials(const GemmArgs &p, const float *smem, int m0, int n0) {
+    constexpr int C4 = BN / 4, RPASS = NT / 8;
+    static_assert(NT % 64 == 0, "whole waves");
+    const int tid = threadIdx.x, s = tid & 7;
+    const int q_end = min(C4, (p.N - n0 + 3) / 4);
+    for (int r = tid >> 3; r < BM; r += RPASS) {  // every lane of a row group runs the same passes
+        float sum = 0.f, sq = 0.f;
+        for (int q = s; q < q_end; q += 8) {
+            const float4 y = *reinterpret_cast<const float4 *>(smem + r * CS + q * 4);
+            sum += y.x, sum += y.y, sum += y.z, sum += y.w;
+            sq = __builtin_fmaf(y.x, y.x, sq);
+            sq = __builtin_fmaf(y.y, y.y, sq);
+            sq = __builtin_fmaf(y.z, y.z, sq);
+            sq = __builtin_fmaf(y.w, y.w, sq);
+        }
+#pragma unroll
+        for (int off = 1; off < 8; off <<= 1) {
+            sum += __shfl_xor(sum, off, 64);
+            sq += __shfl_xor(sq, off, 64);
+        }
+        if (s == 0 && m0 + r < p.M) p.lnp_out[int64_t(m0 + r) * p.lnp_ld + n0 / BN] = float2{sum, sq};
+    }
+}
+
+// kProLnPart: each tile row's mean and 1 / sqrt(var + eps) from its producer's
+// partials, summed in order in f64 (biased variance, as LayerNorm's).
+template <int BM, int NT>
+__device__ __forceinline__ void ln_stats_from_parts(const GemmArgs &p, int m0, float *st) {
+    for (int r = threadIdx.x; r < BM; r += NT) {
+        const int row = min(m0 + r, p.M - 1);
+        const float2 *src = p.lnp_in + int64_t(row) * p.lnp_n;
+        double a = 0.0, b = 0.0;
+        for (int j = 0; j < p.lnp_n; ++j) {
+            const float2 v = src[j];
+            a += double(v.x);
+            b += double(v.y);
+        }
+        const double mean = a / double(p.K);
+        const double var = fmax(b / double(p.K) - mean * mean, 0.0);
+        st[2 * r] = float(mean);
+        st[2 * r + 1] = float(1.0 / sqrt(var + double(p.ln_eps)));
+    }
+}
+
 // Wave layout of a workgroup: WM x WN waves over the output tile, each owning
 // a (BM / WM) x (BN / WN) block of it, times WK wave groups that split every
 // LDS stage's K between them (their sums are added in group order in the
@@ -693,13 +754,18 @@ __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const
                         gq.z = __builtin_fmaf(y.z, y.z, gq.z);
                         gq.w = __builtin_fmaf(y.w, y.w, gq.w);
                     }
+                    if (p.lnp_out) *reinterpret_cast<float4 *>(smem + rr * CS + cc) = y;  // for the row sums
                 }
+            }
+            if (!SPLIT && p.lnp_out) {  // before the GroupNorm sums reuse the C tile's memory
+                __syncthreads();
+                ln_tile_partials<BM, BN, NT, CS>(p, smem, m0, n0);
             }
             if constexpr (kGn) {
                 if (p.gnp) gn_tile_partials<BM, BN>(p, smem, gs, gq, m0, n0);
             }
         } else {
-            const bool gn = !SPLIT && p.gnp;
+            const bool gn = !SPLIT && p.gnp, lnr = !SPLIT && p.lnp_out;
             for (int e = tid; e < BM * C4; e += NT) {
                 const int rr = e / C4, cc = (e - rr * C4) * 4;
                 const int row = m0 + rr, col = n0 + cc;
@@ -711,13 +777,12 @@ __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const
                     *reinterpret_cast<float4 *>(p.partial + (int64_t(z) * p.M + row) * p.N + col) = v;
                 } else {
                     const float4 y = store4<EPI>(p, row, col, v);
-                    if (gn) *reinterpret_cast<float4 *>(c) = y;  // the stored values, for the sums
+                    if (gn || lnr) *reinterpret_cast<float4 *>(c) = y;  // the stored values, for the sums
                 }
             }
-            if (gn) {
-                __syncthreads();
-                gn_tile_partials_lds<BM, BN, NT, CS>(p, smem, m0, n0);
-            }
+            if (gn || lnr) __syncthreads();
+            if (lnr) ln_tile_partials<BM, BN, NT, CS>(p, smem, m0, n0);  // reads the C tile only
+            if (gn) gn_tile_partials_lds<BM, BN, NT, CS>(p, smem, m0, n0);
         }
     } else if (p.vec_out == 2) {
         // Grouped rows (out index (row / rg) * ldc + col * rg + row % rg, rg % 4 == 0,
@@ -1017,11 +1082,12 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(GemmArgs p)
 
     // kProLn: each row's mean and 1 / sqrt(var + eps) from the sums of its K4T
     // load lanes (adjacent lanes of one wave), in f64, for the epilogue.
-    __shared__ float ln_st[PRO == kProLn ? 2 * BM : 1];
+    __shared__ float ln_st[PRO >= kProLn ? 2 * BM : 1];
     if constexpr (PRO == kProLn)
         ln_row_stats<A_LD, RPP, K4T, BM>(p, ln_s1, ln_s2, lrow, lc4, ln_st);
+    if constexpr (PRO == kProLnPart) ln_stats_from_parts<BM, NT>(p, m0, ln_st);
     __syncthreads();
-    write_tile<BM, BN, WM, WN, WK, MF, EPI, SPLIT>(p, smem, acc, m0, n0, ti.z, PRO == kProLn ? ln_st : nullptr);
+    write_tile<BM, BN, WM, WN, WK, MF, EPI, SPLIT>(p, smem, acc, m0, n0, ti.z, PRO >= kProLn ? ln_st : nullptr);
 }
 
 // Sums split-K partials in split order, then (residual + bias) + sum [SiLU].
@@ -1083,6 +1149,17 @@ inline void gn_partials_plan(GemmArgs &p, int bm, int bn, int splits, int batch,
                     (reinterpret_cast<uintptr_t>(p.gnp) & 15) == 0;
     if (ok) p.gn_rows = bm;
     else p.gnp = nullptr;
+}
+
+// Keeps the LayerNorm row partials request (GemmArgs::lnp_out) when the tiling
+// stores plain rows of 16-byte column quads in one pass (no K split, no
+// batch, no segments or grouped rows), and sets the partials per row.
+inline void ln_partials_plan(GemmArgs &p, int bn, int splits, int batch) {
+    if (!p.lnp_out) return;
+    const bool ok = splits == 1 && batch == 1 && p.vec_out == 1 && p.nseg == 0 && p.rg <= 1 &&
+                    (reinterpret_cast<uintptr_t>(p.lnp_out) & 7) == 0;
+    if (ok) p.lnp_ld = int(ceil_div(p.N, bn));
+    else p.lnp_out = nullptr;
 }
 
 // Tile shape and K split, from sweeps of every (tile, split) on MI355X over
@@ -1216,6 +1293,7 @@ void launch_cfg(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int
         p.k_split = pl.k_split;
         p.vec_out = (p.N & 3) == 0 && (reinterpret_cast<uintptr_t>(p.partial) & 15) == 0;
         gn_partials_plan(p, BM, BN, pl.splits, batch, kSquare);
+        ln_partials_plan(p, BN, pl.splits, batch);
         dim3 grid(tiles, 1, pl.splits);
         gemm_f32_kernel<BM, BN, WM, WN, WK, MODE, PRO, F16, BVEC, 0, true, PIPE, BKT><<<grid, NT, 0, ctx.stream>>>(p);
         MH_LAUNCH_CHECK();
@@ -1237,6 +1315,7 @@ void launch_cfg(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, int
         p.k_split = p.K;
         p.vec_out = out_vec_ok(p, BM);
         gn_partials_plan(p, BM, BN, 1, batch, kSquare);
+        ln_partials_plan(p, BN, 1, batch);
         const dim3 grid(tiles, unsigned(batch));
         // The SiLU epilogue is only instantiated for dense operands (the convs never use it).
         if constexpr (MODE <= kDenseScalar) {
@@ -1325,7 +1404,7 @@ void launch_tiles(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
             pl = f;
         }
     }
-    if (batch > 1 || PRO == kProLn) pl.splits = 1;  // the folded LayerNorm needs whole rows of K
+    if (batch > 1 || PRO >= kProLn) pl.splits = 1;  // the folded LayerNorm needs whole rows of K
     if (pl.splits == 1) pl.k_split = p.K;
     if constexpr (kWideOk) {
         const int wi = wide_index(pl);

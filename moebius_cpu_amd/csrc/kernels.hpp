@@ -109,10 +109,20 @@ struct ResidualAffine {
 // x2 (optional): the input is [x | x2] per pixel, x holding the first
 // c_in - c2 channels (a multiple of 64) and x2 the last c2, read from the two
 // buffers in place of their concatenation (not with x_aff).
+// LayerNorm row statistics a producer writes for the LayerNorm that reads its
+// output next: part [pixels][per_row] = per row, (sum y, sum y*y) over
+// per_row disjoint column ranges of the values written. The caller sets part
+// (room for pixels * ceil(c / 32) pairs); the producer sets per_row (0: none
+// written).
+struct LnRowPartials {
+    float2 *part = nullptr;
+    int per_row = 0;
+};
 void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void *weight, WeightType wt, int c_out,
              const float *bias, const float *residual, float *out, GemmEpilogue epi = GemmEpilogue::None,
              const ResidualAffine *raff = nullptr, const float *residual2 = nullptr, GnPartials *gn = nullptr,
-             const ResidualAffine *x_aff = nullptr, const float *x2 = nullptr, int c2 = 0);
+             const ResidualAffine *x_aff = nullptr, const float *x2 = nullptr, int c2 = 0,
+             LnRowPartials *lnp = nullptr);
 // residual2 (optional, [n, ho, wo, c_out]) is added last: out = (bias + conv) + residual2.
 void conv3x3(Context &ctx, const float *x, int n, int h, int w, int c_in, const void *weight, WeightType wt,
              int c_out, const float *bias, int stride, const int pad[4], bool upsample2x, const Affine *prologue,
@@ -136,8 +146,10 @@ struct LnFolded {
     const float *c2 = nullptr;
     float eps = 1e-5f;
 };
+// stats (optional, per_row > 0): each row's statistics from its producer's
+// partials instead of from the values this GEMM loads.
 void conv1x1_ln(Context &ctx, const float *x, int64_t pixels, int c_in, const LnFolded &f, int nseg, const int *widths,
-                float *const *outs, GemmEpilogue epi = GemmEpilogue::None);
+                float *const *outs, GemmEpilogue epi = GemmEpilogue::None, const LnRowPartials *stats = nullptr);
 // Builds LnFolded's tensors on the device from W [n][k] (f32 or f16), gamma,
 // beta [k] and bias [n] (or NULL): w32 [n][k] = W . gamma (f32), w16 its
 // round-to-nearest f16 copy, c1_32 / c1_16 their row sums and c2 = W . beta +
@@ -216,9 +228,11 @@ void lambda_taps(Context &ctx, const float *q, const float *w_aug_t, const float
 void position_term(Context &ctx, const float *q, const float *e, const float *v_branches, int br0, int nb, int hw,
                    int k, const float *yc, const float *residual, float *out);
 // out [nb*hw][8*k] = (residual +) (q . lambda_c[branch] + (q . E) . V[branch]) in one pass;
-// lambda_c [2][k][k] row-major. out may alias residual, not q.
+// lambda_c [2][k][k] row-major. out may alias residual, not q. row_sums
+// (optional, [nb*hw]): per output row, (sum, sum of squares) of the values
+// written, for the LayerNorm that reads out next (one partial per row).
 void cross_lambda(Context &ctx, const float *q, const float *e, const float *lambda_c, const float *v_branches, int br0,
-                  int nb, int hw, int k, const float *residual, float *out);
+                  int nb, int hw, int k, const float *residual, float *out, float2 *row_sums = nullptr);
 
 // ---- VAE (vae_kernels.hip), src/vae
 // In place over rows [nrows][n] (n <= 15360): softmax(scale * row) with

@@ -721,7 +721,8 @@ template <int HG>
 __global__ __launch_bounds__(256) void cross_lambda_kernel(const float *__restrict__ q, const float *__restrict__ e,
                                                            const float *__restrict__ lam,
                                                            const float *__restrict__ vbr, int br0, int nb, int hw,
-                                                           int k, int P, const float *res, float *out) {
+                                                           int k, int P, const float *res, float *out,
+                                                           float2 *__restrict__ row_sums) {
     extern __shared__ float sm[];
     const int c = kHeads * k;
     float *qs = sm;                  // [P][k][8]
@@ -781,12 +782,14 @@ __global__ __launch_bounds__(256) void cross_lambda_kernel(const float *__restri
     __syncthreads();
     const int k4 = k >> 2, per_px = NG * k4;
     const int p = threadIdx.x / per_px;
-    if (p >= np) return;  // no barrier follows
+    // Threads past the block's pixels return here unless the row sums' barriers follow.
+    if (p >= np && !row_sums) return;
+    const int pc = min(p, np - 1);  // (a past-the-end thread computes a real pixel's values, unused)
     const int r = threadIdx.x - p * per_px, hg = r / k4, jq = r - hg * k4;
-    const int64_t pix = pix0 + p;
+    const int64_t pix = pix0 + pc;
     const int br = br0 + int(pix / hw);
     const float4 *l4 = reinterpret_cast<const float4 *>(lam + int64_t(br) * k * k) + jq;
-    const float *qp = qs + size_t(p) * k * kHeads + hg * HG;
+    const float *qp = qs + size_t(pc) * k * kHeads + hg * HG;
     float4 acc[HG];
 #pragma unroll
     for (int i = 0; i < HG; ++i) acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -813,7 +816,7 @@ __global__ __launch_bounds__(256) void cross_lambda_kernel(const float *__restri
         }
     }
     const float4 *v4 = reinterpret_cast<const float4 *>(vbr + int64_t(br) * kTokens * k) + jq;
-    const float *bp = bm + (size_t(p) * kHeads + hg * HG) * kTokens;
+    const float *bp = bm + (size_t(pc) * kHeads + hg * HG) * kTokens;
 #pragma unroll
     for (int m = 0; m < kTokens; ++m) {
         const float4 x = v4[m * k4];
@@ -836,7 +839,44 @@ __global__ __launch_bounds__(256) void cross_lambda_kernel(const float *__restri
             const float4 rr = res4[o];
             u = make_float4(rr.x + u.x, rr.y + u.y, rr.z + u.z, rr.w + u.w);
         }
-        out4[o] = u;
+        if (p < np) out4[o] = u;
+        acc[i] = u;
+    }
+    if (!row_sums) return;
+    // LayerNorm row partials of the written rows: this thread's (sum, sum of
+    // squares) over its values in order, then per pixel the threads' in order,
+    // in chunks of 8 and the chunks in order (through LDS past q and B).
+    float2 *red = reinterpret_cast<float2 *>(sm + size_t(P) * (kHeads * k + kHeads * kTokens));
+    float ls = 0.f, lq = 0.f;
+#pragma unroll
+    for (int i = 0; i < HG; ++i) {
+        ls += acc[i].x, ls += acc[i].y, ls += acc[i].z, ls += acc[i].w;
+        lq = __builtin_fmaf(acc[i].x, acc[i].x, lq);
+        lq = __builtin_fmaf(acc[i].y, acc[i].y, lq);
+        lq = __builtin_fmaf(acc[i].z, acc[i].z, lq);
+        lq = __builtin_fmaf(acc[i].w, acc[i].w, lq);
+    }
+    red[threadIdx.x] = float2{ls, lq};
+    __syncthreads();
+    const int nch = (per_px + 7) / 8;
+    float2 cs{0.f, 0.f};
+    if (p < np && r < nch) {
+        const int j1 = min(per_px, 8 * r + 8);
+        for (int j = 8 * r; j < j1; ++j) {
+            const float2 v = red[p * per_px + j];
+            cs.x += v.x, cs.y += v.y;
+        }
+    }
+    __syncthreads();
+    if (p < np && r < nch) red[p * per_px + r] = cs;
+    __syncthreads();
+    if (p < np && r == 0) {
+        float2 t = red[p * per_px];
+        for (int j = 1; j < nch; ++j) {
+            const float2 v = red[p * per_px + j];
+            t.x += v.x, t.y += v.y;
+        }
+        row_sums[pix] = t;
     }
 }
 
@@ -1007,8 +1047,9 @@ void position_term(Context &ctx, const float *q, const float *e, const float *v_
 }
 
 void cross_lambda(Context &ctx, const float *q, const float *e, const float *lambda_c, const float *v_branches, int br0,
-                  int nb, int hw, int k, const float *residual, float *out) {
+                  int nb, int hw, int k, const float *residual, float *out, float2 *row_sums) {
     MH_REQUIRE(k % 8 == 0 && k <= 256, "cross_lambda: head width must be a multiple of 8, at most 256");
+    MH_REQUIRE((reinterpret_cast<uintptr_t>(row_sums) & 7) == 0, "cross_lambda: row sums must be 8-byte aligned");
     MH_REQUIRE(aligned16(q) && aligned16(e) && aligned16(lambda_c) && aligned16(v_branches) && aligned16(residual) &&
                    aligned16(out),
                "cross_lambda: buffers must be 16-byte aligned");
@@ -1035,20 +1076,21 @@ void cross_lambda(Context &ctx, const float *q, const float *e, const float *lam
     }
     const int P = std::max(1, 256 / ((kHeads / hg) * k4));
     const unsigned threads = unsigned(P * (kHeads / hg) * k4);
-    const size_t lds = (size_t(P) * kHeads * k + size_t(P) * kHeads * kTokens) * sizeof(float);
+    const size_t lds = (size_t(P) * kHeads * k + size_t(P) * kHeads * kTokens) * sizeof(float) +
+                       (row_sums ? size_t(threads) * sizeof(float2) : 0);
     const unsigned blocks = unsigned(ceil_div(npix, P));
     switch (hg) {
         case 8:
             cross_lambda_kernel<8><<<blocks, threads, lds, ctx.stream>>>(q, e, lambda_c, v_branches, br0, nb, hw, k,
-                                                                          P, residual, out);
+                                                                          P, residual, out, row_sums);
             break;
         case 4:
             cross_lambda_kernel<4><<<blocks, threads, lds, ctx.stream>>>(q, e, lambda_c, v_branches, br0, nb, hw, k,
-                                                                          P, residual, out);
+                                                                          P, residual, out, row_sums);
             break;
         default:
             cross_lambda_kernel<2><<<blocks, threads, lds, ctx.stream>>>(q, e, lambda_c, v_branches, br0, nb, hw, k,
-                                                                          P, residual, out);
+                                                                          P, residual, out, row_sums);
     }
     MH_LAUNCH_CHECK();
 }

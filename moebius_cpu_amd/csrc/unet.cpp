@@ -221,6 +221,15 @@ struct Lin {  // Conv1x1 (src/engine/conv.rs:28-55)
         fwd(e, x.p, x.px(), out.p, res ? res->p : nullptr, epi);
         return out;
     }
+    // The same, writing LayerNorm row partials of the output (lnp) for the
+    // LayerNorm that reads it next.
+    DT fwd_lnp(Env &e, const DT &x, LnRowPartials *lnp) const {
+        DT out = e.pool.tensor(x.n, x.h, x.w, co);
+        const DParam wd = w.at(e.ctx);
+        conv1x1(e.ctx, x.p, x.px(), ci, wd.p, wd.wt, co, b, nullptr, out.p, GemmEpilogue::None, nullptr, nullptr,
+                nullptr, nullptr, nullptr, 0, lnp);
+        return out;
+    }
     // The same of [xa | xb] per pixel, read from the two tensors.
     DT fwd2(Env &e, const DT &xa, const DT &xb) const {
         DT out = e.pool.tensor(xa.n, xa.h, xa.w, co);
@@ -232,7 +241,7 @@ struct Lin {  // Conv1x1 (src/engine/conv.rs:28-55)
     // The same of GroupNorm(x) given its affine (ss = [scale | shift] per item
     // and channel, no SiLU), applied as x loads: the normalised tensor is not
     // written, and every value is the one the apply pass would write.
-    DT fwd_gn_in(Env &e, const DT &x, const float *ss) const {
+    DT fwd_gn_in(Env &e, const DT &x, const float *ss, LnRowPartials *lnp = nullptr) const {
         DT out = e.pool.tensor(x.n, x.h, x.w, co);
         ResidualAffine xa;
         xa.scale = ss;
@@ -241,7 +250,7 @@ struct Lin {  // Conv1x1 (src/engine/conv.rs:28-55)
         xa.rows_per_item = x.h * x.w;
         const DParam wd = w.at(e.ctx);
         conv1x1(e.ctx, x.p, x.px(), ci, wd.p, wd.wt, co, b, nullptr, out.p, GemmEpilogue::None, nullptr, nullptr,
-                nullptr, &xa);
+                nullptr, &xa, nullptr, 0, lnp);
         return out;
     }
     // The same, with the GroupNorm partials of the output attached for the
@@ -532,7 +541,7 @@ struct SelfLambda {
     // h [x.px()][c] += SelfLambda(x): the block's residual add is folded into the tap filter.
     // ln: x is the block's hidden state and LayerNorm 1 is folded into the q | k | v GEMM.
     void fwd_add(Env &e, const DT &x, float *h, const LayerNormOut *lno = nullptr,
-                 const LnFolded *ln = nullptr) const {
+                 const LnFolded *ln = nullptr, const LnRowPartials *ln_stats = nullptr) const {
         const int hw = x.h * x.w;
         DT q = e.pool.tensor(x.n, x.h, x.w, c);
         DT kt = e.pool.tensor(x.n, x.h, x.w, k);
@@ -542,7 +551,7 @@ struct SelfLambda {
             float *const outs[3] = {q.p, kt.p, vt.p};
             const bool w32 = wqkv32 && e.ctx.precision == Precision::Exact;
             if (ln)
-                conv1x1_ln(e.ctx, x.p, x.px(), c, *ln, 3, widths, outs);
+                conv1x1_ln(e.ctx, x.p, x.px(), c, *ln, 3, widths, outs, GemmEpilogue::None, ln_stats);
             else
                 conv1x1_segments(e.ctx, x.p, x.px(), c, w32 ? wqkv32 : wqkv, w32 ? kF32 : wt, bqkv, 3, widths,
                                  outs);
@@ -617,11 +626,12 @@ struct CrossLambda {
     }
     // h [x.px()][c] += CrossLambda(x): Yc = Q . lambda_c, the position term and
     // the residual add in one kernel after the q projection.
-    void fwd_add(Env &env, const DT &x, int br0, float *h) const {
+    // row_sums (optional): LayerNorm row partials of the new h, one per pixel.
+    void fwd_add(Env &env, const DT &x, int br0, float *h, float2 *row_sums = nullptr) const {
         const int hw = x.h * x.w;
         if (hw != n) fail(kInvalidArgument, "CrossLambda input size does not match the position table");
         DT q = to_q.fwd(env, x);
-        cross_lambda(env.ctx, q.p, e, lambda_c, v, br0, x.n, hw, k, h, h);
+        cross_lambda(env.ctx, q.p, e, lambda_c, v, br0, x.n, hw, k, h, h, row_sums);
         env.pool.recycle(q);
     }
 };
@@ -676,25 +686,32 @@ struct MixTransformer {
         // (and 640 in FAST) they cost more than the separate apply pass (whole
         // steps: EXACT 7.764 ms unfused, 7.728 to 640, 7.773 to 1280; FAST 5.744,
         // 5.731 to 320, 5.778 to 640).
+        // LayerNorms 1 and 3 (ln_fold 2, the default): folded into the GEMMs that
+        // read them (q | k | v and the inverted 1x1, on W . diag(gamma)), with each
+        // row's statistics from partial sums the producers of h write beside it
+        // (proj_in's epilogue per column tile, the cross-lambda kernel per row):
+        // no LayerNorm launch, no normalised tensor, no second read of h.
+        const int fold = e.ctx.tune.ln_fold;
+        LnRowPartials st1, st3;
+        if (fold == 2) st1.part = reinterpret_cast<float2 *>(e.pool.floats(x.px() * 2 * ceil_div(c, 32)));
         DT h;
         const int max_c = e.ctx.tune.gn_in_maxc >= 0 ? e.ctx.tune.gn_in_maxc
                                                       : (e.ctx.precision == Precision::Fast ? 320 : 640);
         if (x.c <= max_c) {
             float *ss = norm.affine(e, x, nullptr);
-            h = proj_in.fwd_gn_in(e, x, ss);
+            h = proj_in.fwd_gn_in(e, x, ss, fold == 2 ? &st1 : nullptr);
             e.pool.recycle(ss);
         } else {
             DT t = norm.fwd(e, x, nullptr, false);
-            h = proj_in.fwd(e, t);
+            h = fold == 2 ? proj_in.fwd_lnp(e, t, &st1) : proj_in.fwd(e, t);
             e.pool.recycle(t);
         }
         // LayerNorm 2 is written beside h by the tap filter that finishes h: the
         // separate pass costs a launch and a re-read of h (whole step -29 us EXACT,
         // -36 us FAST). The same in the cross-lambda kernel for LayerNorm 3 measured
         // 160 us slower per step, so LayerNorm 3 stays a pass of its own.
-        // LayerNorms 1 and 3 are folded into the GEMMs that read them (q | k | v and
-        // the inverted 1x1), which read h itself: no LayerNorm launch or output.
-        const bool fold = e.ctx.tune.ln_fold != 0;
+        // ln_fold 1: the same folds with the row statistics summed by the GEMMs
+        // from the values they load; 0: LayerNorm passes of their own.
         const LnFolded lnq = ln1q.view(LN_EPS), lnf = ln3f.view(LN_EPS);
         DT t2 = e.pool.tensor(h.n, h.h, h.w, h.c);
         LayerNormOut lno2;
@@ -702,18 +719,25 @@ struct MixTransformer {
         lno2.beta = ln2.b;
         lno2.eps = LN_EPS;
         lno2.out = t2.p;
-        if (fold) {
+        if (fold == 2 && st1.per_row > 0) {
+            attn1.fwd_add(e, h, h.p, &lno2, &lnq, &st1);
+        } else if (fold == 1) {
             attn1.fwd_add(e, h, h.p, &lno2, &lnq);
         } else {
             DT t = ln1.fwd(e, h);
             attn1.fwd_add(e, t, h.p, &lno2);
             e.pool.recycle(t);
         }
+        if (st1.part) e.pool.recycle(reinterpret_cast<float *>(st1.part));
         if (xs.n != xr.n) {
             h = widen(e, h, xr.n);
             t2 = widen(e, t2, xr.n);
         }
-        attn2.fwd_add(e, t2, br0, h.p);
+        if (fold == 2) {
+            st3.part = reinterpret_cast<float2 *>(e.pool.floats(h.px() * 2));
+            st3.per_row = 1;
+        }
+        attn2.fwd_add(e, t2, br0, h.p, st3.part);
         e.pool.recycle(t2);
         // MixFFN (transformer.rs:121-129): SiLU(inverted(LN3 h)) -> GLU depthwise -> point + h
         DT a;
@@ -721,7 +745,8 @@ struct MixTransformer {
             a = e.pool.tensor(h.n, h.h, h.w, 2 * hidden);
             const int width = 2 * hidden;
             float *const outs[1] = {a.p};
-            conv1x1_ln(e.ctx, h.p, h.px(), c, lnf, 1, &width, outs, GemmEpilogue::Silu);
+            conv1x1_ln(e.ctx, h.p, h.px(), c, lnf, 1, &width, outs, GemmEpilogue::Silu, fold == 2 ? &st3 : nullptr);
+            if (st3.part) e.pool.recycle(reinterpret_cast<float *>(st3.part));
         } else {
             DT t = ln3.fwd(e, h);
             a = inverted.fwd(e, t, nullptr, GemmEpilogue::Silu);

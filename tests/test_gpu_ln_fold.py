@@ -4,8 +4,13 @@ src/unet/transformer.rs:100-126): against the oracle's layer_norm then conv1x1
 (src/engine/norm.rs:151-173, conv.rs:38-55) and SiLU, in EXACT (f32 bar, and
 on rows with a mean far from zero, where the fold's x . W' - mean . rowsum
 cancels) and FAST precision (the f16 bar), f32 and f16-stored weights, ragged
-row counts, and every tiling the planner can be forced to."""
+row counts, and every tiling the planner can be forced to. Then the default
+path of the transformers: the row statistics from partial sums the producer of
+h writes (proj_in's epilogue, mh_conv1x1_row_partials; the cross-lambda
+kernel, mh_cross_lambda_row_sums), folded by mh_conv1x1_layer_norm_stats."""
 from __future__ import annotations
+
+import ctypes
 
 import numpy as np
 import pytest
@@ -102,3 +107,119 @@ def test_every_tiling(ctx, plan, tune):
     print(f"ln fold plan {plan}", flush=True)
     got = run(ctx, x, g, be, w, b, True)
     assert max_abs_rel(got, want(x, g, be, w, b, True)) <= F32_TIGHT
+
+
+# ---- row statistics from the producer's partials (the transformers' default path)
+
+
+def producer(ctx, x, w, b, f16=False):
+    """mh_conv1x1_row_partials: y = x . W^T + b and its LayerNorm row partials."""
+    rows, ci = x.shape
+    co = w.shape[0]
+    param = E.Param(ctx, w, f16=f16)
+    xd, bd = E.DeviceArray.from_numpy(ctx, x), E.DeviceArray.from_numpy(ctx, b)
+    out = E.DeviceArray(ctx, (rows, co))
+    part = E.DeviceArray(ctx, (rows, -(-co // 32), 2))
+    per_row = ctypes.c_uint32()
+    E.check(E.lib().mh_conv1x1_row_partials(ctx.h, xd.ptr, rows, ci, param.ptr, param.dtype, co, bd.ptr, out.ptr,
+                                            part.ptr, ctypes.byref(per_row)))
+    n = per_row.value
+    return out.numpy(), part.numpy().reshape(-1)[: rows * n * 2].reshape(rows, n, 2), n
+
+
+def consumer(ctx, x, parts, gamma, beta, w, b, silu, f16=False, eps=1e-5):
+    rows, ci = x.shape
+    co = w.shape[0]
+    param = E.Param(ctx, w, f16=f16)
+    dev = {k: E.DeviceArray.from_numpy(ctx, np.ascontiguousarray(v))
+           for k, v in dict(x=x, g=gamma, be=beta, b=b, p=parts).items()}
+    out = E.DeviceArray(ctx, (rows, co))
+    E.check(E.lib().mh_conv1x1_layer_norm_stats(ctx.h, dev["x"].ptr, rows, ci, dev["g"].ptr, dev["be"].ptr, eps,
+                                                param.ptr, param.dtype, co, dev["b"].ptr, 1 if silu else 0,
+                                                dev["p"].ptr, parts.shape[1], out.ptr))
+    return out.numpy()
+
+
+@pytest.mark.parametrize("rows,c,co", [(512, 320, 400), (512, 320, 1600), (128, 640, 800), (16, 1280, 1600),
+                                       (198, 200, 72)])
+@pytest.mark.parametrize("plan", [None, "32,32,1", "64,64,1", "128,128,1", "64,80,1,4,1,1,1", "32,80,1,2,1,2,1",
+                                  "160,64,1,2,2,1,1,16"])
+def test_row_partials_then_folded_layer_norm(ctx, rows, c, co, plan, tune):
+    """proj_in (c -> c) writes h and its row partials; the q | k | v (or inverted)
+    GEMM folds LayerNorm(h) with those statistics. The partials sum to h's row
+    sums; the result matches the oracle's layer_norm then conv1x1 of that h."""
+    rng = np.random.default_rng(rows + c + co)
+    x = rng.standard_normal((rows, c)).astype(np.float32)
+    wp = (rng.standard_normal((c, c)) / np.sqrt(c)).astype(np.float32)
+    bp = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    _, g, be, w, b = inputs(rows, c, co, 3 + co)
+    if plan:
+        tune("gemm_plan", plan)
+    print(f"row partials {rows}x{c}->{co} plan {plan}", flush=True)
+    h, parts, n = producer(ctx, x, wp, bp)
+    if n == 0:
+        pytest.skip(f"plan {plan} writes no row partials for this shape")
+    hd = h.astype(np.float64)
+    assert np.allclose(parts[:, :, 0].astype(np.float64).sum(1), hd.sum(1), rtol=1e-5, atol=1e-3)
+    assert np.allclose(parts[:, :, 1].astype(np.float64).sum(1), (hd * hd).sum(1), rtol=1e-5, atol=1e-3)
+    tune("gemm_plan", None)
+    got = consumer(ctx, h, parts, g, be, w, b, True)
+    assert max_abs_rel(got, want(h, g, be, w, b, True)) <= F32_TIGHT
+
+
+def test_row_partials_fast_precision(ctx):
+    rows, c, co = 512, 320, 1600
+    rng = np.random.default_rng(77)
+    x = rng.standard_normal((rows, c)).astype(np.float32)
+    wp = (rng.standard_normal((c, c)) / np.sqrt(c)).astype(np.float32)
+    bp = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    _, g, be, w, b = inputs(rows, c, co, 78)
+    ctx.set_precision(True)
+    try:
+        h, parts, n = producer(ctx, x, wp, bp, f16=True)
+        assert n > 0
+        got = consumer(ctx, h, parts, g, be, w, b, True, f16=True)
+    finally:
+        ctx.set_precision(False)
+    assert max_abs_rel(got, want(h, g, be, w.astype(np.float16).astype(np.float32), b, True)) <= F16_TOL
+
+
+@pytest.mark.parametrize("offset", [8.0, -30.0])
+def test_row_partials_rows_far_from_zero_mean(ctx, offset):
+    """sum y*y / K - mean^2 cancels when |mean| >> std: the f32 partials must
+    still give the f32 bar (the rows here have std 1.5)."""
+    rows, c, co = 512, 320, 400
+    rng = np.random.default_rng(11)
+    h = (rng.standard_normal((rows, c)) * 1.5 + offset).astype(np.float32)
+    _, g, be, w, b = inputs(rows, c, co, 12)
+    hd = h.astype(np.float64)
+    # partials as a producer writes them: f32 sums over 64-column tiles
+    t = hd.reshape(rows, c // 64, 64)
+    parts = np.stack([t.sum(2), (t * t).sum(2)], -1).astype(np.float32)
+    got = consumer(ctx, h, parts, g, be, w, b, False)
+    assert max_abs_rel(got, want(h, g, be, w, b, False)) <= F32_TOL
+
+
+@pytest.mark.parametrize("nb,hw,k", [(2, 4096, 40), (2, 1024, 80), (2, 256, 160), (1, 37, 40)])
+def test_cross_lambda_row_sums(ctx, nb, hw, k):
+    """The cross-lambda kernel's row sums are those of the rows it writes, and
+    writing them changes none of the written bits."""
+    rng = np.random.default_rng(k + hw)
+    q = rng.standard_normal((nb, hw, 8 * k)).astype(np.float32)
+    e = rng.standard_normal((hw, 10, k)).astype(np.float32)
+    vb = rng.standard_normal((2, 10, k)).astype(np.float32)
+    lam = (rng.standard_normal((2, k, k)) / np.sqrt(k)).astype(np.float32)
+    h = rng.standard_normal((nb, hw, 8 * k)).astype(np.float32)
+    dv = {n: E.DeviceArray.from_numpy(ctx, v) for n, v in dict(q=q, e=e, vb=vb, lam=lam).items()}
+    print(f"cross-lambda row sums {nb}x{hw} k {k}", flush=True)
+    h1, h2 = E.DeviceArray.from_numpy(ctx, h), E.DeviceArray.from_numpy(ctx, h)
+    sums = E.DeviceArray(ctx, (nb * hw, 2))
+    E.check(E.lib().mh_cross_lambda(ctx.h, dv["q"].ptr, dv["e"].ptr, dv["lam"].ptr, dv["vb"].ptr, 0, nb, hw, k,
+                                    h1.ptr, h1.ptr))
+    E.check(E.lib().mh_cross_lambda_row_sums(ctx.h, dv["q"].ptr, dv["e"].ptr, dv["lam"].ptr, dv["vb"].ptr, 0, nb, hw,
+                                             k, h2.ptr, h2.ptr, sums.ptr))
+    a, b2, s = h1.numpy(), h2.numpy(), sums.numpy()
+    assert np.array_equal(a, b2)
+    rows = a.reshape(nb * hw, 8 * k).astype(np.float64)
+    assert np.allclose(s[:, 0], rows.sum(1), rtol=1e-5, atol=1e-3)
+    assert np.allclose(s[:, 1], (rows * rows).sum(1), rtol=1e-5, atol=1e-3)

@@ -513,8 +513,14 @@ __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__res
 // precision): every operand is rounded to f16 (nearest even, saturating at
 // +-65504) as it is loaded, so the products are those of f16 operands, summed in
 // f32 as the f16 GEMM does.
-constexpr int kTapRows = 240, kTapParts = 3, kPartRows = kTapRows / kTapParts;  // 80
-constexpr int kStageLd = kPartRows * kHeads + 8;  // one pixel's staged run (+8: the two pixels on other banks)
+constexpr int kTapRows = 240;
+// Rows per part (PR, the template argument): 80 (3 tap parts) where the map
+// gives every SIMD several waves, 48 or 16 on the smaller maps, whose waves would
+// otherwise each walk 80 rows in one MFMA chain after another.
+template <int PR>
+constexpr int tap_parts() { return kTapRows / PR; }
+template <int PR>
+constexpr int stage_ld() { return PR * kHeads + 8; }  // one pixel's staged run (+8: the two pixels on other banks)
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 template <bool R16>
@@ -532,18 +538,19 @@ __device__ __forceinline__ float4 op_round4(float4 v) {
     return make_float4(op_round<R16>(v.x), op_round<R16>(v.y), op_round<R16>(v.z), op_round<R16>(v.w));
 }
 
-template <int NF, int TAIL, bool R16>
+template <int NF, int TAIL, bool R16, int PR>
 __global__ __launch_bounds__(256) void lambda_taps_kernel(const float *__restrict__ q,
                                                           const float *__restrict__ w_aug_t,
                                                           const float *__restrict__ lam_t, int hw,
                                                           float *__restrict__ a, float *__restrict__ yc, int part0) {
     constexpr int K = 16 * NF + 4 * TAIL, K4 = K / 4;
     constexpr int WS = K + 4;  // LDS row stride: (K + 4) / 4 odd puts the 16 rows of a read on distinct banks
-    static_assert((WS / 4) % 2 == 1 && K % kPartRows % 4 == 0, "LDS layout");
+    constexpr int kPartRows = PR, kTapParts = tap_parts<PR>(), kStageLd = stage_ld<PR>();
+    static_assert((WS / 4) % 2 == 1 && K % kPartRows % 4 == 0 && kTapRows % PR == 0 && PR % 16 == 0, "LDS layout");
     __shared__ float ws[kPartRows * WS];
     __shared__ float4 st4[4][2 * kStageLd / 4];  // per wave: two pixels' runs
     const int part = int(blockIdx.y) + part0, item = int(blockIdx.z);
-    // parts past the taps: Yc, lambda_t's rows (value channels j) 80 at a time
+    // parts past the taps: Yc, lambda_t's rows (value channels j) PR at a time
     const bool content = part >= kTapParts;
     const int r0 = (content ? part - kTapParts : part) * kPartRows;
     const int rows = min(kPartRows, (content ? K : kTapsB) - r0);  // valid rows of the part
@@ -1013,10 +1020,16 @@ void lambda_taps(Context &ctx, const float *q, const float *w_aug_t, const float
                    (w_aug_t == nullptr) == (a_t == nullptr) && (w_aug_t || lambda_t),
                "lambda position coefficients: operands 16-byte aligned; w_aug_t with a_t, lambda_t with yc");
     if (nb == 0 || hw == 0) return;
-    // LDS per workgroup: its part's rows (80 of k + 4) and 4 waves' staging.
-    const size_t lds = size_t(kPartRows) * (k + 4) * sizeof(float) + size_t(4) * 2 * kStageLd * sizeof(float);
-    const int part0 = w_aug_t ? 0 : kTapParts;  // no w_aug_t: the content part alone
-    const int parts = (w_aug_t ? kTapParts : 0) + (lambda_t ? int(ceil_div(k, kPartRows)) : 0);
+    // Rows per part: 80 from 8192 pixels (the 64x64 latents' batch of two: four
+    // waves per SIMD already), 48 from 2048, else 16 (or Tuning::taps_rows).
+    const int64_t npix = int64_t(nb) * hw;
+    int pr = npix >= 8192 ? 80 : npix >= 2048 ? 48 : 16;
+    if (ctx.tune.taps_rows == 80 || ctx.tune.taps_rows == 48 || ctx.tune.taps_rows == 16) pr = ctx.tune.taps_rows;
+    const int tap_parts_n = kTapRows / pr, ld = pr * kHeads + 8;
+    // LDS per workgroup: its part's rows (pr of k + 4) and 4 waves' staging.
+    const size_t lds = size_t(pr) * (k + 4) * sizeof(float) + size_t(4) * 2 * ld * sizeof(float);
+    const int part0 = w_aug_t ? 0 : tap_parts_n;  // no w_aug_t: the content parts alone
+    const int parts = (w_aug_t ? tap_parts_n : 0) + (lambda_t ? int(ceil_div(k, pr)) : 0);
     const int64_t tasks = (hw + 1) / 2;
     // Workgroups of 4 waves, at most as many as fit on the chip at once, each
     // wave looping over its item's pixel pairs.
@@ -1025,10 +1038,14 @@ void lambda_taps(Context &ctx, const float *q, const float *w_aug_t, const float
     const dim3 grid(unsigned(std::min<int64_t>(ceil_div(tasks, 4), cap)), unsigned(parts), unsigned(nb));
     // FAST contexts take the products of f16-rounded operands, as their GEMMs do.
     auto go = [&](auto kern) { kern<<<grid, 256, 0, ctx.stream>>>(q, w_aug_t, lambda_t, hw, a_t, yc, part0); };
+    auto by_rows = [&](auto k80, auto k48, auto k16) { pr == 80 ? go(k80) : pr == 48 ? go(k48) : go(k16); };
     const bool r16 = ctx.precision == Precision::Fast;
-    if (k == 40) r16 ? go(lambda_taps_kernel<2, 2, true>) : go(lambda_taps_kernel<2, 2, false>);
-    else if (k == 80) r16 ? go(lambda_taps_kernel<5, 0, true>) : go(lambda_taps_kernel<5, 0, false>);
-    else r16 ? go(lambda_taps_kernel<10, 0, true>) : go(lambda_taps_kernel<10, 0, false>);
+#define MH_TAPS(NF, TAIL, R) \
+    by_rows(lambda_taps_kernel<NF, TAIL, R, 80>, lambda_taps_kernel<NF, TAIL, R, 48>, lambda_taps_kernel<NF, TAIL, R, 16>)
+    if (k == 40) r16 ? MH_TAPS(2, 2, true) : MH_TAPS(2, 2, false);
+    else if (k == 80) r16 ? MH_TAPS(5, 0, true) : MH_TAPS(5, 0, false);
+    else r16 ? MH_TAPS(10, 0, true) : MH_TAPS(10, 0, false);
+#undef MH_TAPS
     MH_LAUNCH_CHECK();
 }
 

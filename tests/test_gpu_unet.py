@@ -146,6 +146,34 @@ def test_lambda_position_coeffs_kernel(ctx, nb, hw, k, content):
             assert max_abs_rel(got_yc, gy.numpy()) < 1e-5
 
 
+# Every part height of the kernel (80, 48 and 16 rows; the launcher picks one by
+# map size) runs each output's MFMA chain unchanged: the same bits as the
+# default, for A and Yc, in EXACT and FAST precision.
+@pytest.mark.parametrize("nb,hw,k", [(2, 4096, 40), (2, 1024, 80), (2, 256, 160), (1, 7, 40), (2, 301, 80),
+                                     (1, 9, 160)])
+@pytest.mark.parametrize("fast", [False, True])
+def test_lambda_position_coeffs_every_part_height(ctx, nb, hw, k, fast, tune):
+    rng = np.random.default_rng(3 * hw + k)
+    npx = nb * hw
+    q = rng.standard_normal((npx, 8, k)).astype(np.float32)
+    w = rng.standard_normal((226, k)).astype(np.float32)
+    lam_t = rng.standard_normal((nb, k, k)).astype(np.float32)
+    qd, wd, ld = D(ctx, q), D(ctx, w), D(ctx, lam_t)
+    runs = []
+    ctx.set_precision(fast)
+    try:
+        for rows in (None, 80, 48, 16):
+            tune("taps_rows", rows)
+            print(f"position coeffs {nb}x{hw} k {k} fast={fast} rows {rows}", flush=True)
+            out, yc = E.DeviceArray(ctx, (npx, 226, 8)), E.DeviceArray(ctx, (npx, 8, k))
+            E.check(E.lib().mh_lambda_position_coeffs(ctx.h, qd.ptr, wd.ptr, ld.ptr, nb, hw, k, out.ptr, yc.ptr))
+            runs.append((out.numpy(), yc.numpy()))
+    finally:
+        ctx.set_precision(False)
+    for a, y in runs[1:]:
+        assert np.array_equal(a, runs[0][0]) and np.array_equal(y, runs[0][1])
+
+
 # The content term alone (the cross-lambda's Yc = Q . lambda_c[branch], item b
 # on branch br0 + b): lambda_t points at the first item's branch.
 @pytest.mark.parametrize("br0,nb,hw,k", [(0, 2, 4096, 40), (1, 1, 1024, 80), (0, 2, 256, 160), (0, 2, 37, 40)])

@@ -887,6 +887,167 @@ __global__ __launch_bounds__(256) void cross_lambda_kernel(const float *__restri
     }
 }
 
+// Cross-lambda output with the content term on the matrix cores: Yc =
+// Q . lambda_c[branch] as 16x16x4 f32 MFMA products, rows (pixel, head) and
+// columns the value channels j; then per output, as cross_lambda_kernel, the
+// position term added in the reference's order (o += B[h][m] * V[m] for m =
+// 0..9 with fused multiply-adds, B the 8-lane dots q_h . E[n][m]) and the
+// residual. A block takes P pixels of one item (so one branch) and stages
+// their q and E rows in LDS first, every load in flight at once; phase 1 forms
+// B from LDS; then each wave takes (pixel pair, 16 value channels) tasks: lane
+// (i = l % 16, g = l / 16) supplies q[pixel 2rb + i / 8][head i % 8][kk] and
+// lambda_c[kk][16cb + i] for kk = 16f + 4g + t (instruction t of chunk f), then
+// kk = 16NF + 4u + g, its lambda_c values loaded before the first product;
+// register v of lane l then holds row 4g + v, column l % 16. With lambda_c = 0
+// the products sum to +0 and the output is the position term's exactly.
+// row_sums (optional): LayerNorm row partials of the written rows, per lane
+// over its four rows of one pixel, across the 16 column lanes by an xor
+// butterfly, then per pixel over the column blocks and head halves in order.
+template <int K>
+__device__ __forceinline__ float dot8_lds(const float *a, const float *b) {  // dot8_ref's operations
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < K; i += 8) {
+        const float4 a0 = *reinterpret_cast<const float4 *>(a + i), a1 = *reinterpret_cast<const float4 *>(a + i + 4);
+        const float4 b0 = *reinterpret_cast<const float4 *>(b + i), b1 = *reinterpret_cast<const float4 *>(b + i + 4);
+        acc[0] = __builtin_fmaf(a0.x, b0.x, acc[0]);
+        acc[1] = __builtin_fmaf(a0.y, b0.y, acc[1]);
+        acc[2] = __builtin_fmaf(a0.z, b0.z, acc[2]);
+        acc[3] = __builtin_fmaf(a0.w, b0.w, acc[3]);
+        acc[4] = __builtin_fmaf(a1.x, b1.x, acc[4]);
+        acc[5] = __builtin_fmaf(a1.y, b1.y, acc[5]);
+        acc[6] = __builtin_fmaf(a1.z, b1.z, acc[6]);
+        acc[7] = __builtin_fmaf(a1.w, b1.w, acc[7]);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) s += acc[l];
+    return s + 0.0f;
+}
+
+template <int NF, int TAIL, int P, int NT>
+__global__ __launch_bounds__(NT) void cross_lambda_mfma_kernel(const float *__restrict__ q,
+                                                                const float *__restrict__ e,
+                                                                const float *__restrict__ lam,
+                                                                const float *__restrict__ vbr, int br0, int hw,
+                                                                const float *res, float *out,
+                                                                float2 *__restrict__ row_sums) {
+    constexpr int K = 16 * NF + 4 * TAIL, K4 = K / 4, NCB = (K + 15) / 16, RB = (P + 1) / 2, TASKS = RB * NCB;
+    constexpr int QF4 = P * kHeads * K4, EF4 = P * kTokens * K4, SF4 = QF4 + EF4;
+    constexpr int PER = (SF4 + NT - 1) / NT;
+    static_assert(K % 8 == 0, "8-lane dots over whole chunks");
+    __shared__ float4 stage[SF4];  // q [P][8][K], then E [P][10][K]
+    __shared__ float bm[P][kHeads][kTokens];
+    __shared__ float2 part[P][NCB][2];
+    const int item = int(blockIdx.y);
+    const int p0 = int(blockIdx.x) * P;
+    const int np = min(P, hw - p0);
+    const int64_t pix0 = int64_t(item) * hw + p0;
+    const int br = br0 + item;
+    {
+        const float4 *q4 = reinterpret_cast<const float4 *>(q) + pix0 * (kHeads * K4);
+        const float4 *e4 = reinterpret_cast<const float4 *>(e) + int64_t(p0) * (kTokens * K4);
+        float4 r[PER];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int t = int(threadIdx.x) + NT * i;
+            r[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (t < QF4) {
+                if (t / (kHeads * K4) < np) r[i] = q4[t];
+            } else if (t < SF4) {
+                if ((t - QF4) / (kTokens * K4) < np) r[i] = e4[t - QF4];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int t = int(threadIdx.x) + NT * i;
+            if (t < SF4) stage[t] = r[i];
+        }
+    }
+    __syncthreads();
+    const float *qs = reinterpret_cast<const float *>(stage);
+    const float *es = qs + QF4 * 4;
+    // phase 1: B[p][h][m] = q_h . E[n][m] (the reference's 8-lane dot)
+    for (int t = threadIdx.x; t < P * kHeads * kTokens; t += blockDim.x) {
+        const int p = t / (kHeads * kTokens), hm = t - p * (kHeads * kTokens);
+        const int h = hm / kTokens, m = hm - h * kTokens;
+        bm[p][h][m] = p < np ? dot8_lds<K>(qs + (p * kHeads + h) * K, es + (p * kTokens + m) * K) : 0.f;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = int(blockDim.x) >> 6;
+    const int col = lane & 15, g = lane >> 4;
+    const float *lb = lam + int64_t(br) * K * K;
+    const float *vb = vbr + int64_t(br) * kTokens * K;
+    for (int task = wave; task < TASKS; task += nwaves) {
+        const int rb = task / NCB, cb = task - rb * NCB;
+        const int pa = 2 * rb + (col >> 3), ha = col & 7;  // this lane's A row: pixel, head
+        const float *qa = qs + (min(pa, P - 1) * kHeads + ha) * K;  // (rows past np read staged zeros)
+        const int jb = 16 * cb + col;                              // this lane's B column
+        const bool bv = jb < K;
+        float bf[NF > 0 ? NF : 1][4], bt[TAIL > 0 ? TAIL : 1];
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) bf[f][t] = bv ? lb[int64_t(16 * f + 4 * g + t) * K + jb] : 0.f;
+#pragma unroll
+        for (int u = 0; u < TAIL; ++u) bt[u] = bv ? lb[int64_t(16 * NF + 4 * u + g) * K + jb] : 0.f;
+        floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            const float4 a4 = *reinterpret_cast<const float4 *>(qa + 16 * f + 4 * g);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.x, bf[f][0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.y, bf[f][1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.z, bf[f][2], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.w, bf[f][3], acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < TAIL; ++u)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[16 * NF + 4 * u + g], bt[u], acc, 0, 0, 0);
+        // epilogue: lane (col, g) holds rows 4g..4g+3 (one pixel, heads 4(g&1)..+3) of column jb
+        const int pd = 2 * rb + (g >> 1);
+        const bool ok = pd < np && bv;
+        float ls = 0.f, lq = 0.f;
+        if (ok) {
+            const int64_t pix = pix0 + pd;
+            float vv[kTokens];  // V[m][jb], read once for the four rows (out may alias nothing read here)
+#pragma unroll
+            for (int m = 0; m < kTokens; ++m) vv[m] = vb[m * K + jb];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int h = 4 * (g & 1) + v;
+                float o = acc[v];
+#pragma unroll
+                for (int m = 0; m < kTokens; ++m) o = __builtin_fmaf(bm[pd][h][m], vv[m], o);
+                const int64_t idx = (pix * kHeads + h) * K + jb;
+                const float u = res ? res[idx] + o : o;
+                out[idx] = u;
+                ls += u;
+                lq = __builtin_fmaf(u, u, lq);
+            }
+        }
+        if (row_sums) {
+#pragma unroll
+            for (int off = 1; off < 16; off <<= 1) {
+                ls += __shfl_xor(ls, off, 64);
+                lq += __shfl_xor(lq, off, 64);
+            }
+            if (col == 0 && pd < P) part[pd][cb][g & 1] = float2{ls, lq};
+        }
+    }
+    if (!row_sums) return;
+    __syncthreads();
+    if (int(threadIdx.x) < np) {
+        const int p = threadIdx.x;
+        float2 t{0.f, 0.f};
+        for (int cb = 0; cb < NCB; ++cb)
+            for (int half = 0; half < 2; ++half) {
+                const float2 v = part[p][cb][half];
+                t.x += v.x, t.y += v.y;
+            }
+        row_sums[pix0 + p] = t;
+    }
+}
+
 }  // namespace
 
 void softmax_lambda(Context &ctx, const float *keys, const float *v, int nb, int rows, int k, int vd,
@@ -1074,6 +1235,20 @@ void cross_lambda(Context &ctx, const float *q, const float *e, const float *lam
     MH_REQUIRE(out != q, "cross_lambda: out must not alias q");
     const int64_t npix = int64_t(nb) * hw;
     if (npix == 0) return;
+    // The UNet's head widths take the matrix-core kernel (Tuning::cross_mfma 0 or
+    // a forced head count: the per-thread kernel below).
+    if (ctx.tune.cross_mfma && !ctx.tune.cross_heads && (k == 40 || k == 80 || k == 160)) {
+        // P pixels per block: 12 (64x64 latents, 4 waves) or 10 (8 waves) tasks per block
+        auto go = [&](auto kern, int P, int nt) {
+            const dim3 grid(unsigned(ceil_div(hw, P)), unsigned(nb));
+            kern<<<grid, nt, 0, ctx.stream>>>(q, e, lambda_c, v_branches, br0, hw, residual, out, row_sums);
+        };
+        if (k == 40) go(cross_lambda_mfma_kernel<2, 2, 8, 256>, 8, 256);
+        else if (k == 80) go(cross_lambda_mfma_kernel<5, 0, 4, 512>, 4, 512);
+        else go(cross_lambda_mfma_kernel<10, 0, 2, 512>, 2, 512);
+        MH_LAUNCH_CHECK();
+        return;
+    }
     // Heads per thread: 4 while that still gives every CU a block, else 2
     // (measured at the UNet's sizes: 64x64 / k 40 15.6 us with 4 against 21.1
     // with 8, 32x32 / k 80 14.3 against 16.5 with 2, 16x16 / k 160 16.0 with 2

@@ -257,7 +257,10 @@ def test_position_term_kernel_bit_exact(ctx, br0, nb, k):
 # reference) within the f32 bar. Sizes select the default heads-per-thread
 # variants (4 at 64x64 / k 40 and 32x32 / k 80, 2 at 16x16 / k 160) plus a ragged
 # block; MOEBIUS_HIP_CROSS_HEADS forces each variant, 8 included.
-@pytest.mark.parametrize("br0,nb,hw,k", [(0, 2, 4096, 40), (0, 2, 1024, 80), (0, 2, 256, 160), (1, 1, 37, 40)])
+# None: the default, the matrix-core kernel for these head widths (its pixel
+# blocks never straddle items: 37 and 9 pixels per item leave ragged blocks).
+@pytest.mark.parametrize("br0,nb,hw,k", [(0, 2, 4096, 40), (0, 2, 1024, 80), (0, 2, 256, 160), (1, 1, 37, 40),
+                                         (0, 2, 37, 80), (0, 2, 9, 160), (0, 2, 13, 40)])
 @pytest.mark.parametrize("heads", [None, "2", "4", "8"])
 def test_cross_lambda_kernel(ctx, br0, nb, hw, k, heads, tune):
     if heads:

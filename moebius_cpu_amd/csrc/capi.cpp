@@ -723,6 +723,21 @@ int32_t mh_tap_filter(MhContext *ctx, const float *a_t, const float *v, const fl
     });
 }
 
+int32_t mh_tap_filter_row_sums(MhContext *ctx, const float *a_t, const float *v, const float *yc,
+                               const float *residual, float *out, uint32_t nb, uint32_t hh, uint32_t ww, uint32_t vd,
+                               float *row_sums) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(a_t, "a_t");
+        need(v, "v");
+        need(yc, "yc");
+        need(out, "out");
+        need(row_sums, "row_sums");
+        mh::tap_filter(c, a_t, v, yc, residual, out, dim(nb, "nb"), dim(hh, "hh"), dim(ww, "ww"), dim(vd, "vd"),
+                       nullptr, reinterpret_cast<float2 *>(row_sums));
+    });
+}
+
 int32_t mh_tap_filter_ln(MhContext *ctx, const float *a_t, const float *v, const float *yc, const float *residual,
                          float *out, uint32_t nb, uint32_t hh, uint32_t ww, uint32_t vd, const float *gamma,
                          const float *beta, float eps, float *ln_out) {

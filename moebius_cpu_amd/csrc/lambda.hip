@@ -174,7 +174,52 @@ struct LnOut {
     const float *gamma = nullptr, *beta = nullptr;
     float eps = 0.f;
     float *out = nullptr;  // [pixels][c]
+    // Instead of the LayerNorm: per pixel row, (sum, sum of squares) of the
+    // values written, for a consumer that folds the LayerNorm itself.
+    float2 *row_sums = nullptr;
 };
+
+// LayerNorm row partials of the rows a kernel has just written (LnOut::row_sums):
+// thread r of a pixel's per_px threads sums its HG float4 in order; the
+// threads' sums are added in chunks of 8 and the chunks in order through LDS
+// (red: 2 * blockDim.x floats), so the partials are deterministic. Every
+// thread of the block reaches both barriers.
+template <int HG>
+__device__ __forceinline__ void ln_pixel_sums(const LnOut &ln, const float4 (&u)[HG], bool active, float *red, int p,
+                                              int per_px, int r, int64_t pix) {
+    float s = 0.f, q = 0.f;
+#pragma unroll
+    for (int i = 0; i < HG; ++i) {
+        s += u[i].x, s += u[i].y, s += u[i].z, s += u[i].w;
+        q = __builtin_fmaf(u[i].x, u[i].x, q);
+        q = __builtin_fmaf(u[i].y, u[i].y, q);
+        q = __builtin_fmaf(u[i].z, u[i].z, q);
+        q = __builtin_fmaf(u[i].w, u[i].w, q);
+    }
+    float2 *red2 = reinterpret_cast<float2 *>(red);
+    red2[threadIdx.x] = active ? float2{s, q} : float2{0.f, 0.f};
+    __syncthreads();
+    const int nch = (per_px + 7) / 8;
+    float2 cs{0.f, 0.f};
+    if (active && r < nch) {
+        const int j1 = min(per_px, 8 * r + 8);
+        for (int j = 8 * r; j < j1; ++j) {
+            const float2 v = red2[p * per_px + j];
+            cs.x += v.x, cs.y += v.y;
+        }
+    }
+    __syncthreads();
+    if (active && r < nch) red2[p * per_px + r] = cs;
+    __syncthreads();
+    if (active && r == 0) {
+        float2 t = red2[p * per_px];
+        for (int j = 1; j < nch; ++j) {
+            const float2 v = red2[p * per_px + j];
+            t.x += v.x, t.y += v.y;
+        }
+        ln.row_sums[pix] = t;
+    }
+}
 
 template <int HG>
 __device__ __forceinline__ void ln_pixel_rows(const LnOut &ln, const float4 (&u)[HG], bool active, float *red, int p,
@@ -318,9 +363,9 @@ __global__ __launch_bounds__(256) void tap_filter_kernel(const float *__restrict
             }
         }
     }
-    extern __shared__ float red[];  // LN: [blockDim.x]; RS > 1: then [RS - 1][opb][HG] float4
+    extern __shared__ float red[];  // LN: [2 * blockDim.x]; RS > 1: then [RS - 1][opb][HG] float4
     if constexpr (RS > 1) {
-        float4 *part = reinterpret_cast<float4 *>(red + (LN ? (blockDim.x + 3) / 4 * 4 : 0));  // 16-byte aligned
+        float4 *part = reinterpret_cast<float4 *>(red + (LN ? (2 * blockDim.x + 3) / 4 * 4 : 0));  // 16-byte aligned
         if (split > 0 && active)
 #pragma unroll
             for (int i = 0; i < HG; ++i) part[((split - 1) * opb + lt) * HG + i] = acc[i];
@@ -345,7 +390,8 @@ __global__ __launch_bounds__(256) void tap_filter_kernel(const float *__restrict
     }
     if constexpr (LN) {
         const int tpp = NG * v4;
-        ln_pixel_rows<HG>(ln, acc, owner, red, lt / tpp, tpp, kHeads * vd, pix, hg, jq, v4);
+        if (ln.row_sums) ln_pixel_sums<HG>(ln, acc, owner, red, lt / tpp, tpp, lt % tpp, pix);
+        else ln_pixel_rows<HG>(ln, acc, owner, red, lt / tpp, tpp, kHeads * vd, pix, hg, jq, v4);
     }
 }
 
@@ -491,8 +537,9 @@ __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__res
         }
     }
     if constexpr (LN) {
-        float *red = reinterpret_cast<float *>(cls + 2 * tx * kRowC4);  // [blockDim.x]
-        ln_pixel_rows<HG>(ln, acc, active, red, xl, tpp, kHeads * vd, pix, hg, jq, v4);
+        float *red = reinterpret_cast<float *>(cls + 2 * tx * kRowC4);  // [2 * blockDim.x]
+        if (ln.row_sums) ln_pixel_sums<HG>(ln, acc, active, red, xl, tpp, r, pix);
+        else ln_pixel_rows<HG>(ln, acc, active, red, xl, tpp, kHeads * vd, pix, hg, jq, v4);
     }
 }
 
@@ -1074,13 +1121,14 @@ void softmax_lambda(Context &ctx, const float *keys, const float *v, int nb, int
 }
 
 void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc, const float *residual, float *out,
-                int nb, int hh, int ww, int vd, const LayerNormOut *lno) {
+                int nb, int hh, int ww, int vd, const LayerNormOut *lno, float2 *row_sums) {
     MH_REQUIRE(vd % 4 == 0, "tap_filter: value width must be a multiple of 4");
     MH_REQUIRE(aligned16(a_t) && aligned16(v) && aligned16(yc) && aligned16(residual) && aligned16(out),
                "tap_filter: buffers must be 16-byte aligned");
     const int64_t pix = int64_t(nb) * hh * ww;
     if (pix == 0) return;
     LnOut ln;
+    MH_REQUIRE(!(lno && row_sums), "tap_filter: the LayerNorm output or its row sums, not both");
     if (lno) {
         MH_REQUIRE(lno->gamma && lno->beta && lno->out && aligned16(lno->gamma) && aligned16(lno->beta) &&
                        aligned16(lno->out) && lno->out != out && lno->out != residual && lno->out != yc,
@@ -1090,6 +1138,11 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
         ln.eps = lno->eps;
         ln.out = lno->out;
     }
+    if (row_sums) {
+        MH_REQUIRE((reinterpret_cast<uintptr_t>(row_sums) & 7) == 0, "tap_filter: row sums must be 8-byte aligned");
+        ln.row_sums = row_sums;
+    }
+    const bool lnk = lno || row_sums;  // the kernels' LayerNorm variant (whole pixels per block)
     // Heads per thread: the most (value loads shared by more heads) that still
     // gives the chip about 2048 waves: 4 at 64x64 x 40 channels, 2 at 32x32 x 80,
     // 1 at 16x16 x 160 (batch 2).
@@ -1107,14 +1160,14 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
     if (tile_hg && (kHeads / tile_hg) * v4 <= 256) {
         const int tpp = (kHeads / tile_hg) * v4, tx = std::max(1, std::min(256 / tpp, ww));
         const size_t lds = (size_t(2) * (tx + kWin - 1) * v4 + size_t(2) * tx * (kWin * kHeads / 4)) * 16 +
-                           (lno ? size_t(tx) * tpp * sizeof(float) : 0);
+                           (lnk ? size_t(tx) * tpp * sizeof(float2) : 0);
         const int64_t blocks = int64_t(nb) * hh * ceil_div(ww, tx);
         auto go = [&](auto kern) {
             kern<<<unsigned(blocks), unsigned(tx * tpp), lds, ctx.stream>>>(a_t, v, yc, residual, out, hh, ww, vd, tx,
                                                                            ln);
         };
-        if (tile_hg == 8) lno ? go(tap_filter_tile_kernel<8, true>) : go(tap_filter_tile_kernel<8, false>);
-        else lno ? go(tap_filter_tile_kernel<4, true>) : go(tap_filter_tile_kernel<4, false>);
+        if (tile_hg == 8) lnk ? go(tap_filter_tile_kernel<8, true>) : go(tap_filter_tile_kernel<8, false>);
+        else lnk ? go(tap_filter_tile_kernel<4, true>) : go(tap_filter_tile_kernel<4, false>);
         MH_LAUNCH_CHECK();
         return;
     }
@@ -1124,7 +1177,7 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
         if (want == 1 || want == 2 || want == 4 || want == 8) hg = want;
     }
     const int tpp = (kHeads / hg) * v4;
-    MH_REQUIRE(!lno || tpp <= 256, "tap_filter: LayerNorm output needs a pixel's threads in one block");
+    MH_REQUIRE(!lnk || tpp <= 256, "tap_filter: LayerNorm output needs a pixel's threads in one block");
     // Row split (tap_split tuning: 1, 3 or 5; default 0 chooses): three threads per
     // output while the map gives the chip fewer than two waves per SIMD of unsplit
     // threads and a pixel's 3 * tpp threads fit one block (measured alone with
@@ -1138,9 +1191,9 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
     if (rs * tpp > 256) rs = 1;
     // Blocks of whole outputs: with the LayerNorm or a row split, P whole pixels
     // (P * tpp outputs) times rs threads each; else 256 outputs.
-    const int opb = (lno || rs > 1) ? (256 / (rs * tpp)) * tpp : 256;
+    const int opb = (lnk || rs > 1) ? (256 / (rs * tpp)) * tpp : 256;
     const unsigned threads = unsigned(opb * rs);
-    const size_t lds = (lno ? (threads + 3) / 4 * 4 * sizeof(float) : 0) + size_t(rs - 1) * opb * hg * 16;
+    const size_t lds = (lnk ? (2 * threads + 3) / 4 * 4 * sizeof(float) : 0) + size_t(rs - 1) * opb * hg * 16;
     const int64_t total = pix * tpp;
     const unsigned blocks = unsigned(ceil_div(total, opb));
     auto go = [&](auto kern) {
@@ -1153,19 +1206,19 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
     };
     switch (hg) {
         case 8:
-            lno ? pick(tap_filter_kernel<8, true, 1>, tap_filter_kernel<8, true, 3>, tap_filter_kernel<8, true, 5>)
+            lnk ? pick(tap_filter_kernel<8, true, 1>, tap_filter_kernel<8, true, 3>, tap_filter_kernel<8, true, 5>)
                 : pick(tap_filter_kernel<8, false, 1>, tap_filter_kernel<8, false, 3>, tap_filter_kernel<8, false, 5>);
             break;
         case 4:
-            lno ? pick(tap_filter_kernel<4, true, 1>, tap_filter_kernel<4, true, 3>, tap_filter_kernel<4, true, 5>)
+            lnk ? pick(tap_filter_kernel<4, true, 1>, tap_filter_kernel<4, true, 3>, tap_filter_kernel<4, true, 5>)
                 : pick(tap_filter_kernel<4, false, 1>, tap_filter_kernel<4, false, 3>, tap_filter_kernel<4, false, 5>);
             break;
         case 2:
-            lno ? pick(tap_filter_kernel<2, true, 1>, tap_filter_kernel<2, true, 3>, tap_filter_kernel<2, true, 5>)
+            lnk ? pick(tap_filter_kernel<2, true, 1>, tap_filter_kernel<2, true, 3>, tap_filter_kernel<2, true, 5>)
                 : pick(tap_filter_kernel<2, false, 1>, tap_filter_kernel<2, false, 3>, tap_filter_kernel<2, false, 5>);
             break;
         default:
-            lno ? pick(tap_filter_kernel<1, true, 1>, tap_filter_kernel<1, true, 3>, tap_filter_kernel<1, true, 5>)
+            lnk ? pick(tap_filter_kernel<1, true, 1>, tap_filter_kernel<1, true, 3>, tap_filter_kernel<1, true, 5>)
                 : pick(tap_filter_kernel<1, false, 1>, tap_filter_kernel<1, false, 3>, tap_filter_kernel<1, false, 5>);
     }
     MH_LAUNCH_CHECK();

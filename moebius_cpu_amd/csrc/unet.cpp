@@ -540,8 +540,10 @@ struct SelfLambda {
     }
     // h [x.px()][c] += SelfLambda(x): the block's residual add is folded into the tap filter.
     // ln: x is the block's hidden state and LayerNorm 1 is folded into the q | k | v GEMM.
+    // row_sums (optional, instead of lno): LayerNorm row partials of the new h, one per pixel.
     void fwd_add(Env &e, const DT &x, float *h, const LayerNormOut *lno = nullptr,
-                 const LnFolded *ln = nullptr, const LnRowPartials *ln_stats = nullptr) const {
+                 const LnFolded *ln = nullptr, const LnRowPartials *ln_stats = nullptr,
+                 float2 *row_sums = nullptr) const {
         const int hw = x.h * x.w;
         DT q = e.pool.tensor(x.n, x.h, x.w, c);
         DT kt = e.pool.tensor(x.n, x.h, x.w, k);
@@ -575,7 +577,7 @@ struct SelfLambda {
                     int64_t(TAPS_B) * HEADS, 0, GemmEpilogue::None, HEADS);
         }
         e.pool.recycle(lam_t);
-        tap_filter(e.ctx, a, vt.p, yc.p, h, h, x.n, x.h, x.w, k, lno);
+        tap_filter(e.ctx, a, vt.p, yc.p, h, h, x.n, x.h, x.w, k, lno, row_sums);
         e.pool.recycle(a);
         e.pool.recycle(yc);
         e.pool.recycle(q);
@@ -626,6 +628,18 @@ struct CrossLambda {
     }
     // h [x.px()][c] += CrossLambda(x): Yc = Q . lambda_c, the position term and
     // the residual add in one kernel after the q projection.
+    // The same with LayerNorm 2 of hs folded into to_q (f: to_q on W . diag(gamma),
+    // st: hs's row statistics); hs is h itself, read before the kernel updates it.
+    void fwd_add_ln(Env &env, const DT &hs, int br0, float *h, const LnFolded &f, const LnRowPartials &st,
+                    float2 *row_sums) const {
+        const int hw = hs.h * hs.w;
+        if (hw != n) fail(kInvalidArgument, "CrossLambda input size does not match the position table");
+        DT q = env.pool.tensor(hs.n, hs.h, hs.w, c);
+        float *const outs[1] = {q.p};
+        conv1x1_ln(env.ctx, hs.p, hs.px(), c, f, 1, &c, outs, GemmEpilogue::None, &st);
+        cross_lambda(env.ctx, q.p, e, lambda_c, v, br0, hs.n, hw, k, h, h, row_sums);
+        env.pool.recycle(q);
+    }
     // row_sums (optional): LayerNorm row partials of the new h, one per pixel.
     void fwd_add(Env &env, const DT &x, int br0, float *h, float2 *row_sums = nullptr) const {
         const int hw = x.h * x.w;
@@ -644,7 +658,7 @@ struct MixTransformer {
     LNp ln1, ln2, ln3;
     SelfLambda attn1;
     CrossLambda attn2;
-    LnFold ln1q, ln3f;  // LayerNorm 1 folded into q | k | v, LayerNorm 3 into the inverted 1x1
+    LnFold ln1q, ln2q, ln3f;  // LayerNorms 1, 2, 3 folded into q | k | v, the cross to_q, the inverted 1x1
     const float *dw = nullptr, *dwb = nullptr;
     void load(Env &env, const WeightStore &W, const std::string &p, int c_, const float *ehs_dev) {
         c = c_;
@@ -664,6 +678,7 @@ struct MixTransformer {
         point.load(W, ff + ".point_conv.conv", hidden, c, false);
         proj_out.load(W, p + ".proj_out", c, c, true);
         ln1q.build(env.ctx, attn1.wqkv, attn1.wt, c + 2 * attn1.k, c, ln1.g, ln1.b, attn1.bqkv);
+        ln2q.build(env.ctx, attn2.to_q.w.p, attn2.to_q.w.wt, c, c, ln2.g, ln2.b, attn2.to_q.b);
         ln3f.build(env.ctx, inverted.w.p, inverted.w.wt, 2 * hidden, c, ln3.g, ln3.b, inverted.b);
         HIP_CHECK(hipStreamSynchronize(env.ctx.stream));
     }
@@ -671,6 +686,7 @@ struct MixTransformer {
         attn1.release();
         attn2.release();
         ln1q.release();
+        ln2q.release();
         ln3f.release();
     }
     DT fwd(Env &e, const DT &x, int br0) const { return fwd(e, x, x, br0); }
@@ -706,39 +722,57 @@ struct MixTransformer {
             h = fold == 2 ? proj_in.fwd_lnp(e, t, &st1) : proj_in.fwd(e, t);
             e.pool.recycle(t);
         }
-        // LayerNorm 2 is written beside h by the tap filter that finishes h: the
-        // separate pass costs a launch and a re-read of h (whole step -29 us EXACT,
-        // -36 us FAST). The same in the cross-lambda kernel for LayerNorm 3 measured
-        // 160 us slower per step, so LayerNorm 3 stays a pass of its own.
-        // ln_fold 1: the same folds with the row statistics summed by the GEMMs
-        // from the values they load; 0: LayerNorm passes of their own.
+        // ln_fold 2 folds LayerNorm 2 into the cross-lambda's to_q the same way, from
+        // row sums the tap filter writes as it finishes h. ln_fold 1: LayerNorms 1
+        // and 3 folded with the row statistics summed by the GEMMs from the values
+        // they load; 0: LayerNorm passes of their own. With 1 and 0 LayerNorm 2 is
+        // written beside h by the tap filter (a separate pass costs a launch and a
+        // re-read of h: whole step -29 us EXACT, -36 us FAST).
         const LnFolded lnq = ln1q.view(LN_EPS), lnf = ln3f.view(LN_EPS);
-        DT t2 = e.pool.tensor(h.n, h.h, h.w, h.c);
-        LayerNormOut lno2;
-        lno2.gamma = ln2.g;
-        lno2.beta = ln2.b;
-        lno2.eps = LN_EPS;
-        lno2.out = t2.p;
-        if (fold == 2 && st1.per_row > 0) {
-            attn1.fwd_add(e, h, h.p, &lno2, &lnq, &st1);
-        } else if (fold == 1) {
-            attn1.fwd_add(e, h, h.p, &lno2, &lnq);
-        } else {
-            DT t = ln1.fwd(e, h);
-            attn1.fwd_add(e, t, h.p, &lno2);
-            e.pool.recycle(t);
-        }
-        if (st1.part) e.pool.recycle(reinterpret_cast<float *>(st1.part));
-        if (xs.n != xr.n) {
-            h = widen(e, h, xr.n);
-            t2 = widen(e, t2, xr.n);
-        }
         if (fold == 2) {
+            LnRowPartials st2;
+            st2.part = reinterpret_cast<float2 *>(e.pool.floats(h.px() * 2));
+            st2.per_row = 1;
+            if (st1.per_row > 0) {
+                attn1.fwd_add(e, h, h.p, nullptr, &lnq, &st1, st2.part);
+            } else {
+                DT t = ln1.fwd(e, h);
+                attn1.fwd_add(e, t, h.p, nullptr, nullptr, nullptr, st2.part);
+                e.pool.recycle(t);
+            }
+            e.pool.recycle(reinterpret_cast<float *>(st1.part));
+            if (xs.n != xr.n) {  // h and its row sums repeated to the batch
+                h = widen(e, h, xr.n);
+                float *w2 = e.pool.floats(h.px() * 2);
+                tile_items(e.ctx, reinterpret_cast<const float *>(st2.part), int64_t(xs.px()) * 2, xr.n, w2);
+                e.pool.recycle(reinterpret_cast<float *>(st2.part));
+                st2.part = reinterpret_cast<float2 *>(w2);
+            }
             st3.part = reinterpret_cast<float2 *>(e.pool.floats(h.px() * 2));
             st3.per_row = 1;
+            attn2.fwd_add_ln(e, h, br0, h.p, ln2q.view(LN_EPS), st2, st3.part);
+            e.pool.recycle(reinterpret_cast<float *>(st2.part));
+        } else {
+            DT t2 = e.pool.tensor(h.n, h.h, h.w, h.c);
+            LayerNormOut lno2;
+            lno2.gamma = ln2.g;
+            lno2.beta = ln2.b;
+            lno2.eps = LN_EPS;
+            lno2.out = t2.p;
+            if (fold == 1) {
+                attn1.fwd_add(e, h, h.p, &lno2, &lnq);
+            } else {
+                DT t = ln1.fwd(e, h);
+                attn1.fwd_add(e, t, h.p, &lno2);
+                e.pool.recycle(t);
+            }
+            if (xs.n != xr.n) {
+                h = widen(e, h, xr.n);
+                t2 = widen(e, t2, xr.n);
+            }
+            attn2.fwd_add(e, t2, br0, h.p);
+            e.pool.recycle(t2);
         }
-        attn2.fwd_add(e, t2, br0, h.p, st3.part);
-        e.pool.recycle(t2);
         // MixFFN (transformer.rs:121-129): SiLU(inverted(LN3 h)) -> GLU depthwise -> point + h
         DT a;
         if (fold) {

@@ -353,13 +353,14 @@ int32_t mh_softmax_lambda(MhContext *ctx, const float *keys, const float *v, uin
 int32_t mh_tap_filter(MhContext *ctx, const float *a_t, const float *v, const float *yc, const float *residual,
                       float *out, uint32_t nb, uint32_t hh, uint32_t ww, uint32_t vd);
 
-/* mh_tap_filter that also writes, per output row, the (sum, sum of squares) of
- * the values written (row_sums [nb * hh * ww][2], 8-byte aligned): the
- * statistics of LayerNorm 2, which reads the block's hidden state next
- * (src/unet/transformer.rs:101-103), for mh_conv1x1_layer_norm_stats (per_row 1). */
+/* mh_tap_filter that also writes, per output row, (sum, sum of squares) of the
+ * values written over *per_row disjoint slices of the row (row_sums
+ * [nb * hh * ww][*per_row][2], room for nb * hh * ww * vd / 4 pairs, 8-byte
+ * aligned): the statistics of LayerNorm 2, which reads the block's hidden state
+ * next (src/unet/transformer.rs:101-103), for mh_conv1x1_layer_norm_stats. */
 int32_t mh_tap_filter_row_sums(MhContext *ctx, const float *a_t, const float *v, const float *yc,
                                const float *residual, float *out, uint32_t nb, uint32_t hh, uint32_t ww, uint32_t vd,
-                               float *row_sums);
+                               float *row_sums, uint32_t *per_row);
 
 /* mh_tap_filter followed by the transformer block's `layer_norm` of its output
  * rows (src/unet/transformer.rs:104-108, src/engine/norm.rs:151-173): the same

@@ -103,7 +103,8 @@ SIGNATURES = {
     "mh_selftest_mfma_f32": (_i32, [_vp, _vp, _vp, _vp]),
     "mh_softmax_lambda": (_i32, [_vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
     "mh_tap_filter": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32]),
-    "mh_tap_filter_row_sums": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp]),
+    "mh_tap_filter_row_sums": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp,
+                                      ctypes.POINTER(_u32)]),
     "mh_tap_filter_ln": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _f32, _vp]),
     "mh_lambda_position_coeffs": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _vp, _vp]),
     "mh_position_term": (_i32, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _vp, _vp, _vp]),

@@ -725,7 +725,7 @@ int32_t mh_tap_filter(MhContext *ctx, const float *a_t, const float *v, const fl
 
 int32_t mh_tap_filter_row_sums(MhContext *ctx, const float *a_t, const float *v, const float *yc,
                                const float *residual, float *out, uint32_t nb, uint32_t hh, uint32_t ww, uint32_t vd,
-                               float *row_sums) {
+                               float *row_sums, uint32_t *per_row) {
     return guard([&] {
         mh::Context &c = C(ctx);
         need(a_t, "a_t");
@@ -733,6 +733,9 @@ int32_t mh_tap_filter_row_sums(MhContext *ctx, const float *a_t, const float *v,
         need(yc, "yc");
         need(out, "out");
         need(row_sums, "row_sums");
+        need(per_row, "per_row");
+        MH_REQUIRE(vd % 4 == 0, "tap_filter: value width must be a multiple of 4");
+        *per_row = uint32_t(mh::tap_filter_row_parts(c, dim(hh, "hh"), dim(ww, "ww"), dim(vd, "vd")));
         mh::tap_filter(c, a_t, v, yc, residual, out, dim(nb, "nb"), dim(hh, "hh"), dim(ww, "ww"), dim(vd, "vd"),
                        nullptr, reinterpret_cast<float2 *>(row_sums));
     });

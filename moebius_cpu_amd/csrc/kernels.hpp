@@ -212,10 +212,13 @@ struct LayerNormOut {
 };
 // out [nb*hh*ww][8*vd] = (residual +) (yc + bias tap + 15x15 taps of v); a_t [nb*hh*ww][226][8]
 // (heads innermost). out may alias yc or residual. lno (optional): also the LayerNorm
-// of the out rows; or row_sums (optional, [nb*hh*ww]): per out row, (sum, sum of
-// squares) of the values written, for a consumer that folds the LayerNorm.
+// of the out rows; or row_sums (optional): per out row, (sum, sum of
+// squares) of the values written, for a consumer that folds the LayerNorm; the
+// kernel may write several partials per row (tap_filter_row_parts, each over a
+// slice of the value channels): row_sums [nb*hh*ww][row parts].
 void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc, const float *residual, float *out,
                 int nb, int hh, int ww, int vd, const LayerNormOut *lno = nullptr, float2 *row_sums = nullptr);
+int tap_filter_row_parts(const Context &ctx, int hh, int ww, int vd);
 // Position coefficients A = Q . W_aug (src/unet/lambda.rs:131-137) on the matrix cores:
 // q [nb*hw][8][k] (pixel, head rows of k), w_aug_t [226][k] -> a_t [nb*hw][226][8], the
 // tap-major layout tap_filter reads; with lambda_t [nb][k][k] (softmax_lambda's

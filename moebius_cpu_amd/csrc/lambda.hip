@@ -404,24 +404,28 @@ __global__ __launch_bounds__(256) void tap_filter_kernel(const float *__restrict
 // element the operations are tap_filter_kernel's (the reference's order).
 constexpr int kStageRegs = 4;  // float4 per thread of a staged value / coefficient row
 
+// cq > 0: the block takes the value channel quads [cq * blockIdx.y, + cq) of its
+// pixels only (LayerNorm row sums then per pixel and channel slice, LnOut
+// row_sums [pixels][v4 / cq]; the full LayerNorm needs cq 0, whole rows).
 template <int HG, bool LN>
 __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__restrict__ a_t,
                                                               const float *__restrict__ v, const float *yc,
                                                               const float *res, float *out, int hh, int ww, int vd,
-                                                              int tx, LnOut ln) {
+                                                              int tx, LnOut ln, int cq) {
     extern __shared__ float4 sh4[];
     constexpr int kRowC4 = kWin * kHeads / 4;  // float4 of coefficients per pixel and tap row: 30
     constexpr int NG = kHeads / HG;
-    const int v4 = vd >> 2, tpp = NG * v4, span = tx + kWin - 1;
-    float4 *vls = sh4;                  // [2][span][v4]
-    float4 *cls = sh4 + 2 * span * v4;  // [2][tx][30]
+    const int v4 = vd >> 2, cqn = cq > 0 ? cq : v4, q0 = cq > 0 ? int(blockIdx.y) * cq : 0;
+    const int tpp = NG * cqn, span = tx + kWin - 1;
+    float4 *vls = sh4;                   // [2][span][cqn]
+    float4 *cls = sh4 + 2 * span * cqn;  // [2][tx][30]
     const int tiles_x = (ww + tx - 1) / tx;
     const int bx = int(blockIdx.x % unsigned(tiles_x));
     const int row = int(blockIdx.x / unsigned(tiles_x));  // b * hh + y
     const int b = row / hh, y = row - b * hh;
     const int x0 = bx * tx, ntx = min(tx, ww - x0);
     const int xl = int(threadIdx.x) / tpp, r = int(threadIdx.x) - xl * tpp;
-    const int hg = r / v4, jq = r - hg * v4;
+    const int hg = r / cqn, jl = r - hg * cqn, jq = q0 + jl;
     const int x = x0 + xl;
     const bool active = xl < ntx;
     const int64_t pix0 = int64_t(row) * ww + x0, pix = pix0 + xl;
@@ -454,9 +458,9 @@ __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__res
 #pragma unroll
         for (int i = 0; i < kStageRegs; ++i) {
             const int t = int(threadIdx.x) + i * int(blockDim.x);
-            const int c = t / v4, q = t - c * v4, ix = x0 - kPad + c;
-            sv[i] = (t < span * v4 && ix >= 0 && ix < ww) ? vb[(int64_t(iy) * ww + ix) * v4 + q]
-                                                          : make_float4(0.f, 0.f, 0.f, 0.f);
+            const int c = t / cqn, q = t - c * cqn, ix = x0 - kPad + c;
+            sv[i] = (t < span * cqn && ix >= 0 && ix < ww) ? vb[(int64_t(iy) * ww + ix) * v4 + q0 + q]
+                                                           : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
         for (int i = 0; i < kStageRegs; ++i) {
@@ -470,15 +474,15 @@ __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__res
     // blocks whose rows exceed kStageRegs float4 per thread).
     auto commit = [&](int ky, int buf) {
         const int iy = y + ky - kPad, reg_end = kStageRegs * int(blockDim.x);
-        float4 *vd4 = vls + buf * span * v4;
+        float4 *vd4 = vls + buf * span * cqn;
 #pragma unroll
         for (int i = 0; i < kStageRegs; ++i) {
             const int t = int(threadIdx.x) + i * int(blockDim.x);
-            if (t < span * v4) vd4[t] = sv[i];
+            if (t < span * cqn) vd4[t] = sv[i];
         }
-        for (int t = int(threadIdx.x) + reg_end; t < span * v4; t += blockDim.x) {
-            const int c = t / v4, q = t - c * v4, ix = x0 - kPad + c;
-            vd4[t] = (ix >= 0 && ix < ww) ? vb[(int64_t(iy) * ww + ix) * v4 + q] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int t = int(threadIdx.x) + reg_end; t < span * cqn; t += blockDim.x) {
+            const int c = t / cqn, q = t - c * cqn, ix = x0 - kPad + c;
+            vd4[t] = (ix >= 0 && ix < ww) ? vb[(int64_t(iy) * ww + ix) * v4 + q0 + q] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
         float4 *cd4 = cls + buf * tx * kRowC4;
 #pragma unroll
@@ -499,7 +503,7 @@ __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__res
         const bool next = ky + 1 < ky1;
         if (next) load(ky + 1);
         if (active) {
-            const float4 *vr = vls + buf * span * v4 + xl * v4 + jq;
+            const float4 *vr = vls + buf * span * cqn + xl * cqn + jl;
             const float4 *cr = cls + buf * tx * kRowC4 + xl * kRowC4 + hg * (HG / 4);
 #pragma unroll
             for (int kx = 0; kx < kWin; ++kx) {
@@ -510,7 +514,7 @@ __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__res
                         const float4 c4 = cr[kx * 2 + g];
                         cf[4 * g] = c4.x, cf[4 * g + 1] = c4.y, cf[4 * g + 2] = c4.z, cf[4 * g + 3] = c4.w;
                     }
-                    const float4 s = vr[kx * v4];
+                    const float4 s = vr[kx * cqn];
 #pragma unroll
                     for (int i = 0; i < HG; ++i) {
                         acc[i].x = __builtin_fmaf(cf[i], s.x, acc[i].x);
@@ -538,8 +542,12 @@ __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__res
     }
     if constexpr (LN) {
         float *red = reinterpret_cast<float *>(cls + 2 * tx * kRowC4);  // [2 * blockDim.x]
-        if (ln.row_sums) ln_pixel_sums<HG>(ln, acc, active, red, xl, tpp, r, pix);
-        else ln_pixel_rows<HG>(ln, acc, active, red, xl, tpp, kHeads * vd, pix, hg, jq, v4);
+        if (ln.row_sums) {
+            const int nsl = v4 / cqn;
+            ln_pixel_sums<HG>(ln, acc, active, red, xl, tpp, r, pix * nsl + int(blockIdx.y));
+        } else {
+            ln_pixel_rows<HG>(ln, acc, active, red, xl, tpp, kHeads * vd, pix, hg, jq, v4);
+        }
     }
 }
 
@@ -1120,6 +1128,46 @@ void softmax_lambda(Context &ctx, const float *keys, const float *v, int nb, int
     MH_LAUNCH_CHECK();
 }
 
+namespace {
+
+// Kernel choice of tap_filter (measured on MI355X at the UNet's three sizes):
+// the LDS-staged row-tile kernel with 4 heads per thread and every value
+// channel of its pixels while a block spans 10 or more pixels (its value rows
+// are then staged at most 2.4 times over: 64x64 x 40 59.6 -> 47.2 us); else the
+// per-thread kernel with 4 heads per thread (32x32 x 80: 28.4 us, 16x16 x 160:
+// 18.7 us; the whole-row tile kernel 34.7 / 35.0, on slices of 4 channel quads
+// 36.0 / 32.8 in the step). Tuning: tap_heads "t8" / "t4" forces the tile kernel
+// with 8 / 4 heads per thread, 1, 2, 4 or 8 the per-thread kernel; tap_slice
+// (quads dividing vd / 4) the tile kernel on channel slices of that width.
+struct TapPlan {
+    int tile_hg = 0;  // tile kernel heads per thread, 0: the per-thread kernel
+    int cq = 0;       // tile kernel channel quads per block, 0: all
+};
+
+TapPlan tap_plan(const Context &ctx, int hh, int ww, int vd, bool full_ln) {
+    (void)hh;
+    const int v4 = vd / 4;
+    TapPlan p;
+    const bool forced = ctx.tune.tap_tile >= 0;
+    if (forced) {
+        p.tile_hg = ctx.tune.tap_tile;
+    } else if (std::min(256 / (2 * v4), ww) >= 10) {
+        p.tile_hg = 4;
+    } else if (!full_ln && ctx.tune.tap_slice > 0 && v4 % ctx.tune.tap_slice == 0) {
+        p.tile_hg = 4;
+    }
+    if (p.tile_hg && ctx.tune.tap_slice > 0 && !full_ln && v4 % ctx.tune.tap_slice == 0) p.cq = ctx.tune.tap_slice;
+    if (p.tile_hg && (kHeads / p.tile_hg) * (p.cq ? p.cq : v4) > 256) p = TapPlan{};
+    return p;
+}
+
+}  // namespace
+
+int tap_filter_row_parts(const Context &ctx, int hh, int ww, int vd) {
+    const TapPlan p = tap_plan(ctx, hh, ww, vd, false);
+    return p.tile_hg && p.cq ? (vd / 4) / p.cq : 1;
+}
+
 void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc, const float *residual, float *out,
                 int nb, int hh, int ww, int vd, const LayerNormOut *lno, float2 *row_sums) {
     MH_REQUIRE(vd % 4 == 0, "tap_filter: value width must be a multiple of 4");
@@ -1147,24 +1195,16 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
     // gives the chip about 2048 waves: 4 at 64x64 x 40 channels, 2 at 32x32 x 80,
     // 1 at 16x16 x 160 (batch 2).
     const int v4 = vd / 4;
-    // Default (measured on MI355X at the UNet's three sizes): the LDS-staged
-    // row-tile kernel with 4 heads per thread while a block spans 10 or more
-    // pixels (its value rows are then staged at most 2.4 times over: 64x64 x 40
-    // 59.6 -> 47.2 us), else the per-thread kernel with 4 heads per thread
-    // (32x32 x 80: 28.4 us, 16x16 x 160: 18.7 us; the tile kernel 34.7 / 35.0).
-    // The context's tap_heads tuning forces a variant for A/B runs: "t8" / "t4" the
-    // tile kernel with 8 / 4 heads per thread; 1, 2, 4 or 8 the per-thread kernel.
-    const bool forced = ctx.tune.tap_tile >= 0;
-    int tile_hg = (!forced && std::min(256 / (2 * v4), ww) >= 10) ? 4 : 0;
-    if (forced) tile_hg = ctx.tune.tap_tile;
-    if (tile_hg && (kHeads / tile_hg) * v4 <= 256) {
-        const int tpp = (kHeads / tile_hg) * v4, tx = std::max(1, std::min(256 / tpp, ww));
-        const size_t lds = (size_t(2) * (tx + kWin - 1) * v4 + size_t(2) * tx * (kWin * kHeads / 4)) * 16 +
+    const TapPlan tp = tap_plan(ctx, hh, ww, vd, lno != nullptr);
+    if (tp.tile_hg) {
+        const int tile_hg = tp.tile_hg, cqn = tp.cq ? tp.cq : v4;
+        const int tpp = (kHeads / tile_hg) * cqn, tx = std::max(1, std::min(256 / tpp, ww));
+        const size_t lds = (size_t(2) * (tx + kWin - 1) * cqn + size_t(2) * tx * (kWin * kHeads / 4)) * 16 +
                            (lnk ? size_t(tx) * tpp * sizeof(float2) : 0);
         const int64_t blocks = int64_t(nb) * hh * ceil_div(ww, tx);
+        const dim3 grid(unsigned(blocks), unsigned(v4 / cqn));
         auto go = [&](auto kern) {
-            kern<<<unsigned(blocks), unsigned(tx * tpp), lds, ctx.stream>>>(a_t, v, yc, residual, out, hh, ww, vd, tx,
-                                                                           ln);
+            kern<<<grid, unsigned(tx * tpp), lds, ctx.stream>>>(a_t, v, yc, residual, out, hh, ww, vd, tx, ln, tp.cq);
         };
         if (tile_hg == 8) lnk ? go(tap_filter_tile_kernel<8, true>) : go(tap_filter_tile_kernel<8, false>);
         else lnk ? go(tap_filter_tile_kernel<4, true>) : go(tap_filter_tile_kernel<4, false>);
@@ -1172,7 +1212,7 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
         return;
     }
     int hg = 4;
-    if (forced) {
+    if (ctx.tune.tap_tile >= 0) {
         const int want = ctx.tune.tap_heads;
         if (want == 1 || want == 2 || want == 4 || want == 8) hg = want;
     }

@@ -730,9 +730,9 @@ struct MixTransformer {
         // re-read of h: whole step -29 us EXACT, -36 us FAST).
         const LnFolded lnq = ln1q.view(LN_EPS), lnf = ln3f.view(LN_EPS);
         if (fold == 2) {
-            LnRowPartials st2;
-            st2.part = reinterpret_cast<float2 *>(e.pool.floats(h.px() * 2));
-            st2.per_row = 1;
+            LnRowPartials st2;  // LayerNorm 2's row sums, per_row slices of the channels each
+            st2.per_row = tap_filter_row_parts(e.ctx, h.h, h.w, attn1.k);
+            st2.part = reinterpret_cast<float2 *>(e.pool.floats(h.px() * 2 * st2.per_row));
             if (st1.per_row > 0) {
                 attn1.fwd_add(e, h, h.p, nullptr, &lnq, &st1, st2.part);
             } else {
@@ -743,8 +743,9 @@ struct MixTransformer {
             e.pool.recycle(reinterpret_cast<float *>(st1.part));
             if (xs.n != xr.n) {  // h and its row sums repeated to the batch
                 h = widen(e, h, xr.n);
-                float *w2 = e.pool.floats(h.px() * 2);
-                tile_items(e.ctx, reinterpret_cast<const float *>(st2.part), int64_t(xs.px()) * 2, xr.n, w2);
+                float *w2 = e.pool.floats(h.px() * 2 * st2.per_row);
+                tile_items(e.ctx, reinterpret_cast<const float *>(st2.part), int64_t(xs.px()) * 2 * st2.per_row, xr.n,
+                           w2);
                 e.pool.recycle(reinterpret_cast<float *>(st2.part));
                 st2.part = reinterpret_cast<float2 *>(w2);
             }

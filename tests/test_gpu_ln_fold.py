@@ -227,13 +227,17 @@ def test_cross_lambda_row_sums(ctx, nb, hw, k):
 
 @pytest.mark.parametrize("nb,hh,ww,vd", [(2, 64, 64, 40), (2, 32, 32, 80), (2, 16, 16, 160), (1, 7, 5, 8),
                                          (1, 9, 70, 40)])
-@pytest.mark.parametrize("variant", [None, "t4", "t8", "4", "2"])
-def test_tap_filter_row_sums(ctx, nb, hh, ww, vd, variant, tune):
+@pytest.mark.parametrize("variant,slice_", [(None, None), ("t4", None), ("t8", None), ("4", None), ("2", None),
+                                            (None, "4"), ("t4", "2"), ("t8", "1"), ("t4", "5")])
+def test_tap_filter_row_sums(ctx, nb, hh, ww, vd, variant, slice_, tune):
     """The tap filter's LayerNorm 2 row sums (mh_tap_filter_row_sums) are those
-    of the rows it writes, and writing them changes none of the written bits,
-    in every kernel variant and with the default row split."""
+    of the rows it writes (per channel slice where the kernel slices them), and
+    writing them changes none of the written bits, in every kernel variant and
+    slice width (a width not dividing the row's quads falls back to whole rows)."""
     if variant is not None:
         tune("tap_heads", variant)
+    if slice_ is not None:
+        tune("tap_slice", slice_)
     rng = np.random.default_rng(hh * ww + vd)
     npx = nb * hh * ww
     a = rng.standard_normal((npx, 226, 8)).astype(np.float32)
@@ -242,13 +246,18 @@ def test_tap_filter_row_sums(ctx, nb, hh, ww, vd, variant, tune):
     h = rng.standard_normal((npx, 8 * vd)).astype(np.float32)
     dv = {n: E.DeviceArray.from_numpy(ctx, x) for n, x in dict(a=a, v=v, yc=yc).items()}
     h1, h2 = E.DeviceArray.from_numpy(ctx, h), E.DeviceArray.from_numpy(ctx, h)
-    sums = E.DeviceArray(ctx, (npx, 2))
-    print(f"tap filter row sums {nb}x{hh}x{ww} vd {vd} variant {variant}", flush=True)
+    sums = E.DeviceArray(ctx, (npx * (vd // 4), 2))
+    per_row = ctypes.c_uint32()
+    print(f"tap filter row sums {nb}x{hh}x{ww} vd {vd} variant {variant} slice {slice_}", flush=True)
     E.check(E.lib().mh_tap_filter(ctx.h, dv["a"].ptr, dv["v"].ptr, dv["yc"].ptr, h1.ptr, h1.ptr, nb, hh, ww, vd))
     E.check(E.lib().mh_tap_filter_row_sums(ctx.h, dv["a"].ptr, dv["v"].ptr, dv["yc"].ptr, h2.ptr, h2.ptr, nb, hh,
-                                           ww, vd, sums.ptr))
-    o1, o2, s = h1.numpy(), h2.numpy(), sums.numpy()
+                                           ww, vd, sums.ptr, ctypes.byref(per_row)))
+    o1, o2 = h1.numpy(), h2.numpy()
+    n = per_row.value
+    assert n >= 1 and (vd // 4) % n == 0
+    s = sums.numpy()[: npx * n].reshape(npx, n, 2)
     assert np.array_equal(o1, o2)
-    rows = o1.astype(np.float64)
-    assert np.allclose(s[:, 0], rows.sum(1), rtol=1e-5, atol=1e-2)
-    assert np.allclose(s[:, 1], (rows * rows).sum(1), rtol=1e-5, atol=1e-2)
+    # slice j of a row: value channels [j * vd / n, (j + 1) * vd / n) of every head
+    rows = o1.astype(np.float64).reshape(npx, 8, n, vd // n)
+    assert np.allclose(s[:, :, 0], rows.sum((1, 3)), rtol=1e-5, atol=1e-2)
+    assert np.allclose(s[:, :, 1], (rows * rows).sum((1, 3)), rtol=1e-5, atol=1e-2)

@@ -407,7 +407,7 @@ constexpr int kStageRegs = 4;  // float4 per thread of a staged value / coeffici
 // cq > 0: the block takes the value channel quads [cq * blockIdx.y, + cq) of its
 // pixels only (LayerNorm row sums then per pixel and channel slice, LnOut
 // row_sums [pixels][v4 / cq]; the full LayerNorm needs cq 0, whole rows).
-template <int HG, bool LN>
+template <int HG, bool LN, int JQ = 1>
 __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__restrict__ a_t,
                                                               const float *__restrict__ v, const float *yc,
                                                               const float *res, float *out, int hh, int ww, int vd,
@@ -416,7 +416,7 @@ __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__res
     constexpr int kRowC4 = kWin * kHeads / 4;  // float4 of coefficients per pixel and tap row: 30
     constexpr int NG = kHeads / HG;
     const int v4 = vd >> 2, cqn = cq > 0 ? cq : v4, q0 = cq > 0 ? int(blockIdx.y) * cq : 0;
-    const int tpp = NG * cqn, span = tx + kWin - 1;
+    const int tpp = NG * (cqn / JQ), span = tx + kWin - 1;
     float4 *vls = sh4;                   // [2][span][cqn]
     float4 *cls = sh4 + 2 * span * cqn;  // [2][tx][30]
     const int tiles_x = (ww + tx - 1) / tx;
@@ -425,13 +425,13 @@ __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__res
     const int b = row / hh, y = row - b * hh;
     const int x0 = bx * tx, ntx = min(tx, ww - x0);
     const int xl = int(threadIdx.x) / tpp, r = int(threadIdx.x) - xl * tpp;
-    const int hg = r / cqn, jl = r - hg * cqn, jq = q0 + jl;
+    const int hg = r / (cqn / JQ), jl = (r - hg * (cqn / JQ)) * JQ, jq = q0 + jl;  // JQ quads from jq
     const int x = x0 + xl;
     const bool active = xl < ntx;
     const int64_t pix0 = int64_t(row) * ww + x0, pix = pix0 + xl;
     const float4 *a4 = reinterpret_cast<const float4 *>(a_t);
     const int64_t o4 = pix * (kHeads * v4) + int64_t(hg) * HG * v4 + jq;  // output float4 of head hg*HG
-    float4 acc[HG];
+    float4 acc[JQ * HG];  // acc[u * HG + i]: quad jq + u of head hg * HG + i
     if (active) {
         const float4 *yc4 = reinterpret_cast<const float4 *>(yc);
 #pragma unroll
@@ -439,10 +439,12 @@ __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__res
             const float4 bias = a4[pix * (kTapsB * kHeads / 4) + (kTaps * kHeads) / 4 + hg * (HG / 4) + g];
             const float bb[4] = {bias.x, bias.y, bias.z, bias.w};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float4 c = yc4[o4 + (g * 4 + i) * v4];
-                acc[g * 4 + i] = make_float4(c.x + bb[i], c.y + bb[i], c.z + bb[i], c.w + bb[i]);
-            }
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int u = 0; u < JQ; ++u) {
+                    const float4 c = yc4[o4 + u + (g * 4 + i) * v4];
+                    acc[u * HG + g * 4 + i] = make_float4(c.x + bb[i], c.y + bb[i], c.z + bb[i], c.w + bb[i]);
+                }
         }
     }
     const int ky0 = max(kPad - y, 0), ky1 = min(kWin, hh + kPad - y);
@@ -514,13 +516,17 @@ __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__res
                         const float4 c4 = cr[kx * 2 + g];
                         cf[4 * g] = c4.x, cf[4 * g + 1] = c4.y, cf[4 * g + 2] = c4.z, cf[4 * g + 3] = c4.w;
                     }
-                    const float4 s = vr[kx * cqn];
 #pragma unroll
-                    for (int i = 0; i < HG; ++i) {
-                        acc[i].x = __builtin_fmaf(cf[i], s.x, acc[i].x);
-                        acc[i].y = __builtin_fmaf(cf[i], s.y, acc[i].y);
-                        acc[i].z = __builtin_fmaf(cf[i], s.z, acc[i].z);
-                        acc[i].w = __builtin_fmaf(cf[i], s.w, acc[i].w);
+                    for (int u = 0; u < JQ; ++u) {
+                        const float4 s = vr[kx * cqn + u];
+#pragma unroll
+                        for (int i = 0; i < HG; ++i) {
+                            float4 &a = acc[u * HG + i];
+                            a.x = __builtin_fmaf(cf[i], s.x, a.x);
+                            a.y = __builtin_fmaf(cf[i], s.y, a.y);
+                            a.z = __builtin_fmaf(cf[i], s.z, a.z);
+                            a.w = __builtin_fmaf(cf[i], s.w, a.w);
+                        }
                     }
                 }
             }
@@ -532,20 +538,23 @@ __global__ __launch_bounds__(256) void tap_filter_tile_kernel(const float *__res
         float4 *out4 = reinterpret_cast<float4 *>(out);
         const float4 *res4 = reinterpret_cast<const float4 *>(res);
 #pragma unroll
-        for (int i = 0; i < HG; ++i) {
-            if (res) {
-                const float4 h = res4[o4 + i * v4];
-                acc[i] = make_float4(h.x + acc[i].x, h.y + acc[i].y, h.z + acc[i].z, h.w + acc[i].w);
+        for (int u = 0; u < JQ; ++u)
+#pragma unroll
+            for (int i = 0; i < HG; ++i) {
+                float4 &a = acc[u * HG + i];
+                if (res) {
+                    const float4 h = res4[o4 + u + i * v4];
+                    a = make_float4(h.x + a.x, h.y + a.y, h.z + a.z, h.w + a.w);
+                }
+                out4[o4 + u + i * v4] = a;
             }
-            out4[o4 + i * v4] = acc[i];
-        }
     }
     if constexpr (LN) {
         float *red = reinterpret_cast<float *>(cls + 2 * tx * kRowC4);  // [2 * blockDim.x]
         if (ln.row_sums) {
             const int nsl = v4 / cqn;
-            ln_pixel_sums<HG>(ln, acc, active, red, xl, tpp, r, pix * nsl + int(blockIdx.y));
-        } else {
+            ln_pixel_sums<JQ * HG>(ln, acc, active, red, xl, tpp, r, pix * nsl + int(blockIdx.y));
+        } else if constexpr (JQ == 1) {
             ln_pixel_rows<HG>(ln, acc, active, red, xl, tpp, kHeads * vd, pix, hg, jq, v4);
         }
     }
@@ -1142,6 +1151,7 @@ namespace {
 struct TapPlan {
     int tile_hg = 0;  // tile kernel heads per thread, 0: the per-thread kernel
     int cq = 0;       // tile kernel channel quads per block, 0: all
+    int jq = 1;       // tile kernel channel quads per thread
 };
 
 TapPlan tap_plan(const Context &ctx, int hh, int ww, int vd, bool full_ln) {
@@ -1157,7 +1167,9 @@ TapPlan tap_plan(const Context &ctx, int hh, int ww, int vd, bool full_ln) {
         p.tile_hg = 4;
     }
     if (p.tile_hg && ctx.tune.tap_slice > 0 && !full_ln && v4 % ctx.tune.tap_slice == 0) p.cq = ctx.tune.tap_slice;
-    if (p.tile_hg && (kHeads / p.tile_hg) * (p.cq ? p.cq : v4) > 256) p = TapPlan{};
+    const int cqn = p.cq ? p.cq : v4;
+    if (p.tile_hg && !full_ln && ctx.tune.tap_jq == 2 && cqn % 2 == 0) p.jq = 2;
+    if (p.tile_hg && (kHeads / p.tile_hg) * (cqn / p.jq) > 256) p = TapPlan{};
     return p;
 }
 
@@ -1198,7 +1210,7 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
     const TapPlan tp = tap_plan(ctx, hh, ww, vd, lno != nullptr);
     if (tp.tile_hg) {
         const int tile_hg = tp.tile_hg, cqn = tp.cq ? tp.cq : v4;
-        const int tpp = (kHeads / tile_hg) * cqn, tx = std::max(1, std::min(256 / tpp, ww));
+        const int tpp = (kHeads / tile_hg) * (cqn / tp.jq), tx = std::max(1, std::min(256 / tpp, ww));
         const size_t lds = (size_t(2) * (tx + kWin - 1) * cqn + size_t(2) * tx * (kWin * kHeads / 4)) * 16 +
                            (lnk ? size_t(tx) * tpp * sizeof(float2) : 0);
         const int64_t blocks = int64_t(nb) * hh * ceil_div(ww, tx);
@@ -1206,8 +1218,14 @@ void tap_filter(Context &ctx, const float *a_t, const float *v, const float *yc,
         auto go = [&](auto kern) {
             kern<<<grid, unsigned(tx * tpp), lds, ctx.stream>>>(a_t, v, yc, residual, out, hh, ww, vd, tx, ln, tp.cq);
         };
-        if (tile_hg == 8) lnk ? go(tap_filter_tile_kernel<8, true>) : go(tap_filter_tile_kernel<8, false>);
-        else lnk ? go(tap_filter_tile_kernel<4, true>) : go(tap_filter_tile_kernel<4, false>);
+        if (tp.jq == 2) {
+            if (tile_hg == 8) lnk ? go(tap_filter_tile_kernel<8, true, 2>) : go(tap_filter_tile_kernel<8, false, 2>);
+            else lnk ? go(tap_filter_tile_kernel<4, true, 2>) : go(tap_filter_tile_kernel<4, false, 2>);
+        } else if (tile_hg == 8) {
+            lnk ? go(tap_filter_tile_kernel<8, true>) : go(tap_filter_tile_kernel<8, false>);
+        } else {
+            lnk ? go(tap_filter_tile_kernel<4, true>) : go(tap_filter_tile_kernel<4, false>);
+        }
         MH_LAUNCH_CHECK();
         return;
     }

@@ -228,14 +228,17 @@ def test_cross_lambda_row_sums(ctx, nb, hw, k):
 @pytest.mark.parametrize("nb,hh,ww,vd", [(2, 64, 64, 40), (2, 32, 32, 80), (2, 16, 16, 160), (1, 7, 5, 8),
                                          (1, 9, 70, 40)])
 @pytest.mark.parametrize("variant,slice_", [(None, None), ("t4", None), ("t8", None), ("4", None), ("2", None),
-                                            (None, "4"), ("t4", "2"), ("t8", "1"), ("t4", "5")])
+                                            (None, "4"), ("t4", "2"), ("t8", "1"), ("t4", "5"), ("t4q2", None),
+                                            ("t8q2", None), ("t4q2", "2")])
 def test_tap_filter_row_sums(ctx, nb, hh, ww, vd, variant, slice_, tune):
     """The tap filter's LayerNorm 2 row sums (mh_tap_filter_row_sums) are those
     of the rows it writes (per channel slice where the kernel slices them), and
     writing them changes none of the written bits, in every kernel variant and
     slice width (a width not dividing the row's quads falls back to whole rows)."""
     if variant is not None:
-        tune("tap_heads", variant)
+        tune("tap_heads", variant[:2] if variant.endswith("q2") else variant)
+        if variant.endswith("q2"):
+            tune("tap_jq", 2)
     if slice_ is not None:
         tune("tap_slice", slice_)
     rng = np.random.default_rng(hh * ww + vd)

@@ -50,13 +50,16 @@ def test_softmax_lambda_kernel(ctx, nb, rows, k):
 # 20 x 9); "8"/"4"/"2": the per-thread kernel's variants.
 @pytest.mark.parametrize("nb,hh,ww,vd", [(2, 16, 12, 40), (1, 7, 5, 8), (2, 16, 16, 160), (1, 20, 9, 80),
                                          (1, 9, 70, 40)])
-@pytest.mark.parametrize("heads_per_thread", ["default", "t8", "t4", "8", "4", "2"])
+@pytest.mark.parametrize("heads_per_thread", ["default", "t8", "t4", "8", "4", "2", "t8q2", "t4q2"])
 def test_tap_filter_kernel_bit_exact(ctx, nb, hh, ww, vd, heads_per_thread, tune):
+    """q2: the tile kernel with two value channel quads per thread."""
     tune("tap_split", 1)  # one thread per output: the reference's tap order
     if heads_per_thread == "default":
         tune("tap_heads", None)
     else:
-        tune("tap_heads", heads_per_thread)
+        tune("tap_heads", heads_per_thread[:2] if heads_per_thread.endswith("q2") else heads_per_thread)
+    if heads_per_thread.endswith("q2"):
+        tune("tap_jq", 2)
     rng = np.random.default_rng(hh * ww + vd)
     a = rng.standard_normal((nb, hh * ww, 8, 226)).astype(np.float32)
     v = rng.standard_normal((nb, hh * ww, vd)).astype(np.float32)

@@ -384,6 +384,19 @@ int32_t mh_tap_filter_ln(MhContext *ctx, const float *a_t, const float *v, const
 int32_t mh_lambda_position_coeffs(MhContext *ctx, const float *q, const float *w_aug_t, const float *lambda_t,
                                   uint32_t nb, uint32_t hw, uint32_t k, float *a_t, float *yc);
 
+/* src/unet/lambda.rs:123, 131-137 and 154-185 in one pass: mh_lambda_position_coeffs
+ * (A and yc) followed by mh_tap_filter (vd = k) without writing A or yc, the
+ * position coefficients and the content term being formed where the filter uses
+ * them. q [nb*hh*ww][8][k], w_aug_t [226][k], lambda_t [nb][k][k], v [nb*hh*ww][k],
+ * residual (optional) and out [nb*hh*ww][8*k]; out may alias residual, not q or v.
+ * row_sums (optional, 8-byte aligned): one (sum, sum of squares) pair per out row,
+ * as mh_tap_filter_row_sums writes with one part per row. k must be 40, 80 or 160.
+ * out and row_sums are bit-identical to the two calls' with one thread per output
+ * (the tuning key tap_split = 1). */
+int32_t mh_self_lambda_fused(MhContext *ctx, const float *q, const float *w_aug_t, const float *lambda_t,
+                             const float *v, const float *residual, float *out, uint32_t nb, uint32_t hh, uint32_t ww,
+                             uint32_t k, float *row_sums);
+
 /* src/unet/lambda.rs:276-295 `position_term`: u = yc + (q . E) . V[branch], per
  * element in the reference's order; out = u, or residual + u when residual is
  * given. e [hw][10][k], v_branches [2][10][k], item i using branch br0 + i;

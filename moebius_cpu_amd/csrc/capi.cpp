@@ -776,6 +776,22 @@ int32_t mh_lambda_position_coeffs(MhContext *ctx, const float *q, const float *w
     });
 }
 
+int32_t mh_self_lambda_fused(MhContext *ctx, const float *q, const float *w_aug_t, const float *lambda_t,
+                             const float *v, const float *residual, float *out, uint32_t nb, uint32_t hh, uint32_t ww,
+                             uint32_t k, float *row_sums) {
+    return guard([&] {
+        mh::Context &c = C(ctx);
+        need(q, "q");
+        need(w_aug_t, "w_aug_t");
+        need(lambda_t, "lambda_t");
+        need(v, "v");
+        need(out, "out");
+        if (!mh::lambda_taps_ok(int(k))) mh::fail(mh::kInvalidArgument, "self-lambda position path: k must be 40, 80 or 160");
+        mh::self_lambda_fused(c, q, w_aug_t, lambda_t, v, residual, out, dim(nb, "nb"), dim(hh, "hh"), dim(ww, "ww"),
+                              int(k), reinterpret_cast<float2 *>(row_sums));
+    });
+}
+
 int32_t mh_position_term(MhContext *ctx, const float *q, const float *e, const float *v_branches, uint32_t br0,
                          uint32_t nb, uint32_t hw, uint32_t k, const float *yc, const float *residual, float *out) {
     return guard([&] {

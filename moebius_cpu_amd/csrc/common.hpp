@@ -50,7 +50,7 @@ enum class Precision : uint32_t { Exact = 0, Fast = 1 };
 // (MOEBIUS_HIP_GEMM_PLAN, _GN_IN_MAXC, _DW_TILED, _TAP_HEADS, _CROSS_HEADS,
 // _GN_BLOCKS, _GN_APPLY, _WINO_FUSED, _UP_CONCAT, _LAMBDA_TAPS, _GEMM_LOG,
 // _GEMM_WIDE, _LN_FOLD, _TAP_SPLIT, _GEMM_TIME, _TAPS_ROWS, _CROSS_MFMA, _TAP_SLICE,
-// _TAP_JQ)
+// _TAP_JQ, _TAP_FUSED)
 // when a context is created and changed with set_tuning (mh_context_set_tuning).
 // The defaults are the measured choices; nothing on the hot path reads the
 // environment.
@@ -80,6 +80,8 @@ struct Tuning {
     int cross_mfma = 1;    // cross-lambda: 1 the content term on the matrix cores (head widths 40, 80, 160)
     int tap_slice = 0;     // tap filter: > 0 the tile kernel on value channel slices of this many quads
     int tap_jq = 1;        // tap filter tile kernel: value channel quads per thread (1 or 2)
+    int tap_fused = 1;     // self-lambda coefficients formed inside the tap filter, per head width:
+                           // bit 0 k = 40 (the 64x64 latents), bit 1 k = 80, bit 2 k = 160
 };
 // Sets `key` from its text form (the environment variable's syntax); value NULL
 // or "" restores the default. False for an unknown key or a malformed value.

@@ -227,6 +227,14 @@ int tap_filter_row_parts(const Context &ctx, int hh, int ww, int vd);
 bool lambda_taps_ok(int k);
 void lambda_taps(Context &ctx, const float *q, const float *w_aug_t, const float *lambda_t, int nb, int hw, int k,
                  float *a_t, float *yc);
+// lambda_taps then tap_filter (vd = k, no LayerNorm output) in one kernel that
+// never writes a_t or yc: out [nb*hh*ww][8*k] = (residual +) (Yc + bias tap + 15x15
+// taps of v), bit-identical to the two calls with one thread per output; row_sums
+// (optional): one (sum, sum of squares) pair per out row. self_lambda_fused_ok:
+// the Tuning::tap_fused choice for head width k.
+bool self_lambda_fused_ok(const Context &ctx, int k);
+void self_lambda_fused(Context &ctx, const float *q, const float *w_aug_t, const float *lambda_t, const float *v,
+                       const float *residual, float *out, int nb, int hh, int ww, int k, float2 *row_sums = nullptr);
 // out [nb*hw][8*k] = (residual +) (yc + (q . E) . V[branch]); e [hw][10][k]; v_branches [2][10][k].
 // out may alias yc or residual.
 void position_term(Context &ctx, const float *q, const float *e, const float *v_branches, int br0, int nb, int hw,

@@ -705,6 +705,253 @@ __global__ __launch_bounds__(256) void lambda_taps_kernel(const float *__restric
     }
 }
 
+// The self-lambda's position path in one pass (lambda.rs:123, 131-137 and
+// 154-185): tap_filter_tile_kernel's row tiles, with the coefficients A and the
+// content term Yc formed in the block on the matrix cores from Q, W_aug and
+// lambda_t instead of read back from the [pixel][226][8] and [pixel][8][k]
+// tensors lambda_taps_kernel writes (7.2 KB + 32 k bytes per pixel that would
+// cross HBM twice). Wave w owns the block's pixel pairs w and w + 4 (16 MFMA
+// columns = 2 pixels x 8 heads, their Q rows the B operand, held in registers
+// for the whole block). First the content rows (lambda_t's, 16 at a time) and
+// the bias row (W_aug row 225) go to LDS for the accumulators' start values;
+// then per tap row the A operand is that row's 15 W_aug rows (one per lane row,
+// read through the cache) and the products land in the LDS coefficient rows the
+// tap loop reads, one tap row ahead of it. Each coefficient comes out of
+// lambda_taps_kernel's instruction sequence (K in float4 chunks of 16 by lane
+// group, then the tail) and each output of tap_filter_tile_kernel's tap order,
+// so out and the row sums are bit-identical to those two kernels' (one thread
+// per output). Blocks of 256 threads, tx <= 16 pixels (tx * 4 * k / 4 threads
+// busy in the tap loop); RS: LayerNorm row sums per pixel (LnOut::row_sums).
+template <int NF, int TAIL, bool R16, bool RS>
+__global__ __launch_bounds__(256) void tap_fused_kernel(const float *__restrict__ q,
+                                                        const float *__restrict__ w_aug_t,
+                                                        const float *__restrict__ lam_t,
+                                                        const float *__restrict__ v, const float *res, float *out,
+                                                        int hh, int ww, int tx, LnOut ln) {
+    constexpr int K = 16 * NF + 4 * TAIL, V4 = K / 4;
+    constexpr int HG = 4, NG = kHeads / HG, TPP = NG * V4;  // threads per pixel
+    constexpr int kRowC4 = kWin * kHeads / 4;               // float4 of one pixel's tap-row coefficients
+    constexpr int NBJ = (K + 15) / 16;                      // 16-row blocks of lambda_t
+    extern __shared__ float4 sh4[];
+    const int span = tx + kWin - 1;
+    float4 *vls = sh4;                                             // [2][span][V4]
+    float *cls = reinterpret_cast<float *>(vls + 2 * span * V4);  // [2][tx][15][8]
+    float *ycs = cls + 2 * tx * kRowC4 * 4;                        // [tx][8][K]
+    float *bls = ycs + tx * kHeads * K;                            // [tx][8]
+    float *red = bls + tx * kHeads;                                // row sums: [2 * 256]
+    const int tiles_x = (ww + tx - 1) / tx;
+    const int bx = int(blockIdx.x % unsigned(tiles_x));
+    const int row = int(blockIdx.x / unsigned(tiles_x));  // b * hh + y
+    const int b = row / hh, y = row - b * hh;
+    const int x0 = bx * tx, ntx = min(tx, ww - x0);
+    const int tid = int(threadIdx.x);
+    const int xl = tid / TPP, r = tid - xl * TPP;
+    const int hg = r / V4, jq = r - hg * V4;
+    const int x = x0 + xl;
+    const bool active = xl < ntx;
+    const int64_t pix0 = int64_t(row) * ww + x0, pix = pix0 + xl;
+    // matrix roles: lane (col, g) of wave w; column col = (pixel pc of the pair, head hc)
+    const int lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 15, g = lane >> 4, hc = col & 7, pc = col >> 3;
+    floatx4 bq[2][NF > 0 ? NF : 1];
+    float bt[2][TAIL > 0 ? TAIL : 1];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const int p = 2 * (wave + 4 * s) + pc;
+        const bool pv = p < ntx;
+        const float *qr = q + (pv ? ((pix0 + p) * kHeads + hc) * K : 0);
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            bq[s][f] = pv ? *reinterpret_cast<const floatx4 *>(qr + 16 * f + 4 * g) : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) bq[s][f][t] = op_round<R16>(bq[s][f][t]);
+        }
+#pragma unroll
+        for (int u = 0; u < TAIL; ++u) bt[s][u] = pv ? op_round<R16>(qr[16 * NF + 4 * u + g]) : 0.f;
+    }
+    // One 16-row product for each of this wave's pixel pairs: the A operand is
+    // row `arow` of src (K wide) per lane row, zeros where arow is past rows;
+    // load_a fetches it (ahead of use for the tap rows), products runs the
+    // pairs' MFMA chains, interleaved when the wave has two.
+    struct AOp {
+        floatx4 w[NF > 0 ? NF : 1];
+        float t[TAIL > 0 ? TAIL : 1];
+    };
+    auto load_a = [&](const float *src, int arow, int rows, AOp &o) {
+        const bool av = arow < rows;
+        const float *ar = src + (av ? int64_t(arow) * K : 0);
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            o.w[f] = av ? *reinterpret_cast<const floatx4 *>(ar + 16 * f + 4 * g) : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) o.w[f][t] = op_round<R16>(o.w[f][t]);
+        }
+#pragma unroll
+        for (int u = 0; u < TAIL; ++u) o.t[u] = av ? op_round<R16>(ar[16 * NF + 4 * u + g]) : 0.f;
+    };
+    // The MFMA chains of this wave's two pixel pairs (step i: K chunk f = i / 4,
+    // instruction t = i % 4, then the tail), so they can be spread over other
+    // work; a pair past the row's pixels multiplies zeros and is not stored.
+    constexpr int kSteps = 4 * NF + TAIL;
+    floatx4 pacc[2];
+    auto mfma_step = [&](const AOp &o, int i) {
+        if (i < 4 * NF) {
+            const int f = i >> 2, t = i & 3;
+            pacc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.w[f][t], bq[0][f][t], pacc[0], 0, 0, 0);
+            pacc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.w[f][t], bq[1][f][t], pacc[1], 0, 0, 0);
+        } else {
+            const int u = i - 4 * NF;
+            pacc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.t[u], bt[0][u], pacc[0], 0, 0, 0);
+            pacc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(o.t[u], bt[1][u], pacc[1], 0, 0, 0);
+        }
+    };
+    auto products = [&](const AOp &o) {
+        pacc[0] = pacc[1] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < kSteps; ++i) mfma_step(o, i);
+    };
+    // Content rows j and the bias row into LDS (register v of lane (col, g): row 4 g + v).
+    const float *lamb = lam_t + int64_t(b) * K * K;
+#pragma unroll
+    for (int jb = 0; jb < NBJ; ++jb) {
+        AOp o;
+        load_a(lamb, 16 * jb + col, K, o);
+        products(o);
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int p = 2 * (wave + 4 * s) + pc;
+            if (p >= ntx) continue;
+#pragma unroll
+            for (int vv = 0; vv < 4; ++vv) {
+                const int j = 16 * jb + 4 * g + vv;
+                if (j < K) ycs[(p * kHeads + hc) * K + j] = pacc[s][vv];
+            }
+        }
+    }
+    {
+        AOp o;
+        load_a(w_aug_t, kTaps, kTapsB, o);  // every lane row: W_aug row 225, the bias
+        products(o);
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+        const int p = 2 * (wave + 4 * s) + pc;
+        if (p < ntx && g == 0) bls[p * kHeads + hc] = pacc[s][0];
+    }
+    __syncthreads();
+    float4 acc[HG];
+    if (active) {
+#pragma unroll
+        for (int i = 0; i < HG; ++i) {
+            const int hd = hg * HG + i;
+            const float4 c = *reinterpret_cast<const float4 *>(ycs + (xl * kHeads + hd) * K + 4 * jq);
+            const float bb = bls[xl * kHeads + hd];
+            acc[i] = make_float4(c.x + bb, c.y + bb, c.z + bb, c.w + bb);
+        }
+    }
+    const int ky0 = max(kPad - y, 0), ky1 = min(kWin, hh + kPad - y);
+    const int kx0 = max(kPad - x, 0), kx1 = min(kWin, ww + kPad - x);
+    const float4 *vb = reinterpret_cast<const float4 *>(v) + int64_t(b) * hh * ww * V4;
+    // value rows: registers then LDS, as tap_filter_tile_kernel stages them
+    float4 sv[kStageRegs];
+    auto load_v = [&](int ky) {
+        const int iy = y + ky - kPad;
+#pragma unroll
+        for (int i = 0; i < kStageRegs; ++i) {
+            const int t = tid + i * 256;
+            const int c = t / V4, qd = t - c * V4, ix = x0 - kPad + c;
+            sv[i] = (t < span * V4 && ix >= 0 && ix < ww) ? vb[(int64_t(iy) * ww + ix) * V4 + qd]
+                                                         : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto commit_v = [&](int ky, int buf) {
+        const int iy = y + ky - kPad;
+        float4 *vd4 = vls + buf * span * V4;
+#pragma unroll
+        for (int i = 0; i < kStageRegs; ++i) {
+            const int t = tid + i * 256;
+            if (t < span * V4) vd4[t] = sv[i];
+        }
+        for (int t = tid + kStageRegs * 256; t < span * V4; t += 256) {
+            const int c = t / V4, qd = t - c * V4, ix = x0 - kPad + c;
+            vd4[t] = (ix >= 0 && ix < ww) ? vb[(int64_t(iy) * ww + ix) * V4 + qd] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    // the coefficients of tap row ky (taps 15 ky + kx, lane row kx; row 15 of the
+    // tile is W_aug row 15 ky + 15, computed and dropped) into LDS buffer buf
+    auto put_coeffs = [&](int buf) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            const int p = 2 * (wave + 4 * s) + pc;
+            if (p >= ntx) continue;
+#pragma unroll
+            for (int vv = 0; vv < 4; ++vv) {
+                const int kx = 4 * g + vv;
+                if (kx < kWin) cls[((buf * tx + p) * kWin + kx) * kHeads + hc] = pacc[s][vv];
+            }
+        }
+    };
+    // W_aug rows of the next tap row: loaded one row ahead; their products run
+    // step by step inside the tap loop of the row before and go to LDS after it.
+    AOp wn;
+    load_v(ky0);
+    load_a(w_aug_t, ky0 * kWin + col, kTapsB, wn);
+    products(wn);
+    if (ky0 + 1 < ky1) load_a(w_aug_t, (ky0 + 1) * kWin + col, kTapsB, wn);
+    put_coeffs(0);
+    commit_v(ky0, 0);
+    __syncthreads();
+    for (int ky = ky0; ky < ky1; ++ky) {
+        const int buf = (ky - ky0) & 1;
+        const bool next = ky + 1 < ky1;  // block-uniform
+        if (next) load_v(ky + 1);
+        pacc[0] = pacc[1] = floatx4{0.f, 0.f, 0.f, 0.f};
+        // Tap column kx of row ky, then MFMA step kx of row ky + 1's products:
+        // the matrix unit works beside the FMAs (one step per column, the
+        // steps past column 15 after the loop).
+        const float4 *vr = vls + buf * span * V4 + xl * V4 + jq;
+        const float4 *cr = reinterpret_cast<const float4 *>(cls) + (buf * tx + xl) * kRowC4 + hg;
+#pragma unroll
+        for (int kx = 0; kx < kWin; ++kx) {
+            if (active && kx >= kx0 && kx < kx1) {
+                const float4 c4 = cr[kx * 2];
+                const float cf[4] = {c4.x, c4.y, c4.z, c4.w};
+                const float4 sx = vr[kx * V4];
+#pragma unroll
+                for (int i = 0; i < HG; ++i) {
+                    acc[i].x = __builtin_fmaf(cf[i], sx.x, acc[i].x);
+                    acc[i].y = __builtin_fmaf(cf[i], sx.y, acc[i].y);
+                    acc[i].z = __builtin_fmaf(cf[i], sx.z, acc[i].z);
+                    acc[i].w = __builtin_fmaf(cf[i], sx.w, acc[i].w);
+                }
+            }
+            if (next && kx < kSteps) mfma_step(wn, kx);
+        }
+        if (next) {
+#pragma unroll
+            for (int i = kWin; i < kSteps; ++i) mfma_step(wn, i);
+            if (ky + 2 < ky1) load_a(w_aug_t, (ky + 2) * kWin + col, kTapsB, wn);
+            put_coeffs(buf ^ 1);
+            commit_v(ky + 1, buf ^ 1);
+        }
+        __syncthreads();
+    }
+    if (active) {
+        float4 *out4 = reinterpret_cast<float4 *>(out);
+        const float4 *res4 = reinterpret_cast<const float4 *>(res);
+        const int64_t o4 = pix * (kHeads * V4) + int64_t(hg) * HG * V4 + jq;
+#pragma unroll
+        for (int i = 0; i < HG; ++i) {
+            if (res) {
+                const float4 h = res4[o4 + i * V4];
+                acc[i] = make_float4(h.x + acc[i].x, h.y + acc[i].y, h.z + acc[i].z, h.w + acc[i].w);
+            }
+            out4[o4 + i * V4] = acc[i];
+        }
+    }
+    if constexpr (RS) ln_pixel_sums<HG>(ln, acc, active, red, xl, TPP, r, pix);
+}
+
 // 8-lane dot of src/unet/lambda.rs:297-309 (k a multiple of 8).
 __device__ __forceinline__ float dot8_ref(const float *__restrict__ a, const float *__restrict__ b, int k) {
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -1318,6 +1565,45 @@ void lambda_taps(Context &ctx, const float *q, const float *w_aug_t, const float
     else if (k == 80) r16 ? MH_TAPS(5, 0, true) : MH_TAPS(5, 0, false);
     else r16 ? MH_TAPS(10, 0, true) : MH_TAPS(10, 0, false);
 #undef MH_TAPS
+    MH_LAUNCH_CHECK();
+}
+
+bool self_lambda_fused_ok(const Context &ctx, int k) {
+    const int bit = k == 40 ? 1 : k == 80 ? 2 : k == 160 ? 4 : 0;
+    return (ctx.tune.tap_fused & bit) != 0;
+}
+
+void self_lambda_fused(Context &ctx, const float *q, const float *w_aug_t, const float *lambda_t, const float *v,
+                       const float *residual, float *out, int nb, int hh, int ww, int k, float2 *row_sums) {
+    MH_REQUIRE(lambda_taps_ok(k), "self-lambda position path: k must be 40, 80 or 160");
+    MH_REQUIRE(q && w_aug_t && lambda_t && v && out, "self-lambda position path: q, w_aug_t, lambda_t, v, out needed");
+    MH_REQUIRE(aligned16(q) && aligned16(w_aug_t) && aligned16(lambda_t) && aligned16(v) && aligned16(residual) &&
+                   aligned16(out) && (reinterpret_cast<uintptr_t>(row_sums) & 7) == 0,
+               "self-lambda position path: buffers must be 16-byte aligned (row sums 8-byte)");
+    MH_REQUIRE(out != q && out != v, "self-lambda position path: out must not alias q or v");
+    MH_REQUIRE(nb >= 0 && hh >= 0 && ww >= 0, "self-lambda position path: negative size");
+    const int64_t pix = int64_t(nb) * hh * ww;
+    if (pix == 0) return;
+    LnOut ln;
+    ln.row_sums = row_sums;
+    const int tpp = 2 * (k / 4);  // 4 heads per thread
+    const int tx = std::min(std::min(256 / tpp, ww), 16);
+    const int span = tx + kWin - 1;
+    const size_t lds = size_t(2) * span * (k / 4) * 16 + size_t(2) * tx * kWin * kHeads * 4 +
+                       size_t(tx) * kHeads * k * 4 + size_t(tx) * kHeads * 4 + (row_sums ? 2 * 256 * 4 : 0);
+    const int64_t blocks = int64_t(nb) * hh * ceil_div(ww, tx);
+    MH_REQUIRE(blocks < (int64_t(1) << 31), "self-lambda position path: map too large");
+    auto go = [&](auto kern) {
+        kern<<<unsigned(blocks), 256, lds, ctx.stream>>>(q, w_aug_t, lambda_t, v, residual, out, hh, ww, tx, ln);
+    };
+    const bool r16 = ctx.precision == Precision::Fast, rs = row_sums != nullptr;
+#define MH_FUSED(NF, TAIL)                                                                             \
+    (r16 ? (rs ? go(tap_fused_kernel<NF, TAIL, true, true>) : go(tap_fused_kernel<NF, TAIL, true, false>)) \
+         : (rs ? go(tap_fused_kernel<NF, TAIL, false, true>) : go(tap_fused_kernel<NF, TAIL, false, false>)))
+    if (k == 40) MH_FUSED(2, 2);
+    else if (k == 80) MH_FUSED(5, 0);
+    else MH_FUSED(10, 0);
+#undef MH_FUSED
     MH_LAUNCH_CHECK();
 }
 

@@ -561,6 +561,14 @@ struct SelfLambda {
         float *lam_t = e.pool.floats(int64_t(x.n) * k * k);
         softmax_lambda(e.ctx, kt.p, vt.p, x.n, hw, k, k, lam_t);
         e.pool.recycle(kt);
+        if (!lno && self_lambda_fused_ok(e.ctx, k)) {
+            // A and Yc formed inside the tap filter's row tiles, never written
+            self_lambda_fused(e.ctx, q.p, w_aug_t, lam_t, vt.p, h, h, x.n, x.h, x.w, k, row_sums);
+            e.pool.recycle(lam_t);
+            e.pool.recycle(q);
+            e.pool.recycle(vt);
+            return;
+        }
         DT yc = e.pool.tensor(x.n, x.h, x.w, c);
         // A = Q . W_aug over every pixel and head of the batch, stored [pixel][tap][head],
         // and Yc = Q . lambda_c per item (Q viewed as [(hw*8) x k]), both by one dedicated
@@ -731,7 +739,7 @@ struct MixTransformer {
         const LnFolded lnq = ln1q.view(LN_EPS), lnf = ln3f.view(LN_EPS);
         if (fold == 2) {
             LnRowPartials st2;  // LayerNorm 2's row sums, per_row slices of the channels each
-            st2.per_row = tap_filter_row_parts(e.ctx, h.h, h.w, attn1.k);
+            st2.per_row = self_lambda_fused_ok(e.ctx, attn1.k) ? 1 : tap_filter_row_parts(e.ctx, h.h, h.w, attn1.k);
             st2.part = reinterpret_cast<float2 *>(e.pool.floats(h.px() * 2 * st2.per_row));
             if (st1.per_row > 0) {
                 attn1.fwd_add(e, h, h.p, nullptr, &lnq, &st1, st2.part);

@@ -233,6 +233,63 @@ def test_lambda_position_coeffs_rejects_bad_arguments(ctx):
     assert E.lib().mh_lambda_position_coeffs(ctx.h, q.ptr, w.ptr, w.ptr, 1, 2, 40, out.ptr, None) != 0
 
 
+# The one-pass position path (mh_self_lambda_fused) against the two kernels it
+# replaces, mh_lambda_position_coeffs then the tap filter with one thread per
+# output (tap_split 1, the tile kernel with 4 heads per thread, whose row sums
+# take the same order): the same bits for out and the row sums, with and
+# without a residual, EXACT and FAST. Shapes: the UNet's three levels at batch
+# 2, a partial last row tile with an odd pixel count (70 = 5 x 12 + 10, 17),
+# maps narrower than the window (7 x 5, 1 x 1) and single items.
+@pytest.mark.parametrize("nb,hh,ww,k", [(2, 64, 64, 40), (2, 32, 32, 80), (2, 16, 16, 160), (1, 9, 70, 40),
+                                        (1, 20, 9, 80), (1, 7, 5, 40), (3, 1, 1, 160), (1, 5, 17, 40)])
+@pytest.mark.parametrize("fast", [False, True])
+def test_self_lambda_fused_bit_exact(ctx, nb, hh, ww, k, fast, tune):
+    tune("tap_split", 1)
+    tune("tap_heads", "t4")
+    rng = np.random.default_rng(hh * ww + k + nb)
+    npx = nb * hh * ww
+    q = rng.standard_normal((npx, 8, k)).astype(np.float32)
+    w = (rng.standard_normal((226, k)) * 0.3).astype(np.float32)
+    lam_t = (rng.standard_normal((nb, k, k)) * 0.3).astype(np.float32)
+    v = rng.standard_normal((npx, k)).astype(np.float32)
+    h = rng.standard_normal((npx, 8 * k)).astype(np.float32)
+    qd, wd, ld, vd_ = D(ctx, q), D(ctx, w), D(ctx, lam_t), D(ctx, v)
+    a, yc = E.DeviceArray(ctx, (npx, 226, 8)), E.DeviceArray(ctx, (npx, 8, k))
+    ref_h, got_h = D(ctx, h), D(ctx, h)
+    ref_o, got_o = E.DeviceArray(ctx, (npx, 8 * k)), E.DeviceArray(ctx, (npx, 8 * k))
+    ref_s, got_s = E.DeviceArray(ctx, (npx * k // 4, 2)), E.DeviceArray(ctx, (npx, 2))
+    per_row = ctypes.c_uint32()
+    print(f"self-lambda fused {nb}x{hh}x{ww} k {k} fast={fast}", flush=True)
+    ctx.set_precision(fast)
+    try:
+        E.check(E.lib().mh_lambda_position_coeffs(ctx.h, qd.ptr, wd.ptr, ld.ptr, nb, hh * ww, k, a.ptr, yc.ptr))
+        E.check(E.lib().mh_tap_filter_row_sums(ctx.h, a.ptr, vd_.ptr, yc.ptr, ref_h.ptr, ref_h.ptr, nb, hh, ww, k,
+                                               ref_s.ptr, ctypes.byref(per_row)))
+        E.check(E.lib().mh_tap_filter(ctx.h, a.ptr, vd_.ptr, yc.ptr, None, ref_o.ptr, nb, hh, ww, k))
+        E.check(E.lib().mh_self_lambda_fused(ctx.h, qd.ptr, wd.ptr, ld.ptr, vd_.ptr, got_h.ptr, got_h.ptr, nb, hh, ww,
+                                             k, got_s.ptr))
+        E.check(E.lib().mh_self_lambda_fused(ctx.h, qd.ptr, wd.ptr, ld.ptr, vd_.ptr, None, got_o.ptr, nb, hh, ww, k,
+                                             None))
+    finally:
+        ctx.set_precision(False)
+    assert per_row.value == 1
+    assert np.array_equal(got_h.numpy(), ref_h.numpy())
+    assert np.array_equal(got_s.numpy(), ref_s.numpy()[:npx])
+    assert np.array_equal(got_o.numpy(), ref_o.numpy())
+
+
+def test_self_lambda_fused_rejects_bad_arguments(ctx):
+    q = E.DeviceArray(ctx, (2, 8, 120))
+    w = E.DeviceArray(ctx, (226, 120))
+    lam = E.DeviceArray(ctx, (1, 120, 120))
+    v = E.DeviceArray(ctx, (2, 120))
+    out = E.DeviceArray(ctx, (2, 8 * 120))
+    assert E.lib().mh_self_lambda_fused(ctx.h, q.ptr, w.ptr, lam.ptr, v.ptr, None, out.ptr, 1, 1, 2, 120, None) != 0
+    # out aliasing q
+    assert E.lib().mh_self_lambda_fused(ctx.h, q.ptr, w.ptr, lam.ptr, v.ptr, None, q.ptr, 1, 1, 2, 40, None) != 0
+    assert E.lib().mh_self_lambda_fused(ctx.h, q.ptr, None, lam.ptr, v.ptr, None, out.ptr, 1, 1, 2, 40, None) != 0
+
+
 @pytest.mark.parametrize("br0,nb,k", [(0, 2, 40), (1, 1, 80), (0, 2, 160)])
 def test_position_term_kernel_bit_exact(ctx, br0, nb, k):
     hw = 37
@@ -412,6 +469,23 @@ def test_unet_up_path_two_inputs_is_bit_exact(ctx, gnet, fast, cfg, tune):
     finally:
         ctx.set_precision(False)
     assert np.array_equal(cat, two)
+
+
+@pytest.mark.parametrize("fast", [False, True])
+def test_unet_fused_self_lambda_is_bit_exact(ctx, gnet, fast, tune):
+    """The 64x64 level's self-lambda with its position coefficients and content
+    term formed inside the tap filter (tap_fused 1, the default) gives the bits of
+    writing them first (tap_fused 0): both take one thread per output there."""
+    inp = U.unet_input(seed=5013)
+    ctx.set_precision(fast)
+    try:
+        tune("tap_fused", "0")
+        apart = gnet.forward_host(inp.x, inp.timestep, cfg=True)
+        tune("tap_fused", "1")
+        fused = gnet.forward_host(inp.x, inp.timestep, cfg=True)
+    finally:
+        ctx.set_precision(False)
+    assert np.array_equal(apart, fused)
 
 
 @pytest.mark.parametrize("fast", [False, True])

@@ -183,6 +183,20 @@ __global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__res
     const bool sec = x2 && q0 >= cv1;
     const float4 *xs = sec ? x2 : x;
     const int xld = x2 ? (sec ? cv - cv1 : cv1) : cv, xq0 = sec ? q0 - cv1 : q0;
+    // A thread stages one channel quad (threadIdx.x % kDwCQ, 256 being a
+    // multiple of kDwCQ) for every pixel it loads: its prologue scale/shift per
+    // part are loaded first, with the tile's loads, not per staged value.
+    const int sq = threadIdx.x % kDwCQ;
+    float4 psc[PARTS], psh[PARTS];
+#pragma unroll
+    for (int part = 0; part < PARTS; ++part) {
+        psc[part] = psh[part] = V::zero();
+        if (PRO && q0 + sq < co_v) {
+            const size_t qi = size_t(b) * cv + q0 + sq + part * co_v;
+            psc[part] = reinterpret_cast<const float4 *>(pro.scale)[qi];
+            psh[part] = reinterpret_cast<const float4 *>(pro.shift)[qi];
+        }
+    }
     float4 v[PER];
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
@@ -194,6 +208,20 @@ __global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__res
         v[i] = V::zero();
         if (idx < TOTAL && q0 + qq < co_v && iy >= 0 && iy < h && ix >= 0 && ix < w)
             v[i] = xs[(size_t(b) * h + iy) * size_t(w) * xld + size_t(ix) * xld + xq0 + qq + part * co_v];
+    }
+    // The block's 9 taps and bias per quad and part, staged in LDS beside the
+    // tile (their loads in flight with the tile's), so the products below read
+    // them from LDS instead of waiting on L2 once per tap row.
+    __shared__ float4 wts[PARTS][10][kDwCQ];
+    float4 wv = V::zero();
+    const int wtid = int(threadIdx.x);
+    if (wtid < PARTS * 10 * kDwCQ) {
+        const int wp = wtid / (10 * kDwCQ), wr = wtid - wp * (10 * kDwCQ);
+        const int tap = wr / kDwCQ, wq = wr - tap * kDwCQ;
+        if (q0 + wq < co_v) {
+            const int qw = q0 + wq + wp * co_v;
+            wv = tap < 9 ? wt[tap * cv + qw] : bias[qw];
+        }
     }
     const int qq = threadIdx.x % kDwCQ, g = threadIdx.x / kDwCQ;
     const int r = g / (kDwTW / 4), c0 = (g % (kDwTW / 4)) * 4;
@@ -214,18 +242,19 @@ __global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__res
             if (PRO) {
                 const int iy = oy0 - 1 + pix / (kDwTW + 2), ix = ox0 - 1 + pix % (kDwTW + 2);
                 if (q0 + pq < co_v && iy >= 0 && iy < h && ix >= 0 && ix < w) {
-                    const int qin = q0 + pq + ip * co_v;
-                    v[i] = V::fma(v[i], reinterpret_cast<const float4 *>(pro.scale)[size_t(b) * cv + qin],
-                                  reinterpret_cast<const float4 *>(pro.shift)[size_t(b) * cv + qin]);
+                    v[i] = V::fma(v[i], psc[ip], psh[ip]);  // pq == sq: this thread's quad
                     if (pro.silu) v[i] = V::silu(v[i]);
                 }
             }
             tile[pix][pq] = v[i];
         }
+        if (part == 0 && wtid < PARTS * 10 * kDwCQ) {
+            const int wp = wtid / (10 * kDwCQ), wr = wtid - wp * (10 * kDwCQ);
+            wts[wp][wr / kDwCQ][wr % kDwCQ] = wv;
+        }
         __syncthreads();
         if (active) {
-            const int qw = q + part * co_v;
-            const float4 bv = bias[qw];
+            const float4 bv = wts[part][9][qq];
 #pragma unroll
             for (int j = 0; j < 4; ++j) acc[part][j] = bv;
 #pragma unroll
@@ -235,8 +264,8 @@ __global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__res
                 float4 win[6];
 #pragma unroll
                 for (int j = 0; j < 6; ++j) win[j] = tile[(r + ky) * (kDwTW + 2) + c0 + j][qq];
-                const float4 w0 = wt[(ky * 3 + 0) * cv + qw], w1 = wt[(ky * 3 + 1) * cv + qw],
-                             w2 = wt[(ky * 3 + 2) * cv + qw];
+                const float4 w0 = wts[part][ky * 3 + 0][qq], w1 = wts[part][ky * 3 + 1][qq],
+                             w2 = wts[part][ky * 3 + 2][qq];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     acc[part][j] = V::fma(w0, win[j], acc[part][j]);

@@ -1244,10 +1244,10 @@ __global__ __launch_bounds__(NT) void cross_lambda_mfma_kernel(const float *__re
                                                                 const float *res, float *out,
                                                                 float2 *__restrict__ row_sums) {
     constexpr int K = 16 * NF + 4 * TAIL, K4 = K / 4, NCB = (K + 15) / 16, RB = (P + 1) / 2, TASKS = RB * NCB;
-    constexpr int QF4 = P * kHeads * K4, EF4 = P * kTokens * K4, SF4 = QF4 + EF4;
+    constexpr int QF4 = P * kHeads * K4, EF4 = P * kTokens * K4, VF4 = kTokens * K4, SF4 = QF4 + EF4 + VF4;
     constexpr int PER = (SF4 + NT - 1) / NT;
     static_assert(K % 8 == 0, "8-lane dots over whole chunks");
-    __shared__ float4 stage[SF4];  // q [P][8][K], then E [P][10][K]
+    __shared__ float4 stage[SF4];  // q [P][8][K], then E [P][10][K], then the branch's V [10][K]
     __shared__ float bm[P][kHeads][kTokens];
     __shared__ float2 part[P][NCB][2];
     const int item = int(blockIdx.y);
@@ -1258,6 +1258,7 @@ __global__ __launch_bounds__(NT) void cross_lambda_mfma_kernel(const float *__re
     {
         const float4 *q4 = reinterpret_cast<const float4 *>(q) + pix0 * (kHeads * K4);
         const float4 *e4 = reinterpret_cast<const float4 *>(e) + int64_t(p0) * (kTokens * K4);
+        const float4 *v4 = reinterpret_cast<const float4 *>(vbr) + int64_t(br) * VF4;
         float4 r[PER];
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
@@ -1265,8 +1266,10 @@ __global__ __launch_bounds__(NT) void cross_lambda_mfma_kernel(const float *__re
             r[i] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (t < QF4) {
                 if (t / (kHeads * K4) < np) r[i] = q4[t];
-            } else if (t < SF4) {
+            } else if (t < QF4 + EF4) {
                 if ((t - QF4) / (kTokens * K4) < np) r[i] = e4[t - QF4];
+            } else if (t < SF4) {
+                r[i] = v4[t - QF4 - EF4];
             }
         }
 #pragma unroll
@@ -1278,6 +1281,7 @@ __global__ __launch_bounds__(NT) void cross_lambda_mfma_kernel(const float *__re
     __syncthreads();
     const float *qs = reinterpret_cast<const float *>(stage);
     const float *es = qs + QF4 * 4;
+    const float *vs = es + EF4 * 4;
     // phase 1: B[p][h][m] = q_h . E[n][m] (the reference's 8-lane dot)
     for (int t = threadIdx.x; t < P * kHeads * kTokens; t += blockDim.x) {
         const int p = t / (kHeads * kTokens), hm = t - p * (kHeads * kTokens);
@@ -1288,13 +1292,21 @@ __global__ __launch_bounds__(NT) void cross_lambda_mfma_kernel(const float *__re
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nwaves = int(blockDim.x) >> 6;
     const int col = lane & 15, g = lane >> 4;
     const float *lb = lam + int64_t(br) * K * K;
-    const float *vb = vbr + int64_t(br) * kTokens * K;
     for (int task = wave; task < TASKS; task += nwaves) {
         const int rb = task / NCB, cb = task - rb * NCB;
         const int pa = 2 * rb + (col >> 3), ha = col & 7;  // this lane's A row: pixel, head
         const float *qa = qs + (min(pa, P - 1) * kHeads + ha) * K;  // (rows past np read staged zeros)
         const int jb = 16 * cb + col;                              // this lane's B column
         const bool bv = jb < K;
+        // epilogue: lane (col, g) holds rows 4g..4g+3 (one pixel, heads 4(g&1)..+3) of column jb;
+        // its residuals load with the task's lambda_c values, before the products
+        const int pd = 2 * rb + (g >> 1);
+        const bool ok = pd < np && bv;
+        const int64_t obase = ((pix0 + pd) * kHeads + 4 * (g & 1)) * K + jb;
+        float rv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (ok && res)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) rv[v] = res[obase + v * K];
         float bf[NF > 0 ? NF : 1][4], bt[TAIL > 0 ? TAIL : 1];
 #pragma unroll
         for (int f = 0; f < NF; ++f)
@@ -1314,23 +1326,19 @@ __global__ __launch_bounds__(NT) void cross_lambda_mfma_kernel(const float *__re
 #pragma unroll
         for (int u = 0; u < TAIL; ++u)
             acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[16 * NF + 4 * u + g], bt[u], acc, 0, 0, 0);
-        // epilogue: lane (col, g) holds rows 4g..4g+3 (one pixel, heads 4(g&1)..+3) of column jb
-        const int pd = 2 * rb + (g >> 1);
-        const bool ok = pd < np && bv;
         float ls = 0.f, lq = 0.f;
         if (ok) {
-            const int64_t pix = pix0 + pd;
-            float vv[kTokens];  // V[m][jb], read once for the four rows (out may alias nothing read here)
+            float vv[kTokens];  // V[m][jb], read once for the four rows
 #pragma unroll
-            for (int m = 0; m < kTokens; ++m) vv[m] = vb[m * K + jb];
+            for (int m = 0; m < kTokens; ++m) vv[m] = vs[m * K + jb];
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int h = 4 * (g & 1) + v;
                 float o = acc[v];
 #pragma unroll
                 for (int m = 0; m < kTokens; ++m) o = __builtin_fmaf(bm[pd][h][m], vv[m], o);
-                const int64_t idx = (pix * kHeads + h) * K + jb;
-                const float u = res ? res[idx] + o : o;
+                const int64_t idx = obase + v * K;
+                const float u = res ? rv[v] + o : o;
                 out[idx] = u;
                 ls += u;
                 lq = __builtin_fmaf(u, u, lq);

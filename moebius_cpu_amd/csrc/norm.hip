@@ -113,6 +113,16 @@ __global__ __launch_bounds__(kFinThreads) void gn_finalize_kernel(const float *_
     const int g = blockIdx.x, b = blockIdx.y;
     const int cg = c / groups;
     const int total = nchunks * cg;
+    // This thread's first channel's parameters, loaded before the fold so their
+    // latency overlaps it instead of following the reduction.
+    const int j0 = int(threadIdx.x);
+    float g0 = 0.f, b0 = 0.f, a0 = 0.f;
+    if (j0 < cg) {
+        const int ch = g * cg + j0;
+        g0 = gamma[ch];
+        b0 = beta[ch];
+        if (add) a0 = add[size_t(b) * add_ld + ch];
+    }
     const float *pb = part + size_t(b) * nchunks * c * 2 + size_t(g) * cg * 2;
     const bool fold = part_rows > 0 && add;
     const double r = double(part_rows);
@@ -173,10 +183,11 @@ __global__ __launch_bounds__(kFinThreads) void gn_finalize_kernel(const float *_
     const double rstd = 1.0 / sqrt(var + double(eps));
     for (int j = threadIdx.x; j < cg; j += kFinThreads) {
         const int ch = g * cg + j;
-        const double sc = rstd * double(gamma[ch]);
-        const double pre = add ? double(add[size_t(b) * add_ld + ch]) : 0.0;
+        const bool first = j == j0;
+        const double sc = rstd * double(first ? g0 : gamma[ch]);
+        const double pre = add ? double(first ? a0 : add[size_t(b) * add_ld + ch]) : 0.0;
         scale[size_t(b) * c + ch] = float(sc);
-        shift[size_t(b) * c + ch] = float(double(beta[ch]) + (pre - mean) * sc);
+        shift[size_t(b) * c + ch] = float(double(first ? b0 : beta[ch]) + (pre - mean) * sc);
     }
 }
 

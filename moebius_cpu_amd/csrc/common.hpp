@@ -46,11 +46,17 @@ struct Error : std::runtime_error {
 
 enum class Precision : uint32_t { Exact = 0, Fast = 1 };
 
+// A GEMM tiling forced for every GEMM of one shape (Tuning::gemm_shape_plan).
+struct ShapePlan {
+    int m = 0, n = 0, k = 0;
+    int bm = 0, bn = 0, splits = 0, wm = 2, wn = 2, wk = 1, pipe = 0, bk = 32;
+};
+
 // Tuning overrides for A/B runs and tests, read once from the environment
 // (MOEBIUS_HIP_GEMM_PLAN, _GN_IN_MAXC, _DW_TILED, _TAP_HEADS, _CROSS_HEADS,
 // _GN_BLOCKS, _GN_APPLY, _WINO_FUSED, _UP_CONCAT, _LAMBDA_TAPS, _GEMM_LOG,
 // _GEMM_WIDE, _LN_FOLD, _TAP_SPLIT, _GEMM_TIME, _TAPS_ROWS, _CROSS_MFMA, _TAP_SLICE,
-// _TAP_JQ, _TAP_FUSED)
+// _TAP_JQ, _TAP_FUSED, _GEMM_SHAPE_PLAN)
 // when a context is created and changed with set_tuning (mh_context_set_tuning).
 // The defaults are the measured choices; nothing on the hot path reads the
 // environment.
@@ -80,6 +86,10 @@ struct Tuning {
     int cross_mfma = 1;    // cross-lambda: 1 the content term on the matrix cores (head widths 40, 80, 160)
     int tap_slice = 0;     // tap filter: > 0 the tile kernel on value channel slices of this many quads
     int tap_jq = 1;        // tap filter tile kernel: value channel quads per thread (1 or 2)
+    // gemm_shape_plan: "M,N,K,bm,bn,splits[,wm,wn,wk[,pipe[,bk]]]" entries joined by ';'
+    // (at most 8), each forcing the tiling of the GEMMs of that shape as gemm_plan does for all
+    ShapePlan shape_plans[8];
+    int n_shape_plans = 0;
     int tap_fused = 1;     // self-lambda coefficients formed inside the tap filter, per head width:
                            // bit 0 k = 40 (the 64x64 latents), bit 1 k = 80, bit 2 k = 160
 };

@@ -1,4 +1,5 @@
 // Context, workspace and error plumbing.
+#include <algorithm>
 #include <atomic>
 #include <cstdio>
 #include <cstdlib>
@@ -84,6 +85,27 @@ bool set_tuning(Tuning &t, const char *key, const char *value) {
         t.gemm_wm = wm, t.gemm_wn = wn, t.gemm_wk = wk, t.gemm_pipe = pipe, t.gemm_bk = bk;
         return true;
     }
+    if (k == "gemm_shape_plan") {
+        t.n_shape_plans = 0;
+        if (clear) return true;
+        size_t pos = 0;
+        while (pos <= v.size()) {
+            const size_t end = std::min(v.find(';', pos), v.size());
+            const std::string e = v.substr(pos, end - pos);
+            pos = end + 1;
+            if (e.empty()) continue;
+            ShapePlan sp;
+            const int got = std::sscanf(e.c_str(), "%d,%d,%d,%d,%d,%d,%d,%d,%d,%d,%d", &sp.m, &sp.n, &sp.k, &sp.bm,
+                                        &sp.bn, &sp.splits, &sp.wm, &sp.wn, &sp.wk, &sp.pipe, &sp.bk);
+            if ((got != 6 && got < 9) || t.n_shape_plans >= 8 || sp.splits < 1 || sp.wm < 1 || sp.wn < 1 ||
+                sp.wk < 1 || sp.pipe < 0 || sp.pipe > 1 || (sp.bk != 16 && sp.bk != 32)) {
+                t.n_shape_plans = 0;
+                return false;
+            }
+            t.shape_plans[t.n_shape_plans++] = sp;
+        }
+        return true;
+    }
     if (k == "gn_in_maxc") return to_int(t.gn_in_maxc, -1);
     if (k == "dw_tiled") return to_int(t.dw_tiled, 1);
     if (k == "cross_heads") return to_int(t.cross_heads, 0);
@@ -141,6 +163,7 @@ Context::Context(int dev) : device(dev) {
                                               {"MOEBIUS_HIP_TAP_SLICE", "tap_slice"},
                                               {"MOEBIUS_HIP_TAP_JQ", "tap_jq"},
                                               {"MOEBIUS_HIP_TAP_FUSED", "tap_fused"},
+                                              {"MOEBIUS_HIP_GEMM_SHAPE_PLAN", "gemm_shape_plan"},
                                               {"MOEBIUS_HIP_LN_FOLD", "ln_fold"},
                                               {"MOEBIUS_HIP_TAP_SPLIT", "tap_split"}};
     for (const auto &kv : env_keys)

@@ -274,13 +274,13 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
 //  - implicit-GEMM convs: 64x64 tiles, K split up to 4 ways while each split
 //    keeps 10 or more K tiles (every UNet 3x3 conv: 15-30% faster than unsplit);
 //  - a few rows (the time-embedding linears): 32x32;
-//  - wide outputs (N >= 2048) with 10+ K tiles: 128x128, split in 2 when the
-//    grid is under one tile per CU (the MixFFN inverted 1x1 at 32^2 and 16^2);
 //  - long K (25+ tiles) on small grids: 64x64 with K split up to 4 ways;
 //  - otherwise 64x64, or 32x32 when 64x64 leaves a quarter of the CUs idle.
+// (The wide MixFFN inverted 1x1s, 2048x3200x640 and 512x6400x1280, had 128x128
+// tiles from those sweeps; timed in the UNet step, each with every tiling in
+// turn, 64x64 is faster: the FAST step 13 and 25 us shorter.)
 inline Plan plan_h16(int M, int N, int K, int cus, bool dense) {
     const int ktiles = int(ceil_div(K, BKH));
-    const int64_t t128 = ceil_div(M, 128) * ceil_div(N, 128);
     const int64_t t64 = ceil_div(M, 64) * ceil_div(N, 64);
     auto plan = [&](int bm, int want) {
         want = std::max(1, std::min(want, ktiles));
@@ -290,8 +290,6 @@ inline Plan plan_h16(int M, int N, int K, int cus, bool dense) {
     };
     if (!dense) return plan(64, t64 >= 2 * int64_t(cus) ? 1 : std::min(4, ktiles / 10));
     if (M <= 32) return plan(32, 1);
-    if (ktiles >= 10 && N >= 2048 && 2 * t128 >= int64_t(cus))
-        return plan(128, t128 >= int64_t(cus) || ktiles < 20 ? 1 : 2);
     if (ktiles >= 25 && t64 < 2 * int64_t(cus)) return plan(64, int(std::min<int64_t>(4, ceil_div(2 * cus, t64))));
     if (4 * t64 < 3 * int64_t(cus)) return plan(32, 1);
     return plan(64, 1);
@@ -350,8 +348,9 @@ template <int MODE, int PRO, bool F16, bool BVEC>
 void launch_tiles_h16(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
     Plan pl = plan_h16(p.M, p.N, p.K, int(ceil_div(ctx.cu_count, batch)), MODE <= kDenseScalar);
     // The context's gemm_plan tuning forces the tiling, as for the f32 kernel.
-    if (ctx.tune.gemm_splits > 0) {
-        const int bm = ctx.tune.gemm_bm, bn = ctx.tune.gemm_bn, sp = ctx.tune.gemm_splits;
+    ShapePlan fp;
+    if (forced_plan(ctx.tune, p.M, p.N, p.K, fp)) {
+        const int bm = fp.bm, bn = fp.bn, sp = fp.splits;
         if (bm == bn && (bm == 32 || bm == 64 || bm == 128)) {
             const int ktiles = int(ceil_div(p.K, BKH));
             const int per = int(ceil_div(ktiles, sp));

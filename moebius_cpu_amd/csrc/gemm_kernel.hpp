@@ -1375,6 +1375,22 @@ void launch_wide(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi, in
     }
 }
 
+// The tiling the context's tuning forces on a GEMM of this shape: its
+// gemm_shape_plan entry, else gemm_plan; false when neither applies.
+inline bool forced_plan(const Tuning &t, int M, int N, int K, ShapePlan &f) {
+    for (int i = 0; i < t.n_shape_plans; ++i) {
+        const ShapePlan &s = t.shape_plans[i];
+        if (s.m == M && s.n == N && s.k == K) {
+            f = s;
+            return true;
+        }
+    }
+    if (t.gemm_splits <= 0) return false;
+    f.bm = t.gemm_bm, f.bn = t.gemm_bn, f.splits = t.gemm_splits;
+    f.wm = t.gemm_wm, f.wn = t.gemm_wn, f.wk = t.gemm_wk, f.pipe = t.gemm_pipe, f.bk = t.gemm_bk;
+    return true;
+}
+
 template <int MODE, int PRO, bool F16, bool BVEC>
 void launch_tiles(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
     Plan pl = plan_for(p.M, p.N, p.K, int(ceil_div(ctx.cu_count, batch)), MODE <= kDenseScalar);
@@ -1387,10 +1403,10 @@ void launch_tiles(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
     // The context's gemm_plan tuning ("bm,bn,splits[,wm,wn,wk]") forces the tiling
     // (tuning and A/B runs), as MOEBIUS_GEMM selects the CPU engine's GEMM backend
     // (src/engine/gemm.rs:57-60).
-    if (ctx.tune.gemm_splits > 0) {
-        const int bm = ctx.tune.gemm_bm, bn = ctx.tune.gemm_bn, sp = ctx.tune.gemm_splits;
-        Plan f{bm, bn, 1, p.K, ctx.tune.gemm_wm, ctx.tune.gemm_wn, ctx.tune.gemm_wk, ctx.tune.gemm_pipe,
-               ctx.tune.gemm_bk};
+    ShapePlan fp;
+    if (forced_plan(ctx.tune, p.M, p.N, p.K, fp)) {
+        const int bm = fp.bm, bn = fp.bn, sp = fp.splits;
+        Plan f{bm, bn, 1, p.K, fp.wm, fp.wn, fp.wk, fp.pipe, fp.bk};
         const bool square = (bm == 32 || bm == 64 || bm == 128) && (bn == 32 || bn == 64 || bn == 128) &&
                             (bm == 32) == (bn == 32) && f.wm == 2 && f.wn == 2 && f.wk == 1 && !f.pipe &&
                             f.bk == BK;

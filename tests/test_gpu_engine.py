@@ -259,6 +259,36 @@ def test_conv1x1_every_tiling(ctx, plan, c_out, tune):
     assert max_abs_rel(got, want) <= F32_TOL
 
 
+def test_gemm_shape_plan_forces_one_shape(ctx, tune):
+    """gemm_shape_plan forces the tiling of the GEMMs of its M x N x K only: the
+    same bits as gemm_plan forcing that tiling on every GEMM, and the planner's
+    bits for a shape it does not name."""
+    rng = np.random.default_rng(11)
+    n, h, w, c, c_out = 2, 9, 11, 200, 96
+    x = rng.standard_normal((n, h, w, c)).astype(np.float32)
+    wt = (rng.standard_normal((c_out, c)) / np.sqrt(c)).astype(np.float32)
+    b = (rng.standard_normal(c_out) * 0.1).astype(np.float32)
+    conv = E.Conv1x1(ctx, c, c_out, E.Param(ctx, wt), b)
+    xd = E.Tensor.from_numpy(ctx, x)
+
+    def run():
+        y = E.Tensor(ctx)
+        conv.forward(xd, y)
+        return y.numpy()
+
+    planner = run()
+    tune("gemm_plan", "64,64,2")
+    forced = run()
+    tune("gemm_plan", None)
+    tune("gemm_shape_plan", f"{n * h * w},{c_out},{c},64,64,2")
+    assert np.array_equal(run(), forced)
+    tune("gemm_shape_plan", f"{n * h * w},{c_out},{c + 4},64,64,2;1,2,3,32,32,1")
+    assert np.array_equal(run(), planner)
+    with pytest.raises(RuntimeError):
+        ctx.set_tuning("gemm_shape_plan", "198,96,200,64,64")
+    assert max_abs_rel(forced, oracle.conv1x1(x, wt, b)) <= F32_TOL
+
+
 # ---- tests/kernels.rs:233-265: the fused GN prologue, padding stays zero
 @pytest.mark.parametrize("n,h,w,ci,groups,co", [(2, 7, 9, 40, 8, 24), (2, 37, 23, 768, 32, 16)])
 @pytest.mark.parametrize("up", [False, True])

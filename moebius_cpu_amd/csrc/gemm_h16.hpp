@@ -275,6 +275,10 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
 //    keeps 10 or more K tiles (every UNet 3x3 conv: 15-30% faster than unsplit);
 //  - a few rows (the time-embedding linears): 32x32;
 //  - long K (25+ tiles) on small grids: 64x64 with K split up to 4 ways;
+//  - batched products of 512+ rows on 32 CUs or fewer per item (the 16-plane
+//    Winograd GEMMs of the upsample convs, 16 x 512x1280x1280 and 16 x
+//    2048x640x640): 128x128, half the operand traffic of 64x64 (140 and 129 ->
+//    125 us per launch, FAST step 5.042 -> 5.021 ms);
 //  - otherwise 64x64, or 32x32 when 64x64 leaves a quarter of the CUs idle.
 // (The wide MixFFN inverted 1x1s, 2048x3200x640 and 512x6400x1280, had 128x128
 // tiles from those sweeps; timed in the UNet step, each with every tiling in
@@ -290,6 +294,7 @@ inline Plan plan_h16(int M, int N, int K, int cus, bool dense) {
     };
     if (!dense) return plan(64, t64 >= 2 * int64_t(cus) ? 1 : std::min(4, ktiles / 10));
     if (M <= 32) return plan(32, 1);
+    if (cus <= 32 && M >= 512 && N >= 512 && K >= 512) return plan(128, 1);  // batched planes
     if (ktiles >= 25 && t64 < 2 * int64_t(cus)) return plan(64, int(std::min<int64_t>(4, ceil_div(2 * cus, t64))));
     if (4 * t64 < 3 * int64_t(cus)) return plan(32, 1);
     return plan(64, 1);

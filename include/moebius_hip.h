@@ -54,7 +54,9 @@ extern "C" {
 
 /* Arithmetic of the GEMM-shaped kernels. EXACT: f32 MFMA, f32 accumulate (the
  * reference's arithmetic). FAST: activations and weights rounded to f16, f16
- * MFMA with f32 accumulate. */
+ * MFMA with f32 accumulate, and the SiLU of those kernels and of the depthwise
+ * convs from the hardware exp2 and reciprocal (within a few ulp of the
+ * reference's). */
 #define MH_PRECISION_EXACT 0u
 #define MH_PRECISION_FAST 1u
 

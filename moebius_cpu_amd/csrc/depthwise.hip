@@ -10,7 +10,9 @@
 //
 // Arithmetic matches the reference tap for tap: acc = bias, then for ky, for kx,
 // acc = fma(w, x, acc) (depthwise.rs:118-141); rows outside the image are
-// skipped and columns outside contribute fma(w, 0, acc) == acc.
+// skipped and columns outside contribute fma(w, 0, acc) == acc. The GLU gate's
+// and the GroupNorm prologue's SiLU are the reference's in EXACT contexts and
+// fast_silu (hardware exp2 and reciprocal) in FAST ones.
 #include <cstdlib>
 
 #include "common.hpp"
@@ -33,11 +35,14 @@ struct Vec<4> {
     static __device__ __forceinline__ T relu(T a) {
         return make_float4(relu_ref(a.x), relu_ref(a.y), relu_ref(a.z), relu_ref(a.w));
     }
+    template <bool FM>
     static __device__ __forceinline__ T glu(T v, T g) {
-        return make_float4(v.x * ref_silu(g.x), v.y * ref_silu(g.y), v.z * ref_silu(g.z), v.w * ref_silu(g.w));
+        return make_float4(v.x * silu_of<FM>(g.x), v.y * silu_of<FM>(g.y), v.z * silu_of<FM>(g.z),
+                           v.w * silu_of<FM>(g.w));
     }
+    template <bool FM>
     static __device__ __forceinline__ T silu(T a) {
-        return make_float4(ref_silu(a.x), ref_silu(a.y), ref_silu(a.z), ref_silu(a.w));
+        return make_float4(silu_of<FM>(a.x), silu_of<FM>(a.y), silu_of<FM>(a.z), silu_of<FM>(a.w));
     }
 };
 template <>
@@ -46,8 +51,10 @@ struct Vec<1> {
     static __device__ __forceinline__ T zero() { return 0.f; }
     static __device__ __forceinline__ T fma(T a, T b, T c) { return __builtin_fmaf(a, b, c); }
     static __device__ __forceinline__ T relu(T a) { return relu_ref(a); }
-    static __device__ __forceinline__ T glu(T v, T g) { return v * ref_silu(g); }
-    static __device__ __forceinline__ T silu(T a) { return ref_silu(a); }
+    template <bool FM>
+    static __device__ __forceinline__ T glu(T v, T g) { return v * silu_of<FM>(g); }
+    template <bool FM>
+    static __device__ __forceinline__ T silu(T a) { return silu_of<FM>(a); }
 };
 
 // Optional GroupNorm affine applied to every in-image input value as it is
@@ -59,7 +66,7 @@ struct DwPrologue {
 };
 
 // One channel group (value part or gate part) of TX pixels: returns accumulators.
-template <int VW, int TX, bool PRO>
+template <int VW, int TX, bool PRO, bool FM>
 __device__ __forceinline__ void dw_accumulate(const typename Vec<VW>::T *__restrict__ x, int h, int w, int cv,
                                               int b, int oy, int ox0, int q,
                                               const typename Vec<VW>::T *__restrict__ wt,
@@ -87,7 +94,7 @@ __device__ __forceinline__ void dw_accumulate(const typename Vec<VW>::T *__restr
                 win[j] = row[size_t(ix) * cv];
                 if (PRO) {
                     win[j] = V::fma(win[j], psc, psh);
-                    if (pro.silu) win[j] = V::silu(win[j]);
+                    if (pro.silu) win[j] = V::template silu<FM>(win[j]);
                 }
             } else {
                 win[j] = V::zero();
@@ -104,7 +111,7 @@ __device__ __forceinline__ void dw_accumulate(const typename Vec<VW>::T *__restr
 }
 
 // cv = c / VW vectors per input pixel; co_v = output vectors per pixel.
-template <int VW, int TX, int EPI, bool PRO>
+template <int VW, int TX, int EPI, bool PRO, bool FM>
 __global__ __launch_bounds__(256) void depthwise_kernel(const typename Vec<VW>::T *__restrict__ x, int n, int h,
                                                         int w, int cv, const typename Vec<VW>::T *__restrict__ wt,
                                                         const typename Vec<VW>::T *__restrict__ bias, DwPrologue pro,
@@ -125,14 +132,14 @@ __global__ __launch_bounds__(256) void depthwise_kernel(const typename Vec<VW>::
     const int ox0 = strip * TX;
 
     T acc[TX];
-    dw_accumulate<VW, TX, PRO>(x, h, w, cv, b, oy, ox0, q, wt, bias[q], pro, acc);
+    dw_accumulate<VW, TX, PRO, FM>(x, h, w, cv, b, oy, ox0, q, wt, bias[q], pro, acc);
     T *dst = out + (size_t(b) * h + oy) * size_t(w) * co_v + q;
     if (EPI == 2) {
         T gate[TX];
-        dw_accumulate<VW, TX, PRO>(x, h, w, cv, b, oy, ox0, q + co_v, wt, bias[q + co_v], pro, gate);
+        dw_accumulate<VW, TX, PRO, FM>(x, h, w, cv, b, oy, ox0, q + co_v, wt, bias[q + co_v], pro, gate);
 #pragma unroll
         for (int j = 0; j < TX; ++j)
-            if (ox0 + j < w) dst[size_t(ox0 + j) * co_v] = V::glu(acc[j], gate[j]);
+            if (ox0 + j < w) dst[size_t(ox0 + j) * co_v] = V::template glu<FM>(acc[j], gate[j]);
     } else {
 #pragma unroll
         for (int j = 0; j < TX; ++j)
@@ -155,7 +162,7 @@ constexpr int kDwNP = (kDwTH + 2) * (kDwTW + 2);
 
 // x2 (optional): the input is [x | x2] per pixel, x holding quads [0, cv1)
 // (cv1 a multiple of kDwCQ, so a block reads one of the two) and x2 the rest.
-template <int EPI, bool PRO>
+template <int EPI, bool PRO, bool FM>
 __global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__restrict__ x, int n, int h, int w,
                                                              int cv, const float4 *__restrict__ wt,
                                                              const float4 *__restrict__ bias, DwPrologue pro,
@@ -243,7 +250,7 @@ __global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__res
                 const int iy = oy0 - 1 + pix / (kDwTW + 2), ix = ox0 - 1 + pix % (kDwTW + 2);
                 if (q0 + pq < co_v && iy >= 0 && iy < h && ix >= 0 && ix < w) {
                     v[i] = V::fma(v[i], psc[ip], psh[ip]);  // pq == sq: this thread's quad
-                    if (pro.silu) v[i] = V::silu(v[i]);
+                    if (pro.silu) v[i] = V::template silu<FM>(v[i]);
                 }
             }
             tile[pix][pq] = v[i];
@@ -282,11 +289,26 @@ __global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__res
         const int ox = ox0 + c0 + j;
         if (ox >= w) break;
         float4 y;
-        if (EPI == 2) y = V::glu(acc[0][j], acc[PARTS - 1][j]);
+        if (EPI == 2) y = V::template glu<FM>(acc[0][j], acc[PARTS - 1][j]);
         else if (EPI == 1) y = V::relu(acc[0][j]);
         else y = acc[0][j];
         dst[size_t(ox) * co_v] = y;
     }
+}
+
+template <int EPI, bool PRO>
+void launch_dw_tile_fm(bool fast, dim3 grid, hipStream_t st, const float4 *x, int n, int h, int w, int cv,
+                       const float4 *wt, const float4 *bias, const DwPrologue &pro, float4 *out, const float4 *x2,
+                       int cv1) {
+    if (fast) depthwise_tile_kernel<EPI, PRO, true><<<grid, 256, 0, st>>>(x, n, h, w, cv, wt, bias, pro, out, x2, cv1);
+    else depthwise_tile_kernel<EPI, PRO, false><<<grid, 256, 0, st>>>(x, n, h, w, cv, wt, bias, pro, out, x2, cv1);
+}
+
+template <int VW, int TX, int EPI, bool PRO, typename T>
+void launch_dw_fm(bool fast, unsigned blocks, hipStream_t st, const T *x, int n, int h, int w, int cv, const T *wt,
+                  const T *bias, const DwPrologue &pro, T *out) {
+    if (fast) depthwise_kernel<VW, TX, EPI, PRO, true><<<blocks, 256, 0, st>>>(x, n, h, w, cv, wt, bias, pro, out);
+    else depthwise_kernel<VW, TX, EPI, PRO, false><<<blocks, 256, 0, st>>>(x, n, h, w, cv, wt, bias, pro, out);
 }
 
 template <bool PRO>
@@ -303,10 +325,12 @@ void launch_dw_tile(Context &ctx, const float *x, int n, int h, int w, int c, co
     float4 *ov = reinterpret_cast<float4 *>(out);
     const float4 *x2v = reinterpret_cast<const float4 *>(x2);
     const int cv1 = (c - c2) / 4;
+    const bool fast = ctx.precision == Precision::Fast;
     switch (epilogue) {
-        case 0: depthwise_tile_kernel<0, PRO><<<grid, 256, 0, ctx.stream>>>(xv, n, h, w, cv, wv, bv, pro, ov, x2v, cv1); break;
-        case 1: depthwise_tile_kernel<1, PRO><<<grid, 256, 0, ctx.stream>>>(xv, n, h, w, cv, wv, bv, pro, ov, x2v, cv1); break;
-        default: depthwise_tile_kernel<2, PRO><<<grid, 256, 0, ctx.stream>>>(xv, n, h, w, cv, wv, bv, pro, ov, x2v, cv1); break;
+        // FAST contexts take fast_silu for the GLU gate and the prologue's SiLU
+        case 0: launch_dw_tile_fm<0, PRO>(fast, grid, ctx.stream, xv, n, h, w, cv, wv, bv, pro, ov, x2v, cv1); break;
+        case 1: launch_dw_tile_fm<1, PRO>(fast, grid, ctx.stream, xv, n, h, w, cv, wv, bv, pro, ov, x2v, cv1); break;
+        default: launch_dw_tile_fm<2, PRO>(fast, grid, ctx.stream, xv, n, h, w, cv, wv, bv, pro, ov, x2v, cv1); break;
     }
     MH_LAUNCH_CHECK();
 }
@@ -324,10 +348,11 @@ void launch_dw(Context &ctx, const float *x, int n, int h, int w, int c, const f
     const T *wv = reinterpret_cast<const T *>(wt);
     const T *bv = reinterpret_cast<const T *>(bias);
     T *ov = reinterpret_cast<T *>(out);
+    const bool fast = ctx.precision == Precision::Fast;
     switch (epilogue) {
-        case 0: depthwise_kernel<VW, TX, 0, PRO><<<blocks, 256, 0, ctx.stream>>>(xv, n, h, w, cv, wv, bv, pro, ov); break;
-        case 1: depthwise_kernel<VW, TX, 1, PRO><<<blocks, 256, 0, ctx.stream>>>(xv, n, h, w, cv, wv, bv, pro, ov); break;
-        default: depthwise_kernel<VW, TX, 2, PRO><<<blocks, 256, 0, ctx.stream>>>(xv, n, h, w, cv, wv, bv, pro, ov); break;
+        case 0: launch_dw_fm<VW, TX, 0, PRO>(fast, blocks, ctx.stream, xv, n, h, w, cv, wv, bv, pro, ov); break;
+        case 1: launch_dw_fm<VW, TX, 1, PRO>(fast, blocks, ctx.stream, xv, n, h, w, cv, wv, bv, pro, ov); break;
+        default: launch_dw_fm<VW, TX, 2, PRO>(fast, blocks, ctx.stream, xv, n, h, w, cv, wv, bv, pro, ov); break;
     }
     MH_LAUNCH_CHECK();
 }

@@ -8,7 +8,11 @@
 //     in LDS;
 //   - f16 weights enter as stored; f32 weights are rounded like A;
 //   - products run on v_mfma_f32_32x32x16_f16 (tiles of 64 or more in both
-//     dimensions) or v_mfma_f32_16x16x32_f16 (32-wide tiles), summed in f32.
+//     dimensions) or v_mfma_f32_16x16x32_f16 (32-wide tiles), summed in f32;
+//   - every SiLU (the inverted 1x1's epilogue, the GroupNorm prologue and the
+//     residual transform) is fast_silu, from the hardware exp2 and reciprocal:
+//     the reference's exp polynomial and IEEE division took 12.6 of 51.6 us in
+//     the 8192x1600x320 inverted 1x1.
 // Each lane reads eight consecutive K of one A row and of one B column from
 // LDS with one 16-byte read per instruction; A and B use the same lane-to-K
 // assignment, so the sum covers every K exactly once whatever order the
@@ -65,7 +69,7 @@ __device__ __forceinline__ floatx4 load_a_h(const GemmArgs &p, __amdgpu_buffer_r
     if constexpr (MODE == kDense) {
         const bool ok = m < p.M && k < k_end;
         const floatx4 v = buf_load4(ar, ok ? int((int64_t(m) * (lda < 0 ? p.lda : lda) + k) * 4) : kOob);
-        if constexpr (PRO == kProAffine) return dense_prologue(p, r.b, k, ok, v);
+        if constexpr (PRO == kProAffine) return dense_prologue<true>(p, r.b, k, ok, v);
         return v;
     } else if constexpr (MODE == kConvAligned || MODE == kConvVec) {
         int ky, kx, c;
@@ -84,11 +88,11 @@ __device__ __forceinline__ floatx4 load_a_h(const GemmArgs &p, __amdgpu_buffer_r
         floatx4 v = buf_load4(ar, ok ? int((src + c) * 4) : kOob);
         if constexpr (PRO == kProAffine) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = ok ? prologue1(p, r.b, c + e, v[e]) : 0.0f;
+            for (int e = 0; e < 4; ++e) v[e] = ok ? prologue1<true>(p, r.b, c + e, v[e]) : 0.0f;
         }
         return v;
     } else {  // scalar modes
-        return k < k_end ? load_a<MODE, PRO>(p, r, m, k, tky, tkx, tci) : zero4();
+        return k < k_end ? load_a<MODE, PRO, true>(p, r, m, k, tky, tkx, tci) : zero4();
     }
 }
 
@@ -263,7 +267,7 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
     if constexpr (PRO == kProLn) ln_row_stats<A_LD, 16, KCH, BM>(p, ln_s1, ln_s2, lrow, lc, ln_st);
     if constexpr (PRO == kProLnPart) ln_stats_from_parts<BM, 256>(p, m0, ln_st);
     __syncthreads();
-    write_tile<BM, BN, 2, 2, 1, MF, EPI, SPLIT>(p, reinterpret_cast<float *>(smem), acc, m0, n0, ti.z,
+    write_tile<BM, BN, 2, 2, 1, MF, EPI, SPLIT, true>(p, reinterpret_cast<float *>(smem), acc, m0, n0, ti.z,
                                                 PRO >= kProLn ? ln_st : nullptr);
 }
 
@@ -319,15 +323,15 @@ void launch_cfg_h16(Context &ctx, GemmArgs &p, const Plan &pl, GemmEpilogue epi,
         if (reduce_vec_ok(p)) {
             const unsigned rb = unsigned(std::min<int64_t>(ceil_div(total / 4, 256), 8192));
             if (epi == GemmEpilogue::Silu)
-                splitk_reduce_kernel<1, true><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
+                splitk_reduce_kernel<1, true, true><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
             else
-                splitk_reduce_kernel<0, true><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
+                splitk_reduce_kernel<0, true, true><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
         } else {
             const unsigned rb = unsigned(std::min<int64_t>(ceil_div(total, 256), 8192));
             if (epi == GemmEpilogue::Silu)
-                splitk_reduce_kernel<1, false><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
+                splitk_reduce_kernel<1, false, true><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
             else
-                splitk_reduce_kernel<0, false><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
+                splitk_reduce_kernel<0, false, true><<<rb, 256, 0, ctx.stream>>>(p, pl.splits);
         }
     } else {
         p.k_split = p.K;

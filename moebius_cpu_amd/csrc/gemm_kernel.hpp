@@ -138,7 +138,8 @@ struct GemmArgs {
 
 // (residual [transformed] + bias) + acc [SiLU] (+ res2): the reference's
 // Conv1x1 epilogue (src/engine/conv.rs:38-55) followed by the block's add_inplace.
-template <int EPI>
+// FM: the FAST precision kernel's SiLU (fast_silu) instead of the reference's.
+template <int EPI, bool FM = false>
 __device__ __forceinline__ float epilogue_value(const GemmArgs &p, int row, int col, int64_t o, float acc, float bcol) {
     float y;
     if (p.res) {
@@ -146,14 +147,14 @@ __device__ __forceinline__ float epilogue_value(const GemmArgs &p, int row, int 
         if (p.rsc) {
             const int64_t i = int64_t(row / p.r_rows) * p.N + col;
             rv = __builtin_fmaf(rv, p.rsc[i], p.rsh[i]);
-            if (p.rsilu) rv = ref_silu(rv);
+            if (p.rsilu) rv = silu_of<FM>(rv);
         }
         const float t = p.bias ? rv + bcol : rv;
         y = t + acc;
     } else {
         y = p.bias ? bcol + acc : acc;
     }
-    if (EPI == 1) y = ref_silu(y);
+    if (EPI == 1) y = silu_of<FM>(y);
     if (p.res2) y = y + p.res2[o];
     return y;
 }
@@ -203,7 +204,7 @@ __device__ __forceinline__ float *out_ptr(const GemmArgs &p, int row, int col, i
 // epilogue_value for four adjacent columns col..col+3 of one row, with 16-byte
 // loads and one 16-byte store (the caller has checked out_vec_ok); returns the
 // values stored.
-template <int EPI>
+template <int EPI, bool FM = false>
 __device__ __forceinline__ float4 store4(const GemmArgs &p, int row, int col, float4 s) {
     int64_t o;
     float *dst = out_ptr(p, row, col, o);
@@ -223,7 +224,7 @@ __device__ __forceinline__ float4 store4(const GemmArgs &p, int row, int col, fl
             rv[3] = __builtin_fmaf(rv[3], sc.w, sh.w);
             if (p.rsilu)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) rv[j] = ref_silu(rv[j]);
+                for (int j = 0; j < 4; ++j) rv[j] = silu_of<FM>(rv[j]);
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) y[j] = (p.bias ? rv[j] + bb[j] : rv[j]) + y[j];
@@ -233,7 +234,7 @@ __device__ __forceinline__ float4 store4(const GemmArgs &p, int row, int col, fl
     }
     if (EPI == 1)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) y[j] = ref_silu(y[j]);
+        for (int j = 0; j < 4; ++j) y[j] = silu_of<FM>(y[j]);
     if (p.res2) {
         const float4 r2 = *reinterpret_cast<const float4 *>(p.res2 + o);
         y[0] = y[0] + r2.x, y[1] = y[1] + r2.y, y[2] = y[2] + r2.z, y[3] = y[3] + r2.w;
@@ -292,12 +293,13 @@ __device__ __forceinline__ int64_t conv_src(const GemmArgs &p, const ConvRow &r,
     return ((int64_t(r.b) * p.ch + (iy >> p.up)) * p.cw + (ix >> p.up)) * p.ci;
 }
 
+template <bool FM = false>
 __device__ __forceinline__ float prologue1(const GemmArgs &p, int b, int c, float v) {
     const float y = __builtin_fmaf(v, p.psc[int64_t(b) * p.ci + c], p.psh[int64_t(b) * p.ci + c]);
-    return p.psilu ? ref_silu(y) : y;
+    return p.psilu ? silu_of<FM>(y) : y;
 }
 
-template <int MODE, int PRO>
+template <int MODE, int PRO, bool FM = false>
 __device__ __forceinline__ floatx4 load_a(const GemmArgs &p, const ConvRow &r, int m, int k, int tap_ky,
                                           int tap_kx, int tap_ci0) {
     if (MODE == kDense) {
@@ -329,7 +331,7 @@ __device__ __forceinline__ floatx4 load_a(const GemmArgs &p, const ConvRow &r, i
         floatx4 v = *reinterpret_cast<const floatx4 *>(p.a + off + c);
         if (PRO == kProAffine) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = prologue1(p, r.b, c + e, v[e]);
+            for (int e = 0; e < 4; ++e) v[e] = prologue1<FM>(p, r.b, c + e, v[e]);
         }
         return v;
     } else {  // kConvScalar
@@ -344,7 +346,7 @@ __device__ __forceinline__ floatx4 load_a(const GemmArgs &p, const ConvRow &r, i
             const int64_t off = conv_src(p, r, ky, kx);
             if (off >= 0) {
                 float x = p.a[off + c];
-                if (PRO == kProAffine) x = prologue1(p, r.b, c, x);
+                if (PRO == kProAffine) x = prologue1<FM>(p, r.b, c, x);
                 v[e] = x;
             }
         }
@@ -371,6 +373,7 @@ __device__ __forceinline__ floatx4 buf_load4(__amdgpu_buffer_rsrc_t r, int off) 
 // [SiLU](x . scale + shift) of row item b (r.b = row / pro_rows), channels
 // k..k+3 (psc/psh [items][K], K % 4 == 0, 16-byte aligned), computed as the
 // separate apply pass does; zero where the load was out of range.
+template <bool FM = false>
 __device__ __forceinline__ floatx4 dense_prologue(const GemmArgs &p, int b, int k, bool ok, floatx4 v) {
     const int64_t i = int64_t(b) * p.K + (ok ? k : 0);
     const float4 sc = *reinterpret_cast<const float4 *>(p.psc + i);
@@ -379,7 +382,7 @@ __device__ __forceinline__ floatx4 dense_prologue(const GemmArgs &p, int b, int 
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         float y = __builtin_fmaf(v[e], s4[e], h4[e]);
-        if (p.psilu) y = ref_silu(y);
+        if (p.psilu) y = silu_of<FM>(y);
         v[e] = ok ? y : 0.0f;
     }
     return v;
@@ -689,7 +692,8 @@ struct Waves {
 // partial sum; the K groups' tiles are added in LDS, then each thread finishes
 // four adjacent columns of a row at a time (16-byte loads and stores), or one
 // element at a time where that is not possible.
-template <int BM, int BN, int WM, int WN, int WK, int MF, int EPI, bool SPLIT, typename Acc, int FM, int FN>
+template <int BM, int BN, int WM, int WN, int WK, int MF, int EPI, bool SPLIT, bool FSILU = false, typename Acc,
+          int FM, int FN>
 __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const Acc (&acc)[FM][FN], int m0, int n0,
                                            int z, const float *ln_st = nullptr) {
     using MI = Mf<MF>;
@@ -746,7 +750,7 @@ __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const
                 if (SPLIT) {
                     *reinterpret_cast<float4 *>(p.partial + (int64_t(z) * p.M + row) * p.N + col) = v;
                 } else {
-                    const float4 y = store4<EPI>(p, row, col, v);
+                    const float4 y = store4<EPI, FSILU>(p, row, col, v);
                     if (kGn && p.gnp) {
                         gs.x += y.x, gs.y += y.y, gs.z += y.z, gs.w += y.w;
                         gq.x = __builtin_fmaf(y.x, y.x, gq.x);
@@ -776,7 +780,7 @@ __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const
                 if (SPLIT) {
                     *reinterpret_cast<float4 *>(p.partial + (int64_t(z) * p.M + row) * p.N + col) = v;
                 } else {
-                    const float4 y = store4<EPI>(p, row, col, v);
+                    const float4 y = store4<EPI, FSILU>(p, row, col, v);
                     if (gn || lnr) *reinterpret_cast<float4 *>(c) = y;  // the stored values, for the sums
                 }
             }
@@ -798,7 +802,7 @@ __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const
             const float bcol = p.bias ? p.bias[col] : 0.f;
             float y[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) y[j] = epilogue_value<EPI>(p, row + j, col, o + j, smem[(rr + j) * CS + cc], bcol);
+            for (int j = 0; j < 4; ++j) y[j] = epilogue_value<EPI, FSILU>(p, row + j, col, o + j, smem[(rr + j) * CS + cc], bcol);
             *reinterpret_cast<float4 *>(p.out + o) = float4{y[0], y[1], y[2], y[3]};
         }
     } else {
@@ -815,7 +819,7 @@ __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const
             } else {
                 int64_t o;
                 float *dst = out_ptr(p, row, col, o);
-                dst[o] = epilogue_value<EPI>(p, row, col, o, r, p.bias ? p.bias[col] : 0.f);
+                dst[o] = epilogue_value<EPI, FSILU>(p, row, col, o, r, p.bias ? p.bias[col] : 0.f);
             }
         }
     }
@@ -1094,7 +1098,7 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(GemmArgs p)
 // VEC: four adjacent columns per thread (N, the output's leading dimensions and
 // segment bounds multiples of 4, M * N < 2^31, 16-byte aligned buffers; checked
 // by the launcher), so every load and store is 16 bytes wide.
-template <int EPI, bool VEC>
+template <int EPI, bool VEC, bool FSILU = false>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int splits) {
     const int64_t total = int64_t(p.M) * p.N;
     if constexpr (VEC) {
@@ -1108,7 +1112,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int spli
                 s.x += t.x, s.y += t.y, s.z += t.z, s.w += t.w;
             }
             const int row = int(e / n4);
-            store4<EPI>(p, row, int(e - uint32_t(row) * n4) << 2, s);
+            store4<EPI, FSILU>(p, row, int(e - uint32_t(row) * n4) << 2, s);
         }
     } else {
         for (int64_t e = blockIdx.x * int64_t(256) + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
@@ -1118,7 +1122,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int spli
             const int col = int(e - int64_t(row) * p.N);
             int64_t o;
             float *dst = out_ptr(p, row, col, o);
-            dst[o] = epilogue_value<EPI>(p, row, col, o, s, p.bias ? p.bias[col] : 0.0f);
+            dst[o] = epilogue_value<EPI, FSILU>(p, row, col, o, s, p.bias ? p.bias[col] : 0.0f);
         }
     }
 }

@@ -228,3 +228,34 @@ def test_vae_keeps_f32_on_fast_context(ctx):
     lat = S.normal(21, (1, 8, 6, 4))
     got = Vae(ctx, params).decode_host(lat)
     assert max_abs_rel(got, oracle.Vae(params).decode(lat)) <= 1e-4
+
+
+# FAST contexts evaluate the depthwise conv's GLU gate and GroupNorm-prologue
+# SiLU with fast_silu (the hardware exp2 and reciprocal, dmath.hpp) instead of
+# the reference's exp polynomial and IEEE division: against the oracle (the
+# reference's SiLU, src/engine/math.rs:17-36, in depthwise.rs:31-59's tap
+# order) within a few f32 ulp of the output's scale; EXACT contexts keep the
+# bit-exact SiLU (test_gpu_engine.py).
+@pytest.mark.parametrize("n,h,w,c,ep,silu", [(2, 9, 7, 64, "glu_silu", True), (1, 16, 16, 320, "relu", True),
+                                             (2, 12, 10, 160, "glu_silu", False), (1, 33, 17, 80, "none", True)])
+def test_depthwise_fast_silu(ctx, n, h, w, c, ep, silu):
+    rng = np.random.default_rng(h * w + c + 3)
+    x = (rng.standard_normal((n, h, w, c)) * 3).astype(np.float32)
+    wt = (rng.standard_normal((3, 3, c)) * 0.3).astype(np.float32)
+    b = (rng.standard_normal(c) * 0.1).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(c)).astype(np.float32)
+    beta = (0.1 * rng.standard_normal(c)).astype(np.float32)
+    sc, sh = oracle.group_norm_affine(x, 2, 1e-5, gamma, beta)
+    d = {k: E.DeviceArray.from_numpy(ctx, v) for k, v in dict(x=x, w=wt, b=b, sc=sc, sh=sh).items()}
+    co = c // 2 if ep == "glu_silu" else c
+    out = E.DeviceArray(ctx, (n, h, w, co))
+    E.check(E.lib().mh_depthwise3x3_fused(ctx.h, d["x"].ptr, n, h, w, c, d["w"].ptr, d["b"].ptr, E._lib.EPILOGUE[ep],
+                                          d["sc"].ptr, d["sh"].ptr, int(silu), out.ptr))
+    a = np.stack([oracle.apply_affine(x[i], sc[i * c:(i + 1) * c], sh[i * c:(i + 1) * c], silu) for i in range(n)])
+    want = oracle.depthwise3x3(a, wt, b, ep)
+    assert max_abs_rel(out.numpy(), want) <= 4e-6
+    # the plain depthwise (no prologue) with the GLU epilogue
+    if ep == "glu_silu":
+        plain = E.Tensor(ctx)
+        E.depthwise3x3(T(ctx, x), wt, b, ep, plain)
+        assert max_abs_rel(plain.numpy(), oracle.depthwise3x3(x, wt, b, ep)) <= 4e-6

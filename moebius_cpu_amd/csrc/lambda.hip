@@ -1563,10 +1563,13 @@ void lambda_taps(Context &ctx, const float *q, const float *w_aug_t, const float
     const int per_cu = int(std::max<size_t>(1, (160 * 1024) / lds));
     const int64_t cap = std::max<int64_t>(1, int64_t(ctx.cu_count) * per_cu / (parts * nb));
     const dim3 grid(unsigned(std::min<int64_t>(ceil_div(tasks, 4), cap)), unsigned(parts), unsigned(nb));
-    // FAST contexts take the products of f16-rounded operands, as their GEMMs do.
+    // Products of the operands as given (f32 MFMA) in both precisions: in FAST
+    // contexts they are faster than the products of f16-rounded operands the
+    // FAST GEMMs take (tuning taps_r16 1, which this kernel can also run:
+    // 20.8 against 13.9 us at 16x16), and more accurate.
     auto go = [&](auto kern) { kern<<<grid, 256, 0, ctx.stream>>>(q, w_aug_t, lambda_t, hw, a_t, yc, part0); };
     auto by_rows = [&](auto k80, auto k48, auto k16) { pr == 80 ? go(k80) : pr == 48 ? go(k48) : go(k16); };
-    const bool r16 = ctx.precision == Precision::Fast;
+    const bool r16 = ctx.precision == Precision::Fast && ctx.tune.taps_r16;
 #define MH_TAPS(NF, TAIL, R) \
     by_rows(lambda_taps_kernel<NF, TAIL, R, 80>, lambda_taps_kernel<NF, TAIL, R, 48>, lambda_taps_kernel<NF, TAIL, R, 16>)
     if (k == 40) r16 ? MH_TAPS(2, 2, true) : MH_TAPS(2, 2, false);
@@ -1604,7 +1607,7 @@ void self_lambda_fused(Context &ctx, const float *q, const float *w_aug_t, const
     auto go = [&](auto kern) {
         kern<<<unsigned(blocks), 256, lds, ctx.stream>>>(q, w_aug_t, lambda_t, v, residual, out, hh, ww, tx, ln);
     };
-    const bool r16 = ctx.precision == Precision::Fast, rs = row_sums != nullptr;
+    const bool r16 = ctx.precision == Precision::Fast && ctx.tune.taps_r16, rs = row_sums != nullptr;
 #define MH_FUSED(NF, TAIL)                                                                             \
     (r16 ? (rs ? go(tap_fused_kernel<NF, TAIL, true, true>) : go(tap_fused_kernel<NF, TAIL, true, false>)) \
          : (rs ? go(tap_fused_kernel<NF, TAIL, false, true>) : go(tap_fused_kernel<NF, TAIL, false, false>)))

@@ -198,11 +198,35 @@ def _h16(a):
     return np.clip(a, -65504, 65504).astype(np.float16).astype(np.float64)
 
 
-# FAST contexts: the products of f16-rounded operands (as the FAST GEMMs take
-# them), summed in f32: against the f64 sums of the same products and against
-# the FAST GEMM's output.
+# FAST contexts: by default the products of the f32 operands, the EXACT
+# kernel's bits; with tuning taps_r16 1 the products of f16-rounded operands (as
+# the FAST GEMMs take them), summed in f32: against the f64 sums of the same
+# products and against the FAST GEMM's output.
 @pytest.mark.parametrize("nb,hw,k", [(2, 4096, 40), (2, 1024, 80), (2, 256, 160), (1, 7, 40)])
-def test_lambda_position_coeffs_fast(ctx, nb, hw, k):
+def test_lambda_position_coeffs_fast_default_is_exact(ctx, nb, hw, k):
+    rng = np.random.default_rng(5 * hw + k)
+    npx = nb * hw
+    q = rng.standard_normal((npx, 8, k)).astype(np.float32)
+    w = rng.standard_normal((226, k)).astype(np.float32)
+    lam_t = rng.standard_normal((nb, k, k)).astype(np.float32)
+    want = (q.reshape(npx * 8, k).astype(np.float64) @ w.astype(np.float64).T).reshape(npx, 8, 226).transpose(0, 2, 1)
+    qd, wd, ld = D(ctx, q), D(ctx, w), D(ctx, lam_t)
+    got = {}
+    for fast in (False, True):
+        out, yc = E.DeviceArray(ctx, (npx, 226, 8)), E.DeviceArray(ctx, (npx, 8, k))
+        ctx.set_precision(fast)
+        try:
+            E.check(E.lib().mh_lambda_position_coeffs(ctx.h, qd.ptr, wd.ptr, ld.ptr, nb, hw, k, out.ptr, yc.ptr))
+        finally:
+            ctx.set_precision(False)
+        got[fast] = (out.numpy(), yc.numpy())
+    assert max_abs_rel(got[True][0], want) < 1e-5
+    assert np.array_equal(got[True][0], got[False][0]) and np.array_equal(got[True][1], got[False][1])
+
+
+@pytest.mark.parametrize("nb,hw,k", [(2, 4096, 40), (2, 1024, 80), (2, 256, 160), (1, 7, 40)])
+def test_lambda_position_coeffs_fast(ctx, nb, hw, k, tune):
+    tune("taps_r16", 1)
     rng = np.random.default_rng(7 * hw + k)
     npx = nb * hw
     q = rng.standard_normal((npx, 8, k)).astype(np.float32)
@@ -242,10 +266,13 @@ def test_lambda_position_coeffs_rejects_bad_arguments(ctx):
 # maps narrower than the window (7 x 5, 1 x 1) and single items.
 @pytest.mark.parametrize("nb,hh,ww,k", [(2, 64, 64, 40), (2, 32, 32, 80), (2, 16, 16, 160), (1, 9, 70, 40),
                                         (1, 20, 9, 80), (1, 7, 5, 40), (3, 1, 1, 160), (1, 5, 17, 40)])
-@pytest.mark.parametrize("fast", [False, True])
+@pytest.mark.parametrize("fast", [False, True, "r16"])
 def test_self_lambda_fused_bit_exact(ctx, nb, hh, ww, k, fast, tune):
+    """r16: a FAST context with tuning taps_r16 1 (f16-rounded products)."""
     tune("tap_split", 1)
     tune("tap_heads", "t4")
+    if fast == "r16":
+        tune("taps_r16", 1)
     rng = np.random.default_rng(hh * ww + k + nb)
     npx = nb * hh * ww
     q = rng.standard_normal((npx, 8, k)).astype(np.float32)

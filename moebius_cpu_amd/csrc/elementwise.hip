@@ -122,6 +122,16 @@ __global__ void widen_f16_kernel(const _Float16 *__restrict__ src, int64_t len, 
         dst[e] = float(src[e]);
 }
 
+// f32 -> f16, round to nearest even, finite values beyond f16's range saturated
+// to +-65504 (NaN stays NaN): the rounding the f16 GEMM applies to f32 operands
+// as it stages them.
+__global__ void round_f16_kernel(const float *__restrict__ src, int64_t len, _Float16 *__restrict__ dst) {
+    for (int64_t e = blockIdx.x * int64_t(blockDim.x) + threadIdx.x; e < len; e += int64_t(gridDim.x) * blockDim.x) {
+        const float v = src[e];
+        dst[e] = static_cast<_Float16>(__builtin_fabsf(v) > 65504.0f ? __builtin_copysignf(65504.0f, v) : v);
+    }
+}
+
 // One workgroup per weight row n (LnFolded, kernels.hpp): W' = W . gamma and its
 // f16 rounding (nearest, saturated at +-65504 as the f16 GEMM rounds f32
 // operands), their row sums and W . beta + bias, each summed in f64 per thread
@@ -254,6 +264,12 @@ void tile_items(Context &ctx, const float *src, int64_t item, int n, float *dst)
 void widen_f16(Context &ctx, const void *src, int64_t len, float *dst) {
     if (len == 0) return;
     widen_f16_kernel<<<grid_for(len), 256, 0, ctx.stream>>>(static_cast<const _Float16 *>(src), len, dst);
+    MH_LAUNCH_CHECK();
+}
+
+void round_f16(Context &ctx, const float *src, int64_t len, void *dst) {
+    if (len == 0) return;
+    round_f16_kernel<<<grid_for(len), 256, 0, ctx.stream>>>(src, len, static_cast<_Float16 *>(dst));
     MH_LAUNCH_CHECK();
 }
 

@@ -35,6 +35,8 @@ void concat_channels(Context &ctx, const float *a, int ca, const float *b, int c
 void to_u8(Context &ctx, const float *x, int64_t len, uint8_t *out);
 // f16 [len] -> f32 [len], exact.
 void widen_f16(Context &ctx, const void *src, int64_t len, float *dst);
+// f32 [len] -> f16 [len], nearest even, saturated at +-65504 (the f16 GEMM's operand rounding).
+void round_f16(Context &ctx, const float *src, int64_t len, void *dst);
 void math_eval(Context &ctx, int which, const float *x, int64_t len, float *y);
 // dst [n][item] = src [item]: one item repeated over a batch.
 void tile_items(Context &ctx, const float *src, int64_t item, int n, float *dst);

@@ -113,6 +113,16 @@ const float *WeightStore::winograd_kernel(const DParam &w, int co, int ci) const
     return static_cast<const float *>(u);
 }
 
+const void *WeightStore::winograd_kernel_f16(const float *u, int co, int ci) const {
+    const size_t len = size_t(16) * co * ci;
+    void *u16 = nullptr;
+    mh::dev_malloc(&u16, len * 2);
+    derived_.push_back(u16);
+    derived_bytes_ += len * 2;
+    round_f16(ctx_, u, int64_t(len), u16);
+    return u16;
+}
+
 const float *WeightStore::winograd_kernel_fused(const float *u, int co, int ci) const {
     const size_t bytes = size_t(16) * co * ci * sizeof(float);
     void *uf = nullptr;
@@ -818,19 +828,25 @@ struct Conv3 {
     bool up = false;
     DParam w;
     const float *u = nullptr;
+    const void *u16 = nullptr;  // u rounded to f16, for FAST contexts (the same products, half the bytes)
     const float *b = nullptr;
     void load(const WeightStore &W, const std::string &p, int c_, int stride_, bool up_) {
         c = c_, stride = stride_, up = up_;
         w = W.get(p + ".conv.weight", int64_t(9) * c * c, true);
         b = W.get(p + ".conv.bias", c, false).f();
-        if (stride == 1 && c % 4 == 0) u = W.winograd_kernel(w, c, c);
+        if (stride == 1 && c % 4 == 0) {
+            u = W.winograd_kernel(w, c, c);
+            u16 = W.winograd_kernel_f16(u, c, c);
+        }
     }
     DT fwd(Env &e, const DT &x) const {
         const int pad[4] = {1, 1, 1, 1};
         int ho, wo;
         conv3x3_output_hw(x.h, x.w, stride, pad, up, &ho, &wo);
         DT out = e.pool.tensor(x.n, ho, wo, c);
-        if (u)
+        if (u && e.ctx.precision == Precision::Fast && e.ctx.tune.wino_u16)
+            conv3x3_winograd(e.ctx, x.p, x.n, x.h, x.w, x.c, u16, kF16, c, b, up, nullptr, out.p);
+        else if (u)
             conv3x3_winograd(e.ctx, x.p, x.n, x.h, x.w, x.c, u, kF32, c, b, up, nullptr, out.p);
         else
             conv3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, w.at(e.ctx).p, w.at(e.ctx).wt, c, b, stride, pad, up, nullptr,

@@ -58,6 +58,8 @@ class WeightStore {
     const float *winograd_kernel(const DParam &w, int co, int ci) const;
     // u (from winograd_kernel) in the one-kernel Winograd path's order.
     const float *winograd_kernel_fused(const float *u, int co, int ci) const;
+    // u rounded to f16 as the FAST plane GEMM rounds it on every load, for FAST contexts.
+    const void *winograd_kernel_f16(const float *u, int co, int ci) const;
     size_t bytes() const { return bytes_ + derived_bytes_; }
 
   private:

@@ -261,6 +261,32 @@ void gemm_nt(Context &ctx, const float *a, int64_t lda, int64_t a_bs, const void
         run_dense(ctx, p, wt, epi, batch, false);
 }
 
+void gemm_nt_a16(Context &ctx, const void *a, int64_t lda, int64_t a_bs, const void *b, int64_t ldb, int64_t b_bs,
+                 int m, int n, int k, int batch, float *out, int64_t ldc, int64_t c_bs) {
+    MH_REQUIRE(ctx.precision == Precision::Fast, "gemm (f16 A): FAST contexts only");
+    MH_REQUIRE(m >= 0 && n > 0 && k > 0 && batch > 0, "gemm (f16 A): bad shape");
+    MH_REQUIRE(k % 4 == 0 && lda % 4 == 0 && ldb % 4 == 0 && a_bs % 4 == 0 && b_bs % 4 == 0 &&
+                   (reinterpret_cast<uintptr_t>(a) & 7) == 0 && (reinterpret_cast<uintptr_t>(b) & 7) == 0,
+               "gemm (f16 A): rows of whole, 8-byte aligned 4-element chunks");
+    if (m == 0) return;
+    GemmArgs p{};
+    p.a = static_cast<const float *>(a);  // halves: the A16 kernels read it as such
+    p.lda = lda;
+    p.M = m;
+    p.N = n;
+    p.K = k;
+    p.b = b;
+    p.ldb = ldb;
+    p.a_bytes = extent(m, lda, k, 2);
+    p.b_bytes = extent(n, ldb, k, 2);
+    p.out = out;
+    p.ldc = ldc;
+    p.a_bs = a_bs;
+    p.b_bs = b_bs;
+    p.c_bs = c_bs;
+    gemm::launch_dense_h16_a16(ctx, p, batch);
+}
+
 void conv3x3_output_hw(int h, int w, int stride, const int pad[4], bool upsample2x, int *ho, int *wo) {
     const int up = upsample2x ? 2 : 1;
     const int hh = h * up + pad[0] + pad[2] - 3, ww = w * up + pad[1] + pad[3] - 3;

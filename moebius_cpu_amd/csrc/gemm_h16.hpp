@@ -28,6 +28,9 @@ typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 
 // Launchers of the fast kernels (gemm_fast_dense.hip, gemm_fast_conv.hip).
 void launch_dense_h16(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi, int batch, bool vec);
+// Dense A stored in f16 (GemmArgs::a holds halves; a_bs, lda in halves), f16
+// vector weights, no prologue or epilogue beyond bias and residual, no K split.
+void launch_dense_h16_a16(Context &ctx, GemmArgs &p, int batch);
 void launch_dense_pro_h16(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi);
 void launch_dense_ln_h16(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi);
 void launch_conv_h16(Context &ctx, GemmArgs &p, WeightType wt, int mode, bool pro);
@@ -120,8 +123,17 @@ __device__ __forceinline__ typename BChunk<F16, BVEC>::T load_b_h(const GemmArgs
 __device__ __forceinline__ halfx4 as_h4(halfx4 v) { return v; }
 __device__ __forceinline__ halfx4 as_h4(floatx4 v) { return to_h4(v); }
 
-template <int BM, int BN, int MODE, int PRO, bool F16, bool BVEC, int EPI, bool SPLIT>
+// Four consecutive K of an f16 A row (A16: dense operands already rounded by
+// their producer, e.g. the Winograd input transform of FAST contexts).
+__device__ __forceinline__ halfx4 load_a_f16(const GemmArgs &p, __amdgpu_buffer_rsrc_t ar, int m, int k, int k_end) {
+    const bool ok = m < p.M && k < k_end;
+    const auto raw = __builtin_amdgcn_raw_buffer_load_b64(ar, ok ? int((int64_t(m) * p.lda + k) * 2) : kOob, 0, 0);
+    return __builtin_bit_cast(halfx4, raw);
+}
+
+template <int BM, int BN, int MODE, int PRO, bool F16, bool BVEC, int EPI, bool SPLIT, bool A16 = false>
 __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
+    static_assert(!A16 || (MODE == kDense && PRO == kProNone), "f16 A operands: dense, no prologue");
     constexpr int MF = mf_for<BM, BN>();
     using MI = MfH<MF>;
     constexpr int FM = BM / 2 / MF, FN = BN / 2 / MF;
@@ -130,7 +142,7 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
     const TileIdx ti = tile_index(tiles_m, tiles_n);
     if (ti.y) {
         const int64_t bz = ti.y;
-        p.a += bz * p.a_bs;
+        p.a = reinterpret_cast<const float *>(reinterpret_cast<const char *>(p.a) + bz * p.a_bs * (A16 ? 2 : 4));
         p.b = static_cast<const char *>(p.b) + bz * p.b_bs * (F16 ? 2 : 4);
         p.out += bz * p.c_bs;
         if (p.res) p.res += bz * p.c_bs;
@@ -163,12 +175,13 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
     const __amdgpu_buffer_rsrc_t a2_rsrc = make_rsrc(p.a2 ? p.a2 : p.a, p.a2 ? p.a2_bytes : p.a_bytes);
     const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(p.b, p.b_bytes);
     using BT = typename BChunk<F16, BVEC>::T;
-    floatx4 ra0[A_LD], ra1[A_LD];
+    using AT = std::conditional_t<A16, halfx4, floatx4>;
+    AT ra0[A_LD], ra1[A_LD];
     BT rb0[B_LD], rb1[B_LD];
     double ln_s1[A_LD], ln_s2[A_LD];  // kProLn: row sums of the f32 values as loaded (before rounding)
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) ln_s1[i] = ln_s2[i] = 0.0;
-    auto fetch = [&](int kt, floatx4 (&ra)[A_LD], BT (&rb)[B_LD]) {
+    auto fetch = [&](int kt, AT (&ra)[A_LD], BT (&rb)[B_LD]) {
         const int k0 = k_begin + kt * BKH;
         int tky = 0, tkx = 0, tci = 0;
         if (MODE == kConvAligned) {
@@ -181,11 +194,15 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
         // a tile past ka reads the second operand (whole tiles: ka % BKH == 0)
         const bool sec = MODE == kDense && p.a2 && k0 >= p.ka;
 #pragma unroll
-        for (int i = 0; i < A_LD; ++i)
-            ra[i] = sec ? load_a_h<MODE, PRO>(p, a2_rsrc, crow[i], m0 + lrow + 16 * i, k - p.ka, k_end - p.ka, tky, tkx,
-                                              tci, k0 - p.ka, p.lda2)
-                        : load_a_h<MODE, PRO>(p, a_rsrc, crow[i], m0 + lrow + 16 * i, k, k_end, tky, tkx, tci, k0);
-        if constexpr (PRO == kProLn) {
+        for (int i = 0; i < A_LD; ++i) {
+            if constexpr (A16)
+                ra[i] = load_a_f16(p, a_rsrc, m0 + lrow + 16 * i, k, k_end);
+            else
+                ra[i] = sec ? load_a_h<MODE, PRO>(p, a2_rsrc, crow[i], m0 + lrow + 16 * i, k - p.ka, k_end - p.ka, tky,
+                                                  tkx, tci, k0 - p.ka, p.lda2)
+                            : load_a_h<MODE, PRO>(p, a_rsrc, crow[i], m0 + lrow + 16 * i, k, k_end, tky, tkx, tci, k0);
+        }
+        if constexpr (PRO == kProLn && !A16) {
 #pragma unroll
             for (int i = 0; i < A_LD; ++i) {
                 const double a0 = ra[i][0], a1 = ra[i][1], a2 = ra[i][2], a3 = ra[i][3];
@@ -196,10 +213,10 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
 #pragma unroll
         for (int i = 0; i < B_LD; ++i) rb[i] = load_b_h<F16, BVEC>(p, b_rsrc, n0 + lrow + 16 * i, k, k_end);
     };
-    auto stash = [&](int buf, const floatx4 (&ra)[A_LD], const BT (&rb)[B_LD]) {
+    auto stash = [&](int buf, const AT (&ra)[A_LD], const BT (&rb)[B_LD]) {
 #pragma unroll
         for (int i = 0; i < A_LD; ++i)
-            *reinterpret_cast<halfx4 *>(As[buf] + (lrow + 16 * i) * LDS_H + lc * 4) = to_h4(ra[i]);
+            *reinterpret_cast<halfx4 *>(As[buf] + (lrow + 16 * i) * LDS_H + lc * 4) = as_h4(ra[i]);
 #pragma unroll
         for (int i = 0; i < B_LD; ++i)
             *reinterpret_cast<halfx4 *>(Bs[buf] + (lrow + 16 * i) * LDS_H + lc * 4) = as_h4(rb[i]);
@@ -378,6 +395,21 @@ void launch_tiles_h16(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
         launch_cfg_h16<128, 128, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
     else
         launch_cfg_h16<64, 64, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
+}
+
+// f16 A operands (launch_dense_h16_a16): one tiling, no K split.
+template <int BM, int BN>
+void launch_a16_cfg(Context &ctx, GemmArgs &p, int batch) {
+    const unsigned tiles = unsigned(ceil_div(p.M, BM) * ceil_div(p.N, BN));
+    log_gemm(ctx, "f16a", p, BM, BN, 1, kDense, kProNone, true, GemmEpilogue::None, batch);
+    const GemmTimer timer(ctx, "f16a", p, BM, BN, 2, 2, 1, 1, kDense, batch);
+    p.k_split = p.K;
+    p.vec_out = out_vec_ok(p, BM);
+    gn_partials_plan(p, BM, BN, 1, batch);
+    ln_partials_plan(p, BN, 1, batch);
+    const dim3 grid(tiles, unsigned(batch));
+    gemm_h16_kernel<BM, BN, kDense, kProNone, true, true, 0, false, true><<<grid, 256, 0, ctx.stream>>>(p);
+    MH_LAUNCH_CHECK();
 }
 
 template <int MODE, int PRO>

@@ -164,6 +164,11 @@ void ln_fold_weights(Context &ctx, const void *w, WeightType wt, int n, int k, c
 void gemm_nt(Context &ctx, const float *a, int64_t lda, int64_t a_bs, const void *b, WeightType wt, int64_t ldb,
              int64_t b_bs, int m, int n, int k, int batch, const float *bias, const float *residual, float *out,
              int64_t ldc, int64_t c_bs, GemmEpilogue epi = GemmEpilogue::None, int row_group = 0);
+// gemm_nt without bias or residual for FAST contexts whose A is already f16 ([m][lda]
+// halves, a_bs in halves) and whose B is f16: the products the f16 GEMM takes of f32
+// operands it rounds itself.
+void gemm_nt_a16(Context &ctx, const void *a, int64_t lda, int64_t a_bs, const void *b, int64_t ldb, int64_t b_bs,
+                 int m, int n, int k, int batch, float *out, int64_t ldc, int64_t c_bs);
 void im2col_gather(Context &ctx, const float *x, int n, int h, int w, int c, int stride, const int pad[4],
                    bool upsample2x, int64_t first, int64_t count, float *rows);
 
@@ -172,9 +177,10 @@ void im2col_gather(Context &ctx, const float *x, int n, int h, int w, int c, int
 int64_t winograd_tiles(int n, int h, int w, bool upsample2x);
 // weight [c_out][3][3][c_in] (f32 or f16) -> u [16][c_out][c_in] f32 (G g G^T).
 void winograd_weight_transform(Context &ctx, const void *weight, WeightType wt, int c_out, int c_in, float *u);
-// x [n,h,w,c] -> v [16][tiles][c] (B^T d B), prologue applied to in-image values.
+// x [n,h,w,c] -> v [16][tiles][c] (B^T d B), prologue applied to in-image values;
+// h16: v in f16, rounded to nearest even and saturated as the f16 GEMM rounds operands.
 void winograd_input_transform(Context &ctx, const float *x, int n, int h, int w, int c, bool upsample2x,
-                              const Affine *prologue, float *v);
+                              const Affine *prologue, void *v, bool h16 = false);
 // m [16][tiles][c_out] -> out [n, H, W, c_out] = A^T m A + bias (+ residual2).
 void winograd_output_transform(Context &ctx, const float *m, int n, int h, int w, int c_out, bool upsample2x,
                                const float *bias, const float *residual2, float *out);

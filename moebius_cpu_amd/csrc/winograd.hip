@@ -78,11 +78,25 @@ __global__ void wino_weight_kernel(const void *__restrict__ w, int co, int ci, f
 __device__ __forceinline__ float4 f4sub(float4 a, float4 b) { return make_float4(a.x - b.x, a.y - b.y, a.z - b.z, a.w - b.w); }
 __device__ __forceinline__ float4 f4add(float4 a, float4 b) { return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w); }
 
+// Four V values stored as f32, or (H16, FAST contexts whose plane GEMM takes
+// f16 operands) rounded to f16 as that GEMM rounds them: nearest even,
+// saturated at +-65504, NaN kept.
+template <bool H16>
+__device__ __forceinline__ void store_v4(void *v, int64_t i, float4 q) {
+    if constexpr (H16) {
+        typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+        auto r = [](float x) { return static_cast<_Float16>(__builtin_fabsf(x) > 65504.0f ? __builtin_copysignf(65504.0f, x) : x); };
+        *reinterpret_cast<half4 *>(static_cast<_Float16 *>(v) + i) = half4{r(q.x), r(q.y), r(q.z), r(q.w)};
+    } else {
+        *reinterpret_cast<float4 *>(static_cast<float *>(v) + i) = q;
+    }
+}
+
 // V [16][tiles][ci] (winograd.rs:299-327); one thread per (tile, 4 channels).
-template <bool PRO>
+template <bool PRO, bool H16>
 __global__ __launch_bounds__(256) void wino_input_kernel(const float *__restrict__ x, WinoGeo g, int ci,
                                                          const float *__restrict__ psc, const float *__restrict__ psh,
-                                                         int psilu, float *__restrict__ v) {
+                                                         int psilu, void *__restrict__ v) {
     const int c4 = ci >> 2;
     const int64_t e = blockIdx.x * int64_t(256) + threadIdx.x;
     if (e >= g.tiles * c4) return;
@@ -127,14 +141,14 @@ __global__ __launch_bounds__(256) void wino_input_kernel(const float *__restrict
         tt[12 + col] = f4sub(d1, d3);
     }
     const int64_t plane = g.tiles * ci;
-    float *dst = v + t * ci + c;
+    const int64_t dst = t * ci + c;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const float4 *q = tt + r * 4;
-        *reinterpret_cast<float4 *>(dst + (r * 4) * plane) = f4sub(q[0], q[2]);
-        *reinterpret_cast<float4 *>(dst + (r * 4 + 1) * plane) = f4add(q[1], q[2]);
-        *reinterpret_cast<float4 *>(dst + (r * 4 + 2) * plane) = f4sub(q[2], q[1]);
-        *reinterpret_cast<float4 *>(dst + (r * 4 + 3) * plane) = f4sub(q[1], q[3]);
+        store_v4<H16>(v, dst + (r * 4) * plane, f4sub(q[0], q[2]));
+        store_v4<H16>(v, dst + (r * 4 + 1) * plane, f4add(q[1], q[2]));
+        store_v4<H16>(v, dst + (r * 4 + 2) * plane, f4sub(q[2], q[1]));
+        store_v4<H16>(v, dst + (r * 4 + 3) * plane, f4sub(q[1], q[3]));
     }
 }
 
@@ -195,18 +209,21 @@ void winograd_weight_transform(Context &ctx, const void *weight, WeightType wt, 
 }
 
 void winograd_input_transform(Context &ctx, const float *x, int n, int h, int w, int c, bool upsample2x,
-                              const Affine *prologue, float *v) {
+                              const Affine *prologue, void *v, bool h16) {
     MH_REQUIRE(c % 4 == 0 && aligned16(x) && aligned16(v), "Winograd: channels must be a multiple of 4, 16-byte aligned");
     const WinoGeo g = wino_geo(n, h, w, upsample2x);
     if (g.tiles == 0) return;
     const unsigned blocks = blocks_for(g.tiles * (c / 4));
-    if (prologue) {
+    auto go = [&](auto kern) {
+        if (prologue)
+            kern<<<blocks, 256, 0, ctx.stream>>>(x, g, c, prologue->scale, prologue->shift, prologue->silu ? 1 : 0, v);
+        else
+            kern<<<blocks, 256, 0, ctx.stream>>>(x, g, c, nullptr, nullptr, 0, v);
+    };
+    if (prologue)
         MH_REQUIRE(aligned16(prologue->scale) && aligned16(prologue->shift), "Winograd: prologue must be 16-byte aligned");
-        wino_input_kernel<true><<<blocks, 256, 0, ctx.stream>>>(x, g, c, prologue->scale, prologue->shift,
-                                                                prologue->silu ? 1 : 0, v);
-    } else {
-        wino_input_kernel<false><<<blocks, 256, 0, ctx.stream>>>(x, g, c, nullptr, nullptr, 0, v);
-    }
+    if (h16) prologue ? go(wino_input_kernel<true, true>) : go(wino_input_kernel<false, true>);
+    else prologue ? go(wino_input_kernel<true, false>) : go(wino_input_kernel<false, false>);
     MH_LAUNCH_CHECK();
 }
 
@@ -236,15 +253,22 @@ void conv3x3_winograd(Context &ctx, const float *x, int n, int h, int w, int c_i
                                prologue, out, residual2, gn))
         return;
     // V and M share one workspace block; the batched GEMM (batch > 1) never splits K,
-    // so it does not touch the workspace itself.
-    const size_t vbytes = (size_t(16) * tiles * c_in * sizeof(float) + 255) & ~size_t(255);
+    // so it does not touch the workspace itself. FAST contexts with an f16 U take V in
+    // f16 too (tuning wino_v16): the transform rounds it as the plane GEMM would on
+    // every load, so the products are the same bits, from half the bytes.
+    const bool v16 = ut == kF16 && ctx.precision == Precision::Fast && ctx.tune.wino_v16;
+    const size_t vbytes = (size_t(16) * tiles * c_in * (v16 ? 2 : 4) + 255) & ~size_t(255);
     const size_t mbytes = size_t(16) * tiles * c_out * sizeof(float);
     char *ws = static_cast<char *>(ctx.ws.get(vbytes + mbytes, ctx.stream));
-    float *v = reinterpret_cast<float *>(ws);
+    void *v = ws;
     float *m = reinterpret_cast<float *>(ws + vbytes);
-    winograd_input_transform(ctx, x, n, h, w, c_in, upsample2x, prologue, v);
-    gemm_nt(ctx, v, c_in, tiles * c_in, u, ut, c_in, int64_t(c_out) * c_in, int(tiles), c_out, c_in, 16, nullptr,
-            nullptr, m, c_out, tiles * c_out);
+    winograd_input_transform(ctx, x, n, h, w, c_in, upsample2x, prologue, v, v16);
+    if (v16)
+        gemm_nt_a16(ctx, v, c_in, tiles * c_in, u, c_in, int64_t(c_out) * c_in, int(tiles), c_out, c_in, 16, m, c_out,
+                    tiles * c_out);
+    else
+        gemm_nt(ctx, static_cast<const float *>(v), c_in, tiles * c_in, u, ut, c_in, int64_t(c_out) * c_in, int(tiles),
+                c_out, c_in, 16, nullptr, nullptr, m, c_out, tiles * c_out);
     winograd_output_transform(ctx, m, n, h, w, c_out, upsample2x, bias, residual2, out);
 }
 

@@ -533,19 +533,23 @@ def test_unet_groupnorm_into_proj_in_is_bit_exact(ctx, gnet, fast, tune):
 
 def test_unet_fast_winograd_f16_kernel_is_bit_exact(ctx, gnet, tune):
     """FAST contexts read the upsample convs' Winograd kernel U stored in f16
-    (tuning wino_u16 1, the default): the bits of the plane GEMM rounding the f32
-    U as it loads it (0), since both round to nearest even with the same
-    saturation."""
+    (tuning wino_u16 1, the default) and write the input transform's V in f16
+    (wino_v16 1): the bits of the plane GEMM rounding the f32 U and V as it loads
+    them (both 0), since all round to nearest even with the same saturation."""
     inp = U.unet_input(seed=5019)
     ctx.set_precision(True)
     try:
         tune("wino_u16", "0")
         f32_u = gnet.forward_host(inp.x, inp.timestep, cfg=True)
         tune("wino_u16", "1")
+        tune("wino_v16", "0")
         f16_u = gnet.forward_host(inp.x, inp.timestep, cfg=True)
+        tune("wino_v16", "1")
+        f16_uv = gnet.forward_host(inp.x, inp.timestep, cfg=True)
     finally:
         ctx.set_precision(False)
     assert np.array_equal(f32_u, f16_u)
+    assert np.array_equal(f32_u, f16_uv)
 
 
 def test_unet_pool_stops_allocating(ctx, gnet):

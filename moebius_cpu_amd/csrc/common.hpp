@@ -56,7 +56,7 @@ struct ShapePlan {
 // (MOEBIUS_HIP_GEMM_PLAN, _GN_IN_MAXC, _DW_TILED, _TAP_HEADS, _CROSS_HEADS,
 // _GN_BLOCKS, _GN_APPLY, _WINO_FUSED, _UP_CONCAT, _LAMBDA_TAPS, _GEMM_LOG,
 // _GEMM_WIDE, _LN_FOLD, _TAP_SPLIT, _GEMM_TIME, _TAPS_ROWS, _CROSS_MFMA, _TAP_SLICE,
-// _TAP_JQ, _TAP_FUSED, _GEMM_SHAPE_PLAN, _TAPS_R16, _WINO_U16, _WINO_V16)
+// _TAP_JQ, _TAP_FUSED, _GEMM_SHAPE_PLAN, _TAPS_R16, _WINO_U16, _WINO_V16, _DW_OUT16)
 // when a context is created and changed with set_tuning (mh_context_set_tuning).
 // The defaults are the measured choices; nothing on the hot path reads the
 // environment.
@@ -97,6 +97,7 @@ struct Tuning {
     int wino_u16 = 1;      // FAST contexts: the UNet's Winograd plane GEMMs read U stored in f16 (0: f32,
                            // rounded on every load; the same products)
     int wino_v16 = 1;      // FAST contexts with an f16 U: the input transform writes V in f16 (0: f32)
+    int dw_out16 = 1;      // FAST contexts: depthwise convs read only by an f16 GEMM write f16 (0: f32)
 };
 // Sets `key` from its text form (the environment variable's syntax); value NULL
 // or "" restores the default. False for an unknown key or a malformed value.

@@ -119,6 +119,7 @@ bool set_tuning(Tuning &t, const char *key, const char *value) {
     if (k == "taps_r16") return to_int(t.taps_r16, 0) && t.taps_r16 >= 0 && t.taps_r16 <= 1;
     if (k == "wino_u16") return to_int(t.wino_u16, 1) && t.wino_u16 >= 0 && t.wino_u16 <= 1;
     if (k == "wino_v16") return to_int(t.wino_v16, 1) && t.wino_v16 >= 0 && t.wino_v16 <= 1;
+    if (k == "dw_out16") return to_int(t.dw_out16, 1) && t.dw_out16 >= 0 && t.dw_out16 <= 1;
     if (k == "tap_jq") return to_int(t.tap_jq, 1) && (t.tap_jq == 1 || t.tap_jq == 2);
     if (k == "tap_slice") return to_int(t.tap_slice, 0) && t.tap_slice >= 0 && t.tap_slice <= 64;
     if (k == "cross_mfma") return to_int(t.cross_mfma, 1) && t.cross_mfma >= 0 && t.cross_mfma <= 1;
@@ -170,6 +171,7 @@ Context::Context(int dev) : device(dev) {
                                               {"MOEBIUS_HIP_TAPS_R16", "taps_r16"},
                                               {"MOEBIUS_HIP_WINO_U16", "wino_u16"},
                                               {"MOEBIUS_HIP_WINO_V16", "wino_v16"},
+                                              {"MOEBIUS_HIP_DW_OUT16", "dw_out16"},
                                               {"MOEBIUS_HIP_LN_FOLD", "ln_fold"},
                                               {"MOEBIUS_HIP_TAP_SPLIT", "tap_split"}};
     for (const auto &kv : env_keys)

@@ -162,11 +162,14 @@ constexpr int kDwNP = (kDwTH + 2) * (kDwTW + 2);
 
 // x2 (optional): the input is [x | x2] per pixel, x holding quads [0, cv1)
 // (cv1 a multiple of kDwCQ, so a block reads one of the two) and x2 the rest.
-template <int EPI, bool PRO, bool FM>
+// OUT16 (FAST contexts whose only reader is an f16 GEMM): the output rounded to
+// f16 as that GEMM rounds its f32 operands (nearest even, saturated at
+// +-65504), so the products are the same bits from half the bytes.
+template <int EPI, bool PRO, bool FM, bool OUT16 = false>
 __global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__restrict__ x, int n, int h, int w,
                                                              int cv, const float4 *__restrict__ wt,
                                                              const float4 *__restrict__ bias, DwPrologue pro,
-                                                             float4 *__restrict__ out,
+                                                             void *__restrict__ out,
                                                              const float4 *__restrict__ x2, int cv1) {
     using V = Vec<4>;
     // GLU (EPI 2) convolves two input halves. They pass through one LDS tile in
@@ -283,7 +286,7 @@ __global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__res
         }
     }
     if (!active) return;
-    float4 *dst = out + (size_t(b) * h + oy) * size_t(w) * co_v + q;
+    const size_t o0 = (size_t(b) * h + oy) * size_t(w) * co_v + q;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int ox = ox0 + c0 + j;
@@ -292,16 +295,28 @@ __global__ __launch_bounds__(256) void depthwise_tile_kernel(const float4 *__res
         if (EPI == 2) y = V::template glu<FM>(acc[0][j], acc[PARTS - 1][j]);
         else if (EPI == 1) y = V::relu(acc[0][j]);
         else y = acc[0][j];
-        dst[size_t(ox) * co_v] = y;
+        if constexpr (OUT16) {
+            typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+            auto r16 = [](float v) {
+                return static_cast<_Float16>(__builtin_fabsf(v) > 65504.0f ? __builtin_copysignf(65504.0f, v) : v);
+            };
+            static_cast<half4 *>(out)[o0 + size_t(ox) * co_v] = half4{r16(y.x), r16(y.y), r16(y.z), r16(y.w)};
+        } else {
+            static_cast<float4 *>(out)[o0 + size_t(ox) * co_v] = y;
+        }
     }
 }
 
 template <int EPI, bool PRO>
-void launch_dw_tile_fm(bool fast, dim3 grid, hipStream_t st, const float4 *x, int n, int h, int w, int cv,
-                       const float4 *wt, const float4 *bias, const DwPrologue &pro, float4 *out, const float4 *x2,
-                       int cv1) {
-    if (fast) depthwise_tile_kernel<EPI, PRO, true><<<grid, 256, 0, st>>>(x, n, h, w, cv, wt, bias, pro, out, x2, cv1);
-    else depthwise_tile_kernel<EPI, PRO, false><<<grid, 256, 0, st>>>(x, n, h, w, cv, wt, bias, pro, out, x2, cv1);
+void launch_dw_tile_fm(bool fast, bool out16, dim3 grid, hipStream_t st, const float4 *x, int n, int h, int w,
+                       int cv, const float4 *wt, const float4 *bias, const DwPrologue &pro, void *out,
+                       const float4 *x2, int cv1) {
+    if (out16)
+        depthwise_tile_kernel<EPI, PRO, true, true><<<grid, 256, 0, st>>>(x, n, h, w, cv, wt, bias, pro, out, x2, cv1);
+    else if (fast)
+        depthwise_tile_kernel<EPI, PRO, true><<<grid, 256, 0, st>>>(x, n, h, w, cv, wt, bias, pro, out, x2, cv1);
+    else
+        depthwise_tile_kernel<EPI, PRO, false><<<grid, 256, 0, st>>>(x, n, h, w, cv, wt, bias, pro, out, x2, cv1);
 }
 
 template <int VW, int TX, int EPI, bool PRO, typename T>
@@ -313,7 +328,8 @@ void launch_dw_fm(bool fast, unsigned blocks, hipStream_t st, const T *x, int n,
 
 template <bool PRO>
 void launch_dw_tile(Context &ctx, const float *x, int n, int h, int w, int c, const float *wt, const float *bias,
-                    int epilogue, const DwPrologue &pro, float *out, const float *x2 = nullptr, int c2 = 0) {
+                    int epilogue, const DwPrologue &pro, void *out, const float *x2 = nullptr, int c2 = 0,
+                    bool out16 = false) {
     const int cv = c / 4;
     const int co_v = epilogue == 2 ? cv / 2 : cv;
     const int64_t tiles = int64_t(n) * ceil_div(h, kDwTH) * ceil_div(w, kDwTW);
@@ -322,15 +338,15 @@ void launch_dw_tile(Context &ctx, const float *x, int n, int h, int w, int c, co
     const float4 *xv = reinterpret_cast<const float4 *>(x);
     const float4 *wv = reinterpret_cast<const float4 *>(wt);
     const float4 *bv = reinterpret_cast<const float4 *>(bias);
-    float4 *ov = reinterpret_cast<float4 *>(out);
     const float4 *x2v = reinterpret_cast<const float4 *>(x2);
     const int cv1 = (c - c2) / 4;
     const bool fast = ctx.precision == Precision::Fast;
+    MH_REQUIRE(!out16 || fast, "depthwise: f16 output in FAST contexts only");
     switch (epilogue) {
         // FAST contexts take fast_silu for the GLU gate and the prologue's SiLU
-        case 0: launch_dw_tile_fm<0, PRO>(fast, grid, ctx.stream, xv, n, h, w, cv, wv, bv, pro, ov, x2v, cv1); break;
-        case 1: launch_dw_tile_fm<1, PRO>(fast, grid, ctx.stream, xv, n, h, w, cv, wv, bv, pro, ov, x2v, cv1); break;
-        default: launch_dw_tile_fm<2, PRO>(fast, grid, ctx.stream, xv, n, h, w, cv, wv, bv, pro, ov, x2v, cv1); break;
+        case 0: launch_dw_tile_fm<0, PRO>(fast, out16, grid, ctx.stream, xv, n, h, w, cv, wv, bv, pro, out, x2v, cv1); break;
+        case 1: launch_dw_tile_fm<1, PRO>(fast, out16, grid, ctx.stream, xv, n, h, w, cv, wv, bv, pro, out, x2v, cv1); break;
+        default: launch_dw_tile_fm<2, PRO>(fast, out16, grid, ctx.stream, xv, n, h, w, cv, wv, bv, pro, out, x2v, cv1); break;
     }
     MH_LAUNCH_CHECK();
 }
@@ -358,6 +374,30 @@ void launch_dw(Context &ctx, const float *x, int n, int h, int w, int c, const f
 }
 
 }  // namespace
+
+bool depthwise3x3_h16(Context &ctx, const float *x, int n, int h, int w, int c, const float *weight,
+                      const float *bias, int epilogue, void *out16, const Affine *prologue, const float *x2, int c2) {
+    MH_REQUIRE(epilogue >= 0 && epilogue <= 2, "depthwise: unknown epilogue");
+    if (ctx.precision != Precision::Fast || !ctx.tune.dw_tiled) return false;
+    const int co = epilogue == 2 ? c / 2 : c;
+    if (epilogue == 2 && (c % 2 || x2)) return false;
+    if (x2 && (c2 <= 0 || c2 >= c || (c - c2) % (4 * kDwCQ) != 0 || c2 % 4 != 0)) return false;
+    if (co % 4 || !aligned16(x) || !aligned16(x2) || !aligned16(weight) || !aligned16(bias) ||
+        (reinterpret_cast<uintptr_t>(out16) & 7) || (prologue && (!aligned16(prologue->scale) ||
+                                                                  !aligned16(prologue->shift))))
+        return false;
+    if (int64_t(n) * h * w * c == 0) return true;
+    DwPrologue pro;
+    if (prologue) {
+        pro.scale = prologue->scale;
+        pro.shift = prologue->shift;
+        pro.silu = prologue->silu ? 1 : 0;
+        launch_dw_tile<true>(ctx, x, n, h, w, c, weight, bias, epilogue, pro, out16, x2, c2, true);
+    } else {
+        launch_dw_tile<false>(ctx, x, n, h, w, c, weight, bias, epilogue, pro, out16, x2, c2, true);
+    }
+    return true;
+}
 
 void depthwise3x3(Context &ctx, const float *x, int n, int h, int w, int c, const float *weight, const float *bias,
                   int epilogue, float *out, const Affine *prologue, const float *x2, int c2) {

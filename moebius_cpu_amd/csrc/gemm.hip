@@ -287,6 +287,48 @@ void gemm_nt_a16(Context &ctx, const void *a, int64_t lda, int64_t a_bs, const v
     gemm::launch_dense_h16_a16(ctx, p, batch);
 }
 
+void conv1x1_a16(Context &ctx, const void *x16, int64_t pixels, int c_in, const void *weight, int c_out,
+                 const float *bias, const float *residual, float *out, const ResidualAffine *raff,
+                 const float *residual2, GnPartials *gn) {
+    if (gn) gn->rows = 0;
+    MH_REQUIRE(ctx.precision == Precision::Fast, "Conv1x1 (f16 input): FAST contexts only");
+    MH_REQUIRE(pixels < (int64_t(1) << 31), "Conv1x1: too many pixels");
+    MH_REQUIRE(c_in % 4 == 0 && (reinterpret_cast<uintptr_t>(x16) & 7) == 0 &&
+                   (reinterpret_cast<uintptr_t>(weight) & 7) == 0,
+               "Conv1x1 (f16 input): rows of whole, 8-byte aligned 4-channel chunks");
+    if (raff)
+        MH_REQUIRE(residual && raff->scale && raff->shift && raff->rows_per_item > 0,
+                   "Conv1x1: residual transform needs the residual, scale, shift and rows per item");
+    if (pixels == 0) return;
+    GemmArgs p{};
+    p.a = static_cast<const float *>(x16);  // halves: the A16 kernels read it as such
+    p.lda = c_in;
+    p.M = int(pixels);
+    p.N = c_out;
+    p.K = c_in;
+    p.b = weight;
+    p.ldb = c_in;
+    p.a_bytes = extent(pixels, c_in, c_in, 2);
+    p.b_bytes = extent(c_out, c_in, c_in, 2);
+    p.bias = bias;
+    p.res = residual;
+    p.out = out;
+    p.ldc = c_out;
+    if (raff) {
+        p.rsc = raff->scale;
+        p.rsh = raff->shift;
+        p.rsilu = raff->silu ? 1 : 0;
+        p.r_rows = raff->rows_per_item;
+    }
+    p.res2 = residual2;
+    if (gn) {
+        p.gnp = gn->part;
+        p.gn_item_rows = gn->item_rows;
+    }
+    gemm::launch_dense_h16_a16(ctx, p, 1);
+    if (gn) gn->rows = p.gn_rows;
+}
+
 void conv3x3_output_hw(int h, int w, int stride, const int pad[4], bool upsample2x, int *ho, int *wo) {
     const int up = upsample2x ? 2 : 1;
     const int hh = h * up + pad[0] + pad[2] - 3, ww = w * up + pad[1] + pad[3] - 3;

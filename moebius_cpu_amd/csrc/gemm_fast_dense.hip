@@ -13,10 +13,12 @@ void launch_dense_h16(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi
 }
 
 void launch_dense_h16_a16(Context &ctx, GemmArgs &p, int batch) {
-    const Plan pl = plan_h16(p.M, p.N, p.K, int(ceil_div(ctx.cu_count, batch)), true);
-    if (pl.bm == 32) launch_a16_cfg<32, 32>(ctx, p, batch);
-    else if (pl.bm == 128) launch_a16_cfg<128, 128>(ctx, p, batch);
-    else launch_a16_cfg<64, 64>(ctx, p, batch);
+    Plan pl = plan_h16(p.M, p.N, p.K, int(ceil_div(ctx.cu_count, batch)), true);
+    if (batch > 1) pl.splits = 1;
+    if (pl.splits == 1) pl.k_split = p.K;
+    if (pl.bm == 32) launch_a16_cfg<32, 32>(ctx, p, pl, batch);
+    else if (pl.bm == 128) launch_a16_cfg<128, 128>(ctx, p, pl, batch);
+    else launch_a16_cfg<64, 64>(ctx, p, pl, batch);
 }
 
 }  // namespace gemm

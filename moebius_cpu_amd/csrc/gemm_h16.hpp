@@ -29,7 +29,7 @@ typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 // Launchers of the fast kernels (gemm_fast_dense.hip, gemm_fast_conv.hip).
 void launch_dense_h16(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi, int batch, bool vec);
 // Dense A stored in f16 (GemmArgs::a holds halves; a_bs, lda in halves), f16
-// vector weights, no prologue or epilogue beyond bias and residual, no K split.
+// vector weights, no prologue, no SiLU epilogue.
 void launch_dense_h16_a16(Context &ctx, GemmArgs &p, int batch);
 void launch_dense_pro_h16(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi);
 void launch_dense_ln_h16(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi);
@@ -397,12 +397,32 @@ void launch_tiles_h16(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
         launch_cfg_h16<64, 64, MODE, PRO, F16, BVEC>(ctx, p, pl, epi, batch);
 }
 
-// f16 A operands (launch_dense_h16_a16): one tiling, no K split.
+// f16 A operands (launch_dense_h16_a16): the planner's tiling and K split, as
+// launch_cfg_h16 runs them for f32 A.
 template <int BM, int BN>
-void launch_a16_cfg(Context &ctx, GemmArgs &p, int batch) {
+void launch_a16_cfg(Context &ctx, GemmArgs &p, const Plan &pl, int batch) {
     const unsigned tiles = unsigned(ceil_div(p.M, BM) * ceil_div(p.N, BN));
-    log_gemm(ctx, "f16a", p, BM, BN, 1, kDense, kProNone, true, GemmEpilogue::None, batch);
-    const GemmTimer timer(ctx, "f16a", p, BM, BN, 2, 2, 1, 1, kDense, batch);
+    log_gemm(ctx, "f16a", p, BM, BN, pl.splits, kDense, kProNone, true, GemmEpilogue::None, batch);
+    const GemmTimer timer(ctx, "f16a", p, BM, BN, 2, 2, 1, pl.splits, kDense, batch);
+    if (pl.splits > 1) {
+        p.partial = static_cast<float *>(ctx.ws.get(size_t(pl.splits) * p.M * p.N * sizeof(float), ctx.stream));
+        p.k_split = pl.k_split;
+        p.vec_out = (p.N & 3) == 0 && (reinterpret_cast<uintptr_t>(p.partial) & 15) == 0;
+        gn_partials_plan(p, BM, BN, pl.splits, batch);
+        ln_partials_plan(p, BN, pl.splits, batch);
+        gemm_h16_kernel<BM, BN, kDense, kProNone, true, true, 0, true, true>
+            <<<dim3(tiles, 1, pl.splits), 256, 0, ctx.stream>>>(p);
+        MH_LAUNCH_CHECK();
+        const int64_t total = int64_t(p.M) * p.N;
+        if (reduce_vec_ok(p))
+            splitk_reduce_kernel<0, true, true>
+                <<<unsigned(std::min<int64_t>(ceil_div(total / 4, 256), 8192)), 256, 0, ctx.stream>>>(p, pl.splits);
+        else
+            splitk_reduce_kernel<0, false, true>
+                <<<unsigned(std::min<int64_t>(ceil_div(total, 256), 8192)), 256, 0, ctx.stream>>>(p, pl.splits);
+        MH_LAUNCH_CHECK();
+        return;
+    }
     p.k_split = p.K;
     p.vec_out = out_vec_ok(p, BM);
     gn_partials_plan(p, BM, BN, 1, batch);

@@ -96,6 +96,12 @@ void resize_u8(Context &ctx, const uint8_t *src, int from_w, int from_h, int to_
 void depthwise3x3(Context &ctx, const float *x, int n, int h, int w, int c, const float *weight, const float *bias,
                   int epilogue, float *out, const Affine *prologue = nullptr, const float *x2 = nullptr,
                   int c2 = 0);
+// depthwise3x3 writing out16 in f16 (nearest even, saturated: the f16 GEMM's operand
+// rounding), for FAST contexts whose only reader of the output is an f16 GEMM. False
+// (nothing launched) where the tiled kernel does not take the shape or alignment.
+bool depthwise3x3_h16(Context &ctx, const float *x, int n, int h, int w, int c, const float *weight,
+                      const float *bias, int epilogue, void *out16, const Affine *prologue = nullptr,
+                      const float *x2 = nullptr, int c2 = 0);
 
 // ---- GEMM-shaped convs (gemm.hip) ----
 // Per item and channel transform of a GEMM residual: res' = [SiLU](res . scale + shift),
@@ -125,6 +131,13 @@ void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void 
              const ResidualAffine *raff = nullptr, const float *residual2 = nullptr, GnPartials *gn = nullptr,
              const ResidualAffine *x_aff = nullptr, const float *x2 = nullptr, int c2 = 0,
              LnRowPartials *lnp = nullptr);
+// conv1x1 for FAST contexts whose input is already f16 ([pixels][c_in] halves, e.g.
+// from depthwise3x3_h16) and whose weight is f16: the products of the f16 GEMM on f32
+// input it rounds itself, with the same epilogue (bias, residual and its transform,
+// residual2, GroupNorm partials).
+void conv1x1_a16(Context &ctx, const void *x16, int64_t pixels, int c_in, const void *weight, int c_out,
+                 const float *bias, const float *residual, float *out, const ResidualAffine *raff = nullptr,
+                 const float *residual2 = nullptr, GnPartials *gn = nullptr);
 // residual2 (optional, [n, ho, wo, c_out]) is added last: out = (bias + conv) + residual2.
 void conv3x3(Context &ctx, const float *x, int n, int h, int w, int c_in, const void *weight, WeightType wt,
              int c_out, const float *bias, int stride, const int pad[4], bool upsample2x, const Affine *prologue,

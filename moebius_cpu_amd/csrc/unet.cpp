@@ -334,6 +334,12 @@ struct LNp {
 };
 
 // src/unet/blocks.rs:31-54: pw1x1(relu(dw3x3(x) + b1)) + b2 (+ x when c_in == c_out)
+// FAST contexts: a depthwise conv whose output only the next 1x1 reads writes it
+// in f16 (depthwise3x3_h16) for that 1x1 to read as f16 (conv1x1_a16): the
+// products the f16 GEMM would take of the f32 output, from half the bytes. Needs
+// the 1x1's weight in f16 (tuning dw_out16 0: f32 output).
+bool dw_h16(const Env &e, const DParam &pw) { return e.ctx.tune.dw_out16 && pw.wt == kF16; }
+
 struct DwConv2d {
     int ci = 0, co = 0;
     const float *dw = nullptr, *dwb = nullptr;
@@ -347,11 +353,15 @@ struct DwConv2d {
     // res2: added last (the resnet's shortcut). out: caller's buffer or a new tensor.
     DT fwd(Env &e, const DT &x, const float *res2 = nullptr, float *out_p = nullptr) const {
         DT mid = e.pool.tensor(x.n, x.h, x.w, x.c);
-        depthwise3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, dw, dwb, 1, mid.p);
-        DT out = out_p ? DT{out_p, x.n, x.h, x.w, co} : e.pool.tensor(x.n, x.h, x.w, co);
         const DParam wd = pw.w.at(e.ctx);
-        conv1x1(e.ctx, mid.p, mid.px(), ci, wd.p, wd.wt, co, pw.b, ci == co ? x.p : nullptr, out.p,
-                GemmEpilogue::None, nullptr, res2);
+        const bool h16 = dw_h16(e, wd) && depthwise3x3_h16(e.ctx, x.p, x.n, x.h, x.w, x.c, dw, dwb, 1, mid.p);
+        if (!h16) depthwise3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, dw, dwb, 1, mid.p);
+        DT out = out_p ? DT{out_p, x.n, x.h, x.w, co} : e.pool.tensor(x.n, x.h, x.w, co);
+        if (h16)
+            conv1x1_a16(e.ctx, mid.p, mid.px(), ci, wd.p, co, pw.b, ci == co ? x.p : nullptr, out.p, nullptr, res2);
+        else
+            conv1x1(e.ctx, mid.p, mid.px(), ci, wd.p, wd.wt, co, pw.b, ci == co ? x.p : nullptr, out.p,
+                    GemmEpilogue::None, nullptr, res2);
         e.pool.recycle(mid);
         return out;
     }
@@ -372,13 +382,19 @@ struct DwConv2d {
         aff.shift = ss + int64_t(xa.n) * cc;
         aff.silu = true;
         DT mid = e.pool.tensor(xa.n, xa.h, xa.w, cc);
-        depthwise3x3(e.ctx, xa.p, xa.n, xa.h, xa.w, cc, dw, dwb, 1, mid.p, &aff, xb.p, xb.c);
+        const DParam wd = pw.w.at(e.ctx);
+        const bool h16 = dw_h16(e, wd) &&
+                         depthwise3x3_h16(e.ctx, xa.p, xa.n, xa.h, xa.w, cc, dw, dwb, 1, mid.p, &aff, xb.p, xb.c);
+        if (!h16) depthwise3x3(e.ctx, xa.p, xa.n, xa.h, xa.w, cc, dw, dwb, 1, mid.p, &aff, xb.p, xb.c);
         DT out = e.pool.tensor(xa.n, xa.h, xa.w, co);
         GnPartials gp;
         if (gn_out) gp = gn_request(e, xa, co);
-        const DParam wd = pw.w.at(e.ctx);
-        conv1x1(e.ctx, mid.p, mid.px(), ci, wd.p, wd.wt, co, pw.b, nullptr, out.p, GemmEpilogue::None, nullptr,
-                nullptr, gn_out ? &gp : nullptr);
+        if (h16)
+            conv1x1_a16(e.ctx, mid.p, mid.px(), ci, wd.p, co, pw.b, nullptr, out.p, nullptr, nullptr,
+                        gn_out ? &gp : nullptr);
+        else
+            conv1x1(e.ctx, mid.p, mid.px(), ci, wd.p, wd.wt, co, pw.b, nullptr, out.p, GemmEpilogue::None, nullptr,
+                    nullptr, gn_out ? &gp : nullptr);
         if (gn_out) gn_attach(e, out, gp);
         e.pool.recycle(mid);
         return out;
@@ -390,7 +406,9 @@ struct DwConv2d {
         aff.shift = ss + int64_t(x.n) * x.c;
         aff.silu = true;
         DT mid = e.pool.tensor(x.n, x.h, x.w, x.c);
-        depthwise3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, dw, dwb, 1, mid.p, &aff);
+        const DParam wd = pw.w.at(e.ctx);
+        const bool h16 = dw_h16(e, wd) && depthwise3x3_h16(e.ctx, x.p, x.n, x.h, x.w, x.c, dw, dwb, 1, mid.p, &aff);
+        if (!h16) depthwise3x3(e.ctx, x.p, x.n, x.h, x.w, x.c, dw, dwb, 1, mid.p, &aff);
         DT out = out_p ? DT{out_p, x.n, x.h, x.w, co} : e.pool.tensor(x.n, x.h, x.w, co);
         ResidualAffine ra;
         ra.scale = aff.scale;
@@ -399,9 +417,12 @@ struct DwConv2d {
         ra.rows_per_item = x.h * x.w;
         GnPartials gp;
         if (gn_out) gp = gn_request(e, x, co);
-        const DParam wd = pw.w.at(e.ctx);
-        conv1x1(e.ctx, mid.p, mid.px(), ci, wd.p, wd.wt, co, pw.b, ci == co ? x.p : nullptr, out.p,
-                GemmEpilogue::None, ci == co ? &ra : nullptr, res2, gn_out ? &gp : nullptr);
+        if (h16)
+            conv1x1_a16(e.ctx, mid.p, mid.px(), ci, wd.p, co, pw.b, ci == co ? x.p : nullptr, out.p,
+                        ci == co ? &ra : nullptr, res2, gn_out ? &gp : nullptr);
+        else
+            conv1x1(e.ctx, mid.p, mid.px(), ci, wd.p, wd.wt, co, pw.b, ci == co ? x.p : nullptr, out.p,
+                    GemmEpilogue::None, ci == co ? &ra : nullptr, res2, gn_out ? &gp : nullptr);
         if (gn_out) gn_attach(e, out, gp);
         e.pool.recycle(mid);
         return out;
@@ -806,9 +827,17 @@ struct MixTransformer {
             e.pool.recycle(t);
         }
         DT g = e.pool.tensor(a.n, a.h, a.w, hidden);
-        depthwise3x3(e.ctx, a.p, a.n, a.h, a.w, a.c, dw, dwb, 2, g.p);
+        const DParam pwd = point.w.at(e.ctx);
+        const bool h16 = dw_h16(e, pwd) && depthwise3x3_h16(e.ctx, a.p, a.n, a.h, a.w, a.c, dw, dwb, 2, g.p);
+        if (!h16) depthwise3x3(e.ctx, a.p, a.n, a.h, a.w, a.c, dw, dwb, 2, g.p);
         e.pool.recycle(a);
-        DT u = point.fwd(e, g, &h);
+        DT u;
+        if (h16) {
+            u = e.pool.tensor(g.n, g.h, g.w, point.co);
+            conv1x1_a16(e.ctx, g.p, g.px(), point.ci, pwd.p, point.co, point.b, h.p, u.p);
+        } else {
+            u = point.fwd(e, g, &h);
+        }
         e.pool.recycle(g);
         e.pool.recycle(h);
         DT out = proj_out.fwd_gnp(e, u, &xr);

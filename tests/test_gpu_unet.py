@@ -531,25 +531,26 @@ def test_unet_groupnorm_into_proj_in_is_bit_exact(ctx, gnet, fast, tune):
     assert np.array_equal(apart, fused)
 
 
-def test_unet_fast_winograd_f16_kernel_is_bit_exact(ctx, gnet, tune):
-    """FAST contexts read the upsample convs' Winograd kernel U stored in f16
-    (tuning wino_u16 1, the default) and write the input transform's V in f16
-    (wino_v16 1): the bits of the plane GEMM rounding the f32 U and V as it loads
-    them (both 0), since all round to nearest even with the same saturation."""
+def test_unet_fast_f16_operands_are_bit_exact(ctx, gnet, tune):
+    """FAST contexts store in f16 what only an f16 GEMM reads: the upsample convs'
+    Winograd kernel U (tuning wino_u16) and input transform V (wino_v16), and the
+    depthwise convs' outputs that only the next 1x1 reads (dw_out16; the resnets'
+    DwConv2d and the MixFFN's GLU). Each is rounded to nearest even with the
+    saturation the f16 GEMM applies to f32 operands as it loads them, so every
+    combination gives the bits of all three off."""
     inp = U.unet_input(seed=5019)
     ctx.set_precision(True)
+    outs = []
     try:
-        tune("wino_u16", "0")
-        f32_u = gnet.forward_host(inp.x, inp.timestep, cfg=True)
-        tune("wino_u16", "1")
-        tune("wino_v16", "0")
-        f16_u = gnet.forward_host(inp.x, inp.timestep, cfg=True)
-        tune("wino_v16", "1")
-        f16_uv = gnet.forward_host(inp.x, inp.timestep, cfg=True)
+        for u16, v16, dw16 in ((0, 0, 0), (1, 0, 0), (1, 1, 0), (0, 0, 1), (1, 1, 1)):
+            tune("wino_u16", u16)
+            tune("wino_v16", v16)
+            tune("dw_out16", dw16)
+            outs.append(gnet.forward_host(inp.x, inp.timestep, cfg=True))
     finally:
         ctx.set_precision(False)
-    assert np.array_equal(f32_u, f16_u)
-    assert np.array_equal(f32_u, f16_uv)
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
 
 
 def test_unet_pool_stops_allocating(ctx, gnet):

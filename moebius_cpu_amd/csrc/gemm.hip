@@ -289,7 +289,7 @@ void gemm_nt_a16(Context &ctx, const void *a, int64_t lda, int64_t a_bs, const v
 
 void conv1x1_a16(Context &ctx, const void *x16, int64_t pixels, int c_in, const void *weight, int c_out,
                  const float *bias, const float *residual, float *out, const ResidualAffine *raff,
-                 const float *residual2, GnPartials *gn) {
+                 const float *residual2, GnPartials *gn, bool out16) {
     if (gn) gn->rows = 0;
     MH_REQUIRE(ctx.precision == Precision::Fast, "Conv1x1 (f16 input): FAST contexts only");
     MH_REQUIRE(pixels < (int64_t(1) << 31), "Conv1x1: too many pixels");
@@ -325,7 +325,7 @@ void conv1x1_a16(Context &ctx, const void *x16, int64_t pixels, int c_in, const 
         p.gnp = gn->part;
         p.gn_item_rows = gn->item_rows;
     }
-    gemm::launch_dense_h16_a16(ctx, p, 1);
+    gemm::launch_dense_h16_a16(ctx, p, 1, out16);
     if (gn) gn->rows = p.gn_rows;
 }
 

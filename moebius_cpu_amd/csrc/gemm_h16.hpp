@@ -29,8 +29,9 @@ typedef _Float16 halfx8 __attribute__((ext_vector_type(8)));
 // Launchers of the fast kernels (gemm_fast_dense.hip, gemm_fast_conv.hip).
 void launch_dense_h16(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi, int batch, bool vec);
 // Dense A stored in f16 (GemmArgs::a holds halves; a_bs, lda in halves), f16
-// vector weights, no prologue, no SiLU epilogue.
-void launch_dense_h16_a16(Context &ctx, GemmArgs &p, int batch);
+// vector weights, no prologue, no SiLU epilogue; out16: the output in f16 too
+// (GemmArgs::out holds halves, rounded as the f16 GEMM rounds f32 operands).
+void launch_dense_h16_a16(Context &ctx, GemmArgs &p, int batch, bool out16 = false);
 void launch_dense_pro_h16(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi);
 void launch_dense_ln_h16(Context &ctx, GemmArgs &p, WeightType wt, GemmEpilogue epi);
 void launch_conv_h16(Context &ctx, GemmArgs &p, WeightType wt, int mode, bool pro);
@@ -131,7 +132,8 @@ __device__ __forceinline__ halfx4 load_a_f16(const GemmArgs &p, __amdgpu_buffer_
     return __builtin_bit_cast(halfx4, raw);
 }
 
-template <int BM, int BN, int MODE, int PRO, bool F16, bool BVEC, int EPI, bool SPLIT, bool A16 = false>
+template <int BM, int BN, int MODE, int PRO, bool F16, bool BVEC, int EPI, bool SPLIT, bool A16 = false,
+          bool OUT16 = false>
 __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
     static_assert(!A16 || (MODE == kDense && PRO == kProNone), "f16 A operands: dense, no prologue");
     constexpr int MF = mf_for<BM, BN>();
@@ -284,7 +286,7 @@ __global__ __launch_bounds__(256) void gemm_h16_kernel(GemmArgs p) {
     if constexpr (PRO == kProLn) ln_row_stats<A_LD, 16, KCH, BM>(p, ln_s1, ln_s2, lrow, lc, ln_st);
     if constexpr (PRO == kProLnPart) ln_stats_from_parts<BM, 256>(p, m0, ln_st);
     __syncthreads();
-    write_tile<BM, BN, 2, 2, 1, MF, EPI, SPLIT, true>(p, reinterpret_cast<float *>(smem), acc, m0, n0, ti.z,
+    write_tile<BM, BN, 2, 2, 1, MF, EPI, SPLIT, true, OUT16>(p, reinterpret_cast<float *>(smem), acc, m0, n0, ti.z,
                                                 PRO >= kProLn ? ln_st : nullptr);
 }
 
@@ -399,7 +401,7 @@ void launch_tiles_h16(Context &ctx, GemmArgs &p, GemmEpilogue epi, int batch) {
 
 // f16 A operands (launch_dense_h16_a16): the planner's tiling and K split, as
 // launch_cfg_h16 runs them for f32 A.
-template <int BM, int BN>
+template <int BM, int BN, bool OUT16>
 void launch_a16_cfg(Context &ctx, GemmArgs &p, const Plan &pl, int batch) {
     const unsigned tiles = unsigned(ceil_div(p.M, BM) * ceil_div(p.N, BN));
     log_gemm(ctx, "f16a", p, BM, BN, pl.splits, kDense, kProNone, true, GemmEpilogue::None, batch);
@@ -410,14 +412,15 @@ void launch_a16_cfg(Context &ctx, GemmArgs &p, const Plan &pl, int batch) {
         p.vec_out = (p.N & 3) == 0 && (reinterpret_cast<uintptr_t>(p.partial) & 15) == 0;
         gn_partials_plan(p, BM, BN, pl.splits, batch);
         ln_partials_plan(p, BN, pl.splits, batch);
+        MH_REQUIRE(!OUT16 || (p.vec_out == 1 && reduce_vec_ok(p)), "f16 GEMM output: four columns at a time");
         gemm_h16_kernel<BM, BN, kDense, kProNone, true, true, 0, true, true>
             <<<dim3(tiles, 1, pl.splits), 256, 0, ctx.stream>>>(p);
         MH_LAUNCH_CHECK();
         const int64_t total = int64_t(p.M) * p.N;
         if (reduce_vec_ok(p))
-            splitk_reduce_kernel<0, true, true>
+            splitk_reduce_kernel<0, true, true, OUT16>
                 <<<unsigned(std::min<int64_t>(ceil_div(total / 4, 256), 8192)), 256, 0, ctx.stream>>>(p, pl.splits);
-        else
+        else if constexpr (!OUT16)
             splitk_reduce_kernel<0, false, true>
                 <<<unsigned(std::min<int64_t>(ceil_div(total, 256), 8192)), 256, 0, ctx.stream>>>(p, pl.splits);
         MH_LAUNCH_CHECK();
@@ -425,10 +428,11 @@ void launch_a16_cfg(Context &ctx, GemmArgs &p, const Plan &pl, int batch) {
     }
     p.k_split = p.K;
     p.vec_out = out_vec_ok(p, BM);
+    MH_REQUIRE(!OUT16 || p.vec_out == 1, "f16 GEMM output: four columns at a time");
     gn_partials_plan(p, BM, BN, 1, batch);
     ln_partials_plan(p, BN, 1, batch);
     const dim3 grid(tiles, unsigned(batch));
-    gemm_h16_kernel<BM, BN, kDense, kProNone, true, true, 0, false, true><<<grid, 256, 0, ctx.stream>>>(p);
+    gemm_h16_kernel<BM, BN, kDense, kProNone, true, true, 0, false, true, OUT16><<<grid, 256, 0, ctx.stream>>>(p);
     MH_LAUNCH_CHECK();
 }
 

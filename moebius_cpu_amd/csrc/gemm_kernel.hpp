@@ -204,7 +204,10 @@ __device__ __forceinline__ float *out_ptr(const GemmArgs &p, int row, int col, i
 // epilogue_value for four adjacent columns col..col+3 of one row, with 16-byte
 // loads and one 16-byte store (the caller has checked out_vec_ok); returns the
 // values stored.
-template <int EPI, bool FM = false>
+// OUT16: the output is f16 (GemmArgs::out holds halves), each value rounded to
+// nearest even and saturated as the f16 GEMM rounds its f32 operands; the f32
+// values are returned (for the partial sums).
+template <int EPI, bool FM = false, bool OUT16 = false>
 __device__ __forceinline__ float4 store4(const GemmArgs &p, int row, int col, float4 s) {
     int64_t o;
     float *dst = out_ptr(p, row, col, o);
@@ -240,7 +243,16 @@ __device__ __forceinline__ float4 store4(const GemmArgs &p, int row, int col, fl
         y[0] = y[0] + r2.x, y[1] = y[1] + r2.y, y[2] = y[2] + r2.z, y[3] = y[3] + r2.w;
     }
     const float4 r{y[0], y[1], y[2], y[3]};
-    *reinterpret_cast<float4 *>(dst + o) = r;
+    if constexpr (OUT16) {
+        typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+        auto r16 = [](float v) {
+            return static_cast<_Float16>(__builtin_fabsf(v) > 65504.0f ? __builtin_copysignf(65504.0f, v) : v);
+        };
+        *reinterpret_cast<half4_t *>(reinterpret_cast<_Float16 *>(dst) + o) = half4_t{r16(r.x), r16(r.y), r16(r.z),
+                                                                                     r16(r.w)};
+    } else {
+        *reinterpret_cast<float4 *>(dst + o) = r;
+    }
     return r;
 }
 
@@ -692,8 +704,8 @@ struct Waves {
 // partial sum; the K groups' tiles are added in LDS, then each thread finishes
 // four adjacent columns of a row at a time (16-byte loads and stores), or one
 // element at a time where that is not possible.
-template <int BM, int BN, int WM, int WN, int WK, int MF, int EPI, bool SPLIT, bool FSILU = false, typename Acc,
-          int FM, int FN>
+template <int BM, int BN, int WM, int WN, int WK, int MF, int EPI, bool SPLIT, bool FSILU = false,
+          bool OUT16 = false, typename Acc, int FM, int FN>
 __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const Acc (&acc)[FM][FN], int m0, int n0,
                                            int z, const float *ln_st = nullptr) {
     using MI = Mf<MF>;
@@ -750,7 +762,7 @@ __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const
                 if (SPLIT) {
                     *reinterpret_cast<float4 *>(p.partial + (int64_t(z) * p.M + row) * p.N + col) = v;
                 } else {
-                    const float4 y = store4<EPI, FSILU>(p, row, col, v);
+                    const float4 y = store4<EPI, FSILU, OUT16>(p, row, col, v);
                     if (kGn && p.gnp) {
                         gs.x += y.x, gs.y += y.y, gs.z += y.z, gs.w += y.w;
                         gq.x = __builtin_fmaf(y.x, y.x, gq.x);
@@ -780,7 +792,7 @@ __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const
                 if (SPLIT) {
                     *reinterpret_cast<float4 *>(p.partial + (int64_t(z) * p.M + row) * p.N + col) = v;
                 } else {
-                    const float4 y = store4<EPI, FSILU>(p, row, col, v);
+                    const float4 y = store4<EPI, FSILU, OUT16>(p, row, col, v);
                     if (gn || lnr) *reinterpret_cast<float4 *>(c) = y;  // the stored values, for the sums
                 }
             }
@@ -788,6 +800,8 @@ __device__ __forceinline__ void write_tile(const GemmArgs &p, float *smem, const
             if (lnr) ln_tile_partials<BM, BN, NT, CS>(p, smem, m0, n0);  // reads the C tile only
             if (gn) gn_tile_partials_lds<BM, BN, NT, CS>(p, smem, m0, n0);
         }
+    } else if (OUT16) {
+        // f16 outputs are written four columns at a time only (the launcher checks vec_out)
     } else if (p.vec_out == 2) {
         // Grouped rows (out index (row / rg) * ldc + col * rg + row % rg, rg % 4 == 0,
         // BM % rg == 0): rows 4j..4j+3 of a group at one column are four adjacent
@@ -1098,8 +1112,9 @@ __global__ __launch_bounds__(64 * WM * WN * WK) void gemm_f32_kernel(GemmArgs p)
 // VEC: four adjacent columns per thread (N, the output's leading dimensions and
 // segment bounds multiples of 4, M * N < 2^31, 16-byte aligned buffers; checked
 // by the launcher), so every load and store is 16 bytes wide.
-template <int EPI, bool VEC, bool FSILU = false>
+template <int EPI, bool VEC, bool FSILU = false, bool OUT16 = false>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int splits) {
+    static_assert(!OUT16 || VEC, "f16 outputs: four columns at a time");
     const int64_t total = int64_t(p.M) * p.N;
     if constexpr (VEC) {
         const uint32_t n4 = uint32_t(p.N) >> 2;
@@ -1112,7 +1127,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p, int spli
                 s.x += t.x, s.y += t.y, s.z += t.z, s.w += t.w;
             }
             const int row = int(e / n4);
-            store4<EPI, FSILU>(p, row, int(e - uint32_t(row) * n4) << 2, s);
+            store4<EPI, FSILU, OUT16>(p, row, int(e - uint32_t(row) * n4) << 2, s);
         }
     } else {
         for (int64_t e = blockIdx.x * int64_t(256) + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {

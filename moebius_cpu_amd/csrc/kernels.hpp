@@ -134,10 +134,11 @@ void conv1x1(Context &ctx, const float *x, int64_t pixels, int c_in, const void 
 // conv1x1 for FAST contexts whose input is already f16 ([pixels][c_in] halves, e.g.
 // from depthwise3x3_h16) and whose weight is f16: the products of the f16 GEMM on f32
 // input it rounds itself, with the same epilogue (bias, residual and its transform,
-// residual2, GroupNorm partials).
+// residual2, GroupNorm partials). out16: out holds halves, each output rounded as the
+// f16 GEMM rounds an f32 operand (for an output that only another f16 GEMM reads).
 void conv1x1_a16(Context &ctx, const void *x16, int64_t pixels, int c_in, const void *weight, int c_out,
                  const float *bias, const float *residual, float *out, const ResidualAffine *raff = nullptr,
-                 const float *residual2 = nullptr, GnPartials *gn = nullptr);
+                 const float *residual2 = nullptr, GnPartials *gn = nullptr, bool out16 = false);
 // residual2 (optional, [n, ho, wo, c_out]) is added last: out = (bias + conv) + residual2.
 void conv3x3(Context &ctx, const float *x, int n, int h, int w, int c_in, const void *weight, WeightType wt,
              int c_out, const float *bias, int stride, const int pad[4], bool upsample2x, const Affine *prologue,

@@ -832,15 +832,28 @@ struct MixTransformer {
         if (!h16) depthwise3x3(e.ctx, a.p, a.n, a.h, a.w, a.c, dw, dwb, 2, g.p);
         e.pool.recycle(a);
         DT u;
+        // u, read only by proj_out: f16 as well when proj_out's weight is
+        const DParam powd = proj_out.w.at(e.ctx);
+        const bool u16 = h16 && powd.wt == kF16;
         if (h16) {
             u = e.pool.tensor(g.n, g.h, g.w, point.co);
-            conv1x1_a16(e.ctx, g.p, g.px(), point.ci, pwd.p, point.co, point.b, h.p, u.p);
+            conv1x1_a16(e.ctx, g.p, g.px(), point.ci, pwd.p, point.co, point.b, h.p, u.p, nullptr, nullptr, nullptr,
+                        u16);
         } else {
             u = point.fwd(e, g, &h);
         }
         e.pool.recycle(g);
         e.pool.recycle(h);
-        DT out = proj_out.fwd_gnp(e, u, &xr);
+        DT out;
+        if (u16) {
+            out = e.pool.tensor(u.n, u.h, u.w, proj_out.co);
+            GnPartials gp = gn_request(e, u, proj_out.co);
+            conv1x1_a16(e.ctx, u.p, u.px(), proj_out.ci, powd.p, proj_out.co, proj_out.b, xr.p, out.p, nullptr,
+                        nullptr, &gp);
+            gn_attach(e, out, gp);
+        } else {
+            out = proj_out.fwd_gnp(e, u, &xr);
+        }
         e.pool.recycle(u);
         return out;
     }

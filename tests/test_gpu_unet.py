@@ -531,26 +531,46 @@ def test_unet_groupnorm_into_proj_in_is_bit_exact(ctx, gnet, fast, tune):
     assert np.array_equal(apart, fused)
 
 
-def test_unet_fast_f16_operands_are_bit_exact(ctx, gnet, tune):
+@pytest.fixture(scope="module")
+def g16net(ctx, params):
+    """The UNet with f16-stored GEMM weights (what FAST's f16 stores apply to)."""
+    return UNet(ctx, params, f16_gemm=True)
+
+
+def _f16a_launches(ctx):
+    """Launches of the f16-input GEMM family in the context's GEMM census."""
+    return sum(r["launches"] for r in ctx.gemm_times() if r["config"].startswith("f16a "))
+
+
+def test_unet_fast_f16_operands_are_bit_exact(ctx, g16net, tune):
     """FAST contexts store in f16 what only an f16 GEMM reads: the upsample convs'
-    Winograd kernel U (tuning wino_u16) and input transform V (wino_v16), and the
+    Winograd kernel U (tuning wino_u16) and input transform V (wino_v16), the
     depthwise convs' outputs that only the next 1x1 reads (dw_out16; the resnets'
-    DwConv2d and the MixFFN's GLU). Each is rounded to nearest even with the
+    DwConv2d and the MixFFN's GLU) and the MixFFN's pointwise output that only
+    proj_out reads (with dw_out16). Each is rounded to nearest even with the
     saturation the f16 GEMM applies to f32 operands as it loads them, so every
-    combination gives the bits of all three off."""
+    combination gives the bits of all of them off. The f16 stores need f16-stored
+    GEMM weights; the GEMM census shows the f16-input GEMMs running."""
     inp = U.unet_input(seed=5019)
     ctx.set_precision(True)
-    outs = []
+    outs, f16a = [], []
     try:
+        tune("gemm_time", 1)
+        ctx.gemm_times()
         for u16, v16, dw16 in ((0, 0, 0), (1, 0, 0), (1, 1, 0), (0, 0, 1), (1, 1, 1)):
             tune("wino_u16", u16)
             tune("wino_v16", v16)
             tune("dw_out16", dw16)
-            outs.append(gnet.forward_host(inp.x, inp.timestep, cfg=True))
+            outs.append(g16net.forward_host(inp.x, inp.timestep, cfg=True))
+            f16a.append(_f16a_launches(ctx))
     finally:
         ctx.set_precision(False)
     for o in outs[1:]:
         assert np.array_equal(o, outs[0])
+    # no f16 input with every store off; V in f16 feeds the Winograd plane GEMMs,
+    # the depthwise outputs every resnet and MixFFN 1x1 after them
+    assert f16a[0] == 0 and f16a[1] == 0
+    assert f16a[2] > 0 and f16a[3] > f16a[2] and f16a[4] == f16a[2] + f16a[3]
 
 
 def test_unet_pool_stops_allocating(ctx, gnet):
